@@ -1,0 +1,243 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused dequant-matmul path on one MI355X.
+
+Default workload (one "step" = one decoded token): the Qwen3-4B-shaped q4_0 decode linear
+stack, batch 1, 36 layers x {q 2560->4096, k/v 2560->1024, o 4096->2560, gate/up 2560->9728,
+down 9728->2560}, fp16 activations, seeded synthetic weights (fp16 scales |N(0, 0.01)|,
+uniform nibbles). Per layer four launches: q|k|v fused (one shared x), o, gate|up fused, down;
+the whole token is captured once as a HIP graph and replayed.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config stack|gemv1|...]
+
+Prints one JSON line. ``value`` = aggregate algorithmic GB/s per token (weights + activations
+read and written, the basis stated in DESIGN.md) with all inputs resident in HBM.
+``roofline`` = the dominant kernel (the q4_0 GEMV family) measured live with HIP events on
+the launch stream; ``cpu_baseline`` = the numpy oracle path (f32 decode + BLAS matvec) timed
+on a bounded sample of the same workload on this host.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "dequant-GEMV GB/s (% HBM peak) + prefill/MoE GEMM TFLOP/s (% MFMA peak)"
+
+QWEN3_4B = dict(hidden=2560, q=4096, kv=1024, inter=9728, layers=36)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="stack", choices=["stack", "gemv1"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--seed", type=int, default=0)
+    return ap.parse_args()
+
+
+def q4_0_blocks_gpu(torch, gen, N, K, dev):
+    """Seeded packed q4_0 rows generated on the device: uint8 [N * K/32 * 18]."""
+    nb = N * (K // 32)
+    blk = torch.empty((nb, 18), dtype=torch.uint8, device=dev)
+    d = (torch.randn(nb, generator=gen, device=dev) * 0.01).abs().to(torch.float16)
+    blk[:, 0:2] = d.view(torch.uint8).view(nb, 2)
+    blk[:, 2:] = torch.randint(0, 256, (nb, 16), generator=gen, device=dev, dtype=torch.uint8)
+    return blk.view(-1)
+
+
+def build_stack(torch, dev, seed):
+    c = QWEN3_4B
+    H, Q, KV, I = c["hidden"], c["q"], c["kv"], c["inter"]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    layers = []
+    for _ in range(c["layers"]):
+        layers.append(dict(
+            q=q4_0_blocks_gpu(torch, gen, Q, H, dev), k=q4_0_blocks_gpu(torch, gen, KV, H, dev),
+            v=q4_0_blocks_gpu(torch, gen, KV, H, dev), o=q4_0_blocks_gpu(torch, gen, H, Q, dev),
+            gate=q4_0_blocks_gpu(torch, gen, I, H, dev), up=q4_0_blocks_gpu(torch, gen, I, H, dev),
+            down=q4_0_blocks_gpu(torch, gen, H, I, dev)))
+    f16 = torch.float16
+    acts = dict(
+        x_attn=torch.randn(H, generator=gen, device=dev).to(f16),
+        x_o=torch.randn(Q, generator=gen, device=dev).to(f16),
+        x_mlp=torch.randn(H, generator=gen, device=dev).to(f16),
+        x_down=torch.randn(I, generator=gen, device=dev).to(f16),
+        yq=torch.empty(Q, dtype=f16, device=dev), yk=torch.empty(KV, dtype=f16, device=dev),
+        yv=torch.empty(KV, dtype=f16, device=dev), yo=torch.empty(H, dtype=f16, device=dev),
+        yg=torch.empty(I, dtype=f16, device=dev), yu=torch.empty(I, dtype=f16, device=dev),
+        yd=torch.empty(H, dtype=f16, device=dev))
+    return layers, acts
+
+
+def stack_bytes():
+    c = QWEN3_4B
+    H, Q, KV, I = c["hidden"], c["q"], c["kv"], c["inter"]
+    shapes = [(Q, H), (KV, H), (KV, H), (H, Q), (I, H), (I, H), (H, I)]
+    w = sum(n * k // 32 * 18 for n, k in shapes)
+    act = sum(2 * k + 2 * n for n, k in shapes)
+    flops = sum(2 * n * k for n, k in shapes)
+    return shapes, (w + act) * c["layers"], flops * c["layers"], w
+
+
+def stack_launches(ops, layers, a):
+    """The launches of one token, in order, as closures (for graph capture and timing)."""
+    H, Q, KV, I = QWEN3_4B["hidden"], QWEN3_4B["q"], QWEN3_4B["kv"], QWEN3_4B["inter"]
+    out = []
+    for L in layers:
+        out.append(lambda L=L: ops.gemv_q4_0_seg3(a["x_attn"], H, [(L["q"], a["yq"], Q), (L["k"], a["yk"], KV),
+                                                                    (L["v"], a["yv"], KV)]))
+        out.append(lambda L=L: ops.gemv(ops.GGML_Q4_0, L["o"], a["x_o"], H, Q, out=a["yo"].view(1, H)))
+        out.append(lambda L=L: ops.gemv_q4_0_seg3(a["x_mlp"], H, [(L["gate"], a["yg"], I), (L["up"], a["yu"], I)]))
+        out.append(lambda L=L: ops.gemv(ops.GGML_Q4_0, L["down"], a["x_down"], H, I, out=a["yd"].view(1, H)))
+    return out
+
+
+def cpu_baseline_stack(target_s=12.0):
+    """numpy oracle path on a bounded sample: q4_0 -> f32 decode, then BLAS matvec (1 thread)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import formats
+    from vybforge_amd import synth
+    shapes, _, _, _ = stack_bytes()
+    rng = np.random.default_rng(1)
+    mats = [(synth.q4_0_weights(rng, n, k), n, k) for n, k in shapes]
+    xs = {k: rng.standard_normal(k).astype(np.float16) for _, k in shapes}
+    layer_bytes = sum(raw.size + 2 * k + 2 * n for raw, n, k in mats)
+    done = 0
+    t0 = time.perf_counter()
+    with threadpool_limits(limits=1):
+        while True:
+            for raw, n, k in mats:
+                w = formats.dequant_q4_0(raw).reshape(n, k)
+                y = w @ xs[k].astype(np.float32)
+                y.astype(np.float16)
+            done += 1
+            el = time.perf_counter() - t0
+            if el >= target_s:
+                break
+    return dict(value=round(layer_bytes * done / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                sample=f"{done} layers of the 36-layer stack (7 GEMVs each, 56.8 MB packed), "
+                       "numpy f32 decode + OpenBLAS matvec, 1 thread")
+
+
+def run_stack(args, torch, dev):
+    from vybforge_amd import ops
+    shapes, bytes_tok, flops_tok, wbytes_layer = stack_bytes()
+    layers, acts = build_stack(torch, dev, args.seed)
+    launches = stack_launches(ops, layers, acts)
+    torch.cuda.synchronize()
+
+    # capture one token as a graph
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in launches:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in launches:
+            f()
+    torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        g.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_ev = ev0.elapsed_time(ev1)
+    ms_step = ms_ev / args.steps
+    value = bytes_tok / (ms_step * 1e-3) / 1e9
+
+    # dominant kernel, live: the 144 GEMV launches of a token back to back on one stream,
+    # event-timed over many tokens; the per-launch average includes inter-launch gaps
+    n_launch = len(launches)
+    achieved = bytes_tok / n_launch / (ms_step * 1e-3 / n_launch) / 1e9
+    roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                    kernel="k_gemv_pair<q4_0> (all 144 launches per token)",
+                    avg_launch_us=round(ms_step * 1e3 / n_launch, 3),
+                    bytes_per_launch=round(bytes_tok / n_launch))
+    return dict(value=value, ms_step=ms_step, wall=wall, roofline=roofline, flops=flops_tok,
+                workload="qwen3-4b q4_0 decode linear stack: 36 layers x 7 GEMVs, batch 1, fp16 act",
+                bytes_per_step=bytes_tok, launches_per_step=n_launch)
+
+
+def run_gemv1(args, torch, dev):
+    """Config 1: q4_0 GEMV 9728x2560, fp32 x, fp32 y, rotating 24 weight copies (>300 MB)."""
+    from vybforge_amd import ops
+    N, K = 9728, 2560
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    copies = [q4_0_blocks_gpu(torch, gen, N, K, dev) for _ in range(24)]
+    x = torch.randn(K, generator=gen, device=dev)
+    y = torch.empty(1, N, device=dev)
+    launch = [lambda W=W: ops.gemv(ops.GGML_Q4_0, W, x, N, K, out=y) for W in copies]
+    for f in launch:
+        f()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in launch:
+            f()
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        g.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = ev0.elapsed_time(ev1) / args.steps / len(launch)
+    bytes_call = N * K // 32 * 18 + 4 * K + 4 * N
+    value = bytes_call / (per * 1e-3) / 1e9
+    roofline = dict(bound="hbm", achieved=round(value, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(value / HBM_PEAK_GBS, 4), traffic=None, kernel="k_gemv_pair<q4_0,f32>",
+                    avg_launch_us=round(per * 1e3, 3), bytes_per_launch=bytes_call)
+    return dict(value=value, ms_step=per * len(launch), wall=wall, roofline=roofline,
+                flops=2 * N * K * len(launch), workload="q4_0 GEMV 9728x2560 fp32 x (24 rotated copies)",
+                bytes_per_step=bytes_call * len(launch), launches_per_step=len(launch))
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the fused dequant-matmul path is single-GPU in this "
+              "build (sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        sys.exit("no GPU visible")
+    dev = torch.device("cuda:0")
+    r = run_stack(args, torch, dev) if args.config == "stack" else run_gemv1(args, torch, dev)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_stack() if args.config == "stack" else None
+    line = dict(
+        metric=METRIC, value=round(r["value"], 2), unit="GB/s", n_gpus=1, steps=args.steps,
+        warmup=args.warmup, ms_per_step=round(r["ms_step"], 4), higher_is_better=True,
+        scaling="weak", vs_baseline=None, dtype="f16",
+        data="synthetic (seeded q4_0 weights generated on the device, fp16 activations N(0,1))",
+        config=dict(workload=r["workload"], bytes_per_step=r["bytes_per_step"],
+                    launches_per_step=r["launches_per_step"], hbm_frac=round(r["value"] / HBM_PEAK_GBS, 4),
+                    tflops=round(r["flops"] / (r["ms_step"] * 1e-3) / 1e12, 3)),
+        roofline=r["roofline"], cpu_baseline=cpu)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,112 @@
+/* vybdq.h — MI355X (gfx950) fused dequant-matmul library: flat C-ABI.
+ *
+ * Buffer-in / buffer-out. Every device buffer is a plain device address passed as
+ * uint64_t (the reference host keeps device pointers as Int handles,
+ * native/tensor/tensor.vyb:11-22). Streams are hipStream_t handles passed as uint64_t
+ * (0 = the null stream). The caller allocates and owns every buffer; no entry point
+ * allocates or frees device memory inside a hot call, and none synchronises the stream.
+ *
+ * Return codes: 0 = success; a negative VYBDQ_ERR_* code otherwise, with the message in
+ * vybdq_last_error() (per host thread). Shape preconditions are checked before any launch
+ * (the reference's EXL3FAIL checks, native/glm53/glm_engine.vyb:969-973). No scalar
+ * out-parameters (native/audio/vyb_audio.h:25-28): sizes are returned as int64_t.
+ *
+ * Packed formats (little-endian, GGUF row layout: weight row n = output n, K/32 blocks):
+ *   q4_0: 18 B = [fp16 d][16 B nibbles], w = d * (q - 8)
+ *   Q8_0: 34 B = [fp16 d][32 x int8],    w = d * q
+ *   EXL3 4-bpw: trellis uint16 [K/16][N/16][64], suh fp16 [K], svh fp16 [N]
+ * Results are deterministic: fixed reduction order, no floating-point atomics.
+ */
+#ifndef VYBDQ_H
+#define VYBDQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VYBDQ_ABI_VERSION 1
+
+/* return codes */
+#define VYBDQ_OK 0
+#define VYBDQ_ERR_ARG (-1)       /* null pointer, unknown enum value */
+#define VYBDQ_ERR_SHAPE (-2)     /* shape precondition failed; nothing was launched */
+#define VYBDQ_ERR_ALIGN (-3)     /* buffer alignment precondition failed */
+#define VYBDQ_ERR_HIP (-4)       /* HIP runtime error (launch failure etc.) */
+#define VYBDQ_ERR_WORKSPACE (-5) /* workspace missing or too small */
+
+/* element types (x_dt / y_dt / out_dt) */
+#define VYBDQ_F32 0
+#define VYBDQ_F16 1
+#define VYBDQ_BF16 2
+#define VYBDQ_F64 3
+
+/* q4_0 nibble order within a block */
+#define VYBDQ_Q4_GGML 0        /* element j = low nibble of qs[j], j+16 = high nibble (GGUF) */
+#define VYBDQ_Q4_INTERLEAVED 1 /* element 2s = low, 2s+1 = high nibble of qs[s]; the order of
+                                  the reference's deq_q4_0 intrinsic, pinned by its fixture
+                                  (native/gguf/mk_fixture.vyb:86-99, dequant_gguf.vyb:118-127) */
+
+/* EXL3 codebooks (exllamav3 numbering) */
+#define VYBDQ_EXL3_3INST 0 /* x = w*89226354 + 64248484 (QTIP 3INST) */
+#define VYBDQ_EXL3_MCG 1   /* x = w*0xCBAC1FED: the codebook of the reference's checkpoint */
+
+/* ---- library ------------------------------------------------------------------------- */
+
+/* VYBDQ_ABI_VERSION of the loaded library. */
+int vybdq_abi_version(void);
+
+/* Text of the failure from the last vybdq_* call on this host thread that failed.
+   Never NULL. Mirrors va_lasterr (native/audio/vyb_audio.h:16-19). */
+const char *vybdq_last_error(void);
+
+/* ---- decode-only entry points (the bit-exact gates) ---------------------------------- */
+
+/* out[i] = d * (q - 8) for nblocks*32 elements; out_dt F32, F16 or F64.
+   Replaces q4deq(q, o, n, z) (native/kernels/deq.vyb:4-12), which writes f64. */
+int vybdq_dequant_q4_0(uint64_t W, uint64_t out, int64_t nblocks, int order, int out_dt,
+                       uint64_t stream);
+
+/* out[i] = d * q for nblocks*32 elements; out_dt F32, F16 or F64.
+   Replaces q8_0deq(q, o, n, z=0) (native/kernels/q8_0.vyb:11-30). */
+int vybdq_dequant_q8_0(uint64_t W, uint64_t out, int64_t nblocks, int out_dt, uint64_t stream);
+
+/* ---- GEMV on packed GGUF rows -------------------------------------------------------- */
+
+/* Y[m, n] = RS[m, n] + sum_k X[m, k] * W[n, k] for m < M, n < N.
+   X: x_dt (F32, F16, BF16) [M, K]; Y: y_dt (F32, F16, BF16, F64) [M, N]; RS: same type as
+   Y or 0. K % 32 == 0; 1 <= M <= 8. Accumulation in float32.
+   Replaces gemv_q8_0's sibling for q4_0 (p-block W@0 X@8 Y@16 M@24 N@32 K@40 YE@48 RS@120,
+   native/kernels/rgemv.vyb:13-15, native/kernels/qwen3.vyb:395-440); the reference has no
+   fused q4_0 GEMV, only deq_q4_0 followed by the f64 gemm (native/kernels/gemm.vyb:15-39). */
+int vybdq_gemv_q4_0(uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K,
+                    int x_dt, int y_dt, uint64_t RS, int order, uint64_t stream);
+
+/* Same contract on Q8_0 rows. Replaces gemv_q8_0 (native/kernels/rgemv.vyb:299-368). */
+int vybdq_gemv_q8_0(uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K,
+                    int x_dt, int y_dt, uint64_t RS, uint64_t stream);
+
+/* Fused launch of up to three q4_0 GEMVs that share X (q|k|v, gate|up): rows [0, N) go to
+   W/Y, the next N2 rows to W2/Y2, the next N3 to W3/Y3 (N2 = N3 = 0: one matrix). Mirrors
+   the multi-segment p-block (W2/NS2/Y2/YE2 @56-80, W3/NS3/Y3/YE3 @88-112,
+   native/kernels/qwen3.vyb:416-436). M = 1. */
+int vybdq_gemv_q4_0_seg3(uint64_t X, int64_t K, int x_dt, int order,
+                         uint64_t W, uint64_t Y, int64_t N, int y_dt,
+                         uint64_t W2, uint64_t Y2, int64_t N2, int y_dt2,
+                         uint64_t W3, uint64_t Y3, int64_t N3, int y_dt3, uint64_t stream);
+
+/* ---- activation quantizer ------------------------------------------------------------ */
+
+/* xq8 semantics per row and per 32-value block: a = max|x|, d = a/127, q = sat_s8(rne(x*127/a))
+   (q = 0, d = 0 for an all-zero block). X: x_dt (F32, F16, BF16) [M, K]; Xq int8 [M, K];
+   Xs float32 [M, K/32]. The reference's single-row layout (scales at Y + K) is Xs = Xq + K.
+   Replaces xq8 (native/kernels/rgemv7.vyb:195-214). K % 32 == 0. */
+int vybdq_quant_q8_act(uint64_t X, uint64_t Xq, uint64_t Xs, int64_t M, int64_t K, int x_dt,
+                       uint64_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VYBDQ_H */

@@ -1,0 +1,41 @@
+"""CPU oracle for the fused dequant-matmul path — TEST INFRASTRUCTURE ONLY.
+
+This package is a numpy restatement of the reference algorithms on the packed-weight
+dequant -> GEMV/GEMM path. Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker (or the
+timed CPU baseline). The product path (``vybforge_amd`` + ``libvybdq.so``) never
+imports or calls anything here and fails loudly when the HIP library is missing.
+
+Modules and the reference code each one restates (paths relative to the reference
+repository root):
+
+  formats  q4_0 decode      HANDOFF-VYB-NATIVE-INFERENCE.md:35 (deq_q4_0 spec),
+                            native/kernels/deq.vyb:4-12, native/gguf/mk_fixture.vyb:86-99,
+                            native/gguf/dequant_gguf.vyb:118-127 (fixture order)
+           Q8_0 decode      native/tools/q8_0_ref.py:50-56, native/kernels/q8_0.vyb:11-30
+           xq8 quantizer    native/kernels/rgemv7.vyb:195-214
+  exl3     mcg decode, slot map, Hadamard-128, full dequant
+                            native/exl3/exl3_ref.py:31-120, native/exl3/README.md:24-49,
+                            native/kernels/exl3.vyb:375-422
+  moe      route / clamped SwiGLU / combine
+                            native/glm53/moe_ref.py:25-112, native/kernels/moe.vyb:1-170
+  matmul   fp64 GEMV/GEMM gates and the tolerance metric
+                            native/kernels/rgemv.vyb:13-15,359-366, native/tools/gen_rpf.py:2-8,
+                            native/glm53/verify_layer0.py:134-139
+
+Pinning (what checks each function, all under tests/):
+  q4_0 decode      the reference's frozen GGUF fixture block (interleaved order) and
+                   brute force per nibble; ggml order against the public block layout
+                   via an independent bit-level decoder.                 -> pinned
+  Q8_0 decode      closed form d*q checked against an independent int8/fp16 bit decode
+                   (no reference-held fixture exists).                   -> pinned (closed form)
+  xq8              round-trip bound, RNE ties, zero block, saturation.   -> pinned (properties)
+  exl3 decode      all-zero-trellis KAT (1.84375), exhaustive 65536-window check against
+                   an integer-only fp16 decode, slot-map invariants.     -> pinned
+  exl3 3inst (cb0) QTIP paper constants only; no fixture anywhere.       -> parity unpinned
+  exl3 dequant     closed form of the all-zero trellis after the Hadamard sandwich,
+                   H orthogonality, per-block linearity.                 -> pinned
+  moe              the reference's committed MoE goldens (routing ids/weights, and the
+                   block output on a column slice).                      -> pinned
+  matmul           fp64 numpy matmul (invariant).                        -> pinned
+"""

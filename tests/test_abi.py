@@ -1,0 +1,68 @@
+"""The C-ABI library loads and exports every entry point include/vybdq.h declares; host-side
+precondition checks return their error codes before any launch. CPU only: no call here
+reaches the GPU."""
+
+import os
+import re
+
+import pytest
+
+from tests.conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "vybdq.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vybdq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "vybdq_gemv_q4_0" in names and "vybdq_last_error" in names
+    assert len(names) >= 8
+
+
+def test_library_exports_every_declared_symbol():
+    from vybforge_amd import _lib
+    for name in declared_functions():
+        assert hasattr(_lib.lib, name), f"{name} not exported"
+    # and the ctypes table covers exactly the header
+    assert set(_lib.SIGNATURES) == set(declared_functions())
+
+
+def test_abi_version():
+    from vybforge_amd import _lib
+    assert _lib.lib.vybdq_abi_version() == 1
+
+
+@pytest.mark.parametrize("args,code,text", [
+    # (W, X, Y, M, N, K, x_dt, y_dt, RS, order, stream)
+    ((1, 1, 1, 1, 16, 48, 0, 0, 0, 0, 0), -2, "K must be"),        # K % 32 != 0
+    ((1, 1, 1, 9, 16, 64, 0, 0, 0, 0, 0), -2, "M must be"),        # M > 8
+    ((0, 1, 1, 1, 16, 64, 0, 0, 0, 0, 0), -1, "null W"),
+    ((1, 1, 1, 1, 16, 64, 7, 0, 0, 0, 0), -1, "x_dt"),
+    ((1, 1, 1, 1, 16, 64, 0, 0, 0, 5, 0), -1, "order"),
+    ((2, 1, 1, 1, 16, 64, 0, 0, 0, 0, 0), -3, "aligned"),          # W not 4-byte aligned
+    ((4, 1, 1, 1, 0, 64, 0, 0, 0, 0, 0), -2, "N must be"),
+])
+def test_gemv_preconditions(args, code, text):
+    from vybforge_amd import _lib
+    rc = _lib.lib.vybdq_gemv_q4_0(*args)
+    assert rc == code
+    assert text in _lib.last_error()
+
+
+def test_dequant_preconditions():
+    from vybforge_amd import _lib
+    assert _lib.lib.vybdq_dequant_q4_0(0, 1, 1, 0, 0, 0) == _lib.ERR_ARG
+    assert _lib.lib.vybdq_dequant_q4_0(1, 1, 1, 0, 2, 0) == _lib.ERR_ARG   # BF16 out not offered
+    assert _lib.lib.vybdq_dequant_q8_0(1, 1, -1, 0, 0) == _lib.ERR_SHAPE
+    assert _lib.lib.vybdq_dequant_q8_0(1, 1, 0, 0, 0) == _lib.OK          # empty: no launch
+
+
+def test_quant_preconditions():
+    from vybforge_amd import _lib
+    assert _lib.lib.vybdq_quant_q8_act(1, 1, 1, 2, 33, 0, 0) == _lib.ERR_SHAPE
+    assert _lib.lib.vybdq_quant_q8_act(1, 1, 2, 2, 32, 0, 0) == _lib.ERR_ALIGN

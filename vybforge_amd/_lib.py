@@ -1,0 +1,69 @@
+"""ctypes binding of libvybdq.so (the C-ABI in include/vybdq.h).
+
+The library is loaded from this package directory only (built in-tree by
+``python -m vybforge_amd.build``). There is no fallback: if the library is missing or
+does not export the declared entry points, importing this module raises.
+"""
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libvybdq.so")
+
+# return codes / enums (include/vybdq.h)
+OK = 0
+ERR_ARG, ERR_SHAPE, ERR_ALIGN, ERR_HIP, ERR_WORKSPACE = -1, -2, -3, -4, -5
+F32, F16, BF16, F64 = 0, 1, 2, 3
+Q4_GGML, Q4_INTERLEAVED = 0, 1
+EXL3_3INST, EXL3_MCG = 0, 1
+
+_u64, _i64, _int = ctypes.c_uint64, ctypes.c_int64, ctypes.c_int
+
+# name -> argtypes (restype int unless listed in _RESTYPE)
+SIGNATURES = {
+    "vybdq_abi_version": [],
+    "vybdq_last_error": [],
+    "vybdq_dequant_q4_0": [_u64, _u64, _i64, _int, _int, _u64],
+    "vybdq_dequant_q8_0": [_u64, _u64, _i64, _int, _u64],
+    "vybdq_gemv_q4_0": [_u64, _u64, _u64, _i64, _i64, _i64, _int, _int, _u64, _int, _u64],
+    "vybdq_gemv_q8_0": [_u64, _u64, _u64, _i64, _i64, _i64, _int, _int, _u64, _u64],
+    "vybdq_gemv_q4_0_seg3": [_u64, _i64, _int, _int,
+                             _u64, _u64, _i64, _int,
+                             _u64, _u64, _i64, _int,
+                             _u64, _u64, _i64, _int, _u64],
+    "vybdq_quant_q8_act": [_u64, _u64, _u64, _i64, _i64, _int, _u64],
+}
+_RESTYPE = {"vybdq_last_error": ctypes.c_char_p}
+
+
+class VybdqError(RuntimeError):
+    def __init__(self, code, where, msg):
+        super().__init__(f"{where} failed with code {code}: {msg}")
+        self.code = code
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"libvybdq.so is not built ({LIB_PATH}); run python -m vybforge_amd.build")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)  # AttributeError if the export is missing
+        fn.argtypes = args
+        fn.restype = _RESTYPE.get(name, ctypes.c_int)
+    return lib
+
+
+lib = _load()
+
+
+def last_error():
+    return lib.vybdq_last_error().decode()
+
+
+def call(name, *args):
+    """Call an entry point; raise VybdqError on a nonzero return code."""
+    rc = getattr(lib, name)(*args)
+    if rc != OK:
+        raise VybdqError(rc, name, last_error())
+    return rc

@@ -1,0 +1,72 @@
+"""Build libvybdq.so (gfx950) in-tree with hipcc.
+
+    python -m vybforge_amd.build            # compile every csrc/*.hip and link
+    python -m vybforge_amd.build --clean
+
+Every translation unit is compiled for gfx950 only, with packed-FP32 instructions disabled
+(some of their forms have produced wrong results on the target machines). The output is
+vybforge_amd/libvybdq.so next to this file; it is what vybforge_amd._lib loads.
+"""
+
+import concurrent.futures as cf
+import glob
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OBJ = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "libvybdq.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+CFLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(HERE, "..", "include"),
+]
+
+
+def _compile(src):
+    obj = os.path.join(OBJ, os.path.basename(src) + ".o")
+    deps = [src] + glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(CSRC, "*.inc"))
+    deps.append(os.path.join(HERE, "..", "include", "vybdq.h"))
+    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    msg = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
+                    if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src}:\n{msg}")
+    return obj, msg
+
+
+def build(verbose=False):
+    """Compile all sources and link libvybdq.so. Always rebuilds."""
+    os.makedirs(OBJ, exist_ok=True)
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    if not srcs:
+        raise RuntimeError("no HIP sources found")
+    jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        results = list(ex.map(_compile, srcs))
+    for obj, msg in results:
+        if verbose and msg.strip():
+            print(msg)
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + [o for o, _ in results]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    if "--clean" in sys.argv:
+        for f in glob.glob(os.path.join(OBJ, "*.o")) + [LIB]:
+            if os.path.exists(f):
+                os.remove(f)
+        print("clean")
+    else:
+        print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,96 @@
+// Shared device helpers and host plumbing for libvybdq (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/vybdq.h"
+
+namespace vybdq {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+// ---- host: error state ----------------------------------------------------------------
+
+int set_error(int code, const std::string &msg);
+int check_launch(const char *what);  // hipGetLastError after a launch
+inline hipStream_t as_stream(uint64_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+#define VYBDQ_REQUIRE(cond, code, msg)                                                     \
+  do {                                                                                     \
+    if (!(cond)) return ::vybdq::set_error((code), std::string(__func__) + ": " + (msg));  \
+  } while (0)
+
+inline bool dt_valid_in(int dt) { return dt == VYBDQ_F32 || dt == VYBDQ_F16 || dt == VYBDQ_BF16; }
+inline bool dt_valid_out(int dt) { return dt_valid_in(dt) || dt == VYBDQ_F64; }
+inline int dt_size(int dt) { return dt == VYBDQ_F64 ? 8 : dt == VYBDQ_F32 ? 4 : 2; }
+
+// ---- device: element load/store -------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// float32 -> bfloat16, round to nearest even (NaN kept quiet)
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+template <int DT>
+__device__ __forceinline__ float load_elem(const void *p, int64_t i) {
+  if constexpr (DT == VYBDQ_F32) return static_cast<const float *>(p)[i];
+  else if constexpr (DT == VYBDQ_F16) return static_cast<float>(static_cast<const _Float16 *>(p)[i]);
+  else return bf16_to_f32(static_cast<const uint16_t *>(p)[i]);
+}
+
+// Store y (+ residual of the same type). F64 keeps the reference's f64-output mode
+// (rgemv.vyb:359-366): the f32 accumulator is widened, then the f64 residual is added.
+template <int DT>
+__device__ __forceinline__ void store_elem(void *p, const void *rs, int64_t i, float v) {
+  if constexpr (DT == VYBDQ_F64) {
+    double d = static_cast<double>(v);
+    if (rs) d += static_cast<const double *>(rs)[i];
+    static_cast<double *>(p)[i] = d;
+  } else if constexpr (DT == VYBDQ_F32) {
+    if (rs) v += static_cast<const float *>(rs)[i];
+    static_cast<float *>(p)[i] = v;
+  } else if constexpr (DT == VYBDQ_F16) {
+    if (rs) v += static_cast<float>(static_cast<const _Float16 *>(rs)[i]);
+    static_cast<_Float16 *>(p)[i] = static_cast<_Float16>(v);
+  } else {
+    if (rs) v += bf16_to_f32(static_cast<const uint16_t *>(rs)[i]);
+    static_cast<uint16_t *>(p)[i] = f32_to_bf16(v);
+  }
+}
+
+__device__ __forceinline__ float half_bits_to_f32(uint32_t bits16) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+
+}  // namespace vybdq
+
+// Dispatch a runtime dtype to a template parameter.
+#define VYBDQ_DISPATCH_IN(dt, NAME, ...)                                                    \
+  switch (dt) {                                                                            \
+    case VYBDQ_F32: { constexpr int NAME = VYBDQ_F32; __VA_ARGS__; } break;                \
+    case VYBDQ_F16: { constexpr int NAME = VYBDQ_F16; __VA_ARGS__; } break;                \
+    default: { constexpr int NAME = VYBDQ_BF16; __VA_ARGS__; } break;                      \
+  }
+
+#define VYBDQ_DISPATCH_OUT(dt, NAME, ...)                                                   \
+  switch (dt) {                                                                            \
+    case VYBDQ_F32: { constexpr int NAME = VYBDQ_F32; __VA_ARGS__; } break;                \
+    case VYBDQ_F16: { constexpr int NAME = VYBDQ_F16; __VA_ARGS__; } break;                \
+    case VYBDQ_BF16: { constexpr int NAME = VYBDQ_BF16; __VA_ARGS__; } break;              \
+    default: { constexpr int NAME = VYBDQ_F64; __VA_ARGS__; } break;                       \
+  }

@@ -1,0 +1,100 @@
+"""Host-side mirror of the reference's packed-weight call surface, on torch device tensors.
+
+The reference host picks a kernel by GGUF type id (``gemv_h``/``gemm_h``,
+native/host/ridge_decode.vyb:295-328) and fills a parameter block
+(``set_gemv``/``set_gemm``, ridge_decode.vyb:264-279). Here the same choice is
+``gemv(ty, ...)``/``dequant(ty, ...)`` and the parameters travel as C-ABI arguments.
+All calls are asynchronous on torch's current stream and allocate only their outputs.
+"""
+
+import torch
+
+from . import _lib
+from ._lib import BF16, F16, F32, F64, Q4_GGML, Q4_INTERLEAVED, call  # noqa: F401
+
+GGML_Q4_0 = 2   # ggml_type ids, as the reference dispatches on them
+GGML_Q8_0 = 8
+
+BLOCK_BYTES = {GGML_Q4_0: 18, GGML_Q8_0: 34}
+
+_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.float64: F64}
+
+
+def _dt(t):
+    try:
+        return _DT[t]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t}") from None
+
+
+def _ptr(t):
+    if t is None:
+        return 0
+    if not t.is_cuda:
+        raise ValueError("tensor must be on the GPU")
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return t.data_ptr()
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def row_bytes(ty, K):
+    return (K // 32) * BLOCK_BYTES[ty]
+
+
+def dequant(ty, W, nblocks, out_dtype=torch.float32, order=Q4_GGML, out=None):
+    """Decode nblocks packed blocks to out [nblocks*32] (the bit-exact gate path)."""
+    if out is None:
+        out = torch.empty(nblocks * 32, dtype=out_dtype, device=W.device)
+    if ty == GGML_Q4_0:
+        call("vybdq_dequant_q4_0", _ptr(W), _ptr(out), nblocks, order, _dt(out.dtype), _stream())
+    elif ty == GGML_Q8_0:
+        call("vybdq_dequant_q8_0", _ptr(W), _ptr(out), nblocks, _dt(out.dtype), _stream())
+    else:
+        raise ValueError(f"unsupported GGUF type {ty}")
+    return out
+
+
+def gemv(ty, W, X, N, K, y_dtype=torch.float32, residual=None, order=Q4_GGML, out=None):
+    """Y[m, n] = RS[m, n] + sum_k X[m, k] W[n, k]; X [M, K] or [K]; returns Y [M, N] or [N]."""
+    squeeze = X.dim() == 1
+    X2 = X.reshape(1, K) if squeeze else X
+    M = X2.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=y_dtype, device=X.device)
+    if residual is not None and residual.dtype != out.dtype:
+        raise TypeError("residual must have the output dtype")
+    if ty == GGML_Q4_0:
+        call("vybdq_gemv_q4_0", _ptr(W), _ptr(X2), _ptr(out), M, N, K, _dt(X2.dtype), _dt(out.dtype),
+             _ptr(residual), order, _stream())
+    elif ty == GGML_Q8_0:
+        call("vybdq_gemv_q8_0", _ptr(W), _ptr(X2), _ptr(out), M, N, K, _dt(X2.dtype), _dt(out.dtype),
+             _ptr(residual), _stream())
+    else:
+        raise ValueError(f"unsupported GGUF type {ty}")
+    return out.reshape(N) if squeeze else out
+
+
+def gemv_q4_0_seg3(X, K, segs, order=Q4_GGML):
+    """Fused q4_0 GEMVs sharing X. segs: list of up to 3 (W, Y, N) with Y preallocated."""
+    args = []
+    for i in range(3):
+        if i < len(segs):
+            W, Y, N = segs[i]
+            args += [_ptr(W), _ptr(Y), N, _dt(Y.dtype)]
+        else:
+            args += [0, 0, 0, F32]
+    call("vybdq_gemv_q4_0_seg3", _ptr(X), K, _dt(X.dtype), order, *args, _stream())
+
+
+def quant_q8_act(X):
+    """xq8 quantizer: X [M, K] -> (Xq int8 [M, K], Xs float32 [M, K/32])."""
+    X2 = X.reshape(-1, X.shape[-1])
+    M, K = X2.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=X.device)
+    d = torch.empty((M, K // 32), dtype=torch.float32, device=X.device)
+    call("vybdq_quant_q8_act", _ptr(X2), _ptr(q), _ptr(d), M, K, _dt(X2.dtype), _stream())
+    return q, d

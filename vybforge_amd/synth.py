@@ -1,0 +1,29 @@
+"""Seeded synthetic packed weights and activations (numpy), shaped like the benchmark inputs.
+
+q4_0 / Q8_0 blocks: fp16 scale d = |N(0, 0.01)|, nibbles uniform in [0, 15] / int8 uniform in
+[-127, 127]. Rows are GGUF row layout (row n = output n, K/32 consecutive blocks).
+"""
+
+import numpy as np
+
+
+def q4_0_weights(rng, N, K):
+    """Packed q4_0 bytes uint8 [N * K/32 * 18]."""
+    nb = N * (K // 32)
+    blk = np.empty((nb, 18), np.uint8)
+    blk[:, 0:2] = np.abs(rng.normal(0.0, 0.01, nb)).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    blk[:, 2:] = rng.integers(0, 256, (nb, 16), dtype=np.uint8)
+    return blk.reshape(-1)
+
+
+def q8_0_weights(rng, N, K):
+    """Packed Q8_0 bytes uint8 [N * K/32 * 34]."""
+    nb = N * (K // 32)
+    blk = np.empty((nb, 34), np.uint8)
+    blk[:, 0:2] = np.abs(rng.normal(0.0, 0.01, nb)).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    blk[:, 2:] = rng.integers(-127, 128, (nb, 32), dtype=np.int8).view(np.uint8)
+    return blk.reshape(-1)
+
+
+def activations(rng, shape, dtype=np.float32):
+    return rng.standard_normal(shape).astype(dtype)
