@@ -39,13 +39,14 @@ def test_abi_version():
 
 @pytest.mark.parametrize("args,code,text", [
     # (W, X, Y, M, N, K, x_dt, y_dt, RS, order, stream)
-    ((1, 1, 1, 1, 16, 48, 0, 0, 0, 0, 0), -2, "K must be"),        # K % 32 != 0
-    ((1, 1, 1, 9, 16, 64, 0, 0, 0, 0, 0), -2, "M must be"),        # M > 8
-    ((0, 1, 1, 1, 16, 64, 0, 0, 0, 0, 0), -1, "null W"),
-    ((1, 1, 1, 1, 16, 64, 7, 0, 0, 0, 0), -1, "x_dt"),
-    ((1, 1, 1, 1, 16, 64, 0, 0, 0, 5, 0), -1, "order"),
-    ((2, 1, 1, 1, 16, 64, 0, 0, 0, 0, 0), -3, "aligned"),          # W not 4-byte aligned
-    ((4, 1, 1, 1, 0, 64, 0, 0, 0, 0, 0), -2, "N must be"),
+    ((1, 16, 1, 1, 16, 48, 0, 0, 0, 0, 0), -2, "K must be"),        # K % 32 != 0
+    ((1, 16, 1, 9, 16, 64, 0, 0, 0, 0, 0), -2, "M must be"),        # M > 8
+    ((0, 16, 1, 1, 16, 64, 0, 0, 0, 0, 0), -1, "null W"),
+    ((1, 16, 1, 1, 16, 64, 7, 0, 0, 0, 0), -1, "x_dt"),
+    ((1, 16, 1, 1, 16, 64, 0, 0, 0, 5, 0), -1, "order"),
+    ((2, 16, 1, 1, 16, 64, 0, 0, 0, 0, 0), -3, "W must be"),        # W not 4-byte aligned
+    ((4, 8, 1, 1, 16, 64, 0, 0, 0, 0, 0), -3, "X must be"),         # X not 16-byte aligned
+    ((4, 16, 1, 1, 0, 64, 0, 0, 0, 0, 0), -2, "N must be"),
 ])
 def test_gemv_preconditions(args, code, text):
     from vybforge_amd import _lib

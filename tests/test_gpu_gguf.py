@@ -15,7 +15,20 @@ TDT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16, "f64"
 
 
 def to_dev(a, dev):
-    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return torch.from_numpy(np.array(a, copy=True)).to(dev)
+
+
+def gate(y, ref, out_dtype=torch.float32):
+    """rel_maxnorm after allowing half an ulp of the output type per element: a 16-bit output
+    rounds the float32 accumulator once more, which the 2e-3 accumulation gate does not cover."""
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    if out_dtype in (torch.float16, torch.bfloat16):
+        mant = 10 if out_dtype == torch.float16 else 7
+        half_ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - mant - 1)
+        err = np.maximum(np.abs(y - ref) - half_ulp, 0.0)
+        return float(err.max() / max(np.abs(ref).max(), 1e-300))
+    return matmul.rel_maxnorm(y, ref)
 
 
 def x_as(x32, name, dev):
@@ -88,7 +101,7 @@ def test_gemv_q4_0_dtypes_batch(dev, xdt, ydt, M):
     xd, x64 = x_as(synth.activations(rng, (M, K)), xdt, dev)
     y = ops.gemv(ops.GGML_Q4_0, to_dev(raw, dev), xd, N, K, TDT[ydt]).to(torch.float64).cpu().numpy()
     ref = matmul.gemv_q4_0_f64(raw, x64, N, K)
-    assert matmul.rel_maxnorm(y, ref) < TOL
+    assert gate(y, ref, TDT[ydt]) < TOL
 
 
 @pytest.mark.parametrize("ydt", ["f32", "f64", "f16"])
@@ -102,7 +115,7 @@ def test_gemv_residual(dev, ydt):
     y = ops.gemv(ops.GGML_Q4_0, to_dev(raw, dev), to_dev(x, dev), N, K, TDT[ydt],
                  residual=rs_t.to(dev)).to(torch.float64).cpu().numpy()
     ref = matmul.gemv_q4_0_f64(raw, x, N, K, residual=rs_t.to(torch.float64).numpy())[0]
-    assert matmul.rel_maxnorm(y, ref) < TOL
+    assert gate(y, ref, TDT[ydt]) < TOL
 
 
 @pytest.mark.parametrize("N,K", [(5120, 5120), (48, 5120), (4096, 512), (77, 96)])
@@ -135,7 +148,7 @@ def test_gemv_seg3_qkv(dev):
     ops.gemv_q4_0_seg3(xd, K, [(to_dev(r, dev), y, n) for r, y, n in zip(raws, ys, shapes)])
     for r, y, n in zip(raws, ys, shapes):
         ref = matmul.gemv_q4_0_f64(r, x64, n, K)[0]
-        assert matmul.rel_maxnorm(y.to(torch.float64).cpu().numpy(), ref) < TOL
+        assert gate(y.to(torch.float64).cpu().numpy(), ref, torch.float16) < TOL
 
 
 def test_gemv_deterministic(dev):

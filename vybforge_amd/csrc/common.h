@@ -6,7 +6,7 @@
 #include <stdint.h>
 #include <string>
 
-#include "../../include/vybdq.h"
+#include "vybdq.h"
 
 namespace vybdq {
 

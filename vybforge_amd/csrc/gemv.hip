@@ -6,19 +6,22 @@
 // 68 B for Q8_0. Rows are 4-byte aligned when K % 64 == 0, so a lane fetches its pair with
 // dword-aligned vector loads and re-aligns the 2-byte-offset half with v_alignbit. The G
 // lanes of a row-slot walk the row's pairs with stride G (consecutive lanes read consecutive
-// pairs: a row-slot's loads cover one contiguous span), each lane keeps one float32
-// accumulator per X row, and the G partials are combined by a fixed xor-shuffle tree.
+// pairs), each lane keeps one float32 accumulator per X row, and the G partials are combined
+// by a fixed xor-shuffle tree. G (8..64) is picked per launch so that the grid holds enough
+// waves to cover HBM latency while each lane's pairs fit one batch of registers.
 //
-// Arithmetic. X is staged once per workgroup in LDS as fp16 pairs, permuted so that pair s
-// of a quant dword lines up with the two quants that one v_and_or_b32 extracts:
+// Latency. Every lane issues the loads of its first batch of pairs before anything else;
+// the x stage (coalesced 16-B loads -> LDS, block sums by 4-lane shuffles, one barrier)
+// runs under those loads.
+//
+// Arithmetic. x is staged as fp16 in natural order. A quant byte becomes an fp16 with
 //   fp16 bits 0x6400 | v == 1024 + v   (v < 1024)
-// so each quant dword turns into fp16 pairs (1024+q0, 1024+q1) with one op per pair, and
-// v_dot2_f32_f16 multiplies-and-accumulates two weights per op in float32. Per block,
-//   sum_k x_k (q_k - OFF) = dot - (1024 + OFF) * sum_k x_k,
-// with sum_k x_k of the same fp16-rounded x precomputed at staging, then y += d * partial.
-// OFF = 8 for q4_0 nibbles; Q8_0 bytes are biased to unsigned (q ^ 0x80 = q + 128), OFF = 128.
-// Float32 X is rounded to fp16 at staging; the float32 accumulation error budget is far
-// inside the 2e-3 gate (documented with the measurements).
+// built by v_perm_b32 from the masked quant dword and a 0x64 byte constant, two consecutive
+// weights per register, and v_dot2_f32_f16 multiplies-and-accumulates two weights per op in
+// float32. Per block, sum_k x_k (q_k - OFF) = dot - (1024 + OFF) * sum_k x_k with the block
+// sum of the same fp16 x from the stage, then y += d * partial. OFF = 8 for q4_0 nibbles;
+// Q8_0 bytes are biased to unsigned (q ^ 0x80 = q + 128), OFF = 128. Float32 x is rounded to
+// fp16 at staging; the resulting error (~1e-4 relative) is well inside the 2e-3 gate.
 #include "common.h"
 
 namespace vybdq {
@@ -30,42 +33,17 @@ template <> struct Fmt<FMT_Q4_0> {
   static constexpr int PAIR_BYTES = 36;
   static constexpr int PAIR_DWORDS = 9;
   static constexpr int QDW = 4;                 // quant dwords per block
+  static constexpr int U = 4;                   // pairs per load batch (VGPR budget vs occupancy)
   static constexpr float CORR = 1032.0f;        // 1024 + 8
 };
 template <> struct Fmt<FMT_Q8_0> {
   static constexpr int PAIR_BYTES = 68;
   static constexpr int PAIR_DWORDS = 17;
   static constexpr int QDW = 8;
+  static constexpr int U = 2;
   static constexpr float CORR = 1152.0f;        // 1024 + 128
 };
 
-// Element index (within a 32-weight block) of the two quants that land in half s of the
-// fp16 pair extracted from quant dword t.
-//   q4_0: dword t holds qs bytes 4t..4t+3; s = 0..3 selects (w >> 4s) & 0x000F000F,
-//         i.e. bytes (0,2) low, (0,2) high, (1,3) low, (1,3) high.
-//   Q8_0: dword t holds q[4t..4t+3]; s = 0 -> bytes (0,2), s = 1 -> bytes (1,3).
-template <int FMT, int ORDER>
-__device__ __forceinline__ void pair_elems(int t, int s, int &e0, int &e1) {
-  if constexpr (FMT == FMT_Q8_0) {
-    e0 = 4 * t + s;
-    e1 = 4 * t + s + 2;
-  } else {
-    const int byte_a = 4 * t + (s >> 1);      // byte 0 or 1 of the dword
-    const int byte_b = byte_a + 2;            // byte 2 or 3
-    const int hi = s & 1;                     // high nibble?
-    if constexpr (ORDER == VYBDQ_Q4_GGML) {
-      e0 = byte_a + 16 * hi;
-      e1 = byte_b + 16 * hi;
-    } else {
-      e0 = 2 * byte_a + hi;
-      e1 = 2 * byte_b + hi;
-    }
-  }
-}
-
-// LDS layout per X row m: chunk c (16 B = 4 fp16 pairs) of pair p at xs[m][c * P + p], so the
-// G lanes of a row-slot, which read consecutive pairs, read consecutive 16-B LDS words
-// (conflict-free); block sums at sx[m][2p + h].
 struct Segs {
   const uint8_t *W[3];
   void *Y[3];
@@ -74,44 +52,57 @@ struct Segs {
   int64_t end[3];  // cumulative row ends
 };
 
-template <int FMT, int ORDER, int XDT, int M>
-__device__ __forceinline__ void stage_x(const void *__restrict__ X, int64_t K, int P, u4 *xs,
-                                        float *sx) {
-  constexpr int CH_PER_BLOCK = 4;                       // 16-B chunks per block
-  const int nchunks = P * 2 * CH_PER_BLOCK;
-  for (int m = 0; m < M; ++m) {
-    const void *xm = nullptr;
-    if constexpr (XDT == VYBDQ_F32) xm = static_cast<const float *>(X) + m * K;
-    else xm = static_cast<const uint16_t *>(X) + m * K;
-    for (int c = threadIdx.x; c < nchunks; c += blockDim.x) {
-      const int j = c / P;          // chunk within pair 0..7
-      const int p = c - j * P;      // pair
-      const int h = j >> 2;         // block within pair
-      const int64_t kb = (2 * static_cast<int64_t>(p) + h) * 32;
-      u4 out;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        // chunk j%4 holds 4 consecutive fp16 pairs (t, s) of this block
-        const int idx = (j & 3) * 4 + q;
-        int t, s;
-        if constexpr (FMT == FMT_Q4_0) { t = idx >> 2; s = idx & 3; }
-        else { t = idx >> 1; s = idx & 1; }
-        int e0, e1;
-        pair_elems<FMT, ORDER>(t, s, e0, e1);
-        const _Float16 a = static_cast<_Float16>(load_elem<XDT>(xm, kb + e0));
-        const _Float16 b = static_cast<_Float16>(load_elem<XDT>(xm, kb + e1));
-        h2 v = {a, b};
-        out[q] = __builtin_bit_cast(uint32_t, v);
-      }
-      xs[m * nchunks + j * P + p] = out;
-    }
-    for (int b = threadIdx.x; b < 2 * P; b += blockDim.x) {
-      float s = 0.f;
-      for (int e = 0; e < 32; ++e)
-        s += static_cast<float>(static_cast<_Float16>(load_elem<XDT>(xm, static_cast<int64_t>(b) * 32 + e)));
-      sx[m * 2 * P + b] = s;
-    }
+// LDS x stage, per X row m: pair p (64 fp16, natural order) at byte m*P*144 + 144*p (a 16-B pad
+// per pair keeps the G lanes that read consecutive pairs on distinct banks); block sums at
+// sx[m*2P + b].
+constexpr int XPAIR_STRIDE = 144;
+
+// Raw x chunk (8 consecutive elements) -> registers: XW = 4 dwords for fp16/bf16, 8 for f32.
+template <int XW>
+__device__ __forceinline__ void load_x_chunk(const void *X, int64_t i, uint32_t (&r)[XW]) {
+  if constexpr (XW == 8) {
+    const u4 *p = reinterpret_cast<const u4 *>(static_cast<const float *>(X) + i);
+    const u4 a = p[0], b = p[1];
+    r[0] = a[0]; r[1] = a[1]; r[2] = a[2]; r[3] = a[3];
+    r[4] = b[0]; r[5] = b[1]; r[6] = b[2]; r[7] = b[3];
+  } else {
+    const u4 v = *reinterpret_cast<const u4 *>(static_cast<const uint16_t *>(X) + i);
+    r[0] = v[0]; r[1] = v[1]; r[2] = v[2]; r[3] = v[3];
   }
+}
+
+// Convert a raw chunk to 4 fp16 pairs, store it at its LDS slot and reduce the block sums:
+// chunk c holds x[8c .. 8c+7] (for every X row m, since K = 64 P), lives in pair c>>3 at
+// (c>>3)*144 + (c&7)*16, and its 32-element block is c>>2. The 4 chunks of a block belong to 4
+// consecutive threads, which combine their partial sums with two xor shuffles.
+template <int XW>
+__device__ __forceinline__ void stage_chunk(const uint32_t (&r)[XW], int xdt, int c, char *lds, float *sx) {
+  uint32_t h[4];
+  if constexpr (XW == 8) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      h[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(__uint_as_float(r[2 * j])),
+                                             static_cast<_Float16>(__uint_as_float(r[2 * j + 1]))});
+  } else if (xdt == VYBDQ_BF16) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      h[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(__uint_as_float(r[j] << 16)),
+                                             static_cast<_Float16>(__uint_as_float(r[j] & 0xffff0000u))});
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) h[j] = r[j];
+  }
+  *reinterpret_cast<u4 *>(lds + (c >> 3) * XPAIR_STRIDE + (c & 7) * 16) = u4{h[0], h[1], h[2], h[3]};
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const h2 v = __builtin_bit_cast(h2, h[j]);
+    s += static_cast<float>(v[0]);
+    s += static_cast<float>(v[1]);
+  }
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  if ((c & 3) == 0) sx[c >> 2] = s;
 }
 
 typedef uint32_t u4a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -121,19 +112,55 @@ __device__ __forceinline__ void load_pair(const uint8_t *p, uint32_t (&dw)[Fmt<F
   const u4a4 *v = reinterpret_cast<const u4a4 *>(p);
 #pragma unroll
   for (int i = 0; i < Fmt<FMT>::PAIR_DWORDS / 4; ++i) {
-    const u4a4 t = __builtin_nontemporal_load(v + i);
+    const u4a4 t = v[i];
     dw[4 * i + 0] = t[0];
     dw[4 * i + 1] = t[1];
     dw[4 * i + 2] = t[2];
     dw[4 * i + 3] = t[3];
   }
   dw[Fmt<FMT>::PAIR_DWORDS - 1] =
-      __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p) + Fmt<FMT>::PAIR_DWORDS - 1);
+      reinterpret_cast<const uint32_t *>(p)[Fmt<FMT>::PAIR_DWORDS - 1];
+}
+
+// v_perm_b32 selectors: {S0 = 0x64646464, S1 = v} -> fp16 pair (0x6400 | v.byte a, 0x6400 | v.byte b)
+constexpr uint32_t SEL_B01 = 0x04010400u;
+constexpr uint32_t SEL_B23 = 0x04030402u;
+constexpr uint32_t C64 = 0x64646464u;
+
+// The 16 fp16 weight pairs (1024 + v_e, 1024 + v_e+1), e = 2i, of one block in element order.
+template <int FMT, int ORDER>
+__device__ __forceinline__ void unpack_block(const uint32_t (&q)[Fmt<FMT>::QDW], h2 (&wv)[16]) {
+#pragma unroll
+  for (int t = 0; t < Fmt<FMT>::QDW; ++t) {
+    if constexpr (FMT == FMT_Q8_0) {
+      const uint32_t u = q[t] ^ 0x80808080u;
+      wv[2 * t] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, u, SEL_B01));
+      wv[2 * t + 1] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, u, SEL_B23));
+    } else {
+      const uint32_t lo = q[t] & 0x0F0F0F0Fu;
+      const uint32_t hi = (q[t] >> 4) & 0x0F0F0F0Fu;
+      if constexpr (ORDER == VYBDQ_Q4_GGML) {
+        // qs bytes 4t..4t+3: low nibbles = elements 4t..4t+3, high = 16+4t..16+4t+3
+        wv[2 * t] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, lo, SEL_B01));
+        wv[2 * t + 1] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, lo, SEL_B23));
+        wv[8 + 2 * t] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, hi, SEL_B01));
+        wv[8 + 2 * t + 1] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, hi, SEL_B23));
+      } else {
+        // byte s = (element 2s low, 2s+1 high): interleave low/high bytes first
+        const uint32_t a = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // lo0 hi0 lo1 hi1
+        const uint32_t b = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // lo2 hi2 lo3 hi3
+        wv[4 * t] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, a, SEL_B01));
+        wv[4 * t + 1] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, a, SEL_B23));
+        wv[4 * t + 2] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, b, SEL_B01));
+        wv[4 * t + 3] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, b, SEL_B23));
+      }
+    }
+  }
 }
 
 // Dot products of one pair (two blocks) of one row with the M staged x rows.
-template <int FMT, int M>
-__device__ __forceinline__ void pair_dot(const uint32_t (&dw)[Fmt<FMT>::PAIR_DWORDS], const u4 *xs,
+template <int FMT, int ORDER, int M>
+__device__ __forceinline__ void pair_dot(const uint32_t (&dw)[Fmt<FMT>::PAIR_DWORDS], const char *lds,
                                          const float *sx, int P, int p, float (&acc)[M]) {
   constexpr int QDW = Fmt<FMT>::QDW;
 #pragma unroll
@@ -149,33 +176,21 @@ __device__ __forceinline__ void pair_dot(const uint32_t (&dw)[Fmt<FMT>::PAIR_DWO
       for (int t = 0; t < QDW; ++t) q[t] = dw[QDW + 1 + t];
       d = half_bits_to_f32(dw[QDW] >> 16);
     }
-    // fp16 pairs (1024 + v0, 1024 + v1)
     h2 wv[16];
-#pragma unroll
-    for (int t = 0; t < QDW; ++t) {
-      if constexpr (FMT == FMT_Q4_0) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          wv[4 * t + s] = __builtin_bit_cast(h2, ((q[t] >> (4 * s)) & 0x000F000Fu) | 0x64006400u);
-      } else {
-        const uint32_t u = q[t] ^ 0x80808080u;
-        wv[2 * t + 0] = __builtin_bit_cast(h2, (u & 0x00FF00FFu) | 0x64006400u);
-        wv[2 * t + 1] = __builtin_bit_cast(h2, ((u >> 8) & 0x00FF00FFu) | 0x64006400u);
-      }
-    }
+    unpack_block<FMT, ORDER>(q, wv);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const u4 *xc = xs + m * P * 8 + (4 * h) * P + p;
+      const u4 *xc = reinterpret_cast<const u4 *>(lds + m * P * XPAIR_STRIDE + p * XPAIR_STRIDE + 64 * h);
       float ps = 0.f;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const u4 xv = xc[c * P];
+        const u4 xv = xc[c];
 #pragma unroll
-        for (int q2 = 0; q2 < 4; ++q2) {
+        for (int j = 0; j < 4; ++j) {
           // copy the element to a scalar first: bit-casting a vector element expression
           // directly reads element 0 with this compiler
-          const uint32_t xw = xv[q2];
-          ps = __builtin_amdgcn_fdot2(wv[4 * c + q2], __builtin_bit_cast(h2, xw), ps, false);
+          const uint32_t xw = xv[j];
+          ps = __builtin_amdgcn_fdot2(wv[4 * c + j], __builtin_bit_cast(h2, xw), ps, false);
         }
       }
       const float part = fmaf(-Fmt<FMT>::CORR, sx[m * 2 * P + 2 * p + h], ps);
@@ -184,47 +199,73 @@ __device__ __forceinline__ void pair_dot(const uint32_t (&dw)[Fmt<FMT>::PAIR_DWO
   }
 }
 
-template <int FMT, int G, int ORDER, int XDT, int M>
-__global__ void __launch_bounds__(256) k_gemv_pair(const void *__restrict__ X, int64_t K, Segs segs) {
+template <int FMT, int G, int ORDER, int M, int XW>
+__global__ void __launch_bounds__(256) k_gemv_pair(const void *__restrict__ X, int xdt, int64_t K, Segs segs) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr int U = Fmt<FMT>::U;
+  constexpr int PD = Fmt<FMT>::PAIR_DWORDS;
+  constexpr int XC = 5;  // x chunks per thread prefetched ahead of the weight loads
   const int P = static_cast<int>(K >> 6);
-  u4 *xs = reinterpret_cast<u4 *>(smem);
-  float *sx = reinterpret_cast<float *>(smem + static_cast<size_t>(M) * P * 8 * 16);
-  stage_x<FMT, ORDER, XDT, M>(X, K, P, xs, sx);
-  __syncthreads();
+  char *lds = smem;
+  float *sx = reinterpret_cast<float *>(smem + static_cast<size_t>(M) * P * XPAIR_STRIDE);
 
   const int lane = threadIdx.x & 63;
   const int ks = lane % G;
   const int rs = lane / G;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / G) + (threadIdx.x >> 6) * (64 / G) + rs;
-  const int64_t total = segs.end[2];
-  const bool active = row < total;
+  const bool active = row < segs.end[2];
   int sg = 0;
   if (row >= segs.end[0]) sg = (row >= segs.end[1]) ? 2 : 1;
-  const int64_t lrow = row - (sg == 0 ? 0 : segs.end[sg - 1]);
+  if (!active) sg = 0;
+  const int64_t lrow = active ? row - (sg == 0 ? 0 : segs.end[sg - 1]) : 0;
   const int64_t rowbytes = static_cast<int64_t>(P) * Fmt<FMT>::PAIR_BYTES;
   const uint8_t *wrow = segs.W[sg] + lrow * rowbytes;
+  const int npairs = active && ks < P ? (P - ks + G - 1) / G : 0;
+  // loads are unconditional (no divergent branches, no register shuffling): a lane past its
+  // last pair re-reads a pair of its own row (inactive lanes: row 0 of segment 0)
+  auto pair_ptr = [&](int i) {
+    int p = ks + G * i;
+    p = p < P ? p : (ks < P ? ks : 0);
+    return wrow + static_cast<int64_t>(p) * Fmt<FMT>::PAIR_BYTES;
+  };
+
+  // 1. x chunks (L2-resident, short latency) first, so waiting on them never waits on weights
+  const int nchunk = M * 8 * P;
+  uint32_t xr[XC][XW];
+#pragma unroll
+  for (int j = 0; j < XC; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    if (c < nchunk) load_x_chunk<XW>(X, 8 * static_cast<int64_t>(c), xr[j]);
+  }
+  // 2. the first batch of weight pairs
+  uint32_t dw[U][PD];
+#pragma unroll
+  for (int u = 0; u < U; ++u) load_pair<FMT>(pair_ptr(u), dw[u]);
+  // 3. x -> LDS while the weights stream in
+#pragma unroll
+  for (int j = 0; j < XC; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    if (c < nchunk) stage_chunk<XW>(xr[j], xdt, c, lds, sx);
+  }
+  for (int c = threadIdx.x + 256 * XC; c < nchunk; c += 256) {
+    uint32_t r[XW];
+    load_x_chunk<XW>(X, 8 * static_cast<int64_t>(c), r);
+    stage_chunk<XW>(r, xdt, c, lds, sx);
+  }
+  __syncthreads();
 
   float acc[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = 0.f;
 
-  if (active) {
-    // U pairs in flight per lane: all loads of a batch are issued before any use.
-    constexpr int U = FMT == FMT_Q4_0 ? 4 : 2;
-    for (int p0 = ks; p0 < P; p0 += G * U) {
-      uint32_t dw[U][Fmt<FMT>::PAIR_DWORDS];
+  for (int i0 = 0; i0 < npairs; i0 += U) {
+    if (i0 > 0) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int p = p0 + u * G;
-        if (p < P) load_pair<FMT>(wrow + static_cast<int64_t>(p) * Fmt<FMT>::PAIR_BYTES, dw[u]);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int p = p0 + u * G;
-        if (p < P) pair_dot<FMT, M>(dw[u], xs, sx, P, p, acc);
-      }
+      for (int u = 0; u < U; ++u) load_pair<FMT>(pair_ptr(i0 + u), dw[u]);
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i0 + u < npairs) pair_dot<FMT, ORDER, M>(dw[u], lds, sx, P, ks + G * (i0 + u), acc);
   }
 #pragma unroll
   for (int m = 0; m < M; ++m) {
@@ -293,40 +334,61 @@ __global__ void __launch_bounds__(64) k_gemv_generic(const void *__restrict__ X,
 
 static constexpr int kMaxLds = 160 * 1024;
 
-template <int FMT, int ORDER, int XDT, int M>
-static int launch_pair_m(const void *X, int64_t K, const Segs &segs, hipStream_t s) {
+// Lanes per row: the smallest G whose grid reaches ~4 waves per CU while each lane's pairs
+// fit one load batch.
+template <int FMT>
+static int pick_g(int64_t rows, int P) {
+  constexpr int U = Fmt<FMT>::U;
+  int G = 8;
+  while (G < 64 && (rows * G / 64 < 1024 || (P + G - 1) / G > U)) G *= 2;
+  return G;
+}
+
+template <int FMT, int G, int ORDER, int M, int XW>
+static int launch_g(const void *X, int xdt, int64_t K, const Segs &segs, hipStream_t s) {
   const int64_t rows = segs.end[2];
   const int P = static_cast<int>(K / 64);
-  const size_t lds = static_cast<size_t>(M) * P * (8 * 16 + 2 * 4);
+  const size_t lds = static_cast<size_t>(M) * P * (XPAIR_STRIDE + 2 * 4);
   if (lds > static_cast<size_t>(kMaxLds)) return set_error(VYBDQ_ERR_SHAPE, "gemv: K too large for the LDS x stage at this M");
-  // lanes per row: 8 keeps every BASELINE K (2560, 4096, 9728, 6144, 2048) a whole number of
-  // pair sweeps; small row counts use 16 lanes to put more waves on the chip.
-  constexpr int G = 8;
-  int threads = 256;
-  if (rows <= 4096) threads = 128;
-  if (rows <= 1024) threads = 64;
-  const int rows_per_wg = threads / G;
+  constexpr int threads = 256;
+  constexpr int rows_per_wg = threads / G;
   const unsigned grid = static_cast<unsigned>((rows + rows_per_wg - 1) / rows_per_wg);
   if (lds > 64 * 1024) {
     static bool raised = false;  // one attribute call per instantiation
     if (!raised) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_pair<FMT, G, ORDER, XDT, M>),
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_pair<FMT, G, ORDER, M, XW>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
       if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("gemv: LDS attribute: ") + hipGetErrorString(e));
       raised = true;
     }
   }
-  hipLaunchKernelGGL((k_gemv_pair<FMT, G, ORDER, XDT, M>), dim3(grid), dim3(threads), lds, s, X, K, segs);
+  hipLaunchKernelGGL((k_gemv_pair<FMT, G, ORDER, M, XW>), dim3(grid), dim3(threads), lds, s, X, xdt, K, segs);
   return check_launch("gemv");
 }
 
-template <int FMT, int ORDER, int XDT>
-static int launch_pair(const void *X, int64_t M, int64_t K, const Segs &segs, hipStream_t s) {
+template <int FMT, int ORDER, int M, int XW>
+static int launch_mx(const void *X, int xdt, int64_t K, const Segs &segs, hipStream_t s) {
+  switch (pick_g<FMT>(segs.end[2], static_cast<int>(K / 64))) {
+    case 8: return launch_g<FMT, 8, ORDER, M, XW>(X, xdt, K, segs, s);
+    case 16: return launch_g<FMT, 16, ORDER, M, XW>(X, xdt, K, segs, s);
+    case 32: return launch_g<FMT, 32, ORDER, M, XW>(X, xdt, K, segs, s);
+    default: return launch_g<FMT, 64, ORDER, M, XW>(X, xdt, K, segs, s);
+  }
+}
+
+template <int FMT, int ORDER, int M>
+static int launch_m(const void *X, int xdt, int64_t K, const Segs &segs, hipStream_t s) {
+  if (xdt == VYBDQ_F32) return launch_mx<FMT, ORDER, M, 8>(X, xdt, K, segs, s);
+  return launch_mx<FMT, ORDER, M, 4>(X, xdt, K, segs, s);
+}
+
+template <int FMT, int ORDER>
+static int launch_pair(const void *X, int xdt, int64_t M, int64_t K, const Segs &segs, hipStream_t s) {
   switch (M) {
-    case 1: return launch_pair_m<FMT, ORDER, XDT, 1>(X, K, segs, s);
-    case 2: return launch_pair_m<FMT, ORDER, XDT, 2>(X, K, segs, s);
-    case 3: return launch_pair_m<FMT, ORDER, XDT, 3>(X, K, segs, s);
-    default: return launch_pair_m<FMT, ORDER, XDT, 4>(X, K, segs, s);
+    case 1: return launch_m<FMT, ORDER, 1>(X, xdt, K, segs, s);
+    case 2: return launch_m<FMT, ORDER, 2>(X, xdt, K, segs, s);
+    case 3: return launch_m<FMT, ORDER, 3>(X, xdt, K, segs, s);
+    default: return launch_m<FMT, ORDER, 4>(X, xdt, K, segs, s);
   }
 }
 
@@ -349,8 +411,7 @@ static int gemv_dispatch(const void *X, int64_t M, int64_t K, int x_dt, Segs seg
       if (sc.RS[i]) sc.RS[i] = static_cast<const char *>(sc.RS[i]) + m0 * n * dt_size(segs.ydt[i]);
     }
     const void *Xc = static_cast<const char *>(X) + m0 * K * xs;
-    int rc;
-    VYBDQ_DISPATCH_IN(x_dt, XDT, rc = launch_pair<FMT, ORDER, XDT>(Xc, mc, K, sc, s));
+    const int rc = launch_pair<FMT, ORDER>(Xc, x_dt, mc, K, sc, s);
     if (rc) return rc;
   }
   return VYBDQ_OK;
@@ -359,6 +420,7 @@ static int gemv_dispatch(const void *X, int64_t M, int64_t K, int x_dt, Segs seg
 static int gemv_common(int fmt, int order, uint64_t X, int64_t M, int64_t K, int x_dt, Segs &segs,
                        uint64_t stream) {
   VYBDQ_REQUIRE(X, VYBDQ_ERR_ARG, "null X");
+  VYBDQ_REQUIRE((X & 15) == 0, VYBDQ_ERR_ALIGN, "X must be 16-byte aligned");
   VYBDQ_REQUIRE(dt_valid_in(x_dt), VYBDQ_ERR_ARG, "x_dt must be F32, F16 or BF16");
   VYBDQ_REQUIRE(M >= 1 && M <= 8, VYBDQ_ERR_SHAPE, "M must be in [1, 8]");
   VYBDQ_REQUIRE(K > 0 && K % 32 == 0, VYBDQ_ERR_SHAPE, "K must be a positive multiple of 32");
