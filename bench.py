@@ -33,7 +33,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="stack", choices=["stack", "gemv1"])
+    ap.add_argument("--config", default="stack", choices=["stack", "stack_chain", "gemv1"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--seed", type=int, default=0)
     return ap.parse_args()
@@ -125,11 +125,29 @@ def cpu_baseline_stack(target_s=12.0):
                        "numpy f32 decode + OpenBLAS matvec, 1 thread")
 
 
+def stack_chain(ops, layers, a, dev):
+    """The token as one persistent chain: 144 dependent stages, one launch."""
+    H, Q, KV, I = QWEN3_4B["hidden"], QWEN3_4B["q"], QWEN3_4B["kv"], QWEN3_4B["inter"]
+    stages = []
+    for L in layers:
+        stages.append(ops.pblock(a["x_attn"], H, [(L["q"], a["yq"], Q), (L["k"], a["yk"], KV), (L["v"], a["yv"], KV)]))
+        stages.append(ops.pblock(a["x_o"], Q, [(L["o"], a["yo"], H)]))
+        stages.append(ops.pblock(a["x_mlp"], H, [(L["gate"], a["yg"], I), (L["up"], a["yu"], I)]))
+        stages.append(ops.pblock(a["x_down"], I, [(L["down"], a["yd"], H)]))
+    return ops.GemvChain(ops.GGML_Q4_0, stages, dev)
+
+
 def run_stack(args, torch, dev):
     from vybforge_amd import ops
     shapes, bytes_tok, flops_tok, wbytes_layer = stack_bytes()
     layers, acts = build_stack(torch, dev, args.seed)
-    launches = stack_launches(ops, layers, acts)
+    if args.config == "stack_chain":
+        chain = stack_chain(ops, layers, acts, dev)
+        launches = [chain]
+        kernel = "k_gemv_chain<q4_0> (one persistent launch per token, 144 dependent stages)"
+    else:
+        launches = stack_launches(ops, layers, acts)
+        kernel = "k_gemv_pair<q4_0> (all 144 launches per token)"
     torch.cuda.synchronize()
 
     # capture one token as a graph
@@ -160,13 +178,17 @@ def run_stack(args, torch, dev):
     ms_step = ms_ev / args.steps
     value = bytes_tok / (ms_step * 1e-3) / 1e9
 
-    # dominant kernel, live: the 144 GEMV launches of a token back to back on one stream,
-    # event-timed over many tokens; the per-launch average includes inter-launch gaps
+    if args.config == "stack_chain":
+        st = chain.status()
+        if st != 0:
+            raise RuntimeError(f"gemv chain reported status {st}")
+    # dominant kernel, live: the token's launches back to back on one stream, event-timed
+    # over many tokens; the per-launch average includes inter-launch gaps
     n_launch = len(launches)
     achieved = bytes_tok / n_launch / (ms_step * 1e-3 / n_launch) / 1e9
     roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
-                    kernel="k_gemv_pair<q4_0> (all 144 launches per token)",
+                    kernel=kernel,
                     avg_launch_us=round(ms_step * 1e3 / n_launch, 3),
                     bytes_per_launch=round(bytes_tok / n_launch))
     return dict(value=value, ms_step=ms_step, wall=wall, roofline=roofline, flops=flops_tok,
@@ -223,10 +245,10 @@ def main():
     if not torch.cuda.is_available():
         sys.exit("no GPU visible")
     dev = torch.device("cuda:0")
-    r = run_stack(args, torch, dev) if args.config == "stack" else run_gemv1(args, torch, dev)
+    r = run_gemv1(args, torch, dev) if args.config == "gemv1" else run_stack(args, torch, dev)
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline_stack() if args.config == "stack" else None
+        cpu = cpu_baseline_stack() if args.config != "gemv1" else None
     line = dict(
         metric=METRIC, value=round(r["value"], 2), unit="GB/s", n_gpus=1, steps=args.steps,
         warmup=args.warmup, ms_per_step=round(r["ms_step"], 4), higher_is_better=True,

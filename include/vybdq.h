@@ -96,6 +96,28 @@ int vybdq_gemv_q4_0_seg3(uint64_t X, int64_t K, int x_dt, int order,
                          uint64_t W2, uint64_t Y2, int64_t N2, int y_dt2,
                          uint64_t W3, uint64_t Y3, int64_t N3, int y_dt3, uint64_t stream);
 
+/* ---- persistent chain of dependent GEMV stages --------------------------------------- */
+
+/* Bytes of workspace vybdq_gemv_chain needs for nstages stages (a status word and one counter
+   per stage). Zero-fill it once before the first call; a completed call leaves it zero-filled. */
+int64_t vybdq_chain_workspace_size(int nstages);
+
+/* Run nstages dependent GEMV stages in ONE persistent launch. Stage s is described by the
+   reference's GEMV parameter block at device address P + s*pstride (W@0 X@8 Y@16 M@24 N@32
+   K@40 YE@48 W2@56 NS2@64 Y2@72 YE2@80 W3@88 NS3@96 Y3@104 YE3@112 RS@120 GRID@128,
+   native/host/ridge_decode.vyb:264-270) plus XE@136 (x type: 2 = f16, 258 = bf16, else f32)
+   and ORDER@144 (q4_0 nibble order). YE: 4 = f32, 2 = f16, 258 = bf16, else f64 with the f64
+   residual RS (the reference's YE rule, rgemv.vyb:13-15). M must be 1; K % 64 == 0, K <= max_K.
+   Stage s computes only after every workgroup finished stage s-1, so its X may be stage s-1's
+   Y; its weights are prefetched before that wait. wtype: 2 = q4_0, 8 = Q8_0 (GGUF type ids).
+   Replaces a sequence of lk(gemv, grid, 512, p) launches (ridge_decode.vyb:204-227). */
+int vybdq_gemv_chain(int wtype, uint64_t P, int nstages, int64_t pstride, int64_t max_K, uint64_t ws,
+                     uint64_t stream);
+
+/* Synchronous check of a chain workspace after the stream is idle: 0, or an error if a stage
+   wait timed out or a stage descriptor was invalid in a previous call. */
+int vybdq_chain_status(uint64_t ws);
+
 /* ---- activation quantizer ------------------------------------------------------------ */
 
 /* xq8 semantics per row and per 32-value block: a = max|x|, d = a/127, q = sat_s8(rne(x*127/a))

@@ -1,0 +1,121 @@
+"""GPU parity of the persistent GEMV chain: dependent stages (stage s reads stage s-1's
+output) against the fp64 oracle on the exact inputs each stage saw, multi-segment stages,
+mixed dtypes, residual, Q8_0, repeated calls and the workspace protocol."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import matmul
+from vybforge_amd import _lib, ops, synth
+
+pytestmark = pytest.mark.gpu
+TOL = matmul.TOL
+
+
+def dev_bytes(a, dev):
+    return torch.from_numpy(np.array(a, copy=True)).to(dev)
+
+
+def gate16(y, ref):
+    y = np.asarray(y, np.float64)
+    half_ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 11)
+    return float(np.maximum(np.abs(y - ref) - half_ulp, 0).max() / np.abs(ref).max())
+
+
+def test_chain_dependent_stages_q4_0(dev):
+    rng = np.random.default_rng(11)
+    f16 = torch.float16
+    # stage 0: x0[2560] -> (y0a[1024] | y0b[1536] | y0c[512]); stage 1: y0 (3072 as one buffer)...
+    # build a dependent chain: each stage's X is the previous stage's Y
+    dims = [2560, 3072, 4096, 2560, 9728, 2560]
+    xs = [torch.from_numpy(synth.activations(rng, (dims[0],))).to(f16).to(dev)]
+    raws, Ws, Ys, pbs = [], [], [], []
+    for s in range(len(dims) - 1):
+        K, N = dims[s], dims[s + 1]
+        raw = synth.q4_0_weights(rng, N, K)
+        W = dev_bytes(raw, dev)
+        Y = torch.empty(N, dtype=f16, device=dev)
+        raws.append(raw); Ws.append(W); Ys.append(Y)
+        pbs.append(ops.pblock(xs[-1], K, [(W, Y, N)]))
+        xs.append(Y)
+    ch = ops.GemvChain(ops.GGML_Q4_0, pbs, dev)
+    for rep in range(3):
+        for Y in Ys:
+            Y.fill_(float("nan"))
+        ch()
+        assert ch.status() == 0, _lib.last_error()
+        for s in range(len(Ws)):
+            K, N = dims[s], dims[s + 1]
+            x_in = xs[s].to(torch.float64).cpu().numpy()
+            ref = matmul.gemv_q4_0_f64(raws[s], x_in, N, K)[0]
+            y = Ys[s].to(torch.float64).cpu().numpy()
+            assert gate16(y, ref) < TOL, (rep, s)
+    assert int(ch.ws.abs().sum()) == 0     # counters reset by the last workgroup
+
+
+def test_chain_segments_dtypes_residual(dev):
+    rng = np.random.default_rng(12)
+    K = 2048
+    x = torch.from_numpy(synth.activations(rng, (K,))).to(dev)          # f32 x
+    shapes = [777, 64, 1500]
+    raws = [synth.q4_0_weights(rng, n, K) for n in shapes]
+    Ws = [dev_bytes(r, dev) for r in raws]
+    Y0 = torch.empty(shapes[0], dtype=torch.float64, device=dev)
+    RS = torch.from_numpy(rng.standard_normal(shapes[0])).to(dev)
+    Y1 = torch.empty(shapes[1], dtype=torch.float32, device=dev)
+    Y2 = torch.empty(shapes[2], dtype=torch.bfloat16, device=dev)
+    pb0 = ops.pblock(x, K, [(Ws[0], Y0, shapes[0]), (Ws[1], Y1, shapes[1]), (Ws[2], Y2, shapes[2])],
+                     residual=RS)
+    # a second stage reading the first stage's f32 segment
+    raw_b = synth.q4_0_weights(rng, 256, 64)
+    Yb = torch.empty(256, dtype=torch.float32, device=dev)
+    pb1 = ops.pblock(Y1, 64, [(dev_bytes(raw_b, dev), Yb, 256)])
+    ch = ops.GemvChain(ops.GGML_Q4_0, [pb0, pb1], dev)
+    ch()
+    assert ch.status() == 0, _lib.last_error()
+    x64 = x.to(torch.float64).cpu().numpy()
+    ref0 = matmul.gemv_q4_0_f64(raws[0], x64, shapes[0], K, residual=RS.cpu().numpy())[0]
+    assert matmul.rel_maxnorm(Y0.cpu().numpy(), ref0) < TOL
+    ref1 = matmul.gemv_q4_0_f64(raws[1], x64, shapes[1], K)[0]
+    assert matmul.rel_maxnorm(Y1.cpu().numpy(), ref1) < TOL
+    ref2 = matmul.gemv_q4_0_f64(raws[2], x64, shapes[2], K)[0]
+    y2 = Y2.to(torch.float64).cpu().numpy()
+    half_ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref2), 1e-30))) - 8)
+    assert float(np.maximum(np.abs(y2 - ref2) - half_ulp, 0).max() / np.abs(ref2).max()) < TOL
+    refb = matmul.gemv_q4_0_f64(raw_b, Y1.to(torch.float64).cpu().numpy(), 256, 64)[0]
+    assert matmul.rel_maxnorm(Yb.cpu().numpy(), refb) < TOL
+
+
+def test_chain_q8_0_and_interleaved(dev):
+    rng = np.random.default_rng(13)
+    K, N = 5120, 2048
+    raw8 = synth.q8_0_weights(rng, N, K)
+    x = torch.from_numpy(synth.activations(rng, (K,))).to(torch.bfloat16).to(dev)
+    Y = torch.empty(N, dtype=torch.float32, device=dev)
+    ch = ops.GemvChain(ops.GGML_Q8_0, [ops.pblock(x, K, [(dev_bytes(raw8, dev), Y, N)])], dev)
+    ch()
+    assert ch.status() == 0
+    ref = matmul.gemv_q8_0_f64(raw8, x.to(torch.float64).cpu().numpy(), N, K)[0]
+    assert matmul.rel_maxnorm(Y.cpu().numpy(), ref) < TOL
+    raw4 = synth.q4_0_weights(rng, 300, 1024)
+    x4 = torch.from_numpy(synth.activations(rng, (1024,))).to(dev)
+    Y4 = torch.empty(300, dtype=torch.float32, device=dev)
+    ch4 = ops.GemvChain(ops.GGML_Q4_0, [ops.pblock(x4, 1024, [(dev_bytes(raw4, dev), Y4, 300)],
+                                                   order=ops.Q4_INTERLEAVED)], dev)
+    ch4()
+    ref4 = matmul.gemv_q4_0_f64(raw4, x4.cpu().numpy().astype(np.float64), 300, 1024, order=1)[0]
+    assert matmul.rel_maxnorm(Y4.cpu().numpy(), ref4) < TOL
+
+
+def test_chain_invalid_stage_reports(dev):
+    rng = np.random.default_rng(14)
+    raw = synth.q4_0_weights(rng, 64, 96)           # K % 64 != 0: not a chain shape
+    x = torch.zeros(96, dtype=torch.float32, device=dev)
+    Y = torch.zeros(64, dtype=torch.float32, device=dev)
+    pb = ops.pblock(x, 96, [(dev_bytes(raw, dev), Y, 64)])
+    ch = ops.GemvChain(ops.GGML_Q4_0, [pb], dev)
+    ch.max_k = 128
+    ch()
+    assert ch.status() == _lib.ERR_SHAPE
+    assert "invalid" in _lib.last_error()

@@ -33,8 +33,11 @@ SIGNATURES = {
                              _u64, _u64, _i64, _int,
                              _u64, _u64, _i64, _int, _u64],
     "vybdq_quant_q8_act": [_u64, _u64, _u64, _i64, _i64, _int, _u64],
+    "vybdq_chain_workspace_size": [_int],
+    "vybdq_gemv_chain": [_int, _u64, _int, _i64, _i64, _u64, _u64],
+    "vybdq_chain_status": [_u64],
 }
-_RESTYPE = {"vybdq_last_error": ctypes.c_char_p}
+_RESTYPE = {"vybdq_last_error": ctypes.c_char_p, "vybdq_chain_workspace_size": ctypes.c_int64}
 
 
 class VybdqError(RuntimeError):
@@ -44,6 +47,13 @@ class VybdqError(RuntimeError):
 
 
 def _load():
+    # PyTorch ROCm wheels carry their own libamdhip64. Loading torch first lets this library
+    # bind to that same runtime; loading this library first would put two HIP runtimes in one
+    # process, and torch streams/pointers would not be valid in ours.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     if not os.path.exists(LIB_PATH):
         raise ImportError(f"libvybdq.so is not built ({LIB_PATH}); run python -m vybforge_amd.build")
     lib = ctypes.CDLL(LIB_PATH)

@@ -98,3 +98,65 @@ def quant_q8_act(X):
     d = torch.empty((M, K // 32), dtype=torch.float32, device=X.device)
     call("vybdq_quant_q8_act", _ptr(X2), _ptr(q), _ptr(d), M, K, _dt(X2.dtype), _stream())
     return q, d
+
+
+# ---- persistent GEMV chain ---------------------------------------------------------------
+
+PBLOCK_WORDS = 32        # one stage = the reference's GEMV p-block, 256-byte stride
+_YE = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 258, torch.float64: 8}
+_XE = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 258}
+
+
+class Stage:
+    """A stage descriptor plus the tensors it points at (kept alive as long as the stage)."""
+
+    def __init__(self, words, refs):
+        self.words = words
+        self.refs = refs
+
+
+def pblock(X, K, segs, residual=None, order=Q4_GGML):
+    """One stage descriptor (int64 [32]) in the reference GEMV p-block layout.
+
+    segs: up to 3 (W, Y, N) with preallocated Y; W@0 X@8 Y@16 M@24 N@32 K@40 YE@48
+    W2@56 NS2@64 Y2@72 YE2@80 W3@88 NS3@96 Y3@104 YE3@112 RS@120 GRID@128 XE@136 ORDER@144.
+    The returned Stage holds references to X, W, Y and residual: a descriptor must never
+    outlive the memory it points to.
+    """
+    import numpy as np
+    pb = np.zeros(PBLOCK_WORDS, np.int64)
+    pb[1], pb[3], pb[5] = _ptr(X), 1, K
+    slots = [(0, 2, 4, 6), (7, 9, 8, 10), (11, 13, 12, 14)]
+    for i, (W, Y, N) in enumerate(segs):
+        w, y, n, ye = slots[i]
+        pb[w], pb[y], pb[n], pb[ye] = _ptr(W), _ptr(Y), N, _YE[Y.dtype]
+    for i in range(len(segs), 3):
+        pb[slots[i][3]] = 8
+    pb[15] = _ptr(residual)
+    pb[17] = _XE[X.dtype]
+    pb[18] = order
+    refs = (X, residual) + tuple(t for seg in segs for t in seg[:2])
+    return Stage(pb, refs)
+
+
+class GemvChain:
+    """A device-resident chain of GEMV stages run by one persistent launch per call."""
+
+    def __init__(self, ty, stages, device):
+        import numpy as np
+        self.ty = ty
+        self.n = len(stages)
+        self.refs = [st.refs for st in stages]
+        words = [st.words for st in stages]
+        self.max_k = max(int(pb[5]) for pb in words)
+        self.pb = torch.from_numpy(np.stack(words)).to(device)
+        nbytes = _lib.lib.vybdq_chain_workspace_size(self.n)
+        self.ws = torch.zeros((nbytes + 3) // 4, dtype=torch.int32, device=device)
+
+    def __call__(self):
+        call("vybdq_gemv_chain", self.ty, _ptr(self.pb), self.n, PBLOCK_WORDS * 8, self.max_k,
+             _ptr(self.ws), _stream())
+
+    def status(self):
+        torch.cuda.synchronize()
+        return _lib.lib.vybdq_chain_status(_ptr(self.ws))
