@@ -33,7 +33,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="stack", choices=["stack", "stack_chain", "gemv1"])
+    ap.add_argument("--config", default="stack", choices=["stack", "stack_chain", "gemv1", "exl3"])
+    ap.add_argument("--batch", type=int, default=1, help="batch for --config exl3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--seed", type=int, default=0)
     return ap.parse_args()
@@ -235,6 +236,58 @@ def run_gemv1(args, torch, dev):
                 bytes_per_step=bytes_call * len(launch), launches_per_step=len(launch))
 
 
+def timed_graph(torch, launches, steps, warmup):
+    """Capture the launches as one graph; return (ms per replay, wall seconds)."""
+    for f in launches:
+        f()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in launches:
+            f()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        g.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / steps, time.perf_counter() - t0
+
+
+def run_exl3(args, torch, dev):
+    """Config 4: EXL3 4-bpw GEMM K=5120 x N=17408, batch 1 or 16, 8 rotated trellis copies."""
+    from vybforge_amd import ops
+    K, N, B = 5120, 17408, args.batch
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    ncopy = 8
+    lins = []
+    for _ in range(ncopy):
+        t = torch.randint(0, 65536, (K // 16, N // 16, 64), generator=gen, device=dev, dtype=torch.int32).to(torch.uint16)
+        suh = ((torch.randn(K, generator=gen, device=dev) * 0.01).abs() * (torch.randint(0, 2, (K,), generator=gen, device=dev) * 2 - 1)).to(torch.float16)
+        svh = ((torch.randn(N, generator=gen, device=dev) * 0.01).abs() * (torch.randint(0, 2, (N,), generator=gen, device=dev) * 2 - 1)).to(torch.float16)
+        lins.append(ops.Exl3Linear(t, suh, svh, K, N))
+    x = torch.randn(B, K, generator=gen, device=dev).to(torch.float16)
+    y = torch.empty(B, N, device=dev)
+    launches = [lambda L=L: L(x, out=y) for L in lins]
+    ms, wall = timed_graph(torch, launches, args.steps, args.warmup)
+    per = ms / ncopy
+    bytes_call = K * N // 2 + 2 * K + 2 * N + B * (2 * K + 4 * N)
+    value = bytes_call / (per * 1e-3) / 1e9
+    flops = 2 * K * N * B
+    roofline = dict(bound="hbm", achieved=round(value, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(value / HBM_PEAK_GBS, 4), traffic=None,
+                    kernel="exl3 gemm (xprep + k_exl3_gemm + out; VALU-bound decode)",
+                    avg_launch_us=round(per * 1e3, 3), bytes_per_launch=bytes_call)
+    return dict(value=value, ms_step=ms, wall=wall, roofline=roofline, flops=flops * ncopy,
+                workload=f"EXL3 4-bpw mcg GEMM K=5120 N=17408 batch {B} (8 rotated trellis copies)",
+                bytes_per_step=bytes_call * ncopy, launches_per_step=ncopy)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -245,10 +298,15 @@ def main():
     if not torch.cuda.is_available():
         sys.exit("no GPU visible")
     dev = torch.device("cuda:0")
-    r = run_gemv1(args, torch, dev) if args.config == "gemv1" else run_stack(args, torch, dev)
+    if args.config == "gemv1":
+        r = run_gemv1(args, torch, dev)
+    elif args.config == "exl3":
+        r = run_exl3(args, torch, dev)
+    else:
+        r = run_stack(args, torch, dev)
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline_stack() if args.config != "gemv1" else None
+        cpu = cpu_baseline_stack() if args.config in ("stack", "stack_chain") else None
     line = dict(
         metric=METRIC, value=round(r["value"], 2), unit="GB/s", n_gpus=1, steps=args.steps,
         warmup=args.warmup, ms_per_step=round(r["ms_step"], 4), higher_is_better=True,

@@ -118,6 +118,34 @@ int vybdq_gemv_chain(int wtype, uint64_t P, int nstages, int64_t pstride, int64_
    wait timed out or a stage descriptor was invalid in a previous call. */
 int vybdq_chain_status(uint64_t ws);
 
+/* ---- EXL3 4-bpw trellis ------------------------------------------------------------- */
+
+/* Rotated-basis decode What [K, N] (no Hadamard, no scales); out_dt F32, F16 or F64. The
+   bit-exact gate: replaces exl3deq / exl3deq32 (native/kernels/exl3.vyb:207-242,375-422),
+   with the tile-slot composition built in (native/exl3/tile_slot_composition.json). */
+int vybdq_exl3_decode_tiles(uint64_t trellis, uint64_t out, int64_t K, int64_t N, int codebook,
+                            int out_dt, uint64_t stream);
+
+/* Full original-basis W [K, N] = diag(suh) (H/sqrt128) What (H/sqrt128) diag(svh), per 128x128
+   block, float32 transforms; out_dt F32, F16 or F64; K, N % 128 == 0. Replaces the exl3_deq32
+   pipeline exl3dq1s + exl3had232 + exl3cvt32 (native/glm53/glm_engine.vyb:1103-1200,
+   native/kernels/exl3dq.vyb:46-113). */
+int vybdq_dequant_exl3(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t out, int64_t K, int64_t N,
+                       int codebook, int out_dt, uint64_t stream);
+
+/* Workspace bytes for vybdq_exl3_gemm at (B, K, N), or -1 for an unsupported shape. */
+int64_t vybdq_exl3_workspace_size(int64_t B, int64_t K, int64_t N);
+
+/* Y [B, N] = X [B, K] W, W the EXL3 matrix above, without materialising W: X is rotated
+   (FWHT(X * suh)/sqrt128 per 128 chunk), the trellis is decoded in registers and multiplied
+   (f32 accumulation), and the result rotated back (FWHT(.)/sqrt128 * svh). 1 <= B <= 16,
+   K, N % 128 == 0, trellis 16-byte aligned, ws 256-byte aligned of at least
+   vybdq_exl3_workspace_size bytes. The reference has no fused EXL3 GEMM (it dequantizes each
+   expert to f64/f32 then runs gemm, glm_engine.vyb:2845-2923). */
+int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t X, uint64_t Y, int64_t B,
+                    int64_t K, int64_t N, int codebook, int x_dt, int y_dt, uint64_t ws, int64_t ws_bytes,
+                    uint64_t stream);
+
 /* ---- activation quantizer ------------------------------------------------------------ */
 
 /* xq8 semantics per row and per 32-value block: a = max|x|, d = a/127, q = sat_s8(rne(x*127/a))

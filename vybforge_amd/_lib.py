@@ -36,8 +36,13 @@ SIGNATURES = {
     "vybdq_chain_workspace_size": [_int],
     "vybdq_gemv_chain": [_int, _u64, _int, _i64, _i64, _u64, _u64],
     "vybdq_chain_status": [_u64],
+    "vybdq_exl3_decode_tiles": [_u64, _u64, _i64, _i64, _int, _int, _u64],
+    "vybdq_dequant_exl3": [_u64, _u64, _u64, _u64, _i64, _i64, _int, _int, _u64],
+    "vybdq_exl3_workspace_size": [_i64, _i64, _i64],
+    "vybdq_exl3_gemm": [_u64, _u64, _u64, _u64, _u64, _i64, _i64, _i64, _int, _int, _int, _u64, _i64, _u64],
 }
-_RESTYPE = {"vybdq_last_error": ctypes.c_char_p, "vybdq_chain_workspace_size": ctypes.c_int64}
+_RESTYPE = {"vybdq_last_error": ctypes.c_char_p, "vybdq_chain_workspace_size": ctypes.c_int64,
+            "vybdq_exl3_workspace_size": ctypes.c_int64}
 
 
 class VybdqError(RuntimeError):

@@ -44,6 +44,10 @@ def _compile(src):
 def build(verbose=False):
     """Compile all sources and link libvybdq.so. Always rebuilds."""
     os.makedirs(OBJ, exist_ok=True)
+    # generated tables (the EXL3 per-lane slot table) come first
+    r = subprocess.run([sys.executable, os.path.join(CSRC, "gen_exl3_slots.py")], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("gen_exl3_slots.py failed:\n" + r.stderr)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     if not srcs:
         raise RuntimeError("no HIP sources found")

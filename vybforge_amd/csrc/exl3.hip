@@ -1,0 +1,427 @@
+// EXL3 4-bpw trellis decode, full dequant and the fused GEMM (batch 1..16), gfx950.
+//
+// Format (native/exl3/README.md:24-49, native/exl3/exl3_ref.py:1-120): W [K, N] stored as
+// 16x16 tiles, trellis uint16 [K/16][N/16][64] (256 nibbles per tile, LSB-first), suh fp16 [K],
+// svh fp16 [N]. Tile slot (r, c) takes a 16-bit window of the tile's nibble stream through the
+// tile-slot composition table and decodes it with the codebook hash:
+//   mcg   (1): x = w * 0xCBAC1FED            3inst (0): x = w * 89226354 + 64248484   (mod 2^32)
+//   y = (x & 0x8FFF8FFF) ^ 0x3B603B60;  value = fp16(fp16(y.lo) + fp16(y.hi))
+// Both halves of y always lie in [0.125, 2), so their float32 sum is exact and one fp16 add
+// (round to nearest even) equals the reference's float32-sum-then-round.
+// W = diag(suh) (H/sqrt(128)) What (H/sqrt(128)) diag(svh) per 128x128 block, H = Sylvester
+// Hadamard-128, so x W = FWHT(FWHT(x * suh)/sqrt(128) What)/sqrt(128) * svh per 128 chunk.
+//
+// Lane decomposition (exl3_slots.inc, generated and checked by gen_exl3_slots.py): 8 lanes share
+// a tile; lane j owns columns j and j+8 (32 values), loads the tile's 16-byte chunk j (stream
+// dwords 4j..4j+3) and takes dword 4j-1 from its neighbour by a shuffle; every window is one or
+// two constant-offset funnel extracts of those 5 dwords. A wave covers 8 consecutive tiles along
+// N (one 128-column Hadamard block) and reads 1 KB of contiguous trellis per step.
+#include "common.h"
+
+namespace vybdq {
+
+#include "exl3_slots.inc"
+
+constexpr float kRScale = 0.08838834764831845f;  // 1/sqrt(128)
+
+// bits [o, o+32) of the 192-bit lane window w[0..5] (o is a constant after unrolling)
+__device__ __forceinline__ uint32_t win_extract(const uint32_t (&w)[6], int o) {
+  const int i = o >> 5, s = o & 31;
+  if (s == 0) return w[i];
+  if (i == 5) return w[5] >> s;
+  return __builtin_amdgcn_alignbit(w[i + 1], w[i], s);
+}
+
+template <int CB>
+__device__ __forceinline__ _Float16 decode_window(uint32_t w) {
+  // x = w16 * M (+ A) mod 2^32 from two 16x16-bit products; only the low 16 bits of w are used
+  const uint32_t wl = w & 0xffffu;
+  uint32_t hi, lo;
+  if constexpr (CB == VYBDQ_EXL3_MCG) {
+    hi = wl * 0xCBACu;
+    lo = wl * 0x1FEDu;
+  } else {
+    hi = wl * 0x0551u;
+    lo = wl * 0x7C72u + 0x03D45AA4u;
+  }
+  // keep the two full-rate 16x16 products from being merged into one quarter-rate v_mul_lo_u32
+  asm volatile("" : "+v"(hi));
+  const uint32_t x = (hi << 16) + lo;
+  const uint32_t y = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+  const h2 v = __builtin_bit_cast(h2, y);
+  return v[0] + v[1];
+}
+
+// The 32 values of lane j: val[q] = row q of column j (q < 16), row q-16 of column j+8.
+template <int CB>
+__device__ __forceinline__ void lane_decode(const uint32_t (&w)[6], _Float16 (&val)[32]) {
+#pragma unroll
+  for (int q = 0; q < 32; ++q) {
+    uint32_t x = win_extract(w, kExl3SlotOff0[q]) & kExl3SlotMask0[q];
+    if (kExl3SlotOff1[q] >= 0) x |= win_extract(w, kExl3SlotOff1[q]) & kExl3SlotMask1[q];
+    val[q] = decode_window<CB>(x);
+  }
+}
+
+// Load tile `tile`'s chunk for lane j (of the 8 lanes sharing it) and build the lane window.
+__device__ __forceinline__ void lane_window(const uint16_t *__restrict__ trellis, int64_t tile, int j,
+                                            uint32_t (&w)[6]) {
+  const u4 c = *reinterpret_cast<const u4 *>(trellis + tile * 64 + 8 * j);
+  w[0] = 0;  // stream dword 4j-2: no window reads it (checked by the generator)
+  w[2] = c[0];
+  w[3] = c[1];
+  w[4] = c[2];
+  w[5] = c[3];
+  // stream dword 4j-1 = lane j-1's last chunk dword (lane 7's for j = 0)
+  const int lane = threadIdx.x & 63;
+  const int src = (lane & ~7) | ((lane - 1) & 7);
+  w[1] = __shfl(c[3], src, 64);
+}
+
+// ---- decode-only: rotated basis What [K, N] ------------------------------------------------
+
+template <int CB, int ODT>
+__global__ void __launch_bounds__(256) k_exl3_decode(const uint16_t *__restrict__ trellis, void *__restrict__ out,
+                                                     int64_t ntiles, int NB) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t tile = g >> 3;
+  const int j = static_cast<int>(g & 7);
+  const int64_t safe = tile < ntiles ? tile : 0;  // every lane joins the shuffle
+  uint32_t w[6];
+  lane_window(trellis, safe, j, w);
+  _Float16 v[32];
+  lane_decode<CB>(w, v);
+  if (tile >= ntiles) return;
+  const int64_t kb = tile / NB, nb = tile % NB;
+  const int64_t N = static_cast<int64_t>(NB) * 16;
+#pragma unroll
+  for (int q = 0; q < 32; ++q) {
+    const int64_t r = 16 * kb + (q & 15);
+    const int64_t c = 16 * nb + j + (q >> 4) * 8;
+    store_elem<ODT>(out, nullptr, r * N + c, static_cast<float>(v[q]));
+  }
+}
+
+// ---- 128-point FWHT across a wave (2 elements per lane) -------------------------------------
+
+__device__ __forceinline__ void fwht128_wave(float &a0, float &a1) {
+  const int lane = threadIdx.x & 63;
+  float t0 = a0 + a1, t1 = a0 - a1;
+  a0 = t0;
+  a1 = t1;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const float p0 = __shfl_xor(a0, m, 64), p1 = __shfl_xor(a1, m, 64);
+    const bool upper = (lane & m) != 0;
+    a0 = upper ? p0 - a0 : a0 + p0;
+    a1 = upper ? p1 - a1 : a1 + p1;
+  }
+}
+
+// ---- full dequant: W [K, N] = diag(suh) Hs What Hs diag(svh) -------------------------------
+// One workgroup per 128x128 block: decode the 64 tiles into LDS (float, rows padded to 129),
+// FWHT every row, then every column, scale, store.
+
+template <int CB, int ODT>
+__global__ void __launch_bounds__(256) k_exl3_dequant(const uint16_t *__restrict__ trellis,
+                                                      const _Float16 *__restrict__ suh,
+                                                      const _Float16 *__restrict__ svh, void *__restrict__ out,
+                                                      int NB) {
+  extern __shared__ float blk[];  // [128][129]
+  const int bk = blockIdx.y, bn = blockIdx.x;
+  const int64_t N = static_cast<int64_t>(NB) * 16;
+  for (int task = threadIdx.x; task < 512; task += blockDim.x) {  // 64 tiles x 8 lanes
+    const int tl = task >> 3, j = task & 7;
+    const int tk = tl >> 3, tn = tl & 7;
+    const int64_t tile = static_cast<int64_t>(8 * bk + tk) * NB + (8 * bn + tn);
+    uint32_t w[6];
+    lane_window(trellis, tile, j, w);
+    _Float16 v[32];
+    lane_decode<CB>(w, v);
+#pragma unroll
+    for (int q = 0; q < 32; ++q)
+      blk[(16 * tk + (q & 15)) * 129 + 16 * tn + j + (q >> 4) * 8] = static_cast<float>(v[q]);
+  }
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int row = wave; row < 128; row += 4) {  // column transform: What_row . Hs
+    float a0 = blk[row * 129 + 2 * lane], a1 = blk[row * 129 + 2 * lane + 1];
+    fwht128_wave(a0, a1);
+    blk[row * 129 + 2 * lane] = a0 * kRScale;
+    blk[row * 129 + 2 * lane + 1] = a1 * kRScale;
+  }
+  __syncthreads();
+  for (int col = wave; col < 128; col += 4) {  // row transform: Hs . (.)
+    float a0 = blk[(2 * lane) * 129 + col], a1 = blk[(2 * lane + 1) * 129 + col];
+    fwht128_wave(a0, a1);
+    const float sv = static_cast<float>(svh[128 * bn + col]);
+    const int64_t r0 = 128 * static_cast<int64_t>(bk) + 2 * lane;
+    store_elem<ODT>(out, nullptr, r0 * N + 128 * bn + col, a0 * kRScale * static_cast<float>(suh[r0]) * sv);
+    store_elem<ODT>(out, nullptr, (r0 + 1) * N + 128 * bn + col,
+                    a1 * kRScale * static_cast<float>(suh[r0 + 1]) * sv);
+  }
+}
+
+// ---- fused GEMM ------------------------------------------------------------------------------
+// 1. x' [BP][K] fp16 = FWHT(x * suh) / sqrt(128) per 128 chunk (rows b >= B are zero)
+
+template <int XDT>
+__global__ void __launch_bounds__(64) k_exl3_xprep(const void *__restrict__ X, const _Float16 *__restrict__ suh,
+                                                   _Float16 *__restrict__ xp, int B, int64_t K) {
+  const int chunk = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const int64_t k0 = 128 * static_cast<int64_t>(chunk) + 2 * lane;
+  float a0 = 0.f, a1 = 0.f;
+  if (b < B) {
+    a0 = load_elem<XDT>(X, b * K + k0) * static_cast<float>(suh[k0]);
+    a1 = load_elem<XDT>(X, b * K + k0 + 1) * static_cast<float>(suh[k0 + 1]);
+  }
+  fwht128_wave(a0, a1);
+  xp[b * K + k0] = static_cast<_Float16>(a0 * kRScale);
+  xp[b * K + k0 + 1] = static_cast<_Float16>(a1 * kRScale);
+}
+
+// 2. zpart[s][b][n] = sum over the k-range of split s of x'[b][k] What[k][n]
+//    grid (N/128, S): workgroup = 4 waves on one 128-column block, each wave a quarter of the
+//    split's k-range; the waves' partials are summed in LDS in a fixed order.
+
+template <int CB, int BP>
+__global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ trellis,
+                                                   const _Float16 *__restrict__ xp, float *__restrict__ zpart,
+                                                   int64_t K, int NB, int kb_per_split) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int g = blockIdx.x, s = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = lane >> 3, j = lane & 7;
+  const int KB = static_cast<int>(K / 16);
+  const int kb_begin = s * kb_per_split;
+  const int kb_end = min(kb_begin + kb_per_split, KB);
+  const int nkb = kb_end - kb_begin;
+  // stage x' rows of this split: [BP][16 * nkb] fp16
+  _Float16 *xs = reinterpret_cast<_Float16 *>(smem);
+  const int rows = 16 * nkb;
+  for (int i = threadIdx.x; i < BP * rows / 8; i += blockDim.x) {
+    const int b = i / (rows / 8), c = i % (rows / 8);
+    *reinterpret_cast<u4 *>(xs + b * rows + 8 * c) =
+        *reinterpret_cast<const u4 *>(xp + b * K + 16 * static_cast<int64_t>(kb_begin) + 8 * c);
+  }
+  __syncthreads();
+
+  float acc[BP][2];
+#pragma unroll
+  for (int b = 0; b < BP; ++b) acc[b][0] = acc[b][1] = 0.f;
+  const int per_wave = (nkb + 3) / 4;
+  const int w_begin = wave * per_wave;
+  const int w_end = min(w_begin + per_wave, nkb);
+  const int64_t nb = 8 * static_cast<int64_t>(g) + t;
+  for (int kk = w_begin; kk < w_end; ++kk) {
+    uint32_t w[6];
+    lane_window(trellis, static_cast<int64_t>(kb_begin + kk) * NB + nb, j, w);
+    _Float16 v[32];
+    lane_decode<CB>(w, v);
+    h2 pj[8], pj8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pj[i] = h2{v[2 * i], v[2 * i + 1]};
+      pj8[i] = h2{v[16 + 2 * i], v[16 + 2 * i + 1]};
+    }
+#pragma unroll
+    for (int b = 0; b < BP; ++b) {
+      const u4 *xr = reinterpret_cast<const u4 *>(xs + b * rows + 16 * kk);
+      const u4 x0 = xr[0], x1 = xr[1];
+      const uint32_t xw[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const h2 xv = __builtin_bit_cast(h2, xw[i]);
+        acc[b][0] = __builtin_amdgcn_fdot2(pj[i], xv, acc[b][0], false);
+        acc[b][1] = __builtin_amdgcn_fdot2(pj8[i], xv, acc[b][1], false);
+      }
+    }
+  }
+  // reduce the 4 waves (same columns, different k) in a fixed order
+  __syncthreads();
+  float *red = reinterpret_cast<float *>(smem);  // [4][BP][128]
+  const int c0 = 16 * t + j;                      // this lane's columns: c0 and c0 + 8
+#pragma unroll
+  for (int b = 0; b < BP; ++b) {
+    red[(wave * BP + b) * 128 + c0] = acc[b][0];
+    red[(wave * BP + b) * 128 + c0 + 8] = acc[b][1];
+  }
+  __syncthreads();
+  const int64_t N = static_cast<int64_t>(NB) * 16;
+  for (int i = threadIdx.x; i < BP * 128; i += blockDim.x) {
+    const int b = i / 128, c = i % 128;
+    const float z = ((red[(0 * BP + b) * 128 + c] + red[(1 * BP + b) * 128 + c]) +
+                     red[(2 * BP + b) * 128 + c]) + red[(3 * BP + b) * 128 + c];
+    zpart[(static_cast<int64_t>(s) * BP + b) * N + 128 * static_cast<int64_t>(g) + c] = z;
+  }
+}
+
+// 3. y[b][n] = svh[n] * FWHT(sum_s zpart[s][b][.]) / sqrt(128)
+
+template <int YDT>
+__global__ void __launch_bounds__(64) k_exl3_out(const float *__restrict__ zpart, const _Float16 *__restrict__ svh,
+                                                 void *__restrict__ Y, int BP, int S, int64_t N) {
+  const int blk = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const int64_t n0 = 128 * static_cast<int64_t>(blk) + 2 * lane;
+  float a0 = 0.f, a1 = 0.f;
+  for (int s = 0; s < S; ++s) {
+    a0 += zpart[(static_cast<int64_t>(s) * BP + b) * N + n0];
+    a1 += zpart[(static_cast<int64_t>(s) * BP + b) * N + n0 + 1];
+  }
+  fwht128_wave(a0, a1);
+  store_elem<YDT>(Y, nullptr, b * N + n0, a0 * kRScale * static_cast<float>(svh[n0]));
+  store_elem<YDT>(Y, nullptr, b * N + n0 + 1, a1 * kRScale * static_cast<float>(svh[n0 + 1]));
+}
+
+// ---- host --------------------------------------------------------------------------------
+
+static int exl3_bp(int64_t B) { return B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : B <= 8 ? 8 : 16; }
+
+// K-splits: enough workgroups to fill the chip, bounded so partials stay small
+static int exl3_splits(int64_t K, int64_t N, int BP) {
+  const int KB = static_cast<int>(K / 16);
+  const int64_t groups = N / 128;
+  int S = static_cast<int>((1024 + groups - 1) / groups);
+  const int smax = BP >= 8 ? 4 : 8;
+  if (S > smax) S = smax;
+  if (S > KB / 4) S = KB / 4 > 0 ? KB / 4 : 1;
+  return S < 1 ? 1 : S;
+}
+
+static int64_t exl3_ws_bytes(int64_t B, int64_t K, int64_t N) {
+  const int BP = exl3_bp(B);
+  const int S = exl3_splits(K, N, BP);
+  const int64_t xp = ((BP * K * 2 + 255) / 256) * 256;
+  return xp + static_cast<int64_t>(S) * BP * N * 4;
+}
+
+}  // namespace vybdq
+
+using namespace vybdq;
+
+static int exl3_check(uint64_t trellis, int64_t K, int64_t N, int codebook) {
+  VYBDQ_REQUIRE(trellis, VYBDQ_ERR_ARG, "null trellis");
+  VYBDQ_REQUIRE(codebook == VYBDQ_EXL3_MCG || codebook == VYBDQ_EXL3_3INST, VYBDQ_ERR_ARG, "unknown codebook");
+  VYBDQ_REQUIRE(K > 0 && N > 0 && K % 16 == 0 && N % 16 == 0, VYBDQ_ERR_SHAPE, "K and N must be positive multiples of 16");
+  VYBDQ_REQUIRE((trellis & 15) == 0, VYBDQ_ERR_ALIGN, "trellis must be 16-byte aligned");
+  VYBDQ_REQUIRE(N / 16 < (1 << 30) && K / 16 < (1 << 30), VYBDQ_ERR_SHAPE, "too many tiles");
+  return VYBDQ_OK;
+}
+
+extern "C" int vybdq_exl3_decode_tiles(uint64_t trellis, uint64_t out, int64_t K, int64_t N, int codebook,
+                                       int out_dt, uint64_t stream) {
+  int rc = exl3_check(trellis, K, N, codebook);
+  if (rc) return rc;
+  VYBDQ_REQUIRE(out, VYBDQ_ERR_ARG, "null out");
+  VYBDQ_REQUIRE(out_dt == VYBDQ_F32 || out_dt == VYBDQ_F16 || out_dt == VYBDQ_F64, VYBDQ_ERR_ARG,
+                "out_dt must be F32, F16 or F64");
+  const int NB = static_cast<int>(N / 16);
+  const int64_t ntiles = (K / 16) * NB;
+  const unsigned grid = static_cast<unsigned>((ntiles * 8 + 255) / 256);
+  hipStream_t s = as_stream(stream);
+  const auto *t = reinterpret_cast<const uint16_t *>(trellis);
+  void *o = reinterpret_cast<void *>(out);
+#define L(CB, ODT) hipLaunchKernelGGL((k_exl3_decode<CB, ODT>), dim3(grid), dim3(256), 0, s, t, o, ntiles, NB)
+  if (codebook == VYBDQ_EXL3_MCG) {
+    if (out_dt == VYBDQ_F32) L(VYBDQ_EXL3_MCG, VYBDQ_F32); else if (out_dt == VYBDQ_F16) L(VYBDQ_EXL3_MCG, VYBDQ_F16); else L(VYBDQ_EXL3_MCG, VYBDQ_F64);
+  } else {
+    if (out_dt == VYBDQ_F32) L(VYBDQ_EXL3_3INST, VYBDQ_F32); else if (out_dt == VYBDQ_F16) L(VYBDQ_EXL3_3INST, VYBDQ_F16); else L(VYBDQ_EXL3_3INST, VYBDQ_F64);
+  }
+#undef L
+  return check_launch("vybdq_exl3_decode_tiles");
+}
+
+extern "C" int vybdq_dequant_exl3(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t out, int64_t K, int64_t N,
+                                  int codebook, int out_dt, uint64_t stream) {
+  int rc = exl3_check(trellis, K, N, codebook);
+  if (rc) return rc;
+  VYBDQ_REQUIRE(suh && svh && out, VYBDQ_ERR_ARG, "null suh, svh or out");
+  VYBDQ_REQUIRE(K % 128 == 0 && N % 128 == 0, VYBDQ_ERR_SHAPE, "K and N must be multiples of 128");
+  VYBDQ_REQUIRE(out_dt == VYBDQ_F32 || out_dt == VYBDQ_F16 || out_dt == VYBDQ_F64, VYBDQ_ERR_ARG,
+                "out_dt must be F32, F16 or F64");
+  const int NB = static_cast<int>(N / 16);
+  const dim3 grid(static_cast<unsigned>(N / 128), static_cast<unsigned>(K / 128));
+  const size_t lds = 128 * 129 * 4;
+  hipStream_t s = as_stream(stream);
+  const auto *t = reinterpret_cast<const uint16_t *>(trellis);
+  const auto *su = reinterpret_cast<const _Float16 *>(suh);
+  const auto *sv = reinterpret_cast<const _Float16 *>(svh);
+  void *o = reinterpret_cast<void *>(out);
+#define L(CB, ODT)                                                                                         \
+  do {                                                                                                     \
+    static bool raised = false;                                                                            \
+    if (!raised) {                                                                                         \
+      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_exl3_dequant<CB, ODT>),                   \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));        \
+      raised = true;                                                                                       \
+    }                                                                                                      \
+    hipLaunchKernelGGL((k_exl3_dequant<CB, ODT>), grid, dim3(256), lds, s, t, su, sv, o, NB);             \
+  } while (0)
+  if (codebook == VYBDQ_EXL3_MCG) {
+    if (out_dt == VYBDQ_F32) L(VYBDQ_EXL3_MCG, VYBDQ_F32); else if (out_dt == VYBDQ_F16) L(VYBDQ_EXL3_MCG, VYBDQ_F16); else L(VYBDQ_EXL3_MCG, VYBDQ_F64);
+  } else {
+    if (out_dt == VYBDQ_F32) L(VYBDQ_EXL3_3INST, VYBDQ_F32); else if (out_dt == VYBDQ_F16) L(VYBDQ_EXL3_3INST, VYBDQ_F16); else L(VYBDQ_EXL3_3INST, VYBDQ_F64);
+  }
+#undef L
+  return check_launch("vybdq_dequant_exl3");
+}
+
+extern "C" int64_t vybdq_exl3_workspace_size(int64_t B, int64_t K, int64_t N) {
+  if (B < 1 || B > 16 || K <= 0 || N <= 0 || K % 128 || N % 128) return -1;
+  return exl3_ws_bytes(B, K, N);
+}
+
+template <int CB, int BP>
+static void exl3_gemm_launch(const uint16_t *t, const _Float16 *xp, float *zp, int64_t K, int NB, int S, int kbs,
+                             hipStream_t s) {
+  const size_t xs_bytes = static_cast<size_t>(BP) * 16 * kbs * 2;
+  const size_t red_bytes = static_cast<size_t>(4) * BP * 128 * 4;
+  const size_t lds = xs_bytes > red_bytes ? xs_bytes : red_bytes;
+  hipLaunchKernelGGL((k_exl3_gemm<CB, BP>), dim3(static_cast<unsigned>(NB / 8), static_cast<unsigned>(S)), dim3(256),
+                     lds, s, t, xp, zp, K, NB, kbs);
+}
+
+extern "C" int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t X, uint64_t Y, int64_t B,
+                               int64_t K, int64_t N, int codebook, int x_dt, int y_dt, uint64_t ws,
+                               int64_t ws_bytes, uint64_t stream) {
+  int rc = exl3_check(trellis, K, N, codebook);
+  if (rc) return rc;
+  VYBDQ_REQUIRE(suh && svh && X && Y, VYBDQ_ERR_ARG, "null suh, svh, X or Y");
+  VYBDQ_REQUIRE(B >= 1 && B <= 16, VYBDQ_ERR_SHAPE, "B must be in [1, 16]");
+  VYBDQ_REQUIRE(K % 128 == 0 && N % 128 == 0, VYBDQ_ERR_SHAPE, "K and N must be multiples of 128");
+  VYBDQ_REQUIRE(dt_valid_in(x_dt), VYBDQ_ERR_ARG, "x_dt must be F32, F16 or BF16");
+  VYBDQ_REQUIRE(dt_valid_in(y_dt), VYBDQ_ERR_ARG, "y_dt must be F32, F16 or BF16");
+  VYBDQ_REQUIRE(ws && (ws & 255) == 0, VYBDQ_ERR_WORKSPACE, "workspace must be non-null and 256-byte aligned");
+  VYBDQ_REQUIRE(ws_bytes >= exl3_ws_bytes(B, K, N), VYBDQ_ERR_WORKSPACE,
+                "workspace smaller than vybdq_exl3_workspace_size");
+  const int BP = exl3_bp(B);
+  const int S = exl3_splits(K, N, BP);
+  const int KB = static_cast<int>(K / 16);
+  const int kbs = (KB + S - 1) / S;
+  const int NB = static_cast<int>(N / 16);
+  hipStream_t s = as_stream(stream);
+  auto *xp = reinterpret_cast<_Float16 *>(ws);
+  auto *zp = reinterpret_cast<float *>(ws + ((BP * K * 2 + 255) / 256) * 256);
+  const auto *su = reinterpret_cast<const _Float16 *>(suh);
+  const auto *sv = reinterpret_cast<const _Float16 *>(svh);
+  const auto *t = reinterpret_cast<const uint16_t *>(trellis);
+  const dim3 gx(static_cast<unsigned>(K / 128), static_cast<unsigned>(BP));
+  VYBDQ_DISPATCH_IN(x_dt, XDT,
+      hipLaunchKernelGGL((k_exl3_xprep<XDT>), gx, dim3(64), 0, s, reinterpret_cast<const void *>(X), su, xp,
+                         static_cast<int>(B), K));
+#define G(CB)                                                                                   \
+  switch (BP) {                                                                                 \
+    case 1: exl3_gemm_launch<CB, 1>(t, xp, zp, K, NB, S, kbs, s); break;                       \
+    case 2: exl3_gemm_launch<CB, 2>(t, xp, zp, K, NB, S, kbs, s); break;                       \
+    case 4: exl3_gemm_launch<CB, 4>(t, xp, zp, K, NB, S, kbs, s); break;                       \
+    case 8: exl3_gemm_launch<CB, 8>(t, xp, zp, K, NB, S, kbs, s); break;                       \
+    default: exl3_gemm_launch<CB, 16>(t, xp, zp, K, NB, S, kbs, s); break;                     \
+  }
+  if (codebook == VYBDQ_EXL3_MCG) { G(VYBDQ_EXL3_MCG) } else { G(VYBDQ_EXL3_3INST) }
+#undef G
+  const dim3 go(static_cast<unsigned>(N / 128), static_cast<unsigned>(B));
+  void *y = reinterpret_cast<void *>(Y);
+  VYBDQ_DISPATCH_IN(y_dt, YDT,
+      hipLaunchKernelGGL((k_exl3_out<YDT>), go, dim3(64), 0, s, zp, sv, y, BP, S, N));
+  return check_launch("vybdq_exl3_gemm");
+}

@@ -160,3 +160,44 @@ class GemvChain:
     def status(self):
         torch.cuda.synchronize()
         return _lib.lib.vybdq_chain_status(_ptr(self.ws))
+
+
+# ---- EXL3 --------------------------------------------------------------------------------
+
+EXL3_MCG, EXL3_3INST = _lib.EXL3_MCG, _lib.EXL3_3INST
+
+
+def exl3_decode_tiles(trellis, K, N, out_dtype=torch.float16, codebook=_lib.EXL3_MCG):
+    """trellis uint16/int16 [K/16, N/16, 64] -> rotated-basis What [K, N]."""
+    out = torch.empty((K, N), dtype=out_dtype, device=trellis.device)
+    call("vybdq_exl3_decode_tiles", _ptr(trellis), _ptr(out), K, N, codebook, _dt(out_dtype), _stream())
+    return out
+
+
+def exl3_dequant(trellis, suh, svh, K, N, out_dtype=torch.float32, codebook=_lib.EXL3_MCG):
+    """Full W [K, N] = diag(suh) Hs What Hs diag(svh)."""
+    out = torch.empty((K, N), dtype=out_dtype, device=trellis.device)
+    call("vybdq_dequant_exl3", _ptr(trellis), _ptr(suh), _ptr(svh), _ptr(out), K, N, codebook,
+         _dt(out_dtype), _stream())
+    return out
+
+
+class Exl3Linear:
+    """x [B, K] -> y [B, N] through the fused EXL3 GEMM, with its workspace."""
+
+    def __init__(self, trellis, suh, svh, K, N, codebook=_lib.EXL3_MCG, max_batch=16):
+        self.t, self.suh, self.svh, self.K, self.N, self.cb = trellis, suh, svh, K, N, codebook
+        nbytes = max(_lib.lib.vybdq_exl3_workspace_size(b, K, N) for b in (1, 2, 4, 8, max_batch))
+        if nbytes < 0:
+            raise ValueError("unsupported EXL3 shape")
+        self.ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=trellis.device)
+        self.ws_ptr = (self.ws.data_ptr() + 255) // 256 * 256
+        self.ws_bytes = nbytes
+
+    def __call__(self, X, y_dtype=torch.float32, out=None):
+        B = X.shape[0]
+        if out is None:
+            out = torch.empty((B, self.N), dtype=y_dtype, device=X.device)
+        call("vybdq_exl3_gemm", _ptr(self.t), _ptr(self.suh), _ptr(self.svh), _ptr(X), _ptr(out), B,
+             self.K, self.N, self.cb, _dt(X.dtype), _dt(out.dtype), self.ws_ptr, self.ws_bytes, _stream())
+        return out

@@ -27,3 +27,11 @@ def q8_0_weights(rng, N, K):
 
 def activations(rng, shape, dtype=np.float32):
     return rng.standard_normal(shape).astype(dtype)
+
+
+def exl3_tensors(rng, K, N):
+    """EXL3 4-bpw tensors: random uint16 trellis [K/16, N/16, 64], suh/svh fp16 = +-|N(0, 0.01)|."""
+    trellis = rng.integers(0, 65536, (K // 16, N // 16, 64), dtype=np.uint16)
+    suh = (np.abs(rng.normal(0, 0.01, K)) * rng.choice([-1.0, 1.0], K)).astype(np.float16)
+    svh = (np.abs(rng.normal(0, 0.01, N)) * rng.choice([-1.0, 1.0], N)).astype(np.float16)
+    return trellis, suh, svh
