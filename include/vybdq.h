@@ -146,6 +146,42 @@ int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t X, ui
                     int64_t K, int64_t N, int codebook, int x_dt, int y_dt, uint64_t ws, int64_t ws_bytes,
                     uint64_t stream);
 
+/* ---- prefill / grouped dequant GEMM ----------------------------------------------------- */
+
+/* Y [M, N] (row stride ldy, 0 = N) = X [M, K] W^T (+ RS) with W packed GGUF rows of type wtype
+   (2 = q4_0 GGUF order, 8 = Q8_0): weights are dequantized to fp16 in LDS (d * (q - OFF), one
+   rounding) and multiplied with fp16 MFMA, float32 accumulation; X (f32/f16/bf16) is converted to
+   fp16 (|x| < 65504). K % 64 == 0, N % 64 == 0. Replaces gemm_q80 and its siblings
+   (native/tools/gen_rpf.py:1-10, p-block W@0 X@8 Y@16 S@24 N@32 K@40 LDY@48 RS@56). */
+int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K, int x_dt,
+               int y_dt, int64_t ldy, uint64_t RS, uint64_t stream);
+
+/* ---- MoE layer ---------------------------------------------------------------------------- */
+
+/* Router alone: idx_out int32 [T, topk] (descending choice, ties to the lower id),
+   w_out float32 [T, topk] = sigmoid(logit) renormalised over the selection, times scale.
+   bias (float32 [E] or 0) shifts the selection only. Replaces moe_route
+   (native/kernels/moe.vyb:28-95); semantics native/glm53/moe_ref.py:68-78. */
+int vybdq_moe_route(uint64_t logits, int logits_dt, uint64_t bias, uint64_t idx_out, uint64_t w_out,
+                    int64_t T, int64_t E, int64_t topk, double scale, uint64_t stream);
+
+/* Workspace bytes for vybdq_moe_forward, or -1 for an unsupported shape. */
+int64_t vybdq_moe_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk);
+
+/* out [T, H] = sum_s w[t,s] * FFN_{idx[t,s]}(x[t]) + FFN_shared(x[t]) with
+   FFN(x) = (silu(min(x Wg, limit)) * clamp(x Wu, -limit, limit)) Wd. Routed weights are GGUF
+   expert tensors: w_gate/w_up [E][I rows][H], w_down [E][H rows][I], packed type wtype; the
+   shared expert (s_gate/s_up/s_down, or all 0) is one such matrix each. x [T, H] (f32/f16/bf16,
+   16-byte aligned), logits [T, E]. Tokens are bucketed per expert on the device and each
+   expert's rows run through grouped dequant GEMMs; no host synchronisation. idx_out/w_out
+   (optional) receive the routing. Replaces the reference's per-expert host loop
+   (native/glm53/glm_engine.vyb:2720-2953) and moe_route/moe_act/moe_down (moe.vyb:1-170). */
+int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logits, int logits_dt, uint64_t bias,
+                      uint64_t w_gate, uint64_t w_up, uint64_t w_down, uint64_t s_gate, uint64_t s_up,
+                      uint64_t s_down, uint64_t out, int out_dt, uint64_t idx_out, uint64_t w_out, int64_t T,
+                      int64_t H, int64_t I, int64_t E, int64_t topk, double scale, double limit, uint64_t ws,
+                      int64_t ws_bytes, uint64_t stream);
+
 /* ---- activation quantizer ------------------------------------------------------------ */
 
 /* xq8 semantics per row and per 32-value block: a = max|x|, d = a/127, q = sat_s8(rne(x*127/a))

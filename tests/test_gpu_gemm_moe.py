@@ -1,0 +1,139 @@
+"""GPU parity: dequant MFMA GEMM (q4_0 / Q8_0, 2e-3 of the float64 gate) and the MoE layer
+(router against the reference's committed goldens; full layer against the oracle)."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import formats, matmul, moe
+from tests.conftest import GOLDEN
+from vybforge_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+TOL = matmul.TOL
+TDT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def dev_t(a, dev):
+    return torch.from_numpy(np.array(a, copy=True)).to(dev)
+
+
+def gate16(y, ref, dtype):
+    y = np.asarray(y, np.float64)
+    if dtype in (torch.float16, torch.bfloat16):
+        mant = 10 if dtype == torch.float16 else 7
+        half = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - mant - 1)
+        return float(np.maximum(np.abs(y - ref) - half, 0).max() / np.abs(ref).max())
+    return matmul.rel_maxnorm(y, ref)
+
+
+def weights(ty, rng, N, K):
+    return synth.q4_0_weights(rng, N, K) if ty == ops.GGML_Q4_0 else synth.q8_0_weights(rng, N, K)
+
+
+def ref_rows(ty, raw, N, K):
+    return matmul.q4_0_matrix(raw, N, K) if ty == ops.GGML_Q4_0 else matmul.q8_0_matrix(raw, N, K)
+
+
+@pytest.mark.parametrize("ty", [ops.GGML_Q4_0, ops.GGML_Q8_0])
+@pytest.mark.parametrize("M,N,K", [(512, 256, 5120), (16, 128, 256), (64, 192, 128), (200, 256, 512), (1, 64, 64),
+                                   (130, 128, 1024)])
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+def test_gemm(dev, ty, M, N, K, xdt):
+    rng = np.random.default_rng(M + N + K + ty)
+    raw = weights(ty, rng, N, K)
+    x = torch.from_numpy(synth.activations(rng, (M, K))).to(TDT[xdt])
+    y = ops.gemm(ty, dev_t(raw, dev), x.to(dev), N, K).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x.to(torch.float64).numpy(), ref_rows(ty, raw, N, K))
+    assert matmul.rel_maxnorm(y, ref) < TOL
+
+
+@pytest.mark.parametrize("ty,K", [(ops.GGML_Q8_0, 5120), (ops.GGML_Q8_0, 17408)])
+def test_gemm_config3_rows(dev, ty, K):
+    # the prefill shapes M=512 x K x N: a 512-row slice of N checked against float64
+    rng = np.random.default_rng(K)
+    M, N = 512, 512
+    raw = weights(ty, rng, N, K)
+    x = torch.from_numpy(synth.activations(rng, (M, K))).to(torch.bfloat16)
+    y = ops.gemm(ty, dev_t(raw, dev), x.to(dev), N, K, torch.bfloat16).to(torch.float64).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x.to(torch.float64).numpy(), ref_rows(ty, raw, N, K))
+    assert gate16(y, ref, torch.bfloat16) < TOL
+
+
+def test_gemm_residual_f64(dev):
+    rng = np.random.default_rng(5)
+    M, N, K = 70, 128, 256
+    raw = synth.q4_0_weights(rng, N, K)
+    x = synth.activations(rng, (M, K))
+    rs = rng.standard_normal((M, N))
+    y = ops.gemm(ops.GGML_Q4_0, dev_t(raw, dev), dev_t(x, dev), N, K, torch.float64,
+                 residual=dev_t(rs, dev)).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x, ref_rows(ops.GGML_Q4_0, raw, N, K), rs)
+    assert matmul.rel_maxnorm(y, ref) < TOL
+
+
+# ---- MoE -----------------------------------------------------------------------------------
+
+def test_moe_route_reference_goldens(dev):
+    z = np.load(os.path.join(GOLDEN, "moe_golden.npz"))
+    logits = dev_t(z["logits"].astype(np.float32), dev)
+    bias = dev_t(z["bias"].astype(np.float32), dev)
+    idx, w = ops.moe_route(logits, 8, bias, float(z["scale"]))
+    np.testing.assert_array_equal(idx.cpu().numpy(), z["ref_idx"])
+    assert np.abs(w.cpu().numpy() - z["ref_w"]).max() < 1e-4     # verify_moe_vyb.py:59
+
+
+@pytest.mark.parametrize("T,E,k", [(1, 256, 8), (37, 256, 8), (5, 16, 4), (300, 64, 6)])
+def test_moe_route_oracle(dev, T, E, k):
+    rng = np.random.default_rng(T * E)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    idx, w = ops.moe_route(dev_t(logits, dev), k)
+    ridx, rw = moe.route_logits(logits.astype(np.float64), k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    assert np.abs(w.cpu().numpy() - rw).max() < 1e-6
+
+
+def moe_case(dev, ty, T, H, I, E, k, seed, shared=True):
+    rng = np.random.default_rng(seed)
+    gate = [weights(ty, rng, I, H) for _ in range(E)]
+    up = [weights(ty, rng, I, H) for _ in range(E)]
+    down = [weights(ty, rng, H, I) for _ in range(E)]
+    sh = (weights(ty, rng, I, H), weights(ty, rng, I, H), weights(ty, rng, H, I)) if shared else None
+    x = (rng.standard_normal((T, H)) * 0.5).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    layer = ops.MoeLayer(ty, dev_t(np.concatenate(gate), dev), dev_t(np.concatenate(up), dev),
+                         dev_t(np.concatenate(down), dev), H, I, E, k,
+                         shared=tuple(dev_t(a, dev) for a in sh) if sh else None)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    out, idx, w = layer(xb.to(dev), dev_t(logits, dev), routing=True)
+    experts = lambda e: (ref_rows(ty, gate[e], I, H), ref_rows(ty, up[e], I, H), ref_rows(ty, down[e], H, I))
+    shared_w = tuple(ref_rows(ty, a, n, kk) for a, n, kk in zip(sh, (I, I, H), (H, H, I))) if sh else None
+    x64 = xb.to(torch.float64).numpy()
+    if shared_w is None:
+        ref, ridx, rw = moe.moe_forward(x64, logits.astype(np.float64), experts,
+                                        (np.zeros((1, H)), np.zeros((1, H)), np.zeros((H, 1))), topk=k)
+    else:
+        ref, ridx, rw = moe.moe_forward(x64, logits.astype(np.float64), experts, shared_w, topk=k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    assert np.abs(w.cpu().numpy() - rw).max() < 1e-6
+    return out.cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("ty", [ops.GGML_Q4_0, ops.GGML_Q8_0])
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_moe_layer_small(dev, ty, T):
+    out, ref = moe_case(dev, ty, T, H=256, I=128, E=16, k=4, seed=T + ty)
+    assert matmul.rel_maxnorm(out, ref) < TOL
+
+
+def test_moe_layer_no_shared(dev):
+    out, ref = moe_case(dev, ops.GGML_Q4_0, 9, H=128, I=64, E=8, k=2, seed=3, shared=False)
+    assert matmul.rel_maxnorm(out, ref) < TOL
+
+
+def test_moe_layer_glm_shapes(dev):
+    # GLM-5 expert shapes (H 6144, I 2048) with few experts so the float64 oracle stays cheap
+    out, ref = moe_case(dev, ops.GGML_Q4_0, 16, H=6144, I=2048, E=4, k=2, seed=7)
+    assert matmul.rel_maxnorm(out, ref) < TOL

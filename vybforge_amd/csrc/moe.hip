@@ -1,0 +1,263 @@
+// GLM-style MoE layer on one GPU: router, per-expert bucketing, grouped dequant GEMMs with a
+// fused clamped-SwiGLU epilogue, and an atomics-free combine. gfx950.
+//
+// Semantics (native/glm53/moe_ref.py:25-112, native/kernels/moe.vyb:1-170):
+//   scores = sigmoid(logits); choice = scores + bias (bias only selects); idx = top-k(choice)
+//   (descending, ties to the lower expert id); w = scores[idx] / (sum + 1e-20) * scale
+//   expert e: a = silu(min(x Wg_e, L)) * clamp(x Wu_e, -L, L); e_out = a Wd_e
+//   out[t] = sum_s w[t, s] e_out[idx[t, s]](t) + shared(x[t])
+// Without a bias the selection is by logit (sigmoid is monotone: exact order, no float32
+// saturation ties); with a bias the choice is computed in double, as the reference does.
+//
+// Pipeline (all on the stream, no host syncs): route -> bucket (one workgroup: per-expert
+// counts, stable token order, group row/tile tables) -> grouped gate|up GEMM (SwiGLU epilogue,
+// rows gathered by token) -> grouped down GEMM -> shared expert (plain GEMMs) -> combine.
+#include "gemv_dev.h"
+
+namespace vybdq {
+
+// defined in dqgemm.hip
+int dq_gemm_grouped(int wtype, bool swiglu, const uint8_t *W, const uint8_t *W2, int64_t w_stride, const void *X,
+                    int xdt, int64_t ldx, const int *row_map, const int *grp_rows, const int *grp_tiles, int G,
+                    int M, int N, int64_t K, void *Y, int ydt, int64_t ldy, float limit, int max_mtiles,
+                    hipStream_t s);
+int dq_gemm_bm();
+
+template <int LDT>
+__global__ void __launch_bounds__(64) k_moe_route(const void *__restrict__ logits, const float *__restrict__ bias,
+                                                  int E, int topk, double scale, int *__restrict__ idx_out,
+                                                  float *__restrict__ w_out) {
+  const int t = blockIdx.x, lane = threadIdx.x;
+  constexpr int PER = 16;  // experts per lane (E <= 1024)
+  double key[PER];
+  double score[PER];
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    if (e < E) {
+      const double l = static_cast<double>(load_elem<LDT>(logits, static_cast<int64_t>(t) * E + e));
+      score[i] = 1.0 / (1.0 + exp(-l));
+      key[i] = bias ? score[i] + static_cast<double>(bias[e]) : l;
+    } else {
+      score[i] = 0.0;
+      key[i] = -INFINITY;
+    }
+  }
+  double tot = 0.0;
+  double my_sc = 0.0;  // lane s keeps slot s's raw score
+  for (int s = 0; s < topk; ++s) {
+    // lane-local best (lowest index among equal keys), then wave argmax with the same rule
+    double bk = -INFINITY;
+    int be = 1 << 30;
+    for (int i = 0; i < PER; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E && (key[i] > bk || (key[i] == bk && e < be))) { bk = key[i]; be = e; }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const double ok = __shfl_xor(bk, off, 64);
+      const int oe = __shfl_xor(be, off, 64);
+      if (ok > bk || (ok == bk && oe < be)) { bk = ok; be = oe; }
+    }
+    // the owner retires the winner
+    double sc = 0.0;
+    if ((be & 63) == lane) {
+      const int i = be >> 6;
+      for (int ii = 0; ii < PER; ++ii)
+        if (ii == i) { sc = score[ii]; key[ii] = -INFINITY; }
+    }
+    sc = __shfl(sc, be & 63, 64);
+    if (lane == 0) idx_out[t * topk + s] = be;
+    if (lane == s) my_sc = sc;
+    tot += sc;
+  }
+  if (lane < topk) w_out[t * topk + lane] = static_cast<float>(my_sc / (tot + 1e-20) * scale);
+}
+
+// One workgroup: per-expert counts, exclusive scans, and each (token, slot)'s bucket position
+// in stable token order. grp_rows[E+1], grp_tiles[E+1] (ceil(count/BM) per expert), row_map[T*k]
+// (bucket position -> token), pos[T*k] ((token, slot) -> bucket position).
+__global__ void __launch_bounds__(256) k_moe_bucket(const int *__restrict__ idx, int T, int topk, int E, int BM,
+                                                    int *__restrict__ grp_rows, int *__restrict__ grp_tiles,
+                                                    int *__restrict__ row_map, int *__restrict__ pos) {
+  extern __shared__ int sh[];
+  int *cnt = sh;          // [E]
+  int *scan_r = sh + E;   // [E + 1]
+  int *scan_t = scan_r + E + 1;
+  const int n = T * topk;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += blockDim.x) atomicAdd(&cnt[idx[i]], 1);  // counts are order-free
+  __syncthreads();
+  if (threadIdx.x == 0) {  // E <= 1024: a serial scan is a few microseconds at most
+    int r = 0, tl = 0;
+    for (int e = 0; e < E; ++e) {
+      scan_r[e] = r;
+      scan_t[e] = tl;
+      r += cnt[e];
+      tl += (cnt[e] + BM - 1) / BM;
+    }
+    scan_r[E] = r;
+    scan_t[E] = tl;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e <= E; e += blockDim.x) {
+    grp_rows[e] = scan_r[e];
+    grp_tiles[e] = scan_t[e];
+  }
+  // stable positions: the owner thread of expert e walks the tokens in order
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    if (cnt[e] == 0) continue;
+    int p = scan_r[e];
+    for (int t = 0; t < T; ++t)
+      for (int s = 0; s < topk; ++s)
+        if (idx[t * topk + s] == e) {
+          row_map[p] = t;
+          pos[t * topk + s] = p;
+          ++p;
+        }
+  }
+}
+
+// out[t][h] = sum_s w[t,s] * rows[pos[t,s]][h] (+ shared[t][h]); fixed slot order.
+template <int ODT>
+__global__ void __launch_bounds__(256) k_moe_combine(const float *__restrict__ rows, const float *__restrict__ shared,
+                                                     const int *__restrict__ pos, const float *__restrict__ w, int T,
+                                                     int topk, int64_t H, void *__restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= T * H) return;
+  const int t = static_cast<int>(i / H);
+  const int64_t h = i % H;
+  float acc = 0.f;
+  for (int s = 0; s < topk; ++s) acc = fmaf(w[t * topk + s], rows[static_cast<int64_t>(pos[t * topk + s]) * H + h], acc);
+  if (shared) acc += shared[i];
+  store_elem<ODT>(out, nullptr, i, acc);
+}
+
+struct MoeWs {
+  int *idx, *pos, *grp_rows, *grp_tiles, *row_map;
+  float *w, *rows, *shared;
+  _Float16 *act, *act_s;
+  int64_t bytes;
+};
+
+static MoeWs moe_layout(char *base, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k) {
+  MoeWs m{};
+  int64_t off = 0;
+  auto take = [&](int64_t n) {
+    char *p = base ? base + off : nullptr;
+    off += (n + 255) / 256 * 256;
+    return p;
+  };
+  m.idx = reinterpret_cast<int *>(take(4 * T * k));
+  m.w = reinterpret_cast<float *>(take(4 * T * k));
+  m.pos = reinterpret_cast<int *>(take(4 * T * k));
+  m.row_map = reinterpret_cast<int *>(take(4 * T * k));
+  m.grp_rows = reinterpret_cast<int *>(take(4 * (E + 1)));
+  m.grp_tiles = reinterpret_cast<int *>(take(4 * (E + 1)));
+  m.act = reinterpret_cast<_Float16 *>(take(2 * T * k * I));
+  m.rows = reinterpret_cast<float *>(take(4 * T * k * H));
+  m.act_s = reinterpret_cast<_Float16 *>(take(2 * T * I));
+  m.shared = reinterpret_cast<float *>(take(4 * T * H));
+  m.bytes = off;
+  return m;
+}
+
+}  // namespace vybdq
+
+using namespace vybdq;
+
+extern "C" int64_t vybdq_moe_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk) {
+  if (T < 1 || H < 64 || I < 64 || E < 1 || E > 1024 || topk < 1 || topk > E || topk > 64) return -1;
+  return moe_layout(nullptr, T, H, I, E, topk).bytes;
+}
+
+extern "C" int vybdq_moe_route(uint64_t logits, int logits_dt, uint64_t bias, uint64_t idx_out, uint64_t w_out,
+                               int64_t T, int64_t E, int64_t topk, double scale, uint64_t stream) {
+  VYBDQ_REQUIRE(logits && idx_out && w_out, VYBDQ_ERR_ARG, "null logits, idx_out or w_out");
+  VYBDQ_REQUIRE(dt_valid_in(logits_dt), VYBDQ_ERR_ARG, "logits_dt must be F32, F16 or BF16");
+  VYBDQ_REQUIRE(T >= 1 && T < (1 << 24) && E >= 1 && E <= 1024 && topk >= 1 && topk <= E && topk <= 64,
+                VYBDQ_ERR_SHAPE, "need 1 <= topk <= E <= 1024 and topk <= 64");
+  hipStream_t s = as_stream(stream);
+  const void *lg = reinterpret_cast<const void *>(logits);
+  VYBDQ_DISPATCH_IN(logits_dt, LDT,
+      hipLaunchKernelGGL((k_moe_route<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg,
+                         reinterpret_cast<const float *>(bias), static_cast<int>(E), static_cast<int>(topk), scale,
+                         reinterpret_cast<int *>(idx_out), reinterpret_cast<float *>(w_out)));
+  return check_launch("vybdq_moe_route");
+}
+
+extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logits, int logits_dt, uint64_t bias,
+                                 uint64_t w_gate, uint64_t w_up, uint64_t w_down, uint64_t s_gate, uint64_t s_up,
+                                 uint64_t s_down, uint64_t out, int out_dt, uint64_t idx_out, uint64_t w_out,
+                                 int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk, double scale,
+                                 double limit, uint64_t ws, int64_t ws_bytes, uint64_t stream) {
+  VYBDQ_REQUIRE(wtype == 2 || wtype == 8, VYBDQ_ERR_ARG, "wtype must be 2 (q4_0) or 8 (Q8_0)");
+  VYBDQ_REQUIRE(x && logits && w_gate && w_up && w_down && out, VYBDQ_ERR_ARG, "null input or output");
+  VYBDQ_REQUIRE((s_gate == 0) == (s_up == 0) && (s_up == 0) == (s_down == 0), VYBDQ_ERR_ARG,
+                "shared expert: give all three matrices or none");
+  VYBDQ_REQUIRE(dt_valid_in(x_dt) && dt_valid_in(logits_dt), VYBDQ_ERR_ARG, "x_dt/logits_dt must be F32, F16 or BF16");
+  VYBDQ_REQUIRE(out_dt == VYBDQ_F32 || out_dt == VYBDQ_F16 || out_dt == VYBDQ_BF16, VYBDQ_ERR_ARG,
+                "out_dt must be F32, F16 or BF16");
+  const int64_t need = vybdq_moe_workspace_size(T, H, I, E, topk);
+  VYBDQ_REQUIRE(need > 0, VYBDQ_ERR_SHAPE, "unsupported T, H, I, E or topk (E <= 1024, topk <= 64)");
+  VYBDQ_REQUIRE(H % 64 == 0 && I % 64 == 0, VYBDQ_ERR_SHAPE, "H and I must be multiples of 64");
+  VYBDQ_REQUIRE(T * topk < (1 << 24), VYBDQ_ERR_SHAPE, "too many tokens");
+  VYBDQ_REQUIRE(ws && (ws & 255) == 0 && ws_bytes >= need, VYBDQ_ERR_WORKSPACE,
+                "workspace must be 256-byte aligned and at least vybdq_moe_workspace_size bytes");
+  VYBDQ_REQUIRE((x & 15) == 0 && (w_gate & 3) == 0 && (w_up & 3) == 0 && (w_down & 3) == 0, VYBDQ_ERR_ALIGN,
+                "x must be 16-byte and weights 4-byte aligned");
+  hipStream_t s = as_stream(stream);
+  MoeWs m = moe_layout(reinterpret_cast<char *>(ws), T, H, I, E, topk);
+  const int BM = dq_gemm_bm();
+  const int n = static_cast<int>(T * topk);
+  int *idx = idx_out ? reinterpret_cast<int *>(idx_out) : m.idx;
+  float *wts = w_out ? reinterpret_cast<float *>(w_out) : m.w;
+  const void *lg = reinterpret_cast<const void *>(logits);
+  const float *bs = reinterpret_cast<const float *>(bias);
+  VYBDQ_DISPATCH_IN(logits_dt, LDT,
+      hipLaunchKernelGGL((k_moe_route<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg, bs,
+                         static_cast<int>(E), static_cast<int>(topk), scale, idx, wts));
+  int rc = check_launch("moe route");
+  if (rc) return rc;
+  const size_t sh = static_cast<size_t>(3 * E + 2) * 4;
+  hipLaunchKernelGGL(k_moe_bucket, dim3(1), dim3(256), sh, s, idx, static_cast<int>(T), static_cast<int>(topk),
+                     static_cast<int>(E), BM, m.grp_rows, m.grp_tiles, m.row_map, m.pos);
+  rc = check_launch("moe bucket");
+  if (rc) return rc;
+  const int64_t rb_h = (H / 64) * (wtype == 2 ? 36 : 68);  // row bytes, K = H
+  const int64_t rb_i = (I / 64) * (wtype == 2 ? 36 : 68);  // row bytes, K = I
+  const int max_mt = static_cast<int>((n + BM - 1) / BM + (E < n ? E : n));
+  // routed gate|up with SwiGLU -> act [n][I] (bucket order)
+  rc = dq_gemm_grouped(wtype, true, reinterpret_cast<const uint8_t *>(w_gate), reinterpret_cast<const uint8_t *>(w_up),
+                       I * rb_h, reinterpret_cast<const void *>(x), x_dt, H, m.row_map, m.grp_rows, m.grp_tiles,
+                       static_cast<int>(E), n, static_cast<int>(I), H, m.act, VYBDQ_F16, I,
+                       static_cast<float>(limit), max_mt, s);
+  if (rc) return rc;
+  // routed down -> rows [n][H]
+  rc = dq_gemm_grouped(wtype, false, reinterpret_cast<const uint8_t *>(w_down), nullptr, H * rb_i, m.act, VYBDQ_F16,
+                       I, nullptr, m.grp_rows, m.grp_tiles, static_cast<int>(E), n, static_cast<int>(H), I, m.rows,
+                       VYBDQ_F32, H, 0.f, max_mt, s);
+  if (rc) return rc;
+  const float *shared = nullptr;
+  if (s_gate) {
+    const int mt = static_cast<int>((T + BM - 1) / BM);
+    rc = dq_gemm_grouped(wtype, true, reinterpret_cast<const uint8_t *>(s_gate), reinterpret_cast<const uint8_t *>(s_up),
+                         0, reinterpret_cast<const void *>(x), x_dt, H, nullptr, nullptr, nullptr, 1,
+                         static_cast<int>(T), static_cast<int>(I), H, m.act_s, VYBDQ_F16, I, static_cast<float>(limit),
+                         mt, s);
+    if (rc) return rc;
+    rc = dq_gemm_grouped(wtype, false, reinterpret_cast<const uint8_t *>(s_down), nullptr, 0, m.act_s, VYBDQ_F16, I,
+                         nullptr, nullptr, nullptr, 1, static_cast<int>(T), static_cast<int>(H), I, m.shared,
+                         VYBDQ_F32, H, 0.f, mt, s);
+    if (rc) return rc;
+    shared = m.shared;
+  }
+  const int64_t tot = T * H;
+  const unsigned gc = static_cast<unsigned>((tot + 255) / 256);
+  void *o = reinterpret_cast<void *>(out);
+  switch (out_dt) {
+    case VYBDQ_F32: hipLaunchKernelGGL((k_moe_combine<VYBDQ_F32>), dim3(gc), dim3(256), 0, s, m.rows, shared, m.pos, wts, static_cast<int>(T), static_cast<int>(topk), H, o); break;
+    case VYBDQ_F16: hipLaunchKernelGGL((k_moe_combine<VYBDQ_F16>), dim3(gc), dim3(256), 0, s, m.rows, shared, m.pos, wts, static_cast<int>(T), static_cast<int>(topk), H, o); break;
+    default: hipLaunchKernelGGL((k_moe_combine<VYBDQ_BF16>), dim3(gc), dim3(256), 0, s, m.rows, shared, m.pos, wts, static_cast<int>(T), static_cast<int>(topk), H, o); break;
+  }
+  return check_launch("moe combine");
+}

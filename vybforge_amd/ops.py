@@ -201,3 +201,63 @@ class Exl3Linear:
         call("vybdq_exl3_gemm", _ptr(self.t), _ptr(self.suh), _ptr(self.svh), _ptr(X), _ptr(out), B,
              self.K, self.N, self.cb, _dt(X.dtype), _dt(out.dtype), self.ws_ptr, self.ws_bytes, _stream())
         return out
+
+
+# ---- prefill GEMM and MoE ------------------------------------------------------------------
+
+def gemm(ty, W, X, N, K, y_dtype=torch.float32, residual=None, out=None):
+    """Y [M, N] = X [M, K] W^T (+ residual) through the dequant MFMA GEMM."""
+    M = X.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=y_dtype, device=X.device)
+    call("vybdq_gemm", ty, _ptr(W), _ptr(X), _ptr(out), M, N, K, _dt(X.dtype), _dt(out.dtype), 0,
+         _ptr(residual), _stream())
+    return out
+
+
+def moe_route(logits, topk, bias=None, scale=2.5):
+    T, E = logits.shape
+    idx = torch.empty((T, topk), dtype=torch.int32, device=logits.device)
+    w = torch.empty((T, topk), dtype=torch.float32, device=logits.device)
+    call("vybdq_moe_route", _ptr(logits), _dt(logits.dtype), _ptr(bias), _ptr(idx), _ptr(w), T, E, topk,
+         float(scale), _stream())
+    return idx, w
+
+
+class MoeLayer:
+    """GLM-style MoE layer over packed expert tensors (GGUF row layout, stacked per expert)."""
+
+    def __init__(self, ty, w_gate, w_up, w_down, H, I, E, topk=8, shared=None, scale=2.5, limit=10.0,
+                 bias=None):
+        self.ty, self.H, self.I, self.E, self.topk = ty, H, I, E, topk
+        self.w = (w_gate, w_up, w_down)
+        self.shared = shared
+        self.scale, self.limit, self.bias = scale, limit, bias
+        self._ws = None
+        self._ws_t = 0
+
+    def _workspace(self, T, device):
+        if self._ws is None or self._ws_t < T:
+            n = _lib.lib.vybdq_moe_workspace_size(T, self.H, self.I, self.E, self.topk)
+            if n < 0:
+                raise ValueError("unsupported MoE shape")
+            self._ws = torch.empty(n + 256, dtype=torch.uint8, device=device)
+            self._ws_t = T
+            self._ws_bytes = n
+        return (self._ws.data_ptr() + 255) // 256 * 256, self._ws_bytes
+
+    def __call__(self, x, logits, out_dtype=torch.float32, out=None, routing=False):
+        T = x.shape[0]
+        if out is None:
+            out = torch.empty((T, self.H), dtype=out_dtype, device=x.device)
+        idx = w = None
+        if routing:
+            idx = torch.empty((T, self.topk), dtype=torch.int32, device=x.device)
+            w = torch.empty((T, self.topk), dtype=torch.float32, device=x.device)
+        ws, nb = self._workspace(T, x.device)
+        sg, su, sd = self.shared if self.shared else (None, None, None)
+        call("vybdq_moe_forward", self.ty, _ptr(x), _dt(x.dtype), _ptr(logits), _dt(logits.dtype),
+             _ptr(self.bias), _ptr(self.w[0]), _ptr(self.w[1]), _ptr(self.w[2]), _ptr(sg), _ptr(su), _ptr(sd),
+             _ptr(out), _dt(out.dtype), _ptr(idx), _ptr(w), T, self.H, self.I, self.E, self.topk,
+             float(self.scale), float(self.limit), ws, nb, _stream())
+        return (out, idx, w) if routing else out
