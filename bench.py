@@ -33,7 +33,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="stack", choices=["stack", "stack_chain", "gemv1", "exl3"])
+    ap.add_argument("--config", default="stack", choices=["stack", "stack_chain", "gemv1", "exl3", "prefill", "moe"])
+    ap.add_argument("--tokens", type=int, default=16, help="tokens for --config moe")
     ap.add_argument("--batch", type=int, default=1, help="batch for --config exl3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--seed", type=int, default=0)
@@ -288,6 +289,82 @@ def run_exl3(args, torch, dev):
                 bytes_per_step=bytes_call * ncopy, launches_per_step=ncopy)
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def q8_0_blocks_gpu(torch, gen, N, K, dev):
+    """Seeded packed Q8_0 rows on the device: fp16 d = |N(0, 0.01)|, int8 uniform in [-127, 127]."""
+    nb = N * (K // 32)
+    blk = torch.empty((nb, 34), dtype=torch.uint8, device=dev)
+    d = (torch.randn(nb, generator=gen, device=dev) * 0.01).abs().to(torch.float16)
+    blk[:, 0:2] = d.view(torch.uint8).view(nb, 2)
+    blk[:, 2:] = torch.randint(-127, 128, (nb, 32), generator=gen, device=dev, dtype=torch.int8).view(torch.uint8)
+    return blk.view(-1)
+
+
+def run_prefill(args, torch, dev):
+    """Config 3: Q8_0 prefill GEMMs M=512 (up K=5120 -> N=17408, down K=17408 -> N=5120), bf16 X,
+    f32 Y, 3 rotated weight copies of each (>500 MB, past the 256 MB MALL)."""
+    from vybforge_amd import ops
+    M = 512
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    shapes = [(17408, 5120), (5120, 17408)]
+    ncopy = 3
+    launches, flops, nbytes = [], 0, 0
+    for N, K in shapes:
+        x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
+        y = torch.empty(M, N, device=dev)
+        for _ in range(ncopy):
+            W = q8_0_blocks_gpu(torch, gen, N, K, dev)
+            launches.append(lambda W=W, x=x, y=y, N=N, K=K: ops.gemm(ops.GGML_Q8_0, W, x, N, K, out=y))
+            flops += 2 * M * N * K
+            nbytes += N * K // 32 * 34 + 2 * M * K + 4 * M * N
+    ms, wall = timed_graph(torch, launches, args.steps, args.warmup)
+    tflops = flops / (ms * 1e-3) / 1e12
+    per = ms / len(launches)
+    roofline = dict(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                    frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), traffic=None,
+                    kernel="k_dq_gemm<Q8_0,128,128> (fp16 MFMA 16x16x32)", avg_launch_us=round(per * 1e3, 3),
+                    flops_per_launch=flops // len(launches))
+    return dict(value=tflops, unit="TFLOP/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
+                workload="Q8_0 prefill GEMMs M=512: 5120->17408 and 17408->5120 (bf16 X, f32 Y)",
+                bytes_per_step=nbytes, launches_per_step=len(launches))
+
+
+def run_moe(args, torch, dev):
+    """Config 5: GLM-5-style MoE layer, H=6144, 256 routed + 1 shared expert, top-8, I=2048,
+    q4_0 expert tensors (5.46 GB), T tokens bf16, router logits N(0,1)."""
+    from vybforge_amd import ops
+    H, I, E, k, T = 6144, 2048, 256, 8, args.tokens
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    wg = q4_0_blocks_gpu(torch, gen, E * I, H, dev)
+    wu = q4_0_blocks_gpu(torch, gen, E * I, H, dev)
+    wd = q4_0_blocks_gpu(torch, gen, E * H, I, dev)
+    sh = (q4_0_blocks_gpu(torch, gen, I, H, dev), q4_0_blocks_gpu(torch, gen, I, H, dev),
+          q4_0_blocks_gpu(torch, gen, H, I, dev))
+    layer = ops.MoeLayer(ops.GGML_Q4_0, wg, wu, wd, H, I, E, k, shared=sh)
+    x = torch.randn(T, H, generator=gen, device=dev).to(torch.bfloat16)
+    logits = torch.randn(T, E, generator=gen, device=dev)
+    out = torch.empty(T, H, device=dev)
+    _, idx, _ = layer(x, logits, out=out, routing=True)
+    distinct = int(torch.unique(idx).numel())
+    ms, wall = timed_graph(torch, [lambda: layer(x, logits, out=out)], args.steps, args.warmup)
+    per_expert = 3 * I * H // 32 * 18
+    nbytes = (distinct + 1) * per_expert + T * H * 2 + T * E * 4 + T * H * 4
+    flops = T * (k + 1) * 3 * 2 * I * H
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    roofline = dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None,
+                    kernel="MoE layer (route, bucket, grouped k_dq_gemm gate|up+SwiGLU, down, shared, combine)",
+                    avg_launch_us=round(ms * 1e3, 3), bytes_per_launch=nbytes)
+    return dict(value=gbs, ms_step=ms, wall=wall, roofline=roofline, flops=flops,
+                workload=f"GLM-5-style MoE layer T={T}: H=6144, 256+1 experts, top-8, I=2048, q4_0 "
+                         f"({distinct} distinct routed experts hit)",
+                bytes_per_step=nbytes, launches_per_step=1)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -302,18 +379,23 @@ def main():
         r = run_gemv1(args, torch, dev)
     elif args.config == "exl3":
         r = run_exl3(args, torch, dev)
+    elif args.config == "prefill":
+        r = run_prefill(args, torch, dev)
+    elif args.config == "moe":
+        r = run_moe(args, torch, dev)
     else:
         r = run_stack(args, torch, dev)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_stack() if args.config in ("stack", "stack_chain") else None
     line = dict(
-        metric=METRIC, value=round(r["value"], 2), unit="GB/s", n_gpus=1, steps=args.steps,
+        metric=METRIC, value=round(r["value"], 2), unit=r.get("unit", "GB/s"), n_gpus=1, steps=args.steps,
         warmup=args.warmup, ms_per_step=round(r["ms_step"], 4), higher_is_better=True,
         scaling="weak", vs_baseline=None, dtype="f16",
         data="synthetic (seeded q4_0 weights generated on the device, fp16 activations N(0,1))",
         config=dict(workload=r["workload"], bytes_per_step=r["bytes_per_step"],
-                    launches_per_step=r["launches_per_step"], hbm_frac=round(r["value"] / HBM_PEAK_GBS, 4),
+                    launches_per_step=r["launches_per_step"],
+                    hbm_frac=round(r["bytes_per_step"] / (r["ms_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     tflops=round(r["flops"] / (r["ms_step"] * 1e-3) / 1e12, 3)),
         roofline=r["roofline"], cpu_baseline=cpu)
     print(json.dumps(line))
