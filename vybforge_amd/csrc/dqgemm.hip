@@ -9,17 +9,21 @@
 // The grid is sized for the worst case; workgroups whose tile index falls past the last group's
 // tiles exit at once.
 //
-// Per K step (64 = one q4_0/Q8_0 block pair): each thread dequantizes one 32-weight block of one
-// weight row to fp16 (d * (q - OFF) computed exactly in fp16 then rounded once by the scale
-// multiply) into LDS, X rows are gathered, converted to fp16 and staged into LDS, and every wave
-// issues v_mfma_f32_16x16x32_f16 over its 16x16 sub-tiles. The weight pair of the next K step is
-// loaded into registers before the current step's MFMAs. X is converted to fp16: activations
-// must stay below 65504 in magnitude.
+// Per K step (KP block pairs of 64 k, KP chosen so that the BN weight rows give every thread one
+// 32-weight block): each thread dequantizes its block to fp16 (d * (q - OFF) computed exactly in
+// fp16 then rounded once by the scale multiply) into LDS, X rows are gathered, converted to fp16
+// and staged into LDS, and every wave issues v_mfma_f32_16x16x32_f16 over its 16x16 sub-tiles.
+// Each thread keeps D steps of weight loads in flight (a register ring) and prefetches the next
+// step's X before the MFMAs, so HBM latency is overlapped across steps. A last step with fewer
+// than KP pairs is zero-filled. X is converted to fp16: activations must stay below 65504 in
+// magnitude.
 //
 // Epilogues: STORE (f32/f16/bf16/f64, optional residual of the output type) and SWIGLU: the
 // workgroup's weight rows are BN/2 rows of the gate matrix and the same BN/2 rows of the up
 // matrix, and y = silu(min(g, L)) * clamp(u, -L, L) (native/glm53/moe_ref.py:81-84).
 #include "gemv_dev.h"
+
+#include <type_traits>
 
 namespace vybdq {
 
@@ -64,14 +68,44 @@ __device__ __forceinline__ void dequant_block_f16(const uint32_t (&q)[Fmt<FMT>::
   for (int i = 0; i < 16; ++i) out[i] = (wv[i] + off) * dd;  // exact (q - OFF), one rounding
 }
 
-template <int FMT, int ORDER, int BM, int BN, int EPI>
+// X chunk (8 consecutive k of one row at element offset off) -> 8 fp16 in a u4
+template <int XDT>
+__device__ __forceinline__ u4 load_x8_f16(const void *X, int64_t off) {
+  u4 hv;
+  if constexpr (XDT == VYBDQ_F16) {
+    hv = *reinterpret_cast<const u4 *>(static_cast<const _Float16 *>(X) + off);
+  } else if constexpr (XDT == VYBDQ_BF16) {
+    const u4 v = *reinterpret_cast<const u4 *>(static_cast<const uint16_t *>(X) + off);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t w = v[j];
+      hv[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(__uint_as_float(w << 16)),
+                                              static_cast<_Float16>(__uint_as_float(w & 0xffff0000u))});
+    }
+  } else {
+    const f4 *src = reinterpret_cast<const f4 *>(static_cast<const float *>(X) + off);
+    const f4 x0 = src[0], x1 = src[1];
+    hv[0] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(x0[0]), static_cast<_Float16>(x0[1])});
+    hv[1] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(x0[2]), static_cast<_Float16>(x0[3])});
+    hv[2] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(x1[0]), static_cast<_Float16>(x1[1])});
+    hv[3] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(x1[2]), static_cast<_Float16>(x1[3])});
+  }
+  return hv;
+}
+
+template <int FMT, int ORDER, int XDT, int BM, int BN, int EPI>
 __global__ void __launch_bounds__(256) k_dq_gemm(GemmArgs a) {
-  constexpr int BK = 64;
+  // KP weight pairs (64 k each) per step so that BN rows x 2 blocks x KP = 256 block tasks
+  constexpr int KP = BN * 2 >= 256 ? 1 : 256 / (BN * 2);
+  constexpr int BK = 64 * KP;
+  static_assert(BN * 2 * KP == 256, "one 32-weight block per thread per step");
   constexpr int LDA = BK + 8;  // fp16 row stride in LDS (pad: 16 B)
   constexpr int PD = Fmt<FMT>::PAIR_DWORDS;
   constexpr int QDW = Fmt<FMT>::QDW;
   constexpr int NT = BN / 64;  // 16-column MFMA tiles per wave (4 waves split BN)
   constexpr int MT = BM / 16;
+  constexpr int D = FMT == FMT_Q4_0 ? 4 : 2;  // weight steps in flight per thread
+  constexpr int XC = (BM * BK / 8 + 255) / 256;  // X chunks (8 k) per thread per step
   __shared__ __attribute__((aligned(16))) _Float16 As[BM * LDA];
   __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * LDA];
 
@@ -83,7 +117,7 @@ __global__ void __launch_bounds__(256) k_dq_gemm(GemmArgs a) {
   if (a.grp_tiles) {
     const int total = a.grp_tiles[a.G];
     if (mt_global >= total) return;
-    int lo = 0, hi = a.G - 1;  // last group with grp_tiles[g] <= mt_global
+    int lo = 0, hi = a.G - 1;  // last group with grp_tiles[g] <= mt_global (skips empty groups)
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (a.grp_tiles[mid] <= mt_global) lo = mid; else hi = mid - 1;
@@ -101,13 +135,15 @@ __global__ void __launch_bounds__(256) k_dq_gemm(GemmArgs a) {
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int P = static_cast<int>(a.K >> 6);
+  const int S = (P + KP - 1) / KP;  // K steps; the last one may hold fewer than KP pairs
   const int64_t rowbytes = static_cast<int64_t>(P) * Fmt<FMT>::PAIR_BYTES;
 
-  // ---- this thread's dequant task: weight row br (of BN), block h of the pair
-  const int br = tid >> 1, bh = tid & 1;
-  const bool has_task = br < BN;
-  const uint8_t *wrow = nullptr;
-  if (has_task) {
+  // ---- dequant task: weight row br, pair kp of the step, block bh of the pair
+  const int br = tid / (2 * KP);
+  const int kp = (tid / 2) % KP;
+  const int bh = tid & 1;
+  const uint8_t *wrow;
+  {
     int n = ntile * BN + br;
     const uint8_t *base = a.W;
     if constexpr (EPI == EPI_SWIGLU) {
@@ -118,6 +154,32 @@ __global__ void __launch_bounds__(256) k_dq_gemm(GemmArgs a) {
     }
     wrow = base + static_cast<int64_t>(mat) * a.w_stride + static_cast<int64_t>(n) * rowbytes;
   }
+  auto wptr = [&](int step) {
+    int pi = step * KP + kp;
+    pi = pi < P ? pi : P - 1;  // loads past the end re-read the last pair
+    return wrow + static_cast<int64_t>(pi) * Fmt<FMT>::PAIR_BYTES;
+  };
+  // ---- X task: chunks c = tid + 256 i of the BM x BK tile. Row offsets (through row_map) are
+  // resolved once here: a dependent index load inside the K loop would make the wait for it
+  // drain every weight load in flight. Loads are unconditional: tile rows past `rows` read row
+  // row0 (they only feed output rows that are never stored) and k past K (a last step with
+  // fewer than KP pairs) re-reads k - 64, which meets zero weights.
+  int64_t xbase[XC];
+  int xk[XC];
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int c = tid + 256 * i;
+    const int m = c / (BK / 8), kc = c % (BK / 8);
+    const int r = row0 + (c < BM * BK / 8 && m < rows ? m : 0);
+    const int64_t xr = a.row_map ? a.row_map[r] : r;
+    xbase[i] = xr * a.ldx;
+    xk[i] = 8 * kc;
+  }
+  auto x_off = [&](int i, int step) {
+    int64_t k = static_cast<int64_t>(step) * BK + xk[i];
+    k = k < a.K ? k : k - 64;
+    return xbase[i] + k;
+  };
 
   f4 acc[MT][NT];
 #pragma unroll
@@ -125,65 +187,56 @@ __global__ void __launch_bounds__(256) k_dq_gemm(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  uint32_t dw[PD];
-  if (has_task) load_pair<FMT>(wrow, dw);
+  // ring of D steps: X and weights of step s + D are issued, in that order, when step s is consumed
+  // (loads complete in issue order, so X fetched one step ahead would make every wait for it also
+  // wait for the weight loads issued before it); the prologue issues in the same order
+  uint32_t dw[D][PD];
+  u4 xr[D][XC];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+#pragma unroll
+    for (int i = 0; i < XC; ++i) xr[d][i] = load_x8_f16<XDT>(a.X, x_off(i, d < S ? d : S - 1));
+    load_pair<FMT>(wptr(d), dw[d]);
+    // keep the issue order (the scheduler would otherwise interleave the stages, and the loop's
+    // first wait would then have to drain them all)
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
-  for (int p = 0; p < P; ++p) {
-    // stage the dequantized weight block
-    if (has_task) {
+  // one K step from ring slot DC; REFILL: issue the loads of step + D into the slot
+  auto k_step = [&](auto dc, auto refill, int step) {
+    constexpr int d = decltype(dc)::value;
+    // weights of this step -> LDS (block bh of the pair, branch-free: bh differs between lanes)
+    {
       uint32_t q[QDW];
-      uint32_t d16;
-      if (bh == 0) {
 #pragma unroll
-        for (int t = 0; t < QDW; ++t) q[t] = __builtin_amdgcn_alignbit(dw[t + 1], dw[t], 16);
-        d16 = dw[0] & 0xffffu;
-      } else {
-#pragma unroll
-        for (int t = 0; t < QDW; ++t) q[t] = dw[QDW + 1 + t];
-        d16 = dw[QDW] >> 16;
-      }
+      for (int t = 0; t < QDW; ++t)
+        q[t] = bh ? dw[d][QDW + 1 + t] : __builtin_amdgcn_alignbit(dw[d][t + 1], dw[d][t], 16);
+      uint32_t d16 = bh ? dw[d][QDW] >> 16 : dw[d][0] & 0xffffu;
+      if (KP > 1) d16 = step * KP + kp < P ? d16 : 0u;  // pair past the end: zero scale, zero weights
       h2 w16[16];
       dequant_block_f16<FMT, ORDER>(q, d16, w16);
-      u4 *dst = reinterpret_cast<u4 *>(Bs + br * LDA + 32 * bh);
+      u4 *dst = reinterpret_cast<u4 *>(Bs + br * LDA + 64 * kp + 32 * bh);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         dst[i] = u4{__builtin_bit_cast(uint32_t, w16[4 * i]), __builtin_bit_cast(uint32_t, w16[4 * i + 1]),
                     __builtin_bit_cast(uint32_t, w16[4 * i + 2]), __builtin_bit_cast(uint32_t, w16[4 * i + 3])};
-      if (p + 1 < P) load_pair<FMT>(wrow + static_cast<int64_t>(p + 1) * Fmt<FMT>::PAIR_BYTES, dw);
     }
-    // stage X rows (gathered), fp16: BM rows x 64 k = BM*8 chunks of 8
-    for (int c = tid; c < BM * 8; c += 256) {
-      const int m = c >> 3, kc = c & 7;
-      u4 hv = u4{0, 0, 0, 0};
-      if (m < rows) {
-        const int r = row0 + m;
-        const int64_t xr = a.row_map ? a.row_map[r] : r;
-        const int64_t off = xr * a.ldx + 64 * static_cast<int64_t>(p) + 8 * kc;
-        if (a.xdt == VYBDQ_F16) {
-          hv = *reinterpret_cast<const u4 *>(static_cast<const _Float16 *>(a.X) + off);
-        } else if (a.xdt == VYBDQ_BF16) {
-          const u4 v = *reinterpret_cast<const u4 *>(static_cast<const uint16_t *>(a.X) + off);
+    // X of this step -> LDS
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint32_t w = v[j];
-            hv[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(__uint_as_float(w << 16)),
-                                                    static_cast<_Float16>(__uint_as_float(w & 0xffff0000u))});
-          }
-        } else {
-          const f4 *src = reinterpret_cast<const f4 *>(static_cast<const float *>(a.X) + off);
-          const f4 x0 = src[0], x1 = src[1];
-          hv[0] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(x0[0]), static_cast<_Float16>(x0[1])});
-          hv[1] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(x0[2]), static_cast<_Float16>(x0[3])});
-          hv[2] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(x1[0]), static_cast<_Float16>(x1[1])});
-          hv[3] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(x1[2]), static_cast<_Float16>(x1[3])});
-        }
-      }
-      *reinterpret_cast<u4 *>(As + m * LDA + 8 * kc) = hv;
+    for (int i = 0; i < XC; ++i) {
+      const int c = tid + 256 * i;
+      if (c < BM * BK / 8) *reinterpret_cast<u4 *>(As + (c / (BK / 8)) * LDA + 8 * (c % (BK / 8))) = xr[d][i];
+    }
+    if constexpr (decltype(refill)::value) {
+      const int nx = step + D < S ? step + D : S - 1;  // past the end: re-read the last step (cache hits)
+#pragma unroll
+      for (int i = 0; i < XC; ++i) xr[d][i] = load_x8_f16<XDT>(a.X, x_off(i, nx));
+      load_pair<FMT>(wptr(step + D), dw[d]);
     }
     __syncthreads();
     // MFMA: wave owns weight rows [wave*BN/4, (wave+1)*BN/4)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+    for (int kk = 0; kk < BK / 32; ++kk) {
       hf8 bf[NT];
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
@@ -199,6 +252,29 @@ __global__ void __launch_bounds__(256) k_dq_gemm(GemmArgs a) {
       }
     }
     __syncthreads();
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  using Yes = std::true_type;
+  using No = std::false_type;
+  static_assert(D == 2 || D == 4, "ring depth");
+  // steady state: whole groups of D steps, every path through the body issues the same loads in
+  // the same order, so the waits at the top stay partial; the tail has no back edge
+  int s0 = 0;
+  for (; s0 + D <= S; s0 += D) {
+    k_step(I0{}, Yes{}, s0);
+    k_step(I1{}, Yes{}, s0 + 1);
+    if constexpr (D == 4) {
+      k_step(I2{}, Yes{}, s0 + 2);
+      k_step(I3{}, Yes{}, s0 + 3);
+    }
+  }
+  if (s0 < S) k_step(I0{}, No{}, s0);
+  if (s0 + 1 < S) k_step(I1{}, No{}, s0 + 1);
+  if constexpr (D == 4) {
+    if (s0 + 2 < S) k_step(I2{}, No{}, s0 + 2);
   }
 
   // ---- epilogue: acc[i][j][r] = C[m = 16i + 4(lane>>4) + r][n = wave*BN/4 + 16j + (lane&15)]
@@ -265,22 +341,31 @@ __global__ void __launch_bounds__(256) k_dq_gemm(GemmArgs a) {
   }
 }
 
-template <int FMT, int ORDER, int BM, int BN, int EPI>
+template <int FMT, int ORDER, int XDT, int BM, int BN, int EPI>
 static int launch_dq(const GemmArgs &a, int max_mtiles, hipStream_t s) {
   const int n_tiles = (EPI == EPI_SWIGLU ? a.N * 2 : a.N) / BN;
   const int64_t grid = static_cast<int64_t>(max_mtiles) * n_tiles;
   if (grid <= 0) return VYBDQ_OK;
   if (grid >= (int64_t(1) << 31)) return set_error(VYBDQ_ERR_SHAPE, "dq gemm: grid too large");
-  hipLaunchKernelGGL((k_dq_gemm<FMT, ORDER, BM, BN, EPI>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((k_dq_gemm<FMT, ORDER, XDT, BM, BN, EPI>), dim3(static_cast<unsigned>(grid)), dim3(256), 0, s, a);
   return check_launch("dq gemm");
+}
+
+template <int FMT, int BM, int BN, int EPI>
+static int launch_x(const GemmArgs &a, int max_mtiles, hipStream_t s) {
+  switch (a.xdt) {
+    case VYBDQ_F16: return launch_dq<FMT, VYBDQ_Q4_GGML, VYBDQ_F16, BM, BN, EPI>(a, max_mtiles, s);
+    case VYBDQ_BF16: return launch_dq<FMT, VYBDQ_Q4_GGML, VYBDQ_BF16, BM, BN, EPI>(a, max_mtiles, s);
+    default: return launch_dq<FMT, VYBDQ_Q4_GGML, VYBDQ_F32, BM, BN, EPI>(a, max_mtiles, s);
+  }
 }
 
 // Plain GEMM: Y [M, N] = X [M, K] W^T (+ RS). BM chosen by M.
 template <int FMT>
 static int gemm_plain(GemmArgs a, hipStream_t s) {
-  if (a.M >= 128) return launch_dq<FMT, VYBDQ_Q4_GGML, 128, 128, EPI_STORE>(a, (a.M + 127) / 128, s);
-  if (a.M >= 64) return launch_dq<FMT, VYBDQ_Q4_GGML, 64, 128, EPI_STORE>(a, (a.M + 63) / 64, s);
-  return launch_dq<FMT, VYBDQ_Q4_GGML, 16, 64, EPI_STORE>(a, (a.M + 15) / 16, s);
+  if (a.M >= 128) return launch_x<FMT, 128, 128, EPI_STORE>(a, (a.M + 127) / 128, s);
+  if (a.M >= 64) return launch_x<FMT, 64, 128, EPI_STORE>(a, (a.M + 63) / 64, s);
+  return launch_x<FMT, 16, 64, EPI_STORE>(a, (a.M + 15) / 16, s);
 }
 
 // Grouped entry used by the MoE pipeline: BM = 16 token rows per tile, BN = 64 weight rows.
@@ -309,11 +394,11 @@ int dq_gemm_grouped(int wtype, bool swiglu, const uint8_t *W, const uint8_t *W2,
   a.ldy = ldy;
   a.limit = limit;
   if (swiglu) {
-    if (wtype == 2) return launch_dq<FMT_Q4_0, VYBDQ_Q4_GGML, 16, 64, EPI_SWIGLU>(a, max_mtiles, s);
-    return launch_dq<FMT_Q8_0, VYBDQ_Q4_GGML, 16, 64, EPI_SWIGLU>(a, max_mtiles, s);
+    if (wtype == 2) return launch_x<FMT_Q4_0, 16, 64, EPI_SWIGLU>(a, max_mtiles, s);
+    return launch_x<FMT_Q8_0, 16, 64, EPI_SWIGLU>(a, max_mtiles, s);
   }
-  if (wtype == 2) return launch_dq<FMT_Q4_0, VYBDQ_Q4_GGML, 16, 64, EPI_STORE>(a, max_mtiles, s);
-  return launch_dq<FMT_Q8_0, VYBDQ_Q4_GGML, 16, 64, EPI_STORE>(a, max_mtiles, s);
+  if (wtype == 2) return launch_x<FMT_Q4_0, 16, 64, EPI_STORE>(a, max_mtiles, s);
+  return launch_x<FMT_Q8_0, 16, 64, EPI_STORE>(a, max_mtiles, s);
 }
 
 }  // namespace vybdq
@@ -346,8 +431,8 @@ extern "C" int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t
   a.G = 1;
   hipStream_t s = as_stream(stream);
   if (N % 128 != 0 || M < 64) {
-    if (wtype == 2) return launch_dq<FMT_Q4_0, VYBDQ_Q4_GGML, 16, 64, EPI_STORE>(a, static_cast<int>((M + 15) / 16), s);
-    return launch_dq<FMT_Q8_0, VYBDQ_Q4_GGML, 16, 64, EPI_STORE>(a, static_cast<int>((M + 15) / 16), s);
+    if (wtype == 2) return launch_x<FMT_Q4_0, 16, 64, EPI_STORE>(a, static_cast<int>((M + 15) / 16), s);
+    return launch_x<FMT_Q8_0, 16, 64, EPI_STORE>(a, static_cast<int>((M + 15) / 16), s);
   }
   if (wtype == 2) return gemm_plain<FMT_Q4_0>(a, s);
   return gemm_plain<FMT_Q8_0>(a, s);
