@@ -311,13 +311,14 @@ def run_prefill(args, torch, dev):
     gen.manual_seed(args.seed)
     shapes = [(17408, 5120), (5120, 17408)]
     ncopy = 3
+    ws = ops.GemmWorkspace([(M, N, K) for N, K in shapes], dev, ops.GGML_Q8_0)
     launches, flops, nbytes = [], 0, 0
     for N, K in shapes:
         x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
         y = torch.empty(M, N, device=dev)
         for _ in range(ncopy):
             W = q8_0_blocks_gpu(torch, gen, N, K, dev)
-            launches.append(lambda W=W, x=x, y=y, N=N, K=K: ops.gemm(ops.GGML_Q8_0, W, x, N, K, out=y))
+            launches.append(lambda W=W, x=x, y=y, N=N, K=K: ops.gemm(ops.GGML_Q8_0, W, x, N, K, out=y, workspace=ws))
             flops += 2 * M * N * K
             nbytes += N * K // 32 * 34 + 2 * M * K + 4 * M * N
     ms, wall = timed_graph(torch, launches, args.steps, args.warmup)
@@ -325,7 +326,7 @@ def run_prefill(args, torch, dev):
     per = ms / len(launches)
     roofline = dict(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s",
                     frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), traffic=None,
-                    kernel="k_dq_gemm<Q8_0,128,128> (fp16 MFMA 16x16x32)", avg_launch_us=round(per * 1e3, 3),
+                    kernel="k_mmq<Q8_0,bf16> (fp16 MFMA 16x16x32, weights dequantized into operand registers)", avg_launch_us=round(per * 1e3, 3),
                     flops_per_launch=flops // len(launches))
     return dict(value=tflops, unit="TFLOP/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
                 workload="Q8_0 prefill GEMMs M=512: 5120->17408 and 17408->5120 (bf16 X, f32 Y)",

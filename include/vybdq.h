@@ -156,6 +156,21 @@ int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t X, ui
 int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K, int x_dt,
                int y_dt, int64_t ldy, uint64_t RS, uint64_t stream);
 
+/* Workspace bytes vybdq_gemm_ws can use at (M, N, K) to split K across workgroups, 0 when the
+   shape gains nothing from a split. */
+int64_t vybdq_gemm_workspace_size(int wtype, int64_t M, int64_t N, int64_t K);
+
+/* vybdq_gemm with a caller workspace ws (256-byte aligned, ws_bytes; zero-filled once before its
+   first use, every call leaves it zero-filled; 0 = none). With a workspace of at least
+   vybdq_gemm_workspace_size bytes, long-K shapes split K across workgroups: each writes float32
+   partials and the last workgroup of a tile sums them in split order, so results stay
+   deterministic for a fixed shape and workspace (they may differ in the last bits from the
+   unsplit vybdq_gemm). Calls that share a workspace must not overlap. The reference's gemm_q80
+   has no workspace (native/tools/gen_rpf.py:58-62); this is the same GEMM for shapes whose
+   tiles alone do not fill the GPU. */
+int vybdq_gemm_ws(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K, int x_dt,
+                  int y_dt, int64_t ldy, uint64_t RS, uint64_t ws, int64_t ws_bytes, uint64_t stream);
+
 /* ---- MoE layer ---------------------------------------------------------------------------- */
 
 /* Router alone: idx_out int32 [T, topk] (descending choice, ties to the lower id),

@@ -62,6 +62,64 @@ def test_gemm_config3_rows(dev, ty, K):
     assert gate16(y, ref, torch.bfloat16) < TOL
 
 
+@pytest.mark.parametrize("ty", [ops.GGML_Q4_0, ops.GGML_Q8_0])
+@pytest.mark.parametrize("M,N,K", [(64, 16, 256), (128, 272, 512), (200, 320, 1024), (77, 48, 768),
+                                   (128, 256, 8192), (300, 64, 4096)])
+@pytest.mark.parametrize("xdt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("split", [False, True])
+def test_gemm_mfma_tiles(dev, ty, M, N, K, xdt, split):
+    """The register-B MFMA GEMM (K % 256 == 0, M >= 64): odd fragment counts per tile, partial
+    M tiles, and long K split across workgroups through the workspace."""
+    rng = np.random.default_rng(M * 7 + N + K + ty)
+    raw = weights(ty, rng, N, K)
+    x = torch.from_numpy(synth.activations(rng, (M, K))).to(TDT[xdt])
+    ws = ops.GemmWorkspace([(M, N, K)], dev, ty) if split else None
+    W = dev_t(raw, dev)
+    y = ops.gemm(ty, W, x.to(dev), N, K, workspace=ws).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x.to(torch.float64).numpy(), ref_rows(ty, raw, N, K))
+    assert matmul.rel_maxnorm(y, ref) < TOL
+    if split:
+        # deterministic, and the counters are left zeroed for the next call
+        y2 = ops.gemm(ty, W, x.to(dev), N, K, workspace=ws).cpu().numpy()
+        np.testing.assert_array_equal(y, y2)
+
+
+@pytest.mark.parametrize("F", [1, 2, 3, 5, 6, 7, 9, 11, 13, 15, 17, 18, 19, 20])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_gemm_mfma_forced_tiles(dev, monkeypatch, F, splits):
+    """Every per-wave fragment count (0..5) and a ragged last tile, with and without a K split."""
+    monkeypatch.setenv("VYBDQ_MMQ_PLAN", f"{F},{splits}")
+    ty = ops.GGML_Q8_0 if F % 2 else ops.GGML_Q4_0
+    M, N, K = 150, 16 * (2 * F + 3), 768
+    rng = np.random.default_rng(F * 10 + splits)
+    raw = weights(ty, rng, N, K)
+    x = torch.from_numpy(synth.activations(rng, (M, K))).to(torch.bfloat16)
+    ws = ops.GemmWorkspace([(M, N, K)], dev, ty) if splits > 1 else None
+    if ws is not None:
+        # the override applies to the workspace query as well
+        assert ws.nbytes > 0
+    y = ops.gemm(ty, dev_t(raw, dev), x.to(dev), N, K, workspace=ws).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x.to(torch.float64).numpy(), ref_rows(ty, raw, N, K))
+    assert matmul.rel_maxnorm(y, ref) < TOL
+
+
+@pytest.mark.parametrize("N,K,cols", [(17408, 5120, 320), (5120, 17408, 256)])
+def test_gemm_config3_full_shape(dev, N, K, cols):
+    """The prefill shapes at full size (the benchmark's tiling and K split), checked against float64
+    on a column slice taken from the start and the end of N."""
+    rng = np.random.default_rng(N + K)
+    M = 512
+    raw = synth.q8_0_weights(rng, N, K)
+    x = torch.from_numpy(synth.activations(rng, (M, K))).to(torch.bfloat16)
+    ws = ops.GemmWorkspace([(M, N, K)], dev, ops.GGML_Q8_0)
+    y = ops.gemm(ops.GGML_Q8_0, dev_t(raw, dev), x.to(dev), N, K, workspace=ws).cpu().numpy()
+    rows = raw.reshape(N, -1)
+    x64 = x.to(torch.float64).numpy()
+    for c0 in (0, N - cols):
+        ref = matmul.gemm_rows_f64(x64, ref_rows(ops.GGML_Q8_0, rows[c0:c0 + cols].reshape(-1), cols, K))
+        assert matmul.rel_maxnorm(y[:, c0:c0 + cols], ref) < TOL
+
+
 def test_gemm_residual_f64(dev):
     rng = np.random.default_rng(5)
     M, N, K = 70, 128, 256

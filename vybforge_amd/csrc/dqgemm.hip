@@ -31,6 +31,12 @@ typedef _Float16 hf8 __attribute__((ext_vector_type(8)));
 
 enum { EPI_STORE = 0, EPI_SWIGLU = 1 };
 
+// the MFMA GEMM with weights in operand registers (mmq_host.hip)
+bool mmq_supported(int64_t M, int64_t N, int64_t K);
+int64_t mmq_workspace_size(int64_t M, int64_t N, int64_t K);
+int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
+             int64_t ldy, const void *RS, void *ws, int64_t ws_bytes, hipStream_t s);
+
 struct GemmArgs {
   const uint8_t *W;       // group g's matrix at W + g * w_stride (gate matrix for SWIGLU)
   const uint8_t *W2;      // SWIGLU: up matrix, same layout
@@ -405,17 +411,45 @@ int dq_gemm_grouped(int wtype, bool swiglu, const uint8_t *W, const uint8_t *W2,
 
 using namespace vybdq;
 
-extern "C" int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K,
-                          int x_dt, int y_dt, int64_t ldy, uint64_t RS, uint64_t stream) {
+static int gemm_check(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K, int x_dt,
+                      int y_dt, int64_t ldy) {
   VYBDQ_REQUIRE(W && X && Y, VYBDQ_ERR_ARG, "null W, X or Y");
   VYBDQ_REQUIRE(wtype == 2 || wtype == 8, VYBDQ_ERR_ARG, "wtype must be 2 (q4_0) or 8 (Q8_0)");
   VYBDQ_REQUIRE(dt_valid_in(x_dt), VYBDQ_ERR_ARG, "x_dt must be F32, F16 or BF16");
   VYBDQ_REQUIRE(dt_valid_out(y_dt), VYBDQ_ERR_ARG, "y_dt must be F32, F16, BF16 or F64");
   VYBDQ_REQUIRE(M >= 1 && M < (1 << 24), VYBDQ_ERR_SHAPE, "M out of range");
   VYBDQ_REQUIRE(K >= 64 && K % 64 == 0, VYBDQ_ERR_SHAPE, "K must be a positive multiple of 64");
-  VYBDQ_REQUIRE(N >= 64 && N % 64 == 0 && N < (1 << 24), VYBDQ_ERR_SHAPE, "N must be a positive multiple of 64");
+  VYBDQ_REQUIRE(N >= 16 && N % 16 == 0 && N < (1 << 24), VYBDQ_ERR_SHAPE, "N must be a positive multiple of 16");
+  VYBDQ_REQUIRE(N % 64 == 0 || (M >= 64 && mmq_supported(M, N, K)), VYBDQ_ERR_SHAPE,
+                "N must be a multiple of 64 unless M >= 64 and K % 256 == 0");
   VYBDQ_REQUIRE(ldy == 0 || ldy >= N, VYBDQ_ERR_SHAPE, "ldy must be 0 (= N) or >= N");
   VYBDQ_REQUIRE((W & 3) == 0 && (X & 15) == 0, VYBDQ_ERR_ALIGN, "W must be 4-byte and X 16-byte aligned");
+  return VYBDQ_OK;
+}
+
+extern "C" int64_t vybdq_gemm_workspace_size(int wtype, int64_t M, int64_t N, int64_t K) {
+  if ((wtype != 2 && wtype != 8) || M < 64 || !mmq_supported(M, N, K)) return 0;
+  return mmq_workspace_size(M, N, K);
+}
+
+extern "C" int vybdq_gemm_ws(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K,
+                             int x_dt, int y_dt, int64_t ldy, uint64_t RS, uint64_t ws, int64_t ws_bytes,
+                             uint64_t stream) {
+  const int rc = gemm_check(wtype, W, X, Y, M, N, K, x_dt, y_dt, ldy);
+  if (rc) return rc;
+  VYBDQ_REQUIRE(ws == 0 || (ws & 255) == 0, VYBDQ_ERR_ALIGN, "workspace must be 256-byte aligned");
+  VYBDQ_REQUIRE(ws_bytes >= 0, VYBDQ_ERR_WORKSPACE, "negative workspace size");
+  if (M >= 64 && mmq_supported(M, N, K))
+    return mmq_gemm(wtype, reinterpret_cast<const void *>(W), reinterpret_cast<const void *>(X), x_dt,
+                    reinterpret_cast<void *>(Y), y_dt, M, N, K, ldy ? ldy : N, reinterpret_cast<const void *>(RS),
+                    ws ? reinterpret_cast<void *>(ws) : nullptr, ws ? ws_bytes : 0, as_stream(stream));
+  return vybdq_gemm(wtype, W, X, Y, M, N, K, x_dt, y_dt, ldy, RS, stream);
+}
+
+extern "C" int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K,
+                          int x_dt, int y_dt, int64_t ldy, uint64_t RS, uint64_t stream) {
+  const int rc = gemm_check(wtype, W, X, Y, M, N, K, x_dt, y_dt, ldy);
+  if (rc) return rc;
   GemmArgs a{};
   a.W = reinterpret_cast<const uint8_t *>(W);
   a.X = reinterpret_cast<const void *>(X);
@@ -430,6 +464,8 @@ extern "C" int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t
   a.RS = reinterpret_cast<const void *>(RS);
   a.G = 1;
   hipStream_t s = as_stream(stream);
+  if (M >= 64 && mmq_supported(M, N, K))
+    return mmq_gemm(wtype, a.W, a.X, x_dt, a.Y, y_dt, M, N, K, a.ldy, a.RS, nullptr, 0, s);
   if (N % 128 != 0 || M < 64) {
     if (wtype == 2) return launch_x<FMT_Q4_0, 16, 64, EPI_STORE>(a, static_cast<int>((M + 15) / 16), s);
     return launch_x<FMT_Q8_0, 16, 64, EPI_STORE>(a, static_cast<int>((M + 15) / 16), s);

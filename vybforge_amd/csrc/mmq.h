@@ -1,0 +1,471 @@
+// Prefill dequant GEMM on packed GGUF rows with fp16 MFMA, gfx950, weights dequantized straight
+// into MFMA operand registers.
+//
+// Y[m, n] = RS[m, n] + sum_k X[m, k] * W[n, k]   (W: q4_0 or Q8_0 rows, GGUF row layout)
+//
+// Workgroup = 4 waves, tile = BM (= 16 MT) rows x F 16-column fragments; the F fragments are
+// split among the waves (wave w owns nf_w of them, nf_w = F/4 or F/4 + 1), so a wave's weight
+// rows are private to it and never pass through LDS.
+//
+// K is walked in super-steps of 128 (four 32-weight blocks). The MFMA is
+// v_mfma_f32_16x16x32_f16: lane L supplies B[k-slot 8(L>>4) .. +8][n = L & 15]. The k-slots of
+// the four MFMAs of a super-step are assigned so that lane group g = L >> 4 covers block g of the
+// super-step: in step t (0..3) its 8 slots hold elements 8t .. 8t+7 of block 4s + g. A lane thus
+// loads whole blocks (one 20-byte (q4_0) or 36-byte (Q8_0) dword-aligned window per fragment per
+// super-step), and only its own block scale applies to it. The A operand (X) uses the same
+// k-slot assignment: it is staged into LDS in MFMA fragment order, chunk (m-fragment i, step t)
+// = 64 lanes x 8 fp16, so every A fragment read is one conflict-free ds_read_b128 per lane.
+//
+// Dequantization: a quant byte v becomes the fp16 0x64vv = 1024 + v (v_perm_b32 with a 0x64 byte
+// constant), then (h - OFF) is exact in fp16 (a small integer) and the multiply by the block's
+// fp16 scale rounds once: the fp16 weight is round(d * q) exactly as in the decode. OFF = 1032
+// for q4_0 nibbles (q - 8), 1152 for Q8_0 bytes biased by 128.
+//
+// Pipelining: each lane keeps D super-steps of weight windows in flight (a register ring),
+// prefetches the next super-step's X chunks into registers before the MFMAs, and converts them
+// into the other half of a double-buffered LDS tile afterwards; one barrier per super-step.
+// Loads past the end of the K range re-read the last super-step, so every path through the loop
+// issues the same loads and the waits stay exact.
+//
+// Split-K: a tile's super-steps may be split among `splits` workgroups. Each writes its f32
+// partial tile (in fragment order) with coherent stores, then bumps the tile's arrival counter;
+// the last to arrive sums the partials in split order (fixed order: results do not depend on
+// arrival order) and runs the epilogue, then re-zeroes the counter.
+#pragma once
+#include "gemv_dev.h"
+#include <type_traits>
+
+namespace vybdq {
+
+constexpr int kMmMT = 8;    // BM = 128
+constexpr int kMmNFX = 5;   // up to 20 fragments (320 columns) per tile
+
+typedef _Float16 hf8 __attribute__((ext_vector_type(8)));
+
+struct MmArgs {
+  const uint8_t *W;
+  int64_t rowbytes;
+  const void *X;
+  int64_t ldx;            // elements between X rows
+  const int *row_map;     // output row -> X row (null: identity)
+  int M, N;
+  int S;                  // super-steps (K / 128)
+  int F;                  // 16-column fragments per tile
+  int m_tiles, n_tiles, splits, sps;  // sps: super-steps per split
+  int xcd;                // 1: consecutive units of one XCD share weight rows
+  void *Y;
+  int ydt;
+  int64_t ldy;
+  const void *RS;
+  float *part;            // split partials [tile][split][4 waves][NFX][MT][64][4]
+  uint32_t *cnt;          // [tile] arrival counters
+};
+
+template <int FMT> struct MmFmt;
+template <> struct MmFmt<FMT_Q4_0> {
+  static constexpr int BB = 18, WD = 5, D = 4;
+  static constexpr float OFF = 1032.0f;
+};
+template <> struct MmFmt<FMT_Q8_0> {
+  static constexpr int BB = 34, WD = 9, D = 3;
+  static constexpr float OFF = 1152.0f;
+};
+
+// a WD-dword window starting at a 4-byte-aligned address
+template <int WD>
+__device__ __forceinline__ void load_window(const uint8_t *p, uint32_t (&w)[WD]) {
+  const u4a4 *v = reinterpret_cast<const u4a4 *>(p);
+#pragma unroll
+  for (int i = 0; i < WD / 4; ++i) {
+    const u4a4 t = v[i];
+    w[4 * i + 0] = t[0];
+    w[4 * i + 1] = t[1];
+    w[4 * i + 2] = t[2];
+    w[4 * i + 3] = t[3];
+  }
+  w[WD - 1] = reinterpret_cast<const uint32_t *>(p)[WD - 1];
+}
+
+// The 8 fp16 weights of step t (elements 8t .. 8t+7 of the lane's block) from its window.
+// sel: v_perm selector that extracts the quant dword j from window dwords (j, j+1) (depends on
+// whether the block starts 0 or 2 bytes into the window); shd: bit offset of the scale.
+template <int FMT>
+__device__ __forceinline__ hf8 dequant_step(const uint32_t (&w)[MmFmt<FMT>::WD], int t, uint32_t sel, uint32_t shd) {
+  const uint32_t d16 = __builtin_amdgcn_ubfe(w[0], shd, 16);
+  const _Float16 d = __builtin_bit_cast(_Float16, static_cast<uint16_t>(d16));
+  const h2 dd = {d, d};
+  const h2 off = {static_cast<_Float16>(-MmFmt<FMT>::OFF), static_cast<_Float16>(-MmFmt<FMT>::OFF)};
+  uint32_t v[2];
+  if constexpr (FMT == FMT_Q8_0) {
+    // elements 8t .. 8t+7 = quant dwords 2t, 2t+1 (block bytes 2 + 8t ..)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) v[h] = __builtin_amdgcn_perm(w[2 * t + h + 1], w[2 * t + h], sel) ^ 0x80808080u;
+  } else {
+    // GGUF order: element j < 16 = low nibble of qs[j], j + 16 = high nibble; step t reads
+    // qs dwords 2(t & 1), 2(t & 1) + 1, low nibbles for t < 2, high for t >= 2
+    const int j0 = 2 * (t & 1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t q = __builtin_amdgcn_perm(w[j0 + h + 1], w[j0 + h], sel);
+      v[h] = (t < 2 ? q : q >> 4) & 0x0F0F0F0Fu;
+    }
+  }
+  hf8 r;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const h2 p0 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, v[h], SEL_B01)) + off) * dd;
+    const h2 p1 = (__builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, v[h], SEL_B23)) + off) * dd;
+    r[4 * h + 0] = p0[0];
+    r[4 * h + 1] = p0[1];
+    r[4 * h + 2] = p1[0];
+    r[4 * h + 3] = p1[1];
+  }
+  return r;
+}
+
+// X chunk (8 elements) raw registers and its fp16 conversion
+template <int XDT> struct XChunk { u4 r; };
+template <> struct XChunk<VYBDQ_F32> { u4 r[2]; };
+
+template <int XDT>
+__device__ __forceinline__ void x_load(const void *X, uint32_t off, XChunk<XDT> &c) {
+  if constexpr (XDT == VYBDQ_F32) {
+    const u4 *p = reinterpret_cast<const u4 *>(static_cast<const float *>(X) + off);
+    c.r[0] = p[0];
+    c.r[1] = p[1];
+  } else {
+    c.r = *reinterpret_cast<const u4 *>(static_cast<const uint16_t *>(X) + off);
+  }
+}
+
+template <int XDT>
+__device__ __forceinline__ u4 x_to_f16(const XChunk<XDT> &c) {
+  u4 o;
+  if constexpr (XDT == VYBDQ_F16) {
+    o = c.r;
+  } else if constexpr (XDT == VYBDQ_BF16) {
+    // bf16 -> fp16 is exact for |x| in the fp16 normal range, so truncation loses nothing there
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t v = c.r[j];
+      o[j] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(v << 16), __uint_as_float(v & 0xffff0000u)));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u4 &s = c.r[j >> 1];
+      const uint32_t a = s[2 * (j & 1)], b = s[2 * (j & 1) + 1];
+      o[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(__uint_as_float(a)), static_cast<_Float16>(__uint_as_float(b))});
+    }
+  }
+  return o;
+}
+
+// LDS: the X tile ring (one array per stage) and the split-K flag
+template <int MT>
+struct MmLds {
+  uint8_t *a[4];
+  uint32_t *last;
+};
+
+// Per-wave body for NF owned fragments (NF wave-uniform; NF = 0 waves only stage X).
+template <int FMT, int XDT, int MT, int NFX, int NF>
+__device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, int tile, int split, int row0, int fb,
+                                        int s0, int s1) {
+  constexpr int WD = MmFmt<FMT>::WD;
+  constexpr int D = MmFmt<FMT>::D;
+  constexpr int BB = MmFmt<FMT>::BB;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, nl = lane & 15;
+
+  // ---- weight windows: lane (nl, g), fragment f -> row (fb + f) * 16 + nl, block 4s + g
+  const uint8_t *wrow[NF > 0 ? NF : 1];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const int64_t n = static_cast<int64_t>(fb + f) * 16 + nl;
+    wrow[f] = a.W + n * a.rowbytes + (g * BB - 2 * (g & 1));
+  }
+  const uint32_t sel = (g & 1) ? 0x07060504u : 0x05040302u;  // quant dword j from (w[j+1], w[j])
+  const uint32_t shd = (g & 1) ? 16u : 0u;
+  auto wptr = [&](int f, int s) {
+    s = s < s1 ? s : s1 - 1;
+    return wrow[f] + static_cast<int64_t>(s) * (4 * BB);
+  };
+
+  // ---- X chunks: thread (w, lane) stages chunk (i, t = w) for i < MT: row row0 + 16 i + nl,
+  // k = 128 s + 32 g + 8 w
+  uint32_t xoff[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    int r = row0 + 16 * i + nl;
+    r = r < a.M ? r : a.M - 1;
+    const int xr = a.row_map ? a.row_map[r] : r;
+    xoff[i] = static_cast<uint32_t>(static_cast<int64_t>(xr) * a.ldx) + 32 * g + 8 * w;
+  }
+  auto xk = [&](int s) {
+    s = s < s1 ? s : s1 - 1;
+    return static_cast<uint32_t>(s) * 128u;
+  };
+  // fp16 X goes straight from global memory into an LDS stage (global_load_lds_dwordx4: lane L
+  // of the wave writes chunk base + 16 L, the fragment-order slot of its chunk), NA - 1 stages
+  // ahead; other types pass through registers one stage ahead and are converted to fp16 before
+  // the LDS store
+  constexpr bool DMA = XDT == VYBDQ_F16;
+  constexpr int NA = D;  // X stages in LDS (the register path uses them one stage ahead)
+  static_assert(D % NA == 0, "ring slot and LDS stage advance together");
+  XChunk<XDT> xc[DMA ? 1 : MT];
+  auto x_dma = [&](int s, uint8_t *dst) {
+    const uint32_t k = xk(s);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      __builtin_amdgcn_global_load_lds(
+          (const void __attribute__((address_space(1))) *)(static_cast<const uint16_t *>(a.X) + xoff[i] + k),
+          (void __attribute__((address_space(3))) *)(dst + (i * 4 + w) * 1024), 16, 0, 0);
+  };
+  auto x_regs = [&](int s) {
+    const uint32_t k = xk(s);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) x_load<XDT>(a.X, xoff[i] + k, xc[i]);
+  };
+  auto x_stage = [&](uint8_t *dst) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i) *reinterpret_cast<u4 *>(dst + ((i * 4 + w) * 64 + lane) * 16) = x_to_f16<XDT>(xc[i]);
+  };
+  // Workgroup barrier without memory fences: each wave has already waited for the memory
+  // operations the other waves depend on (its X DMA by vmcnt, its LDS stores by lgkmcnt), and
+  // __syncthreads()' release fence would wait for every weight load in flight as well. The empty
+  // asm and sched_barriers keep the compiler from moving memory operations across it.
+  auto bar = [] {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+  };
+  // vmcnt wait that leaves the N most recent loads in flight (expcnt and lgkmcnt not waited)
+  auto wait_vm = [](auto n) {
+    constexpr int N = decltype(n)::value;
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  };
+  constexpr int LPW = WD / 4 + 1;  // load instructions per weight window
+  // Loads younger than X(s + 1) when step s ends in the steady state: W(s + 2 - NA + D), then per
+  // step X(.) and W(.) for the NA - 2 steps after it. Earlier steps have at least as many, so
+  // waiting for this many is safe everywhere (it may wait a little longer in the first steps).
+  constexpr int YOUNGER = (NA - 2) * (MT + NF * LPW) + NF * LPW;
+
+  f4 acc[MT][NF > 0 ? NF : 1];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int f = 0; f < (NF > 0 ? NF : 1); ++f) acc[i][f] = f4{0.f, 0.f, 0.f, 0.f};
+
+  uint32_t ring[D][NF > 0 ? NF : 1][WD];
+
+  // ---- prologue: X(s0 .. s0 + NA - 2) and weights s0 .. s0 + D - 1, interleaved as the steady
+  // state issues them
+  if (s0 < s1) {
+    if constexpr (DMA) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) {
+        if (j < NA - 1) x_dma(s0 + j, sm.a[j]);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) load_window<WD>(wptr(f, s0 + j), ring[j][f]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      wait_vm(std::integral_constant<int, (NA - 2) * (MT + NF * LPW) + 2 * NF * LPW < 64
+                                              ? (NA - 2) * (MT + NF * LPW) + 2 * NF * LPW : 63>{});
+      if constexpr ((NA - 2) * (MT + NF * LPW) + 2 * NF * LPW >= 64) wait_vm(std::integral_constant<int, 0>{});
+    } else {
+      x_regs(s0);
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+#pragma unroll
+        for (int f = 0; f < NF; ++f) load_window<WD>(wptr(f, s0 + d), ring[d][f]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      x_stage(sm.a[0]);
+    }
+  }
+  __syncthreads();
+
+  // MFMAs of one super-step: A fragments of step t + 1 and the B fragment after the current one
+  // are produced while the current MFMAs run
+  auto compute = [&](const uint32_t (&slot)[NF > 0 ? NF : 1][WD], const uint8_t *abase) {
+    if constexpr (NF > 0) {
+      hf8 af[2][MT];
+#pragma unroll
+      for (int i = 0; i < MT; ++i) af[0][i] = *reinterpret_cast<const hf8 *>(abase + (i * 4 * 64 + lane) * 16);
+      hf8 bcur = dequant_step<FMT>(slot[0], 0, sel, shd);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (t < 3) {
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+            af[(t + 1) & 1][i] = *reinterpret_cast<const hf8 *>(abase + ((i * 4 + t + 1) * 64 + lane) * 16);
+        }
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          const bool last = t == 3 && f == NF - 1;
+          const int fn = f + 1 < NF ? f + 1 : 0;
+          const int tn = f + 1 < NF ? t : t + 1;
+          hf8 bnext = bcur;
+          if (!last) bnext = dequant_step<FMT>(slot[fn], tn, sel, shd);
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+            acc[i][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t & 1][i], bcur, acc[i][f], 0, 0, 0);
+          bcur = bnext;
+        }
+      }
+    }
+  };
+
+  // one super-step s from ring slot DC = (s - s0) % D (a compile-time constant; the LDS stage is
+  // DC % NA); REFILL issues the weights of s + D into the slot
+  auto step = [&](auto dc, auto refill, int s) {
+    constexpr int d = decltype(dc)::value;
+    if constexpr (DMA) x_dma(s + NA - 1, sm.a[(d + NA - 1) % NA]);
+    else x_regs(s + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(ring[d], sm.a[d % NA]);
+    if constexpr (decltype(refill)::value) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int f = 0; f < NF; ++f) load_window<WD>(wptr(f, s + D), ring[d][f]);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (DMA) wait_vm(std::integral_constant<int, YOUNGER>{});
+    } else {
+      if constexpr (DMA) wait_vm(std::integral_constant<int, 0>{});
+    }
+    if constexpr (!DMA) {
+      x_stage(sm.a[(d + 1) % NA]);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the LDS stores are done
+    }
+    bar();
+  };
+  using Yes = std::true_type;
+  using No = std::false_type;
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  static_assert(D >= 2 && D <= 4, "ring depth");
+  int s = s0;
+  for (; s + D <= s1; s += D) {
+    step(I0{}, Yes{}, s);
+    step(I1{}, Yes{}, s + 1);
+    if constexpr (D >= 3) step(I2{}, Yes{}, s + 2);
+    if constexpr (D >= 4) step(I3{}, Yes{}, s + 3);
+  }
+  if (s < s1) step(I0{}, No{}, s);
+  if (s + 1 < s1) step(I1{}, No{}, s + 1);
+  if constexpr (D >= 4) {
+    if (s + 2 < s1) step(I2{}, No{}, s + 2);
+  }
+
+  // ---- split-K: publish the partial, the last workgroup of the tile reduces
+  if (a.splits > 1) {
+    constexpr int PER_WAVE = NFX * MT * 64 * 4;  // floats
+    float *mine = a.part + ((static_cast<int64_t>(tile) * a.splits + split) * 4 + w) * PER_WAVE;
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          __hip_atomic_store(mine + ((f * MT + i) * 64 + lane) * 4 + r, acc[i][f][r], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *sm.last = old == static_cast<uint32_t>(a.splits - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!*sm.last) return;
+    // fixed-order sum over the splits, element by element (no second accumulator set)
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t e = ((f * MT + i) * 64 + lane) * 4 + r;
+          const float own = acc[i][f][r];
+          float tot = 0.f;
+          for (int j = 0; j < a.splits; ++j) {
+            const float *pj = a.part + ((static_cast<int64_t>(tile) * a.splits + j) * 4 + w) * PER_WAVE;
+            tot += j == split ? own : __hip_atomic_load(pj + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          acc[i][f][r] = tot;
+        }
+    if (tid == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // ---- epilogue: acc[i][f][r] = C[row0 + 16 i + 4 g + r][(fb + f) * 16 + nl]
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const int64_t n = static_cast<int64_t>(fb + f) * 16 + nl;
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = row0 + 16 * i + 4 * g + r;
+        if (m >= a.M) continue;
+        const int64_t idx = static_cast<int64_t>(m) * a.ldy + n;
+        switch (a.ydt) {
+          case VYBDQ_F32: store_elem<VYBDQ_F32>(a.Y, a.RS, idx, acc[i][f][r]); break;
+          case VYBDQ_F16: store_elem<VYBDQ_F16>(a.Y, a.RS, idx, acc[i][f][r]); break;
+          case VYBDQ_BF16: store_elem<VYBDQ_BF16>(a.Y, a.RS, idx, acc[i][f][r]); break;
+          default: store_elem<VYBDQ_F64>(a.Y, a.RS, idx, acc[i][f][r]); break;
+        }
+      }
+  }
+}
+
+template <int FMT, int XDT, int MT, int NFX>
+__global__ void __launch_bounds__(256, 1) k_mmq(MmArgs a) {
+  constexpr int NA = MmFmt<FMT>::D;
+  __shared__ __attribute__((aligned(16))) uint8_t a0[MT * 4096];
+  __shared__ __attribute__((aligned(16))) uint8_t a1[MT * 4096];
+  __shared__ __attribute__((aligned(16))) uint8_t a2[NA > 2 ? MT * 4096 : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t a3[NA > 3 ? MT * 4096 : 16];
+  __shared__ uint32_t last;
+  const MmLds<MT> sm{{a0, a1, a2, a3}, &last};
+  const int units = a.m_tiles * a.n_tiles * a.splits;
+  int id = blockIdx.x;
+  if (a.xcd) id = (blockIdx.x & 7) * (units >> 3) + (blockIdx.x >> 3);
+  const int mt = id % a.m_tiles;
+  const int rest = id / a.m_tiles;
+  const int ntile = rest % a.n_tiles;
+  const int split = rest / a.n_tiles;
+  const int tile = ntile * a.m_tiles + mt;
+  const int s0 = split * a.sps;
+  const int s1 = s0 + a.sps < a.S ? s0 + a.sps : a.S;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int Fq = a.F >> 2, Fr = a.F & 3;
+  const int fb = ntile * a.F + w * Fq + (w < Fr ? w : Fr);
+  int nf = Fq + (w < Fr ? 1 : 0);
+  const int left = (a.N >> 4) - fb;
+  nf = nf < left ? nf : (left > 0 ? left : 0);
+  const int row0 = mt * 16 * MT;
+  static_assert(NFX <= 5, "fragment variants");
+  switch (nf) {
+    case 5: if constexpr (NFX >= 5) mm_body<FMT, XDT, MT, NFX, 5>(a, sm, tile, split, row0, fb, s0, s1); break;
+    case 4: if constexpr (NFX >= 4) mm_body<FMT, XDT, MT, NFX, 4>(a, sm, tile, split, row0, fb, s0, s1); break;
+    case 3: mm_body<FMT, XDT, MT, NFX, 3>(a, sm, tile, split, row0, fb, s0, s1); break;
+    case 2: mm_body<FMT, XDT, MT, NFX, 2>(a, sm, tile, split, row0, fb, s0, s1); break;
+    case 1: mm_body<FMT, XDT, MT, NFX, 1>(a, sm, tile, split, row0, fb, s0, s1); break;
+    default: mm_body<FMT, XDT, MT, NFX, 0>(a, sm, tile, split, row0, fb, s0, s1); break;
+  }
+}
+
+template <int FMT, int XDT>
+int mmq_launch(MmArgs &a, hipStream_t s) {
+  const int64_t units = static_cast<int64_t>(a.m_tiles) * a.n_tiles * a.splits;
+  a.xcd = units % 8 == 0 ? 1 : 0;
+  hipLaunchKernelGGL((k_mmq<FMT, XDT, kMmMT, kMmNFX>), dim3(static_cast<unsigned>(units)), dim3(256), 0, s, a);
+  return check_launch("mmq gemm");
+}
+
+}  // namespace vybdq

@@ -1,0 +1,175 @@
+// Host side of the MFMA dequant GEMM: tiling plan (fragments per tile, split-K) and dispatch.
+// The kernels are instantiated one format x activation type per translation unit (mmq_k_*.hip).
+#include "mmq.h"
+
+#include <cstdio>
+#include <cstdlib>
+
+namespace vybdq {
+
+extern template int mmq_launch<FMT_Q4_0, VYBDQ_F16>(MmArgs &, hipStream_t);
+extern template int mmq_launch<FMT_Q4_0, VYBDQ_BF16>(MmArgs &, hipStream_t);
+extern template int mmq_launch<FMT_Q4_0, VYBDQ_F32>(MmArgs &, hipStream_t);
+extern template int mmq_launch<FMT_Q8_0, VYBDQ_F16>(MmArgs &, hipStream_t);
+extern template int mmq_launch<FMT_Q8_0, VYBDQ_BF16>(MmArgs &, hipStream_t);
+extern template int mmq_launch<FMT_Q8_0, VYBDQ_F32>(MmArgs &, hipStream_t);
+
+// ---- host --------------------------------------------------------------------------------
+
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+struct MmPlan {
+  int m_tiles, n_tiles, F, splits, sps;
+  int64_t ws_bytes;  // partials + counters (0 without split-K)
+};
+
+static int64_t mm_part_bytes(int64_t tiles, int splits) {
+  return tiles * splits * 4LL * kMmNFX * kMmMT * 64 * 4 * 4;
+}
+
+// Tiling: pick fragments per tile F and the K split that minimise an estimate of the run time:
+//   rounds(units / CUs) x super-steps per unit x cycles per super-step
+// where a super-step costs the larger of its MFMA time (64 MT cycles per fragment a wave owns, at
+// ~80% issue efficiency) and its LDS time (the X tile: 4 waves read it, one writes it, ~156 MT
+// cycles at 128 B/cycle), plus the HBM traffic of split partials (written, then read back).
+static MmPlan mm_plan(int M, int N, int S, bool allow_split) {
+  const int cus = device_cus();
+  const int m_tiles = (M + 16 * kMmMT - 1) / (16 * kMmMT);
+  const int Ftot = N / 16;
+  MmPlan best{};
+  double best_t = -1;
+  const double lds_cycles = 156.0 * kMmMT * 1.1;
+  for (int F = 1; F <= 4 * kMmNFX && F <= Ftot; ++F) {
+    const int n_tiles = (Ftot + F - 1) / F;
+    if ((n_tiles - 1) * F >= Ftot) continue;
+    const int nfw = (F + 3) / 4;
+    const double mfma_cycles = 64.0 * kMmMT * nfw / 0.8;
+    const double step_us = (mfma_cycles > lds_cycles ? mfma_cycles : lds_cycles) / 2.4e3;
+    for (int splits = 1; splits <= (allow_split ? 8 : 1) && splits <= S; ++splits) {
+      const int sps = (S + splits - 1) / splits;
+      if ((splits - 1) * sps >= S) continue;
+      const int64_t units = static_cast<int64_t>(m_tiles) * n_tiles * splits;
+      const int64_t rounds = (units + cus - 1) / cus;
+      double t = static_cast<double>(rounds) * sps * step_us;
+      if (splits > 1) {
+        const double bytes = static_cast<double>(units) * 16 * kMmMT * F * 16 * 4 * (2.0 - 1.0 / splits);
+        t += bytes / 5.0e6;  // ~5 TB/s
+      }
+      if (best_t < 0 || t < best_t - 1e-9) {
+        best_t = t;
+        best.m_tiles = m_tiles;
+        best.n_tiles = n_tiles;
+        best.F = F;
+        best.splits = splits;
+        best.sps = sps;
+      }
+    }
+  }
+  // tuning / test override: VYBDQ_MMQ_PLAN="F,splits" (ignored when it does not fit the shape)
+  if (const char *ov = getenv("VYBDQ_MMQ_PLAN")) {
+    int F = 0, splits = 1;
+    if (sscanf(ov, "%d,%d", &F, &splits) >= 1 && F >= 1 && F <= 4 * kMmNFX && F <= Ftot && splits >= 1 &&
+        splits <= 8 && splits <= S && (splits == 1 || allow_split)) {
+      const int sps = (S + splits - 1) / splits;
+      if ((splits - 1) * sps < S) {
+        best.F = F;
+        best.n_tiles = (Ftot + F - 1) / F;
+        best.splits = splits;
+        best.sps = sps;
+      }
+    }
+  }
+  const int64_t tiles = static_cast<int64_t>(best.m_tiles) * best.n_tiles;
+  best.ws_bytes = best.splits > 1 ? mm_part_bytes(tiles, best.splits) + ((tiles * 4 + 255) / 256) * 256 : 0;
+  return best;
+}
+
+bool mmq_supported(int64_t M, int64_t N, int64_t K) {
+  return M >= 1 && K % 256 == 0 && N % 16 == 0 && N >= 16 && M * K < (int64_t(1) << 31);
+}
+
+// X -> fp16 copy (8 elements per thread): bf16 is exact in the fp16 normal range, f32 rounds to
+// nearest even. The GEMM then streams the fp16 copy straight into LDS.
+template <int XDT>
+__global__ void __launch_bounds__(256) k_x_to_f16(const void *__restrict__ X, u4 *__restrict__ Xh, int64_t n8) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n8) return;
+  XChunk<XDT> c;
+  x_load<XDT>(X, static_cast<uint32_t>(i * 8), c);
+  Xh[i] = x_to_f16<XDT>(c);
+}
+
+static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+// workspace: [split partials + tile counters][fp16 copy of X]
+int64_t mmq_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (!mmq_supported(M, N, K)) return 0;
+  return align256(mm_plan(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K / 128), true).ws_bytes) +
+         align256(M * K * 2);
+}
+
+int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
+             int64_t ldy, const void *RS, void *ws, int64_t ws_bytes, hipStream_t s) {
+  const int S = static_cast<int>(K / 128);
+  MmPlan p = mm_plan(static_cast<int>(M), static_cast<int>(N), S, ws != nullptr);
+  if (p.splits > 1 && ws_bytes < p.ws_bytes) p = mm_plan(static_cast<int>(M), static_cast<int>(N), S, false);
+  // with room for it, a non-fp16 X is converted once up front (instead of once per N tile)
+  const int64_t xh_off = align256(p.ws_bytes);
+  if (ws && xdt != VYBDQ_F16 && ws_bytes >= xh_off + M * K * 2) {
+    u4 *xh = reinterpret_cast<u4 *>(static_cast<char *>(ws) + xh_off);
+    const int64_t n8 = M * K / 8;
+    const unsigned grid = static_cast<unsigned>((n8 + 255) / 256);
+    if (xdt == VYBDQ_BF16) hipLaunchKernelGGL(k_x_to_f16<VYBDQ_BF16>, dim3(grid), dim3(256), 0, s, X, xh, n8);
+    else hipLaunchKernelGGL(k_x_to_f16<VYBDQ_F32>, dim3(grid), dim3(256), 0, s, X, xh, n8);
+    const int rc = check_launch("mmq x->f16");
+    if (rc) return rc;
+    X = xh;
+    xdt = VYBDQ_F16;
+  }
+  MmArgs a{};
+  a.W = static_cast<const uint8_t *>(W);
+  a.rowbytes = K / 32 * (wtype == 2 ? 18 : 34);
+  a.X = X;
+  a.ldx = K;
+  a.M = static_cast<int>(M);
+  a.N = static_cast<int>(N);
+  a.S = S;
+  a.F = p.F;
+  a.m_tiles = p.m_tiles;
+  a.n_tiles = p.n_tiles;
+  a.splits = p.splits;
+  a.sps = p.sps;
+  a.Y = Y;
+  a.ydt = ydt;
+  a.ldy = ldy;
+  a.RS = RS;
+  if (p.splits > 1) {
+    const int64_t tiles = static_cast<int64_t>(p.m_tiles) * p.n_tiles;
+    a.part = static_cast<float *>(ws);
+    a.cnt = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + mm_part_bytes(tiles, p.splits));
+  }
+  if (wtype == 2) {
+    switch (xdt) {
+      case VYBDQ_F16: return mmq_launch<FMT_Q4_0, VYBDQ_F16>(a, s);
+      case VYBDQ_BF16: return mmq_launch<FMT_Q4_0, VYBDQ_BF16>(a, s);
+      default: return mmq_launch<FMT_Q4_0, VYBDQ_F32>(a, s);
+    }
+  }
+  switch (xdt) {
+    case VYBDQ_F16: return mmq_launch<FMT_Q8_0, VYBDQ_F16>(a, s);
+    case VYBDQ_BF16: return mmq_launch<FMT_Q8_0, VYBDQ_BF16>(a, s);
+    default: return mmq_launch<FMT_Q8_0, VYBDQ_F32>(a, s);
+  }
+}
+
+}  // namespace vybdq

@@ -205,14 +205,29 @@ class Exl3Linear:
 
 # ---- prefill GEMM and MoE ------------------------------------------------------------------
 
-def gemm(ty, W, X, N, K, y_dtype=torch.float32, residual=None, out=None):
-    """Y [M, N] = X [M, K] W^T (+ residual) through the dequant MFMA GEMM."""
+def gemm(ty, W, X, N, K, y_dtype=torch.float32, residual=None, out=None, workspace=None):
+    """Y [M, N] = X [M, K] W^T (+ residual) through the dequant MFMA GEMM.
+
+    workspace: a GemmWorkspace (split-K partials) or None for the unsplit GEMM."""
     M = X.shape[0]
     if out is None:
         out = torch.empty((M, N), dtype=y_dtype, device=X.device)
-    call("vybdq_gemm", ty, _ptr(W), _ptr(X), _ptr(out), M, N, K, _dt(X.dtype), _dt(out.dtype), 0,
-         _ptr(residual), _stream())
+    if workspace is None:
+        call("vybdq_gemm", ty, _ptr(W), _ptr(X), _ptr(out), M, N, K, _dt(X.dtype), _dt(out.dtype), 0,
+             _ptr(residual), _stream())
+    else:
+        call("vybdq_gemm_ws", ty, _ptr(W), _ptr(X), _ptr(out), M, N, K, _dt(X.dtype), _dt(out.dtype), 0,
+             _ptr(residual), workspace.ptr, workspace.nbytes, _stream())
     return out
+
+
+class GemmWorkspace:
+    """Zero-filled, 256-byte aligned workspace for vybdq_gemm_ws, sized for the given shapes."""
+
+    def __init__(self, shapes, device, ty=GGML_Q8_0):
+        self.nbytes = max([_lib.lib.vybdq_gemm_workspace_size(ty, M, N, K) for M, N, K in shapes] + [0])
+        self.buf = torch.zeros(self.nbytes + 256, dtype=torch.uint8, device=device)
+        self.ptr = (self.buf.data_ptr() + 255) // 256 * 256 if self.nbytes else 0
 
 
 def moe_route(logits, topk, bias=None, scale=2.5):
