@@ -33,7 +33,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="stack", choices=["stack", "stack_chain", "gemv1", "exl3", "prefill", "moe"])
+    ap.add_argument("--config", default="stack", choices=["stack", "stack_chain", "gemv1", "exl3", "prefill", "prefill_i8", "moe"])
     ap.add_argument("--tokens", type=int, default=16, help="tokens for --config moe")
     ap.add_argument("--batch", type=int, default=1, help="batch for --config exl3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -333,6 +333,46 @@ def run_prefill(args, torch, dev):
                 bytes_per_step=nbytes, launches_per_step=len(launches))
 
 
+MFMA_I8_PEAK_TOPS = 5000.0
+
+
+def run_prefill_i8(args, torch, dev):
+    """Config 3, int8 path: the same two Q8_0 GEMMs with the activations quantized per 32-value
+    block (xq8) on the device and int8 MFMA; the quantizer runs inside the timed step."""
+    from vybforge_amd import ops
+    M = 512
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    shapes = [(17408, 5120), (5120, 17408)]
+    ncopy = 3
+    ws = ops.GemmWorkspace([(M, N, K) for N, K in shapes], dev, int8=True)
+    launches, flops, nbytes = [], 0, 0
+    for N, K in shapes:
+        x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
+        q = (torch.empty(M, K, dtype=torch.int8, device=dev), torch.empty(M, K // 32, device=dev))
+        y = torch.empty(M, N, device=dev)
+        for _ in range(ncopy):
+            W = q8_0_blocks_gpu(torch, gen, N, K, dev)
+
+            def f(W=W, x=x, q=q, y=y, N=N, K=K):
+                ops.quant_q8_act(x, out=q)
+                ops.gemm_q8_0_i8(W, q[0], q[1], N, K, out=y, workspace=ws)
+            launches.append(f)
+            flops += 2 * M * N * K
+            nbytes += N * K // 32 * 34 + 2 * M * K + 4 * M * N
+    ms, wall = timed_graph(torch, launches, args.steps, args.warmup)
+    tops = flops / (ms * 1e-3) / 1e12
+    per = ms / len(launches)
+    roofline = dict(bound="mfma", achieved=round(tops, 2), peak=MFMA_I8_PEAK_TOPS, unit="TOP/s",
+                    frac=round(tops / MFMA_I8_PEAK_TOPS, 4), traffic=None,
+                    kernel="xq8 + k_mmq_i8 (int8 MFMA 16x16x32 per block, float32 block scaling; VALU-bound)",
+                    avg_launch_us=round(per * 1e3, 3), flops_per_launch=flops // len(launches),
+                    frac_of_bf16_peak=round(tops / MFMA_BF16_PEAK_TFLOPS, 4))
+    return dict(value=tops, unit="TOP/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
+                workload="Q8_0 prefill GEMMs M=512 int8 path: xq8(X bf16) then int8 MFMA, 5120->17408 and 17408->5120",
+                bytes_per_step=nbytes, launches_per_step=len(launches))
+
+
 def run_moe(args, torch, dev):
     """Config 5: GLM-5-style MoE layer, H=6144, 256 routed + 1 shared expert, top-8, I=2048,
     q4_0 expert tensors (5.46 GB), T tokens bf16, router logits N(0,1)."""
@@ -382,6 +422,8 @@ def main():
         r = run_exl3(args, torch, dev)
     elif args.config == "prefill":
         r = run_prefill(args, torch, dev)
+    elif args.config == "prefill_i8":
+        r = run_prefill_i8(args, torch, dev)
     elif args.config == "moe":
         r = run_moe(args, torch, dev)
     else:

@@ -171,6 +171,21 @@ int64_t vybdq_gemm_workspace_size(int wtype, int64_t M, int64_t N, int64_t K);
 int vybdq_gemm_ws(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K, int x_dt,
                   int y_dt, int64_t ldy, uint64_t RS, uint64_t ws, int64_t ws_bytes, uint64_t stream);
 
+/* Workspace bytes vybdq_gemm_q8_0_i8 can use at (M, N, K) to split K across workgroups, 0 when the
+   shape gains nothing from a split. */
+int64_t vybdq_gemm_q8_0_i8_workspace_size(int64_t M, int64_t N, int64_t K);
+
+/* int8 path. Y [M, N] (row stride ldy, 0 = N) = RS + sum_b Xs[m, b] * d[n, b] * (Xq[m, b] . q[n, b])
+   over the 32-element blocks b, with Xq int8 [M, K] and Xs float32 [M, K/32] as written by
+   vybdq_quant_q8_act (xq8 semantics) and W packed Q8_0 rows (d fp16, q int8). Each block product
+   is an exact int32 MFMA; scaling and accumulation are float32. K % 256 == 0, N % 16 == 0; W, Xq and
+   Xs 16-byte aligned; ws / ws_bytes as for vybdq_gemm_ws (sized by
+   vybdq_gemm_q8_0_i8_workspace_size). The reference quantizes activations with xq8 and runs
+   q8_1 x Q8_0 dot-product GEMVs (native/kernels/rgemv7.vyb:195-214, native/tools/gen_rgemv7.py:1-8);
+   this is the same arithmetic as a prefill GEMM. */
+int vybdq_gemm_q8_0_i8(uint64_t W, uint64_t Xq, uint64_t Xs, uint64_t Y, int64_t M, int64_t N, int64_t K, int y_dt,
+                       int64_t ldy, uint64_t RS, uint64_t ws, int64_t ws_bytes, uint64_t stream);
+
 /* ---- MoE layer ---------------------------------------------------------------------------- */
 
 /* Router alone: idx_out int32 [T, topk] (descending choice, ties to the lower id),

@@ -120,6 +120,58 @@ def test_gemm_config3_full_shape(dev, N, K, cols):
         assert matmul.rel_maxnorm(y[:, c0:c0 + cols], ref) < TOL
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 16, 256), (64, 48, 768), (130, 272, 512), (200, 256, 5120), (77, 320, 1024),
+                                   (128, 64, 8192)])
+@pytest.mark.parametrize("split", [False, True])
+def test_gemm_int8_path(dev, M, N, K, split):
+    """int8 path: xq8 on the GPU, then the int8 MFMA GEMM, against the float64 gate of the
+    dequantized activations and weights."""
+    rng = np.random.default_rng(M * 3 + N + K)
+    raw = synth.q8_0_weights(rng, N, K)
+    x = synth.activations(rng, (M, K))
+    xq, xs = ops.quant_q8_act(dev_t(x, dev))
+    ref_q, ref_s = formats.quant_q8_act(x.reshape(-1, K))
+    np.testing.assert_array_equal(xq.cpu().numpy(), ref_q.reshape(M, K))
+    ws = ops.GemmWorkspace([(M, N, K)], dev, int8=True) if split else None
+    W = dev_t(raw, dev)
+    y = ops.gemm_q8_0_i8(W, xq, xs, N, K, workspace=ws).cpu().numpy()
+    ref = matmul.gemm_q8_0_int8_f64(raw, ref_q, ref_s, N, K).reshape(M, N)
+    assert matmul.rel_maxnorm(y, ref) < TOL
+    if split:
+        np.testing.assert_array_equal(y, ops.gemm_q8_0_i8(W, xq, xs, N, K, workspace=ws).cpu().numpy())
+
+
+@pytest.mark.parametrize("F,splits", [(1, 1), (3, 2), (5, 1), (7, 3), (13, 1), (16, 2)])
+def test_gemm_int8_forced_tiles(dev, monkeypatch, F, splits):
+    monkeypatch.setenv("VYBDQ_MMQ_PLAN", f"{F},{splits}")
+    M, N, K = 150, 16 * (2 * F + 3), 768
+    rng = np.random.default_rng(F * 11 + splits)
+    raw = synth.q8_0_weights(rng, N, K)
+    x = synth.activations(rng, (M, K))
+    xq, xs = ops.quant_q8_act(dev_t(x, dev))
+    ws = ops.GemmWorkspace([(M, N, K)], dev, int8=True) if splits > 1 else None
+    y = ops.gemm_q8_0_i8(dev_t(raw, dev), xq, xs, N, K, workspace=ws).cpu().numpy()
+    ref_q, ref_s = formats.quant_q8_act(x.reshape(-1, K))
+    ref = matmul.gemm_q8_0_int8_f64(raw, ref_q, ref_s, N, K).reshape(M, N)
+    assert matmul.rel_maxnorm(y, ref) < TOL
+
+
+@pytest.mark.parametrize("N,K,cols", [(17408, 5120, 272), (5120, 17408, 256)])
+def test_gemm_int8_config3_full_shape(dev, N, K, cols):
+    rng = np.random.default_rng(N * 2 + K)
+    M = 512
+    raw = synth.q8_0_weights(rng, N, K)
+    x = synth.activations(rng, (M, K))
+    xq, xs = ops.quant_q8_act(dev_t(x, dev))
+    ws = ops.GemmWorkspace([(M, N, K)], dev, int8=True)
+    y = ops.gemm_q8_0_i8(dev_t(raw, dev), xq, xs, N, K, workspace=ws).cpu().numpy()
+    ref_q, ref_s = formats.quant_q8_act(x.reshape(-1, K))
+    rows = raw.reshape(N, -1)
+    for c0 in (0, N - cols):
+        ref = matmul.gemm_q8_0_int8_f64(rows[c0:c0 + cols].reshape(-1), ref_q, ref_s, cols, K).reshape(M, cols)
+        assert matmul.rel_maxnorm(y[:, c0:c0 + cols], ref) < TOL
+
+
 def test_gemm_residual_f64(dev):
     rng = np.random.default_rng(5)
     M, N, K = 70, 128, 256

@@ -43,6 +43,8 @@ SIGNATURES = {
     "vybdq_gemm": [_int, _u64, _u64, _u64, _i64, _i64, _i64, _int, _int, _i64, _u64, _u64],
     "vybdq_gemm_workspace_size": [_int, _i64, _i64, _i64],
     "vybdq_gemm_ws": [_int, _u64, _u64, _u64, _i64, _i64, _i64, _int, _int, _i64, _u64, _u64, _i64, _u64],
+    "vybdq_gemm_q8_0_i8_workspace_size": [_i64, _i64, _i64],
+    "vybdq_gemm_q8_0_i8": [_u64, _u64, _u64, _u64, _i64, _i64, _i64, _int, _i64, _u64, _u64, _i64, _u64],
     "vybdq_moe_route": [_u64, _int, _u64, _u64, _u64, _i64, _i64, _i64, ctypes.c_double, _u64],
     "vybdq_moe_workspace_size": [_i64, _i64, _i64, _i64, _i64],
     "vybdq_moe_forward": [_int, _u64, _int, _u64, _int, _u64, _u64, _u64, _u64, _u64, _u64, _u64, _u64, _int,
@@ -51,7 +53,7 @@ SIGNATURES = {
 }
 _RESTYPE = {"vybdq_last_error": ctypes.c_char_p, "vybdq_chain_workspace_size": ctypes.c_int64,
             "vybdq_exl3_workspace_size": ctypes.c_int64, "vybdq_moe_workspace_size": ctypes.c_int64,
-            "vybdq_gemm_workspace_size": ctypes.c_int64}
+            "vybdq_gemm_workspace_size": ctypes.c_int64, "vybdq_gemm_q8_0_i8_workspace_size": ctypes.c_int64}
 
 
 class VybdqError(RuntimeError):

@@ -36,6 +36,9 @@ bool mmq_supported(int64_t M, int64_t N, int64_t K);
 int64_t mmq_workspace_size(int64_t M, int64_t N, int64_t K);
 int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
              int64_t ldy, const void *RS, void *ws, int64_t ws_bytes, hipStream_t s);
+int64_t mmq_i8_workspace_size(int64_t M, int64_t N, int64_t K);
+int mmq_i8_gemm(const void *W, const int8_t *Xq, const float *Xs, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
+                int64_t ldy, const void *RS, void *ws, int64_t ws_bytes, hipStream_t s);
 
 struct GemmArgs {
   const uint8_t *W;       // group g's matrix at W + g * w_stride (gate matrix for SWIGLU)
@@ -473,3 +476,27 @@ extern "C" int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t
   if (wtype == 2) return gemm_plain<FMT_Q4_0>(a, s);
   return gemm_plain<FMT_Q8_0>(a, s);
 }
+
+extern "C" int64_t vybdq_gemm_q8_0_i8_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || !mmq_supported(M, N, K)) return 0;
+  return mmq_i8_workspace_size(M, N, K);
+}
+
+extern "C" int vybdq_gemm_q8_0_i8(uint64_t W, uint64_t Xq, uint64_t Xs, uint64_t Y, int64_t M, int64_t N, int64_t K,
+                                  int y_dt, int64_t ldy, uint64_t RS, uint64_t ws, int64_t ws_bytes, uint64_t stream) {
+  VYBDQ_REQUIRE(W && Xq && Xs && Y, VYBDQ_ERR_ARG, "null W, Xq, Xs or Y");
+  VYBDQ_REQUIRE(dt_valid_out(y_dt), VYBDQ_ERR_ARG, "y_dt must be F32, F16, BF16 or F64");
+  VYBDQ_REQUIRE(M >= 1 && M < (1 << 24), VYBDQ_ERR_SHAPE, "M out of range");
+  VYBDQ_REQUIRE(K >= 256 && K % 256 == 0, VYBDQ_ERR_SHAPE, "K must be a positive multiple of 256");
+  VYBDQ_REQUIRE(N >= 16 && N % 16 == 0 && N < (1 << 24), VYBDQ_ERR_SHAPE, "N must be a positive multiple of 16");
+  VYBDQ_REQUIRE(M * K < (int64_t(1) << 31), VYBDQ_ERR_SHAPE, "M * K too large");
+  VYBDQ_REQUIRE(ldy == 0 || ldy >= N, VYBDQ_ERR_SHAPE, "ldy must be 0 (= N) or >= N");
+  VYBDQ_REQUIRE((W & 15) == 0 && (Xq & 15) == 0 && (Xs & 15) == 0, VYBDQ_ERR_ALIGN,
+                "W, Xq and Xs must be 16-byte aligned");
+  VYBDQ_REQUIRE(ws == 0 || (ws & 255) == 0, VYBDQ_ERR_ALIGN, "workspace must be 256-byte aligned");
+  return mmq_i8_gemm(reinterpret_cast<const void *>(W), reinterpret_cast<const int8_t *>(Xq),
+                     reinterpret_cast<const float *>(Xs), reinterpret_cast<void *>(Y), y_dt, M, N, K, ldy ? ldy : N,
+                     reinterpret_cast<const void *>(RS), ws ? reinterpret_cast<void *>(ws) : nullptr, ws ? ws_bytes : 0,
+                     as_stream(stream));
+}
+

@@ -168,6 +168,73 @@ struct MmLds {
   uint32_t *last;
 };
 
+// Split-K reduction (when the tile's super-steps were split) and the epilogue store of one wave's
+// accumulators acc[i][f][r] = C[row0 + 16 i + 4 g + r][(fb + f) * 16 + nl].
+template <int MT, int NFX, int NF>
+__device__ __forceinline__ void mm_finish(const MmArgs &a, uint32_t *last, int tile, int split, int row0, int fb,
+                                          f4 (&acc)[MT][NF > 0 ? NF : 1]) {
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, nl = lane & 15;
+  // ---- split-K: publish the partial, the last workgroup of the tile reduces
+  if (a.splits > 1) {
+    constexpr int PER_WAVE = NFX * MT * 64 * 4;  // floats
+    float *mine = a.part + ((static_cast<int64_t>(tile) * a.splits + split) * 4 + w) * PER_WAVE;
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          __hip_atomic_store(mine + ((f * MT + i) * 64 + lane) * 4 + r, acc[i][f][r], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *last = old == static_cast<uint32_t>(a.splits - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!*last) return;
+    // fixed-order sum over the splits, element by element (no second accumulator set)
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t e = ((f * MT + i) * 64 + lane) * 4 + r;
+          const float own = acc[i][f][r];
+          float tot = 0.f;
+          for (int j = 0; j < a.splits; ++j) {
+            const float *pj = a.part + ((static_cast<int64_t>(tile) * a.splits + j) * 4 + w) * PER_WAVE;
+            tot += j == split ? own : __hip_atomic_load(pj + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          acc[i][f][r] = tot;
+        }
+    if (tid == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // ---- epilogue: acc[i][f][r] = C[row0 + 16 i + 4 g + r][(fb + f) * 16 + nl]
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    const int64_t n = static_cast<int64_t>(fb + f) * 16 + nl;
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = row0 + 16 * i + 4 * g + r;
+        if (m >= a.M) continue;
+        const int64_t idx = static_cast<int64_t>(m) * a.ldy + n;
+        switch (a.ydt) {
+          case VYBDQ_F32: store_elem<VYBDQ_F32>(a.Y, a.RS, idx, acc[i][f][r]); break;
+          case VYBDQ_F16: store_elem<VYBDQ_F16>(a.Y, a.RS, idx, acc[i][f][r]); break;
+          case VYBDQ_BF16: store_elem<VYBDQ_BF16>(a.Y, a.RS, idx, acc[i][f][r]); break;
+          default: store_elem<VYBDQ_F64>(a.Y, a.RS, idx, acc[i][f][r]); break;
+        }
+      }
+  }
+}
+
 // Per-wave body for NF owned fragments (NF wave-uniform; NF = 0 waves only stage X).
 template <int FMT, int XDT, int MT, int NFX, int NF>
 __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, int tile, int split, int row0, int fb,
@@ -363,64 +430,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
     if (s + 2 < s1) step(I2{}, No{}, s + 2);
   }
 
-  // ---- split-K: publish the partial, the last workgroup of the tile reduces
-  if (a.splits > 1) {
-    constexpr int PER_WAVE = NFX * MT * 64 * 4;  // floats
-    float *mine = a.part + ((static_cast<int64_t>(tile) * a.splits + split) * 4 + w) * PER_WAVE;
-#pragma unroll
-    for (int f = 0; f < NF; ++f)
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          __hip_atomic_store(mine + ((f * MT + i) * 64 + lane) * 4 + r, acc[i][f][r], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      *sm.last = old == static_cast<uint32_t>(a.splits - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!*sm.last) return;
-    // fixed-order sum over the splits, element by element (no second accumulator set)
-#pragma unroll
-    for (int f = 0; f < NF; ++f)
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t e = ((f * MT + i) * 64 + lane) * 4 + r;
-          const float own = acc[i][f][r];
-          float tot = 0.f;
-          for (int j = 0; j < a.splits; ++j) {
-            const float *pj = a.part + ((static_cast<int64_t>(tile) * a.splits + j) * 4 + w) * PER_WAVE;
-            tot += j == split ? own : __hip_atomic_load(pj + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-          acc[i][f][r] = tot;
-        }
-    if (tid == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-
-  // ---- epilogue: acc[i][f][r] = C[row0 + 16 i + 4 g + r][(fb + f) * 16 + nl]
-#pragma unroll
-  for (int f = 0; f < NF; ++f) {
-    const int64_t n = static_cast<int64_t>(fb + f) * 16 + nl;
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = row0 + 16 * i + 4 * g + r;
-        if (m >= a.M) continue;
-        const int64_t idx = static_cast<int64_t>(m) * a.ldy + n;
-        switch (a.ydt) {
-          case VYBDQ_F32: store_elem<VYBDQ_F32>(a.Y, a.RS, idx, acc[i][f][r]); break;
-          case VYBDQ_F16: store_elem<VYBDQ_F16>(a.Y, a.RS, idx, acc[i][f][r]); break;
-          case VYBDQ_BF16: store_elem<VYBDQ_BF16>(a.Y, a.RS, idx, acc[i][f][r]); break;
-          default: store_elem<VYBDQ_F64>(a.Y, a.RS, idx, acc[i][f][r]); break;
-        }
-      }
-  }
+  mm_finish<MT, NFX, NF>(a, sm.last, tile, split, row0, fb, acc);
 }
 
 template <int FMT, int XDT, int MT, int NFX>

@@ -1,6 +1,7 @@
 // Host side of the MFMA dequant GEMM: tiling plan (fragments per tile, split-K) and dispatch.
 // The kernels are instantiated one format x activation type per translation unit (mmq_k_*.hip).
 #include "mmq.h"
+#include "mmq_i8.h"
 
 #include <cstdio>
 #include <cstdlib>
@@ -42,19 +43,21 @@ static int64_t mm_part_bytes(int64_t tiles, int splits) {
 // where a super-step costs the larger of its MFMA time (64 MT cycles per fragment a wave owns, at
 // ~80% issue efficiency) and its LDS time (the X tile: 4 waves read it, one writes it, ~156 MT
 // cycles at 128 B/cycle), plus the HBM traffic of split partials (written, then read back).
-static MmPlan mm_plan(int M, int N, int S, bool allow_split) {
+// nfx: most fragments one wave can own; frag_cycles: a super-step's cost per fragment a wave
+// owns; fixed_cycles: its cost floor (X tile traffic, barrier).
+static MmPlan mm_plan(int M, int N, int S, bool allow_split, int nfx = kMmNFX, double frag_cycles = 64.0 * kMmMT / 0.8,
+                      double fixed_cycles = 156.0 * kMmMT * 1.1) {
   const int cus = device_cus();
   const int m_tiles = (M + 16 * kMmMT - 1) / (16 * kMmMT);
   const int Ftot = N / 16;
   MmPlan best{};
   double best_t = -1;
-  const double lds_cycles = 156.0 * kMmMT * 1.1;
-  for (int F = 1; F <= 4 * kMmNFX && F <= Ftot; ++F) {
+  for (int F = 1; F <= 4 * nfx && F <= Ftot; ++F) {
     const int n_tiles = (Ftot + F - 1) / F;
     if ((n_tiles - 1) * F >= Ftot) continue;
     const int nfw = (F + 3) / 4;
-    const double mfma_cycles = 64.0 * kMmMT * nfw / 0.8;
-    const double step_us = (mfma_cycles > lds_cycles ? mfma_cycles : lds_cycles) / 2.4e3;
+    const double var_cycles = frag_cycles * nfw;
+    const double step_us = (var_cycles > fixed_cycles ? var_cycles : fixed_cycles) / 2.4e3;
     for (int splits = 1; splits <= (allow_split ? 8 : 1) && splits <= S; ++splits) {
       const int sps = (S + splits - 1) / splits;
       if ((splits - 1) * sps >= S) continue;
@@ -78,7 +81,7 @@ static MmPlan mm_plan(int M, int N, int S, bool allow_split) {
   // tuning / test override: VYBDQ_MMQ_PLAN="F,splits" (ignored when it does not fit the shape)
   if (const char *ov = getenv("VYBDQ_MMQ_PLAN")) {
     int F = 0, splits = 1;
-    if (sscanf(ov, "%d,%d", &F, &splits) >= 1 && F >= 1 && F <= 4 * kMmNFX && F <= Ftot && splits >= 1 &&
+    if (sscanf(ov, "%d,%d", &F, &splits) >= 1 && F >= 1 && F <= 4 * nfx && F <= Ftot && splits >= 1 &&
         splits <= 8 && splits <= S && (splits == 1 || allow_split)) {
       const int sps = (S + splits - 1) / splits;
       if ((splits - 1) * sps < S) {
@@ -172,4 +175,53 @@ int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   }
 }
 
+// ---- int8 path -------------------------------------------------------------------------------
+
+static MmPlan i8_plan(int M, int N, int S, bool allow_split) {
+  // a super-step costs ~12 VALU operations x 4 cycles per 16x16 int32 tile and block
+  return mm_plan(M, N, S, allow_split, kI8NFX, kI8MT * 4 * 12 * 4 / 0.8, 600.0);
+}
+
+int64_t mmq_i8_workspace_size(int64_t M, int64_t N, int64_t K) {
+  if (!mmq_supported(M, N, K)) return 0;
+  return align256(i8_plan(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K / 128), true).ws_bytes);
+}
+
+int mmq_i8_gemm(const void *W, const int8_t *Xq, const float *Xs, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
+                int64_t ldy, const void *RS, void *ws, int64_t ws_bytes, hipStream_t s) {
+  const int S = static_cast<int>(K / 128);
+  MmPlan p = i8_plan(static_cast<int>(M), static_cast<int>(N), S, ws != nullptr);
+  if (p.splits > 1 && ws_bytes < p.ws_bytes) p = i8_plan(static_cast<int>(M), static_cast<int>(N), S, false);
+  I8Args ia{};
+  MmArgs &a = ia.m;
+  a.W = static_cast<const uint8_t *>(W);
+  a.rowbytes = K / 32 * 34;
+  a.M = static_cast<int>(M);
+  a.N = static_cast<int>(N);
+  a.S = S;
+  a.F = p.F;
+  a.m_tiles = p.m_tiles;
+  a.n_tiles = p.n_tiles;
+  a.splits = p.splits;
+  a.sps = p.sps;
+  a.Y = Y;
+  a.ydt = ydt;
+  a.ldy = ldy;
+  a.RS = RS;
+  if (p.splits > 1) {
+    const int64_t tiles = static_cast<int64_t>(p.m_tiles) * p.n_tiles;
+    a.part = static_cast<float *>(ws);
+    a.cnt = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + mm_part_bytes(tiles, p.splits));
+  }
+  ia.Xq = Xq;
+  ia.Xs = Xs;
+  ia.ldq = K;
+  ia.lds = K / 32;
+  const int64_t units = static_cast<int64_t>(a.m_tiles) * a.n_tiles * a.splits;
+  a.xcd = units % 8 == 0 ? 1 : 0;
+  hipLaunchKernelGGL(k_mmq_i8, dim3(static_cast<unsigned>(units)), dim3(256), 0, s, ia);
+  return check_launch("mmq int8 gemm");
+}
+
 }  // namespace vybdq
+

@@ -90,12 +90,15 @@ def gemv_q4_0_seg3(X, K, segs, order=Q4_GGML):
     call("vybdq_gemv_q4_0_seg3", _ptr(X), K, _dt(X.dtype), order, *args, _stream())
 
 
-def quant_q8_act(X):
-    """xq8 quantizer: X [M, K] -> (Xq int8 [M, K], Xs float32 [M, K/32])."""
+def quant_q8_act(X, out=None):
+    """xq8 quantizer: X [M, K] -> (Xq int8 [M, K], Xs float32 [M, K/32]); out: preallocated (Xq, Xs)."""
     X2 = X.reshape(-1, X.shape[-1])
     M, K = X2.shape
-    q = torch.empty((M, K), dtype=torch.int8, device=X.device)
-    d = torch.empty((M, K // 32), dtype=torch.float32, device=X.device)
+    if out is None:
+        q = torch.empty((M, K), dtype=torch.int8, device=X.device)
+        d = torch.empty((M, K // 32), dtype=torch.float32, device=X.device)
+    else:
+        q, d = out
     call("vybdq_quant_q8_act", _ptr(X2), _ptr(q), _ptr(d), M, K, _dt(X2.dtype), _stream())
     return q, d
 
@@ -221,11 +224,28 @@ def gemm(ty, W, X, N, K, y_dtype=torch.float32, residual=None, out=None, workspa
     return out
 
 
-class GemmWorkspace:
-    """Zero-filled, 256-byte aligned workspace for vybdq_gemm_ws, sized for the given shapes."""
+def gemm_q8_0_i8(W, Xq, Xs, N, K, y_dtype=torch.float32, residual=None, out=None, workspace=None):
+    """int8 path: Y [M, N] from xq8-quantized activations (Xq int8 [M, K], Xs float32 [M, K/32])
+    and packed Q8_0 rows W, through int8 MFMA with per-block float32 scaling."""
+    M = Xq.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=y_dtype, device=Xq.device)
+    ws, nb = (workspace.ptr, workspace.nbytes) if workspace is not None else (0, 0)
+    call("vybdq_gemm_q8_0_i8", _ptr(W), _ptr(Xq), _ptr(Xs), _ptr(out), M, N, K, _dt(out.dtype), 0, _ptr(residual),
+         ws, nb, _stream())
+    return out
 
-    def __init__(self, shapes, device, ty=GGML_Q8_0):
-        self.nbytes = max([_lib.lib.vybdq_gemm_workspace_size(ty, M, N, K) for M, N, K in shapes] + [0])
+
+class GemmWorkspace:
+    """Zero-filled, 256-byte aligned workspace for vybdq_gemm_ws (int8=False) or vybdq_gemm_q8_0_i8
+    (int8=True), sized for the given (M, N, K) shapes."""
+
+    def __init__(self, shapes, device, ty=GGML_Q8_0, int8=False):
+        if int8:
+            sizes = [_lib.lib.vybdq_gemm_q8_0_i8_workspace_size(M, N, K) for M, N, K in shapes]
+        else:
+            sizes = [_lib.lib.vybdq_gemm_workspace_size(ty, M, N, K) for M, N, K in shapes]
+        self.nbytes = max(sizes + [0])
         self.buf = torch.zeros(self.nbytes + 256, dtype=torch.uint8, device=device)
         self.ptr = (self.buf.data_ptr() + 255) // 256 * 256 if self.nbytes else 0
 
