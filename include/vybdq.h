@@ -160,12 +160,12 @@ int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t
    shape gains nothing from a split. */
 int64_t vybdq_gemm_workspace_size(int wtype, int64_t M, int64_t N, int64_t K);
 
-/* vybdq_gemm with a caller workspace ws (256-byte aligned, ws_bytes; zero-filled once before its
-   first use, every call leaves it zero-filled; 0 = none). With a workspace of at least
-   vybdq_gemm_workspace_size bytes, long-K shapes split K across workgroups: each writes float32
-   partials and the last workgroup of a tile sums them in split order, so results stay
-   deterministic for a fixed shape and workspace (they may differ in the last bits from the
-   unsplit vybdq_gemm). Calls that share a workspace must not overlap. The reference's gemm_q80
+/* vybdq_gemm with a caller workspace ws (256-byte aligned, ws_bytes, any contents; 0 = none). With
+   a workspace of at least vybdq_gemm_workspace_size bytes, long-K shapes split K across
+   workgroups: each stores float32 partials and a second kernel sums them in split order, so
+   results stay deterministic for a fixed shape and workspace (they may differ in the last bits
+   from the unsplit vybdq_gemm); bf16/f32 X is converted to fp16 once into the workspace instead of
+   once per output tile. Calls that share a workspace must not overlap. The reference's gemm_q80
    has no workspace (native/tools/gen_rpf.py:58-62); this is the same GEMM for shapes whose
    tiles alone do not fill the GPU. */
 int vybdq_gemm_ws(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K, int x_dt,

@@ -27,10 +27,9 @@
 // Loads past the end of the K range re-read the last super-step, so every path through the loop
 // issues the same loads and the waits stay exact.
 //
-// Split-K: a tile's super-steps may be split among `splits` workgroups. Each writes its f32
-// partial tile (in fragment order) with coherent stores, then bumps the tile's arrival counter;
-// the last to arrive sums the partials in split order (fixed order: results do not depend on
-// arrival order) and runs the epilogue, then re-zeroes the counter.
+// Split-K: a tile's super-steps may be split among `splits` workgroups. Each stores its f32
+// partial tile (in fragment order); a second kernel sums the partials of every output in split
+// order (fixed order: deterministic) and runs the epilogue.
 #pragma once
 #include "gemv_dev.h"
 #include <type_traits>
@@ -57,8 +56,7 @@ struct MmArgs {
   int ydt;
   int64_t ldy;
   const void *RS;
-  float *part;            // split partials [tile][split][4 waves][NFX][MT][64][4]
-  uint32_t *cnt;          // [tile] arrival counters
+  float *part;            // split partials [tile][split][waves][NFX][MT][64][4]
 };
 
 template <int FMT> struct MmFmt;
@@ -169,49 +167,22 @@ struct MmLds {
 };
 
 // Split-K reduction (when the tile's super-steps were split) and the epilogue store of one wave's
-// accumulators acc[i][f][r] = C[row0 + 16 i + 4 g + r][(fb + f) * 16 + nl].
-template <int MT, int NFX, int NF>
+// accumulators acc[i][f][r] = C[row0 + 16 i + 4 g + r][(fb + f) * 16 + nl]; NW waves per workgroup.
+template <int MT, int NFX, int NF, int NW = 4>
 __device__ __forceinline__ void mm_finish(const MmArgs &a, uint32_t *last, int tile, int split, int row0, int fb,
                                           f4 (&acc)[MT][NF > 0 ? NF : 1]) {
+  (void)last;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, nl = lane & 15;
-  // ---- split-K: publish the partial, the last workgroup of the tile reduces
+  // ---- split-K: store the partial tile; k_mm_reduce sums the splits in order and stores Y
   if (a.splits > 1) {
     constexpr int PER_WAVE = NFX * MT * 64 * 4;  // floats
-    float *mine = a.part + ((static_cast<int64_t>(tile) * a.splits + split) * 4 + w) * PER_WAVE;
+    float *mine = a.part + ((static_cast<int64_t>(tile) * a.splits + split) * NW + w) * PER_WAVE;
 #pragma unroll
     for (int f = 0; f < NF; ++f)
 #pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          __hip_atomic_store(mine + ((f * MT + i) * 64 + lane) * 4 + r, acc[i][f][r], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      *last = old == static_cast<uint32_t>(a.splits - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!*last) return;
-    // fixed-order sum over the splits, element by element (no second accumulator set)
-#pragma unroll
-    for (int f = 0; f < NF; ++f)
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t e = ((f * MT + i) * 64 + lane) * 4 + r;
-          const float own = acc[i][f][r];
-          float tot = 0.f;
-          for (int j = 0; j < a.splits; ++j) {
-            const float *pj = a.part + ((static_cast<int64_t>(tile) * a.splits + j) * 4 + w) * PER_WAVE;
-            tot += j == split ? own : __hip_atomic_load(pj + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-          acc[i][f][r] = tot;
-        }
-    if (tid == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int i = 0; i < MT; ++i) *reinterpret_cast<f4 *>(mine + ((f * MT + i) * 64 + lane) * 4) = acc[i][f];
+    return;
   }
 
   // ---- epilogue: acc[i][f][r] = C[row0 + 16 i + 4 g + r][(fb + f) * 16 + nl]
@@ -470,12 +441,68 @@ __global__ void __launch_bounds__(256, 1) k_mmq(MmArgs a) {
   }
 }
 
+// Split-K reduction: Y = RS + sum over splits (in split order) of the partial tiles, one float4
+// (4 rows of one column) per thread. Partial layout [tile][split][wave][fragment][m-fragment]
+// [lane][4]; NW waves per workgroup, MT m-fragments per wave, MH = 2 when waves w and w + 4 own the
+// two 64-row halves of the tile (int8 path), 1 when every wave owns all the tile's rows.
+template <int NW, int MT, int NFX, int MH>
+__global__ void __launch_bounds__(256) k_mm_reduce(MmArgs a) {
+  constexpr int PER_WAVE = NFX * MT * 64 * 4;
+  constexpr int CHUNKS = NW * NFX * MT * 64;  // float4 per tile
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int tile = static_cast<int>(c / CHUNKS);
+  if (tile >= a.m_tiles * a.n_tiles) return;
+  int e = static_cast<int>(c % CHUNKS);
+  const int lane = e & 63;
+  e >>= 6;
+  const int i = e % MT;
+  e /= MT;
+  const int f = e % NFX;
+  const int w = e / NFX;
+  const int mt = tile % a.m_tiles, ntile = tile / a.m_tiles;
+  const int q = w % (NW / MH);  // fragment quarter of this wave
+  const int mh = w / (NW / MH);
+  const int Fq = a.F >> 2, Fr = a.F & 3;
+  const int fb = ntile * a.F + q * Fq + (q < Fr ? q : Fr);
+  int nf = Fq + (q < Fr ? 1 : 0);
+  const int left = (a.N >> 4) - fb;
+  nf = nf < left ? nf : (left > 0 ? left : 0);
+  if (f >= nf) return;
+  const float *p = a.part + (static_cast<int64_t>(tile) * a.splits * NW + w) * PER_WAVE + ((f * MT + i) * 64 + lane) * 4;
+  f4 tot = *reinterpret_cast<const f4 *>(p);
+  for (int j = 1; j < a.splits; ++j) tot += *reinterpret_cast<const f4 *>(p + static_cast<int64_t>(j) * NW * PER_WAVE);
+  const int64_t n = static_cast<int64_t>(fb + f) * 16 + (lane & 15);
+  const int row0 = mt * 16 * MT * MH + mh * 16 * MT + 16 * i + 4 * (lane >> 4);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = row0 + r;
+    if (m >= a.M) continue;
+    const int64_t idx = static_cast<int64_t>(m) * a.ldy + n;
+    switch (a.ydt) {
+      case VYBDQ_F32: store_elem<VYBDQ_F32>(a.Y, a.RS, idx, tot[r]); break;
+      case VYBDQ_F16: store_elem<VYBDQ_F16>(a.Y, a.RS, idx, tot[r]); break;
+      case VYBDQ_BF16: store_elem<VYBDQ_BF16>(a.Y, a.RS, idx, tot[r]); break;
+      default: store_elem<VYBDQ_F64>(a.Y, a.RS, idx, tot[r]); break;
+    }
+  }
+}
+
+template <int NW, int MT, int NFX, int MH>
+int mm_reduce_launch(const MmArgs &a, hipStream_t s) {
+  if (a.splits <= 1) return VYBDQ_OK;
+  const int64_t chunks = static_cast<int64_t>(a.m_tiles) * a.n_tiles * NW * NFX * MT * 64;
+  hipLaunchKernelGGL((k_mm_reduce<NW, MT, NFX, MH>), dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, s, a);
+  return check_launch("mmq split-K reduce");
+}
+
 template <int FMT, int XDT>
 int mmq_launch(MmArgs &a, hipStream_t s) {
   const int64_t units = static_cast<int64_t>(a.m_tiles) * a.n_tiles * a.splits;
   a.xcd = units % 8 == 0 ? 1 : 0;
   hipLaunchKernelGGL((k_mmq<FMT, XDT, kMmMT, kMmNFX>), dim3(static_cast<unsigned>(units)), dim3(256), 0, s, a);
-  return check_launch("mmq gemm");
+  const int rc = check_launch("mmq gemm");
+  if (rc) return rc;
+  return mm_reduce_launch<4, kMmMT, kMmNFX, 1>(a, s);
 }
 
 }  // namespace vybdq

@@ -43,10 +43,11 @@ static int64_t mm_part_bytes(int64_t tiles, int splits) {
 // where a super-step costs the larger of its MFMA time (64 MT cycles per fragment a wave owns, at
 // ~80% issue efficiency) and its LDS time (the X tile: 4 waves read it, one writes it, ~156 MT
 // cycles at 128 B/cycle), plus the HBM traffic of split partials (written, then read back).
-// nfx: most fragments one wave can own; frag_cycles: a super-step's cost per fragment a wave
-// owns; fixed_cycles: its cost floor (X tile traffic, barrier).
-static MmPlan mm_plan(int M, int N, int S, bool allow_split, int nfx = kMmNFX, double frag_cycles = 64.0 * kMmMT / 0.8,
-                      double fixed_cycles = 156.0 * kMmMT * 1.1) {
+// nfx: most fragments one wave can own; a super-step costs fixed_cycles (X tile traffic, barrier)
+// plus frag_cycles per fragment the busiest wave owns (measured on MI355X at the prefill shapes,
+// in 2.4 GHz cycles).
+static MmPlan mm_plan(int M, int N, int S, bool allow_split, int nfx = kMmNFX, double frag_cycles = 1584.0,
+                      double fixed_cycles = 1440.0) {
   const int cus = device_cus();
   const int m_tiles = (M + 16 * kMmMT - 1) / (16 * kMmMT);
   const int Ftot = N / 16;
@@ -56,8 +57,7 @@ static MmPlan mm_plan(int M, int N, int S, bool allow_split, int nfx = kMmNFX, d
     const int n_tiles = (Ftot + F - 1) / F;
     if ((n_tiles - 1) * F >= Ftot) continue;
     const int nfw = (F + 3) / 4;
-    const double var_cycles = frag_cycles * nfw;
-    const double step_us = (var_cycles > fixed_cycles ? var_cycles : fixed_cycles) / 2.4e3;
+    const double step_us = (fixed_cycles + frag_cycles * nfw) / 2.4e3;
     for (int splits = 1; splits <= (allow_split ? 8 : 1) && splits <= S; ++splits) {
       const int sps = (S + splits - 1) / splits;
       if ((splits - 1) * sps >= S) continue;
@@ -66,7 +66,7 @@ static MmPlan mm_plan(int M, int N, int S, bool allow_split, int nfx = kMmNFX, d
       double t = static_cast<double>(rounds) * sps * step_us;
       if (splits > 1) {
         const double bytes = static_cast<double>(units) * 16 * kMmMT * F * 16 * 4 * (2.0 - 1.0 / splits);
-        t += bytes / 5.0e6;  // ~5 TB/s
+        t += bytes / 2.5e6;  // written, then read back by the reducing workgroups
       }
       if (best_t < 0 || t < best_t - 1e-9) {
         best_t = t;
@@ -93,7 +93,7 @@ static MmPlan mm_plan(int M, int N, int S, bool allow_split, int nfx = kMmNFX, d
     }
   }
   const int64_t tiles = static_cast<int64_t>(best.m_tiles) * best.n_tiles;
-  best.ws_bytes = best.splits > 1 ? mm_part_bytes(tiles, best.splits) + ((tiles * 4 + 255) / 256) * 256 : 0;
+  best.ws_bytes = best.splits > 1 ? mm_part_bytes(tiles, best.splits) : 0;
   return best;
 }
 
@@ -114,7 +114,7 @@ __global__ void __launch_bounds__(256) k_x_to_f16(const void *__restrict__ X, u4
 
 static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 
-// workspace: [split partials + tile counters][fp16 copy of X]
+// workspace: [split partials][fp16 copy of X]
 int64_t mmq_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (!mmq_supported(M, N, K)) return 0;
   return align256(mm_plan(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K / 128), true).ws_bytes) +
@@ -157,9 +157,7 @@ int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   a.ldy = ldy;
   a.RS = RS;
   if (p.splits > 1) {
-    const int64_t tiles = static_cast<int64_t>(p.m_tiles) * p.n_tiles;
     a.part = static_cast<float *>(ws);
-    a.cnt = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + mm_part_bytes(tiles, p.splits));
   }
   if (wtype == 2) {
     switch (xdt) {
@@ -178,8 +176,7 @@ int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
 // ---- int8 path -------------------------------------------------------------------------------
 
 static MmPlan i8_plan(int M, int N, int S, bool allow_split) {
-  // a super-step costs ~12 VALU operations x 4 cycles per 16x16 int32 tile and block
-  return mm_plan(M, N, S, allow_split, kI8NFX, kI8MT * 4 * 12 * 4 / 0.8, 600.0);
+  return mm_plan(M, N, S, allow_split, kI8NFX, 2200.0, 2500.0);
 }
 
 int64_t mmq_i8_workspace_size(int64_t M, int64_t N, int64_t K) {
@@ -209,9 +206,7 @@ int mmq_i8_gemm(const void *W, const int8_t *Xq, const float *Xs, void *Y, int y
   a.ldy = ldy;
   a.RS = RS;
   if (p.splits > 1) {
-    const int64_t tiles = static_cast<int64_t>(p.m_tiles) * p.n_tiles;
     a.part = static_cast<float *>(ws);
-    a.cnt = reinterpret_cast<uint32_t *>(static_cast<char *>(ws) + mm_part_bytes(tiles, p.splits));
   }
   ia.Xq = Xq;
   ia.Xs = Xs;
@@ -219,8 +214,10 @@ int mmq_i8_gemm(const void *W, const int8_t *Xq, const float *Xs, void *Y, int y
   ia.lds = K / 32;
   const int64_t units = static_cast<int64_t>(a.m_tiles) * a.n_tiles * a.splits;
   a.xcd = units % 8 == 0 ? 1 : 0;
-  hipLaunchKernelGGL(k_mmq_i8, dim3(static_cast<unsigned>(units)), dim3(256), 0, s, ia);
-  return check_launch("mmq int8 gemm");
+  hipLaunchKernelGGL(k_mmq_i8, dim3(static_cast<unsigned>(units)), dim3(kI8Threads), 0, s, ia);
+  const int rc = check_launch("mmq int8 gemm");
+  if (rc) return rc;
+  return mm_reduce_launch<8, kI8MT / 2, kI8NFX, 2>(a, s);
 }
 
 }  // namespace vybdq

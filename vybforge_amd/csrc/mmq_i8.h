@@ -8,8 +8,9 @@
 // scales, dx[m, b] * dw[n, b] (the xq8 row scale and the Q8_0 block scale): three VALU operations
 // per output element per block, which bound this path (the MFMA itself is a small share).
 //
-// Workgroup = 4 waves, tile = 128 rows x F 16-column fragments split among the waves (as in the
-// fp16 path). Each super-step covers 128 k (4 blocks). Everything the super-step reads is
+// Workgroup = 8 waves (two per SIMD: a single wave issues VALU work at half the SIMD's rate),
+// tile = 128 rows x F 16-column fragments: wave (h, n) owns rows 64 h .. 64 h + 63 and quarter n of
+// the fragments. Each super-step covers 128 k (4 blocks). Everything the super-step reads is
 // brought into LDS by coalesced direct-to-LDS loads, double buffered:
 //   - the tile's weight rows: each row's 136-byte span of the super-step, as the 16-byte-aligned
 //     144-byte window around it (9 global_load_lds_dwordx4 pieces per row, consecutive lanes on
@@ -22,8 +23,9 @@
 
 namespace vybdq {
 
-constexpr int kI8MT = 8;   // 128 rows
-constexpr int kI8NFX = 4;  // up to 16 fragments (256 columns) per tile
+constexpr int kI8MT = 8;   // 128 rows per tile (4 m-fragments per wave)
+constexpr int kI8Threads = 512;
+constexpr int kI8NFX = 5;  // up to 20 fragments (320 columns) per tile
 constexpr int kI8Pieces = 9;  // 16-byte pieces per row window (144 B)
 
 struct I8Args {
@@ -35,19 +37,20 @@ struct I8Args {
 };
 
 // LDS bytes of one stage for F fragments per tile
-__host__ __device__ constexpr int i8_b_bytes(int F) { return ((F * 16 * kI8Pieces + 255) / 256) * 256 * 16; }
+__host__ __device__ constexpr int i8_b_bytes(int F) { return ((F * 16 * kI8Pieces + kI8Threads - 1) / kI8Threads) * kI8Threads * 16; }
 constexpr int kI8ABytes = kI8MT * 2 * 1024;     // Xq: (m-fragment, block pair) chunks
 constexpr int kI8SBytes = kI8MT * 16 * 4 * 4;   // Xs: row x 4 blocks
 constexpr int kI8StageBytes = kI8ABytes + kI8SBytes + i8_b_bytes(4 * kI8NFX);
-constexpr int kI8JB = i8_b_bytes(4 * kI8NFX) / 4096;  // weight DMA instructions per thread per super-step
+constexpr int kI8JB = i8_b_bytes(4 * kI8NFX) / (kI8Threads * 16);  // weight DMA instructions per thread per super-step
 
 template <int NF>
 __device__ __forceinline__ void i8_body(const I8Args &ia, uint8_t *st0, uint8_t *st1, uint32_t *last, int tile, int split,
                                         int row0, int fb, int fb_tile, int s0, int s1) {
-  constexpr int MT = kI8MT;
+  constexpr int MT = kI8MT / 2;  // m-fragments of this wave
   constexpr int NFA = NF > 0 ? NF : 1;
   const MmArgs &a = ia.m;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int mh = w >> 2;  // which 64 rows of the tile
   const int g = lane >> 4, nl = lane & 15;
   const int R = a.F * 16;                    // weight rows of the tile
   const int rows_total = a.N;
@@ -74,16 +77,16 @@ __device__ __forceinline__ void i8_body(const I8Args &ia, uint8_t *st0, uint8_t 
     // MFMA lane (row r, k-group g) of block t = 2 tp + u later reads 8 bytes at lane l = r + 16 (2u + g / 2),
     // offset 8 (g % 2). Instruction j = w + 4 jj covers (i, tp) = (j / 2, j % 2).
 #pragma unroll
-    for (int jj = 0; jj < MT / 2; ++jj) {
-      const int j = w + 4 * jj;
+    for (int jj = 0; jj < kI8MT * 2 / 8; ++jj) {
+      const int j = w + 8 * jj;
       const int i = j >> 1, tp = j & 1;
       int r = row0 + 16 * i + (lane & 15);
       r = r < a.M ? r : a.M - 1;
       const int8_t *src = ia.Xq + static_cast<int64_t>(r) * ia.ldq + 128 * s + 64 * tp + 16 * (lane >> 4);
       dma(src, st + j * 1024, D16{});
     }
-    // Xs: [row][the 4 block scales of the super-step]; waves w and w + 2 fetch the same 64 rows
-    // (identical bytes to the same place: no branch around the load)
+    // Xs: [row][the 4 block scales of the super-step]; the even and the odd waves each fetch the same
+    // 64 rows (identical bytes to the same place: no branch around the load)
     {
       int r = row0 + 64 * (w & 1) + lane;
       r = r < a.M ? r : a.M - 1;
@@ -95,12 +98,12 @@ __device__ __forceinline__ void i8_body(const I8Args &ia, uint8_t *st0, uint8_t 
     // unused part of the stage): a data-dependent trip count here costs the whole loop its registers
 #pragma unroll
     for (int j = 0; j < kI8JB; ++j) {
-      int p = 256 * j + tid;
+      int p = kI8Threads * j + tid;
       p = p < R * kI8Pieces ? p : R * kI8Pieces - 1;
       int row = fb_tile * 16 + p / kI8Pieces;
       row = row < rows_total ? row : rows_total - 1;
       const uint8_t *src = a.W + static_cast<int64_t>(row) * a.rowbytes + span + 16 * (p % kI8Pieces);
-      dma(src, st + kI8ABytes + kI8SBytes + 256 * 16 * j + 64 * 16 * w, D16{});
+      dma(src, st + kI8ABytes + kI8SBytes + kI8Threads * 16 * j + 64 * 16 * w, D16{});
     }
   };
   auto bar = [] {
@@ -154,6 +157,7 @@ __device__ __forceinline__ void i8_body(const I8Args &ia, uint8_t *st0, uint8_t 
         typedef int i4 __attribute__((ext_vector_type(4)));
         // A fragment of (i, t): 8 bytes at lane (l % 16) + 16 (2 (t % 2) + g / 2) of chunk (i, t / 2)
         auto a_frag = [&](int i) {
+          i += MT * mh;
           return *reinterpret_cast<const long *>(st + (i * 2 + t / 2) * 1024 +
                                                   ((lane & 15) + 16 * (2 * (t & 1) + (g >> 1))) * 16 + 8 * (g & 1));
         };
@@ -170,7 +174,7 @@ __device__ __forceinline__ void i8_body(const I8Args &ia, uint8_t *st0, uint8_t 
           // xq8 scales of this lane's 4 output rows (16 i + 4 g + r) for block t
           float dx[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) dx[r] = xs[(16 * i + 4 * g + r) * 4 + t];
+          for (int r = 0; r < 4; ++r) dx[r] = xs[(16 * (i + MT * mh) + 4 * g + r) * 4 + t];
 #pragma unroll
           for (int f = 0; f < NF; ++f)
 #pragma unroll
@@ -199,10 +203,10 @@ __device__ __forceinline__ void i8_body(const I8Args &ia, uint8_t *st0, uint8_t 
   }
   if (s < s1) compute(s, st0);
 
-  mm_finish<MT, kI8NFX, NF>(a, last, tile, split, row0, fb, acc);
+  mm_finish<MT, kI8NFX, NF, 8>(a, last, tile, split, row0 + 64 * mh, fb, acc);
 }
 
-__global__ void __launch_bounds__(256, 1) k_mmq_i8(I8Args ia) {
+__global__ void __launch_bounds__(kI8Threads, 1) k_mmq_i8(I8Args ia) {
   __shared__ __attribute__((aligned(16))) uint8_t st0[kI8StageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t st1[kI8StageBytes];
   __shared__ uint32_t last;
@@ -217,7 +221,7 @@ __global__ void __launch_bounds__(256, 1) k_mmq_i8(I8Args ia) {
   const int tile = ntile * a.m_tiles + mt;
   const int s0 = split * a.sps;
   const int s1 = s0 + a.sps < a.S ? s0 + a.sps : a.S;
-  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)) & 3;  // N quarter
   const int Fq = a.F >> 2, Fr = a.F & 3;
   const int fb_tile = ntile * a.F;
   const int fb = fb_tile + w * Fq + (w < Fr ? w : Fr);
@@ -226,6 +230,7 @@ __global__ void __launch_bounds__(256, 1) k_mmq_i8(I8Args ia) {
   nf = nf < left ? nf : (left > 0 ? left : 0);
   const int row0 = mt * 16 * kI8MT;
   switch (nf) {
+    case 5: i8_body<5>(ia, st0, st1, &last, tile, split, row0, fb, fb_tile, s0, s1); break;
     case 4: i8_body<4>(ia, st0, st1, &last, tile, split, row0, fb, fb_tile, s0, s1); break;
     case 3: i8_body<3>(ia, st0, st1, &last, tile, split, row0, fb, fb_tile, s0, s1); break;
     case 2: i8_body<2>(ia, st0, st1, &last, tile, split, row0, fb, fb_tile, s0, s1); break;

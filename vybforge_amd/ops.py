@@ -237,8 +237,8 @@ def gemm_q8_0_i8(W, Xq, Xs, N, K, y_dtype=torch.float32, residual=None, out=None
 
 
 class GemmWorkspace:
-    """Zero-filled, 256-byte aligned workspace for vybdq_gemm_ws (int8=False) or vybdq_gemm_q8_0_i8
-    (int8=True), sized for the given (M, N, K) shapes."""
+    """256-byte aligned workspace for vybdq_gemm_ws (int8=False) or vybdq_gemm_q8_0_i8 (int8=True),
+    sized for the given (M, N, K) shapes."""
 
     def __init__(self, shapes, device, ty=GGML_Q8_0, int8=False):
         if int8:
