@@ -205,8 +205,8 @@ __global__ void __launch_bounds__(kChainThreads) k_gemv_chain(const int64_t *__r
           }
         }
         first = false;
-        for (int off = G / 2; off > 0; off >>= 1) acc[0] += __shfl_xor(acc[0], off, 64);
-        if (act && ks == 0) {
+        acc[0] = G == 16 ? group_sum<16>(acc[0]) : (G == 32 ? group_sum<32>(acc[0]) : group_sum<64>(acc[0]));
+        if (act && ks == G - 1) {
           const void *RS = sg == 0 ? st.RS : nullptr;
           switch (st.ydt[sg]) {
             case VYBDQ_F32: store_elem<VYBDQ_F32>(st.Y[sg], RS, lrow, acc[0]); break;

@@ -7,11 +7,12 @@
 // dword-aligned vector loads and re-aligns the 2-byte-offset half with v_alignbit. The G
 // lanes of a row-slot walk the row's pairs with stride G (consecutive lanes read consecutive
 // pairs), each lane keeps one float32 accumulator per X row, and the G partials are combined
-// by a fixed xor-shuffle tree. G (8..64) is picked per launch so that the grid holds enough
-// waves to cover HBM latency while each lane's pairs fit one batch of registers.
+// by a fixed DPP tree on the VALU (group_sum; no LDS round trips in the tail). G (8..64) is
+// picked per launch so that the grid holds enough waves to cover HBM latency while each lane's
+// pairs fit one batch of registers.
 //
 // Latency. Every lane issues the loads of its first batch of pairs before anything else;
-// the x stage (coalesced 16-B loads -> LDS, block sums by 4-lane shuffles, one barrier)
+// the x stage (coalesced 16-B loads -> LDS, block sums by 4-lane DPP swaps, one barrier)
 // runs under those loads.
 //
 // Arithmetic. x is staged as fp16 in natural order. A quant byte becomes an fp16 with
@@ -95,11 +96,8 @@ __global__ void __launch_bounds__(256) k_gemv_pair(const void *__restrict__ X, i
       if (i0 + u < npairs) pair_dot<FMT, ORDER, M>(dw[u], lds, sx, P, ks + G * (i0 + u), acc);
   }
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-#pragma unroll
-    for (int off = G / 2; off > 0; off >>= 1) acc[m] += __shfl_xor(acc[m], off, 64);
-  }
-  if (active && ks == 0) {
+  for (int m = 0; m < M; ++m) acc[m] = group_sum<G>(acc[m]);
+  if (active && ks == G - 1) {
     const int64_t N = segs.end[sg] - (sg == 0 ? 0 : segs.end[sg - 1]);
     void *Y = segs.Y[sg];
     const void *RS = segs.RS[sg];

@@ -50,6 +50,35 @@ __device__ __forceinline__ void load_x_chunk(const void *X, int64_t i, uint32_t 
   }
 }
 
+// DPP lane exchange added to v: v + (the value of the lane that CTRL selects), on the VALU with
+// no LDS round trip. Lanes of 16-lane rows outside ROWS add 0.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float dpp_add(float v) {
+  const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xf, false);
+  return v + __builtin_bit_cast(float, t);
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1;     // quad_perm [1, 0, 3, 2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;     // quad_perm [2, 3, 0, 1]
+constexpr int DPP_ROW_MIRROR = 0x140;   // lane i <- lane 15 - i of its row
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane i <- lane 7 - i of its half-row
+constexpr int DPP_BCAST15 = 0x142;      // row r <- lane 15 of row r - 1
+constexpr int DPP_BCAST31 = 0x143;      // rows 2, 3 <- lane 31
+
+// Sum over each aligned group of G consecutive lanes (G = 8, 16, 32 or 64). After the quad swaps
+// and the mirrors every lane of a 16-lane row holds its row's (or half-row's) sum; the
+// broadcasts then fold rows together. The group total is in the group's last lane (G - 1).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(G == 8 || G == 16 || G == 32 || G == 64, "group size");
+  v = dpp_add<DPP_QUAD_XOR1>(v);
+  v = dpp_add<DPP_QUAD_XOR2>(v);
+  v = dpp_add<DPP_HALF_MIRROR>(v);
+  if constexpr (G >= 16) v = dpp_add<DPP_ROW_MIRROR>(v);
+  if constexpr (G >= 32) v = dpp_add<DPP_BCAST15, 0xA>(v);  // rows 1, 3 += rows 0, 2
+  if constexpr (G >= 64) v = dpp_add<DPP_BCAST31, 0x8>(v);  // row 3 += rows 0 + 1
+  return v;
+}
+
 // Convert a raw chunk to 4 fp16 pairs, store it at its LDS slot and reduce the block sums:
 // chunk c holds x[8c .. 8c+7] (for every X row m, since K = 64 P), lives in pair c>>3 at
 // (c>>3)*144 + (c&7)*16, and its 32-element block is c>>2. The 4 chunks of a block belong to 4
@@ -79,8 +108,8 @@ __device__ __forceinline__ void stage_chunk(const uint32_t (&r)[XW], int xdt, in
     s += static_cast<float>(v[0]);
     s += static_cast<float>(v[1]);
   }
-  s += __shfl_xor(s, 1, 64);
-  s += __shfl_xor(s, 2, 64);
+  s = dpp_add<DPP_QUAD_XOR1>(s);
+  s = dpp_add<DPP_QUAD_XOR2>(s);
   if ((c & 3) == 0) sx[c >> 2] = s;
 }
 
