@@ -151,6 +151,30 @@ def test_gemv_seg3_qkv(dev):
         assert gate(y.to(torch.float64).cpu().numpy(), ref, torch.float16) < TOL
 
 
+@pytest.mark.parametrize("plan", ["8,5,256", "8,1,64", "16,3,128", "16,2,256", "32,2,128", "32,5,64",
+                                  "64,3,256", "64,1,128"])
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+def test_gemv_forced_launch_plans(dev, plan, fmt):
+    """Every (lanes per row, pairs per batch, threads) shape on ragged rows: lanes past their last
+    pair, partial last workgroups and multi-batch rows (batch smaller than the row)."""
+    import os
+    N, K = 301, 2560
+    rng = np.random.default_rng(17)
+    if fmt == "q4_0":
+        raw, ty, ref_fn = synth.q4_0_weights(rng, N, K), ops.GGML_Q4_0, matmul.gemv_q4_0_f64
+    else:
+        raw, ty, ref_fn = synth.q8_0_weights(rng, N, K), ops.GGML_Q8_0, matmul.gemv_q8_0_f64
+        g, u, t = plan.split(",")
+        plan = ",".join([g, str(min(int(u), 3)), t])
+    x = synth.activations(rng, (K,))
+    os.environ["VYBDQ_GEMV_PLAN"] = plan
+    try:
+        y = ops.gemv(ty, to_dev(raw, dev), to_dev(x, dev), N, K).cpu().numpy()
+    finally:
+        os.environ.pop("VYBDQ_GEMV_PLAN", None)
+    assert matmul.rel_maxnorm(y, ref_fn(raw, x, N, K)[0]) < TOL
+
+
 def test_gemv_deterministic(dev):
     N, K = 4096, 4096
     rng = np.random.default_rng(3)

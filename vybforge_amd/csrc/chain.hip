@@ -121,8 +121,8 @@ __global__ void __launch_bounds__(kChainThreads) k_gemv_chain(const int64_t *__r
       sg = 0;
       if (row >= st.end[0]) sg = (row >= st.end[1]) ? 2 : 1;
       if (!act) sg = 0;
-      lrow = act ? row - (sg == 0 ? 0 : st.end[sg - 1]) : 0;
-      wrow = st.W[sg] + lrow * (static_cast<int64_t>(P) * Fmt<FMT>::PAIR_BYTES);
+      lrow = act ? row - (sg == 0 ? 0 : (sg == 1 ? st.end[0] : st.end[1])) : 0;
+      wrow = pick3_ptr(st.W, sg) + lrow * (static_cast<int64_t>(P) * Fmt<FMT>::PAIR_BYTES);
     };
     auto pair_ptr = [&](const uint8_t *wrow, int i) {
       int p = ks + G * i;
@@ -208,11 +208,12 @@ __global__ void __launch_bounds__(kChainThreads) k_gemv_chain(const int64_t *__r
         acc[0] = G == 16 ? group_sum<16>(acc[0]) : (G == 32 ? group_sum<32>(acc[0]) : group_sum<64>(acc[0]));
         if (act && ks == G - 1) {
           const void *RS = sg == 0 ? st.RS : nullptr;
-          switch (st.ydt[sg]) {
-            case VYBDQ_F32: store_elem<VYBDQ_F32>(st.Y[sg], RS, lrow, acc[0]); break;
-            case VYBDQ_F16: store_elem<VYBDQ_F16>(st.Y[sg], RS, lrow, acc[0]); break;
-            case VYBDQ_BF16: store_elem<VYBDQ_BF16>(st.Y[sg], RS, lrow, acc[0]); break;
-            default: store_elem<VYBDQ_F64>(st.Y[sg], RS, lrow, acc[0]); break;
+          void *Y = pick3_ptr(st.Y, sg);
+          switch (pick3(st.ydt, sg)) {
+            case VYBDQ_F32: store_elem<VYBDQ_F32>(Y, RS, lrow, acc[0]); break;
+            case VYBDQ_F16: store_elem<VYBDQ_F16>(Y, RS, lrow, acc[0]); break;
+            case VYBDQ_BF16: store_elem<VYBDQ_BF16>(Y, RS, lrow, acc[0]); break;
+            default: store_elem<VYBDQ_F64>(Y, RS, lrow, acc[0]); break;
           }
         }
       }

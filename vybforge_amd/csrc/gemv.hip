@@ -27,16 +27,16 @@
 
 namespace vybdq {
 
-template <int FMT, int G, int ORDER, int M, int XW>
+template <int FMT, int G, int ORDER, int M, int XW, int U>
 __global__ void __launch_bounds__(256) k_gemv_pair(const void *__restrict__ X, int xdt, int64_t K, Segs segs) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  constexpr int U = Fmt<FMT>::U;
   constexpr int PD = Fmt<FMT>::PAIR_DWORDS;
   constexpr int XC = 5;  // x chunks per thread prefetched ahead of the weight loads
   const int P = static_cast<int>(K >> 6);
   char *lds = smem;
   float *sx = reinterpret_cast<float *>(smem + static_cast<size_t>(M) * P * XPAIR_STRIDE);
 
+  const int T = blockDim.x;  // 64, 128 or 256
   const int lane = threadIdx.x & 63;
   const int ks = lane % G;
   const int rs = lane / G;
@@ -45,9 +45,10 @@ __global__ void __launch_bounds__(256) k_gemv_pair(const void *__restrict__ X, i
   int sg = 0;
   if (row >= segs.end[0]) sg = (row >= segs.end[1]) ? 2 : 1;
   if (!active) sg = 0;
-  const int64_t lrow = active ? row - (sg == 0 ? 0 : segs.end[sg - 1]) : 0;
+  const int64_t seg_lo = sg == 0 ? 0 : (sg == 1 ? segs.end[0] : segs.end[1]);
+  const int64_t lrow = active ? row - seg_lo : 0;
   const int64_t rowbytes = static_cast<int64_t>(P) * Fmt<FMT>::PAIR_BYTES;
-  const uint8_t *wrow = segs.W[sg] + lrow * rowbytes;
+  const uint8_t *wrow = pick3_ptr(segs.W, sg) + lrow * rowbytes;
   const int npairs = active && ks < P ? (P - ks + G - 1) / G : 0;
   // loads are unconditional (no divergent branches, no register shuffling): a lane past its
   // last pair re-reads a pair of its own row (inactive lanes: row 0 of segment 0)
@@ -62,7 +63,7 @@ __global__ void __launch_bounds__(256) k_gemv_pair(const void *__restrict__ X, i
   uint32_t xr[XC][XW];
 #pragma unroll
   for (int j = 0; j < XC; ++j) {
-    const int c = threadIdx.x + 256 * j;
+    const int c = threadIdx.x + T * j;
     if (c < nchunk) load_x_chunk<XW>(X, 8 * static_cast<int64_t>(c), xr[j]);
   }
   // 2. the first batch of weight pairs
@@ -72,10 +73,10 @@ __global__ void __launch_bounds__(256) k_gemv_pair(const void *__restrict__ X, i
   // 3. x -> LDS while the weights stream in
 #pragma unroll
   for (int j = 0; j < XC; ++j) {
-    const int c = threadIdx.x + 256 * j;
+    const int c = threadIdx.x + T * j;
     if (c < nchunk) stage_chunk<XW>(xr[j], xdt, c, lds, sx);
   }
-  for (int c = threadIdx.x + 256 * XC; c < nchunk; c += 256) {
+  for (int c = threadIdx.x + T * XC; c < nchunk; c += T) {
     uint32_t r[XW];
     load_x_chunk<XW>(X, 8 * static_cast<int64_t>(c), r);
     stage_chunk<XW>(r, xdt, c, lds, sx);
@@ -98,13 +99,14 @@ __global__ void __launch_bounds__(256) k_gemv_pair(const void *__restrict__ X, i
 #pragma unroll
   for (int m = 0; m < M; ++m) acc[m] = group_sum<G>(acc[m]);
   if (active && ks == G - 1) {
-    const int64_t N = segs.end[sg] - (sg == 0 ? 0 : segs.end[sg - 1]);
-    void *Y = segs.Y[sg];
-    const void *RS = segs.RS[sg];
+    const int64_t N = pick3(segs.end, sg) - seg_lo;
+    void *Y = pick3_ptr(segs.Y, sg);
+    const void *RS = pick3_ptr(segs.RS, sg);
+    const int ydt = pick3(segs.ydt, sg);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const int64_t i = m * N + lrow;
-      switch (segs.ydt[sg]) {
+      switch (ydt) {
         case VYBDQ_F32: store_elem<VYBDQ_F32>(Y, RS, i, acc[m]); break;
         case VYBDQ_F16: store_elem<VYBDQ_F16>(Y, RS, i, acc[m]); break;
         case VYBDQ_BF16: store_elem<VYBDQ_BF16>(Y, RS, i, acc[m]); break;
@@ -159,45 +161,102 @@ __global__ void __launch_bounds__(64) k_gemv_generic(const void *__restrict__ X,
 
 static constexpr int kMaxLds = 160 * 1024;
 
-// Lanes per row: the smallest G whose grid reaches ~4 waves per CU while each lane's pairs
-// fit one load batch.
-template <int FMT>
-static int pick_g(int64_t rows, int P) {
-  constexpr int U = Fmt<FMT>::U;
-  int G = 8;
-  while (G < 64 && (rows * G / 64 < 1024 || (P + G - 1) / G > U)) G *= 2;
-  return G;
+static int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
 }
 
-template <int FMT, int G, int ORDER, int M, int XW>
-static int launch_g(const void *X, int xdt, int64_t K, const Segs &segs, hipStream_t s) {
+// Launch shape of the pair kernel: G lanes per row, U pairs per lane and load batch, T threads
+// per workgroup (T / G rows).
+struct PairPlan {
+  int G, U, T;
+};
+
+// Largest load batch per format (VGPRs: U pair windows of 9 or 17 dwords in flight per lane).
+static int pair_umax(int fmt) { return fmt == FMT_Q8_0 ? 3 : 5; }
+
+// For one X row (decode): the widest G that still gives each lane at least two pairs (two pair
+// windows in flight per lane; one-pair lanes were measured slower at every decode shape), widened
+// further while the grid has fewer workgroups than CUs, 256 threads, and a batch of exactly
+// ceil(P / G) pairs (up to the format's largest). For batches (M > 1) the smallest G with ~4 waves
+// per CU whose row fits one widest batch. VYBDQ_GEMV_PLAN="G,U,T" overrides the plan.
+static PairPlan pair_plan(int fmt, int64_t rows, int P, int64_t M) {
+  const int umax = pair_umax(fmt);
+  PairPlan pl{64, umax, 256};
+  if (M > 1) {
+    int G = 8;
+    while (G < 64 && (rows * G / 64 < 1024 || (P + G - 1) / G > umax)) G *= 2;
+    pl.G = G;
+  } else {
+    int G = 8;
+    while (G < 64 && (P + 2 * G - 1) / (2 * G) >= 2) G *= 2;  // ceil(P / 2G) >= 2
+    while (G < 64 && rows * G / 256 < device_cu_count()) G *= 2;
+    const int U = (P + G - 1) / G;
+    pl.G = G;
+    pl.U = U < umax ? U : umax;
+  }
+  if (const char *e = getenv("VYBDQ_GEMV_PLAN")) {
+    int g = 0, u = 0, t = 0;
+    if (sscanf(e, "%d,%d,%d", &g, &u, &t) == 3 && (g == 8 || g == 16 || g == 32 || g == 64) && u >= 1 &&
+        u <= umax && (t == 64 || t == 128 || t == 256) && t >= g) {
+      pl.G = g; pl.U = u; pl.T = t;
+    }
+  }
+  return pl;
+}
+
+template <int FMT, int G, int ORDER, int M, int XW, int U>
+static int launch_gu(const void *X, int xdt, int64_t K, const Segs &segs, int threads, hipStream_t s) {
   const int64_t rows = segs.end[2];
   const int P = static_cast<int>(K / 64);
   const size_t lds = static_cast<size_t>(M) * P * (XPAIR_STRIDE + 2 * 4);
   if (lds > static_cast<size_t>(kMaxLds)) return set_error(VYBDQ_ERR_SHAPE, "gemv: K too large for the LDS x stage at this M");
-  constexpr int threads = 256;
-  constexpr int rows_per_wg = threads / G;
+  const int rows_per_wg = threads / G;
   const unsigned grid = static_cast<unsigned>((rows + rows_per_wg - 1) / rows_per_wg);
   if (lds > 64 * 1024) {
     static bool raised = false;  // one attribute call per instantiation
     if (!raised) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_pair<FMT, G, ORDER, M, XW>),
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_pair<FMT, G, ORDER, M, XW, U>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
       if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("gemv: LDS attribute: ") + hipGetErrorString(e));
       raised = true;
     }
   }
-  hipLaunchKernelGGL((k_gemv_pair<FMT, G, ORDER, M, XW>), dim3(grid), dim3(threads), lds, s, X, xdt, K, segs);
+  hipLaunchKernelGGL((k_gemv_pair<FMT, G, ORDER, M, XW, U>), dim3(grid), dim3(threads), lds, s, X, xdt, K, segs);
   return check_launch("gemv");
+}
+
+template <int FMT, int G, int ORDER, int M, int XW>
+static int launch_g(const void *X, int xdt, int64_t K, const Segs &segs, const PairPlan &pl, hipStream_t s) {
+  constexpr int UM = FMT == FMT_Q8_0 ? 3 : 5;
+  if constexpr (M > 1) {
+    return launch_gu<FMT, G, ORDER, M, XW, UM>(X, xdt, K, segs, pl.T, s);
+  } else {
+    switch (pl.U) {
+      case 1: return launch_gu<FMT, G, ORDER, M, XW, 1>(X, xdt, K, segs, pl.T, s);
+      case 2: return launch_gu<FMT, G, ORDER, M, XW, 2>(X, xdt, K, segs, pl.T, s);
+      case 3: return launch_gu<FMT, G, ORDER, M, XW, 3>(X, xdt, K, segs, pl.T, s);
+      case 4: return launch_gu<FMT, G, ORDER, M, XW, (UM < 4 ? UM : 4)>(X, xdt, K, segs, pl.T, s);
+      default: return launch_gu<FMT, G, ORDER, M, XW, UM>(X, xdt, K, segs, pl.T, s);
+    }
+  }
 }
 
 template <int FMT, int ORDER, int M, int XW>
 static int launch_mx(const void *X, int xdt, int64_t K, const Segs &segs, hipStream_t s) {
-  switch (pick_g<FMT>(segs.end[2], static_cast<int>(K / 64))) {
-    case 8: return launch_g<FMT, 8, ORDER, M, XW>(X, xdt, K, segs, s);
-    case 16: return launch_g<FMT, 16, ORDER, M, XW>(X, xdt, K, segs, s);
-    case 32: return launch_g<FMT, 32, ORDER, M, XW>(X, xdt, K, segs, s);
-    default: return launch_g<FMT, 64, ORDER, M, XW>(X, xdt, K, segs, s);
+  const PairPlan pl = pair_plan(FMT, segs.end[2], static_cast<int>(K / 64), M);
+  switch (pl.G) {
+    case 8: return launch_g<FMT, 8, ORDER, M, XW>(X, xdt, K, segs, pl, s);
+    case 16: return launch_g<FMT, 16, ORDER, M, XW>(X, xdt, K, segs, pl, s);
+    case 32: return launch_g<FMT, 32, ORDER, M, XW>(X, xdt, K, segs, pl, s);
+    default: return launch_g<FMT, 64, ORDER, M, XW>(X, xdt, K, segs, pl, s);
   }
 }
 

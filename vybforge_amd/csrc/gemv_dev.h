@@ -2,6 +2,7 @@
 // GGUF block formats, pair loads, quant unpack to fp16 pairs, the x stage and the pair dot.
 #pragma once
 #include "common.h"
+#include <type_traits>
 
 namespace vybdq {
 
@@ -30,6 +31,31 @@ struct Segs {
   int ydt[3];
   int64_t end[3];  // cumulative row ends
 };
+
+// Element i (0..2) of a three-entry kernel-argument array, chosen with selects: indexing the
+// by-value array with a per-lane i would make the compiler fetch the argument block through
+// vector memory loads, and the wait for them would delay the first weight load.
+// The empty asm keeps the three values in scalar registers; without it the compiler folds the
+// selects into one load through a selected address, which is the same memory access again.
+template <class V>
+__device__ __forceinline__ V pick3(const V (&a)[3], int i) {
+  using B = typename std::conditional<sizeof(V) == 8, uint64_t, uint32_t>::type;
+  static_assert(sizeof(V) == sizeof(B), "pick3: 4- or 8-byte values");
+  B b0 = __builtin_bit_cast(B, a[0]), b1 = __builtin_bit_cast(B, a[1]), b2 = __builtin_bit_cast(B, a[2]);
+  asm volatile("" : "+s"(b0), "+s"(b1), "+s"(b2));
+  return __builtin_bit_cast(V, i == 0 ? b0 : (i == 1 ? b1 : b2));
+}
+
+// pick3 for pointers: the result is formed as an offset from a[0], so the compiler still sees
+// a global-memory pointer (a pointer straight out of the asm would be generic: flat loads).
+template <class V>
+__device__ __forceinline__ V *pick3_ptr(V *const (&a)[3], int i) {
+  uint64_t b0 = reinterpret_cast<uint64_t>(a[0]), b1 = reinterpret_cast<uint64_t>(a[1]),
+           b2 = reinterpret_cast<uint64_t>(a[2]);
+  asm volatile("" : "+s"(b0), "+s"(b1), "+s"(b2));
+  const uint64_t d = (i == 0 ? b0 : (i == 1 ? b1 : b2)) - b0;  // byte distance from a[0] (mod 2^64)
+  return (V *)((const char *)a[0] + d);
+}
 
 // LDS x stage, per X row m: pair p (64 fp16, natural order) at byte m*P*144 + 144*p (a 16-B pad
 // per pair keeps the G lanes that read consecutive pairs on distinct banks); block sums at
