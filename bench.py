@@ -26,6 +26,7 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "dequant-GEMV GB/s (% HBM peak) + prefill/MoE GEMM TFLOP/s (% MFMA peak)"
 
 QWEN3_4B = dict(hidden=2560, q=4096, kv=1024, inter=9728, layers=36)
+STACK_TRAFFIC_PER_LAUNCH = 14419405  # measured HBM bytes per decode-stack launch (see run_stack)
 
 
 def parse():
@@ -33,7 +34,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="stack", choices=["stack", "stack_chain", "gemv1", "exl3", "prefill", "prefill_i8", "moe"])
+    ap.add_argument("--config", default="stack",
+                    choices=["stack", "stack_chain", "gemv1", "exl3", "prefill", "prefill_i8", "moe", "copy"])
     ap.add_argument("--tokens", type=int, default=16, help="tokens for --config moe")
     ap.add_argument("--batch", type=int, default=1, help="batch for --config exl3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -188,8 +190,11 @@ def run_stack(args, torch, dev):
     # over many tokens; the per-launch average includes inter-launch gaps
     n_launch = len(launches)
     achieved = bytes_tok / n_launch / (ms_step * 1e-3 / n_launch) / 1e9
+    # HBM bytes per launch from rocprofv3 FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00 (factors from a
+    # plain 256 MiB copy), averaged over the four launches of a layer: profiles/q4_0_gemv_decode_stack.md
+    traffic = STACK_TRAFFIC_PER_LAUNCH if args.config == "stack" else None
     roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic,
                     kernel=kernel,
                     avg_launch_us=round(ms_step * 1e3 / n_launch, 3),
                     bytes_per_launch=round(bytes_tok / n_launch))
@@ -406,6 +411,34 @@ def run_moe(args, torch, dev):
                 bytes_per_step=nbytes, launches_per_step=1)
 
 
+def run_copy(args, torch, dev):
+    """Calibration leg for the HBM traffic counters: a plain device copy of known size, 256 MiB
+    read + 256 MiB written per step. rocprofv3 FETCH_SIZE / WRITE_SIZE of this run, divided by
+    those sizes, give the factors that turn the counters of the other configs into bytes."""
+    n = 64 * 1024 * 1024
+    src = torch.ones(n, device=dev)
+    dst = torch.empty(n, device=dev)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    nbytes = 2 * n * 4
+    gbs = nbytes / (ms_step * 1e-3) / 1e9
+    roofline = dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None, kernel="torch device copy (calibration)")
+    return dict(value=gbs, ms_step=ms_step, wall=wall, roofline=roofline, flops=0,
+                workload="device copy 256 MiB -> 256 MiB (counter calibration)", bytes_per_step=nbytes,
+                launches_per_step=1)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -426,6 +459,8 @@ def main():
         r = run_prefill_i8(args, torch, dev)
     elif args.config == "moe":
         r = run_moe(args, torch, dev)
+    elif args.config == "copy":
+        r = run_copy(args, torch, dev)
     else:
         r = run_stack(args, torch, dev)
     cpu = None
