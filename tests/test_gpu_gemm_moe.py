@@ -205,7 +205,7 @@ def test_moe_route_oracle(dev, T, E, k):
     assert np.abs(w.cpu().numpy() - rw).max() < 1e-6
 
 
-def moe_case(dev, ty, T, H, I, E, k, seed, shared=True):
+def moe_case(dev, ty, T, H, I, E, k, seed, shared=True, xdtype=torch.bfloat16):
     rng = np.random.default_rng(seed)
     gate = [weights(ty, rng, I, H) for _ in range(E)]
     up = [weights(ty, rng, I, H) for _ in range(E)]
@@ -216,7 +216,7 @@ def moe_case(dev, ty, T, H, I, E, k, seed, shared=True):
     layer = ops.MoeLayer(ty, dev_t(np.concatenate(gate), dev), dev_t(np.concatenate(up), dev),
                          dev_t(np.concatenate(down), dev), H, I, E, k,
                          shared=tuple(dev_t(a, dev) for a in sh) if sh else None)
-    xb = torch.from_numpy(x).to(torch.bfloat16)
+    xb = torch.from_numpy(x).to(xdtype)
     out, idx, w = layer(xb.to(dev), dev_t(logits, dev), routing=True)
     experts = lambda e: (ref_rows(ty, gate[e], I, H), ref_rows(ty, up[e], I, H), ref_rows(ty, down[e], H, I))
     shared_w = tuple(ref_rows(ty, a, n, kk) for a, n, kk in zip(sh, (I, I, H), (H, H, I))) if sh else None
@@ -240,6 +240,23 @@ def test_moe_layer_small(dev, ty, T):
 
 def test_moe_layer_no_shared(dev):
     out, ref = moe_case(dev, ops.GGML_Q4_0, 9, H=128, I=64, E=8, k=2, seed=3, shared=False)
+    assert matmul.rel_maxnorm(out, ref) < TOL
+
+
+@pytest.mark.parametrize("ty", [ops.GGML_Q4_0, ops.GGML_Q8_0])
+@pytest.mark.parametrize("T", [1, 7, 16, 17, 40])
+@pytest.mark.parametrize("shared", [True, False])
+def test_moe_layer_grouped_mfma(dev, ty, T, shared):
+    """H and I multiples of 256: the grouped register-operand MFMA path. T <= 16 uses 16-row
+    m-tiles, larger T 32-row ones; with 8 experts and top-4 several experts get more rows than one
+    m-tile, and the shared expert is one more group over all tokens."""
+    out, ref = moe_case(dev, ty, T, H=512, I=256, E=8, k=4, seed=100 + T + ty, shared=shared)
+    assert matmul.rel_maxnorm(out, ref) < TOL
+
+
+@pytest.mark.parametrize("xdtype", [torch.float32, torch.float16])
+def test_moe_layer_grouped_mfma_x_dtypes(dev, xdtype):
+    out, ref = moe_case(dev, ops.GGML_Q4_0, 12, H=768, I=512, E=16, k=8, seed=5, xdtype=xdtype)
     assert matmul.rel_maxnorm(out, ref) < TOL
 
 

@@ -57,7 +57,11 @@ struct MmArgs {
   int64_t ldy;
   const void *RS;
   float *part;            // split partials [tile][split][waves][NFX][MT][64][4]
+  const uint8_t *W2;      // SwiGLU: the up rows (W holds the gate rows, same layout)
+  float limit;            // SwiGLU clamp
 };
+
+__device__ __forceinline__ float mm_silu(float g) { return g / (1.0f + __expf(-g)); }
 
 template <int FMT> struct MmFmt;
 template <> struct MmFmt<FMT_Q4_0> {
@@ -168,14 +172,16 @@ struct MmLds {
 
 // Split-K reduction (when the tile's super-steps were split) and the epilogue store of one wave's
 // accumulators acc[i][f][r] = C[row0 + 16 i + 4 g + r][(fb + f) * 16 + nl]; NW waves per workgroup.
-template <int MT, int NFX, int NF, int NW = 4>
+// SWI: the wave holds NF gate fragments then the NF up fragments of the same columns, and the
+// output is silu(min(g, limit)) * clamp(u, -limit, limit) (no split-K).
+template <int MT, int NFX, int NF, int NW = 4, bool SWI = false>
 __device__ __forceinline__ void mm_finish(const MmArgs &a, uint32_t *last, int tile, int split, int row0, int fb,
-                                          f4 (&acc)[MT][NF > 0 ? NF : 1]) {
+                                          f4 (&acc)[MT][(SWI ? 2 : 1) * NF > 0 ? (SWI ? 2 : 1) * NF : 1]) {
   (void)last;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, nl = lane & 15;
   // ---- split-K: store the partial tile; k_mm_reduce sums the splits in order and stores Y
-  if (a.splits > 1) {
+  if (!SWI && a.splits > 1) {
     constexpr int PER_WAVE = NFX * MT * 64 * 4;  // floats
     float *mine = a.part + ((static_cast<int64_t>(tile) * a.splits + split) * NW + w) * PER_WAVE;
 #pragma unroll
@@ -196,18 +202,25 @@ __device__ __forceinline__ void mm_finish(const MmArgs &a, uint32_t *last, int t
         const int m = row0 + 16 * i + 4 * g + r;
         if (m >= a.M) continue;
         const int64_t idx = static_cast<int64_t>(m) * a.ldy + n;
+        float v = acc[i][f][r];
+        if constexpr (SWI) {
+          const float gt = fminf(v, a.limit);
+          const float up = fminf(fmaxf(acc[i][NF + f][r], -a.limit), a.limit);
+          v = mm_silu(gt) * up;
+        }
         switch (a.ydt) {
-          case VYBDQ_F32: store_elem<VYBDQ_F32>(a.Y, a.RS, idx, acc[i][f][r]); break;
-          case VYBDQ_F16: store_elem<VYBDQ_F16>(a.Y, a.RS, idx, acc[i][f][r]); break;
-          case VYBDQ_BF16: store_elem<VYBDQ_BF16>(a.Y, a.RS, idx, acc[i][f][r]); break;
-          default: store_elem<VYBDQ_F64>(a.Y, a.RS, idx, acc[i][f][r]); break;
+          case VYBDQ_F32: store_elem<VYBDQ_F32>(a.Y, a.RS, idx, v); break;
+          case VYBDQ_F16: store_elem<VYBDQ_F16>(a.Y, a.RS, idx, v); break;
+          case VYBDQ_BF16: store_elem<VYBDQ_BF16>(a.Y, a.RS, idx, v); break;
+          default: store_elem<VYBDQ_F64>(a.Y, a.RS, idx, v); break;
         }
       }
   }
 }
 
-// Per-wave body for NF owned fragments (NF wave-uniform; NF = 0 waves only stage X).
-template <int FMT, int XDT, int MT, int NFX, int NF>
+// Per-wave body for NF owned fragments (NF wave-uniform; NF = 0 waves only stage X). SWI: each
+// owned fragment is a pair, gate rows from W and the same up rows from W2 (2 NF B fragments).
+template <int FMT, int XDT, int MT, int NFX, int NF, bool SWI = false>
 __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, int tile, int split, int row0, int fb,
                                         int s0, int s1) {
   constexpr int WD = MmFmt<FMT>::WD;
@@ -216,12 +229,14 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, nl = lane & 15;
 
+  constexpr int NB = (SWI ? 2 : 1) * NF;  // B fragments per step
   // ---- weight windows: lane (nl, g), fragment f -> row (fb + f) * 16 + nl, block 4s + g
-  const uint8_t *wrow[NF > 0 ? NF : 1];
+  const uint8_t *wrow[NB > 0 ? NB : 1];
 #pragma unroll
-  for (int f = 0; f < NF; ++f) {
-    const int64_t n = static_cast<int64_t>(fb + f) * 16 + nl;
-    wrow[f] = a.W + n * a.rowbytes + (g * BB - 2 * (g & 1));
+  for (int f = 0; f < NB; ++f) {
+    const int fr = f < NF ? f : f - NF;
+    const int64_t n = static_cast<int64_t>(fb + fr) * 16 + nl;
+    wrow[f] = (f < NF ? a.W : a.W2) + n * a.rowbytes + (g * BB - 2 * (g & 1));
   }
   const uint32_t sel = (g & 1) ? 0x07060504u : 0x05040302u;  // quant dword j from (w[j+1], w[j])
   const uint32_t shd = (g & 1) ? 16u : 0u;
@@ -290,15 +305,15 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
   // Loads younger than X(s + 1) when step s ends in the steady state: W(s + 2 - NA + D), then per
   // step X(.) and W(.) for the NA - 2 steps after it. Earlier steps have at least as many, so
   // waiting for this many is safe everywhere (it may wait a little longer in the first steps).
-  constexpr int YOUNGER = (NA - 2) * (MT + NF * LPW) + NF * LPW;
+  constexpr int YOUNGER = (NA - 2) * (MT + NB * LPW) + NB * LPW;
 
-  f4 acc[MT][NF > 0 ? NF : 1];
+  f4 acc[MT][NB > 0 ? NB : 1];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int f = 0; f < (NF > 0 ? NF : 1); ++f) acc[i][f] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int f = 0; f < (NB > 0 ? NB : 1); ++f) acc[i][f] = f4{0.f, 0.f, 0.f, 0.f};
 
-  uint32_t ring[D][NF > 0 ? NF : 1][WD];
+  uint32_t ring[D][NB > 0 ? NB : 1][WD];
 
   // ---- prologue: X(s0 .. s0 + NA - 2) and weights s0 .. s0 + D - 1, interleaved as the steady
   // state issues them
@@ -308,18 +323,18 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
       for (int j = 0; j < D; ++j) {
         if (j < NA - 1) x_dma(s0 + j, sm.a[j]);
 #pragma unroll
-        for (int f = 0; f < NF; ++f) load_window<WD>(wptr(f, s0 + j), ring[j][f]);
+        for (int f = 0; f < NB; ++f) load_window<WD>(wptr(f, s0 + j), ring[j][f]);
         __builtin_amdgcn_sched_barrier(0);
       }
-      wait_vm(std::integral_constant<int, (NA - 2) * (MT + NF * LPW) + 2 * NF * LPW < 64
-                                              ? (NA - 2) * (MT + NF * LPW) + 2 * NF * LPW : 63>{});
-      if constexpr ((NA - 2) * (MT + NF * LPW) + 2 * NF * LPW >= 64) wait_vm(std::integral_constant<int, 0>{});
+      wait_vm(std::integral_constant<int, (NA - 2) * (MT + NB * LPW) + 2 * NB * LPW < 64
+                                              ? (NA - 2) * (MT + NB * LPW) + 2 * NB * LPW : 63>{});
+      if constexpr ((NA - 2) * (MT + NB * LPW) + 2 * NB * LPW >= 64) wait_vm(std::integral_constant<int, 0>{});
     } else {
       x_regs(s0);
 #pragma unroll
       for (int d = 0; d < D; ++d) {
 #pragma unroll
-        for (int f = 0; f < NF; ++f) load_window<WD>(wptr(f, s0 + d), ring[d][f]);
+        for (int f = 0; f < NB; ++f) load_window<WD>(wptr(f, s0 + d), ring[d][f]);
         __builtin_amdgcn_sched_barrier(0);
       }
       x_stage(sm.a[0]);
@@ -329,8 +344,8 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
 
   // MFMAs of one super-step: A fragments of step t + 1 and the B fragment after the current one
   // are produced while the current MFMAs run
-  auto compute = [&](const uint32_t (&slot)[NF > 0 ? NF : 1][WD], const uint8_t *abase) {
-    if constexpr (NF > 0) {
+  auto compute = [&](const uint32_t (&slot)[NB > 0 ? NB : 1][WD], const uint8_t *abase) {
+    if constexpr (NB > 0) {
       hf8 af[2][MT];
 #pragma unroll
       for (int i = 0; i < MT; ++i) af[0][i] = *reinterpret_cast<const hf8 *>(abase + (i * 4 * 64 + lane) * 16);
@@ -343,10 +358,10 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
             af[(t + 1) & 1][i] = *reinterpret_cast<const hf8 *>(abase + ((i * 4 + t + 1) * 64 + lane) * 16);
         }
 #pragma unroll
-        for (int f = 0; f < NF; ++f) {
-          const bool last = t == 3 && f == NF - 1;
-          const int fn = f + 1 < NF ? f + 1 : 0;
-          const int tn = f + 1 < NF ? t : t + 1;
+        for (int f = 0; f < NB; ++f) {
+          const bool last = t == 3 && f == NB - 1;
+          const int fn = f + 1 < NB ? f + 1 : 0;
+          const int tn = f + 1 < NB ? t : t + 1;
           hf8 bnext = bcur;
           if (!last) bnext = dequant_step<FMT>(slot[fn], tn, sel, shd);
 #pragma unroll
@@ -369,7 +384,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
     if constexpr (decltype(refill)::value) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int f = 0; f < NF; ++f) load_window<WD>(wptr(f, s + D), ring[d][f]);
+      for (int f = 0; f < NB; ++f) load_window<WD>(wptr(f, s + D), ring[d][f]);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (DMA) wait_vm(std::integral_constant<int, YOUNGER>{});
     } else {
@@ -401,7 +416,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
     if (s + 2 < s1) step(I2{}, No{}, s + 2);
   }
 
-  mm_finish<MT, NFX, NF>(a, sm.last, tile, split, row0, fb, acc);
+  mm_finish<MT, NFX, NF, 4, SWI>(a, sm.last, tile, split, row0, fb, acc);
 }
 
 template <int FMT, int XDT, int MT, int NFX>

@@ -9,10 +9,14 @@
 // Without a bias the selection is by logit (sigmoid is monotone: exact order, no float32
 // saturation ties); with a bias the choice is computed in double, as the reference does.
 //
-// Pipeline (all on the stream, no host syncs): route -> bucket (one workgroup: per-expert
-// counts, stable token order, group row/tile tables) -> grouped gate|up GEMM (SwiGLU epilogue,
-// rows gathered by token) -> grouped down GEMM -> shared expert (plain GEMMs) -> combine.
+// Pipeline (all on the stream, no host syncs), when H and I are multiples of 256: route ->
+// bucket (one workgroup: per-expert counts, a parallel scan, the m-tile list of the experts that
+// received tokens, each (token, slot)'s row) -> grouped gate|up GEMM with the SwiGLU epilogue
+// (moe_mm.h; the shared expert is one more group over all tokens) -> grouped down GEMM ->
+// combine. Other shapes run the routed and shared experts through the LDS-staged grouped GEMM
+// of dqgemm.hip (one group per expert, 16-row tiles).
 #include "gemv_dev.h"
+#include "moe_mm.h"
 
 namespace vybdq {
 
@@ -117,6 +121,67 @@ __global__ void __launch_bounds__(256) k_moe_bucket(const int *__restrict__ idx,
   }
 }
 
+// One workgroup. Rows are grouped by expert: expert e's rows are [off_e, off_e + cnt_e) in
+// expert order, the shared expert (when present) owns rows [n, n + T) (n = T * topk) in token
+// order. Writes pos[t * topk + s] (the row of slot s of token t), row_map (row -> token), the
+// m-tile list tiles[j] = {expert (-1 shared), r0, r1, m} (the shared expert's tiles first, then
+// the routed experts' in expert order) and its length. A row's place inside its expert's range
+// comes from an atomic cursor, so it may change from run to run; no result depends on it (each
+// output row is computed from its own token row alone, and the combine reads through pos).
+__global__ void __launch_bounds__(256) k_moe_bucket_tiles(const int *__restrict__ idx, int T, int topk, int E, int BMr,
+                                                          int shared, int *__restrict__ pos, int *__restrict__ row_map,
+                                                          int4 *__restrict__ tiles, int *__restrict__ ntiles) {
+  extern __shared__ int sh[];
+  int *cnt = sh;       // [E]
+  int *cur = sh + E;   // [E]
+  __shared__ int scan_r[256], scan_t[256];
+  const int tid = threadIdx.x;
+  const int n = T * topk;
+  for (int e = tid; e < E; e += 256) cnt[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += 256) atomicAdd(&cnt[idx[i]], 1);
+  __syncthreads();
+  // thread tid owns experts [e0, e1): their row and m-tile totals, then a block scan of those
+  const int per = (E + 255) / 256;
+  const int e0 = tid * per < E ? tid * per : E;
+  const int e1 = e0 + per < E ? e0 + per : E;
+  int rs = 0, ts = 0;
+  for (int e = e0; e < e1; ++e) {
+    rs += cnt[e];
+    ts += (cnt[e] + BMr - 1) / BMr;
+  }
+  scan_r[tid] = rs;
+  scan_t[tid] = ts;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const int ar = tid >= off ? scan_r[tid - off] : 0;
+    const int at = tid >= off ? scan_t[tid - off] : 0;
+    __syncthreads();
+    scan_r[tid] += ar;
+    scan_t[tid] += at;
+    __syncthreads();
+  }
+  const int tsh = shared ? (T + BMr - 1) / BMr : 0;
+  int r = scan_r[tid] - rs, t = tsh + scan_t[tid] - ts;
+  for (int e = e0; e < e1; ++e) {
+    const int c = cnt[e], mt = (c + BMr - 1) / BMr;
+    cur[e] = r;
+    for (int m = 0; m < mt; ++m) tiles[t + m] = make_int4(e, r, r + c, m);
+    r += c;
+    t += mt;
+  }
+  if (tid == 255) *ntiles = tsh + scan_t[255];
+  for (int j = tid; j < tsh; j += 256) tiles[j] = make_int4(-1, n, n + T, j);
+  if (shared)
+    for (int i = tid; i < T; i += 256) row_map[n + i] = i;
+  __syncthreads();
+  for (int i = tid; i < n; i += 256) {
+    const int p = atomicAdd(&cur[idx[i]], 1);
+    pos[i] = p;
+    row_map[p] = i / topk;
+  }
+}
+
 // out[t][h] = sum_s w[t,s] * rows[pos[t,s]][h] (+ shared[t][h]); fixed slot order.
 template <int ODT>
 __global__ void __launch_bounds__(256) k_moe_combine(const float *__restrict__ rows, const float *__restrict__ shared,
@@ -133,11 +198,19 @@ __global__ void __launch_bounds__(256) k_moe_combine(const float *__restrict__ r
 }
 
 struct MoeWs {
-  int *idx, *pos, *grp_rows, *grp_tiles, *row_map;
+  int *idx, *pos, *grp_rows, *grp_tiles, *row_map, *ntiles;
+  int4 *tiles;
   float *w, *rows, *shared;
   _Float16 *act, *act_s;
   int64_t bytes;
 };
+
+// Upper bound of the m-tile list: ceil(T / 16) shared tiles, and per expert with rows at most
+// one tile more than its rows / 16.
+static int64_t moe_max_tiles(int64_t T, int64_t E, int64_t k) {
+  const int64_t n = T * k;
+  return (T + 15) / 16 + (E < n ? E : n) + n / 16 + 1;
+}
 
 static MoeWs moe_layout(char *base, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k) {
   MoeWs m{};
@@ -150,11 +223,13 @@ static MoeWs moe_layout(char *base, int64_t T, int64_t H, int64_t I, int64_t E, 
   m.idx = reinterpret_cast<int *>(take(4 * T * k));
   m.w = reinterpret_cast<float *>(take(4 * T * k));
   m.pos = reinterpret_cast<int *>(take(4 * T * k));
-  m.row_map = reinterpret_cast<int *>(take(4 * T * k));
+  m.row_map = reinterpret_cast<int *>(take(4 * (T * k + T)));
   m.grp_rows = reinterpret_cast<int *>(take(4 * (E + 1)));
   m.grp_tiles = reinterpret_cast<int *>(take(4 * (E + 1)));
-  m.act = reinterpret_cast<_Float16 *>(take(2 * T * k * I));
-  m.rows = reinterpret_cast<float *>(take(4 * T * k * H));
+  m.tiles = reinterpret_cast<int4 *>(take(16 * moe_max_tiles(T, E, k)));
+  m.ntiles = reinterpret_cast<int *>(take(4));
+  m.act = reinterpret_cast<_Float16 *>(take(2 * (T * k + T) * I));
+  m.rows = reinterpret_cast<float *>(take(4 * (T * k + T) * H));
   m.act_s = reinterpret_cast<_Float16 *>(take(2 * T * I));
   m.shared = reinterpret_cast<float *>(take(4 * T * H));
   m.bytes = off;
@@ -207,6 +282,86 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
                 "x must be 16-byte and weights 4-byte aligned");
   hipStream_t s = as_stream(stream);
   MoeWs m = moe_layout(reinterpret_cast<char *>(ws), T, H, I, E, topk);
+  if (H % 256 == 0 && I % 256 == 0) {
+    const int MT = T > 16 ? 2 : 1;  // 16-row fragments per m-tile
+    const int n = static_cast<int>(T * topk);
+    const bool shared = s_gate != 0;
+    int *idx = idx_out ? reinterpret_cast<int *>(idx_out) : m.idx;
+    float *wts = w_out ? reinterpret_cast<float *>(w_out) : m.w;
+    const void *lg = reinterpret_cast<const void *>(logits);
+    const float *bs = reinterpret_cast<const float *>(bias);
+    VYBDQ_DISPATCH_IN(logits_dt, LDT,
+        hipLaunchKernelGGL((k_moe_route<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg, bs,
+                           static_cast<int>(E), static_cast<int>(topk), scale, idx, wts));
+    int rc = check_launch("moe route");
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_moe_bucket_tiles, dim3(1), dim3(256), static_cast<size_t>(2 * E) * 4, s, idx,
+                       static_cast<int>(T), static_cast<int>(topk), static_cast<int>(E), 16 * MT, shared ? 1 : 0,
+                       m.pos, m.row_map, m.tiles, m.ntiles);
+    rc = check_launch("moe bucket");
+    if (rc) return rc;
+    const int max_tiles = static_cast<int>(moe_max_tiles(T, E, topk));
+    const int64_t rb_h = (H / 64) * (wtype == 2 ? 36 : 68);  // row bytes, K = H
+    const int64_t rb_i = (I / 64) * (wtype == 2 ? 36 : 68);  // row bytes, K = I
+    auto run = [&](int xdt, bool swi, const MoeMmArgs &g) {
+      return wtype == 2 ? moe_mm_q4(xdt, MT, swi, g, max_tiles, s) : moe_mm_q8(xdt, MT, swi, g, max_tiles, s);
+    };
+    // gate|up with SwiGLU -> act [n + T][I] fp16
+    MoeMmArgs g{};
+    g.m.W = reinterpret_cast<const uint8_t *>(w_gate);
+    g.m.W2 = reinterpret_cast<const uint8_t *>(w_up);
+    g.m.rowbytes = rb_h;
+    g.m.X = reinterpret_cast<const void *>(x);
+    g.m.ldx = H;
+    g.m.row_map = m.row_map;
+    g.m.N = static_cast<int>(I);
+    g.m.S = static_cast<int>(H / 128);
+    g.m.F = kMoeF;
+    g.m.n_tiles = static_cast<int>(I / (16 * kMoeF));
+    g.m.splits = 1;
+    g.m.sps = g.m.S;
+    g.m.Y = m.act;
+    g.m.ydt = VYBDQ_F16;
+    g.m.ldy = I;
+    g.m.limit = static_cast<float>(limit);
+    g.w_stride = I * rb_h;
+    g.Ws = reinterpret_cast<const uint8_t *>(s_gate);
+    g.W2s = reinterpret_cast<const uint8_t *>(s_up);
+    g.tiles = m.tiles;
+    g.ntiles = m.ntiles;
+    rc = run(x_dt, true, g);
+    if (rc) return rc;
+    // down -> rows [n + T][H] f32
+    MoeMmArgs d = g;
+    d.m.W = reinterpret_cast<const uint8_t *>(w_down);
+    d.m.W2 = nullptr;
+    d.m.rowbytes = rb_i;
+    d.m.X = m.act;
+    d.m.ldx = I;
+    d.m.row_map = nullptr;
+    d.m.N = static_cast<int>(H);
+    d.m.S = static_cast<int>(I / 128);
+    d.m.n_tiles = static_cast<int>(H / (16 * kMoeF));
+    d.m.sps = d.m.S;
+    d.m.Y = m.rows;
+    d.m.ydt = VYBDQ_F32;
+    d.m.ldy = H;
+    d.w_stride = H * rb_i;
+    d.Ws = reinterpret_cast<const uint8_t *>(s_down);
+    d.W2s = nullptr;
+    rc = run(VYBDQ_F16, false, d);
+    if (rc) return rc;
+    const float *shr = shared ? m.rows + static_cast<int64_t>(n) * H : nullptr;
+    const int64_t tot = T * H;
+    const unsigned gc = static_cast<unsigned>((tot + 255) / 256);
+    void *o = reinterpret_cast<void *>(out);
+    switch (out_dt) {
+      case VYBDQ_F32: hipLaunchKernelGGL((k_moe_combine<VYBDQ_F32>), dim3(gc), dim3(256), 0, s, m.rows, shr, m.pos, wts, static_cast<int>(T), static_cast<int>(topk), H, o); break;
+      case VYBDQ_F16: hipLaunchKernelGGL((k_moe_combine<VYBDQ_F16>), dim3(gc), dim3(256), 0, s, m.rows, shr, m.pos, wts, static_cast<int>(T), static_cast<int>(topk), H, o); break;
+      default: hipLaunchKernelGGL((k_moe_combine<VYBDQ_BF16>), dim3(gc), dim3(256), 0, s, m.rows, shr, m.pos, wts, static_cast<int>(T), static_cast<int>(topk), H, o); break;
+    }
+    return check_launch("moe combine");
+  }
   const int BM = dq_gemm_bm();
   const int n = static_cast<int>(T * topk);
   int *idx = idx_out ? reinterpret_cast<int *>(idx_out) : m.idx;
