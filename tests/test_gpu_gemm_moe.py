@@ -254,6 +254,21 @@ def test_moe_layer_grouped_mfma(dev, ty, T, shared):
     assert matmul.rel_maxnorm(out, ref) < TOL
 
 
+@pytest.mark.parametrize("ty", [ops.GGML_Q4_0, ops.GGML_Q8_0])
+@pytest.mark.parametrize("T,gemv_max_t", [(1, 16), (7, 0), (16, 16), (40, 64), (40, 0)])
+def test_moe_layer_expert_paths(dev, ty, T, gemv_max_t):
+    """Both grouped expert kernels, forced through VYBDQ_MOE_GEMV_MAX_T: the multi-token GEMV
+    (groups of up to 4 tokens per x stage; 40 tokens over 8 experts gives groups of several
+    chunks and a 10-chunk shared expert) and the MFMA GEMM (0)."""
+    import os
+    os.environ["VYBDQ_MOE_GEMV_MAX_T"] = str(gemv_max_t)
+    try:
+        out, ref = moe_case(dev, ty, T, H=512, I=256, E=8, k=4, seed=200 + T + ty)
+    finally:
+        os.environ.pop("VYBDQ_MOE_GEMV_MAX_T", None)
+    assert matmul.rel_maxnorm(out, ref) < TOL
+
+
 @pytest.mark.parametrize("xdtype", [torch.float32, torch.float16])
 def test_moe_layer_grouped_mfma_x_dtypes(dev, xdtype):
     out, ref = moe_case(dev, ops.GGML_Q4_0, 12, H=768, I=512, E=16, k=8, seed=5, xdtype=xdtype)

@@ -10,12 +10,15 @@
 // saturation ties); with a bias the choice is computed in double, as the reference does.
 //
 // Pipeline (all on the stream, no host syncs), when H and I are multiples of 256: route ->
-// bucket (one workgroup: per-expert counts, a parallel scan, the m-tile list of the experts that
-// received tokens, each (token, slot)'s row) -> grouped gate|up GEMM with the SwiGLU epilogue
-// (moe_mm.h; the shared expert is one more group over all tokens) -> grouped down GEMM ->
-// combine. Other shapes run the routed and shared experts through the LDS-staged grouped GEMM
-// of dqgemm.hip (one group per expert, 16-row tiles).
+// bucket (one workgroup: per-expert counts, a parallel scan, the lists of row groups of the
+// experts that received tokens, each (token, slot)'s row) -> grouped gate|up with the SwiGLU
+// epilogue -> grouped down -> combine. The shared expert is one more group over all tokens. Up to
+// 64 tokens the grouped kernels are multi-token GEMVs over groups of at most 4 rows (moe_gemv.h:
+// each expert row is streamed as a contiguous run); above that, MFMA GEMMs over 16/32-row
+// m-tiles (moe_mm.h). Other shapes run the routed and shared experts through the LDS-staged
+// grouped GEMM of dqgemm.hip (one group per expert, 16-row tiles).
 #include "gemv_dev.h"
+#include "moe_gemv.h"
 #include "moe_mm.h"
 
 namespace vybdq {
@@ -128,13 +131,17 @@ __global__ void __launch_bounds__(256) k_moe_bucket(const int *__restrict__ idx,
 // the routed experts' in expert order) and its length. A row's place inside its expert's range
 // comes from an atomic cursor, so it may change from run to run; no result depends on it (each
 // output row is computed from its own token row alone, and the combine reads through pos).
+// Two tile lists of the same rows are written, of at most BMr and BMr2 rows per tile (one per
+// grouped kernel of the layer); tiles2 may be null.
 __global__ void __launch_bounds__(256) k_moe_bucket_tiles(const int *__restrict__ idx, int T, int topk, int E, int BMr,
-                                                          int shared, int *__restrict__ pos, int *__restrict__ row_map,
-                                                          int4 *__restrict__ tiles, int *__restrict__ ntiles) {
+                                                          int BMr2, int shared, int *__restrict__ pos,
+                                                          int *__restrict__ row_map, int4 *__restrict__ tiles,
+                                                          int *__restrict__ ntiles, int4 *__restrict__ tiles2,
+                                                          int *__restrict__ ntiles2) {
   extern __shared__ int sh[];
   int *cnt = sh;       // [E]
   int *cur = sh + E;   // [E]
-  __shared__ int scan_r[256], scan_t[256];
+  __shared__ int scan_r[256], scan_t[256], scan_t2[256];
   const int tid = threadIdx.x;
   const int n = T * topk;
   for (int e = tid; e < E; e += 256) cnt[e] = 0;
@@ -145,33 +152,47 @@ __global__ void __launch_bounds__(256) k_moe_bucket_tiles(const int *__restrict_
   const int per = (E + 255) / 256;
   const int e0 = tid * per < E ? tid * per : E;
   const int e1 = e0 + per < E ? e0 + per : E;
-  int rs = 0, ts = 0;
+  int rs = 0, ts = 0, ts2 = 0;
   for (int e = e0; e < e1; ++e) {
     rs += cnt[e];
     ts += (cnt[e] + BMr - 1) / BMr;
+    ts2 += (cnt[e] + BMr2 - 1) / BMr2;
   }
   scan_r[tid] = rs;
   scan_t[tid] = ts;
+  scan_t2[tid] = ts2;
   __syncthreads();
   for (int off = 1; off < 256; off <<= 1) {
     const int ar = tid >= off ? scan_r[tid - off] : 0;
     const int at = tid >= off ? scan_t[tid - off] : 0;
+    const int at2 = tid >= off ? scan_t2[tid - off] : 0;
     __syncthreads();
     scan_r[tid] += ar;
     scan_t[tid] += at;
+    scan_t2[tid] += at2;
     __syncthreads();
   }
   const int tsh = shared ? (T + BMr - 1) / BMr : 0;
-  int r = scan_r[tid] - rs, t = tsh + scan_t[tid] - ts;
+  const int tsh2 = shared ? (T + BMr2 - 1) / BMr2 : 0;
+  int r = scan_r[tid] - rs, t = tsh + scan_t[tid] - ts, t2 = tsh2 + scan_t2[tid] - ts2;
   for (int e = e0; e < e1; ++e) {
-    const int c = cnt[e], mt = (c + BMr - 1) / BMr;
+    const int c = cnt[e], mt = (c + BMr - 1) / BMr, mt2 = (c + BMr2 - 1) / BMr2;
     cur[e] = r;
     for (int m = 0; m < mt; ++m) tiles[t + m] = make_int4(e, r, r + c, m);
+    if (tiles2)
+      for (int m = 0; m < mt2; ++m) tiles2[t2 + m] = make_int4(e, r + m * BMr2, r + (c < (m + 1) * BMr2 ? c : (m + 1) * BMr2), 0);
     r += c;
     t += mt;
+    t2 += mt2;
   }
-  if (tid == 255) *ntiles = tsh + scan_t[255];
+  if (tid == 255) {
+    *ntiles = tsh + scan_t[255];
+    if (ntiles2) *ntiles2 = tsh2 + scan_t2[255];
+  }
   for (int j = tid; j < tsh; j += 256) tiles[j] = make_int4(-1, n, n + T, j);
+  if (tiles2)
+    for (int j = tid; j < tsh2; j += 256)
+      tiles2[j] = make_int4(-1, n + j * BMr2, n + (T < (j + 1) * BMr2 ? T : (j + 1) * BMr2), 0);
   if (shared)
     for (int i = tid; i < T; i += 256) row_map[n + i] = i;
   __syncthreads();
@@ -198,18 +219,18 @@ __global__ void __launch_bounds__(256) k_moe_combine(const float *__restrict__ r
 }
 
 struct MoeWs {
-  int *idx, *pos, *grp_rows, *grp_tiles, *row_map, *ntiles;
-  int4 *tiles;
+  int *idx, *pos, *grp_rows, *grp_tiles, *row_map, *ntiles, *ntiles2;
+  int4 *tiles, *tiles2;
   float *w, *rows, *shared;
   _Float16 *act, *act_s;
   int64_t bytes;
 };
 
-// Upper bound of the m-tile list: ceil(T / 16) shared tiles, and per expert with rows at most
-// one tile more than its rows / 16.
-static int64_t moe_max_tiles(int64_t T, int64_t E, int64_t k) {
+// Upper bound of the m-tile list for tiles of at least `rows` rows: ceil(T / rows) shared
+// tiles, and per expert with rows at most one tile more than its rows / rows.
+static int64_t moe_max_tiles(int64_t T, int64_t E, int64_t k, int64_t rows = 1) {
   const int64_t n = T * k;
-  return (T + 15) / 16 + (E < n ? E : n) + n / 16 + 1;
+  return (T + rows - 1) / rows + (E < n ? E : n) + n / rows + 1;
 }
 
 static MoeWs moe_layout(char *base, int64_t T, int64_t H, int64_t I, int64_t E, int64_t k) {
@@ -228,6 +249,8 @@ static MoeWs moe_layout(char *base, int64_t T, int64_t H, int64_t I, int64_t E, 
   m.grp_tiles = reinterpret_cast<int *>(take(4 * (E + 1)));
   m.tiles = reinterpret_cast<int4 *>(take(16 * moe_max_tiles(T, E, k)));
   m.ntiles = reinterpret_cast<int *>(take(4));
+  m.tiles2 = reinterpret_cast<int4 *>(take(16 * moe_max_tiles(T, E, k)));
+  m.ntiles2 = reinterpret_cast<int *>(take(4));
   m.act = reinterpret_cast<_Float16 *>(take(2 * (T * k + T) * I));
   m.rows = reinterpret_cast<float *>(take(4 * (T * k + T) * H));
   m.act_s = reinterpret_cast<_Float16 *>(take(2 * T * I));
@@ -295,62 +318,129 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
                            static_cast<int>(E), static_cast<int>(topk), scale, idx, wts));
     int rc = check_launch("moe route");
     if (rc) return rc;
+    // few tokens per expert: grouped GEMV (one tile per expert); else the grouped MFMA GEMM
+    int gv_max = 64;  // measured crossover (T = 1..64: the GEMV path is faster)
+    if (const char *e = getenv("VYBDQ_MOE_GEMV_MAX_T")) gv_max = atoi(e);
+    const bool gv = T <= gv_max && H / 64 <= 256 * 4 && I / 64 <= 256 * 4;
+    // GEMV groups hold at most one x stage of tokens: larger experts (and the shared expert)
+    // become several groups over the same weights that run side by side
+    int mc = kMoeGvMC;  // tokens per GEMV group (experts with more rows: several groups)
+    if (const char *e = getenv("VYBDQ_MOE_GEMV_MC")) mc = atoi(e) < 1 ? 1 : (atoi(e) > kMoeGvMC ? kMoeGvMC : atoi(e));
+    // tiles: m-tiles of 16 MT rows for the MFMA GEMM; tiles2: groups of at most mc rows for the GEMV
+    const int BMr = 16 * MT;
     hipLaunchKernelGGL(k_moe_bucket_tiles, dim3(1), dim3(256), static_cast<size_t>(2 * E) * 4, s, idx,
-                       static_cast<int>(T), static_cast<int>(topk), static_cast<int>(E), 16 * MT, shared ? 1 : 0,
-                       m.pos, m.row_map, m.tiles, m.ntiles);
+                       static_cast<int>(T), static_cast<int>(topk), static_cast<int>(E), BMr, mc, shared ? 1 : 0,
+                       m.pos, m.row_map, m.tiles, m.ntiles, gv ? m.tiles2 : nullptr, gv ? m.ntiles2 : nullptr);
     rc = check_launch("moe bucket");
     if (rc) return rc;
-    const int max_tiles = static_cast<int>(moe_max_tiles(T, E, topk));
+    const int max_tiles = static_cast<int>(moe_max_tiles(T, E, topk, BMr));
     const int64_t rb_h = (H / 64) * (wtype == 2 ? 36 : 68);  // row bytes, K = H
     const int64_t rb_i = (I / 64) * (wtype == 2 ? 36 : 68);  // row bytes, K = I
-    auto run = [&](int xdt, bool swi, const MoeMmArgs &g) {
-      return wtype == 2 ? moe_mm_q4(xdt, MT, swi, g, max_tiles, s) : moe_mm_q8(xdt, MT, swi, g, max_tiles, s);
-    };
-    // gate|up with SwiGLU -> act [n + T][I] fp16
-    MoeMmArgs g{};
-    g.m.W = reinterpret_cast<const uint8_t *>(w_gate);
-    g.m.W2 = reinterpret_cast<const uint8_t *>(w_up);
-    g.m.rowbytes = rb_h;
-    g.m.X = reinterpret_cast<const void *>(x);
-    g.m.ldx = H;
-    g.m.row_map = m.row_map;
-    g.m.N = static_cast<int>(I);
-    g.m.S = static_cast<int>(H / 128);
-    g.m.F = kMoeF;
-    g.m.n_tiles = static_cast<int>(I / (16 * kMoeF));
-    g.m.splits = 1;
-    g.m.sps = g.m.S;
-    g.m.Y = m.act;
-    g.m.ydt = VYBDQ_F16;
-    g.m.ldy = I;
-    g.m.limit = static_cast<float>(limit);
-    g.w_stride = I * rb_h;
-    g.Ws = reinterpret_cast<const uint8_t *>(s_gate);
-    g.W2s = reinterpret_cast<const uint8_t *>(s_up);
-    g.tiles = m.tiles;
-    g.ntiles = m.ntiles;
-    rc = run(x_dt, true, g);
-    if (rc) return rc;
-    // down -> rows [n + T][H] f32
-    MoeMmArgs d = g;
-    d.m.W = reinterpret_cast<const uint8_t *>(w_down);
-    d.m.W2 = nullptr;
-    d.m.rowbytes = rb_i;
-    d.m.X = m.act;
-    d.m.ldx = I;
-    d.m.row_map = nullptr;
-    d.m.N = static_cast<int>(H);
-    d.m.S = static_cast<int>(I / 128);
-    d.m.n_tiles = static_cast<int>(H / (16 * kMoeF));
-    d.m.sps = d.m.S;
-    d.m.Y = m.rows;
-    d.m.ydt = VYBDQ_F32;
-    d.m.ldy = H;
-    d.w_stride = H * rb_i;
-    d.Ws = reinterpret_cast<const uint8_t *>(s_down);
-    d.W2s = nullptr;
-    rc = run(VYBDQ_F16, false, d);
-    if (rc) return rc;
+    if (gv) {
+      const int max_groups = static_cast<int>(moe_max_tiles(T, E, topk, mc));
+      MoeGvArgs ga{};
+      ga.W = reinterpret_cast<const uint8_t *>(w_gate);
+      ga.W2 = reinterpret_cast<const uint8_t *>(w_up);
+      ga.w_stride = I * rb_h;
+      ga.Ws = reinterpret_cast<const uint8_t *>(s_gate);
+      ga.W2s = reinterpret_cast<const uint8_t *>(s_up);
+      ga.rowbytes = rb_h;
+      ga.P = static_cast<int>(H / 64);
+      ga.X = reinterpret_cast<const void *>(x);
+      ga.xdt = x_dt;
+      ga.ldx = H;
+      ga.row_map = m.row_map;
+      ga.groups = m.tiles2;
+      ga.ngroups = m.ntiles2;
+      // columns per workgroup: 128, fewer when there are few groups (so the grid covers the CUs)
+      int cus = 256;
+      {
+        int dev = 0;
+        if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+      }
+      auto cols_for = [&](int64_t N, int cpp) {
+        int64_t c = 128;
+        while (c > cpp && (N / c) * (1 + (E < n ? E : n)) < 2 * cus) c /= 2;
+        return static_cast<int>(c);
+      };
+      ga.N = static_cast<int>(I);
+      ga.cols_per_wg = cols_for(I, 4);
+      ga.Y = m.act;
+      ga.ydt = VYBDQ_F16;
+      ga.ldy = I;
+      ga.limit = static_cast<float>(limit);
+      ga.mc = mc;
+      rc = wtype == 2 ? moe_gemv_q4(true, ga, max_groups, s) : moe_gemv_q8(true, ga, max_groups, s);
+      if (rc) return rc;
+      MoeGvArgs gd = ga;
+      gd.W = reinterpret_cast<const uint8_t *>(w_down);
+      gd.W2 = nullptr;
+      gd.w_stride = H * rb_i;
+      gd.Ws = reinterpret_cast<const uint8_t *>(s_down);
+      gd.W2s = nullptr;
+      gd.rowbytes = rb_i;
+      gd.P = static_cast<int>(I / 64);
+      gd.X = m.act;
+      gd.xdt = VYBDQ_F16;
+      gd.ldx = I;
+      gd.row_map = nullptr;
+      gd.N = static_cast<int>(H);
+      gd.cols_per_wg = cols_for(H, 16);
+      gd.Y = m.rows;
+      gd.ydt = VYBDQ_F32;
+      gd.ldy = H;
+      rc = wtype == 2 ? moe_gemv_q4(false, gd, max_groups, s) : moe_gemv_q8(false, gd, max_groups, s);
+      if (rc) return rc;
+    } else {
+      auto run = [&](int xdt, bool swi, const MoeMmArgs &g) {
+        return wtype == 2 ? moe_mm_q4(xdt, MT, swi, g, max_tiles, s) : moe_mm_q8(xdt, MT, swi, g, max_tiles, s);
+      };
+      // gate|up with SwiGLU -> act [n + T][I] fp16
+      MoeMmArgs g{};
+      g.m.W = reinterpret_cast<const uint8_t *>(w_gate);
+      g.m.W2 = reinterpret_cast<const uint8_t *>(w_up);
+      g.m.rowbytes = rb_h;
+      g.m.X = reinterpret_cast<const void *>(x);
+      g.m.ldx = H;
+      g.m.row_map = m.row_map;
+      g.m.N = static_cast<int>(I);
+      g.m.S = static_cast<int>(H / 128);
+      g.m.F = kMoeF;
+      g.m.n_tiles = static_cast<int>(I / (16 * kMoeF));
+      g.m.splits = 1;
+      g.m.sps = g.m.S;
+      g.m.Y = m.act;
+      g.m.ydt = VYBDQ_F16;
+      g.m.ldy = I;
+      g.m.limit = static_cast<float>(limit);
+      g.w_stride = I * rb_h;
+      g.Ws = reinterpret_cast<const uint8_t *>(s_gate);
+      g.W2s = reinterpret_cast<const uint8_t *>(s_up);
+      g.tiles = m.tiles;
+      g.ntiles = m.ntiles;
+      rc = run(x_dt, true, g);
+      if (rc) return rc;
+      // down -> rows [n + T][H] f32
+      MoeMmArgs d = g;
+      d.m.W = reinterpret_cast<const uint8_t *>(w_down);
+      d.m.W2 = nullptr;
+      d.m.rowbytes = rb_i;
+      d.m.X = m.act;
+      d.m.ldx = I;
+      d.m.row_map = nullptr;
+      d.m.N = static_cast<int>(H);
+      d.m.S = static_cast<int>(I / 128);
+      d.m.n_tiles = static_cast<int>(H / (16 * kMoeF));
+      d.m.sps = d.m.S;
+      d.m.Y = m.rows;
+      d.m.ydt = VYBDQ_F32;
+      d.m.ldy = H;
+      d.w_stride = H * rb_i;
+      d.Ws = reinterpret_cast<const uint8_t *>(s_down);
+      d.W2s = nullptr;
+      rc = run(VYBDQ_F16, false, d);
+      if (rc) return rc;
+    }
     const float *shr = shared ? m.rows + static_cast<int64_t>(n) * H : nullptr;
     const int64_t tot = T * H;
     const unsigned gc = static_cast<unsigned>((tot + 255) / 256);
