@@ -32,6 +32,23 @@ __device__ __forceinline__ uint32_t win_extract(const uint32_t (&w)[6], int o) {
   return __builtin_amdgcn_alignbit(w[i + 1], w[i], s);
 }
 
+// The codebook hash of a window up to the two fp16 halves (before they are added).
+template <int CB>
+__device__ __forceinline__ uint32_t decode_window_halves(uint32_t w) {
+  const uint32_t wl = w & 0xffffu;
+  uint32_t hi, lo;
+  if constexpr (CB == VYBDQ_EXL3_MCG) {
+    hi = wl * 0xCBACu;
+    lo = wl * 0x1FEDu;
+  } else {
+    hi = wl * 0x0551u;
+    lo = wl * 0x7C72u + 0x03D45AA4u;
+  }
+  asm volatile("" : "+v"(hi));
+  const uint32_t x = (hi << 16) + lo;
+  return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+}
+
 template <int CB>
 __device__ __forceinline__ _Float16 decode_window(uint32_t w) {
   // x = w16 * M (+ A) mod 2^32 from two 16x16-bit products; only the low 16 bits of w are used
@@ -196,13 +213,28 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   const int kb_begin = s * kb_per_split;
   const int kb_end = min(kb_begin + kb_per_split, KB);
   const int nkb = kb_end - kb_begin;
-  // stage x' rows of this split: [BP][16 * nkb] fp16
+  // Small batches dot the two fp16 halves of each decoded value with (x, x) (one v_dot2 per weight
+  // and batch row: x lo + x hi, the float32 sum the fp16 value rounds), which saves the half add
+  // and the pairing of decoded values; x' is staged duplicated for that. Larger batches round
+  // the value to fp16 once and share it across the batch rows.
+  constexpr bool HALVES = BP <= 2;
+  // stage x' rows of this split: [BP][16 * nkb] fp16 (HALVES: fp16 pairs (x, x))
   _Float16 *xs = reinterpret_cast<_Float16 *>(smem);
   const int rows = 16 * nkb;
-  for (int i = threadIdx.x; i < BP * rows / 8; i += blockDim.x) {
-    const int b = i / (rows / 8), c = i % (rows / 8);
-    *reinterpret_cast<u4 *>(xs + b * rows + 8 * c) =
-        *reinterpret_cast<const u4 *>(xp + b * K + 16 * static_cast<int64_t>(kb_begin) + 8 * c);
+  if constexpr (HALVES) {
+    uint32_t *xd = reinterpret_cast<uint32_t *>(smem);
+    for (int i = threadIdx.x; i < BP * rows / 2; i += blockDim.x) {
+      const int b = i / (rows / 2), c = i % (rows / 2);
+      const uint32_t v = *reinterpret_cast<const uint32_t *>(xp + b * K + 16 * static_cast<int64_t>(kb_begin) + 2 * c);
+      *reinterpret_cast<u2 *>(xd + b * rows + 2 * c) =
+          u2{__builtin_amdgcn_perm(v, v, 0x01000100u), __builtin_amdgcn_perm(v, v, 0x03020302u)};
+    }
+  } else {
+    for (int i = threadIdx.x; i < BP * rows / 8; i += blockDim.x) {
+      const int b = i / (rows / 8), c = i % (rows / 8);
+      *reinterpret_cast<u4 *>(xs + b * rows + 8 * c) =
+          *reinterpret_cast<const u4 *>(xp + b * K + 16 * static_cast<int64_t>(kb_begin) + 8 * c);
+    }
   }
   __syncthreads();
 
@@ -216,6 +248,21 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   for (int kk = w_begin; kk < w_end; ++kk) {
     uint32_t w[6];
     lane_window(trellis, static_cast<int64_t>(kb_begin + kk) * NB + nb, j, w);
+    if constexpr (HALVES) {
+      const uint32_t *xd = reinterpret_cast<const uint32_t *>(smem);
+#pragma unroll
+      for (int q = 0; q < 32; ++q) {
+        uint32_t x = win_extract(w, kExl3SlotOff0[q]) & kExl3SlotMask0[q];
+        if (kExl3SlotOff1[q] >= 0) x |= win_extract(w, kExl3SlotOff1[q]) & kExl3SlotMask1[q];
+        const h2 y = __builtin_bit_cast(h2, decode_window_halves<CB>(x));
+#pragma unroll
+        for (int b = 0; b < BP; ++b) {
+          const h2 xv = __builtin_bit_cast(h2, xd[b * rows + 16 * kk + (q & 15)]);
+          acc[b][q >> 4] = __builtin_amdgcn_fdot2(y, xv, acc[b][q >> 4], false);
+        }
+      }
+      continue;
+    }
     _Float16 v[32];
     lane_decode<CB>(w, v);
     h2 pj[8], pj8[8];
@@ -374,7 +421,7 @@ extern "C" int64_t vybdq_exl3_workspace_size(int64_t B, int64_t K, int64_t N) {
 template <int CB, int BP>
 static void exl3_gemm_launch(const uint16_t *t, const _Float16 *xp, float *zp, int64_t K, int NB, int S, int kbs,
                              hipStream_t s) {
-  const size_t xs_bytes = static_cast<size_t>(BP) * 16 * kbs * 2;
+  const size_t xs_bytes = static_cast<size_t>(BP) * 16 * kbs * (BP <= 2 ? 4 : 2);
   const size_t red_bytes = static_cast<size_t>(4) * BP * 128 * 4;
   const size_t lds = xs_bytes > red_bytes ? xs_bytes : red_bytes;
   hipLaunchKernelGGL((k_exl3_gemm<CB, BP>), dim3(static_cast<unsigned>(NB / 8), static_cast<unsigned>(S)), dim3(256),
