@@ -205,6 +205,32 @@ def test_moe_route_oracle(dev, T, E, k):
     assert np.abs(w.cpu().numpy() - rw).max() < 1e-6
 
 
+@pytest.mark.parametrize("ldt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("E,k", [(256, 8), (300, 8), (1024, 16), (7, 7)])
+def test_moe_route_ties_and_types(dev, ldt, E, k):
+    """Logits on a coarse grid (many exact ties: the lower expert id must win), every logit dtype,
+    E up to 1024 and k = E."""
+    rng = np.random.default_rng(E + k)
+    logits = (rng.integers(-6, 7, (5, E)) * 0.5).astype(np.float32)
+    zero = logits == 0
+    logits[zero] *= rng.choice(np.array([-1.0, 1.0], np.float32), int(zero.sum()))  # -0 ties with +0
+    lt = torch.from_numpy(logits).to(ldt)
+    idx, w = ops.moe_route(lt.to(dev), k)
+    ridx, rw = moe.route_logits(lt.to(torch.float64).numpy(), k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+    assert np.abs(w.cpu().numpy() - rw).max() < 1e-6
+
+
+def test_moe_route_zero_bias_matches_unbiased(dev):
+    """A zero bias (the double-precision selection path) and no bias (the logit path) agree."""
+    rng = np.random.default_rng(9)
+    logits = dev_t(rng.standard_normal((64, 256)).astype(np.float32), dev)
+    i0, w0 = ops.moe_route(logits, 8)
+    i1, w1 = ops.moe_route(logits, 8, dev_t(np.zeros(256, np.float32), dev))
+    assert torch.equal(i0, i1)
+    assert torch.equal(w0, w1)
+
+
 def moe_case(dev, ty, T, H, I, E, k, seed, shared=True, xdtype=torch.bfloat16):
     rng = np.random.default_rng(seed)
     gate = [weights(ty, rng, I, H) for _ in range(E)]
@@ -266,6 +292,19 @@ def test_moe_layer_expert_paths(dev, ty, T, gemv_max_t):
         out, ref = moe_case(dev, ty, T, H=512, I=256, E=8, k=4, seed=200 + T + ty)
     finally:
         os.environ.pop("VYBDQ_MOE_GEMV_MAX_T", None)
+    assert matmul.rel_maxnorm(out, ref) < TOL
+
+
+@pytest.mark.parametrize("ty", [ops.GGML_Q4_0, ops.GGML_Q8_0])
+@pytest.mark.parametrize("T", [1, 3, 7, 17])
+@pytest.mark.parametrize("cols,grid", [("-1,-1", "1,1"), ("-1,-1", "3,5"), ("-1,-1", "-3,-2"), ("8,32", "0,0")])
+def test_moe_gemv_work_splits(dev, monkeypatch, ty, T, cols, grid):
+    """The multi-token GEMV's two ways of cutting the work, forced through VYBDQ_MOE_GEMV_COLS /
+    VYBDQ_MOE_GEMV_GRID: equal ranges over grids of several sizes (ranges that span groups, a
+    grid of one workgroup per CU, multiples of the resident count) and small column blocks."""
+    monkeypatch.setenv("VYBDQ_MOE_GEMV_COLS", cols)
+    monkeypatch.setenv("VYBDQ_MOE_GEMV_GRID", grid)
+    out, ref = moe_case(dev, ty, T, H=512, I=256, E=8, k=4, seed=300 + T + ty)
     assert matmul.rel_maxnorm(out, ref) < TOL
 
 

@@ -23,6 +23,19 @@ int set_error(int code, const std::string &msg);
 int check_launch(const char *what);  // hipGetLastError after a launch
 inline hipStream_t as_stream(uint64_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Compute units of the current device (cached per device; 256 if the query fails).
+inline int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 #define VYBDQ_REQUIRE(cond, code, msg)                                                     \
   do {                                                                                     \
     if (!(cond)) return ::vybdq::set_error((code), std::string(__func__) + ": " + (msg));  \

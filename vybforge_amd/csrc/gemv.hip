@@ -161,18 +161,6 @@ __global__ void __launch_bounds__(64) k_gemv_generic(const void *__restrict__ X,
 
 static constexpr int kMaxLds = 160 * 1024;
 
-static int device_cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
-
 // Launch shape of the pair kernel: G lanes per row, U pairs per lane and load batch, T threads
 // per workgroup (T / G rows).
 struct PairPlan {

@@ -17,17 +17,6 @@ extern template int mmq_launch<FMT_Q8_0, VYBDQ_F32>(MmArgs &, hipStream_t);
 
 // ---- host --------------------------------------------------------------------------------
 
-static int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
 
 struct MmPlan {
   int m_tiles, n_tiles, F, splits, sps;
@@ -48,7 +37,7 @@ static int64_t mm_part_bytes(int64_t tiles, int splits) {
 // in 2.4 GHz cycles).
 static MmPlan mm_plan(int M, int N, int S, bool allow_split, int nfx = kMmNFX, double frag_cycles = 1584.0,
                       double fixed_cycles = 1440.0) {
-  const int cus = device_cus();
+  const int cus = device_cu_count();
   const int m_tiles = (M + 16 * kMmMT - 1) / (16 * kMmMT);
   const int Ftot = N / 16;
   MmPlan best{};

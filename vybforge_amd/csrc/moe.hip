@@ -20,6 +20,8 @@
 #include "gemv_dev.h"
 #include "moe_gemv.h"
 #include "moe_mm.h"
+#include <cstdio>
+#include <type_traits>
 
 namespace vybdq {
 
@@ -29,6 +31,76 @@ int dq_gemm_grouped(int wtype, bool swiglu, const uint8_t *W, const uint8_t *W2,
                     int M, int N, int64_t K, void *Y, int ydt, int64_t ldy, float limit, int max_mtiles,
                     hipStream_t s);
 int dq_gemm_bm();
+
+// Largest 64-bit value over the wave, on the VALU (DPP steps as in group_sum), in every lane.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  auto step = [&](auto ctrl, auto rows) {
+    constexpr int C = decltype(ctrl)::value, R = decltype(rows)::value;
+    const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
+    const uint32_t olo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(lo), C, R, 0xf, false));
+    const uint32_t ohi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(hi), C, R, 0xf, false));
+    const uint64_t o = (static_cast<uint64_t>(ohi) << 32) | olo;
+    v = o > v ? o : v;
+  };
+  step(std::integral_constant<int, DPP_QUAD_XOR1>{}, std::integral_constant<int, 0xf>{});
+  step(std::integral_constant<int, DPP_QUAD_XOR2>{}, std::integral_constant<int, 0xf>{});
+  step(std::integral_constant<int, DPP_HALF_MIRROR>{}, std::integral_constant<int, 0xf>{});
+  step(std::integral_constant<int, DPP_ROW_MIRROR>{}, std::integral_constant<int, 0xf>{});
+  step(std::integral_constant<int, DPP_BCAST15>{}, std::integral_constant<int, 0xa>{});
+  step(std::integral_constant<int, DPP_BCAST31>{}, std::integral_constant<int, 0x8>{});
+  // lane 63 holds the maximum
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), 63);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(v >> 32), 63);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Router without a selection bias (the selection is then by logit): each candidate is one 64-bit
+// key, the order-preserving bits of its float32 logit above the complement of its expert id (so
+// equal logits prefer the lower id), and the wave maximum of the keys is taken on the VALU; the
+// double-precision sigmoid is evaluated only for the k winners, in selection order (the same
+// arithmetic as k_moe_route).
+template <int LDT>
+__global__ void __launch_bounds__(64) k_moe_route_logit(const void *__restrict__ logits, int E, int topk, double scale,
+                                                        int *__restrict__ idx_out, float *__restrict__ w_out) {
+  const int t = blockIdx.x, lane = threadIdx.x;
+  constexpr int PER = 16;  // experts per lane (E <= 1024)
+  uint64_t key[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    key[i] = 0;  // below every real key
+    if (e < E) {
+      uint32_t u = __float_as_uint(load_elem<LDT>(logits, static_cast<int64_t>(t) * E + e));
+      if (u == 0x80000000u) u = 0;  // -0 ties with +0
+      u ^= (u >> 31) ? 0xffffffffu : 0x80000000u;
+      key[i] = (static_cast<uint64_t>(u) << 32) | (0xffffffffu - static_cast<uint32_t>(e));
+    }
+  }
+  float my_l = 0.f;  // lane s keeps the logit of the s-th winner
+  for (int s = 0; s < topk; ++s) {
+    uint64_t bk = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) bk = key[i] > bk ? key[i] : bk;
+    bk = wave_max_u64(bk);
+    const int be = static_cast<int>(0xffffffffu - static_cast<uint32_t>(bk));
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (key[i] == bk) key[i] = 0;  // the owner retires the winner
+    const uint32_t hk = static_cast<uint32_t>(bk >> 32);  // the logit's bits, mapped back
+    if (lane == 0) idx_out[t * topk + s] = be;
+    if (lane == s) my_l = __uint_as_float(hk ^ ((hk >> 31) ? 0x80000000u : 0xffffffffu));
+  }
+  // the k sigmoids in parallel (lane s: winner s), summed in selection order
+  const double my_sc = lane < topk ? 1.0 / (1.0 + exp(-static_cast<double>(my_l))) : 0.0;
+  double tot = 0.0;
+  for (int s = 0; s < topk; ++s) {
+    const uint64_t b = __double_as_longlong(my_sc);
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(b), s);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(b >> 32), s);
+    tot += __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+  }
+  if (lane < topk) w_out[t * topk + lane] = static_cast<float>(my_sc / (tot + 1e-20) * scale);
+}
 
 template <int LDT>
 __global__ void __launch_bounds__(64) k_moe_route(const void *__restrict__ logits, const float *__restrict__ bias,
@@ -276,6 +348,13 @@ extern "C" int vybdq_moe_route(uint64_t logits, int logits_dt, uint64_t bias, ui
                 VYBDQ_ERR_SHAPE, "need 1 <= topk <= E <= 1024 and topk <= 64");
   hipStream_t s = as_stream(stream);
   const void *lg = reinterpret_cast<const void *>(logits);
+  if (!bias) {
+    VYBDQ_DISPATCH_IN(logits_dt, LDT,
+        hipLaunchKernelGGL((k_moe_route_logit<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg,
+                           static_cast<int>(E), static_cast<int>(topk), scale, reinterpret_cast<int *>(idx_out),
+                           reinterpret_cast<float *>(w_out)));
+    return check_launch("vybdq_moe_route");
+  }
   VYBDQ_DISPATCH_IN(logits_dt, LDT,
       hipLaunchKernelGGL((k_moe_route<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg,
                          reinterpret_cast<const float *>(bias), static_cast<int>(E), static_cast<int>(topk), scale,
@@ -313,9 +392,15 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
     float *wts = w_out ? reinterpret_cast<float *>(w_out) : m.w;
     const void *lg = reinterpret_cast<const void *>(logits);
     const float *bs = reinterpret_cast<const float *>(bias);
-    VYBDQ_DISPATCH_IN(logits_dt, LDT,
-        hipLaunchKernelGGL((k_moe_route<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg, bs,
-                           static_cast<int>(E), static_cast<int>(topk), scale, idx, wts));
+    if (bs) {
+      VYBDQ_DISPATCH_IN(logits_dt, LDT,
+          hipLaunchKernelGGL((k_moe_route<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg, bs,
+                             static_cast<int>(E), static_cast<int>(topk), scale, idx, wts));
+    } else {
+      VYBDQ_DISPATCH_IN(logits_dt, LDT,
+          hipLaunchKernelGGL((k_moe_route_logit<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg,
+                             static_cast<int>(E), static_cast<int>(topk), scale, idx, wts));
+    }
     int rc = check_launch("moe route");
     if (rc) return rc;
     // few tokens per expert: grouped GEMV (one tile per expert); else the grouped MFMA GEMM
@@ -326,6 +411,7 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
     // become several groups over the same weights that run side by side
     int mc = kMoeGvMC;  // tokens per GEMV group (experts with more rows: several groups)
     if (const char *e = getenv("VYBDQ_MOE_GEMV_MC")) mc = atoi(e) < 1 ? 1 : (atoi(e) > kMoeGvMC ? kMoeGvMC : atoi(e));
+    if (mc > T) mc = static_cast<int>(T);  // no group holds more rows than there are tokens
     // tiles: m-tiles of 16 MT rows for the MFMA GEMM; tiles2: groups of at most mc rows for the GEMV
     const int BMr = 16 * MT;
     hipLaunchKernelGGL(k_moe_bucket_tiles, dim3(1), dim3(256), static_cast<size_t>(2 * E) * 4, s, idx,
@@ -352,19 +438,28 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       ga.row_map = m.row_map;
       ga.groups = m.tiles2;
       ga.ngroups = m.ntiles2;
-      // columns per workgroup: 128, fewer when there are few groups (so the grid covers the CUs)
-      int cus = 256;
-      {
-        int dev = 0;
-        if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-      }
-      auto cols_for = [&](int64_t N, int cpp) {
+      // Up to 4 tokens (groups of one row, but for the shared expert's): equal ranges over a
+      // grid of the workgroups the device holds at once (3-4 tokens: twice that, so that the
+      // dispatcher evens out the shared expert's costlier units); VYBDQ_MOE_GEMV_GRID=
+      // "gate_up,down" workgroups per CU overrides. More tokens: blocks of 128 columns, halved
+      // while the grid would hold under two workgroups per CU (VYBDQ_MOE_GEMV_COLS="gate_up,down"
+      // overrides; -1: equal ranges). Measured on H = 6144, I = 2048, 256 experts, top-8.
+      const int grid_def = T <= 2 ? 0 : -2;
+      int grid_env[2] = {grid_def, grid_def}, cols_env[2] = {0, 0};
+      if (const char *e = getenv("VYBDQ_MOE_GEMV_GRID")) sscanf(e, "%d,%d", &grid_env[0], &grid_env[1]);
+      if (const char *e = getenv("VYBDQ_MOE_GEMV_COLS")) sscanf(e, "%d,%d", &cols_env[0], &cols_env[1]);
+      const int cus = device_cu_count();
+      auto cols_for = [&](int64_t N, int cpp, int forced) {
+        if (forced < 0) return 0;
+        if (forced > 0) return forced;
+        if (T <= 4) return 0;
         int64_t c = 128;
         while (c > cpp && (N / c) * (1 + (E < n ? E : n)) < 2 * cus) c /= 2;
         return static_cast<int>(c);
       };
       ga.N = static_cast<int>(I);
-      ga.cols_per_wg = cols_for(I, 4);
+      ga.cols_per_wg = cols_for(I, moe_gv_cpp(32, true), cols_env[0]);
+      ga.wg_per_cu = grid_env[0];
       ga.Y = m.act;
       ga.ydt = VYBDQ_F16;
       ga.ldy = I;
@@ -385,7 +480,8 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       gd.ldx = I;
       gd.row_map = nullptr;
       gd.N = static_cast<int>(H);
-      gd.cols_per_wg = cols_for(H, 16);
+      gd.cols_per_wg = cols_for(H, moe_gv_cpp(16, false), cols_env[1]);
+      gd.wg_per_cu = grid_env[1];
       gd.Y = m.rows;
       gd.ydt = VYBDQ_F32;
       gd.ldy = H;

@@ -1,14 +1,23 @@
 // Grouped multi-token dequant GEMV for the MoE experts when each expert receives few tokens
 // (decode-sized batches), gfx950.
 //
-// Work unit: (group a, block of output columns). A group is an expert that received tokens (or
-// the shared expert) with its rows [r0, r1) of the bucketed row order; row_map gives each row's
-// token. The workgroup stages the x rows of its (at most MC) tokens into LDS (fp16 + block sums,
-// the layout pair_dot reads) and then walks its weight rows in passes of T/G rows, G lanes per row
-// reading consecutive pairs (one contiguous run of the row per load instruction), with the next
-// passes' pair windows in flight while the current pass computes (a register ring). The bucketing splits experts with
-// more rows into groups of MC rows over the same weights (the kernel would otherwise repeat the
-// walk per chunk of MC tokens).
+// A group is an expert that received tokens (or the shared expert) with its rows [r0, r1) of the
+// bucketed row order; row_map gives each row's token. The bucketing splits experts with more rows
+// into groups of at most MC rows over the same weights, so that no workgroup repeats a walk over
+// the weights per chunk of MC tokens. The work is (group, slice of CPP output columns) units in
+// group-major order, cut in one of two ways:
+//  - single tokens (every group one row, so every unit costs the same): equal contiguous ranges,
+//    one per workgroup of a grid sized to the workgroups the device holds at once, so every
+//    workgroup streams the same number of weight rows (a range can span the end of one group
+//    and the start of the next) and none waits for a second round of the grid;
+//  - several tokens (units cost more in groups with more rows): one block of columns of one
+//    group per workgroup, many more workgroups than the device holds, so the dispatcher evens
+//    out the cost.
+// For each group in its range the workgroup stages the x
+// rows of the group's tokens into LDS (fp16 + block sums, the layout pair_dot reads) and walks
+// its weight rows in passes of 256/G rows, G lanes per row reading consecutive pairs (one
+// contiguous run of the row per load instruction), with the next passes' pair windows in flight
+// while the current pass computes (a register ring).
 //
 // SwiGLU (gate|up): each wave holds gate rows in its first 32 lanes and the up rows of the same
 // output columns in its last 32, so after the DPP row reduction the pair (g, u) is one lane
@@ -32,7 +41,9 @@ struct MoeGvArgs {
   const int4 *groups;      // {expert (-1 shared), r0, r1, -}
   const int *ngroups;
   int N;                   // output columns
-  int cols_per_wg;         // output columns per workgroup
+  int cols_per_wg;         // > 0: one (group, block of this many columns) per workgroup
+  int wg_per_cu;           // cols_per_wg = 0: grid = wg_per_cu x CUs (0: what a CU holds at
+                           // once, -k: k times that)
   void *Y;
   int ydt;                 // F16 or F32
   int64_t ldy;
@@ -42,6 +53,9 @@ struct MoeGvArgs {
 
 constexpr int kMoeGvMC = 4;  // largest x stage
 constexpr int kMoeGvD = 3;   // passes of pair windows in flight per lane (a register ring)
+
+// output columns per pass: 4 waves x (64 / G rows, SwiGLU: half of them gate, half up)
+constexpr int moe_gv_cpp(int G, bool swi) { return 4 * (swi ? 32 / G : 64 / G); }
 
 __device__ __forceinline__ float moe_silu(float g) { return g / (1.0f + __expf(-g)); }
 
@@ -58,23 +72,11 @@ __device__ __forceinline__ void moe_gv_chunk(const MoeGvArgs &a, const uint8_t *
   constexpr int RPW = 64 / G;                 // rows per wave per pass
   constexpr int CPW = SWI ? RPW / 2 : RPW;    // output columns per wave per pass
   static_assert(!SWI || RPW >= 2, "SwiGLU needs a gate and an up row per wave");
-  constexpr int CPP = 4 * CPW;                // columns per pass
+  constexpr int CPP = moe_gv_cpp(G, SWI);     // columns per pass (4 CPW)
   // this lane's column offset within the pass and its matrix
   const bool up = SWI && rs >= RPW / 2;
   const int cslot = w * CPW + (up ? rs - RPW / 2 : rs);
   const uint8_t *Wm = up ? Wu : Wg;
-
-  // x rows of the chunk -> LDS (fp16 pairs + block sums)
-  __syncthreads();  // the previous chunk's readers are done
-  const int nchunk = MC * 8 * P;
-  for (int c = threadIdx.x; c < nchunk; c += T) {
-    const int m = c / (8 * P);
-    const int xr = a.row_map ? a.row_map[r0c + m] : r0c + m;
-    uint32_t r[XW];
-    load_x_chunk<XW>(a.X, static_cast<int64_t>(xr) * a.ldx + 8 * static_cast<int64_t>(c - m * 8 * P), r);
-    stage_chunk<XW>(r, a.xdt, c, lds, sx);
-  }
-  __syncthreads();
 
   const int npairs = ks < P ? (P - ks + G - 1) / G : 0;
   auto pair_ptr = [&](int col, int i) {
@@ -92,6 +94,51 @@ __device__ __forceinline__ void moe_gv_chunk(const MoeGvArgs &a, const uint8_t *
 #pragma unroll
     for (int u = 0; u < U; ++u) load_pair<FMT>(pair_ptr(col, u), d[u]);
   };
+  // Order of the loads: the chunk's token rows, the first NB x chunks of every thread, then the
+  // first passes' weights (which do not depend on x), so the weights are in flight while x is
+  // staged; longer x stages (several tokens, long rows) load the rest afterwards.
+  int xr[MC];
+#pragma unroll
+  for (int m = 0; m < MC; ++m) xr[m] = a.row_map ? a.row_map[r0c + m] : r0c + m;
+  const int cpr = 8 * P;  // 16-byte chunks per x row
+  const int nchunk = MC * cpr;
+  constexpr int NB = 4;
+  auto load_x = [&](int c, uint32_t (&r)[XW]) {
+    const int m = c / cpr;
+    int row = xr[0];
+#pragma unroll
+    for (int mm = 1; mm < MC; ++mm) row = m == mm ? xr[mm] : row;
+    load_x_chunk<XW>(a.X, static_cast<int64_t>(row) * a.ldx + 8 * static_cast<int64_t>(c - m * cpr), r);
+  };
+  // (no branches around these loads: out-of-range chunks and passes re-read the last one)
+  uint32_t r0[NB][XW];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int c = threadIdx.x + b * T;
+    load_x(c < nchunk ? c : nchunk - 1, r0[b]);
+  }
+  uint32_t ring[kMoeGvD][U][PD];
+#pragma unroll
+  for (int j = 0; j < kMoeGvD - 1; ++j) load_pass(j < npass ? j : npass - 1, ring[j]);
+
+  // x rows of the chunk -> LDS (fp16 pairs + block sums)
+  __syncthreads();  // the previous chunk's readers are done
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+    if (threadIdx.x + b * T < nchunk) stage_chunk<XW>(r0[b], a.xdt, threadIdx.x + b * T, lds, sx);
+  for (int c0 = threadIdx.x + NB * T; c0 < nchunk; c0 += NB * T) {
+    uint32_t r[NB][XW];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int c = c0 + b * T;
+      load_x(c < nchunk ? c : nchunk - 1, r[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      if (c0 + b * T < nchunk) stage_chunk<XW>(r[b], a.xdt, c0 + b * T, lds, sx);
+  }
+  __syncthreads();
+
   // pass ps from buffer cur; first pass ps + kMoeGvD - 1 is issued into nxt (the buffer of pass
   // ps - 1, already consumed), so kMoeGvD - 1 passes stay in flight while a pass computes
   auto pass = [&](int ps, uint32_t (&cur)[U][PD], uint32_t (&nxt)[U][PD]) {
@@ -130,10 +177,6 @@ __device__ __forceinline__ void moe_gv_chunk(const MoeGvArgs &a, const uint8_t *
       }
     }
   };
-  uint32_t ring[kMoeGvD][U][PD];
-#pragma unroll
-  for (int j = 0; j < kMoeGvD - 1; ++j)
-    if (j < npass) load_pass(j, ring[j]);
   for (int ps = 0; ps < npass; ps += kMoeGvD) {
 #pragma unroll
     for (int k = 0; k < kMoeGvD; ++k)
@@ -141,51 +184,105 @@ __device__ __forceinline__ void moe_gv_chunk(const MoeGvArgs &a, const uint8_t *
   }
 }
 
-template <int FMT, int G, int U, bool SWI, int XW>
+// MCMAX: the largest group (1 when every group holds one row: a single token).
+template <int FMT, int G, int U, bool SWI, int XW, int MCMAX>
 __global__ void __launch_bounds__(256) k_moe_gemv(MoeGvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int nblk = (a.N + a.cols_per_wg - 1) / a.cols_per_wg;
-  const int g = blockIdx.x / nblk;
-  const int blk = blockIdx.x - g * nblk;
-  if (g >= *a.ngroups) return;
-  const int4 d = a.groups[g];
-  const uint8_t *Wg, *Wu = nullptr;
-  if (d.x < 0) {
-    Wg = a.Ws;
-    Wu = a.W2s;
+  constexpr int CPP = moe_gv_cpp(G, SWI);
+  const int spg = (a.N + CPP - 1) / CPP;  // column slices per group
+  int64_t beg, end;
+  if (a.cols_per_wg > 0) {
+    const int bs = a.cols_per_wg / CPP;  // slices per block
+    const int nblk = (spg + bs - 1) / bs;
+    const int g = blockIdx.x / nblk;
+    if (g >= *a.ngroups) return;
+    beg = static_cast<int64_t>(g) * spg + static_cast<int64_t>(blockIdx.x - g * nblk) * bs;
+    end = beg + bs < static_cast<int64_t>(g + 1) * spg ? beg + bs : static_cast<int64_t>(g + 1) * spg;
   } else {
-    Wg = a.W + static_cast<int64_t>(d.x) * a.w_stride;
-    if constexpr (SWI) Wu = a.W2 + static_cast<int64_t>(d.x) * a.w_stride;
+    const int64_t tot = static_cast<int64_t>(*a.ngroups) * spg;
+    beg = tot * blockIdx.x / gridDim.x;
+    end = tot * (blockIdx.x + 1) / gridDim.x;
   }
-  const int n0 = blk * a.cols_per_wg;
-  const int ncols = a.N - n0 < a.cols_per_wg ? a.N - n0 : a.cols_per_wg;
   char *lds = smem;
   float *sx = reinterpret_cast<float *>(smem + static_cast<size_t>(a.mc) * a.P * XPAIR_STRIDE);
-  for (int r = d.y; r < d.z; r += a.mc) {
-    switch (d.z - r < a.mc ? d.z - r : a.mc) {
-      case 1: moe_gv_chunk<FMT, G, U, 1, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
-      case 2: moe_gv_chunk<FMT, G, U, 2, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
-      case 3: moe_gv_chunk<FMT, G, U, 3, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
-      default: moe_gv_chunk<FMT, G, U, 4, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
+  for (int64_t u = beg; u < end;) {
+    const int g = static_cast<int>(u / spg);
+    const int64_t gb = static_cast<int64_t>(g) * spg;
+    const int n0 = static_cast<int>(u - gb) * CPP;
+    const int s1 = static_cast<int>(end - gb < spg ? end - gb : spg);
+    const int ncols = (s1 * CPP < a.N ? s1 * CPP : a.N) - n0;
+    const int4 d = a.groups[g];
+    const uint8_t *Wg, *Wu = nullptr;
+    if (d.x < 0) {
+      Wg = a.Ws;
+      Wu = a.W2s;
+    } else {
+      Wg = a.W + static_cast<int64_t>(d.x) * a.w_stride;
+      if constexpr (SWI) Wu = a.W2 + static_cast<int64_t>(d.x) * a.w_stride;
     }
+    for (int r = d.y; r < d.z; r += a.mc) {
+      if constexpr (MCMAX == 1) {
+        moe_gv_chunk<FMT, G, U, 1, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx);
+      } else {
+        switch (d.z - r < a.mc ? d.z - r : a.mc) {
+          case 1: moe_gv_chunk<FMT, G, U, 1, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
+          case 2: moe_gv_chunk<FMT, G, U, 2, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
+          case 3: moe_gv_chunk<FMT, G, U, 3, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
+          default: moe_gv_chunk<FMT, G, U, 4, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
+        }
+      }
+    }
+    u = gb + spg;
   }
 }
 
-template <int FMT, int G, int U, bool SWI, int XW>
-int moe_gemv_launch1(const MoeGvArgs &a, int max_groups, hipStream_t s) {
+template <int FMT, int G, int U, bool SWI, int XW, int MCMAX>
+int moe_gemv_launch2(const MoeGvArgs &a, int max_groups, hipStream_t s) {
+  const void *fn = reinterpret_cast<const void *>(&k_moe_gemv<FMT, G, U, SWI, XW, MCMAX>);
   const size_t lds = static_cast<size_t>(a.mc) * a.P * (XPAIR_STRIDE + 2 * 4);
   if (lds > 64 * 1024) {
     static bool raised = false;  // one attribute call per instantiation
     if (!raised) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_moe_gemv<FMT, G, U, SWI, XW>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
       if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("moe gemv: LDS attribute: ") + hipGetErrorString(e));
       raised = true;
     }
   }
-  const int nblk = (a.N + a.cols_per_wg - 1) / a.cols_per_wg;
-  hipLaunchKernelGGL((k_moe_gemv<FMT, G, U, SWI, XW>), dim3(static_cast<unsigned>(max_groups * nblk)), dim3(256), lds, s, a);
+  constexpr int CPP = moe_gv_cpp(G, SWI);
+  const int spg = (a.N + CPP - 1) / CPP;
+  if (a.cols_per_wg > 0) {
+    if (a.cols_per_wg % CPP) return set_error(VYBDQ_ERR_SHAPE, "moe gemv: columns per workgroup not a multiple of the pass");
+    const int bs = a.cols_per_wg / CPP;
+    const int64_t grid = static_cast<int64_t>(max_groups) * ((spg + bs - 1) / bs);
+    hipLaunchKernelGGL((k_moe_gemv<FMT, G, U, SWI, XW, MCMAX>), dim3(static_cast<unsigned>(grid)), dim3(256), lds, s, a);
+    return check_launch("moe grouped gemv");
+  }
+  int per_cu = a.wg_per_cu;
+  if (per_cu <= 0) {
+    const int mult = per_cu < 0 ? -per_cu : 1;
+    // resident workgroups per CU for this LDS size (the last query per instantiation is kept)
+    static size_t q_lds = ~size_t(0);
+    static int q_nb = 0;
+    if (q_lds != lds) {
+      int nb = 0;
+      const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, 256, lds);
+      if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("moe gemv: occupancy: ") + hipGetErrorString(e));
+      q_nb = nb < 1 ? 1 : nb;
+      q_lds = lds;
+    }
+    per_cu = q_nb * mult;
+  }
+  const int64_t units = static_cast<int64_t>(max_groups) * spg;
+  int64_t grid = static_cast<int64_t>(per_cu) * device_cu_count();
+  grid = grid < units ? grid : units;
+  hipLaunchKernelGGL((k_moe_gemv<FMT, G, U, SWI, XW, MCMAX>), dim3(static_cast<unsigned>(grid)), dim3(256), lds, s, a);
   return check_launch("moe grouped gemv");
+}
+
+template <int FMT, int G, int U, bool SWI, int XW>
+int moe_gemv_launch1(const MoeGvArgs &a, int max_groups, hipStream_t s) {
+  return a.mc == 1 ? moe_gemv_launch2<FMT, G, U, SWI, XW, 1>(a, max_groups, s)
+                   : moe_gemv_launch2<FMT, G, U, SWI, XW, kMoeGvMC>(a, max_groups, s);
 }
 
 // gate|up (swi): 32 lanes per row; down: 16. The pair batch covers a row's pairs per lane (at
