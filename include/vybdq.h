@@ -140,7 +140,9 @@ int64_t vybdq_exl3_workspace_size(int64_t B, int64_t K, int64_t N);
    (FWHT(X * suh)/sqrt128 per 128 chunk), the trellis is decoded in registers and multiplied
    (f32 accumulation), and the result rotated back (FWHT(.)/sqrt128 * svh). 1 <= B <= 16,
    K, N % 128 == 0, trellis 16-byte aligned, ws 256-byte aligned of at least
-   vybdq_exl3_workspace_size bytes. The reference has no fused EXL3 GEMM (it dequantizes each
+   vybdq_exl3_workspace_size bytes, zero-filled once before the first call (it holds arrival
+   counters that every completed call leaves at zero; calls sharing a workspace must not run
+   concurrently). One kernel launch for B <= 2, three above. The reference has no fused EXL3 GEMM (it dequantizes each
    expert to f64/f32 then runs gemm, glm_engine.vyb:2845-2923). */
 int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t X, uint64_t Y, int64_t B,
                     int64_t K, int64_t N, int codebook, int x_dt, int y_dt, uint64_t ws, int64_t ws_bytes,

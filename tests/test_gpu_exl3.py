@@ -82,6 +82,55 @@ def test_exl3_gemm_config4_shape(dev):
     assert matmul.rel_maxnorm(y[:, cols], ref) < matmul.TOL
 
 
+@pytest.mark.parametrize("K,N", [(128, 256), (1152, 256), (2048, 384)])
+def test_exl3_gemm_splits_and_reuse(dev, K, N):
+    """One workspace across calls of several batch sizes and dtypes (the per-block arrival
+    counters must come back to zero after every call): a single k-split (K = 128), a ragged last
+    split (K = 1152: 72 k-blocks in splits of 16), repeated calls bit-identical."""
+    rng = np.random.default_rng(K + N)
+    t, suh, svh = synth.exl3_tensors(rng, K, N)
+    lin = ops.Exl3Linear(dev_t(t, dev), dev_t(suh, dev), dev_t(svh, dev), K, N)
+    w = exl3.dequant_exl3_f64(t, suh, svh)
+    first = {}
+    for B, xdt, ydt in [(16, torch.bfloat16, torch.float32), (1, torch.float32, torch.float16), (5, torch.float16, torch.bfloat16),
+                        (2, torch.float16, torch.float32), (16, torch.bfloat16, torch.float32), (1, torch.float32, torch.float16)]:
+        x = torch.from_numpy(np.random.default_rng(B).standard_normal((B, K)).astype(np.float32)).to(xdt)
+        y = lin(x.to(dev), ydt).to(torch.float64).cpu().numpy()
+        ref = x.to(torch.float64).numpy() @ w
+        tol = matmul.TOL if ydt == torch.float32 else 8e-3
+        assert matmul.rel_maxnorm(y, ref) < tol, (B, xdt, ydt)
+        key = (B, xdt, ydt)
+        if key in first:
+            np.testing.assert_array_equal(y, first[key])
+        first[key] = y
+
+
+def test_exl3_gemm_graph_replays(dev):
+    """Captured once, replayed with other work between the replays: every replay matches eager."""
+    rng = np.random.default_rng(7)
+    K, N = 1024, 512
+    t, suh, svh = synth.exl3_tensors(rng, K, N)
+    lin = ops.Exl3Linear(dev_t(t, dev), dev_t(suh, dev), dev_t(svh, dev), K, N)
+    x = dev_t(rng.standard_normal((3, K)).astype(np.float16), dev)
+    out = torch.empty((3, N), dtype=torch.float32, device=dev)
+    eager = lin(x).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        lin(x, out=out)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        lin(x, out=out)
+    for i in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        lin(x)  # eager call between replays on the same workspace
+        torch.cuda.synchronize()
+
+
 def test_exl3_workspace_errors(dev):
     assert _lib.lib.vybdq_exl3_workspace_size(17, 128, 128) == -1
     assert _lib.lib.vybdq_exl3_workspace_size(1, 100, 128) == -1

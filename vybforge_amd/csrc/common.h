@@ -45,6 +45,17 @@ inline bool dt_valid_in(int dt) { return dt == VYBDQ_F32 || dt == VYBDQ_F16 || d
 inline bool dt_valid_out(int dt) { return dt_valid_in(dt) || dt == VYBDQ_F64; }
 inline int dt_size(int dt) { return dt == VYBDQ_F64 ? 8 : dt == VYBDQ_F32 ? 4 : 2; }
 
+// ---- device: DPP lane permutations (update_dpp controls) -------------------------------
+
+constexpr int DPP_QUAD_XOR1 = 0xB1;     // quad_perm [1, 0, 3, 2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;     // quad_perm [2, 3, 0, 1]
+constexpr int DPP_ROW_MIRROR = 0x140;   // lane i <- lane 15 - i of its row
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane i <- lane 7 - i of its half-row
+constexpr int DPP_BCAST15 = 0x142;      // row r <- lane 15 of row r - 1
+constexpr int DPP_BCAST31 = 0x143;      // rows 2, 3 <- lane 31
+constexpr int DPP_ROW_SHL = 0x100;     // + n: lane i <- lane i + n of its row (n = 1..15)
+constexpr int DPP_ROW_SHR = 0x110;     // + n: lane i <- lane i - n of its row
+
 // ---- device: element load/store -------------------------------------------------------
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {

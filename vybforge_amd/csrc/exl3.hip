@@ -121,18 +121,43 @@ __global__ void __launch_bounds__(256) k_exl3_decode(const uint16_t *__restrict_
 
 // ---- 128-point FWHT across a wave (2 elements per lane) -------------------------------------
 
+// The value of lane ^ M. M = 1, 2: a quad permutation; M = 4, 8: a row shift each way, picked by
+// the lane's bit M (both on the VALU); M = 16, 32: ds_bpermute.
+template <int M>
+__device__ __forceinline__ float xor_lane(float v, bool upper) {
+  const int b = __builtin_bit_cast(int, v);
+  if constexpr (M == 1) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, DPP_QUAD_XOR1, 0xf, 0xf, false));
+  } else if constexpr (M == 2) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, DPP_QUAD_XOR2, 0xf, 0xf, false));
+  } else if constexpr (M == 4 || M == 8) {
+    const int hi = __builtin_amdgcn_update_dpp(0, b, DPP_ROW_SHL + M, 0xf, 0xf, false);  // lane + M
+    const int lo = __builtin_amdgcn_update_dpp(0, b, DPP_ROW_SHR + M, 0xf, 0xf, false);  // lane - M
+    return __builtin_bit_cast(float, upper ? lo : hi);
+  } else {
+    return __shfl_xor(v, M, 64);
+  }
+}
+
+template <int M>
+__device__ __forceinline__ void fwht_stage(float &a0, float &a1, int lane) {
+  const bool upper = (lane & M) != 0;
+  const float p0 = xor_lane<M>(a0, upper), p1 = xor_lane<M>(a1, upper);
+  a0 = upper ? p0 - a0 : a0 + p0;
+  a1 = upper ? p1 - a1 : a1 + p1;
+}
+
 __device__ __forceinline__ void fwht128_wave(float &a0, float &a1) {
   const int lane = threadIdx.x & 63;
   float t0 = a0 + a1, t1 = a0 - a1;
   a0 = t0;
   a1 = t1;
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const float p0 = __shfl_xor(a0, m, 64), p1 = __shfl_xor(a1, m, 64);
-    const bool upper = (lane & m) != 0;
-    a0 = upper ? p0 - a0 : a0 + p0;
-    a1 = upper ? p1 - a1 : a1 + p1;
-  }
+  fwht_stage<1>(a0, a1, lane);
+  fwht_stage<2>(a0, a1, lane);
+  fwht_stage<4>(a0, a1, lane);
+  fwht_stage<8>(a0, a1, lane);
+  fwht_stage<16>(a0, a1, lane);
+  fwht_stage<32>(a0, a1, lane);
 }
 
 // ---- full dequant: W [K, N] = diag(suh) Hs What Hs diag(svh) -------------------------------
@@ -180,7 +205,21 @@ __global__ void __launch_bounds__(256) k_exl3_dequant(const uint16_t *__restrict
 }
 
 // ---- fused GEMM ------------------------------------------------------------------------------
-// 1. x' [BP][K] fp16 = FWHT(x * suh) / sqrt(128) per 128 chunk (rows b >= B are zero)
+// grid (N/128 column blocks, S k-splits), 4 waves per workgroup; a split's k-range is whole 128
+// chunks.
+// 1. x' [BP][k-range] = FWHT(x * suh) / sqrt(128) per 128 chunk. Batch <= 2: computed by the
+//    GEMM workgroup itself for its k-range, in LDS; larger batches: by k_exl3_xprep into the
+//    workspace (a workgroup would otherwise rotate BP chunks per wave before its first weight).
+// 2. z[b][n] over the split's k-range = sum x'[b][k] What[k][n]: each wave a quarter of the
+//    k-range on the block's 128 columns, the waves' partials summed in LDS in a fixed order.
+// 3. y[b][n] = svh[n] * FWHT(sum_s z_s[b][.]) / sqrt(128), sums in split order. Batch <= 2: the
+//    last split of a column block to arrive (a per-block arrival counter, reset by that last
+//    arrival so the counters stay zero between calls) does it; larger batches: k_exl3_out.
+//    The single-launch form publishes the partials with device-coherent stores (written
+//    through the XCD's L2) that have completed (s_waitcnt vmcnt(0)) before the arrival is
+//    counted, and the last arrival reads them with device-coherent loads issued after the
+//    count has returned. An agent-scope release/acquire pair around the count would instead
+//    write back and invalidate whole L2s: measured 17 us more per call at batch 1.
 
 template <int XDT>
 __global__ void __launch_bounds__(64) k_exl3_xprep(const void *__restrict__ X, const _Float16 *__restrict__ suh,
@@ -197,16 +236,16 @@ __global__ void __launch_bounds__(64) k_exl3_xprep(const void *__restrict__ X, c
   xp[b * K + k0 + 1] = static_cast<_Float16>(a1 * kRScale);
 }
 
-// 2. zpart[s][b][n] = sum over the k-range of split s of x'[b][k] What[k][n]
-//    grid (N/128, S): workgroup = 4 waves on one 128-column block, each wave a quarter of the
-//    split's k-range; the waves' partials are summed in LDS in a fixed order.
-
 template <int CB, int BP>
-__global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ trellis,
-                                                   const _Float16 *__restrict__ xp, float *__restrict__ zpart,
-                                                   int64_t K, int NB, int kb_per_split) {
+__global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ trellis, const void *__restrict__ X,
+                                                   int xdt, const _Float16 *__restrict__ suh,
+                                                   const _Float16 *__restrict__ svh, void *__restrict__ Y, int ydt,
+                                                   int B, const _Float16 *__restrict__ xp, float *__restrict__ zpart,
+                                                   uint32_t *__restrict__ arrivals, int64_t K, int NB,
+                                                   int kb_per_split) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int g = blockIdx.x, s = blockIdx.y;
+  __shared__ int is_last;
+  const int g = blockIdx.x, s = blockIdx.y, S = gridDim.y;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = lane >> 3, j = lane & 7;
   const int KB = static_cast<int>(K / 16);
@@ -218,26 +257,43 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   // and the pairing of decoded values; x' is staged duplicated for that. Larger batches round
   // the value to fp16 once and share it across the batch rows.
   constexpr bool HALVES = BP <= 2;
-  // stage x' rows of this split: [BP][16 * nkb] fp16 (HALVES: fp16 pairs (x, x))
-  _Float16 *xs = reinterpret_cast<_Float16 *>(smem);
+  constexpr bool FUSED = BP <= 2;  // x rotation and output rotation in this launch
+  // 1. x' rows of this split: [BP][16 * nkb] fp16 (HALVES: u32 pairs (x, x))
   const int rows = 16 * nkb;
-  if constexpr (HALVES) {
-    uint32_t *xd = reinterpret_cast<uint32_t *>(smem);
-    for (int i = threadIdx.x; i < BP * rows / 2; i += blockDim.x) {
-      const int b = i / (rows / 2), c = i % (rows / 2);
-      const uint32_t v = *reinterpret_cast<const uint32_t *>(xp + b * K + 16 * static_cast<int64_t>(kb_begin) + 2 * c);
-      *reinterpret_cast<u2 *>(xd + b * rows + 2 * c) =
-          u2{__builtin_amdgcn_perm(v, v, 0x01000100u), __builtin_amdgcn_perm(v, v, 0x03020302u)};
-    }
-  } else {
+  const int nch = nkb / 8;
+  if constexpr (!FUSED) {
     for (int i = threadIdx.x; i < BP * rows / 8; i += blockDim.x) {
       const int b = i / (rows / 8), c = i % (rows / 8);
-      *reinterpret_cast<u4 *>(xs + b * rows + 8 * c) =
+      *reinterpret_cast<u4 *>(reinterpret_cast<_Float16 *>(smem) + b * rows + 8 * c) =
           *reinterpret_cast<const u4 *>(xp + b * K + 16 * static_cast<int64_t>(kb_begin) + 8 * c);
     }
   }
+  for (int cb = wave; FUSED && cb < BP * nch; cb += 4) {  // one 128 chunk per wave at a time
+    const int b = cb / nch, c = cb - b * nch;
+    const int r = 128 * c + 2 * lane;
+    const int64_t k = 16 * static_cast<int64_t>(kb_begin) + r;
+    float a0 = 0.f, a1 = 0.f;
+    if (b < B) {
+      const int64_t i = b * K + k;
+      if (xdt == VYBDQ_F32) { a0 = load_elem<VYBDQ_F32>(X, i); a1 = load_elem<VYBDQ_F32>(X, i + 1); }
+      else if (xdt == VYBDQ_F16) { a0 = load_elem<VYBDQ_F16>(X, i); a1 = load_elem<VYBDQ_F16>(X, i + 1); }
+      else { a0 = load_elem<VYBDQ_BF16>(X, i); a1 = load_elem<VYBDQ_BF16>(X, i + 1); }
+      a0 *= static_cast<float>(suh[k]);
+      a1 *= static_cast<float>(suh[k + 1]);
+    }
+    fwht128_wave(a0, a1);
+    const uint32_t h0 = __builtin_bit_cast(uint16_t, static_cast<_Float16>(a0 * kRScale));
+    const uint32_t h1 = __builtin_bit_cast(uint16_t, static_cast<_Float16>(a1 * kRScale));
+    if constexpr (HALVES) {
+      *reinterpret_cast<u2 *>(reinterpret_cast<uint32_t *>(smem) + b * rows + r) = u2{h0 | (h0 << 16), h1 | (h1 << 16)};
+    } else {
+      *reinterpret_cast<uint32_t *>(reinterpret_cast<_Float16 *>(smem) + b * rows + r) = h0 | (h1 << 16);
+    }
+  }
   __syncthreads();
+  const _Float16 *xs = reinterpret_cast<const _Float16 *>(smem);
 
+  // 2. this split's partial
   float acc[BP][2];
 #pragma unroll
   for (int b = 0; b < BP; ++b) acc[b][0] = acc[b][1] = 0.f;
@@ -295,15 +351,45 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   }
   __syncthreads();
   const int64_t N = static_cast<int64_t>(NB) * 16;
-  for (int i = threadIdx.x; i < BP * 128; i += blockDim.x) {
+  auto zp = [&](int split, int b, int c) {
+    return reinterpret_cast<uint32_t *>(zpart) + (static_cast<int64_t>(split) * BP + b) * N + 128 * static_cast<int64_t>(g) + c;
+  };
+  for (int i = threadIdx.x; i < B * 128; i += blockDim.x) {
     const int b = i / 128, c = i % 128;
     const float z = ((red[(0 * BP + b) * 128 + c] + red[(1 * BP + b) * 128 + c]) +
                      red[(2 * BP + b) * 128 + c]) + red[(3 * BP + b) * 128 + c];
-    zpart[(static_cast<int64_t>(s) * BP + b) * N + 128 * static_cast<int64_t>(g) + c] = z;
+    if constexpr (FUSED) __hip_atomic_store(zp(s, b, c), __float_as_uint(z), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *zp(s, b, c) = __float_as_uint(z);
+  }
+  if constexpr (!FUSED) return;
+
+  // 3. arrival; the last split of the block applies the output rotation
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partials are performed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(arrivals + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = old == static_cast<uint32_t>(S - 1);
+    if (is_last) __hip_atomic_store(arrivals + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  for (int b = wave; b < B; b += 4) {
+    float a0 = 0.f, a1 = 0.f;
+    for (int sp = 0; sp < S; ++sp) {
+      a0 += __uint_as_float(__hip_atomic_load(zp(sp, b, 2 * lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      a1 += __uint_as_float(__hip_atomic_load(zp(sp, b, 2 * lane + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    }
+    fwht128_wave(a0, a1);
+    const int64_t n0 = 128 * static_cast<int64_t>(g) + 2 * lane;
+    const float y0 = a0 * kRScale * static_cast<float>(svh[n0]);
+    const float y1 = a1 * kRScale * static_cast<float>(svh[n0 + 1]);
+    if (ydt == VYBDQ_F32) { store_elem<VYBDQ_F32>(Y, nullptr, b * N + n0, y0); store_elem<VYBDQ_F32>(Y, nullptr, b * N + n0 + 1, y1); }
+    else if (ydt == VYBDQ_F16) { store_elem<VYBDQ_F16>(Y, nullptr, b * N + n0, y0); store_elem<VYBDQ_F16>(Y, nullptr, b * N + n0 + 1, y1); }
+    else { store_elem<VYBDQ_BF16>(Y, nullptr, b * N + n0, y0); store_elem<VYBDQ_BF16>(Y, nullptr, b * N + n0 + 1, y1); }
   }
 }
 
-// 3. y[b][n] = svh[n] * FWHT(sum_s zpart[s][b][.]) / sqrt(128)
+// 3. (batch > 2) y[b][n] = svh[n] * FWHT(sum_s zpart[s][b][.]) / sqrt(128)
 
 template <int YDT>
 __global__ void __launch_bounds__(64) k_exl3_out(const float *__restrict__ zpart, const _Float16 *__restrict__ svh,
@@ -324,22 +410,32 @@ __global__ void __launch_bounds__(64) k_exl3_out(const float *__restrict__ zpart
 
 static int exl3_bp(int64_t B) { return B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : B <= 8 ? 8 : 16; }
 
-// K-splits: enough workgroups to fill the chip, bounded so partials stay small
-static int exl3_splits(int64_t K, int64_t N, int BP) {
+// K-splits: enough workgroups to fill the chip, bounded so partials stay small; a split's
+// k-range is whole 128 chunks (the x rotation is done per chunk inside the GEMM)
+struct Exl3Split {
+  int S;    // splits
+  int kbs;  // 16-row k-blocks per split (a multiple of 8)
+};
+static Exl3Split exl3_splits(int64_t K, int64_t N, int BP) {
   const int KB = static_cast<int>(K / 16);
   const int64_t groups = N / 128;
   int S = static_cast<int>((1024 + groups - 1) / groups);
   const int smax = BP >= 8 ? 4 : 8;
   if (S > smax) S = smax;
   if (S > KB / 4) S = KB / 4 > 0 ? KB / 4 : 1;
-  return S < 1 ? 1 : S;
+  if (S < 1) S = 1;
+  int kbs = (KB + S - 1) / S;
+  kbs = (kbs + 7) / 8 * 8;
+  return {(KB + kbs - 1) / kbs, kbs};
 }
+
+// workspace: per-column-block arrival counters (zero between calls), x' (batch > 2), partials
+static int64_t exl3_arrival_bytes(int64_t N) { return ((N / 128 * 4 + 255) / 256) * 256; }
+static int64_t exl3_xp_bytes(int BP, int64_t K) { return BP <= 2 ? 0 : ((BP * K * 2 + 255) / 256) * 256; }
 
 static int64_t exl3_ws_bytes(int64_t B, int64_t K, int64_t N) {
   const int BP = exl3_bp(B);
-  const int S = exl3_splits(K, N, BP);
-  const int64_t xp = ((BP * K * 2 + 255) / 256) * 256;
-  return xp + static_cast<int64_t>(S) * BP * N * 4;
+  return exl3_arrival_bytes(N) + exl3_xp_bytes(BP, K) + static_cast<int64_t>(exl3_splits(K, N, BP).S) * BP * N * 4;
 }
 
 }  // namespace vybdq
@@ -419,13 +515,14 @@ extern "C" int64_t vybdq_exl3_workspace_size(int64_t B, int64_t K, int64_t N) {
 }
 
 template <int CB, int BP>
-static void exl3_gemm_launch(const uint16_t *t, const _Float16 *xp, float *zp, int64_t K, int NB, int S, int kbs,
-                             hipStream_t s) {
-  const size_t xs_bytes = static_cast<size_t>(BP) * 16 * kbs * (BP <= 2 ? 4 : 2);
+static void exl3_gemm_launch(const uint16_t *t, const void *X, int xdt, const _Float16 *su, const _Float16 *sv,
+                             void *Y, int ydt, int B, const _Float16 *xp, float *zp, uint32_t *arr, int64_t K,
+                             int NB, const Exl3Split &sp, hipStream_t s) {
+  const size_t xs_bytes = static_cast<size_t>(BP) * 16 * sp.kbs * (BP <= 2 ? 4 : 2);
   const size_t red_bytes = static_cast<size_t>(4) * BP * 128 * 4;
   const size_t lds = xs_bytes > red_bytes ? xs_bytes : red_bytes;
-  hipLaunchKernelGGL((k_exl3_gemm<CB, BP>), dim3(static_cast<unsigned>(NB / 8), static_cast<unsigned>(S)), dim3(256),
-                     lds, s, t, xp, zp, K, NB, kbs);
+  hipLaunchKernelGGL((k_exl3_gemm<CB, BP>), dim3(static_cast<unsigned>(NB / 8), static_cast<unsigned>(sp.S)),
+                     dim3(256), lds, s, t, X, xdt, su, sv, Y, ydt, B, xp, zp, arr, K, NB, sp.kbs);
 }
 
 extern "C" int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t X, uint64_t Y, int64_t B,
@@ -442,33 +539,35 @@ extern "C" int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uin
   VYBDQ_REQUIRE(ws_bytes >= exl3_ws_bytes(B, K, N), VYBDQ_ERR_WORKSPACE,
                 "workspace smaller than vybdq_exl3_workspace_size");
   const int BP = exl3_bp(B);
-  const int S = exl3_splits(K, N, BP);
-  const int KB = static_cast<int>(K / 16);
-  const int kbs = (KB + S - 1) / S;
+  const Exl3Split sp = exl3_splits(K, N, BP);
   const int NB = static_cast<int>(N / 16);
   hipStream_t s = as_stream(stream);
-  auto *xp = reinterpret_cast<_Float16 *>(ws);
-  auto *zp = reinterpret_cast<float *>(ws + ((BP * K * 2 + 255) / 256) * 256);
+  auto *arr = reinterpret_cast<uint32_t *>(ws);
+  auto *xp = reinterpret_cast<_Float16 *>(ws + exl3_arrival_bytes(N));
+  auto *zp = reinterpret_cast<float *>(ws + exl3_arrival_bytes(N) + exl3_xp_bytes(BP, K));
   const auto *su = reinterpret_cast<const _Float16 *>(suh);
   const auto *sv = reinterpret_cast<const _Float16 *>(svh);
   const auto *t = reinterpret_cast<const uint16_t *>(trellis);
-  const dim3 gx(static_cast<unsigned>(K / 128), static_cast<unsigned>(BP));
-  VYBDQ_DISPATCH_IN(x_dt, XDT,
-      hipLaunchKernelGGL((k_exl3_xprep<XDT>), gx, dim3(64), 0, s, reinterpret_cast<const void *>(X), su, xp,
-                         static_cast<int>(B), K));
-#define G(CB)                                                                                   \
-  switch (BP) {                                                                                 \
-    case 1: exl3_gemm_launch<CB, 1>(t, xp, zp, K, NB, S, kbs, s); break;                       \
-    case 2: exl3_gemm_launch<CB, 2>(t, xp, zp, K, NB, S, kbs, s); break;                       \
-    case 4: exl3_gemm_launch<CB, 4>(t, xp, zp, K, NB, S, kbs, s); break;                       \
-    case 8: exl3_gemm_launch<CB, 8>(t, xp, zp, K, NB, S, kbs, s); break;                       \
-    default: exl3_gemm_launch<CB, 16>(t, xp, zp, K, NB, S, kbs, s); break;                     \
+  const void *x = reinterpret_cast<const void *>(X);
+  void *y = reinterpret_cast<void *>(Y);
+  const int b = static_cast<int>(B);
+  if (BP > 2) {
+    const dim3 gx(static_cast<unsigned>(K / 128), static_cast<unsigned>(BP));
+    VYBDQ_DISPATCH_IN(x_dt, XDT, hipLaunchKernelGGL((k_exl3_xprep<XDT>), gx, dim3(64), 0, s, x, su, xp, b, K));
+  }
+#define G(CB)                                                                                         \
+  switch (BP) {                                                                                       \
+    case 1: exl3_gemm_launch<CB, 1>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;   \
+    case 2: exl3_gemm_launch<CB, 2>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;   \
+    case 4: exl3_gemm_launch<CB, 4>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;   \
+    case 8: exl3_gemm_launch<CB, 8>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;   \
+    default: exl3_gemm_launch<CB, 16>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break; \
   }
   if (codebook == VYBDQ_EXL3_MCG) { G(VYBDQ_EXL3_MCG) } else { G(VYBDQ_EXL3_3INST) }
 #undef G
-  const dim3 go(static_cast<unsigned>(N / 128), static_cast<unsigned>(B));
-  void *y = reinterpret_cast<void *>(Y);
-  VYBDQ_DISPATCH_IN(y_dt, YDT,
-      hipLaunchKernelGGL((k_exl3_out<YDT>), go, dim3(64), 0, s, zp, sv, y, BP, S, N));
+  if (BP > 2) {
+    const dim3 go(static_cast<unsigned>(N / 128), static_cast<unsigned>(B));
+    VYBDQ_DISPATCH_IN(y_dt, YDT, hipLaunchKernelGGL((k_exl3_out<YDT>), go, dim3(64), 0, s, zp, sv, y, BP, sp.S, N));
+  }
   return check_launch("vybdq_exl3_gemm");
 }

@@ -83,12 +83,6 @@ __device__ __forceinline__ float dpp_add(float v) {
   const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xf, false);
   return v + __builtin_bit_cast(float, t);
 }
-constexpr int DPP_QUAD_XOR1 = 0xB1;     // quad_perm [1, 0, 3, 2]
-constexpr int DPP_QUAD_XOR2 = 0x4E;     // quad_perm [2, 3, 0, 1]
-constexpr int DPP_ROW_MIRROR = 0x140;   // lane i <- lane 15 - i of its row
-constexpr int DPP_HALF_MIRROR = 0x141;  // lane i <- lane 7 - i of its half-row
-constexpr int DPP_BCAST15 = 0x142;      // row r <- lane 15 of row r - 1
-constexpr int DPP_BCAST31 = 0x143;      // rows 2, 3 <- lane 31
 
 // Sum over each aligned group of G consecutive lanes (G = 8, 16, 32 or 64). After the quad swaps
 // and the mirrors every lane of a 16-lane row holds its row's (or half-row's) sum; the

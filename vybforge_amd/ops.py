@@ -193,7 +193,8 @@ class Exl3Linear:
         nbytes = max(_lib.lib.vybdq_exl3_workspace_size(b, K, N) for b in (1, 2, 4, 8, max_batch))
         if nbytes < 0:
             raise ValueError("unsupported EXL3 shape")
-        self.ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=trellis.device)
+        # zero-filled once: the arrival counters at its start must be zero (each call leaves them so)
+        self.ws = torch.zeros(nbytes + 256, dtype=torch.uint8, device=trellis.device)
         self.ws_ptr = (self.ws.data_ptr() + 255) // 256 * 256
         self.ws_bytes = nbytes
 
