@@ -287,7 +287,8 @@ def run_exl3(args, torch, dev):
     flops = 2 * K * N * B
     roofline = dict(bound="hbm", achieved=round(value, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=round(value / HBM_PEAK_GBS, 4), traffic=None,
-                    kernel="exl3 gemm (xprep + k_exl3_gemm + out; VALU-bound decode)",
+                    kernel=("k_exl3_gemm, one launch with the x and output rotations" if B <= 2 else
+                            "k_exl3_xprep + k_exl3_gemm + k_exl3_out") + " (VALU-bound trellis decode)",
                     avg_launch_us=round(per * 1e3, 3), bytes_per_launch=bytes_call)
     return dict(value=value, ms_step=ms, wall=wall, roofline=roofline, flops=flops * ncopy,
                 workload=f"EXL3 4-bpw mcg GEMM K=5120 N=17408 batch {B} (8 rotated trellis copies)",
@@ -403,7 +404,8 @@ def run_moe(args, torch, dev):
     gbs = nbytes / (ms * 1e-3) / 1e9
     roofline = dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None,
-                    kernel="MoE layer (route, bucket, grouped k_dq_gemm gate|up+SwiGLU, down, shared, combine)",
+                    kernel=f"MoE layer: route, bucket, {'k_moe_gemv' if T <= 64 else 'k_moe_mm'} gate|up+SwiGLU "
+                           "and down over the routed and shared experts, combine",
                     avg_launch_us=round(ms * 1e3, 3), bytes_per_launch=nbytes)
     return dict(value=gbs, ms_step=ms, wall=wall, roofline=roofline, flops=flops,
                 workload=f"GLM-5-style MoE layer T={T}: H=6144, 256+1 experts, top-8, I=2048, q4_0 "
