@@ -35,7 +35,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="stack",
-                    choices=["stack", "stack_chain", "gemv1", "exl3", "prefill", "prefill_i8", "moe", "copy"])
+                    choices=["stack", "stack_chain", "gemv1", "kquant", "exl3", "prefill", "prefill_i8", "moe", "copy"])
+    ap.add_argument("--wtype", type=int, default=12, choices=[12, 13, 14],
+                    help="GGML type id for --config kquant (12 Q4_K, 13 Q5_K, 14 Q6_K)")
     ap.add_argument("--tokens", type=int, default=16, help="tokens for --config moe")
     ap.add_argument("--batch", type=int, default=1, help="batch for --config exl3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -50,6 +52,18 @@ def q4_0_blocks_gpu(torch, gen, N, K, dev):
     d = (torch.randn(nb, generator=gen, device=dev) * 0.01).abs().to(torch.float16)
     blk[:, 0:2] = d.view(torch.uint8).view(nb, 2)
     blk[:, 2:] = torch.randint(0, 256, (nb, 16), generator=gen, device=dev, dtype=torch.uint8)
+    return blk.view(-1)
+
+
+def kquant_blocks_gpu(torch, gen, ty, N, K, dev):
+    """Seeded packed Q4_K / Q5_K / Q6_K rows on the device: uniform random bytes, the fp16
+    scale fields = |N(0, 1e-4)|."""
+    sbytes = {12: 144, 13: 176, 14: 210}[ty]
+    nb = N * (K // 256)
+    blk = torch.randint(0, 256, (nb, sbytes), generator=gen, device=dev, dtype=torch.uint8)
+    for off in ((0, 2) if ty in (12, 13) else (208,)):
+        d = (torch.randn(nb, generator=gen, device=dev) * 1e-4).abs().to(torch.float16)
+        blk[:, off:off + 2] = d.view(torch.uint8).view(nb, 2)
     return blk.view(-1)
 
 
@@ -240,6 +254,30 @@ def run_gemv1(args, torch, dev):
     return dict(value=value, ms_step=per * len(launch), wall=wall, roofline=roofline,
                 flops=2 * N * K * len(launch), workload="q4_0 GEMV 9728x2560 fp32 x (24 rotated copies)",
                 bytes_per_step=bytes_call * len(launch), launches_per_step=len(launch))
+
+
+def run_kquant(args, torch, dev):
+    """K-quant GEMV at the Qwen3-4B MLP shape 9728x2560 (fp16 x, f32 y), 24 rotated weight copies
+    (> the 256 MB MALL), one GEMV per copy in one graph."""
+    from vybforge_amd import ops
+    N, K, ty = 9728, 2560, args.wtype
+    name = {12: "Q4_K", 13: "Q5_K", 14: "Q6_K"}[ty]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    copies = [kquant_blocks_gpu(torch, gen, ty, N, K, dev) for _ in range(24)]
+    x = torch.randn(K, generator=gen, device=dev).to(torch.float16)
+    y = torch.empty(1, N, device=dev)
+    ms, wall = timed_graph(torch, [lambda W=W: ops.gemv(ty, W, x, N, K, out=y) for W in copies], args.steps,
+                           args.warmup)
+    per = ms / len(copies)
+    bytes_call = ops.row_bytes(ty, K) * N + 2 * K + 4 * N
+    value = bytes_call / (per * 1e-3) / 1e9
+    roofline = dict(bound="hbm", achieved=round(value, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(value / HBM_PEAK_GBS, 4), traffic=None, kernel=f"k_gemv_pair<{name}>",
+                    avg_launch_us=round(per * 1e3, 3), bytes_per_launch=bytes_call)
+    return dict(value=value, ms_step=ms, wall=wall, roofline=roofline, flops=2 * N * K * len(copies),
+                workload=f"{name} GEMV 9728x2560 fp16 x (24 rotated copies)",
+                bytes_per_step=bytes_call * len(copies), launches_per_step=len(copies))
 
 
 def timed_graph(torch, launches, steps, warmup):
@@ -453,6 +491,8 @@ def main():
     dev = torch.device("cuda:0")
     if args.config == "gemv1":
         r = run_gemv1(args, torch, dev)
+    elif args.config == "kquant":
+        r = run_kquant(args, torch, dev)
     elif args.config == "exl3":
         r = run_exl3(args, torch, dev)
     elif args.config == "prefill":

@@ -15,6 +15,10 @@
  *   q4_0: 18 B = [fp16 d][16 B nibbles], w = d * (q - 8)
  *   Q8_0: 34 B = [fp16 d][32 x int8],    w = d * q
  *   EXL3 4-bpw: trellis uint16 [K/16][N/16][64], suh fp16 [K], svh fp16 [N]
+ * GGUF K-quant super-blocks (256 weights, rows are K/256 super-blocks; llama.cpp layouts):
+ *   Q4_K: 144 B = [fp16 d][fp16 dmin][scales 12 B: 6-bit sc, m per 32][qs 128 B]
+ *   Q5_K: 176 B = [fp16 d][fp16 dmin][scales 12 B][qh 32 B][qs 128 B]
+ *   Q6_K: 210 B = [ql 128 B][qh 64 B][int8 scales per 16][fp16 d]
  * Results are deterministic: fixed reduction order, no floating-point atomics.
  */
 #ifndef VYBDQ_H
@@ -72,7 +76,23 @@ int vybdq_dequant_q4_0(uint64_t W, uint64_t out, int64_t nblocks, int order, int
    Replaces q8_0deq(q, o, n, z=0) (native/kernels/q8_0.vyb:11-30). */
 int vybdq_dequant_q8_0(uint64_t W, uint64_t out, int64_t nblocks, int out_dt, uint64_t stream);
 
+/* out[i] = weight i of n consecutive weights of type wtype (GGML type id: 2 = q4_0 in GGUF
+   order, 8 = Q8_0, 12 = Q4_K, 13 = Q5_K, 14 = Q6_K); n % 32 == 0 (K-quants: n % 256 == 0);
+   out_dt F32, F16 or F64 (F64: exact; F32: the exact value rounded once; F16: the F32 rounded).
+   Replaces q4kdeq / q4kdeq32 (native/kernels/q4k.vyb:9-70) and the q5_K / q6_K decodes the
+   reference gates (native/tools/q5k_ref.py:40-65, native/gguf/q6k_verify.py:20-40). */
+int vybdq_dequant(int wtype, uint64_t W, uint64_t out, int64_t n, int out_dt, uint64_t stream);
+
 /* ---- GEMV on packed GGUF rows -------------------------------------------------------- */
+
+/* The GEMV below for any GGUF weight type, dispatched on the GGML type id as the reference's
+   gemv_h(ty) does (native/host/ridge_decode.vyb:303-311): 2 = q4_0 (GGUF nibble order), 8 = Q8_0,
+   12 = Q4_K, 13 = Q5_K, 14 = Q6_K. K-quants need K % 256 == 0 and W 4-byte aligned. Replaces
+   gemv_q4k (native/kernels/qwen3.vyb:403-576), gemv_q6k (qwen3.vyb:726-887) and gemv_q5k
+   (native/kernels/rgemv.vyb:202-297), p-block W@0 X@8 Y@16 N@32 K@40 YE@48 RS@120. */
+int vybdq_gemv(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K,
+               int x_dt, int y_dt, uint64_t RS, uint64_t stream);
+
 
 /* Y[m, n] = RS[m, n] + sum_k X[m, k] * W[n, k] for m < M, n < N.
    X: x_dt (F32, F16, BF16) [M, K]; Y: y_dt (F32, F16, BF16, F64) [M, N]; RS: same type as

@@ -1,0 +1,96 @@
+"""GPU parity for the GGUF K-quants (Q4_K, Q5_K, Q6_K) through the type-id entry points
+vybdq_dequant (bit-exact against the oracle) and vybdq_gemv (2e-3 of the float64 gate,
+native/glm53/verify_layer0.py:134-139)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kquants, matmul
+from tests.test_gpu_gguf import TDT, gate, to_dev, x_as
+from vybforge_amd import _lib, ops, synth
+
+pytestmark = pytest.mark.gpu
+
+KQ = [ops.GGML_Q4_K, ops.GGML_Q5_K, ops.GGML_Q6_K]
+TOL = matmul.TOL
+
+
+@pytest.mark.parametrize("ty", KQ)
+@pytest.mark.parametrize("odt", [torch.float64, torch.float32, torch.float16])
+def test_dequant_bit_exact(dev, ty, odt):
+    rng = np.random.default_rng(ty)
+    raw = synth.kquant_weights(rng, ty, 7, 768)
+    got = ops.dequant_any(ty, to_dev(raw, dev), 7 * 768, odt).cpu().numpy()
+    ref = kquants.DEQUANT[ty](raw)
+    want = ref if odt == torch.float64 else ref.astype(np.float32)
+    if odt == torch.float16:
+        want = want.astype(np.float16)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("ty", KQ)
+def test_dequant_extreme_fields(dev, ty):
+    """Every byte value in the scale/quant fields and fp16 scales from subnormal to large."""
+    rng = np.random.default_rng(100 + ty)
+    nb = 64
+    raw = rng.integers(0, 256, (nb, kquants.BLOCK_BYTES[ty]), dtype=np.uint8)
+    fp = [0, 2] if ty != ops.GGML_Q6_K else [208]
+    vals = np.array([6e-8, 1e-5, 0.001, 0.5, 2.0, 100.0, -0.25, 0.0], np.float16)
+    for o in fp:
+        raw[:, o:o + 2] = vals[rng.integers(0, vals.size, nb)].view(np.uint8).reshape(nb, 2)
+    raw = raw.reshape(-1)
+    got = ops.dequant_any(ty, to_dev(raw, dev), nb * 256, torch.float64).cpu().numpy()
+    np.testing.assert_array_equal(got, kquants.DEQUANT[ty](raw))
+
+
+@pytest.mark.parametrize("ty", KQ)
+@pytest.mark.parametrize("N,K", [(256, 256), (300, 2560), (64, 4096), (1000, 768), (17, 9728)])
+@pytest.mark.parametrize("M", [1, 3])
+def test_gemv(dev, ty, N, K, M):
+    """Odd super-block counts per row (K = 768: Q6_K rows start 2 bytes past a dword boundary
+    every other row), ragged row counts, long rows, several X rows."""
+    rng = np.random.default_rng(N * 7 + K + M + ty)
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = synth.activations(rng, (M, K))
+    y = ops.gemv(ty, to_dev(raw, dev), torch.from_numpy(x).to(dev), N, K).cpu().numpy()
+    ref = x.astype(np.float64) @ kquants.matrix(ty, raw, N, K).T
+    assert matmul.rel_maxnorm(y, ref) < TOL
+
+
+@pytest.mark.parametrize("ty", KQ)
+@pytest.mark.parametrize("xdt", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("ydt", ["f32", "f16", "bf16", "f64"])
+def test_gemv_dtypes_residual(dev, ty, xdt, ydt):
+    rng = np.random.default_rng(ty * 3 + len(xdt) + len(ydt))
+    N, K, M = 320, 1536, 2
+    raw = synth.kquant_weights(rng, ty, N, K)
+    xd, x64 = x_as(synth.activations(rng, (M, K)), xdt, dev)
+    rs = torch.from_numpy(rng.standard_normal((M, N))).to(TDT[ydt])
+    y = ops.gemv(ty, to_dev(raw, dev), xd, N, K, TDT[ydt], residual=rs.to(dev))
+    ref = x64 @ kquants.matrix(ty, raw, N, K).T + rs.to(torch.float64).numpy()
+    assert gate(y.to(torch.float64).cpu().numpy(), ref, TDT[ydt]) < TOL
+
+
+@pytest.mark.parametrize("ty", KQ)
+@pytest.mark.parametrize("plan", ["8,1,64", "16,2,128", "32,2,256", "64,1,256"])
+def test_gemv_forced_plans(dev, monkeypatch, ty, plan):
+    """Launch shapes the planner does not pick (lanes per row, units per batch, threads)."""
+    monkeypatch.setenv("VYBDQ_GEMV_PLAN", plan)
+    rng = np.random.default_rng(ty + len(plan))
+    N, K = 200, 3328
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = synth.activations(rng, (K,))
+    y = ops.gemv(ty, to_dev(raw, dev), torch.from_numpy(x).to(dev), N, K).cpu().numpy()
+    ref = kquants.matrix(ty, raw, N, K) @ x.astype(np.float64)
+    assert matmul.rel_maxnorm(y, ref) < TOL
+
+
+def test_type_id_errors(dev):
+    x = torch.zeros(256, device=dev)
+    y = torch.zeros(4, device=dev)
+    w = torch.zeros(4 * 210, dtype=torch.uint8, device=dev)
+    lib = _lib.lib
+    assert lib.vybdq_gemv(3, w.data_ptr(), x.data_ptr(), y.data_ptr(), 1, 4, 256, 0, 0, 0, 0) == _lib.ERR_ARG
+    assert lib.vybdq_gemv(14, w.data_ptr(), x.data_ptr(), y.data_ptr(), 1, 4, 128, 0, 0, 0, 0) == _lib.ERR_SHAPE
+    assert lib.vybdq_dequant(12, w.data_ptr(), y.data_ptr(), 100, 0, 0) == _lib.ERR_SHAPE

@@ -26,6 +26,8 @@ SIGNATURES = {
     "vybdq_last_error": [],
     "vybdq_dequant_q4_0": [_u64, _u64, _i64, _int, _int, _u64],
     "vybdq_dequant_q8_0": [_u64, _u64, _i64, _int, _u64],
+    "vybdq_dequant": [_int, _u64, _u64, _i64, _int, _u64],
+    "vybdq_gemv": [_int, _u64, _u64, _u64, _i64, _i64, _i64, _int, _int, _u64, _u64],
     "vybdq_gemv_q4_0": [_u64, _u64, _u64, _i64, _i64, _i64, _int, _int, _u64, _int, _u64],
     "vybdq_gemv_q8_0": [_u64, _u64, _u64, _i64, _i64, _i64, _int, _int, _u64, _u64],
     "vybdq_gemv_q4_0_seg3": [_u64, _i64, _int, _int,

@@ -6,7 +6,9 @@
 
 namespace vybdq {
 
-enum { FMT_Q4_0 = 0, FMT_Q8_0 = 1 };
+enum { FMT_Q4_0 = 0, FMT_Q8_0 = 1, FMT_Q4_K = 2, FMT_Q5_K = 3, FMT_Q6_K = 4 };
+
+template <int FMT> constexpr bool is_kquant() { return FMT == FMT_Q4_K || FMT == FMT_Q5_K || FMT == FMT_Q6_K; }
 
 template <int FMT> struct Fmt;
 template <> struct Fmt<FMT_Q4_0> {
@@ -225,6 +227,33 @@ __device__ __forceinline__ void pair_dot(const uint32_t (&dw)[Fmt<FMT>::PAIR_DWO
       acc[m] = fmaf(d, part, acc[m]);
     }
   }
+}
+
+}  // namespace vybdq
+
+#include "kquant_dev.h"
+
+namespace vybdq {
+
+// Bytes of one packed row of P 64-weight units.
+template <int FMT>
+__host__ __device__ constexpr int64_t unit_row_bytes(int64_t P) {
+  if constexpr (is_kquant<FMT>()) return (P / 4) * Fmt<FMT>::SB_BYTES;
+  else return P * Fmt<FMT>::PAIR_BYTES;
+}
+
+// Unit p (weights 64p .. 64p+63) of the row at wrow: loads, then the dot with the staged x.
+template <int FMT>
+__device__ __forceinline__ void load_unit(const uint8_t *wrow, int p, uint32_t (&dw)[Fmt<FMT>::PAIR_DWORDS]) {
+  if constexpr (is_kquant<FMT>()) load_unit_kq<FMT>(wrow, p, dw);
+  else load_pair<FMT>(wrow + static_cast<int64_t>(p) * Fmt<FMT>::PAIR_BYTES, dw);
+}
+
+template <int FMT, int ORDER, int M>
+__device__ __forceinline__ void unit_dot(const uint32_t (&dw)[Fmt<FMT>::PAIR_DWORDS], const char *lds,
+                                         const float *sx, int P, int p, float (&acc)[M]) {
+  if constexpr (is_kquant<FMT>()) unit_dot_kq<FMT, M>(dw, lds, sx, P, p, acc);
+  else pair_dot<FMT, ORDER, M>(dw, lds, sx, P, p, acc);
 }
 
 }  // namespace vybdq

@@ -14,8 +14,13 @@ from ._lib import BF16, F16, F32, F64, Q4_GGML, Q4_INTERLEAVED, call  # noqa: F4
 
 GGML_Q4_0 = 2   # ggml_type ids, as the reference dispatches on them
 GGML_Q8_0 = 8
+GGML_Q4_K = 12
+GGML_Q5_K = 13
+GGML_Q6_K = 14
+KQUANTS = (GGML_Q4_K, GGML_Q5_K, GGML_Q6_K)
 
-BLOCK_BYTES = {GGML_Q4_0: 18, GGML_Q8_0: 34}
+BLOCK_BYTES = {GGML_Q4_0: 18, GGML_Q8_0: 34, GGML_Q4_K: 144, GGML_Q5_K: 176, GGML_Q6_K: 210}
+BLOCK_WEIGHTS = {GGML_Q4_0: 32, GGML_Q8_0: 32, GGML_Q4_K: 256, GGML_Q5_K: 256, GGML_Q6_K: 256}
 
 _DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.float64: F64}
 
@@ -42,7 +47,7 @@ def _stream():
 
 
 def row_bytes(ty, K):
-    return (K // 32) * BLOCK_BYTES[ty]
+    return (K // BLOCK_WEIGHTS[ty]) * BLOCK_BYTES[ty]
 
 
 def dequant(ty, W, nblocks, out_dtype=torch.float32, order=Q4_GGML, out=None):
@@ -55,6 +60,14 @@ def dequant(ty, W, nblocks, out_dtype=torch.float32, order=Q4_GGML, out=None):
         call("vybdq_dequant_q8_0", _ptr(W), _ptr(out), nblocks, _dt(out.dtype), _stream())
     else:
         raise ValueError(f"unsupported GGUF type {ty}")
+    return out
+
+
+def dequant_any(ty, W, n, out_dtype=torch.float32, out=None):
+    """Decode the first n weights of a packed tensor of GGML type ty (vybdq_dequant)."""
+    if out is None:
+        out = torch.empty(n, dtype=out_dtype, device=W.device)
+    call("vybdq_dequant", ty, _ptr(W), _ptr(out), n, _dt(out.dtype), _stream())
     return out
 
 
@@ -72,6 +85,9 @@ def gemv(ty, W, X, N, K, y_dtype=torch.float32, residual=None, order=Q4_GGML, ou
              _ptr(residual), order, _stream())
     elif ty == GGML_Q8_0:
         call("vybdq_gemv_q8_0", _ptr(W), _ptr(X2), _ptr(out), M, N, K, _dt(X2.dtype), _dt(out.dtype),
+             _ptr(residual), _stream())
+    elif ty in KQUANTS:
+        call("vybdq_gemv", ty, _ptr(W), _ptr(X2), _ptr(out), M, N, K, _dt(X2.dtype), _dt(out.dtype),
              _ptr(residual), _stream())
     else:
         raise ValueError(f"unsupported GGUF type {ty}")

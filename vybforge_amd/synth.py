@@ -35,3 +35,21 @@ def exl3_tensors(rng, K, N):
     suh = (np.abs(rng.normal(0, 0.01, K)) * rng.choice([-1.0, 1.0], K)).astype(np.float16)
     svh = (np.abs(rng.normal(0, 0.01, N)) * rng.choice([-1.0, 1.0], N)).astype(np.float16)
     return trellis, suh, svh
+
+
+KQ_BYTES = {12: 144, 13: 176, 14: 210}
+
+
+def kquant_weights(rng, ty, N, K):
+    """Packed Q4_K (12) / Q5_K (13) / Q6_K (14) bytes uint8 [N * K/256 * block]: uniform random
+    quant, scale and high-bit bytes; the fp16 fields (d and dmin; Q6_K: d) = |N(0, 1e-4)|."""
+    nb = N * (K // 256)
+    sb = KQ_BYTES[ty]
+    blk = rng.integers(0, 256, (nb, sb), dtype=np.uint8)
+    f16 = lambda: np.abs(rng.normal(0.0, 1e-4, nb)).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    if ty in (12, 13):
+        blk[:, 0:2] = f16()
+        blk[:, 2:4] = f16()
+    else:
+        blk[:, 208:210] = f16()
+    return blk.reshape(-1)
