@@ -35,7 +35,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="stack",
-                    choices=["stack", "stack_chain", "gemv1", "kquant", "exl3", "prefill", "prefill_i8", "moe", "copy"])
+                    choices=["stack", "stack_chain", "gemv1", "kquant", "producers", "exl3", "prefill", "prefill_i8",
+                             "moe", "copy"])
     ap.add_argument("--wtype", type=int, default=12, choices=[12, 13, 14],
                     help="GGML type id for --config kquant (12 Q4_K, 13 Q5_K, 14 Q6_K)")
     ap.add_argument("--tokens", type=int, default=16, help="tokens for --config moe")
@@ -280,6 +281,32 @@ def run_kquant(args, torch, dev):
                 bytes_per_step=bytes_call * len(copies), launches_per_step=len(copies))
 
 
+def run_producers(args, torch, dev):
+    """Producer-side q8 at the 27B decode shapes: RMSNorm of one float64 row of 5120 (float32 copy
+    + q8 copy) and SwiGLU of 17408 float64 pairs (float32 h + q8 copy), 16 of each per graph."""
+    from vybforge_amd import ops
+    N, F = 5120, 17408
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    xs = [torch.randn(1, N, generator=gen, device=dev, dtype=torch.float64) for _ in range(16)]
+    w = torch.rand(N, generator=gen, device=dev, dtype=torch.float64) + 0.5
+    gs = [torch.randn(F, generator=gen, device=dev, dtype=torch.float64) for _ in range(16)]
+    u = torch.randn(F, generator=gen, device=dev, dtype=torch.float64)
+    launches = [lambda x=x: ops.rmsnorm_q8(x, w, 1e-6, f32_copy=True) for x in xs]
+    launches += [lambda g=g: ops.swiglu_q8(g, u) for g in gs]
+    ms, wall = timed_graph(torch, launches, args.steps, args.warmup)
+    rms_bytes = 8 * N * 2 + 4 * N + N + 4 * (N // 32)
+    swi_bytes = 8 * F * 2 + 4 * F + F + 4 * (F // 32)
+    per = ms / len(launches)
+    value = (rms_bytes + swi_bytes) * 16 / (ms * 1e-3) / 1e9
+    roofline = dict(bound="hbm", achieved=round(value, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(value / HBM_PEAK_GBS, 4), traffic=None, kernel="k_rms_q8 + k_swiglu_q8",
+                    avg_launch_us=round(per * 1e3, 3), bytes_per_launch=(rms_bytes + swi_bytes) // 2)
+    return dict(value=value, ms_step=ms, wall=wall, roofline=roofline, flops=0,
+                workload="RMSNorm+q8 (1x5120 f64) and SwiGLU+q8 (17408 f64), 16 each per step",
+                bytes_per_step=(rms_bytes + swi_bytes) * 16, launches_per_step=len(launches))
+
+
 def timed_graph(torch, launches, steps, warmup):
     """Capture the launches as one graph; return (ms per replay, wall seconds)."""
     for f in launches:
@@ -493,6 +520,8 @@ def main():
         r = run_gemv1(args, torch, dev)
     elif args.config == "kquant":
         r = run_kquant(args, torch, dev)
+    elif args.config == "producers":
+        r = run_producers(args, torch, dev)
     elif args.config == "exl3":
         r = run_exl3(args, torch, dev)
     elif args.config == "prefill":

@@ -116,6 +116,24 @@ int vybdq_gemv_q4_0_seg3(uint64_t X, int64_t K, int x_dt, int order,
                          uint64_t W2, uint64_t Y2, int64_t N2, int y_dt2,
                          uint64_t W3, uint64_t Y3, int64_t N3, int y_dt3, uint64_t stream);
 
+/* ---- producer-side q8 activation quantization ---------------------------------------- */
+
+/* Per row of X [M, N]: y = x * r * w with r = 1 / sqrt(sum x^2 / N + eps), in float64 with the
+   reference's summation order and seeded-Newton square root; writes any of Y [M, N] (y_dt),
+   Y32 [M, N] float32 and the q8 copy of the float32 values (Xq int8 [M, N], Xs float32
+   [M, N/32], N % 32 == 0; xq8 semantics). X and W [N] have element type x_dt (F64, F32, F16,
+   BF16). Replaces rms_blkg with its Y32 and Y8 outputs (native/kernels/layer.vyb:989-1066,
+   VYB_RMSQ8); the reference's single Y8 buffer is Xq followed by Xs (M = 1). */
+int vybdq_rmsnorm_q8(uint64_t X, uint64_t W, uint64_t Y, uint64_t Y32, uint64_t Xq, uint64_t Xs,
+                     int64_t M, int64_t N, double eps, int x_dt, int y_dt, uint64_t stream);
+
+/* h = g * sigmoid(g) * u elementwise in float64 with the reference's exp (vmath.vyb:7-40);
+   writes H [n] (h_dt, F32 in the reference) and/or the q8 copy of float32(h) (Xq, Xs;
+   n % 32 == 0). G and U have element type g_dt (F64, F32, F16, BF16). Replaces silu32q
+   (native/kernels/layer.vyb:1567-1590, VYB_SWQ8). */
+int vybdq_swiglu_q8(uint64_t G, uint64_t U, uint64_t H, uint64_t Xq, uint64_t Xs, int64_t n, int g_dt,
+                    int h_dt, uint64_t stream);
+
 /* ---- persistent chain of dependent GEMV stages --------------------------------------- */
 
 /* Bytes of workspace vybdq_gemv_chain needs for nstages stages (a status word and one counter

@@ -35,6 +35,8 @@ SIGNATURES = {
                              _u64, _u64, _i64, _int,
                              _u64, _u64, _i64, _int, _u64],
     "vybdq_quant_q8_act": [_u64, _u64, _u64, _i64, _i64, _int, _u64],
+    "vybdq_rmsnorm_q8": [_u64, _u64, _u64, _u64, _u64, _u64, _i64, _i64, ctypes.c_double, _int, _int, _u64],
+    "vybdq_swiglu_q8": [_u64, _u64, _u64, _u64, _u64, _i64, _int, _int, _u64],
     "vybdq_chain_workspace_size": [_int],
     "vybdq_gemv_chain": [_int, _u64, _int, _i64, _i64, _u64, _u64],
     "vybdq_chain_status": [_u64],

@@ -121,6 +121,34 @@ def quant_q8_act(X, out=None):
 
 # ---- persistent GEMV chain ---------------------------------------------------------------
 
+def rmsnorm_q8(X, W, eps, y_dtype=None, f32_copy=False, q8=True):
+    """RMSNorm of the rows of X [M, N] (or [N]) with the q8 copy of its float32 output
+    (vybdq_rmsnorm_q8). Returns (Y or None, Y32 or None, Xq or None, Xs or None)."""
+    X2 = X.reshape(1, -1) if X.dim() == 1 else X
+    M, N = X2.shape
+    dev = X.device
+    Y = torch.empty((M, N), dtype=y_dtype, device=dev) if y_dtype is not None else None
+    Y32 = torch.empty((M, N), dtype=torch.float32, device=dev) if f32_copy else None
+    Xq = torch.empty((M, N), dtype=torch.int8, device=dev) if q8 else None
+    Xs = torch.empty((M, N // 32), dtype=torch.float32, device=dev) if q8 else None
+    call("vybdq_rmsnorm_q8", _ptr(X2), _ptr(W), _ptr(Y), _ptr(Y32), _ptr(Xq), _ptr(Xs), M, N, float(eps),
+         _dt(X2.dtype), _dt(Y.dtype) if Y is not None else F32, _stream())
+    return Y, Y32, Xq, Xs
+
+
+def swiglu_q8(G, U, h_dtype=torch.float32, q8=True):
+    """h = silu(G) * U elementwise with the q8 copy of float32(h) (vybdq_swiglu_q8).
+    Returns (H or None, Xq or None, Xs or None)."""
+    n = G.numel()
+    dev = G.device
+    H = torch.empty(n, dtype=h_dtype, device=dev) if h_dtype is not None else None
+    Xq = torch.empty(n, dtype=torch.int8, device=dev) if q8 else None
+    Xs = torch.empty(n // 32, dtype=torch.float32, device=dev) if q8 else None
+    call("vybdq_swiglu_q8", _ptr(G), _ptr(U), _ptr(H), _ptr(Xq), _ptr(Xs), n, _dt(G.dtype),
+         _dt(H.dtype) if H is not None else F32, _stream())
+    return H, Xq, Xs
+
+
 PBLOCK_WORDS = 32        # one stage = the reference's GEMV p-block, 256-byte stride
 _YE = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 258, torch.float64: 8}
 _XE = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 258}
