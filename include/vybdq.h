@@ -134,6 +134,45 @@ int vybdq_rmsnorm_q8(uint64_t X, uint64_t W, uint64_t Y, uint64_t Y32, uint64_t 
 int vybdq_swiglu_q8(uint64_t G, uint64_t U, uint64_t H, uint64_t Xq, uint64_t Xs, int64_t n, int g_dt,
                     int h_dt, uint64_t stream);
 
+/* ---- GGUF reader and packed-slab residency (host) ------------------------------------ */
+
+/* Opens and indexes a GGUF v2/v3 file (header, every metadata pair, every tensor info); returns
+   a handle >= 1 or a negative error code. Replaces the reference's Vyb readers
+   (native/gguf/parse_gguf.vyb, native/gguf/read_real_meta.vyb). */
+int64_t vybdq_gguf_open(const char *path);
+int vybdq_gguf_close(int64_t h);
+/* what: 0 version, 1 tensor count, 2 metadata count, 3 alignment, 4 end of the tensor infos,
+   5 data section start (4 rounded up to the alignment), 6 file size. */
+int64_t vybdq_gguf_info(int64_t h, int what);
+/* index of the tensor / metadata pair with that name, -1 if absent */
+int64_t vybdq_gguf_find_tensor(int64_t h, const char *name);
+int64_t vybdq_gguf_find_kv(int64_t h, const char *key);
+/* copies the name (NUL-terminated, at most cap - 1 bytes) and returns its full length */
+int64_t vybdq_gguf_tensor_name(int64_t h, int64_t i, char *buf, int64_t cap);
+/* what: 0 ggml type, 1 n_dims, 2 + d dims[d], -1 the raw offset field, -2 data bytes
+   (-1 for a type this library does not size) */
+int64_t vybdq_gguf_tensor_field(int64_t h, int64_t i, int what);
+int64_t vybdq_gguf_kv_key(int64_t h, int64_t i, char *buf, int64_t cap);
+/* what: 0 value type, 1 integer value (integer and bool types), 2 array element type,
+   3 array length */
+int64_t vybdq_gguf_kv_field(int64_t h, int64_t i, int what);
+/* float value of a f32 / f64 pair (integers converted; 0.0 for a bad handle or index) */
+double vybdq_gguf_kv_float(int64_t h, int64_t i);
+int64_t vybdq_gguf_kv_string(int64_t h, int64_t i, char *buf, int64_t cap);
+/* Reads tensor i's bytes into host memory (cap >= its size); absolute = 1 takes the offset
+   field as a file offset (the convention of the reference's fixture writer,
+   native/gguf/mk_fixture.vyb), 0 as relative to the data section (the GGUF convention).
+   Returns the byte count. */
+int64_t vybdq_gguf_read_tensor(int64_t h, int64_t i, int absolute, void *dst, int64_t cap);
+/* One-buffer residency (the reference's resident packed slab, native/host/ridge_decode.vyb:1-3):
+   every tensor in index order at an offset rounded up to align (a power of two). */
+int64_t vybdq_gguf_slab_offset(int64_t h, int64_t i, int64_t align);
+int64_t vybdq_gguf_slab_bytes(int64_t h, int64_t align);
+/* Copies every tensor into the device slab dev (dev_bytes >= vybdq_gguf_slab_bytes) on stream
+   through a host buffer; returns when the copies have finished. */
+int vybdq_gguf_load_slab(int64_t h, uint64_t dev, int64_t dev_bytes, int64_t align, int absolute,
+                         uint64_t stream);
+
 /* ---- persistent chain of dependent GEMV stages --------------------------------------- */
 
 /* Bytes of workspace vybdq_gemv_chain needs for nstages stages (a status word and one counter

@@ -35,6 +35,21 @@ SIGNATURES = {
                              _u64, _u64, _i64, _int,
                              _u64, _u64, _i64, _int, _u64],
     "vybdq_quant_q8_act": [_u64, _u64, _u64, _i64, _i64, _int, _u64],
+    "vybdq_gguf_open": [ctypes.c_char_p],
+    "vybdq_gguf_close": [_i64],
+    "vybdq_gguf_info": [_i64, _int],
+    "vybdq_gguf_find_tensor": [_i64, ctypes.c_char_p],
+    "vybdq_gguf_find_kv": [_i64, ctypes.c_char_p],
+    "vybdq_gguf_tensor_name": [_i64, _i64, ctypes.c_char_p, _i64],
+    "vybdq_gguf_tensor_field": [_i64, _i64, _int],
+    "vybdq_gguf_kv_key": [_i64, _i64, ctypes.c_char_p, _i64],
+    "vybdq_gguf_kv_field": [_i64, _i64, _int],
+    "vybdq_gguf_kv_float": [_i64, _i64],
+    "vybdq_gguf_kv_string": [_i64, _i64, ctypes.c_char_p, _i64],
+    "vybdq_gguf_read_tensor": [_i64, _i64, _int, ctypes.c_void_p, _i64],
+    "vybdq_gguf_slab_offset": [_i64, _i64, _i64],
+    "vybdq_gguf_slab_bytes": [_i64, _i64],
+    "vybdq_gguf_load_slab": [_i64, _u64, _i64, _i64, _int, _u64],
     "vybdq_rmsnorm_q8": [_u64, _u64, _u64, _u64, _u64, _u64, _i64, _i64, ctypes.c_double, _int, _int, _u64],
     "vybdq_swiglu_q8": [_u64, _u64, _u64, _u64, _u64, _i64, _int, _int, _u64],
     "vybdq_chain_workspace_size": [_int],
@@ -57,7 +72,12 @@ SIGNATURES = {
 }
 _RESTYPE = {"vybdq_last_error": ctypes.c_char_p, "vybdq_chain_workspace_size": ctypes.c_int64,
             "vybdq_exl3_workspace_size": ctypes.c_int64, "vybdq_moe_workspace_size": ctypes.c_int64,
-            "vybdq_gemm_workspace_size": ctypes.c_int64, "vybdq_gemm_q8_0_i8_workspace_size": ctypes.c_int64}
+            "vybdq_gemm_workspace_size": ctypes.c_int64, "vybdq_gemm_q8_0_i8_workspace_size": ctypes.c_int64,
+            "vybdq_gguf_kv_float": ctypes.c_double}
+for _n in ("vybdq_gguf_open", "vybdq_gguf_info", "vybdq_gguf_find_tensor", "vybdq_gguf_find_kv",
+           "vybdq_gguf_tensor_name", "vybdq_gguf_tensor_field", "vybdq_gguf_kv_key", "vybdq_gguf_kv_field",
+           "vybdq_gguf_kv_string", "vybdq_gguf_read_tensor", "vybdq_gguf_slab_offset", "vybdq_gguf_slab_bytes"):
+    _RESTYPE[_n] = ctypes.c_int64
 
 
 class VybdqError(RuntimeError):
