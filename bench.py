@@ -37,8 +37,8 @@ def parse():
     ap.add_argument("--config", default="stack",
                     choices=["stack", "stack_chain", "gemv1", "kquant", "producers", "exl3", "prefill", "prefill_i8",
                              "moe", "copy"])
-    ap.add_argument("--wtype", type=int, default=12, choices=[12, 13, 14],
-                    help="GGML type id for --config kquant (12 Q4_K, 13 Q5_K, 14 Q6_K)")
+    ap.add_argument("--wtype", type=int, default=12, choices=[12, 13, 14, 22],
+                    help="GGML type id for --config kquant (12 Q4_K, 13 Q5_K, 14 Q6_K, 22 IQ2_S)")
     ap.add_argument("--tokens", type=int, default=16, help="tokens for --config moe")
     ap.add_argument("--batch", type=int, default=1, help="batch for --config exl3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -59,10 +59,10 @@ def q4_0_blocks_gpu(torch, gen, N, K, dev):
 def kquant_blocks_gpu(torch, gen, ty, N, K, dev):
     """Seeded packed Q4_K / Q5_K / Q6_K rows on the device: uniform random bytes, the fp16
     scale fields = |N(0, 1e-4)|."""
-    sbytes = {12: 144, 13: 176, 14: 210}[ty]
+    sbytes = {12: 144, 13: 176, 14: 210, 22: 82}[ty]
     nb = N * (K // 256)
     blk = torch.randint(0, 256, (nb, sbytes), generator=gen, device=dev, dtype=torch.uint8)
-    for off in ((0, 2) if ty in (12, 13) else (208,)):
+    for off in {12: (0, 2), 13: (0, 2), 14: (208,), 22: (0,)}[ty]:
         d = (torch.randn(nb, generator=gen, device=dev) * 1e-4).abs().to(torch.float16)
         blk[:, off:off + 2] = d.view(torch.uint8).view(nb, 2)
     return blk.view(-1)
@@ -262,7 +262,7 @@ def run_kquant(args, torch, dev):
     (> the 256 MB MALL), one GEMV per copy in one graph."""
     from vybforge_amd import ops
     N, K, ty = 9728, 2560, args.wtype
-    name = {12: "Q4_K", 13: "Q5_K", 14: "Q6_K"}[ty]
+    name = {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 22: "IQ2_S"}[ty]
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
     copies = [kquant_blocks_gpu(torch, gen, ty, N, K, dev) for _ in range(24)]

@@ -77,7 +77,8 @@ int vybdq_dequant_q4_0(uint64_t W, uint64_t out, int64_t nblocks, int order, int
 int vybdq_dequant_q8_0(uint64_t W, uint64_t out, int64_t nblocks, int out_dt, uint64_t stream);
 
 /* out[i] = weight i of n consecutive weights of type wtype (GGML type id: 2 = q4_0 in GGUF
-   order, 8 = Q8_0, 12 = Q4_K, 13 = Q5_K, 14 = Q6_K); n % 32 == 0 (K-quants: n % 256 == 0);
+   order, 8 = Q8_0, 12 = Q4_K, 13 = Q5_K, 14 = Q6_K, 22 = IQ2_S); n % 32 == 0 (super-block types:
+   n % 256 == 0);
    out_dt F32, F16 or F64 (F64: exact; F32: the exact value rounded once; F16: the F32 rounded).
    Replaces q4kdeq / q4kdeq32 (native/kernels/q4k.vyb:9-70) and the q5_K / q6_K decodes the
    reference gates (native/tools/q5k_ref.py:40-65, native/gguf/q6k_verify.py:20-40). */
@@ -87,7 +88,8 @@ int vybdq_dequant(int wtype, uint64_t W, uint64_t out, int64_t n, int out_dt, ui
 
 /* The GEMV below for any GGUF weight type, dispatched on the GGML type id as the reference's
    gemv_h(ty) does (native/host/ridge_decode.vyb:303-311): 2 = q4_0 (GGUF nibble order), 8 = Q8_0,
-   12 = Q4_K, 13 = Q5_K, 14 = Q6_K. K-quants need K % 256 == 0 and W 4-byte aligned. Replaces
+   12 = Q4_K, 13 = Q5_K, 14 = Q6_K, 22 = IQ2_S. Super-block types need K % 256 == 0 and W 4-byte
+   aligned. Replaces gemv_iq2s (native/kernels/rgemv.vyb:24-80),
    gemv_q4k (native/kernels/qwen3.vyb:403-576), gemv_q6k (qwen3.vyb:726-887) and gemv_q5k
    (native/kernels/rgemv.vyb:202-297), p-block W@0 X@8 Y@16 N@32 K@40 YE@48 RS@120. */
 int vybdq_gemv(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K,

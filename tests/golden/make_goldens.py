@@ -11,6 +11,12 @@ imports and runs no reference code. Outputs, all in this directory:
   exl3_tile_slot_composition.json native/exl3/tile_slot_composition.json, re-serialised as a
                                   sorted slot list, plus a digest of native/exl3/map.bin
                                   re-derived from it (gen_map_bin.py:1-37 layout)
+  ../../vybforge_amd/data/iq2s_grid.json
+                                  the IQ2_S grid (1024 x 8 bytes) and sign masks: llama.cpp's
+                                  iq2s_grid / kmask_iq2xs tables (MIT) as the reference holds
+                                  them in native/gguf/iq2s_tables.py, read as text (the hex
+                                  literals), not imported; the library build turns it into a
+                                  device table, the oracle reads it
   moe_golden.npz                  from native/glm53/prep/*.f32 (prepare_moe_fixture.py:21-70):
                                   router logits (y @ gate^T in float64), bias, the reference's
                                   routing ids/weights, the expert pre-activations g/u (float64),
@@ -97,10 +103,28 @@ def moe():
         scale=np.float64(2.5), limit=np.float64(10.0))
 
 
+def iq2s_grid():
+    import re
+    p = os.path.join(REF, "native/gguf/iq2s_tables.py")
+    text = open(p).read()
+    body = text[text.index("IQ2_S_GRID = ("):]
+    body = body[:body.index(")")]
+    grid = [int(h, 16) for h in re.findall(r"0x[0-9a-fA-F]{16}", body)]
+    assert len(grid) == 1024, len(grid)
+    kmask = [int(v) for v in re.search(r"IQ2_S_KMASK = \(([^)]*)\)", text).group(1).split(",")]
+    assert kmask == [1, 2, 4, 8, 16, 32, 64, 128], kmask
+    out = os.path.join(HERE, "..", "..", "vybforge_amd", "data", "iq2s_grid.json")
+    json.dump({"source": SRC_NOTE + " (native/gguf/iq2s_tables.py, itself llama.cpp ggml-common.h, MIT)",
+               "grid_u64_hex": [f"{g:016x}" for g in grid], "kmask": kmask},
+              open(out, "w"), indent=0)
+    print("wrote", out)
+
+
 if __name__ == "__main__":
     if not os.path.isdir(REF):
         sys.exit(f"reference checkout not found at {REF}")
     q4_0_fixture()
     exl3_map()
     moe()
+    iq2s_grid()
     print("goldens written to", HERE)

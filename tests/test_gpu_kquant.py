@@ -1,4 +1,4 @@
-"""GPU parity for the GGUF K-quants (Q4_K, Q5_K, Q6_K) through the type-id entry points
+"""GPU parity for the GGUF super-block types (Q4_K, Q5_K, Q6_K, IQ2_S) through the type-id entry points
 vybdq_dequant (bit-exact against the oracle) and vybdq_gemv (2e-3 of the float64 gate,
 native/glm53/verify_layer0.py:134-139)."""
 
@@ -6,14 +6,23 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import kquants, matmul
+from oracle import iquants, kquants, matmul
 from tests.test_gpu_gguf import TDT, gate, to_dev, x_as
 from vybforge_amd import _lib, ops, synth
 
 pytestmark = pytest.mark.gpu
 
-KQ = [ops.GGML_Q4_K, ops.GGML_Q5_K, ops.GGML_Q6_K]
+KQ = [ops.GGML_Q4_K, ops.GGML_Q5_K, ops.GGML_Q6_K, ops.GGML_IQ2_S]
 TOL = matmul.TOL
+BLOCK = {**kquants.BLOCK_BYTES, ops.GGML_IQ2_S: iquants.IQ2_S_BYTES}
+
+
+def dequant_ref(ty, raw):
+    return iquants.dequant_iq2_s(raw) if ty == ops.GGML_IQ2_S else kquants.DEQUANT[ty](raw)
+
+
+def matrix_ref(ty, raw, N, K):
+    return dequant_ref(ty, raw).reshape(N, K)
 
 
 @pytest.mark.parametrize("ty", KQ)
@@ -22,7 +31,7 @@ def test_dequant_bit_exact(dev, ty, odt):
     rng = np.random.default_rng(ty)
     raw = synth.kquant_weights(rng, ty, 7, 768)
     got = ops.dequant_any(ty, to_dev(raw, dev), 7 * 768, odt).cpu().numpy()
-    ref = kquants.DEQUANT[ty](raw)
+    ref = dequant_ref(ty, raw)
     want = ref if odt == torch.float64 else ref.astype(np.float32)
     if odt == torch.float16:
         want = want.astype(np.float16)
@@ -34,14 +43,14 @@ def test_dequant_extreme_fields(dev, ty):
     """Every byte value in the scale/quant fields and fp16 scales from subnormal to large."""
     rng = np.random.default_rng(100 + ty)
     nb = 64
-    raw = rng.integers(0, 256, (nb, kquants.BLOCK_BYTES[ty]), dtype=np.uint8)
-    fp = [0, 2] if ty != ops.GGML_Q6_K else [208]
+    raw = rng.integers(0, 256, (nb, BLOCK[ty]), dtype=np.uint8)
+    fp = {ops.GGML_Q6_K: [208], ops.GGML_IQ2_S: [0]}.get(ty, [0, 2])
     vals = np.array([6e-8, 1e-5, 0.001, 0.5, 2.0, 100.0, -0.25, 0.0], np.float16)
     for o in fp:
         raw[:, o:o + 2] = vals[rng.integers(0, vals.size, nb)].view(np.uint8).reshape(nb, 2)
     raw = raw.reshape(-1)
     got = ops.dequant_any(ty, to_dev(raw, dev), nb * 256, torch.float64).cpu().numpy()
-    np.testing.assert_array_equal(got, kquants.DEQUANT[ty](raw))
+    np.testing.assert_array_equal(got, dequant_ref(ty, raw))
 
 
 @pytest.mark.parametrize("ty", KQ)
@@ -54,7 +63,7 @@ def test_gemv(dev, ty, N, K, M):
     raw = synth.kquant_weights(rng, ty, N, K)
     x = synth.activations(rng, (M, K))
     y = ops.gemv(ty, to_dev(raw, dev), torch.from_numpy(x).to(dev), N, K).cpu().numpy()
-    ref = x.astype(np.float64) @ kquants.matrix(ty, raw, N, K).T
+    ref = x.astype(np.float64) @ matrix_ref(ty, raw, N, K).T
     assert matmul.rel_maxnorm(y, ref) < TOL
 
 
@@ -68,7 +77,7 @@ def test_gemv_dtypes_residual(dev, ty, xdt, ydt):
     xd, x64 = x_as(synth.activations(rng, (M, K)), xdt, dev)
     rs = torch.from_numpy(rng.standard_normal((M, N))).to(TDT[ydt])
     y = ops.gemv(ty, to_dev(raw, dev), xd, N, K, TDT[ydt], residual=rs.to(dev))
-    ref = x64 @ kquants.matrix(ty, raw, N, K).T + rs.to(torch.float64).numpy()
+    ref = x64 @ matrix_ref(ty, raw, N, K).T + rs.to(torch.float64).numpy()
     assert gate(y.to(torch.float64).cpu().numpy(), ref, TDT[ydt]) < TOL
 
 
@@ -82,7 +91,7 @@ def test_gemv_forced_plans(dev, monkeypatch, ty, plan):
     raw = synth.kquant_weights(rng, ty, N, K)
     x = synth.activations(rng, (K,))
     y = ops.gemv(ty, to_dev(raw, dev), torch.from_numpy(x).to(dev), N, K).cpu().numpy()
-    ref = kquants.matrix(ty, raw, N, K) @ x.astype(np.float64)
+    ref = matrix_ref(ty, raw, N, K) @ x.astype(np.float64)
     assert matmul.rel_maxnorm(y, ref) < TOL
 
 

@@ -44,10 +44,11 @@ def _compile(src):
 def build(verbose=False):
     """Compile all sources and link libvybdq.so. Always rebuilds."""
     os.makedirs(OBJ, exist_ok=True)
-    # generated tables (the EXL3 per-lane slot table) come first
-    r = subprocess.run([sys.executable, os.path.join(CSRC, "gen_exl3_slots.py")], capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError("gen_exl3_slots.py failed:\n" + r.stderr)
+    # generated tables (the EXL3 per-lane slot table, the IQ2_S grid) come first
+    for gen in ("gen_exl3_slots.py", "gen_iq2s_grid.py"):
+        r = subprocess.run([sys.executable, os.path.join(CSRC, gen)], capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"{gen} failed:\n" + r.stderr)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     if not srcs:
         raise RuntimeError("no HIP sources found")

@@ -83,7 +83,7 @@ static int gemv_common(int fmt, int order, uint64_t X, int64_t M, int64_t K, int
   VYBDQ_REQUIRE(acc < (int64_t(1) << 31), VYBDQ_ERR_SHAPE, "too many rows");
   const void *x = reinterpret_cast<const void *>(X);
   hipStream_t s = as_stream(stream);
-  if (fmt == FMT_Q4_K || fmt == FMT_Q5_K || fmt == FMT_Q6_K) {
+  if (fmt == FMT_Q4_K || fmt == FMT_Q5_K || fmt == FMT_Q6_K || fmt == FMT_IQ2_S) {
     VYBDQ_REQUIRE(K % 256 == 0, VYBDQ_ERR_SHAPE, "K-quant rows need K % 256 == 0");
     return gemv_kq_dispatch(fmt, x, M, K, x_dt, segs, s);
   }
@@ -149,7 +149,9 @@ extern "C" int vybdq_gemv(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t
     case 12: fmt = FMT_Q4_K; break;
     case 13: fmt = FMT_Q5_K; break;
     case 14: fmt = FMT_Q6_K; break;
-    default: return set_error(VYBDQ_ERR_ARG, "vybdq_gemv: wtype must be 2 (q4_0), 8 (Q8_0), 12 (Q4_K), 13 (Q5_K) or 14 (Q6_K)");
+    case 22: fmt = FMT_IQ2_S; break;
+    default:
+      return set_error(VYBDQ_ERR_ARG, "vybdq_gemv: wtype must be 2 (q4_0), 8 (Q8_0), 12 (Q4_K), 13 (Q5_K), 14 (Q6_K) or 22 (IQ2_S)");
   }
   Segs s = one_seg(W, Y, RS, N, y_dt);
   return gemv_common(fmt, VYBDQ_Q4_GGML, X, M, K, x_dt, s, stream);

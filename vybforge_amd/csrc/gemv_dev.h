@@ -6,9 +6,12 @@
 
 namespace vybdq {
 
-enum { FMT_Q4_0 = 0, FMT_Q8_0 = 1, FMT_Q4_K = 2, FMT_Q5_K = 3, FMT_Q6_K = 4 };
+enum { FMT_Q4_0 = 0, FMT_Q8_0 = 1, FMT_Q4_K = 2, FMT_Q5_K = 3, FMT_Q6_K = 4, FMT_IQ2_S = 5 };
 
-template <int FMT> constexpr bool is_kquant() { return FMT == FMT_Q4_K || FMT == FMT_Q5_K || FMT == FMT_Q6_K; }
+// formats of 256-weight super-blocks (walked as four 64-weight units each)
+template <int FMT> constexpr bool is_kquant() {
+  return FMT == FMT_Q4_K || FMT == FMT_Q5_K || FMT == FMT_Q6_K || FMT == FMT_IQ2_S;
+}
 
 template <int FMT> struct Fmt;
 template <> struct Fmt<FMT_Q4_0> {

@@ -84,6 +84,13 @@ __global__ void __launch_bounds__(256) k_gemv_pair(const void *__restrict__ X, i
     load_x_chunk<XW>(X, 8 * static_cast<int64_t>(c), r);
     stage_chunk<XW>(r, xdt, c, lds, sx);
   }
+  if constexpr (FMT == FMT_IQ2_S) {  // the IQ2_S grid (8 KB) after the x stage
+    uint2 *grid = reinterpret_cast<uint2 *>(sx + 2 * M * P);
+    for (int i = threadIdx.x; i < 1024; i += T) {
+      const unsigned long long e = kIq2sGrid[i];
+      grid[i] = uint2{static_cast<uint32_t>(e), static_cast<uint32_t>(e >> 32)};
+    }
+  }
   __syncthreads();
 
   float acc[M];
@@ -131,7 +138,7 @@ struct PairPlan {
 
 // Largest load batch per format (VGPRs: U unit windows of PAIR_DWORDS dwords in flight per lane).
 template <int FMT> constexpr int kUmax() {
-  return FMT == FMT_Q4_0 ? 5 : FMT == FMT_Q8_0 ? 3 : FMT == FMT_Q4_K ? 4 : 2;
+  return FMT == FMT_Q4_0 ? 5 : FMT == FMT_Q8_0 ? 3 : (FMT == FMT_Q4_K || FMT == FMT_IQ2_S) ? 4 : 2;
 }
 static int pair_umax(int fmt) {
   switch (fmt) {
@@ -139,6 +146,7 @@ static int pair_umax(int fmt) {
     case FMT_Q8_0: return kUmax<FMT_Q8_0>();
     case FMT_Q4_K: return kUmax<FMT_Q4_K>();
     case FMT_Q5_K: return kUmax<FMT_Q5_K>();
+    case FMT_IQ2_S: return kUmax<FMT_IQ2_S>();
     default: return kUmax<FMT_Q6_K>();
   }
 }
@@ -177,7 +185,7 @@ template <int FMT, int G, int ORDER, int M, int XW, int U>
 static int launch_gu(const void *X, int xdt, int64_t K, const Segs &segs, int threads, hipStream_t s) {
   const int64_t rows = segs.end[2];
   const int P = static_cast<int>(K / 64);
-  const size_t lds = static_cast<size_t>(M) * P * (XPAIR_STRIDE + 2 * 4);
+  const size_t lds = static_cast<size_t>(M) * P * (XPAIR_STRIDE + 2 * 4) + (FMT == FMT_IQ2_S ? 8192 : 0);
   if (lds > static_cast<size_t>(kMaxLds)) return set_error(VYBDQ_ERR_SHAPE, "gemv: K too large for the LDS x stage at this M");
   const int rows_per_wg = threads / G;
   const unsigned grid = static_cast<unsigned>((rows + rows_per_wg - 1) / rows_per_wg);

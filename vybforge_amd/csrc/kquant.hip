@@ -1,4 +1,4 @@
-// K-quant super-block decode (Q4_K, Q5_K, Q6_K) and the type-id dequant dispatch, gfx950.
+// Super-block decode (Q4_K, Q5_K, Q6_K, IQ2_S) and the type-id dequant dispatch, gfx950.
 //
 // One thread per 4 consecutive weights of a super-block (64 threads per super-block): the bytes
 // are read directly (the decode is a gate, not a hot path). Every weight is exact before its
@@ -8,6 +8,7 @@
 // Layouts: llama.cpp ggml-quants.c dequantize_row_q4_K / q5_K / q6_K as ported by the reference
 // (native/kernels/q4k.vyb:9-70, native/tools/q5k_ref.py:40-65, native/gguf/q6k_verify.py:20-40).
 #include "common.h"
+#include "iq2s_grid.inc"
 
 namespace vybdq {
 
@@ -28,7 +29,15 @@ __device__ __forceinline__ void scale_min_bytes(const uint8_t *s, int j, int &sc
 
 template <int WT, typename T>
 __device__ __forceinline__ T kq_value(const uint8_t *sb, int e) {
-  if constexpr (WT == 12 || WT == 13) {
+  if constexpr (WT == 22) {  // IQ2_S: group l = e / 8 of sub-block ib = e / 32, exact in float32
+    const int ib = e >> 5, l = (e >> 3) & 3, j = e & 7, grp = 4 * ib + l;
+    const int idx = sb[2 + grp] | (((sb[66 + ib] >> (2 * l)) & 3) << 8);
+    const int g = static_cast<int>((kIq2sGrid[idx] >> (8 * j)) & 255);
+    const int nib = l < 2 ? (sb[74 + ib] & 15) : (sb[74 + ib] >> 4);
+    const T db = static_cast<T>(f16_at(sb)) * (static_cast<T>(0.5) + static_cast<T>(nib)) * static_cast<T>(0.25);
+    const T v = db * static_cast<T>(g);
+    return ((sb[34 + grp] >> j) & 1) ? -v : v;
+  } else if constexpr (WT == 12 || WT == 13) {
     const int g = e >> 6, hi = (e >> 5) & 1, l = e & 31;
     int sc, m;
     scale_min_bytes(sb + 4, 2 * g + hi, sc, m);
@@ -52,7 +61,7 @@ __device__ __forceinline__ T kq_value(const uint8_t *sb, int e) {
 template <int WT, int ODT>
 __global__ void __launch_bounds__(256) k_dequant_kq(const uint8_t *__restrict__ W, void *__restrict__ out,
                                                     int64_t nsb) {
-  constexpr int SB = WT == 12 ? 144 : WT == 13 ? 176 : 210;
+  constexpr int SB = WT == 12 ? 144 : WT == 13 ? 176 : WT == 22 ? 82 : 210;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= nsb * 64) return;
   const int64_t b = t >> 6;
@@ -89,8 +98,8 @@ extern "C" int vybdq_dequant(int wtype, uint64_t W, uint64_t out, int64_t n, int
     return wtype == 2 ? vybdq_dequant_q4_0(W, out, n / 32, VYBDQ_Q4_GGML, out_dt, stream)
                       : vybdq_dequant_q8_0(W, out, n / 32, out_dt, stream);
   }
-  VYBDQ_REQUIRE(wtype == 12 || wtype == 13 || wtype == 14, VYBDQ_ERR_ARG,
-                "wtype must be 2 (q4_0), 8 (Q8_0), 12 (Q4_K), 13 (Q5_K) or 14 (Q6_K)");
+  VYBDQ_REQUIRE(wtype == 12 || wtype == 13 || wtype == 14 || wtype == 22, VYBDQ_ERR_ARG,
+                "wtype must be 2 (q4_0), 8 (Q8_0), 12 (Q4_K), 13 (Q5_K), 14 (Q6_K) or 22 (IQ2_S)");
   VYBDQ_REQUIRE(n % 256 == 0, VYBDQ_ERR_SHAPE, "K-quants: n must be a multiple of 256");
   if (n == 0) return VYBDQ_OK;
   const auto *w = reinterpret_cast<const uint8_t *>(W);
@@ -98,6 +107,7 @@ extern "C" int vybdq_dequant(int wtype, uint64_t W, uint64_t out, int64_t n, int
   hipStream_t s = as_stream(stream);
   if (wtype == 12) launch_kq<12>(w, o, n / 256, out_dt, s);
   else if (wtype == 13) launch_kq<13>(w, o, n / 256, out_dt, s);
+  else if (wtype == 22) launch_kq<22>(w, o, n / 256, out_dt, s);
   else launch_kq<14>(w, o, n / 256, out_dt, s);
   return check_launch("vybdq_dequant");
 }

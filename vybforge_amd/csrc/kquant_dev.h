@@ -18,7 +18,13 @@
 // re-alignment (v_alignbit by 0 or 16) happens at use, so nothing waits at load time.
 // The layouts follow llama.cpp's ggml-quants.c, as ported by the reference
 // (native/kernels/q4k.vyb:1-70, native/tools/q5k_ref.py:40-65, native/gguf/q6k_verify.py:20-40).
+//   IQ2_S (82 B: d, qs[32] grid-index bytes, 32 sign bytes, qh[8], scales[8]): unit u = sub-blocks
+//     2u, 2u+1 = groups 8u .. 8u+7 of 8 weights; group l takes grid entry
+//     qs[8u+l] | ((qh[2u + l/4] >> 2(l%4)) & 3) << 8 (8 magnitudes 8/25/43, from the grid staged
+//     in LDS), negated per the bits of sign byte 8u+l, scaled by d*(0.5 + 4-bit scale)/4 per 16.
 #pragma once
+
+#include "iq2s_grid.inc"
 
 namespace vybdq {
 
@@ -29,6 +35,10 @@ template <> struct Fmt<FMT_Q4_K> {
 template <> struct Fmt<FMT_Q5_K> {
   static constexpr int SB_BYTES = 176;
   static constexpr int PAIR_DWORDS = 20;  // header + qh[32] + 32 B of qs
+};
+template <> struct Fmt<FMT_IQ2_S> {
+  static constexpr int SB_BYTES = 82;
+  static constexpr int PAIR_DWORDS = 10;  // index window 3 + sign window 3 + qh pair + scale pair + d + shift
 };
 template <> struct Fmt<FMT_Q6_K> {
   static constexpr int SB_BYTES = 210;
@@ -66,6 +76,15 @@ __device__ __forceinline__ void load_unit_kq(const uint8_t *wrow, int p, uint32_
   } else if constexpr (FMT == FMT_Q5_K) {
     load_dwords<12>(reinterpret_cast<const uint32_t *>(sb), dw);  // header + qh
     load_dwords<8>(reinterpret_cast<const uint32_t *>(sb + 48 + 32 * g), dw + 12);
+  } else if constexpr (FMT == FMT_IQ2_S) {
+    // super-blocks are 2-byte aligned; both 8-byte windows sit 2 bytes past a dword boundary
+    // exactly when the super-block starts on one
+    load_dwords<3>(dword_floor<FMT>(sb + 2 + 8 * g), dw);
+    load_dwords<3>(dword_floor<FMT>(sb + 34 + 8 * g), dw + 3);
+    dw[6] = *reinterpret_cast<const uint16_t *>(sb + 66 + 2 * g);  // qh of sub-blocks 2g, 2g+1
+    dw[7] = *reinterpret_cast<const uint16_t *>(sb + 74 + 2 * g);  // their scales
+    dw[8] = *reinterpret_cast<const uint16_t *>(sb);                // d
+    dw[9] = (reinterpret_cast<uintptr_t>(sb) & 2) ? 0u : 16u;
   } else {
     const int h = g >> 1, part = g & 1;
     const bool odd = (reinterpret_cast<uintptr_t>(sb) & 2) != 0;  // 2 bytes past a dword boundary
@@ -161,6 +180,41 @@ __device__ __forceinline__ void unit_dot_kq(const uint32_t (&dw)[Fmt<FMT>::PAIR_
         const float ps = block_dot(wv, lds + m * P * XPAIR_STRIDE + p * XPAIR_STRIDE + 64 * h);
         const float s = sx[m * 2 * P + 2 * p + h];
         acc[m] = fmaf(ds, fmaf(-1024.0f, s, ps), fmaf(-dm, s, acc[m]));
+      }
+    }
+  } else if constexpr (FMT == FMT_IQ2_S) {
+    const uint32_t sh = dw[9];
+    const uint32_t ix[2] = {__builtin_amdgcn_alignbit(dw[1], dw[0], sh), __builtin_amdgcn_alignbit(dw[2], dw[1], sh)};
+    const uint32_t sg[2] = {__builtin_amdgcn_alignbit(dw[4], dw[3], sh), __builtin_amdgcn_alignbit(dw[5], dw[4], sh)};
+    const float d = half_bits_to_f32(dw[8]) * 0.25f;
+    const uint2 *grid = reinterpret_cast<const uint2 *>(sx + 2 * M * P);
+    const h2 m1024 = h2{static_cast<_Float16>(-1024.0f), static_cast<_Float16>(-1024.0f)};
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const int ib = l >> 2, l2 = l & 3;
+      const uint32_t idx = __builtin_amdgcn_ubfe(ix[l >> 2], 8 * (l & 3), 8) |
+                           (__builtin_amdgcn_ubfe(dw[6], 8 * ib + 2 * l2, 2) << 8);
+      const uint2 e = grid[idx];
+      const uint32_t sb8 = __builtin_amdgcn_ubfe(sg[l >> 2], 8 * (l & 3), 8);
+      const float dl = d * (0.5f + static_cast<float>(__builtin_amdgcn_ubfe(dw[7], 8 * ib + 4 * (l2 >> 1), 4)));
+      h2 wv[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t src = k < 2 ? e.x : e.y;
+        h2 w = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, src, (k & 1) ? SEL_B23 : SEL_B01)) + m1024;
+        const uint32_t neg = (__builtin_amdgcn_ubfe(sb8, 2 * k, 1) << 15) | (__builtin_amdgcn_ubfe(sb8, 2 * k + 1, 1) << 31);
+        wv[k] = __builtin_bit_cast(h2, __builtin_bit_cast(uint32_t, w) ^ neg);
+      }
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const u4 xv = *reinterpret_cast<const u4 *>(lds + m * P * XPAIR_STRIDE + p * XPAIR_STRIDE + 64 * ib + 16 * l2);
+        float ps = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t xw = xv[k];
+          ps = __builtin_amdgcn_fdot2(wv[k], __builtin_bit_cast(h2, xw), ps, false);
+        }
+        acc[m] = fmaf(dl, ps, acc[m]);
       }
     }
   } else {

@@ -17,10 +17,11 @@ GGML_Q8_0 = 8
 GGML_Q4_K = 12
 GGML_Q5_K = 13
 GGML_Q6_K = 14
-KQUANTS = (GGML_Q4_K, GGML_Q5_K, GGML_Q6_K)
+GGML_IQ2_S = 22
+KQUANTS = (GGML_Q4_K, GGML_Q5_K, GGML_Q6_K, GGML_IQ2_S)
 
-BLOCK_BYTES = {GGML_Q4_0: 18, GGML_Q8_0: 34, GGML_Q4_K: 144, GGML_Q5_K: 176, GGML_Q6_K: 210}
-BLOCK_WEIGHTS = {GGML_Q4_0: 32, GGML_Q8_0: 32, GGML_Q4_K: 256, GGML_Q5_K: 256, GGML_Q6_K: 256}
+BLOCK_BYTES = {GGML_Q4_0: 18, GGML_Q8_0: 34, GGML_Q4_K: 144, GGML_Q5_K: 176, GGML_Q6_K: 210, GGML_IQ2_S: 82}
+BLOCK_WEIGHTS = {GGML_Q4_0: 32, GGML_Q8_0: 32, GGML_Q4_K: 256, GGML_Q5_K: 256, GGML_Q6_K: 256, GGML_IQ2_S: 256}
 
 _DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.float64: F64}
 

@@ -37,12 +37,13 @@ def exl3_tensors(rng, K, N):
     return trellis, suh, svh
 
 
-KQ_BYTES = {12: 144, 13: 176, 14: 210}
+KQ_BYTES = {12: 144, 13: 176, 14: 210, 22: 82}
 
 
 def kquant_weights(rng, ty, N, K):
-    """Packed Q4_K (12) / Q5_K (13) / Q6_K (14) bytes uint8 [N * K/256 * block]: uniform random
-    quant, scale and high-bit bytes; the fp16 fields (d and dmin; Q6_K: d) = |N(0, 1e-4)|."""
+    """Packed Q4_K (12) / Q5_K (13) / Q6_K (14) / IQ2_S (22) bytes uint8 [N * K/256 * block]:
+    uniform random quant, index, sign, scale and high-bit bytes; the fp16 fields (d and dmin;
+    Q6_K and IQ2_S: d) = |N(0, 1e-4)|."""
     nb = N * (K // 256)
     sb = KQ_BYTES[ty]
     blk = rng.integers(0, 256, (nb, sb), dtype=np.uint8)
@@ -50,6 +51,8 @@ def kquant_weights(rng, ty, N, K):
     if ty in (12, 13):
         blk[:, 0:2] = f16()
         blk[:, 2:4] = f16()
+    elif ty == 22:
+        blk[:, 0:2] = f16()
     else:
         blk[:, 208:210] = f16()
     return blk.reshape(-1)
