@@ -35,11 +35,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="stack",
-                    choices=["stack", "stack_chain", "gemv1", "kquant", "producers", "exl3", "prefill", "prefill_i8",
-                             "moe", "copy"])
+                    choices=["stack", "stack_chain", "gemv1", "kquant", "producers", "router", "exl3", "prefill",
+                             "prefill_i8", "moe", "copy"])
     ap.add_argument("--wtype", type=int, default=12, choices=[12, 13, 14, 22],
                     help="GGML type id for --config kquant (12 Q4_K, 13 Q5_K, 14 Q6_K, 22 IQ2_S)")
-    ap.add_argument("--tokens", type=int, default=16, help="tokens for --config moe")
+    ap.add_argument("--tokens", type=int, default=16, help="tokens for --config moe / router")
     ap.add_argument("--batch", type=int, default=1, help="batch for --config exl3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--seed", type=int, default=0)
@@ -307,6 +307,27 @@ def run_producers(args, torch, dev):
                 bytes_per_step=(rms_bytes + swi_bytes) * 16, launches_per_step=len(launches))
 
 
+def run_router(args, torch, dev):
+    """GLM-5 router logits: T tokens of 6144 (bf16) against the 256 x 6144 bf16 gate weight,
+    float64 accumulation and output, 8 rotated weight copies per graph."""
+    from vybforge_amd import ops
+    T, E, H = args.tokens, 256, 6144
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    ws = [(torch.randn(E, H, generator=gen, device=dev) * 0.02).to(torch.bfloat16) for _ in range(8)]
+    x = torch.randn(T, H, generator=gen, device=dev).to(torch.bfloat16)
+    ms, wall = timed_graph(torch, [lambda w=w: ops.router_logits(x, w) for w in ws], args.steps, args.warmup)
+    per = ms / len(ws)
+    nbytes = E * H * 2 + T * H * 2 + T * E * 8
+    value = nbytes / (per * 1e-3) / 1e9
+    roofline = dict(bound="hbm", achieved=round(value, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(value / HBM_PEAK_GBS, 4), traffic=None, kernel="k_router_logits<bf16, bf16>",
+                    avg_launch_us=round(per * 1e3, 3), bytes_per_launch=nbytes)
+    return dict(value=value, ms_step=ms, wall=wall, roofline=roofline, flops=2 * T * E * H * len(ws),
+                workload=f"GLM-5 router logits T={T}: 256 x 6144 bf16 gate, float64 accumulation",
+                bytes_per_step=nbytes * len(ws), launches_per_step=len(ws))
+
+
 def timed_graph(torch, launches, steps, warmup):
     """Capture the launches as one graph; return (ms per replay, wall seconds)."""
     for f in launches:
@@ -522,6 +543,8 @@ def main():
         r = run_kquant(args, torch, dev)
     elif args.config == "producers":
         r = run_producers(args, torch, dev)
+    elif args.config == "router":
+        r = run_router(args, torch, dev)
     elif args.config == "exl3":
         r = run_exl3(args, torch, dev)
     elif args.config == "prefill":

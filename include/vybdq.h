@@ -118,6 +118,14 @@ int vybdq_gemv_q4_0_seg3(uint64_t X, int64_t K, int x_dt, int order,
                          uint64_t W2, uint64_t Y2, int64_t N2, int y_dt2,
                          uint64_t W3, uint64_t Y3, int64_t N3, int y_dt3, uint64_t stream);
 
+/* Router logits Y [T, E] = X [T, H] W^T with W [E, H] (w_dt F32, F16 or BF16; the checkpoint's
+   router weight is bf16), X of x_dt (F32, F16, BF16 or F64), accumulated in float64 (every
+   product exact; fixed lane-strided order); y_dt F64 or F32. vybdq_moe_route / vybdq_moe_forward
+   take F64 logits as they are. Replaces the router GEMM of native/glm53/glm_engine.vyb:2728-2745
+   (deq_bf16 to float64, then a float64 matmul). */
+int vybdq_router_logits(uint64_t X, int x_dt, uint64_t W, int w_dt, uint64_t Y, int y_dt, int64_t T,
+                        int64_t E, int64_t H, uint64_t stream);
+
 /* ---- producer-side q8 activation quantization ---------------------------------------- */
 
 /* Per row of X [M, N]: y = x * r * w with r = 1 / sqrt(sum x^2 / N + eps), in float64 with the

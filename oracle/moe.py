@@ -21,6 +21,36 @@ def sigmoid(x):
     return 1.0 / (1.0 + np.exp(-x))
 
 
+def router_logits_f64(x, w):
+    """Router logits [T, E] = x [T, H] w [E, H]^T in float64 in the library's summation order
+    (H % 32 == 0): wave q of 4 sums the quarter [q H/4, (q+1) H/4), lane l of 64 the elements
+    q H/4 + 512 k + 8 l + j in (k, j) order, each as a product then a sum; the 64 lane sums fold
+    as s_l + s_(l xor d), d = 32 .. 1; the wave sums add as ((w0 + w1) + w2) + w3
+    (glm_engine.vyb:2728-2745 computes the same float64 matmul in its own order)."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    T, H = x.shape
+    E = w.shape[0]
+    Hq = H // 4
+    lanes = np.arange(64)
+    out = np.empty((T, E))
+    for t in range(T):
+        ws = []
+        for q in range(4):
+            part = np.zeros((E, 64))
+            for k in range(0, Hq, 512):
+                for j in range(8):
+                    h = q * Hq + k + 8 * lanes + j
+                    ok = (k + 8 * lanes) < Hq
+                    hh = np.where(ok, h, 0)
+                    part = np.where(ok[None, :], part + x[t, hh][None, :] * w[:, hh], part)
+            for d in (32, 16, 8, 4, 2, 1):
+                part = part + part[:, lanes ^ d]
+            ws.append(part[:, 0])
+        out[t] = ((ws[0] + ws[1]) + ws[2]) + ws[3]
+    return out
+
+
 def route_logits(logits, topk=8, bias=None, scale=SCALE):
     """logits [T, E] -> (idx int64 [T, topk], w float64 [T, topk]) (moe_ref.py:68-78)."""
     scores = sigmoid(logits)

@@ -17,6 +17,10 @@ imports and runs no reference code. Outputs, all in this directory:
                                   them in native/gguf/iq2s_tables.py, read as text (the hex
                                   literals), not imported; the library build turns it into a
                                   device table, the oracle reads it
+  router_golden.npz               the router inputs of the same prep: y (4 x 4096 float32) and the
+                                  gate weight (288 x 4096, exactly bf16 values, stored as bf16
+                                  bits), so the router GEMM can be checked end to end against the
+                                  reference's routing ids/weights in moe_golden.npz
   moe_golden.npz                  from native/glm53/prep/*.f32 (prepare_moe_fixture.py:21-70):
                                   router logits (y @ gate^T in float64), bias, the reference's
                                   routing ids/weights, the expert pre-activations g/u (float64),
@@ -103,6 +107,16 @@ def moe():
         scale=np.float64(2.5), limit=np.float64(10.0))
 
 
+def router():
+    P = os.path.join(REF, "native/glm53/prep")
+    f = lambda n, shape: np.fromfile(os.path.join(P, n + ".f32"), dtype="<f4").reshape(shape)
+    y, gate = f("y", (4, 4096)), f("gate", (288, 4096))
+    bits = gate.view(np.uint32)
+    assert (bits & 0xFFFF).max() == 0, "gate weights are not exactly bf16"
+    np.savez_compressed(os.path.join(HERE, "router_golden.npz"), y=y, gate_bf16=(bits >> 16).astype(np.uint16),
+                        source=np.array(SRC_NOTE))
+
+
 def iq2s_grid():
     import re
     p = os.path.join(REF, "native/gguf/iq2s_tables.py")
@@ -126,5 +140,6 @@ if __name__ == "__main__":
     q4_0_fixture()
     exl3_map()
     moe()
+    router()
     iq2s_grid()
     print("goldens written to", HERE)

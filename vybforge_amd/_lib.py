@@ -50,6 +50,7 @@ SIGNATURES = {
     "vybdq_gguf_slab_offset": [_i64, _i64, _i64],
     "vybdq_gguf_slab_bytes": [_i64, _i64],
     "vybdq_gguf_load_slab": [_i64, _u64, _i64, _i64, _int, _u64],
+    "vybdq_router_logits": [_u64, _int, _u64, _int, _u64, _int, _i64, _i64, _i64, _u64],
     "vybdq_rmsnorm_q8": [_u64, _u64, _u64, _u64, _u64, _u64, _i64, _i64, ctypes.c_double, _int, _int, _u64],
     "vybdq_swiglu_q8": [_u64, _u64, _u64, _u64, _u64, _i64, _int, _int, _u64],
     "vybdq_chain_workspace_size": [_int],

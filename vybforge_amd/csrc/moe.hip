@@ -32,6 +32,13 @@ int dq_gemm_grouped(int wtype, bool swiglu, const uint8_t *W, const uint8_t *W2,
                     hipStream_t s);
 int dq_gemm_bm();
 
+// A router logit as float64 (F64 logits as stored; F32 / F16 / BF16 widened exactly).
+template <int LDT>
+__device__ __forceinline__ double load_logit(const void *p, int64_t i) {
+  if constexpr (LDT == VYBDQ_F64) return static_cast<const double *>(p)[i];
+  else return static_cast<double>(load_elem<LDT>(p, i));
+}
+
 // Largest 64-bit value over the wave, on the VALU (DPP steps as in group_sum), in every lane.
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   auto step = [&](auto ctrl, auto rows) {
@@ -113,7 +120,7 @@ __global__ void __launch_bounds__(64) k_moe_route(const void *__restrict__ logit
   for (int i = 0; i < PER; ++i) {
     const int e = lane + 64 * i;
     if (e < E) {
-      const double l = static_cast<double>(load_elem<LDT>(logits, static_cast<int64_t>(t) * E + e));
+      const double l = load_logit<LDT>(logits, static_cast<int64_t>(t) * E + e);
       score[i] = 1.0 / (1.0 + exp(-l));
       key[i] = bias ? score[i] + static_cast<double>(bias[e]) : l;
     } else {
@@ -340,26 +347,33 @@ extern "C" int64_t vybdq_moe_workspace_size(int64_t T, int64_t H, int64_t I, int
   return moe_layout(nullptr, T, H, I, E, topk).bytes;
 }
 
+// The router launch: without a selection bias and with 32-bit or narrower logits, the keyed
+// kernel (selection by logit); otherwise the double-precision kernel (F64 logits select by
+// their own value, with the same ties-to-the-lower-id rule).
+static int launch_route(const void *lg, int logits_dt, const float *bias, int64_t T, int64_t E, int64_t topk,
+                        double scale, int *idx, float *w, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(T)), block(64);
+  const int e = static_cast<int>(E), k = static_cast<int>(topk);
+  if (logits_dt == VYBDQ_F64) {
+    hipLaunchKernelGGL((k_moe_route<VYBDQ_F64>), grid, block, 0, s, lg, bias, e, k, scale, idx, w);
+  } else if (!bias) {
+    VYBDQ_DISPATCH_IN(logits_dt, LDT,
+        hipLaunchKernelGGL((k_moe_route_logit<LDT>), grid, block, 0, s, lg, e, k, scale, idx, w));
+  } else {
+    VYBDQ_DISPATCH_IN(logits_dt, LDT, hipLaunchKernelGGL((k_moe_route<LDT>), grid, block, 0, s, lg, bias, e, k, scale, idx, w));
+  }
+  return check_launch("moe route");
+}
+
 extern "C" int vybdq_moe_route(uint64_t logits, int logits_dt, uint64_t bias, uint64_t idx_out, uint64_t w_out,
                                int64_t T, int64_t E, int64_t topk, double scale, uint64_t stream) {
   VYBDQ_REQUIRE(logits && idx_out && w_out, VYBDQ_ERR_ARG, "null logits, idx_out or w_out");
-  VYBDQ_REQUIRE(dt_valid_in(logits_dt), VYBDQ_ERR_ARG, "logits_dt must be F32, F16 or BF16");
+  VYBDQ_REQUIRE(dt_valid_out(logits_dt), VYBDQ_ERR_ARG, "logits_dt must be F32, F16, BF16 or F64");
   VYBDQ_REQUIRE(T >= 1 && T < (1 << 24) && E >= 1 && E <= 1024 && topk >= 1 && topk <= E && topk <= 64,
                 VYBDQ_ERR_SHAPE, "need 1 <= topk <= E <= 1024 and topk <= 64");
-  hipStream_t s = as_stream(stream);
-  const void *lg = reinterpret_cast<const void *>(logits);
-  if (!bias) {
-    VYBDQ_DISPATCH_IN(logits_dt, LDT,
-        hipLaunchKernelGGL((k_moe_route_logit<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg,
-                           static_cast<int>(E), static_cast<int>(topk), scale, reinterpret_cast<int *>(idx_out),
-                           reinterpret_cast<float *>(w_out)));
-    return check_launch("vybdq_moe_route");
-  }
-  VYBDQ_DISPATCH_IN(logits_dt, LDT,
-      hipLaunchKernelGGL((k_moe_route<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg,
-                         reinterpret_cast<const float *>(bias), static_cast<int>(E), static_cast<int>(topk), scale,
-                         reinterpret_cast<int *>(idx_out), reinterpret_cast<float *>(w_out)));
-  return check_launch("vybdq_moe_route");
+  return launch_route(reinterpret_cast<const void *>(logits), logits_dt, reinterpret_cast<const float *>(bias), T, E,
+                      topk, scale, reinterpret_cast<int *>(idx_out), reinterpret_cast<float *>(w_out),
+                      as_stream(stream));
 }
 
 extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logits, int logits_dt, uint64_t bias,
@@ -371,7 +385,8 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
   VYBDQ_REQUIRE(x && logits && w_gate && w_up && w_down && out, VYBDQ_ERR_ARG, "null input or output");
   VYBDQ_REQUIRE((s_gate == 0) == (s_up == 0) && (s_up == 0) == (s_down == 0), VYBDQ_ERR_ARG,
                 "shared expert: give all three matrices or none");
-  VYBDQ_REQUIRE(dt_valid_in(x_dt) && dt_valid_in(logits_dt), VYBDQ_ERR_ARG, "x_dt/logits_dt must be F32, F16 or BF16");
+  VYBDQ_REQUIRE(dt_valid_in(x_dt), VYBDQ_ERR_ARG, "x_dt must be F32, F16 or BF16");
+  VYBDQ_REQUIRE(dt_valid_out(logits_dt), VYBDQ_ERR_ARG, "logits_dt must be F32, F16, BF16 or F64");
   VYBDQ_REQUIRE(out_dt == VYBDQ_F32 || out_dt == VYBDQ_F16 || out_dt == VYBDQ_BF16, VYBDQ_ERR_ARG,
                 "out_dt must be F32, F16 or BF16");
   const int64_t need = vybdq_moe_workspace_size(T, H, I, E, topk);
@@ -390,18 +405,8 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
     const bool shared = s_gate != 0;
     int *idx = idx_out ? reinterpret_cast<int *>(idx_out) : m.idx;
     float *wts = w_out ? reinterpret_cast<float *>(w_out) : m.w;
-    const void *lg = reinterpret_cast<const void *>(logits);
-    const float *bs = reinterpret_cast<const float *>(bias);
-    if (bs) {
-      VYBDQ_DISPATCH_IN(logits_dt, LDT,
-          hipLaunchKernelGGL((k_moe_route<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg, bs,
-                             static_cast<int>(E), static_cast<int>(topk), scale, idx, wts));
-    } else {
-      VYBDQ_DISPATCH_IN(logits_dt, LDT,
-          hipLaunchKernelGGL((k_moe_route_logit<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg,
-                             static_cast<int>(E), static_cast<int>(topk), scale, idx, wts));
-    }
-    int rc = check_launch("moe route");
+    int rc = launch_route(reinterpret_cast<const void *>(logits), logits_dt, reinterpret_cast<const float *>(bias), T,
+                          E, topk, scale, idx, wts, s);
     if (rc) return rc;
     // few tokens per expert: grouped GEMV (one tile per expert); else the grouped MFMA GEMM
     int gv_max = 64;  // measured crossover (T = 1..64: the GEMV path is faster)
@@ -552,12 +557,8 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
   const int n = static_cast<int>(T * topk);
   int *idx = idx_out ? reinterpret_cast<int *>(idx_out) : m.idx;
   float *wts = w_out ? reinterpret_cast<float *>(w_out) : m.w;
-  const void *lg = reinterpret_cast<const void *>(logits);
-  const float *bs = reinterpret_cast<const float *>(bias);
-  VYBDQ_DISPATCH_IN(logits_dt, LDT,
-      hipLaunchKernelGGL((k_moe_route<LDT>), dim3(static_cast<unsigned>(T)), dim3(64), 0, s, lg, bs,
-                         static_cast<int>(E), static_cast<int>(topk), scale, idx, wts));
-  int rc = check_launch("moe route");
+  int rc = launch_route(reinterpret_cast<const void *>(logits), logits_dt, reinterpret_cast<const float *>(bias), T, E,
+                        topk, scale, idx, wts, s);
   if (rc) return rc;
   const size_t sh = static_cast<size_t>(3 * E + 2) * 4;
   hipLaunchKernelGGL(k_moe_bucket, dim3(1), dim3(256), sh, s, idx, static_cast<int>(T), static_cast<int>(topk),

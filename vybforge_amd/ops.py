@@ -296,6 +296,16 @@ class GemmWorkspace:
         self.ptr = (self.buf.data_ptr() + 255) // 256 * 256 if self.nbytes else 0
 
 
+def router_logits(X, W, y_dtype=torch.float64):
+    """Y [T, E] = X [T, H] W^T (W [E, H]) accumulated in float64 (vybdq_router_logits)."""
+    T, H = X.shape
+    E = W.shape[0]
+    Y = torch.empty((T, E), dtype=y_dtype, device=X.device)
+    call("vybdq_router_logits", _ptr(X), _dt(X.dtype), _ptr(W), _dt(W.dtype), _ptr(Y), _dt(Y.dtype), T, E, H,
+         _stream())
+    return Y
+
+
 def moe_route(logits, topk, bias=None, scale=2.5):
     T, E = logits.shape
     idx = torch.empty((T, topk), dtype=torch.int32, device=logits.device)
