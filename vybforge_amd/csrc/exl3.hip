@@ -18,6 +18,8 @@
 // N (one 128-column Hadamard block) and reads 1 KB of contiguous trellis per step.
 #include "common.h"
 
+#include <cstdlib>
+
 namespace vybdq {
 
 #include "exl3_slots.inc"
@@ -93,6 +95,20 @@ __device__ __forceinline__ void lane_window(const uint16_t *__restrict__ trellis
   const int lane = threadIdx.x & 63;
   const int src = (lane & ~7) | ((lane - 1) & 7);
   w[1] = __shfl(c[3], src, 64);
+}
+
+// The lane window from an already loaded chunk c: dword 1 is lane j-1's last chunk dword (lane
+// 7's for j = 0), taken by DPP row shifts (lane - 1, or lane + 7 for j = 0).
+__device__ __forceinline__ void chunk_window(const u4 c, uint32_t (&w)[6]) {
+  const int j = threadIdx.x & 7;
+  const int prev = __builtin_amdgcn_update_dpp(0, static_cast<int>(c[3]), DPP_ROW_SHR + 1, 0xf, 0xf, false);
+  const int wrap = __builtin_amdgcn_update_dpp(0, static_cast<int>(c[3]), DPP_ROW_SHL + 7, 0xf, 0xf, false);
+  w[0] = 0;
+  w[1] = static_cast<uint32_t>(j == 0 ? wrap : prev);
+  w[2] = c[0];
+  w[3] = c[1];
+  w[4] = c[2];
+  w[5] = c[3];
 }
 
 // ---- decode-only: rotated basis What [K, N] ------------------------------------------------
@@ -258,6 +274,21 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   // the value to fp16 once and share it across the batch rows.
   constexpr bool HALVES = BP <= 2;
   constexpr bool FUSED = BP <= 2;  // x rotation and output rotation in this launch
+  // This wave's k-blocks and the first kD of its trellis chunks, loaded before anything else (they
+  // do not depend on x); the loop keeps kD chunks in flight per lane (a register ring).
+  constexpr int kD = 4;
+  const int per_wave = (nkb + 3) / 4;
+  const int w_begin = wave * per_wave;
+  const int w_end = min(w_begin + per_wave, nkb);
+  const int64_t nb = 8 * static_cast<int64_t>(g) + t;
+  auto load_chunk = [&](int kk) {
+    const int kc = kk < w_end ? kk : (w_end > w_begin ? w_end - 1 : 0);  // in range: re-read the last
+    const int64_t tile = static_cast<int64_t>(kb_begin + kc) * NB + nb;
+    return *reinterpret_cast<const u4 *>(trellis + tile * 64 + 8 * j);
+  };
+  u4 ring[kD];
+#pragma unroll
+  for (int d = 0; d < kD; ++d) ring[d] = load_chunk(w_begin + d);
   // 1. x' rows of this split: [BP][16 * nkb] fp16 (HALVES: u32 pairs (x, x))
   const int rows = 16 * nkb;
   const int nch = nkb / 8;
@@ -297,27 +328,34 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   float acc[BP][2];
 #pragma unroll
   for (int b = 0; b < BP; ++b) acc[b][0] = acc[b][1] = 0.f;
-  const int per_wave = (nkb + 3) / 4;
-  const int w_begin = wave * per_wave;
-  const int w_end = min(w_begin + per_wave, nkb);
-  const int64_t nb = 8 * static_cast<int64_t>(g) + t;
-  for (int kk = w_begin; kk < w_end; ++kk) {
+  auto step = [&](int kk, const u4 c) {
     uint32_t w[6];
-    lane_window(trellis, static_cast<int64_t>(kb_begin + kk) * NB + nb, j, w);
+    chunk_window(c, w);
     if constexpr (HALVES) {
-      const uint32_t *xd = reinterpret_cast<const uint32_t *>(smem);
+      // the 16 (x, x) pairs of this k-block per batch row: four 16-B LDS reads
+      uint32_t xq[BP][16];
+#pragma unroll
+      for (int b = 0; b < BP; ++b) {
+        const u4 *src = reinterpret_cast<const u4 *>(reinterpret_cast<const uint32_t *>(smem) + b * rows + 16 * kk);
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) {
+          const u4 v4 = src[c4];
+          xq[b][4 * c4 + 0] = v4[0];
+          xq[b][4 * c4 + 1] = v4[1];
+          xq[b][4 * c4 + 2] = v4[2];
+          xq[b][4 * c4 + 3] = v4[3];
+        }
+      }
 #pragma unroll
       for (int q = 0; q < 32; ++q) {
         uint32_t x = win_extract(w, kExl3SlotOff0[q]) & kExl3SlotMask0[q];
         if (kExl3SlotOff1[q] >= 0) x |= win_extract(w, kExl3SlotOff1[q]) & kExl3SlotMask1[q];
         const h2 y = __builtin_bit_cast(h2, decode_window_halves<CB>(x));
 #pragma unroll
-        for (int b = 0; b < BP; ++b) {
-          const h2 xv = __builtin_bit_cast(h2, xd[b * rows + 16 * kk + (q & 15)]);
-          acc[b][q >> 4] = __builtin_amdgcn_fdot2(y, xv, acc[b][q >> 4], false);
-        }
+        for (int b = 0; b < BP; ++b)
+          acc[b][q >> 4] = __builtin_amdgcn_fdot2(y, __builtin_bit_cast(h2, xq[b][q & 15]), acc[b][q >> 4], false);
       }
-      continue;
+      return;
     }
     _Float16 v[32];
     lane_decode<CB>(w, v);
@@ -337,6 +375,16 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
         const h2 xv = __builtin_bit_cast(h2, xw[i]);
         acc[b][0] = __builtin_amdgcn_fdot2(pj[i], xv, acc[b][0], false);
         acc[b][1] = __builtin_amdgcn_fdot2(pj8[i], xv, acc[b][1], false);
+      }
+    }
+  };
+  for (int k0 = w_begin; k0 < w_end; k0 += kD) {
+#pragma unroll
+    for (int d = 0; d < kD; ++d) {
+      if (k0 + d < w_end) {
+        const u4 c = ring[d];
+        ring[d] = load_chunk(k0 + d + kD);
+        step(k0 + d, c);
       }
     }
   }
@@ -419,10 +467,12 @@ struct Exl3Split {
 static Exl3Split exl3_splits(int64_t K, int64_t N, int BP) {
   const int KB = static_cast<int>(K / 16);
   const int64_t groups = N / 128;
-  int S = static_cast<int>((1024 + groups - 1) / groups);
-  const int smax = BP >= 8 ? 4 : 8;
-  if (S > smax) S = smax;
+  // measured at K = 5120, N = 17408: batch 1 is flat from 8 to 16 splits, batch 16 best at 16
+  const int64_t target = BP >= 8 ? 2048 : 1024;
+  int S = static_cast<int>((target + groups - 1) / groups);
+  if (S > 16) S = 16;
   if (S > KB / 4) S = KB / 4 > 0 ? KB / 4 : 1;
+  if (const char *e = getenv("VYBDQ_EXL3_SPLITS")) S = atoi(e);  // tuning override
   if (S < 1) S = 1;
   int kbs = (KB + S - 1) / S;
   kbs = (kbs + 7) / 8 * 8;

@@ -400,7 +400,8 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
   hipStream_t s = as_stream(stream);
   MoeWs m = moe_layout(reinterpret_cast<char *>(ws), T, H, I, E, topk);
   if (H % 256 == 0 && I % 256 == 0) {
-    const int MT = T > 16 ? 2 : 1;  // 16-row fragments per m-tile
+    int MT = T > 16 ? 2 : 1;  // 16-row fragments per m-tile (VYBDQ_MOE_MT overrides: 1 or 2)
+    if (const char *e = getenv("VYBDQ_MOE_MT")) MT = atoi(e) == 1 ? 1 : 2;
     const int n = static_cast<int>(T * topk);
     const bool shared = s_gate != 0;
     int *idx = idx_out ? reinterpret_cast<int *>(idx_out) : m.idx;
