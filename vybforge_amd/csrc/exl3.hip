@@ -46,6 +46,8 @@ __device__ __forceinline__ uint32_t decode_window_halves(uint32_t w) {
     hi = wl * 0x0551u;
     lo = wl * 0x7C72u + 0x03D45AA4u;
   }
+  // keeps the two 16 x 16-bit products apart (full-rate 24-bit multiplies): combined, the compiler
+  // would emit one quarter-rate 32-bit multiply
   asm volatile("" : "+v"(hi));
   const uint32_t x = (hi << 16) + lo;
   return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;

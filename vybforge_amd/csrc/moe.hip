@@ -67,9 +67,10 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // double-precision sigmoid is evaluated only for the k winners, in selection order (the same
 // arithmetic as k_moe_route).
 template <int LDT>
-__global__ void __launch_bounds__(64) k_moe_route_logit(const void *__restrict__ logits, int E, int topk, double scale,
-                                                        int *__restrict__ idx_out, float *__restrict__ w_out) {
-  const int t = blockIdx.x, lane = threadIdx.x;
+__device__ __forceinline__ void route_keyed(const void *__restrict__ logits, int t, int E, int topk, double scale,
+                                            int *__restrict__ idx_out, float *__restrict__ w_out,
+                                            int *__restrict__ idx_copy) {
+  const int lane = threadIdx.x & 63;
   constexpr int PER = 16;  // experts per lane (E <= 1024)
   uint64_t key[PER];
 #pragma unroll
@@ -94,7 +95,10 @@ __global__ void __launch_bounds__(64) k_moe_route_logit(const void *__restrict__
     for (int i = 0; i < PER; ++i)
       if (key[i] == bk) key[i] = 0;  // the owner retires the winner
     const uint32_t hk = static_cast<uint32_t>(bk >> 32);  // the logit's bits, mapped back
-    if (lane == 0) idx_out[t * topk + s] = be;
+    if (lane == 0) {
+      idx_out[t * topk + s] = be;
+      if (idx_copy) idx_copy[t * topk + s] = be;
+    }
     if (lane == s) my_l = __uint_as_float(hk ^ ((hk >> 31) ? 0x80000000u : 0xffffffffu));
   }
   // the k sigmoids in parallel (lane s: winner s), summed in selection order
@@ -110,10 +114,16 @@ __global__ void __launch_bounds__(64) k_moe_route_logit(const void *__restrict__
 }
 
 template <int LDT>
-__global__ void __launch_bounds__(64) k_moe_route(const void *__restrict__ logits, const float *__restrict__ bias,
-                                                  int E, int topk, double scale, int *__restrict__ idx_out,
-                                                  float *__restrict__ w_out) {
-  const int t = blockIdx.x, lane = threadIdx.x;
+__global__ void __launch_bounds__(64) k_moe_route_logit(const void *__restrict__ logits, int E, int topk, double scale,
+                                                        int *__restrict__ idx_out, float *__restrict__ w_out) {
+  route_keyed<LDT>(logits, blockIdx.x, E, topk, scale, idx_out, w_out, nullptr);
+}
+
+template <int LDT>
+__device__ __forceinline__ void route_double(const void *__restrict__ logits, const float *__restrict__ bias, int t,
+                                             int E, int topk, double scale, int *__restrict__ idx_out,
+                                             float *__restrict__ w_out, int *__restrict__ idx_copy) {
+  const int lane = threadIdx.x & 63;
   constexpr int PER = 16;  // experts per lane (E <= 1024)
   double key[PER];
   double score[PER];
@@ -151,11 +161,21 @@ __global__ void __launch_bounds__(64) k_moe_route(const void *__restrict__ logit
         if (ii == i) { sc = score[ii]; key[ii] = -INFINITY; }
     }
     sc = __shfl(sc, be & 63, 64);
-    if (lane == 0) idx_out[t * topk + s] = be;
+    if (lane == 0) {
+      idx_out[t * topk + s] = be;
+      if (idx_copy) idx_copy[t * topk + s] = be;
+    }
     if (lane == s) my_sc = sc;
     tot += sc;
   }
   if (lane < topk) w_out[t * topk + lane] = static_cast<float>(my_sc / (tot + 1e-20) * scale);
+}
+
+template <int LDT>
+__global__ void __launch_bounds__(64) k_moe_route(const void *__restrict__ logits, const float *__restrict__ bias,
+                                                  int E, int topk, double scale, int *__restrict__ idx_out,
+                                                  float *__restrict__ w_out) {
+  route_double<LDT>(logits, bias, blockIdx.x, E, topk, scale, idx_out, w_out, nullptr);
 }
 
 // One workgroup: per-expert counts, exclusive scans, and each (token, slot)'s bucket position
@@ -212,12 +232,10 @@ __global__ void __launch_bounds__(256) k_moe_bucket(const int *__restrict__ idx,
 // output row is computed from its own token row alone, and the combine reads through pos).
 // Two tile lists of the same rows are written, of at most BMr and BMr2 rows per tile (one per
 // grouped kernel of the layer); tiles2 may be null.
-__global__ void __launch_bounds__(256) k_moe_bucket_tiles(const int *__restrict__ idx, int T, int topk, int E, int BMr,
-                                                          int BMr2, int shared, int *__restrict__ pos,
-                                                          int *__restrict__ row_map, int4 *__restrict__ tiles,
-                                                          int *__restrict__ ntiles, int4 *__restrict__ tiles2,
-                                                          int *__restrict__ ntiles2) {
-  extern __shared__ int sh[];
+__device__ __forceinline__ void bucket_tiles(const int *idx, int T, int topk, int E, int BMr, int BMr2, int shared,
+                                             int *__restrict__ pos, int *__restrict__ row_map,
+                                             int4 *__restrict__ tiles, int *__restrict__ ntiles,
+                                             int4 *__restrict__ tiles2, int *__restrict__ ntiles2, int *sh) {
   int *cnt = sh;       // [E]
   int *cur = sh + E;   // [E]
   __shared__ int scan_r[256], scan_t[256], scan_t2[256];
@@ -280,6 +298,34 @@ __global__ void __launch_bounds__(256) k_moe_bucket_tiles(const int *__restrict_
     pos[i] = p;
     row_map[p] = i / topk;
   }
+}
+
+__global__ void __launch_bounds__(256) k_moe_bucket_tiles(const int *__restrict__ idx, int T, int topk, int E, int BMr,
+                                                          int BMr2, int shared, int *__restrict__ pos,
+                                                          int *__restrict__ row_map, int4 *__restrict__ tiles,
+                                                          int *__restrict__ ntiles, int4 *__restrict__ tiles2,
+                                                          int *__restrict__ ntiles2) {
+  extern __shared__ int sh[];
+  bucket_tiles(idx, T, topk, E, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2, sh);
+}
+
+// Few tokens: routing (wave w takes tokens w, w + 4, ...) and bucketing in one workgroup; the
+// routed ids also go to LDS, where the bucketing reads them.
+template <int LDT, bool KEYED>
+__global__ void __launch_bounds__(256) k_moe_route_bucket(const void *__restrict__ logits, const float *__restrict__ bias,
+                                                          int E, int topk, double scale, int *__restrict__ idx_out,
+                                                          float *__restrict__ w_out, int T, int BMr, int BMr2,
+                                                          int shared, int *__restrict__ pos, int *__restrict__ row_map,
+                                                          int4 *__restrict__ tiles, int *__restrict__ ntiles,
+                                                          int4 *__restrict__ tiles2, int *__restrict__ ntiles2) {
+  extern __shared__ int sh[];
+  int *idx_lds = sh + 2 * E;  // [T * topk]
+  for (int t = threadIdx.x >> 6; t < T; t += 4) {
+    if constexpr (KEYED) route_keyed<LDT>(logits, t, E, topk, scale, idx_out, w_out, idx_lds);
+    else route_double<LDT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds);
+  }
+  __syncthreads();
+  bucket_tiles(idx_lds, T, topk, E, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2, sh);
 }
 
 // out[t][h] = sum_s w[t,s] * rows[pos[t,s]][h] (+ shared[t][h]); fixed slot order.
@@ -406,9 +452,14 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
     const bool shared = s_gate != 0;
     int *idx = idx_out ? reinterpret_cast<int *>(idx_out) : m.idx;
     float *wts = w_out ? reinterpret_cast<float *>(w_out) : m.w;
-    int rc = launch_route(reinterpret_cast<const void *>(logits), logits_dt, reinterpret_cast<const float *>(bias), T,
-                          E, topk, scale, idx, wts, s);
-    if (rc) return rc;
+    // up to 8 tokens: routing and bucketing in one launch (below)
+    const bool fused_route = T <= 8;
+    int rc = VYBDQ_OK;
+    if (!fused_route) {
+      rc = launch_route(reinterpret_cast<const void *>(logits), logits_dt, reinterpret_cast<const float *>(bias), T, E,
+                        topk, scale, idx, wts, s);
+      if (rc) return rc;
+    }
     // few tokens per expert: grouped GEMV (one tile per expert); else the grouped MFMA GEMM
     int gv_max = 64;  // measured crossover (T = 1..64: the GEMV path is faster)
     if (const char *e = getenv("VYBDQ_MOE_GEMV_MAX_T")) gv_max = atoi(e);
@@ -420,10 +471,27 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
     if (mc > T) mc = static_cast<int>(T);  // no group holds more rows than there are tokens
     // tiles: m-tiles of 16 MT rows for the MFMA GEMM; tiles2: groups of at most mc rows for the GEMV
     const int BMr = 16 * MT;
-    hipLaunchKernelGGL(k_moe_bucket_tiles, dim3(1), dim3(256), static_cast<size_t>(2 * E) * 4, s, idx,
-                       static_cast<int>(T), static_cast<int>(topk), static_cast<int>(E), BMr, mc, shared ? 1 : 0,
-                       m.pos, m.row_map, m.tiles, m.ntiles, gv ? m.tiles2 : nullptr, gv ? m.ntiles2 : nullptr);
-    rc = check_launch("moe bucket");
+    if (fused_route) {
+      const void *lg = reinterpret_cast<const void *>(logits);
+      const float *bs = reinterpret_cast<const float *>(bias);
+      const size_t shb = static_cast<size_t>(2 * E + T * topk) * 4;
+      const int e = static_cast<int>(E), k = static_cast<int>(topk), tt = static_cast<int>(T);
+      int4 *t2 = gv ? m.tiles2 : nullptr;
+      int *n2 = gv ? m.ntiles2 : nullptr;
+#define RB(LDT, KEYED)                                                                                          \
+  hipLaunchKernelGGL((k_moe_route_bucket<LDT, KEYED>), dim3(1), dim3(256), shb, s, lg, bs, e, k, scale, idx, wts, tt, \
+                     BMr, mc, shared ? 1 : 0, m.pos, m.row_map, m.tiles, m.ntiles, t2, n2)
+      if (logits_dt == VYBDQ_F64) RB(VYBDQ_F64, false);
+      else if (bs) { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT, false)); }
+      else { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT, true)); }
+#undef RB
+      rc = check_launch("moe route + bucket");
+    } else {
+      hipLaunchKernelGGL(k_moe_bucket_tiles, dim3(1), dim3(256), static_cast<size_t>(2 * E) * 4, s, idx,
+                         static_cast<int>(T), static_cast<int>(topk), static_cast<int>(E), BMr, mc, shared ? 1 : 0,
+                         m.pos, m.row_map, m.tiles, m.ntiles, gv ? m.tiles2 : nullptr, gv ? m.ntiles2 : nullptr);
+      rc = check_launch("moe bucket");
+    }
     if (rc) return rc;
     const int max_tiles = static_cast<int>(moe_max_tiles(T, E, topk, BMr));
     const int64_t rb_h = (H / 64) * (wtype == 2 ? 36 : 68);  // row bytes, K = H
