@@ -22,7 +22,10 @@ import os
 import sys
 import time
 
-HBM_PEAK_GBS = 8000.0
+# roofline constants (MI355X datasheet, dense) live in roofline.json beside this file
+with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "roofline.json")) as _f:
+    ROOFLINE = json.load(_f)
+HBM_PEAK_GBS = float(ROOFLINE["hbm_GBps"])
 METRIC = "dequant-GEMV GB/s (% HBM peak) + prefill/MoE GEMM TFLOP/s (% MFMA peak)"
 
 QWEN3_4B = dict(hidden=2560, q=4096, kv=1024, inter=9728, layers=36)
@@ -116,10 +119,11 @@ def stack_launches(ops, layers, a):
     return out
 
 
-def cpu_baseline_stack(target_s=12.0):
-    """numpy oracle path on a bounded sample: q4_0 -> f32 decode, then BLAS matvec (1 thread)."""
+def cpu_baseline_stack(target_s=10.0, target_all_s=6.0):
+    """numpy oracle path on a bounded sample: q4_0 -> f32 decode, then BLAS matvec. The reported
+    value is one thread; the same sample is also timed with BLAS on every host core."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
+    from threadpoolctl import threadpool_info, threadpool_limits
     from oracle import formats
     from vybforge_amd import synth
     shapes, _, _, _ = stack_bytes()
@@ -127,21 +131,32 @@ def cpu_baseline_stack(target_s=12.0):
     mats = [(synth.q4_0_weights(rng, n, k), n, k) for n, k in shapes]
     xs = {k: rng.standard_normal(k).astype(np.float16) for _, k in shapes}
     layer_bytes = sum(raw.size + 2 * k + 2 * n for raw, n, k in mats)
-    done = 0
-    t0 = time.perf_counter()
-    with threadpool_limits(limits=1):
-        while True:
-            for raw, n, k in mats:
-                w = formats.dequant_q4_0(raw).reshape(n, k)
-                y = w @ xs[k].astype(np.float32)
-                y.astype(np.float16)
-            done += 1
-            el = time.perf_counter() - t0
-            if el >= target_s:
-                break
+
+    def run(limit, seconds):
+        done = 0
+        t0 = time.perf_counter()
+        with threadpool_limits(limits=limit):
+            while True:
+                for raw, n, k in mats:
+                    w = formats.dequant_q4_0(raw).reshape(n, k)
+                    y = w @ xs[k].astype(np.float32)
+                    y.astype(np.float16)
+                done += 1
+                el = time.perf_counter() - t0
+                if el >= seconds:
+                    return done, el
+
+    done, el = run(1, target_s)
+    ncpu = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    done_all, el_all = run(ncpu, target_all_s)
+    blas = ", ".join(f"{i.get('internal_api')} {i.get('version')}" for i in threadpool_info()
+                     if i.get("user_api") == "blas") or "unknown"
     return dict(value=round(layer_bytes * done / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
                 sample=f"{done} layers of the 36-layer stack (7 GEMVs each, 56.8 MB packed), "
-                       "numpy f32 decode + OpenBLAS matvec, 1 thread")
+                       "numpy f32 decode + BLAS matvec, 1 thread",
+                value_all_cores=round(layer_bytes * done_all / el_all / 1e9, 3), cores_all=ncpu,
+                host=dict(cpu_count=os.cpu_count(), affinity=ncpu, blas=blas,
+                          omp_num_threads=os.environ.get("OMP_NUM_THREADS")))
 
 
 def stack_chain(ops, layers, a, dev):
@@ -381,7 +396,7 @@ def run_exl3(args, torch, dev):
                 bytes_per_step=bytes_call * ncopy, launches_per_step=ncopy)
 
 
-MFMA_BF16_PEAK_TFLOPS = 2500.0
+MFMA_BF16_PEAK_TFLOPS = float(ROOFLINE["mfma_dense_TFLOPs"]["bf16"])
 
 
 def q8_0_blocks_gpu(torch, gen, N, K, dev):
@@ -425,7 +440,7 @@ def run_prefill(args, torch, dev):
                 bytes_per_step=nbytes, launches_per_step=len(launches))
 
 
-MFMA_I8_PEAK_TOPS = 5000.0
+MFMA_I8_PEAK_TOPS = float(ROOFLINE["mfma_dense_TFLOPs"]["int8_TOPs"])
 
 
 def run_prefill_i8(args, torch, dev):

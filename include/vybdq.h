@@ -183,6 +183,44 @@ int64_t vybdq_gguf_slab_bytes(int64_t h, int64_t align);
 int vybdq_gguf_load_slab(int64_t h, uint64_t dev, int64_t dev_bytes, int64_t align, int absolute,
                          uint64_t stream);
 
+/* ---- safetensors reader and sharded-checkpoint index (host) ------------------------- */
+
+/* Opens and indexes a safetensors file (u64 LE header length, JSON header, data region): every
+   tensor's dtype, shape and byte range (checked against the file and, for the sized dtypes,
+   against shape x element size) and the __metadata__ strings. Returns a handle >= 1 or a
+   negative error code. Replaces native/torchload/safetensors.vyb (container layout :8-19,
+   dtype table :48-66). */
+int64_t vybdq_st_open(const char *path);
+int vybdq_st_close(int64_t h);
+/* what: 0 tensor count, 1 metadata count, 2 header length, 3 data region start, 4 file size */
+int64_t vybdq_st_info(int64_t h, int what);
+/* tensor index (header order) of name, -1 if absent */
+int64_t vybdq_st_find(int64_t h, const char *name);
+/* copy the name / dtype spelling (NUL-terminated, at most cap - 1 bytes); return full length */
+int64_t vybdq_st_tensor_name(int64_t h, int64_t i, char *buf, int64_t cap);
+int64_t vybdq_st_tensor_dtype(int64_t h, int64_t i, char *buf, int64_t cap);
+/* what: 0 element size (0 for a dtype not sized here), 1 ndim, 2 + d shape[d], -1 absolute file
+   offset of the data, -2 data bytes */
+int64_t vybdq_st_tensor_field(int64_t h, int64_t i, int what);
+/* __metadata__ value for key (full length), -1 if absent */
+int64_t vybdq_st_meta(int64_t h, const char *key, char *buf, int64_t cap);
+/* key of metadata pair i (header order; full length) */
+int64_t vybdq_st_meta_key(int64_t h, int64_t i, char *buf, int64_t cap);
+/* tensor i's bytes into host memory (cap >= its size); returns the byte count */
+int64_t vybdq_st_read(int64_t h, int64_t i, void *dst, int64_t cap);
+/* tensor i's bytes into device memory dev (dev_bytes >= its size), ordered on stream; returns the
+   byte count after the copies have finished */
+int64_t vybdq_st_upload(int64_t h, int64_t i, uint64_t dev, int64_t dev_bytes, uint64_t stream);
+/* model.safetensors.index.json: tensor name -> shard file through "weight_map" (the name -> shard
+   step of native/glm53/gx.vyb:1-16). */
+int64_t vybdq_st_index_open(const char *path);
+int vybdq_st_index_close(int64_t h);
+int64_t vybdq_st_index_count(int64_t h);
+/* entry i (file order): copies the tensor name and its shard file; returns the name's full length */
+int64_t vybdq_st_index_entry(int64_t h, int64_t i, char *name, int64_t name_cap, char *shard, int64_t shard_cap);
+/* shard file of a tensor (full length), -1 if the index does not list it */
+int64_t vybdq_st_index_shard(int64_t h, const char *name, char *buf, int64_t cap);
+
 /* ---- persistent chain of dependent GEMV stages --------------------------------------- */
 
 /* Bytes of workspace vybdq_gemv_chain needs for nstages stages (a status word and one counter

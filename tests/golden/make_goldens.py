@@ -134,6 +134,25 @@ def iq2s_grid():
     print("wrote", out)
 
 
+def st_header():
+    """The header of the reference's safetensors fixture (the 66 MB LoRA adapter its container gate
+    reads, native/torchload/st_ref.py:38): the 8-byte length, the JSON bytes (gzipped) and the data
+    region size. Tests rebuild a file of the same layout with a zero data region."""
+    import gzip
+    src = os.path.join(REF, "artifacts", "vybos-configurator-lora", "adapter_model.safetensors")
+    size = os.path.getsize(src)
+    with open(src, "rb") as f:
+        n = int.from_bytes(f.read(8), "little")
+        hdr = f.read(n)
+    out = os.path.join(HERE, "st_lora_header.json.gz")
+    with gzip.GzipFile(out, "wb", mtime=0) as g:
+        g.write(hdr)
+    json.dump({"source": SRC_NOTE + " (artifacts/vybos-configurator-lora/adapter_model.safetensors)",
+               "header_len": n, "data_size": size - 8 - n},
+              open(os.path.join(HERE, "st_lora_header.meta.json"), "w"), indent=1)
+    print("wrote", out)
+
+
 if __name__ == "__main__":
     if not os.path.isdir(REF):
         sys.exit(f"reference checkout not found at {REF}")
@@ -142,4 +161,5 @@ if __name__ == "__main__":
     moe()
     router()
     iq2s_grid()
+    st_header()
     print("goldens written to", HERE)

@@ -50,6 +50,22 @@ SIGNATURES = {
     "vybdq_gguf_slab_offset": [_i64, _i64, _i64],
     "vybdq_gguf_slab_bytes": [_i64, _i64],
     "vybdq_gguf_load_slab": [_i64, _u64, _i64, _i64, _int, _u64],
+    "vybdq_st_open": [ctypes.c_char_p],
+    "vybdq_st_close": [_i64],
+    "vybdq_st_info": [_i64, _int],
+    "vybdq_st_find": [_i64, ctypes.c_char_p],
+    "vybdq_st_tensor_name": [_i64, _i64, ctypes.c_char_p, _i64],
+    "vybdq_st_tensor_dtype": [_i64, _i64, ctypes.c_char_p, _i64],
+    "vybdq_st_tensor_field": [_i64, _i64, _int],
+    "vybdq_st_meta": [_i64, ctypes.c_char_p, ctypes.c_char_p, _i64],
+    "vybdq_st_meta_key": [_i64, _i64, ctypes.c_char_p, _i64],
+    "vybdq_st_read": [_i64, _i64, ctypes.c_void_p, _i64],
+    "vybdq_st_upload": [_i64, _i64, _u64, _i64, _u64],
+    "vybdq_st_index_open": [ctypes.c_char_p],
+    "vybdq_st_index_close": [_i64],
+    "vybdq_st_index_count": [_i64],
+    "vybdq_st_index_entry": [_i64, _i64, ctypes.c_char_p, _i64, ctypes.c_char_p, _i64],
+    "vybdq_st_index_shard": [_i64, ctypes.c_char_p, ctypes.c_char_p, _i64],
     "vybdq_router_logits": [_u64, _int, _u64, _int, _u64, _int, _i64, _i64, _i64, _u64],
     "vybdq_rmsnorm_q8": [_u64, _u64, _u64, _u64, _u64, _u64, _i64, _i64, ctypes.c_double, _int, _int, _u64],
     "vybdq_swiglu_q8": [_u64, _u64, _u64, _u64, _u64, _i64, _int, _int, _u64],
@@ -77,7 +93,10 @@ _RESTYPE = {"vybdq_last_error": ctypes.c_char_p, "vybdq_chain_workspace_size": c
             "vybdq_gguf_kv_float": ctypes.c_double}
 for _n in ("vybdq_gguf_open", "vybdq_gguf_info", "vybdq_gguf_find_tensor", "vybdq_gguf_find_kv",
            "vybdq_gguf_tensor_name", "vybdq_gguf_tensor_field", "vybdq_gguf_kv_key", "vybdq_gguf_kv_field",
-           "vybdq_gguf_kv_string", "vybdq_gguf_read_tensor", "vybdq_gguf_slab_offset", "vybdq_gguf_slab_bytes"):
+           "vybdq_gguf_kv_string", "vybdq_gguf_read_tensor", "vybdq_gguf_slab_offset", "vybdq_gguf_slab_bytes",
+           "vybdq_st_open", "vybdq_st_info", "vybdq_st_find", "vybdq_st_tensor_name", "vybdq_st_tensor_dtype",
+           "vybdq_st_tensor_field", "vybdq_st_meta", "vybdq_st_meta_key", "vybdq_st_read", "vybdq_st_upload",
+           "vybdq_st_index_open", "vybdq_st_index_count", "vybdq_st_index_entry", "vybdq_st_index_shard"):
     _RESTYPE[_n] = ctypes.c_int64
 
 
