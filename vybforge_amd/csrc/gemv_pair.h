@@ -153,9 +153,11 @@ static int pair_umax(int fmt) {
 
 // For one X row (decode): the widest G that still gives each lane at least two pairs (two pair
 // windows in flight per lane; one-pair lanes were measured slower at every decode shape), widened
-// further while the grid has fewer workgroups than CUs, 256 threads, and a batch of exactly
-// ceil(P / G) pairs (up to the format's largest). For batches (M > 1) the smallest G with ~4 waves
-// per CU whose row fits one widest batch. VYBDQ_GEMV_PLAN="G,U,T" overrides the plan.
+// further while the grid would hold fewer rows than 64 / G per CU x 4 waves, a batch of exactly
+// ceil(P / G) pairs (up to the format's largest), narrowed while the grid would not be resident in
+// one round; 256 threads (one workgroup of 16 waves per CU was measured 16% slower on the decode
+// stack). For batches (M > 1) the smallest G with ~4 waves per CU whose row fits one widest batch.
+// VYBDQ_GEMV_PLAN="G,U,T" overrides the plan.
 static PairPlan pair_plan(int fmt, int64_t rows, int P, int64_t M) {
   const int umax = pair_umax(fmt);
   PairPlan pl{64, umax, 256};
@@ -167,6 +169,10 @@ static PairPlan pair_plan(int fmt, int64_t rows, int P, int64_t M) {
     int G = 8;
     while (G < 64 && (P + 2 * G - 1) / (2 * G) >= 2) G *= 2;  // ceil(P / 2G) >= 2
     while (G < 64 && rows * G / 256 < device_cu_count()) G *= 2;
+    // more waves than fit at once (8 per SIMD) would start a second round one HBM latency late:
+    // narrow G (more pairs per lane) until the grid is resident in one round
+    const int64_t resident = 32LL * device_cu_count();
+    while (G > 16 && rows * G / 64 > resident) G /= 2;
     const int U = (P + G - 1) / G;
     pl.G = G;
     pl.U = U < umax ? U : umax;
