@@ -126,13 +126,11 @@ __device__ __forceinline__ void stage_chunk(const uint32_t (&r)[XW], int xdt, in
     for (int j = 0; j < 4; ++j) h[j] = r[j];
   }
   *reinterpret_cast<u4 *>(lds + (c >> 3) * XPAIR_STRIDE + (c & 7) * 16) = u4{h[0], h[1], h[2], h[3]};
+  // block sum of the staged fp16 values: v_dot2 against (1, 1) adds two exact fp16 values per op
+  const h2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const h2 v = __builtin_bit_cast(h2, h[j]);
-    s += static_cast<float>(v[0]);
-    s += static_cast<float>(v[1]);
-  }
+  for (int j = 0; j < 4; ++j) s = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, h[j]), ones, s, false);
   s = dpp_add<DPP_QUAD_XOR1>(s);
   s = dpp_add<DPP_QUAD_XOR2>(s);
   if ((c & 3) == 0) sx[c >> 2] = s;
