@@ -29,7 +29,7 @@ HBM_PEAK_GBS = float(ROOFLINE["hbm_GBps"])
 METRIC = "dequant-GEMV GB/s (% HBM peak) + prefill/MoE GEMM TFLOP/s (% MFMA peak)"
 
 QWEN3_4B = dict(hidden=2560, q=4096, kv=1024, inter=9728, layers=36)
-STACK_TRAFFIC_PER_LAUNCH = 14419405  # measured HBM bytes per decode-stack launch (see run_stack)
+STACK_TRAFFIC_PER_LAUNCH = 14402381  # measured HBM bytes per decode-stack launch (see run_stack)
 
 
 def parse():
