@@ -10,7 +10,7 @@ the whole token is captured once as a HIP graph and replayed.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config stack|gemv1|...]
 
 Prints one JSON line. ``value`` = aggregate algorithmic GB/s per token (weights + activations
-read and written, the basis stated in DESIGN.md) with all inputs resident in HBM.
+read and written once per token) with all inputs resident in HBM.
 ``roofline`` = the dominant kernel (the q4_0 GEMV family) measured live with HIP events on
 the launch stream; ``cpu_baseline`` = the numpy oracle path (f32 decode + BLAS matvec) timed
 on a bounded sample of the same workload on this host.
@@ -545,8 +545,8 @@ def run_copy(args, torch, dev):
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: the fused dequant-matmul path is single-GPU in this "
-              "build (sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: the fused dequant-matmul path runs on a single GPU "
+              "(each GPU would hold a row / expert shard); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():

@@ -190,7 +190,7 @@ def test_exl3_slot_map_invariants():
         assert sorted(pos[i].tolist()) == [0, 1, 2, 3]
         assert len(set(nib[i].tolist())) == 4
         assert nib[i].min() >= 0 and nib[i].max() < 256
-    # the published example (native/exl3/README.md / SURVEY): slot (0,1) = {39@0,24@1,25@2,26@3}
+    # the published example (native/exl3/README.md): slot (0,1) = {39@0,24@1,25@2,26@3}
     i = int(np.nonzero((rows == 0) & (cols == 1))[0][0])
     assert dict(zip(nib[i].tolist(), pos[i].tolist())) == {39: 0, 24: 1, 25: 2, 26: 3}
 
