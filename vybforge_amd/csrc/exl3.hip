@@ -26,6 +26,27 @@ namespace vybdq {
 
 constexpr float kRScale = 0.08838834764831845f;  // 1/sqrt(128)
 
+// LDS of the fused GEMM: the x' stage of a split (fp16, duplicated (x, x) pairs for batch <= 2),
+// then for batches of 4..16 one [128 columns][32 k] fp16 tile per wave, column stride
+// kExl3WtStride bytes (five 16-B slots: 16 consecutive columns fall on distinct banks)
+constexpr int kExl3WtStride = 80;
+constexpr int kExl3WtBytes = 128 * kExl3WtStride;  // one wave's tile
+// the per-wave partials [4 waves][BP rows][kExl3RedStride floats] reuse the stage after the loop;
+// 4 floats of padding per row put the 16-column groups of 4 batch rows on different banks
+constexpr int kExl3RedStride = 132;
+// one launch (x rotation per workgroup, output rotation by the last split) up to batch 2; at
+// batch 4..16 the per-workgroup rotation of every batch row costs more than the two extra
+// launches (batch 16 measured 39 us with k_exl3_xprep / k_exl3_out, 68 us in one launch)
+__host__ __device__ constexpr bool exl3_fused(int BP) { return BP <= 2; }
+__host__ __device__ constexpr size_t exl3_xs_bytes(int BP, int kbs) {
+  return BP <= 2 ? static_cast<size_t>(BP) * 16 * kbs * 4 : static_cast<size_t>(BP) * (16 * kbs + 8) * 2;
+}
+static size_t exl3_lds_bytes(int BP, int kbs) {
+  const size_t main = exl3_xs_bytes(BP, kbs) + (BP >= 4 ? static_cast<size_t>(4) * kExl3WtBytes : 0);
+  const size_t red = static_cast<size_t>(4) * BP * kExl3RedStride * 4;
+  return main > red ? main : red;
+}
+
 // bits [o, o+32) of the 192-bit lane window w[0..5] (o is a constant after unrolling)
 __device__ __forceinline__ uint32_t win_extract(const uint32_t (&w)[6], int o) {
   const int i = o >> 5, s = o & 31;
@@ -275,7 +296,12 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   // and the pairing of decoded values; x' is staged duplicated for that. Larger batches round
   // the value to fp16 once and share it across the batch rows.
   constexpr bool HALVES = BP <= 2;
-  constexpr bool FUSED = BP <= 2;  // x rotation and output rotation in this launch
+  constexpr bool FUSED = exl3_fused(BP);  // x rotation and output rotation in this launch
+  // Batches of 4..16 multiply on the matrix cores: each wave writes its decoded values of two
+  // k-blocks into its own LDS tile [128 columns][32 k] (column stride kExl3WtStride bytes), then
+  // runs one v_mfma_f32_16x16x32_f16 per 16-column fragment with the x' rows as the A operand
+  // (rows past the batch read as zero). The VALU keeps only the decode.
+  constexpr bool MMA = BP >= 4;
   // This wave's k-blocks and the first kD of its trellis chunks, loaded before anything else (they
   // do not depend on x); the loop keeps kD chunks in flight per lane (a register ring).
   constexpr int kD = 4;
@@ -293,11 +319,15 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   for (int d = 0; d < kD; ++d) ring[d] = load_chunk(w_begin + d);
   // 1. x' rows of this split: [BP][16 * nkb] fp16 (HALVES: u32 pairs (x, x))
   const int rows = 16 * nkb;
+  // x' row stride of the stage (elements): the matrix-core A reads take 16 batch rows at once,
+  // so their rows are 16 B apart in the banks (a stride of whole 128-B lines would put all 16
+  // reads on the same banks)
+  const int xstride = MMA ? rows + 8 : rows;
   const int nch = nkb / 8;
   if constexpr (!FUSED) {
     for (int i = threadIdx.x; i < BP * rows / 8; i += blockDim.x) {
       const int b = i / (rows / 8), c = i % (rows / 8);
-      *reinterpret_cast<u4 *>(reinterpret_cast<_Float16 *>(smem) + b * rows + 8 * c) =
+      *reinterpret_cast<u4 *>(reinterpret_cast<_Float16 *>(smem) + b * xstride + 8 * c) =
           *reinterpret_cast<const u4 *>(xp + b * K + 16 * static_cast<int64_t>(kb_begin) + 8 * c);
     }
   }
@@ -330,6 +360,10 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   float acc[BP][2];
 #pragma unroll
   for (int b = 0; b < BP; ++b) acc[b][0] = acc[b][1] = 0.f;
+  f4 accm[MMA ? 8 : 1];
+#pragma unroll
+  for (int f = 0; f < (MMA ? 8 : 1); ++f) accm[f] = f4{0.f, 0.f, 0.f, 0.f};
+  char *wt = smem + exl3_xs_bytes(BP, kb_per_split) + static_cast<size_t>(wave) * kExl3WtBytes;
   auto step = [&](int kk, const u4 c) {
     uint32_t w[6];
     chunk_window(c, w);
@@ -361,6 +395,32 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
     }
     _Float16 v[32];
     lane_decode<CB>(w, v);
+    if constexpr (MMA) {
+      // v[i] = W[16 kk + i][c0], v[16 + i] = W[16 kk + i][c0 + 8]: into k half (kk & 1) of the tile
+      const int c0 = 16 * t + j;
+      const int half = kk & 1;
+      uint32_t pk[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pk[i] = __builtin_bit_cast(uint32_t, h2{v[2 * i], v[2 * i + 1]});
+      u4 *d0 = reinterpret_cast<u4 *>(wt + c0 * kExl3WtStride + 32 * half);
+      u4 *d1 = reinterpret_cast<u4 *>(wt + (c0 + 8) * kExl3WtStride + 32 * half);
+      d0[0] = u4{pk[0], pk[1], pk[2], pk[3]};
+      d0[1] = u4{pk[4], pk[5], pk[6], pk[7]};
+      d1[0] = u4{pk[8], pk[9], pk[10], pk[11]};
+      d1[1] = u4{pk[12], pk[13], pk[14], pk[15]};
+      if (half == 1) {
+        // k-blocks kk - 1 and kk complete: A = x'[m][16 (kk - 1) + 8 g .. + 8], B = the tile
+        const int m = lane & 15, gk = lane >> 4;
+        h8 a = h8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (m < BP) a = *reinterpret_cast<const h8 *>(xs + m * xstride + 16 * (kk - 1) + 8 * gk);
+#pragma unroll
+        for (int f = 0; f < 8; ++f) {
+          const h8 b = *reinterpret_cast<const h8 *>(wt + (16 * f + m) * kExl3WtStride + 16 * gk);
+          accm[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, accm[f], 0, 0, 0);
+        }
+      }
+      return;
+    }
     h2 pj[8], pj8[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -392,12 +452,23 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   }
   // reduce the 4 waves (same columns, different k) in a fixed order
   __syncthreads();
-  float *red = reinterpret_cast<float *>(smem);  // [4][BP][128]
-  const int c0 = 16 * t + j;                      // this lane's columns: c0 and c0 + 8
+  float *red = reinterpret_cast<float *>(smem);  // [4][BP][kExl3RedStride]
+  if constexpr (MMA) {
+    // accm[f][r] = z[batch 4 (lane >> 4) + r][column 16 f + (lane & 15)]
 #pragma unroll
-  for (int b = 0; b < BP; ++b) {
-    red[(wave * BP + b) * 128 + c0] = acc[b][0];
-    red[(wave * BP + b) * 128 + c0 + 8] = acc[b][1];
+    for (int f = 0; f < 8; ++f)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int b = 4 * (lane >> 4) + r;
+        if (b < BP) red[(wave * BP + b) * kExl3RedStride + 16 * f + (lane & 15)] = accm[f][r];
+      }
+  } else {
+    const int c0 = 16 * t + j;  // this lane's columns: c0 and c0 + 8
+#pragma unroll
+    for (int b = 0; b < BP; ++b) {
+      red[(wave * BP + b) * kExl3RedStride + c0] = acc[b][0];
+      red[(wave * BP + b) * kExl3RedStride + c0 + 8] = acc[b][1];
+    }
   }
   __syncthreads();
   const int64_t N = static_cast<int64_t>(NB) * 16;
@@ -406,8 +477,8 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   };
   for (int i = threadIdx.x; i < B * 128; i += blockDim.x) {
     const int b = i / 128, c = i % 128;
-    const float z = ((red[(0 * BP + b) * 128 + c] + red[(1 * BP + b) * 128 + c]) +
-                     red[(2 * BP + b) * 128 + c]) + red[(3 * BP + b) * 128 + c];
+    const float z = ((red[(0 * BP + b) * kExl3RedStride + c] + red[(1 * BP + b) * kExl3RedStride + c]) +
+                     red[(2 * BP + b) * kExl3RedStride + c]) + red[(3 * BP + b) * kExl3RedStride + c];
     if constexpr (FUSED) __hip_atomic_store(zp(s, b, c), __float_as_uint(z), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     else *zp(s, b, c) = __float_as_uint(z);
   }
@@ -483,7 +554,7 @@ static Exl3Split exl3_splits(int64_t K, int64_t N, int BP) {
 
 // workspace: per-column-block arrival counters (zero between calls), x' (batch > 2), partials
 static int64_t exl3_arrival_bytes(int64_t N) { return ((N / 128 * 4 + 255) / 256) * 256; }
-static int64_t exl3_xp_bytes(int BP, int64_t K) { return BP <= 2 ? 0 : ((BP * K * 2 + 255) / 256) * 256; }
+static int64_t exl3_xp_bytes(int BP, int64_t K) { return exl3_fused(BP) ? 0 : ((BP * K * 2 + 255) / 256) * 256; }
 
 static int64_t exl3_ws_bytes(int64_t B, int64_t K, int64_t N) {
   const int BP = exl3_bp(B);
@@ -570,9 +641,16 @@ template <int CB, int BP>
 static void exl3_gemm_launch(const uint16_t *t, const void *X, int xdt, const _Float16 *su, const _Float16 *sv,
                              void *Y, int ydt, int B, const _Float16 *xp, float *zp, uint32_t *arr, int64_t K,
                              int NB, const Exl3Split &sp, hipStream_t s) {
-  const size_t xs_bytes = static_cast<size_t>(BP) * 16 * sp.kbs * (BP <= 2 ? 4 : 2);
-  const size_t red_bytes = static_cast<size_t>(4) * BP * 128 * 4;
-  const size_t lds = xs_bytes > red_bytes ? xs_bytes : red_bytes;
+  const size_t lds = exl3_lds_bytes(BP, sp.kbs);  // <= 160 KB, checked by the caller
+  if (lds > 64 * 1024) {
+    static bool raised = false;  // one attribute call per instantiation
+    if (!raised) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void *>(&k_exl3_gemm<CB, BP>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+        return;  // the launch below then fails and check_launch reports it
+      raised = true;
+    }
+  }
   hipLaunchKernelGGL((k_exl3_gemm<CB, BP>), dim3(static_cast<unsigned>(NB / 8), static_cast<unsigned>(sp.S)),
                      dim3(256), lds, s, t, X, xdt, su, sv, Y, ydt, B, xp, zp, arr, K, NB, sp.kbs);
 }
@@ -592,6 +670,8 @@ extern "C" int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uin
                 "workspace smaller than vybdq_exl3_workspace_size");
   const int BP = exl3_bp(B);
   const Exl3Split sp = exl3_splits(K, N, BP);
+  VYBDQ_REQUIRE(exl3_lds_bytes(BP, sp.kbs) <= 160 * 1024, VYBDQ_ERR_SHAPE,
+                "K too large for one split's x' stage in LDS at this batch");
   const int NB = static_cast<int>(N / 16);
   hipStream_t s = as_stream(stream);
   auto *arr = reinterpret_cast<uint32_t *>(ws);
@@ -603,7 +683,7 @@ extern "C" int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uin
   const void *x = reinterpret_cast<const void *>(X);
   void *y = reinterpret_cast<void *>(Y);
   const int b = static_cast<int>(B);
-  if (BP > 2) {
+  if (!exl3_fused(BP)) {
     const dim3 gx(static_cast<unsigned>(K / 128), static_cast<unsigned>(BP));
     VYBDQ_DISPATCH_IN(x_dt, XDT, hipLaunchKernelGGL((k_exl3_xprep<XDT>), gx, dim3(64), 0, s, x, su, xp, b, K));
   }
@@ -617,7 +697,7 @@ extern "C" int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uin
   }
   if (codebook == VYBDQ_EXL3_MCG) { G(VYBDQ_EXL3_MCG) } else { G(VYBDQ_EXL3_3INST) }
 #undef G
-  if (BP > 2) {
+  if (!exl3_fused(BP)) {
     const dim3 go(static_cast<unsigned>(N / 128), static_cast<unsigned>(B));
     VYBDQ_DISPATCH_IN(y_dt, YDT, hipLaunchKernelGGL((k_exl3_out<YDT>), go, dim3(64), 0, s, zp, sv, y, BP, sp.S, N));
   }
