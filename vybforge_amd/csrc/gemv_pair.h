@@ -84,11 +84,24 @@ __global__ void __launch_bounds__(256) k_gemv_pair(const void *__restrict__ X, i
     load_x_chunk<XW>(X, 8 * static_cast<int64_t>(c), r);
     stage_chunk<XW>(r, xdt, c, lds, sx);
   }
-  if constexpr (FMT == FMT_IQ2_S) {  // the IQ2_S grid (8 KB) after the x stage
-    uint2 *grid = reinterpret_cast<uint2 *>(sx + 2 * M * P);
-    for (int i = threadIdx.x; i < 1024; i += T) {
-      const unsigned long long e = kIq2sGrid[i];
-      grid[i] = uint2{static_cast<uint32_t>(e), static_cast<uint32_t>(e >> 32)};
+  if constexpr (FMT == FMT_IQ2_S) {
+    // after the x stage: the IQ2_S grid as fp16 (16 KB: entry i = its 8 magnitudes, exact) and
+    // the 256 sign patterns as fp16 sign-bit masks (4 KB: bit j of s -> bit 15 of half j)
+    u4 *gridh = iq2s_lds_grid(sx, M, P);
+    for (int i = threadIdx.x; i < 1024 + 256; i += T) {
+      uint32_t q[4];
+      if (i < 1024) {
+        const unsigned long long e = kIq2sGrid[i];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          q[k] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(static_cast<float>((e >> (16 * k)) & 0xff)),
+                                                 static_cast<_Float16>(static_cast<float>((e >> (16 * k + 8)) & 0xff))});
+      } else {
+        const uint32_t sb = static_cast<uint32_t>(i - 1024);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[k] = (((sb >> (2 * k)) & 1u) << 15) | (((sb >> (2 * k + 1)) & 1u) << 31);
+      }
+      gridh[i] = u4{q[0], q[1], q[2], q[3]};
     }
   }
   __syncthreads();
@@ -191,7 +204,7 @@ template <int FMT, int G, int ORDER, int M, int XW, int U>
 static int launch_gu(const void *X, int xdt, int64_t K, const Segs &segs, int threads, hipStream_t s) {
   const int64_t rows = segs.end[2];
   const int P = static_cast<int>(K / 64);
-  const size_t lds = static_cast<size_t>(M) * P * (XPAIR_STRIDE + 2 * 4) + (FMT == FMT_IQ2_S ? 8192 : 0);
+  const size_t lds = static_cast<size_t>(M) * P * (XPAIR_STRIDE + 2 * 4) + (FMT == FMT_IQ2_S ? kIq2sLdsBytes : 0);
   if (lds > static_cast<size_t>(kMaxLds)) return set_error(VYBDQ_ERR_SHAPE, "gemv: K too large for the LDS x stage at this M");
   const int rows_per_wg = threads / G;
   const unsigned grid = static_cast<unsigned>((rows + rows_per_wg - 1) / rows_per_wg);

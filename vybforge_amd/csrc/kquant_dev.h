@@ -36,6 +36,13 @@ template <> struct Fmt<FMT_Q5_K> {
   static constexpr int SB_BYTES = 176;
   static constexpr int PAIR_DWORDS = 20;  // header + qh[32] + 32 B of qs
 };
+// LDS of the IQ2_S tables behind the x stage and its block sums (16-B aligned): 1024 grid
+// entries of 8 fp16 magnitudes, then 256 sign patterns as fp16 sign-bit masks, 16 B each
+constexpr size_t kIq2sLdsBytes = (1024 + 256) * 16 + 16;
+__device__ __forceinline__ u4 *iq2s_lds_grid(float *sx, int M, int P) {
+  return reinterpret_cast<u4 *>(sx + ((2 * M * P + 3) & ~3));  // sx is 16-B aligned
+}
+
 template <> struct Fmt<FMT_IQ2_S> {
   static constexpr int SB_BYTES = 82;
   static constexpr int PAIR_DWORDS = 10;  // index window 3 + sign window 3 + qh pair + scale pair + d + shift
@@ -187,23 +194,20 @@ __device__ __forceinline__ void unit_dot_kq(const uint32_t (&dw)[Fmt<FMT>::PAIR_
     const uint32_t ix[2] = {__builtin_amdgcn_alignbit(dw[1], dw[0], sh), __builtin_amdgcn_alignbit(dw[2], dw[1], sh)};
     const uint32_t sg[2] = {__builtin_amdgcn_alignbit(dw[4], dw[3], sh), __builtin_amdgcn_alignbit(dw[5], dw[4], sh)};
     const float d = half_bits_to_f32(dw[8]) * 0.25f;
-    const uint2 *grid = reinterpret_cast<const uint2 *>(sx + 2 * M * P);
-    const h2 m1024 = h2{static_cast<_Float16>(-1024.0f), static_cast<_Float16>(-1024.0f)};
+    const u4 *gridh = iq2s_lds_grid(const_cast<float *>(sx), M, P);  // [1024 grid][256 signs]
 #pragma unroll
     for (int l = 0; l < 8; ++l) {
       const int ib = l >> 2, l2 = l & 3;
       const uint32_t idx = __builtin_amdgcn_ubfe(ix[l >> 2], 8 * (l & 3), 8) |
                            (__builtin_amdgcn_ubfe(dw[6], 8 * ib + 2 * l2, 2) << 8);
-      const uint2 e = grid[idx];
-      const uint32_t sb8 = __builtin_amdgcn_ubfe(sg[l >> 2], 8 * (l & 3), 8);
+      const u4 e = gridh[idx];
+      const u4 sm = gridh[1024 + __builtin_amdgcn_ubfe(sg[l >> 2], 8 * (l & 3), 8)];
       const float dl = d * (0.5f + static_cast<float>(__builtin_amdgcn_ubfe(dw[7], 8 * ib + 4 * (l2 >> 1), 4)));
       h2 wv[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const uint32_t src = k < 2 ? e.x : e.y;
-        h2 w = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, src, (k & 1) ? SEL_B23 : SEL_B01)) + m1024;
-        const uint32_t neg = (__builtin_amdgcn_ubfe(sb8, 2 * k, 1) << 15) | (__builtin_amdgcn_ubfe(sb8, 2 * k + 1, 1) << 31);
-        wv[k] = __builtin_bit_cast(h2, __builtin_bit_cast(uint32_t, w) ^ neg);
+        const uint32_t ek = e[k], sk = sm[k];  // vector elements to scalars before the bit casts
+        wv[k] = __builtin_bit_cast(h2, ek ^ sk);
       }
 #pragma unroll
       for (int m = 0; m < M; ++m) {
