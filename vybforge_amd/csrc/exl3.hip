@@ -541,8 +541,9 @@ static Exl3Split exl3_splits(int64_t K, int64_t N, int BP) {
   const int KB = static_cast<int>(K / 16);
   const int64_t groups = N / 128;
   // measured at K = 5120, N = 17408: batch 1 best at 7 splits (952 workgroups: 1680 GB/s against
-  // 1625 at 8 and 1466 at 4), batch 16 at 16 (8 and 12 measured 11% slower)
-  const int64_t target = BP >= 8 ? 2048 : 896;
+  // 1625 at 8 and 1466 at 4); the matrix-core batches (4..16) at 16 (batch 4: 1294 against 1194 GB/s
+  // at 8; batch 16: 8, 12, 20 and 24 splits 9-11% slower)
+  const int64_t target = BP >= 4 ? 2048 : 896;
   int S = static_cast<int>((target + groups - 1) / groups);
   if (S > 16) S = 16;
   if (S > KB / 4) S = KB / 4 > 0 ? KB / 4 : 1;
