@@ -68,18 +68,31 @@ def test_exl3_gemm(dev, B, cb):
     assert matmul.rel_maxnorm(y, ref) < matmul.TOL
 
 
-def test_exl3_gemm_config4_shape(dev):
+@pytest.fixture(scope="module")
+def exl3_config4(dev):
     rng = np.random.default_rng(44)
     K, N = 5120, 17408
     t, suh, svh = synth.exl3_tensors(rng, K, N)
-    x = rng.standard_normal((1, K)).astype(np.float32)
     lin = ops.Exl3Linear(dev_t(t, dev), dev_t(suh, dev), dev_t(svh, dev), K, N)
-    y = lin(dev_t(x, dev)).cpu().numpy()
-    # float64 oracle on a column slice (the full float64 dequant is 89M weights)
-    cols = np.arange(0, N, 1)[:1024]
-    w = exl3.dequant_exl3_f64(t[:, :64], suh, svh[:1024])
-    ref = x.astype(np.float64) @ w
-    assert matmul.rel_maxnorm(y[:, cols], ref) < matmul.TOL
+    # float64 oracle on column slices (the full float64 dequant is 89M weights): the first 1024
+    # columns and the last 1024 (the last column blocks of every k-split)
+    slices = {0: exl3.dequant_exl3_f64(t[:, :64], suh, svh[:1024]),
+              N - 1024: exl3.dequant_exl3_f64(t[:, -64:], suh, svh[-1024:])}
+    return lin, slices, K, N
+
+
+@pytest.mark.parametrize("B,xdt", [(1, torch.float32), (2, torch.float16), (4, torch.float16),
+                                   (16, torch.float16), (16, torch.bfloat16)])
+def test_exl3_gemm_config4_shape(dev, exl3_config4, B, xdt):
+    """K = 5120, N = 17408 at every batch regime: one fused launch with 7 k-splits (B <= 2), and
+    the three-launch matrix-core path with 16 k-splits over 2176 workgroups (B = 4, 16)."""
+    lin, slices, K, N = exl3_config4
+    x = torch.from_numpy(np.random.default_rng(B).standard_normal((B, K)).astype(np.float32)).to(xdt)
+    y = lin(x.to(dev)).cpu().numpy()
+    x64 = x.to(torch.float64).numpy()
+    for c0, w in slices.items():
+        ref = x64 @ w
+        assert matmul.rel_maxnorm(y[:, c0:c0 + 1024], ref) < matmul.TOL, (B, c0)
 
 
 @pytest.mark.parametrize("K,N", [(128, 256), (1152, 256), (2048, 384)])

@@ -56,3 +56,28 @@ def kquant_weights(rng, ty, N, K):
     else:
         blk[:, 208:210] = f16()
     return blk.reshape(-1)
+
+
+def q4_0_weights_torch(gen, N, K, device):
+    """Seeded packed q4_0 rows generated on the device (torch generator ``gen``): uint8
+    [N * K/32 * 18], fp16 d = |N(0, 0.01)|, uniform nibble bytes. For workloads too large to
+    build on the host (a 256-expert layer is 5.4 GB)."""
+    import torch
+    nb = N * (K // 32)
+    blk = torch.empty((nb, 18), dtype=torch.uint8, device=device)
+    d = (torch.randn(nb, generator=gen, device=device) * 0.01).abs().to(torch.float16)
+    blk[:, 0:2] = d.view(torch.uint8).view(nb, 2)
+    blk[:, 2:] = torch.randint(0, 256, (nb, 16), generator=gen, device=device, dtype=torch.uint8)
+    return blk.view(-1)
+
+
+def q8_0_weights_torch(gen, N, K, device):
+    """Seeded packed Q8_0 rows on the device: fp16 d = |N(0, 0.01)|, int8 uniform in [-127, 127]."""
+    import torch
+    nb = N * (K // 32)
+    blk = torch.empty((nb, 34), dtype=torch.uint8, device=device)
+    d = (torch.randn(nb, generator=gen, device=device) * 0.01).abs().to(torch.float16)
+    blk[:, 0:2] = d.view(torch.uint8).view(nb, 2)
+    blk[:, 2:] = torch.randint(-127, 128, (nb, 32), generator=gen, device=device,
+                               dtype=torch.int8).view(torch.uint8)
+    return blk.view(-1)
