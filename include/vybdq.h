@@ -341,6 +341,25 @@ int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logits, int logi
                       int64_t H, int64_t I, int64_t E, int64_t topk, double scale, double limit, uint64_t ws,
                       int64_t ws_bytes, uint64_t stream);
 
+/* Largest workspace (bytes) vybdq_moe_forward_noalloc can use: its per-GPU scratch array. At
+   H = 6144, I = 2048, E = 256, topk = 8 this covers T <= 233 tokens. */
+#define VYBDQ_MOE_NOALLOC_MAX_BYTES (64ll * 1024 * 1024)
+
+/* vybdq_moe_forward without a workspace argument, and without allocating anything: no
+   counterpart in the reference; for callers that cannot allocate device memory (code under HIP
+   graph capture, tight serving loops, harnesses that forbid hipMalloc). The workspace is a
+   library-owned device array of VYBDQ_MOE_NOALLOC_MAX_BYTES per GPU, held until the process
+   ends; its address is looked up on the first call on each device (the only set-up step). A
+   shape whose vybdq_moe_workspace_size exceeds the array returns VYBDQ_ERR_WORKSPACE before
+   any launch. Every call on one GPU shares that GPU's array, so calls that overlap on one GPU
+   (several streams or host threads) race: the caller serialises them. Nothing in the array has
+   to start at zero (every call rewrites what it reads). Results equal vybdq_moe_forward's. */
+int vybdq_moe_forward_noalloc(int wtype, uint64_t x, int x_dt, uint64_t logits, int logits_dt, uint64_t bias,
+                              uint64_t w_gate, uint64_t w_up, uint64_t w_down, uint64_t s_gate, uint64_t s_up,
+                              uint64_t s_down, uint64_t out, int out_dt, uint64_t idx_out, uint64_t w_out,
+                              int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk, double scale,
+                              double limit, uint64_t stream);
+
 /* ---- activation quantizer ------------------------------------------------------------ */
 
 /* xq8 semantics per row and per 32-value block: a = max|x|, d = a/127, q = sat_s8(rne(x*127/a))

@@ -67,3 +67,16 @@ def test_quant_preconditions():
     from vybforge_amd import _lib
     assert _lib.lib.vybdq_quant_q8_act(1, 1, 1, 2, 33, 0, 0) == _lib.ERR_SHAPE
     assert _lib.lib.vybdq_quant_q8_act(1, 1, 2, 2, 32, 0, 0) == _lib.ERR_ALIGN
+
+
+def test_moe_noalloc_size_limit_on_host():
+    """The allocation-free MoE entry rejects a shape whose workspace exceeds its scratch before it
+    touches the device (GLM-5 shapes at 4096 tokens)."""
+    from vybforge_amd import _lib
+    assert _lib.lib.vybdq_moe_workspace_size(4096, 6144, 2048, 256, 8) > _lib.MOE_NOALLOC_MAX_BYTES
+    assert _lib.lib.vybdq_moe_workspace_size(233, 6144, 2048, 256, 8) <= _lib.MOE_NOALLOC_MAX_BYTES
+    assert _lib.lib.vybdq_moe_workspace_size(234, 6144, 2048, 256, 8) > _lib.MOE_NOALLOC_MAX_BYTES
+    rc = _lib.lib.vybdq_moe_forward_noalloc(2, 16, 2, 16, 0, 0, 16, 16, 16, 0, 0, 0, 16, 0, 0, 0, 4096, 6144, 2048,
+                                            256, 8, 2.5, 10.0, 0)
+    assert rc == _lib.ERR_WORKSPACE
+    assert "scratch" in _lib.last_error()

@@ -17,6 +17,7 @@ ERR_ARG, ERR_SHAPE, ERR_ALIGN, ERR_HIP, ERR_WORKSPACE = -1, -2, -3, -4, -5
 F32, F16, BF16, F64 = 0, 1, 2, 3
 Q4_GGML, Q4_INTERLEAVED = 0, 1
 EXL3_3INST, EXL3_MCG = 0, 1
+MOE_NOALLOC_MAX_BYTES = 64 * 1024 * 1024  # VYBDQ_MOE_NOALLOC_MAX_BYTES
 
 _u64, _i64, _int = ctypes.c_uint64, ctypes.c_int64, ctypes.c_int
 
@@ -86,6 +87,9 @@ SIGNATURES = {
     "vybdq_moe_forward": [_int, _u64, _int, _u64, _int, _u64, _u64, _u64, _u64, _u64, _u64, _u64, _u64, _int,
                           _u64, _u64, _i64, _i64, _i64, _i64, _i64, ctypes.c_double, ctypes.c_double, _u64,
                           _i64, _u64],
+    "vybdq_moe_forward_noalloc": [_int, _u64, _int, _u64, _int, _u64, _u64, _u64, _u64, _u64, _u64, _u64, _u64,
+                                  _int, _u64, _u64, _i64, _i64, _i64, _i64, _i64, ctypes.c_double,
+                                  ctypes.c_double, _u64],
 }
 _RESTYPE = {"vybdq_last_error": ctypes.c_char_p, "vybdq_chain_workspace_size": ctypes.c_int64,
             "vybdq_exl3_workspace_size": ctypes.c_int64, "vybdq_moe_workspace_size": ctypes.c_int64,

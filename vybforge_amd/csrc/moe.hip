@@ -21,6 +21,8 @@
 #include "moe_gemv.h"
 #include "moe_mm.h"
 #include <cstdio>
+#include <mutex>
+#include <string>
 #include <type_traits>
 
 namespace vybdq {
@@ -671,4 +673,54 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
     default: hipLaunchKernelGGL((k_moe_combine<VYBDQ_BF16>), dim3(gc), dim3(256), 0, s, m.rows, shared, m.pos, wts, static_cast<int>(T), static_cast<int>(topk), H, o); break;
   }
   return check_launch("moe combine");
+}
+
+// ---- allocation-free variant --------------------------------------------------------------
+//
+// The workspace of vybdq_moe_forward_noalloc: one array per GPU (each device that loads this
+// code object holds its own copy until the process ends). Host code never passes the array's
+// name to a kernel: its device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) char scratch[VYBDQ_MOE_NOALLOC_MAX_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint64_t g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device (0: not yet set up)
+
+// Device address of the current device's scratch array; set up on the first call per device.
+int scratch_address(uint64_t &ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(VYBDQ_ERR_HIP, "vybdq_moe_forward_noalloc: no current HIP device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(VYBDQ_ERR_HIP, std::string("vybdq_moe_forward_noalloc: hipGetSymbolAddress failed: ") +
+                                          hipGetErrorString(e));
+    g_scratch_ptr[dev] = reinterpret_cast<uint64_t>(p);
+  }
+  ptr = g_scratch_ptr[dev];
+  return VYBDQ_OK;
+}
+}  // namespace
+
+extern "C" int vybdq_moe_forward_noalloc(int wtype, uint64_t x, int x_dt, uint64_t logits, int logits_dt,
+                                         uint64_t bias, uint64_t w_gate, uint64_t w_up, uint64_t w_down,
+                                         uint64_t s_gate, uint64_t s_up, uint64_t s_down, uint64_t out, int out_dt,
+                                         uint64_t idx_out, uint64_t w_out, int64_t T, int64_t H, int64_t I,
+                                         int64_t E, int64_t topk, double scale, double limit, uint64_t stream) {
+  const int64_t need = vybdq_moe_workspace_size(T, H, I, E, topk);
+  VYBDQ_REQUIRE(need > 0, VYBDQ_ERR_SHAPE, "unsupported T, H, I, E or topk (E <= 1024, topk <= 64)");
+  VYBDQ_REQUIRE(need <= VYBDQ_MOE_NOALLOC_MAX_BYTES, VYBDQ_ERR_WORKSPACE,
+                "the shape needs " + std::to_string(need) + " workspace bytes, more than the " +
+                    std::to_string(static_cast<long long>(VYBDQ_MOE_NOALLOC_MAX_BYTES)) +
+                    " of the library's scratch; use vybdq_moe_forward with a caller workspace");
+  uint64_t ws = 0;
+  const int rc = scratch_address(ws);
+  if (rc) return rc;
+  return vybdq_moe_forward(wtype, x, x_dt, logits, logits_dt, bias, w_gate, w_up, w_down, s_gate, s_up, s_down, out,
+                           out_dt, idx_out, w_out, T, H, I, E, topk, scale, limit, ws, VYBDQ_MOE_NOALLOC_MAX_BYTES,
+                           stream);
 }

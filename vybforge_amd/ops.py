@@ -337,7 +337,9 @@ class MoeLayer:
             self._ws_bytes = n
         return (self._ws.data_ptr() + 255) // 256 * 256, self._ws_bytes
 
-    def __call__(self, x, logits, out_dtype=torch.float32, out=None, routing=False):
+    def __call__(self, x, logits, out_dtype=torch.float32, out=None, routing=False, noalloc=False):
+        """out [T, H] for x [T, H] and logits [T, E]. noalloc: run through
+        vybdq_moe_forward_noalloc (the library's per-GPU scratch instead of this layer's workspace)."""
         T = x.shape[0]
         if out is None:
             out = torch.empty((T, self.H), dtype=out_dtype, device=x.device)
@@ -345,10 +347,14 @@ class MoeLayer:
         if routing:
             idx = torch.empty((T, self.topk), dtype=torch.int32, device=x.device)
             w = torch.empty((T, self.topk), dtype=torch.float32, device=x.device)
-        ws, nb = self._workspace(T, x.device)
         sg, su, sd = self.shared if self.shared else (None, None, None)
-        call("vybdq_moe_forward", self.ty, _ptr(x), _dt(x.dtype), _ptr(logits), _dt(logits.dtype),
-             _ptr(self.bias), _ptr(self.w[0]), _ptr(self.w[1]), _ptr(self.w[2]), _ptr(sg), _ptr(su), _ptr(sd),
-             _ptr(out), _dt(out.dtype), _ptr(idx), _ptr(w), T, self.H, self.I, self.E, self.topk,
-             float(self.scale), float(self.limit), ws, nb, _stream())
+        args = (self.ty, _ptr(x), _dt(x.dtype), _ptr(logits), _dt(logits.dtype),
+                _ptr(self.bias), _ptr(self.w[0]), _ptr(self.w[1]), _ptr(self.w[2]), _ptr(sg), _ptr(su), _ptr(sd),
+                _ptr(out), _dt(out.dtype), _ptr(idx), _ptr(w), T, self.H, self.I, self.E, self.topk,
+                float(self.scale), float(self.limit))
+        if noalloc:
+            call("vybdq_moe_forward_noalloc", *args, _stream())
+        else:
+            ws, nb = self._workspace(T, x.device)
+            call("vybdq_moe_forward", *args, ws, nb, _stream())
         return (out, idx, w) if routing else out
