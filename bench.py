@@ -1,19 +1,21 @@
 #!/usr/bin/env python3
 """Benchmark of the fused dequant-matmul path on one MI355X.
 
-Default workload (one "step" = one decoded token): the Qwen3-4B-shaped q4_0 decode linear
-stack, batch 1, 36 layers x {q 2560->4096, k/v 2560->1024, o 4096->2560, gate/up 2560->9728,
-down 9728->2560}, fp16 activations, seeded synthetic weights (fp16 scales |N(0, 0.01)|,
-uniform nibbles). Per layer four launches: q|k|v fused (one shared x), o, gate|up fused, down;
-the whole token is captured once as a HIP graph and replayed.
+Headline (one "step" = one decoded token): the Qwen3-4B-shaped q4_0 decode linear stack, batch 1,
+36 layers x {q 2560->4096, k/v 2560->1024, o 4096->2560, gate/up 2560->9728, down 9728->2560},
+fp16 activations, seeded synthetic weights (fp16 scales |N(0, 0.01)|, uniform nibbles). Per layer
+four launches (q|k|v fused on one shared x, o, gate|up fused, down), captured once as a HIP graph
+and replayed.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config stack|gemv1|...]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|stack|gemv1|...]
 
-Prints one JSON line. ``value`` = aggregate algorithmic GB/s per token (weights + activations
-read and written once per token) with all inputs resident in HBM.
-``roofline`` = the dominant kernel (the q4_0 GEMV family) measured live with HIP events on
-the launch stream; ``cpu_baseline`` = the numpy oracle path (f32 decode + BLAS matvec) timed
-on a bounded sample of the same workload on this host.
+The default (``--config all``) prints ONE JSON line: the headline stack figures plus a ``configs``
+record per workload of the metric (q4_0 GEMV 9728x2560, Q8_0 prefill GEMM M=512 on both paths,
+EXL3 K=5120 N=17408 at batch 1 and 16, the GLM-5 MoE layer at T=1/16/256), each timed with HIP
+events on its launch stream and each output checked against the numpy oracle after its timed
+region (a mismatch exits non-zero). ``--config X`` runs one workload alone (for profiling).
+Inputs are resident in HBM before timing; every workload whose weights fit the 256 MB MALL is
+rotated over enough distinct copies to exceed it.
 """
 
 import argparse
@@ -22,14 +24,24 @@ import os
 import sys
 import time
 
+HERE = os.path.dirname(os.path.abspath(__file__))
 # roofline constants (MI355X datasheet, dense) live in roofline.json beside this file
-with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "roofline.json")) as _f:
+with open(os.path.join(HERE, "roofline.json")) as _f:
     ROOFLINE = json.load(_f)
 HBM_PEAK_GBS = float(ROOFLINE["hbm_GBps"])
+MFMA_BF16_PEAK_TFLOPS = float(ROOFLINE["mfma_dense_TFLOPs"]["bf16"])
+MFMA_I8_PEAK_TOPS = float(ROOFLINE["mfma_dense_TFLOPs"]["int8_TOPs"])
 METRIC = "dequant-GEMV GB/s (% HBM peak) + prefill/MoE GEMM TFLOP/s (% MFMA peak)"
+GATE = 2e-3  # max|y - ref| / max|ref| against the float64 oracle (native/glm53/verify_layer0.py:134-139)
 
 QWEN3_4B = dict(hidden=2560, q=4096, kv=1024, inter=9728, layers=36)
-STACK_TRAFFIC_PER_LAUNCH = 14402381  # measured HBM bytes per decode-stack launch (see run_stack)
+# HBM bytes per decode-stack launch from rocprofv3 FETCH_SIZE / WRITE_SIZE (scaled by a plain
+# copy's counters), averaged over the four launches of a layer: measured by the profile below,
+# not by this run
+STACK_TRAFFIC = dict(bytes_per_launch=14402381, source="profiles/q4_0_gemv_decode_stack.md (rocprofv3 --pmc)")
+
+CONFIGS = ["stack", "stack_chain", "gemv1", "kquant", "producers", "router", "exl3", "prefill", "prefill_i8",
+           "moe", "copy"]
 
 
 def parse():
@@ -37,30 +49,88 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="stack",
-                    choices=["stack", "stack_chain", "gemv1", "kquant", "producers", "router", "exl3", "prefill",
-                             "prefill_i8", "moe", "copy"])
+    ap.add_argument("--config", default="all", choices=["all"] + CONFIGS)
     ap.add_argument("--wtype", type=int, default=12, choices=[12, 13, 14, 22],
                     help="GGML type id for --config kquant (12 Q4_K, 13 Q5_K, 14 Q6_K, 22 IQ2_S)")
     ap.add_argument("--tokens", type=int, default=16, help="tokens for --config moe / router")
     ap.add_argument("--batch", type=int, default=1, help="batch for --config exl3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-check", action="store_true", help="skip the oracle checks after timing")
     ap.add_argument("--seed", type=int, default=0)
     return ap.parse_args()
 
 
-def q4_0_blocks_gpu(torch, gen, N, K, dev):
-    """Seeded packed q4_0 rows generated on the device: uint8 [N * K/32 * 18]."""
-    nb = N * (K // 32)
-    blk = torch.empty((nb, 18), dtype=torch.uint8, device=dev)
-    d = (torch.randn(nb, generator=gen, device=dev) * 0.01).abs().to(torch.float16)
-    blk[:, 0:2] = d.view(torch.uint8).view(nb, 2)
-    blk[:, 2:] = torch.randint(0, 256, (nb, 16), generator=gen, device=dev, dtype=torch.uint8)
-    return blk.view(-1)
+class CheckFailed(RuntimeError):
+    pass
 
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---- timing ---------------------------------------------------------------------------------
+
+def timed_graph(torch, launches, steps, warmup):
+    """Capture the launches as one graph on a side stream; replay warmup + steps times on that
+    stream; return (ms per replay from HIP events recorded on the replay stream, wall seconds)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for f in launches:  # eager warm-up on the capture stream (first-use set-up stays out of the graph)
+            f()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for f in launches:
+            f()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record(s)
+        for _ in range(steps):
+            g.replay()
+        ev1.record(s)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    return ev0.elapsed_time(ev1) / steps, wall
+
+
+def hbm_roofline(gbs, kernel, basis, traffic=None, **extra):
+    r = dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4),
+             traffic=traffic, kernel=kernel, basis=basis)
+    r.update(extra)
+    return r
+
+
+# ---- oracle checks (outside the timed regions) ------------------------------------------------
+
+def rel_gate(y, ref, dtype_bits=None):
+    """max|y - ref| / max|ref|; for 16-bit outputs half an output ulp of ref is forgiven first."""
+    import numpy as np
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    d = np.abs(y - ref)
+    if dtype_bits is not None:
+        half = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - dtype_bits - 1)
+        d = np.maximum(d - half, 0)
+    return float(d.max() / max(float(np.abs(ref).max()), 1e-300))
+
+
+def expect(name, rel, tol=GATE):
+    if not rel < tol:
+        raise CheckFailed(f"{name}: rel {rel:.3e} >= {tol:.1e}")
+    return float(f"{rel:.3e}")
+
+
+# ---- synthetic inputs -----------------------------------------------------------------------
 
 def kquant_blocks_gpu(torch, gen, ty, N, K, dev):
-    """Seeded packed Q4_K / Q5_K / Q6_K rows on the device: uniform random bytes, the fp16
+    """Seeded packed Q4_K / Q5_K / Q6_K / IQ2_S rows on the device: uniform random bytes, the fp16
     scale fields = |N(0, 1e-4)|."""
     sbytes = {12: 144, 13: 176, 14: 210, 22: 82}[ty]
     nb = N * (K // 256)
@@ -71,18 +141,17 @@ def kquant_blocks_gpu(torch, gen, ty, N, K, dev):
     return blk.view(-1)
 
 
+# ---- headline: the decode stack ---------------------------------------------------------------
+
 def build_stack(torch, dev, seed):
+    from vybforge_amd import synth
     c = QWEN3_4B
     H, Q, KV, I = c["hidden"], c["q"], c["kv"], c["inter"]
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    layers = []
-    for _ in range(c["layers"]):
-        layers.append(dict(
-            q=q4_0_blocks_gpu(torch, gen, Q, H, dev), k=q4_0_blocks_gpu(torch, gen, KV, H, dev),
-            v=q4_0_blocks_gpu(torch, gen, KV, H, dev), o=q4_0_blocks_gpu(torch, gen, H, Q, dev),
-            gate=q4_0_blocks_gpu(torch, gen, I, H, dev), up=q4_0_blocks_gpu(torch, gen, I, H, dev),
-            down=q4_0_blocks_gpu(torch, gen, H, I, dev)))
+    q4 = lambda n, k: synth.q4_0_weights_torch(gen, n, k, dev)
+    layers = [dict(q=q4(Q, H), k=q4(KV, H), v=q4(KV, H), o=q4(H, Q), gate=q4(I, H), up=q4(I, H), down=q4(H, I))
+              for _ in range(c["layers"])]
     f16 = torch.float16
     acts = dict(
         x_attn=torch.randn(H, generator=gen, device=dev).to(f16),
@@ -117,6 +186,65 @@ def stack_launches(ops, layers, a):
         out.append(lambda L=L: ops.gemv_q4_0_seg3(a["x_mlp"], H, [(L["gate"], a["yg"], I), (L["up"], a["yu"], I)]))
         out.append(lambda L=L: ops.gemv(ops.GGML_Q4_0, L["down"], a["x_down"], H, I, out=a["yd"].view(1, H)))
     return out
+
+
+def stack_chain(ops, layers, a, dev):
+    """The token as one persistent chain: 144 dependent stages, one launch."""
+    H, Q, KV, I = QWEN3_4B["hidden"], QWEN3_4B["q"], QWEN3_4B["kv"], QWEN3_4B["inter"]
+    stages = []
+    for L in layers:
+        stages.append(ops.pblock(a["x_attn"], H, [(L["q"], a["yq"], Q), (L["k"], a["yk"], KV), (L["v"], a["yv"], KV)]))
+        stages.append(ops.pblock(a["x_o"], Q, [(L["o"], a["yo"], H)]))
+        stages.append(ops.pblock(a["x_mlp"], H, [(L["gate"], a["yg"], I), (L["up"], a["yu"], I)]))
+        stages.append(ops.pblock(a["x_down"], I, [(L["down"], a["yd"], H)]))
+    return ops.GemvChain(ops.GGML_Q4_0, stages, dev)
+
+
+def check_stack(torch, layers, a):
+    """The outputs of the last replay are the last layer's: each of its 7 GEMVs against float64."""
+    from oracle import matmul
+    H, Q, KV, I = QWEN3_4B["hidden"], QWEN3_4B["q"], QWEN3_4B["kv"], QWEN3_4B["inter"]
+    L = layers[-1]
+    worst = 0.0
+    for w, x, y, n, k in [("q", "x_attn", "yq", Q, H), ("k", "x_attn", "yk", KV, H), ("v", "x_attn", "yv", KV, H),
+                          ("o", "x_o", "yo", H, Q), ("gate", "x_mlp", "yg", I, H), ("up", "x_mlp", "yu", I, H),
+                          ("down", "x_down", "yd", H, I)]:
+        ref = matmul.gemv_q4_0_f64(L[w].cpu().numpy(), a[x].float().cpu().numpy(), n, k)[0]
+        worst = max(worst, expect(f"stack {w}", rel_gate(a[y].float().cpu().numpy(), ref, 10)))
+    return dict(ok=True, rel=worst, what="last layer, all 7 GEMVs (fp16 out), float64 oracle")
+
+
+def run_stack(args, torch, dev):
+    from vybforge_amd import ops
+    shapes, bytes_tok, flops_tok, wbytes_layer = stack_bytes()
+    layers, acts = build_stack(torch, dev, args.seed)
+    if args.config == "stack_chain":
+        chain = stack_chain(ops, layers, acts, dev)
+        launches = [chain]
+        kernel = "k_gemv_chain<q4_0> (one persistent launch per token, 144 dependent stages)"
+    else:
+        launches = stack_launches(ops, layers, acts)
+        kernel = "k_gemv_pair<q4_0> (all 144 launches per token)"
+    torch.cuda.synchronize()
+    ms_step, wall = timed_graph(torch, launches, args.steps, args.warmup)
+    value = bytes_tok / (ms_step * 1e-3) / 1e9
+    if args.config == "stack_chain":
+        st = chain.status()
+        if st != 0:
+            raise RuntimeError(f"gemv chain reported status {st}")
+    n_launch = len(launches)
+    per_launch_us = ms_step * 1e3 / n_launch
+    achieved = bytes_tok / n_launch / (per_launch_us * 1e-6) / 1e9
+    traffic = STACK_TRAFFIC["bytes_per_launch"] if args.config == "stack" else None
+    roofline = hbm_roofline(achieved, kernel,
+                            basis="algorithmic bytes per launch / (HIP-event time of the timed replays / launches); "
+                                  "the per-launch time includes the gap between dependent launches",
+                            traffic=traffic, traffic_source=STACK_TRAFFIC["source"] if traffic else None,
+                            avg_launch_us=round(per_launch_us, 3), bytes_per_launch=round(bytes_tok / n_launch))
+    check = None if args.no_check else check_stack(torch, layers, acts)
+    return dict(value=value, ms_step=ms_step, wall=wall, roofline=roofline, flops=flops_tok,
+                workload="qwen3-4b q4_0 decode linear stack: 36 layers x 7 GEMVs, batch 1, fp16 act",
+                bytes_per_step=bytes_tok, launches_per_step=n_launch, check=check)
 
 
 def cpu_baseline_stack(target_s=10.0, target_all_s=6.0):
@@ -159,122 +287,36 @@ def cpu_baseline_stack(target_s=10.0, target_all_s=6.0):
                           omp_num_threads=os.environ.get("OMP_NUM_THREADS")))
 
 
-def stack_chain(ops, layers, a, dev):
-    """The token as one persistent chain: 144 dependent stages, one launch."""
-    H, Q, KV, I = QWEN3_4B["hidden"], QWEN3_4B["q"], QWEN3_4B["kv"], QWEN3_4B["inter"]
-    stages = []
-    for L in layers:
-        stages.append(ops.pblock(a["x_attn"], H, [(L["q"], a["yq"], Q), (L["k"], a["yk"], KV), (L["v"], a["yv"], KV)]))
-        stages.append(ops.pblock(a["x_o"], Q, [(L["o"], a["yo"], H)]))
-        stages.append(ops.pblock(a["x_mlp"], H, [(L["gate"], a["yg"], I), (L["up"], a["yu"], I)]))
-        stages.append(ops.pblock(a["x_down"], I, [(L["down"], a["yd"], H)]))
-    return ops.GemvChain(ops.GGML_Q4_0, stages, dev)
-
-
-def run_stack(args, torch, dev):
-    from vybforge_amd import ops
-    shapes, bytes_tok, flops_tok, wbytes_layer = stack_bytes()
-    layers, acts = build_stack(torch, dev, args.seed)
-    if args.config == "stack_chain":
-        chain = stack_chain(ops, layers, acts, dev)
-        launches = [chain]
-        kernel = "k_gemv_chain<q4_0> (one persistent launch per token, 144 dependent stages)"
-    else:
-        launches = stack_launches(ops, layers, acts)
-        kernel = "k_gemv_pair<q4_0> (all 144 launches per token)"
-    torch.cuda.synchronize()
-
-    # capture one token as a graph
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for f in launches:
-            f()
-    torch.cuda.current_stream().wait_stream(side)
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for f in launches:
-            f()
-    torch.cuda.synchronize()
-
-    for _ in range(args.warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record()
-    for _ in range(args.steps):
-        g.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_ev = ev0.elapsed_time(ev1)
-    ms_step = ms_ev / args.steps
-    value = bytes_tok / (ms_step * 1e-3) / 1e9
-
-    if args.config == "stack_chain":
-        st = chain.status()
-        if st != 0:
-            raise RuntimeError(f"gemv chain reported status {st}")
-    # dominant kernel, live: the token's launches back to back on one stream, event-timed
-    # over many tokens; the per-launch average includes inter-launch gaps
-    n_launch = len(launches)
-    achieved = bytes_tok / n_launch / (ms_step * 1e-3 / n_launch) / 1e9
-    # HBM bytes per launch from rocprofv3 FETCH_SIZE x 2.00 + WRITE_SIZE x 1.00 (factors from a
-    # plain 256 MiB copy), averaged over the four launches of a layer: profiles/q4_0_gemv_decode_stack.md
-    traffic = STACK_TRAFFIC_PER_LAUNCH if args.config == "stack" else None
-    roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic,
-                    kernel=kernel,
-                    avg_launch_us=round(ms_step * 1e3 / n_launch, 3),
-                    bytes_per_launch=round(bytes_tok / n_launch))
-    return dict(value=value, ms_step=ms_step, wall=wall, roofline=roofline, flops=flops_tok,
-                workload="qwen3-4b q4_0 decode linear stack: 36 layers x 7 GEMVs, batch 1, fp16 act",
-                bytes_per_step=bytes_tok, launches_per_step=n_launch)
-
+# ---- config 1: one q4_0 GEMV ----------------------------------------------------------------
 
 def run_gemv1(args, torch, dev):
-    """Config 1: q4_0 GEMV 9728x2560, fp32 x, fp32 y, rotating 24 weight copies (>300 MB)."""
-    from vybforge_amd import ops
+    """q4_0 GEMV 9728x2560, fp32 x, fp32 y, rotating 24 weight copies (336 MB > the MALL)."""
+    from oracle import matmul
+    from vybforge_amd import ops, synth
     N, K = 9728, 2560
     gen = torch.Generator(device=dev)
-    gen.manual_seed(args.seed)
-    copies = [q4_0_blocks_gpu(torch, gen, N, K, dev) for _ in range(24)]
+    gen.manual_seed(args.seed + 1)
+    copies = [synth.q4_0_weights_torch(gen, N, K, dev) for _ in range(24)]
     x = torch.randn(K, generator=gen, device=dev)
     y = torch.empty(1, N, device=dev)
-    launch = [lambda W=W: ops.gemv(ops.GGML_Q4_0, W, x, N, K, out=y) for W in copies]
-    for f in launch:
-        f()
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for f in launch:
-            f()
-    for _ in range(args.warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record()
-    for _ in range(args.steps):
-        g.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per = ev0.elapsed_time(ev1) / args.steps / len(launch)
+    ms, wall = timed_graph(torch, [lambda W=W: ops.gemv(ops.GGML_Q4_0, W, x, N, K, out=y) for W in copies],
+                           args.steps, args.warmup)
+    per = ms / len(copies)
     bytes_call = N * K // 32 * 18 + 4 * K + 4 * N
     value = bytes_call / (per * 1e-3) / 1e9
-    roofline = dict(bound="hbm", achieved=round(value, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(value / HBM_PEAK_GBS, 4), traffic=None, kernel="k_gemv_pair<q4_0,f32>",
-                    avg_launch_us=round(per * 1e3, 3), bytes_per_launch=bytes_call)
-    return dict(value=value, ms_step=per * len(launch), wall=wall, roofline=roofline,
-                flops=2 * N * K * len(launch), workload="q4_0 GEMV 9728x2560 fp32 x (24 rotated copies)",
-                bytes_per_step=bytes_call * len(launch), launches_per_step=len(launch))
+    check = None
+    if not args.no_check:
+        ref = matmul.gemv_q4_0_f64(copies[-1].cpu().numpy(), x.cpu().numpy(), N, K)
+        check = dict(ok=True, rel=expect("gemv1", rel_gate(y.cpu().numpy(), ref)), what="last copy, all 9728 rows")
+    return dict(value=value, unit="GB/s", ms_step=ms, wall=wall, flops=2 * N * K * len(copies),
+                roofline=hbm_roofline(value, "k_gemv_pair<q4_0, f32 x>", "bytes per GEMV / (event time / 24 launches)",
+                                      avg_launch_us=round(per * 1e3, 3), bytes_per_launch=bytes_call),
+                workload="q4_0 GEMV 9728x2560 fp32 x -> fp32 y (24 rotated weight copies)",
+                bytes_per_step=bytes_call * len(copies), launches_per_step=len(copies), check=check)
 
 
 def run_kquant(args, torch, dev):
-    """K-quant GEMV at the Qwen3-4B MLP shape 9728x2560 (fp16 x, f32 y), 24 rotated weight copies
-    (> the 256 MB MALL), one GEMV per copy in one graph."""
+    """K-quant GEMV at the Qwen3-4B MLP shape 9728x2560 (fp16 x, f32 y), 24 rotated weight copies."""
     from vybforge_amd import ops
     N, K, ty = 9728, 2560, args.wtype
     name = {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 22: "IQ2_S"}[ty]
@@ -288,10 +330,9 @@ def run_kquant(args, torch, dev):
     per = ms / len(copies)
     bytes_call = ops.row_bytes(ty, K) * N + 2 * K + 4 * N
     value = bytes_call / (per * 1e-3) / 1e9
-    roofline = dict(bound="hbm", achieved=round(value, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(value / HBM_PEAK_GBS, 4), traffic=None, kernel=f"k_gemv_pair<{name}>",
-                    avg_launch_us=round(per * 1e3, 3), bytes_per_launch=bytes_call)
-    return dict(value=value, ms_step=ms, wall=wall, roofline=roofline, flops=2 * N * K * len(copies),
+    return dict(value=value, ms_step=ms, wall=wall, flops=2 * N * K * len(copies),
+                roofline=hbm_roofline(value, f"k_gemv_pair<{name}>", "bytes per GEMV / (event time / 24 launches)",
+                                      avg_launch_us=round(per * 1e3, 3), bytes_per_launch=bytes_call),
                 workload=f"{name} GEMV 9728x2560 fp16 x (24 rotated copies)",
                 bytes_per_step=bytes_call * len(copies), launches_per_step=len(copies))
 
@@ -314,152 +355,150 @@ def run_producers(args, torch, dev):
     swi_bytes = 8 * F * 2 + 4 * F + F + 4 * (F // 32)
     per = ms / len(launches)
     value = (rms_bytes + swi_bytes) * 16 / (ms * 1e-3) / 1e9
-    roofline = dict(bound="hbm", achieved=round(value, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(value / HBM_PEAK_GBS, 4), traffic=None, kernel="k_rms_q8 + k_swiglu_q8",
-                    avg_launch_us=round(per * 1e3, 3), bytes_per_launch=(rms_bytes + swi_bytes) // 2)
-    return dict(value=value, ms_step=ms, wall=wall, roofline=roofline, flops=0,
+    return dict(value=value, ms_step=ms, wall=wall, flops=0,
+                roofline=hbm_roofline(value, "k_rms_q8 + k_swiglu_q8", "bytes / event time",
+                                      avg_launch_us=round(per * 1e3, 3)),
                 workload="RMSNorm+q8 (1x5120 f64) and SwiGLU+q8 (17408 f64), 16 each per step",
                 bytes_per_step=(rms_bytes + swi_bytes) * 16, launches_per_step=len(launches))
 
 
 def run_router(args, torch, dev):
     """GLM-5 router logits: T tokens of 6144 (bf16) against the 256 x 6144 bf16 gate weight,
-    float64 accumulation and output, 8 rotated weight copies per graph."""
+    float64 accumulation and output, 96 rotated weight copies per graph (302 MB > the MALL)."""
     from vybforge_amd import ops
     T, E, H = args.tokens, 256, 6144
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed)
-    ws = [(torch.randn(E, H, generator=gen, device=dev) * 0.02).to(torch.bfloat16) for _ in range(8)]
+    ws = [(torch.randn(E, H, generator=gen, device=dev) * 0.02).to(torch.bfloat16) for _ in range(96)]
     x = torch.randn(T, H, generator=gen, device=dev).to(torch.bfloat16)
-    ms, wall = timed_graph(torch, [lambda w=w: ops.router_logits(x, w) for w in ws], args.steps, args.warmup)
+    y = torch.empty(T, E, dtype=torch.float64, device=dev)
+
+    def launch(w):
+        from vybforge_amd._lib import call
+        call("vybdq_router_logits", x.data_ptr(), ops.BF16, w.data_ptr(), ops.BF16, y.data_ptr(), ops.F64, T, E, H,
+             torch.cuda.current_stream().cuda_stream)
+    ms, wall = timed_graph(torch, [lambda w=w: launch(w) for w in ws], args.steps, args.warmup)
     per = ms / len(ws)
     nbytes = E * H * 2 + T * H * 2 + T * E * 8
     value = nbytes / (per * 1e-3) / 1e9
-    roofline = dict(bound="hbm", achieved=round(value, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(value / HBM_PEAK_GBS, 4), traffic=None, kernel="k_router_logits<bf16, bf16>",
-                    avg_launch_us=round(per * 1e3, 3), bytes_per_launch=nbytes)
-    return dict(value=value, ms_step=ms, wall=wall, roofline=roofline, flops=2 * T * E * H * len(ws),
-                workload=f"GLM-5 router logits T={T}: 256 x 6144 bf16 gate, float64 accumulation",
+    return dict(value=value, ms_step=ms, wall=wall, flops=2 * T * E * H * len(ws),
+                roofline=hbm_roofline(value, "k_router_logits<bf16, bf16>", "bytes per call / (event time / 96)",
+                                      avg_launch_us=round(per * 1e3, 3), bytes_per_launch=nbytes),
+                workload=f"GLM-5 router logits T={T}: 256 x 6144 bf16 gate, float64 accumulation (96 rotated copies)",
                 bytes_per_step=nbytes * len(ws), launches_per_step=len(ws))
 
 
-def timed_graph(torch, launches, steps, warmup):
-    """Capture the launches as one graph; return (ms per replay, wall seconds)."""
-    for f in launches:
-        f()
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for f in launches:
-            f()
-    for _ in range(warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record()
-    for _ in range(steps):
-        g.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    return ev0.elapsed_time(ev1) / steps, time.perf_counter() - t0
+# ---- config 4: EXL3 ---------------------------------------------------------------------------
 
-
-def run_exl3(args, torch, dev):
-    """Config 4: EXL3 4-bpw GEMM K=5120 x N=17408, batch 1 or 16, 8 rotated trellis copies."""
+def run_exl3(args, torch, dev, batch=None):
+    """EXL3 4-bpw GEMM K=5120 x N=17408, 8 rotated trellis copies (357 MB > the MALL)."""
+    import numpy as np
+    from oracle import exl3
     from vybforge_amd import ops
-    K, N, B = 5120, 17408, args.batch
+    K, N = 5120, 17408
+    B = batch or args.batch
     gen = torch.Generator(device=dev)
-    gen.manual_seed(args.seed)
+    gen.manual_seed(args.seed + 4)
     ncopy = 8
     lins = []
     for _ in range(ncopy):
         t = torch.randint(0, 65536, (K // 16, N // 16, 64), generator=gen, device=dev, dtype=torch.int32).to(torch.uint16)
-        suh = ((torch.randn(K, generator=gen, device=dev) * 0.01).abs() * (torch.randint(0, 2, (K,), generator=gen, device=dev) * 2 - 1)).to(torch.float16)
-        svh = ((torch.randn(N, generator=gen, device=dev) * 0.01).abs() * (torch.randint(0, 2, (N,), generator=gen, device=dev) * 2 - 1)).to(torch.float16)
+        sgn = lambda n: torch.randint(0, 2, (n,), generator=gen, device=dev) * 2 - 1
+        suh = ((torch.randn(K, generator=gen, device=dev) * 0.01).abs() * sgn(K)).to(torch.float16)
+        svh = ((torch.randn(N, generator=gen, device=dev) * 0.01).abs() * sgn(N)).to(torch.float16)
         lins.append(ops.Exl3Linear(t, suh, svh, K, N))
     x = torch.randn(B, K, generator=gen, device=dev).to(torch.float16)
     y = torch.empty(B, N, device=dev)
-    launches = [lambda L=L: L(x, out=y) for L in lins]
-    ms, wall = timed_graph(torch, launches, args.steps, args.warmup)
+    ms, wall = timed_graph(torch, [lambda L=L: L(x, out=y) for L in lins], args.steps, args.warmup)
     per = ms / ncopy
     bytes_call = K * N // 2 + 2 * K + 2 * N + B * (2 * K + 4 * N)
     value = bytes_call / (per * 1e-3) / 1e9
-    flops = 2 * K * N * B
-    roofline = dict(bound="hbm", achieved=round(value, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(value / HBM_PEAK_GBS, 4), traffic=None,
-                    kernel=("k_exl3_gemm, one launch with the x and output rotations" if B <= 2 else
-                            "k_exl3_xprep + k_exl3_gemm + k_exl3_out") + " (VALU-bound trellis decode)",
-                    avg_launch_us=round(per * 1e3, 3), bytes_per_launch=bytes_call)
-    return dict(value=value, ms_step=ms, wall=wall, roofline=roofline, flops=flops * ncopy,
-                workload=f"EXL3 4-bpw mcg GEMM K=5120 N=17408 batch {B} (8 rotated trellis copies)",
-                bytes_per_step=bytes_call * ncopy, launches_per_step=ncopy)
+    check = None
+    if not args.no_check:
+        L = lins[-1]
+        t_last = L.t.view(torch.int16).cpu().numpy().view(np.uint16)
+        w = exl3.dequant_exl3_f64(t_last[:, -64:], L.suh.cpu().numpy(), L.svh.cpu().numpy()[-1024:])
+        ref = x.to(torch.float64).cpu().numpy() @ w
+        check = dict(ok=True, rel=expect(f"exl3 b{B}", rel_gate(y[:, -1024:].cpu().numpy(), ref)),
+                     what="last copy, last 1024 columns, float64 oracle")
+    kernel = ("k_exl3_gemm, one launch with the x and output rotations" if B <= 2 else
+              "k_exl3_xprep + k_exl3_gemm (matrix-core products) + k_exl3_out")
+    return dict(value=value, unit="GB/s", ms_step=ms, wall=wall, flops=2 * K * N * B * ncopy,
+                roofline=hbm_roofline(value, kernel, "bytes per call / (event time / 8 calls)",
+                                      avg_launch_us=round(per * 1e3, 3), bytes_per_launch=bytes_call),
+                workload=f"EXL3 4-bpw mcg GEMM K=5120 N=17408 batch {B} fp16 x (8 rotated trellis copies)",
+                bytes_per_step=bytes_call * ncopy, launches_per_step=ncopy, check=check)
 
 
-MFMA_BF16_PEAK_TFLOPS = float(ROOFLINE["mfma_dense_TFLOPs"]["bf16"])
+# ---- config 3: Q8_0 prefill ---------------------------------------------------------------------
+
+PREFILL_SHAPES = [(17408, 5120), (5120, 17408)]  # (N, K): up, down
 
 
-def q8_0_blocks_gpu(torch, gen, N, K, dev):
-    """Seeded packed Q8_0 rows on the device: fp16 d = |N(0, 0.01)|, int8 uniform in [-127, 127]."""
-    nb = N * (K // 32)
-    blk = torch.empty((nb, 34), dtype=torch.uint8, device=dev)
-    d = (torch.randn(nb, generator=gen, device=dev) * 0.01).abs().to(torch.float16)
-    blk[:, 0:2] = d.view(torch.uint8).view(nb, 2)
-    blk[:, 2:] = torch.randint(-127, 128, (nb, 32), generator=gen, device=dev, dtype=torch.int8).view(torch.uint8)
-    return blk.view(-1)
+def _prefill_check(args, name, W, y, N, K, xref):
+    from oracle import matmul
+    if args.no_check:
+        return None
+    cols = 256
+    rb = K // 32 * 34
+    wrows = matmul.q8_0_matrix(W[:cols * rb].cpu().numpy(), cols, K)
+    ref = matmul.gemm_rows_f64(xref, wrows)
+    return expect(f"{name} N={N} K={K}", rel_gate(y[:, :cols].cpu().numpy(), ref))
 
 
 def run_prefill(args, torch, dev):
-    """Config 3: Q8_0 prefill GEMMs M=512 (up K=5120 -> N=17408, down K=17408 -> N=5120), bf16 X,
-    f32 Y, 3 rotated weight copies of each (>500 MB, past the 256 MB MALL)."""
-    from vybforge_amd import ops
+    """Q8_0 prefill GEMMs M=512 (up K=5120 -> N=17408, down K=17408 -> N=5120), bf16 X, f32 Y, 3 rotated
+    weight copies of each (568 MB > the MALL)."""
+    from vybforge_amd import ops, synth
     M = 512
     gen = torch.Generator(device=dev)
-    gen.manual_seed(args.seed)
-    shapes = [(17408, 5120), (5120, 17408)]
+    gen.manual_seed(args.seed + 3)
     ncopy = 3
-    ws = ops.GemmWorkspace([(M, N, K) for N, K in shapes], dev, ops.GGML_Q8_0)
-    launches, flops, nbytes = [], 0, 0
-    for N, K in shapes:
+    ws = ops.GemmWorkspace([(M, N, K) for N, K in PREFILL_SHAPES], dev, ops.GGML_Q8_0)
+    launches, flops, nbytes, last = [], 0, 0, []
+    for N, K in PREFILL_SHAPES:
         x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
         y = torch.empty(M, N, device=dev)
         for _ in range(ncopy):
-            W = q8_0_blocks_gpu(torch, gen, N, K, dev)
+            W = synth.q8_0_weights_torch(gen, N, K, dev)
             launches.append(lambda W=W, x=x, y=y, N=N, K=K: ops.gemm(ops.GGML_Q8_0, W, x, N, K, out=y, workspace=ws))
             flops += 2 * M * N * K
             nbytes += N * K // 32 * 34 + 2 * M * K + 4 * M * N
+        last.append((W, x, y, N, K))
     ms, wall = timed_graph(torch, launches, args.steps, args.warmup)
     tflops = flops / (ms * 1e-3) / 1e12
     per = ms / len(launches)
+    check = None
+    if not args.no_check:
+        rels = [_prefill_check(args, "prefill", W, y, N, K, x.to(torch.float64).cpu().numpy()) for W, x, y, N, K in last]
+        check = dict(ok=True, rel=max(rels), what="last copy of each shape, 512 rows x first 256 columns, float64 oracle")
     roofline = dict(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s",
                     frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), traffic=None,
-                    kernel="k_mmq<Q8_0,bf16> (fp16 MFMA 16x16x32, weights dequantized into operand registers)", avg_launch_us=round(per * 1e3, 3),
+                    kernel="k_mmq<Q8_0,bf16> (fp16 MFMA 16x16x32, weights dequantized into operand registers)",
+                    basis="flops per step / event time", avg_launch_us=round(per * 1e3, 3),
                     flops_per_launch=flops // len(launches))
     return dict(value=tflops, unit="TFLOP/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
                 workload="Q8_0 prefill GEMMs M=512: 5120->17408 and 17408->5120 (bf16 X, f32 Y)",
-                bytes_per_step=nbytes, launches_per_step=len(launches))
-
-
-MFMA_I8_PEAK_TOPS = float(ROOFLINE["mfma_dense_TFLOPs"]["int8_TOPs"])
+                bytes_per_step=nbytes, launches_per_step=len(launches), check=check)
 
 
 def run_prefill_i8(args, torch, dev):
-    """Config 3, int8 path: the same two Q8_0 GEMMs with the activations quantized per 32-value
-    block (xq8) on the device and int8 MFMA; the quantizer runs inside the timed step."""
-    from vybforge_amd import ops
+    """The same two Q8_0 GEMMs with the activations quantized per 32-value block (xq8) on the device
+    and int8 MFMA; the quantizer runs inside the timed step."""
+    from oracle import formats
+    from vybforge_amd import ops, synth
     M = 512
     gen = torch.Generator(device=dev)
-    gen.manual_seed(args.seed)
-    shapes = [(17408, 5120), (5120, 17408)]
+    gen.manual_seed(args.seed + 3)
     ncopy = 3
-    ws = ops.GemmWorkspace([(M, N, K) for N, K in shapes], dev, int8=True)
-    launches, flops, nbytes = [], 0, 0
-    for N, K in shapes:
+    ws = ops.GemmWorkspace([(M, N, K) for N, K in PREFILL_SHAPES], dev, int8=True)
+    launches, flops, nbytes, last = [], 0, 0, []
+    for N, K in PREFILL_SHAPES:
         x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
         q = (torch.empty(M, K, dtype=torch.int8, device=dev), torch.empty(M, K // 32, device=dev))
         y = torch.empty(M, N, device=dev)
         for _ in range(ncopy):
-            W = q8_0_blocks_gpu(torch, gen, N, K, dev)
+            W = synth.q8_0_weights_torch(gen, N, K, dev)
 
             def f(W=W, x=x, q=q, y=y, N=N, K=K):
                 ops.quant_q8_act(x, out=q)
@@ -467,51 +506,121 @@ def run_prefill_i8(args, torch, dev):
             launches.append(f)
             flops += 2 * M * N * K
             nbytes += N * K // 32 * 34 + 2 * M * K + 4 * M * N
+        last.append((W, q, y, N, K))
     ms, wall = timed_graph(torch, launches, args.steps, args.warmup)
     tops = flops / (ms * 1e-3) / 1e12
     per = ms / len(launches)
+    check = None
+    if not args.no_check:
+        rels = [_prefill_check(args, "prefill_i8", W, y, N, K,
+                               formats.dequant_q8_act(q[0].cpu().numpy(), q[1].cpu().numpy()).astype("float64"))
+                for W, q, y, N, K in last]
+        check = dict(ok=True, rel=max(rels), what="last copy of each shape, 512 rows x first 256 columns, float64 "
+                                                  "oracle of the xq8-dequantized X")
     roofline = dict(bound="mfma", achieved=round(tops, 2), peak=MFMA_I8_PEAK_TOPS, unit="TOP/s",
                     frac=round(tops / MFMA_I8_PEAK_TOPS, 4), traffic=None,
-                    kernel="xq8 + k_mmq_i8 (int8 MFMA 16x16x32 per block, float32 block scaling; VALU-bound)",
-                    avg_launch_us=round(per * 1e3, 3), flops_per_launch=flops // len(launches),
-                    frac_of_bf16_peak=round(tops / MFMA_BF16_PEAK_TFLOPS, 4))
+                    kernel="xq8 + k_mmq_i8 (int8 MFMA 16x16x32 per block, float32 block scaling)",
+                    basis="ops per step / event time (the xq8 launches included)", avg_launch_us=round(per * 1e3, 3),
+                    flops_per_launch=flops // len(launches), frac_of_bf16_peak=round(tops / MFMA_BF16_PEAK_TFLOPS, 4))
     return dict(value=tops, unit="TOP/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
                 workload="Q8_0 prefill GEMMs M=512 int8 path: xq8(X bf16) then int8 MFMA, 5120->17408 and 17408->5120",
-                bytes_per_step=nbytes, launches_per_step=len(launches))
+                bytes_per_step=nbytes, launches_per_step=len(launches), check=check)
 
 
-def run_moe(args, torch, dev):
-    """Config 5: GLM-5-style MoE layer, H=6144, 256 routed + 1 shared expert, top-8, I=2048,
-    q4_0 expert tensors (5.46 GB), T tokens bf16, router logits N(0,1)."""
-    from vybforge_amd import ops
-    H, I, E, k, T = 6144, 2048, 256, 8, args.tokens
+# ---- config 5: GLM-5 MoE layer --------------------------------------------------------------------
+
+MOE = dict(H=6144, I=2048, E=256, k=8)
+
+
+def build_moe(torch, dev, seed):
+    from vybforge_amd import ops, synth
+    H, I, E, k = MOE["H"], MOE["I"], MOE["E"], MOE["k"]
     gen = torch.Generator(device=dev)
-    gen.manual_seed(args.seed)
-    wg = q4_0_blocks_gpu(torch, gen, E * I, H, dev)
-    wu = q4_0_blocks_gpu(torch, gen, E * I, H, dev)
-    wd = q4_0_blocks_gpu(torch, gen, E * H, I, dev)
-    sh = (q4_0_blocks_gpu(torch, gen, I, H, dev), q4_0_blocks_gpu(torch, gen, I, H, dev),
-          q4_0_blocks_gpu(torch, gen, H, I, dev))
-    layer = ops.MoeLayer(ops.GGML_Q4_0, wg, wu, wd, H, I, E, k, shared=sh)
-    x = torch.randn(T, H, generator=gen, device=dev).to(torch.bfloat16)
-    logits = torch.randn(T, E, generator=gen, device=dev)
-    out = torch.empty(T, H, device=dev)
-    _, idx, _ = layer(x, logits, out=out, routing=True)
-    distinct = int(torch.unique(idx).numel())
-    ms, wall = timed_graph(torch, [lambda: layer(x, logits, out=out)], args.steps, args.warmup)
+    gen.manual_seed(seed)
+    q4 = lambda n, kk: synth.q4_0_weights_torch(gen, n, kk, dev)
+    layer = ops.MoeLayer(ops.GGML_Q4_0, q4(E * I, H), q4(E * I, H), q4(E * H, I), H, I, E, k,
+                         shared=(q4(I, H), q4(I, H), q4(H, I)))
+    return layer, gen
+
+
+def check_moe(torch, layer, x, logits, out, idx, w, ntok=2):
+    """Routing of every token against the oracle router (identical sets, |dw| < 1e-4,
+    native/glm53/verify_moe_vyb.py:54-59); ntok tokens' outputs on 256 columns of H against the
+    float64 oracle (gate/up of each hit expert and the slice's down rows decoded on the host)."""
+    import numpy as np
+    from oracle import matmul, moe
+    H, I, k = MOE["H"], MOE["I"], MOE["k"]
+    rbh, rbi = H // 32 * 18, I // 32 * 18
+    T = x.shape[0]
+    idx, w = idx.cpu().numpy(), w.cpu().numpy()
+    ridx, rw = moe.route_logits(logits.to(torch.float64).cpu().numpy(), k)
+    for t in range(T):
+        a, b = dict(zip(idx[t].tolist(), w[t].tolist())), dict(zip(ridx[t].tolist(), rw[t].tolist()))
+        if set(a) != set(b) or max(abs(a[e] - b[e]) for e in a) >= 1e-4:
+            raise CheckFailed(f"moe T={T}: routing of token {t} differs from the oracle")
+    c0 = (T * 997) % (H - 256) // 64 * 64
+    cols = slice(c0, c0 + 256)
+    x64 = x.to(torch.float64).cpu().numpy()
+    toks = sorted({0, T - 1})[:ntok]
+
+    def ffn(e, xt):
+        if e < 0:
+            gb, ub, db = layer.shared
+        else:
+            gb = layer.w[0][e * I * rbh:(e + 1) * I * rbh]
+            ub = layer.w[1][e * I * rbh:(e + 1) * I * rbh]
+            db = layer.w[2][e * H * rbi:(e + 1) * H * rbi]
+        g = matmul.q4_0_matrix(gb.cpu().numpy(), I, H)
+        u = matmul.q4_0_matrix(ub.cpu().numpy(), I, H)
+        d = matmul.q4_0_matrix(db[c0 * rbi:(c0 + 256) * rbi].cpu().numpy(), 256, I)
+        return moe.ffn_rows(xt, g, u, d)[0]
+    ref = np.zeros((len(toks), 256))
+    for r, t in enumerate(toks):
+        xt = x64[t:t + 1]
+        ref[r] = sum(rw[t, s] * ffn(int(ridx[t, s]), xt) for s in range(k)) + ffn(-1, xt)
+    return expect(f"moe T={T}", rel_gate(out.cpu().numpy()[toks][:, cols], ref))
+
+
+def run_moe(args, torch, dev, tokens=None, built=None):
+    """GLM-5-style MoE layer, H=6144, 256 routed + 1 shared expert, top-8, I=2048, q4_0 expert tensors
+    (5.46 GB), T tokens bf16, router logits N(0,1). T <= 16: the step is R layer calls on R distinct
+    (x, logits) pairs, so the experts hit per step exceed the 256 MB MALL."""
+    H, E, k = MOE["H"], MOE["E"], MOE["k"]
+    I = MOE["I"]
+    T = tokens or args.tokens
+    layer, gen = built or build_moe(torch, dev, args.seed + 5)
+    R = 8 if T == 1 else (2 if T <= 16 else 1)
+    xs = [torch.randn(T, H, generator=gen, device=dev).to(torch.bfloat16) for _ in range(R)]
+    lgs = [torch.randn(T, E, generator=gen, device=dev) for _ in range(R)]
+    outs = [torch.empty(T, H, device=dev) for _ in range(R)]
+    routed = [layer(xs[r], lgs[r], routing=True) for r in range(R)]
+    distinct = [int(torch.unique(rt[1]).numel()) for rt in routed]
+    union = int(torch.unique(torch.cat([rt[1].reshape(-1) for rt in routed])).numel())
+    ms, wall = timed_graph(torch, [lambda r=r: layer(xs[r], lgs[r], out=outs[r]) for r in range(R)], args.steps,
+                           args.warmup)
     per_expert = 3 * I * H // 32 * 18
-    nbytes = (distinct + 1) * per_expert + T * H * 2 + T * E * 4 + T * H * 4
-    flops = T * (k + 1) * 3 * 2 * I * H
+    nbytes = sum((d + 1) * per_expert + T * H * 2 + T * E * 4 + T * H * 4 for d in distinct)
+    flops = R * T * (k + 1) * 3 * 2 * I * H
     gbs = nbytes / (ms * 1e-3) / 1e9
-    roofline = dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None,
-                    kernel=f"MoE layer: route, bucket, {'k_moe_gemv' if T <= 64 else 'k_moe_mm'} gate|up+SwiGLU "
-                           "and down over the routed and shared experts, combine",
-                    avg_launch_us=round(ms * 1e3, 3), bytes_per_launch=nbytes)
-    return dict(value=gbs, ms_step=ms, wall=wall, roofline=roofline, flops=flops,
-                workload=f"GLM-5-style MoE layer T={T}: H=6144, 256+1 experts, top-8, I=2048, q4_0 "
-                         f"({distinct} distinct routed experts hit)",
-                bytes_per_step=nbytes, launches_per_step=1)
+    check = None
+    if not args.no_check:
+        rels = []
+        for r in sorted({0, R - 1}):
+            if not torch.equal(outs[r], routed[r][0]):
+                raise CheckFailed(f"moe T={T}: graph replay output differs from the eager call")
+            rels.append(check_moe(torch, layer, xs[r], lgs[r], outs[r], routed[r][1], routed[r][2]))
+        check = dict(ok=True, rel=max(rels), what="routing of every token; 2 tokens x 256 columns vs float64 oracle; "
+                                                  "graph replay == eager")
+    path = "k_moe_gemv" if T <= 64 else "k_moe_mm"
+    roofline = hbm_roofline(gbs, f"MoE layer: route+bucket, {path} gate|up+SwiGLU and down, combine",
+                            "algorithmic bytes (hit experts + shared + activations) / event time",
+                            avg_layer_us=round(ms * 1e3 / R, 3), bytes_per_layer=nbytes // R)
+    return dict(value=gbs, unit="GB/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
+                tflops=round(flops / (ms * 1e-3) / 1e12, 3),
+                workload=f"GLM-5-style MoE layer T={T}: H=6144, 256+1 experts, top-8, I=2048, q4_0; {R} layer "
+                         f"call(s) per step on distinct inputs ({sum(distinct) / R:.1f} routed experts hit per call, "
+                         f"{union} distinct per step)",
+                bytes_per_step=nbytes, launches_per_step=R, check=check)
 
 
 def run_copy(args, torch, dev):
@@ -521,25 +630,53 @@ def run_copy(args, torch, dev):
     n = 64 * 1024 * 1024
     src = torch.ones(n, device=dev)
     dst = torch.empty(n, device=dev)
-    for _ in range(args.warmup):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record()
-    for _ in range(args.steps):
-        dst.copy_(src)
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = ev0.elapsed_time(ev1) / args.steps
+    ms, wall = timed_graph(torch, [lambda: dst.copy_(src)], args.steps, args.warmup)
     nbytes = 2 * n * 4
-    gbs = nbytes / (ms_step * 1e-3) / 1e9
-    roofline = dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=round(gbs / HBM_PEAK_GBS, 4), traffic=None, kernel="torch device copy (calibration)")
-    return dict(value=gbs, ms_step=ms_step, wall=wall, roofline=roofline, flops=0,
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(value=gbs, ms_step=ms, wall=wall, flops=0,
+                roofline=hbm_roofline(gbs, "torch device copy (calibration)", "bytes / event time"),
                 workload="device copy 256 MiB -> 256 MiB (counter calibration)", bytes_per_step=nbytes,
                 launches_per_step=1)
+
+
+# ---- driver ---------------------------------------------------------------------------------------
+
+def sub_record(r):
+    rec = dict(workload=r["workload"], value=round(r["value"], 2), unit=r.get("unit", "GB/s"),
+               ms_per_step=round(r["ms_step"], 4), roofline=r["roofline"], check=r.get("check"))
+    if "tflops" in r:
+        rec["tflops"] = r["tflops"]
+    return rec
+
+
+def run_all(args, torch, dev):
+    """Every workload of the metric, each as a sub-record (fewer steps than the headline: each
+    replay is 0.3-15 ms of GPU work)."""
+    import copy
+    sub = copy.copy(args)
+    sub.steps, sub.warmup = max(5, min(args.steps, 20)), max(2, min(args.warmup, 3))
+    recs = {}
+
+    def leg(name, fn, *a, **kw):
+        log(f"config {name} ...")
+        t0 = time.perf_counter()
+        r = fn(sub, torch, dev, *a, **kw)
+        recs[name] = sub_record(r)
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        log(f"config {name}: {recs[name]['value']} {recs[name]['unit']} ({time.perf_counter() - t0:.1f} s)")
+
+    leg("cfg1_q4_0_gemv_9728x2560", run_gemv1)
+    leg("cfg3_q8_0_prefill_m512_fp16mfma", run_prefill)
+    leg("cfg3_q8_0_prefill_m512_int8mfma", run_prefill_i8)
+    leg("cfg4_exl3_b1", run_exl3, batch=1)
+    leg("cfg4_exl3_b16", run_exl3, batch=16)
+    built = build_moe(torch, dev, args.seed + 5)
+    for T in (1, 16, 256):
+        leg(f"cfg5_moe_T{T}", run_moe, tokens=T, built=built)
+    del built
+    torch.cuda.empty_cache()
+    return recs
 
 
 def main():
@@ -548,43 +685,42 @@ def main():
         print("bench.py measures one GPU: the fused dequant-matmul path runs on a single GPU "
               "(each GPU would hold a row / expert shard); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    sys.path.insert(0, HERE)
     import torch
     if not torch.cuda.is_available():
         sys.exit("no GPU visible")
     dev = torch.device("cuda:0")
-    if args.config == "gemv1":
-        r = run_gemv1(args, torch, dev)
-    elif args.config == "kquant":
-        r = run_kquant(args, torch, dev)
-    elif args.config == "producers":
-        r = run_producers(args, torch, dev)
-    elif args.config == "router":
-        r = run_router(args, torch, dev)
-    elif args.config == "exl3":
-        r = run_exl3(args, torch, dev)
-    elif args.config == "prefill":
-        r = run_prefill(args, torch, dev)
-    elif args.config == "prefill_i8":
-        r = run_prefill_i8(args, torch, dev)
-    elif args.config == "moe":
-        r = run_moe(args, torch, dev)
-    elif args.config == "copy":
-        r = run_copy(args, torch, dev)
-    else:
-        r = run_stack(args, torch, dev)
+    runners = dict(gemv1=run_gemv1, kquant=run_kquant, producers=run_producers, router=run_router, exl3=run_exl3,
+                   prefill=run_prefill, prefill_i8=run_prefill_i8, moe=run_moe, copy=run_copy)
+    configs = None
+    try:
+        if args.config in ("all", "stack", "stack_chain"):
+            log("headline: decode stack ...")
+            r = run_stack(args, torch, dev)
+            torch.cuda.empty_cache()
+            if args.config == "all":
+                configs = run_all(args, torch, dev)
+        else:
+            r = runners[args.config](args, torch, dev)
+    except CheckFailed as e:
+        print(f"bench.py: output check failed: {e}", file=sys.stderr)
+        sys.exit(3)
     cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline_stack() if args.config in ("stack", "stack_chain") else None
+    if not args.no_cpu and args.config in ("all", "stack", "stack_chain"):
+        log("cpu baseline ...")
+        cpu = cpu_baseline_stack()
     line = dict(
         metric=METRIC, value=round(r["value"], 2), unit=r.get("unit", "GB/s"), n_gpus=1, steps=args.steps,
         warmup=args.warmup, ms_per_step=round(r["ms_step"], 4), higher_is_better=True,
         scaling="weak", vs_baseline=None, dtype="f16",
-        data="synthetic (seeded q4_0 weights generated on the device, fp16 activations N(0,1))",
+        data="synthetic (seeded q4_0 / Q8_0 / EXL3 weights generated on the device, activations N(0,1))",
         config=dict(workload=r["workload"], bytes_per_step=r["bytes_per_step"],
                     launches_per_step=r["launches_per_step"],
                     hbm_frac=round(r["bytes_per_step"] / (r["ms_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                     tflops=round(r["flops"] / (r["ms_step"] * 1e-3) / 1e12, 3)),
-        roofline=r["roofline"], cpu_baseline=cpu)
+        roofline=r["roofline"], cpu_baseline=cpu, check=r.get("check"))
+    if configs is not None:
+        line["configs"] = configs
     print(json.dumps(line))
 
 
