@@ -118,6 +118,18 @@ int vybdq_gemv_q4_0_seg3(uint64_t X, int64_t K, int x_dt, int order,
                          uint64_t W2, uint64_t Y2, int64_t N2, int y_dt2,
                          uint64_t W3, uint64_t Y3, int64_t N3, int y_dt3, uint64_t stream);
 
+/* Fused launch of up to three GEMVs of GGUF type wtype (2, 8, 12, 13, 14, 22 as vybdq_gemv) that
+   share X [M, K] (M <= 8): segment i has N_i rows W_i -> Y_i [M, N_i] of y_dt_i, plus its optional
+   residual RS_i of the same type; a segment with N_i = 0 is absent (its pointers are ignored).
+   Mirrors the multi-segment p-block of gemv_q4k / gemv_q6k, which fuses q|k|v and gate|up
+   (W2/NS2/Y2/YE2 @56-80, W3/NS3/Y3/YE3 @88-112, RS@120, native/kernels/qwen3.vyb:416-436), and the
+   two Q8_0 matrices of one gemv_q8_0_sk launch (p and p+256, native/kernels/rq80s.vyb:1-12):
+   one launch, X staged once. */
+int vybdq_gemv_seg3(int wtype, uint64_t X, int64_t M, int64_t K, int x_dt,
+                    uint64_t W, uint64_t Y, int64_t N, int y_dt, uint64_t RS,
+                    uint64_t W2, uint64_t Y2, int64_t N2, int y_dt2, uint64_t RS2,
+                    uint64_t W3, uint64_t Y3, int64_t N3, int y_dt3, uint64_t RS3, uint64_t stream);
+
 /* Router logits Y [T, E] = X [T, H] W^T with W [E, H] (w_dt F32, F16 or BF16; the checkpoint's
    router weight is bf16), X of x_dt (F32, F16, BF16 or F64), accumulated in float64 (every
    product exact; fixed lane-strided order); y_dt F64 or F32. vybdq_moe_route / vybdq_moe_forward

@@ -103,3 +103,50 @@ def test_type_id_errors(dev):
     assert lib.vybdq_gemv(3, w.data_ptr(), x.data_ptr(), y.data_ptr(), 1, 4, 256, 0, 0, 0, 0) == _lib.ERR_ARG
     assert lib.vybdq_gemv(14, w.data_ptr(), x.data_ptr(), y.data_ptr(), 1, 4, 128, 0, 0, 0, 0) == _lib.ERR_SHAPE
     assert lib.vybdq_dequant(12, w.data_ptr(), y.data_ptr(), 100, 0, 0) == _lib.ERR_SHAPE
+
+
+SEG_TYPES = [ops.GGML_Q4_0, ops.GGML_Q8_0] + KQ
+
+
+def _weights(ty, rng, N, K):
+    if ty == ops.GGML_Q4_0:
+        return synth.q4_0_weights(rng, N, K)
+    if ty == ops.GGML_Q8_0:
+        return synth.q8_0_weights(rng, N, K)
+    return synth.kquant_weights(rng, ty, N, K)
+
+
+def _rows(ty, raw, N, K):
+    if ty == ops.GGML_Q4_0:
+        return matmul.q4_0_matrix(raw, N, K)
+    if ty == ops.GGML_Q8_0:
+        return matmul.q8_0_matrix(raw, N, K)
+    return matrix_ref(ty, raw, N, K)
+
+
+@pytest.mark.parametrize("ty", SEG_TYPES)
+@pytest.mark.parametrize("shapes,K,M,xdt", [([4096, 1024, 1024], 2560, 1, "f16"),   # q|k|v
+                                            ([9728, 9728], 2560, 1, "bf16"),         # gate|up
+                                            ([5120, 5120], 5120, 1, "f32"),          # two Q8_0 matrices per launch
+                                            ([300, 77, 1000], 768, 3, "f32"),        # ragged segments, 3 rows
+                                            ([64, 0, 128], 1024, 6, "f16")])         # an absent middle segment, 6 rows
+def test_gemv_seg3_every_type(dev, ty, shapes, K, M, xdt):
+    """vybdq_gemv_seg3: up to three matrices of one GGUF type sharing X in one launch, each with its
+    own output dtype and residual, against the float64 gate (native/kernels/qwen3.vyb:416-436)."""
+    rng = np.random.default_rng(sum(shapes) + K + M + ty)
+    x = synth.activations(rng, (M, K))
+    xd, x64 = x_as(x, xdt, dev)
+    ydts = [torch.float32, torch.float16, torch.float64]
+    segs, refs = [], []
+    for i, n in enumerate(shapes):
+        raw = _weights(ty, rng, max(n, 1), K)
+        ydt = ydts[i]
+        rs = torch.from_numpy(synth.activations(rng, (M, max(n, 1))).astype(np.float64)).to(ydt)
+        y = torch.empty((M, max(n, 1)), dtype=ydt, device=dev)
+        segs.append((to_dev(raw, dev), y, n, rs.to(dev)))
+        refs.append(None if n == 0 else matmul.gemm_rows_f64(x64.reshape(M, K), _rows(ty, raw, n, K),
+                                                             rs.to(torch.float64).numpy()))
+    ops.gemv_seg3(ty, xd.reshape(M, K), K, segs)
+    for (W, y, n, rs), ref in zip(segs, refs):
+        if n:
+            assert gate(y.to(torch.float64).cpu().numpy(), ref, y.dtype) < TOL, (n, y.dtype)

@@ -35,6 +35,10 @@ SIGNATURES = {
                              _u64, _u64, _i64, _int,
                              _u64, _u64, _i64, _int,
                              _u64, _u64, _i64, _int, _u64],
+    "vybdq_gemv_seg3": [_int, _u64, _i64, _i64, _int,
+                        _u64, _u64, _i64, _int, _u64,
+                        _u64, _u64, _i64, _int, _u64,
+                        _u64, _u64, _i64, _int, _u64, _u64],
     "vybdq_quant_q8_act": [_u64, _u64, _u64, _i64, _i64, _int, _u64],
     "vybdq_gguf_open": [ctypes.c_char_p],
     "vybdq_gguf_close": [_i64],

@@ -140,19 +140,45 @@ extern "C" int vybdq_gemv_q4_0_seg3(uint64_t X, int64_t K, int x_dt, int order,
   return gemv_common(FMT_Q4_0, order, X, 1, K, x_dt, s, stream);
 }
 
+// GGML type id -> pair-kernel format, or -1
+static int wtype_fmt(int wtype) {
+  switch (wtype) {
+    case 2: return FMT_Q4_0;
+    case 8: return FMT_Q8_0;
+    case 12: return FMT_Q4_K;
+    case 13: return FMT_Q5_K;
+    case 14: return FMT_Q6_K;
+    case 22: return FMT_IQ2_S;
+    default: return -1;
+  }
+}
+
 extern "C" int vybdq_gemv(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K,
                           int x_dt, int y_dt, uint64_t RS, uint64_t stream) {
-  int fmt;
-  switch (wtype) {
-    case 2: fmt = FMT_Q4_0; break;
-    case 8: fmt = FMT_Q8_0; break;
-    case 12: fmt = FMT_Q4_K; break;
-    case 13: fmt = FMT_Q5_K; break;
-    case 14: fmt = FMT_Q6_K; break;
-    case 22: fmt = FMT_IQ2_S; break;
-    default:
-      return set_error(VYBDQ_ERR_ARG, "vybdq_gemv: wtype must be 2 (q4_0), 8 (Q8_0), 12 (Q4_K), 13 (Q5_K), 14 (Q6_K) or 22 (IQ2_S)");
-  }
+  const int fmt = wtype_fmt(wtype);
+  if (fmt < 0)
+    return set_error(VYBDQ_ERR_ARG, "vybdq_gemv: wtype must be 2 (q4_0), 8 (Q8_0), 12 (Q4_K), 13 (Q5_K), 14 (Q6_K) or 22 (IQ2_S)");
   Segs s = one_seg(W, Y, RS, N, y_dt);
+  return gemv_common(fmt, VYBDQ_Q4_GGML, X, M, K, x_dt, s, stream);
+}
+
+extern "C" int vybdq_gemv_seg3(int wtype, uint64_t X, int64_t M, int64_t K, int x_dt,
+                               uint64_t W, uint64_t Y, int64_t N, int y_dt, uint64_t RS,
+                               uint64_t W2, uint64_t Y2, int64_t N2, int y_dt2, uint64_t RS2,
+                               uint64_t W3, uint64_t Y3, int64_t N3, int y_dt3, uint64_t RS3, uint64_t stream) {
+  const int fmt = wtype_fmt(wtype);
+  if (fmt < 0)
+    return set_error(VYBDQ_ERR_ARG, "vybdq_gemv_seg3: wtype must be 2 (q4_0), 8 (Q8_0), 12 (Q4_K), 13 (Q5_K), 14 (Q6_K) or 22 (IQ2_S)");
+  Segs s{};
+  const uint64_t w[3] = {W, W2, W3}, y[3] = {Y, Y2, Y3}, rs[3] = {RS, RS2, RS3};
+  const int64_t n[3] = {N, N2, N3};
+  const int dt[3] = {y_dt, y_dt2, y_dt3};
+  for (int i = 0; i < 3; ++i) {
+    s.W[i] = reinterpret_cast<const uint8_t *>(w[i]);
+    s.Y[i] = reinterpret_cast<void *>(y[i]);
+    s.RS[i] = reinterpret_cast<const void *>(rs[i]);
+    s.ydt[i] = n[i] > 0 ? dt[i] : VYBDQ_F32;
+    s.end[i] = n[i];
+  }
   return gemv_common(fmt, VYBDQ_Q4_GGML, X, M, K, x_dt, s, stream);
 }

@@ -107,6 +107,28 @@ def gemv_q4_0_seg3(X, K, segs, order=Q4_GGML):
     call("vybdq_gemv_q4_0_seg3", _ptr(X), K, _dt(X.dtype), order, *args, _stream())
 
 
+def gemv_seg3(ty, X, K, segs):
+    """Fused GEMVs of GGUF type ty sharing X [M, K] (or [K]) in one launch (vybdq_gemv_seg3).
+    segs: up to 3 (W, Y, N) or (W, Y, N, residual) with Y preallocated [M, N] (or [N])."""
+    X2 = X.reshape(1, K) if X.dim() == 1 else X
+    M = X2.shape[0]
+    args = []
+    for i in range(3):
+        if i < len(segs) and segs[i][2] > 0:
+            W, Y, N = segs[i][:3]
+            RS = segs[i][3] if len(segs[i]) > 3 else None
+            if Y.numel() != M * N:
+                raise ValueError(f"segment {i}: Y holds {Y.numel()} elements, expected {M} x {N}")
+            if W.numel() * W.element_size() < N * row_bytes(ty, K):
+                raise ValueError(f"segment {i}: W holds fewer than N rows of {row_bytes(ty, K)} B")
+            if RS is not None and (RS.dtype != Y.dtype or RS.numel() != Y.numel()):
+                raise ValueError(f"segment {i}: residual must match Y")
+            args += [_ptr(W), _ptr(Y), N, _dt(Y.dtype), _ptr(RS)]
+        else:
+            args += [0, 0, 0, F32, 0]
+    call("vybdq_gemv_seg3", ty, _ptr(X2), M, K, _dt(X2.dtype), *args, _stream())
+
+
 def quant_q8_act(X, out=None):
     """xq8 quantizer: X [M, K] -> (Xq int8 [M, K], Xs float32 [M, K/32]); out: preallocated (Xq, Xs)."""
     X2 = X.reshape(-1, X.shape[-1])
