@@ -41,7 +41,7 @@ QWEN3_4B = dict(hidden=2560, q=4096, kv=1024, inter=9728, layers=36)
 STACK_TRAFFIC = dict(bytes_per_launch=14402381, source="profiles/q4_0_gemv_decode_stack.md (rocprofv3 --pmc)")
 
 CONFIGS = ["stack", "stack_chain", "gemv1", "kquant", "producers", "router", "exl3", "prefill", "prefill_i8",
-           "moe", "copy"]
+           "prefill_kq", "moe", "copy"]
 
 
 def parse():
@@ -51,7 +51,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="all", choices=["all"] + CONFIGS)
     ap.add_argument("--wtype", type=int, default=12, choices=[12, 13, 14, 22],
-                    help="GGML type id for --config kquant (12 Q4_K, 13 Q5_K, 14 Q6_K, 22 IQ2_S)")
+                    help="GGML type id for --config kquant / prefill_kq (12 Q4_K, 13 Q5_K, 14 Q6_K, 22 IQ2_S)")
     ap.add_argument("--tokens", type=int, default=16, help="tokens for --config moe / router")
     ap.add_argument("--batch", type=int, default=1, help="batch for --config exl3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -482,6 +482,34 @@ def run_prefill(args, torch, dev):
                 bytes_per_step=nbytes, launches_per_step=len(launches), check=check)
 
 
+def run_prefill_kq(args, torch, dev):
+    """The prefill GEMM shapes (M=512: 5120->17408 and 17408->5120, bf16 X, f32 Y) on the super-block
+    types (--wtype 12 Q4_K, 13 Q5_K, 14 Q6_K, 22 IQ2_S), 3 rotated weight copies of each."""
+    from vybforge_amd import ops
+    M, ty = 512, args.wtype
+    name = {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 22: "IQ2_S"}[ty]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 6)
+    launches, flops, nbytes = [], 0, 0
+    for N, K in PREFILL_SHAPES:
+        x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
+        y = torch.empty(M, N, device=dev)
+        for _ in range(3):
+            W = kquant_blocks_gpu(torch, gen, ty, N, K, dev)
+            launches.append(lambda W=W, x=x, y=y, N=N, K=K: ops.gemm(ty, W, x, N, K, out=y))
+            flops += 2 * M * N * K
+            nbytes += ops.row_bytes(ty, K) * N + 2 * M * K + 4 * M * N
+    ms, wall = timed_graph(torch, launches, args.steps, args.warmup)
+    tflops = flops / (ms * 1e-3) / 1e12
+    roofline = dict(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                    frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), traffic=None,
+                    kernel=f"k_kq_gemm<{name}> (units decoded to fp16 in LDS, fp16 MFMA 16x16x32)",
+                    basis="flops per step / event time", avg_launch_us=round(ms * 1e3 / len(launches), 3))
+    return dict(value=tflops, unit="TFLOP/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
+                workload=f"{name} prefill GEMMs M=512: 5120->17408 and 17408->5120 (bf16 X, f32 Y)",
+                bytes_per_step=nbytes, launches_per_step=len(launches))
+
+
 def run_prefill_i8(args, torch, dev):
     """The same two Q8_0 GEMMs with the activations quantized per 32-value block (xq8) on the device
     and int8 MFMA; the quantizer runs inside the timed step."""
@@ -691,7 +719,8 @@ def main():
         sys.exit("no GPU visible")
     dev = torch.device("cuda:0")
     runners = dict(gemv1=run_gemv1, kquant=run_kquant, producers=run_producers, router=run_router, exl3=run_exl3,
-                   prefill=run_prefill, prefill_i8=run_prefill_i8, moe=run_moe, copy=run_copy)
+                   prefill=run_prefill, prefill_i8=run_prefill_i8, prefill_kq=run_prefill_kq, moe=run_moe,
+                   copy=run_copy)
     configs = None
     try:
         if args.config in ("all", "stack", "stack_chain"):

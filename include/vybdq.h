@@ -288,12 +288,15 @@ int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t X, ui
 /* ---- prefill / grouped dequant GEMM ----------------------------------------------------- */
 
 /* Y [M, N] (row stride ldy, 0 = N) = X [M, K] W^T (+ RS) with W packed GGUF rows of type wtype
-   (2 = q4_0 GGUF order, 8 = Q8_0): weights are dequantized to fp16 (d * (q - OFF), one rounding)
-   and multiplied with fp16 MFMA, float32 accumulation; X (f32/f16/bf16) is converted to fp16
-   (|x| < 65504). K % 64 == 0. M >= 64 with K % 256 == 0 and N % 16 == 0 runs the kernel that
+   (2 = q4_0 GGUF order, 8 = Q8_0, 12 = Q4_K, 13 = Q5_K, 14 = Q6_K, 22 = IQ2_S): weights are
+   dequantized to fp16 (q4_0 / Q8_0: d * (q - OFF), one rounding; super-block types: the exact
+   value rounded to float32, then to fp16, as vybdq_dequant's F16 output) and multiplied with fp16
+   MFMA, float32 accumulation; X (f32/f16/bf16) is converted to fp16 (|x| < 65504).
+   q4_0 / Q8_0: K % 64 == 0; M >= 64 with K % 256 == 0 and N % 16 == 0 runs the kernel that
    dequantizes into the MFMA operand registers; other shapes need N % 64 == 0 and stage the
-   dequantized tile in LDS. Replaces gemm_q80 and its siblings (native/tools/gen_rpf.py:1-10,
-   p-block W@0 X@8 Y@16 S@24 N@32 K@40 LDY@48 RS@56). */
+   dequantized tile in LDS. Super-block types: K % 256 == 0, N % 64 == 0, any M.
+   Replaces gemm_q80 and its siblings picked by gemm_h(ty) (native/host/ridge_decode.vyb:295-302,
+   native/tools/gen_rpf.py:1-10,142-149, p-block W@0 X@8 Y@16 S@24 N@32 K@40 LDY@48 RS@56). */
 int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K, int x_dt,
                int y_dt, int64_t ldy, uint64_t RS, uint64_t stream);
 

@@ -150,3 +150,57 @@ def test_gemv_seg3_every_type(dev, ty, shapes, K, M, xdt):
     for (W, y, n, rs), ref in zip(segs, refs):
         if n:
             assert gate(y.to(torch.float64).cpu().numpy(), ref, y.dtype) < TOL, (n, y.dtype)
+
+
+@pytest.mark.parametrize("ty", KQ)
+@pytest.mark.parametrize("M,N,K", [(1, 64, 256), (7, 192, 768), (64, 128, 2560), (100, 64, 1024), (130, 320, 512)])
+@pytest.mark.parametrize("xdt", ["bf16", "f32", "f16"])
+def test_gemm_superblock_types(dev, ty, M, N, K, xdt):
+    """vybdq_gemm on the super-block types (the reference's gemm_h type dispatch,
+    native/host/ridge_decode.vyb:295-302): partial m-tiles, odd super-block counts per row (K = 768:
+    Q6_K / IQ2_S rows 2 bytes past a dword boundary), every activation type."""
+    rng = np.random.default_rng(M * 3 + N + K + ty)
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = synth.activations(rng, (M, K))
+    xd, x64 = x_as(x, xdt, dev)
+    y = ops.gemm(ty, to_dev(raw, dev), xd.reshape(M, K), N, K).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x64.reshape(M, K), matrix_ref(ty, raw, N, K))
+    assert matmul.rel_maxnorm(y, ref) < TOL
+
+
+@pytest.mark.parametrize("ty", KQ)
+@pytest.mark.parametrize("ydt", [torch.float16, torch.float64])
+def test_gemm_superblock_residual_ldy(dev, ty, ydt):
+    """Residual of the output type and an output row stride wider than N."""
+    M, N, K, ldy = 70, 128, 512, 200
+    rng = np.random.default_rng(ty + 11)
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = synth.activations(rng, (M, K))
+    rs = torch.from_numpy(synth.activations(rng, (M, ldy)).astype(np.float64)).to(ydt)
+    y = rs.clone().to(dev)
+    Wd, Xd = to_dev(raw, dev), to_dev(x, dev)  # held until the launch has run
+    from vybforge_amd._lib import call
+    call("vybdq_gemm", ty, Wd.data_ptr(), Xd.data_ptr(), y.data_ptr(), M, N, K,
+         ops.F32, ops._dt(ydt), ldy, y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    got = y.to(torch.float64).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x, matrix_ref(ty, raw, N, K), rs.to(torch.float64).numpy()[:, :N])
+    assert gate(got[:, :N], ref, ydt) < TOL
+    np.testing.assert_array_equal(got[:, N:], rs.to(torch.float64).numpy()[:, N:])  # columns past N untouched
+
+
+@pytest.mark.parametrize("ty", KQ)
+@pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 17408)])
+def test_gemm_superblock_prefill_shape(dev, ty, N, K):
+    """The prefill shapes M = 512 x K x N (up 5120 -> 17408, down 17408 -> 5120) with bf16 X: every
+    output computed on the device, 256 columns from the first and the last weight tiles checked
+    against the float64 oracle."""
+    M = 512
+    rng = np.random.default_rng(N + ty)
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = torch.from_numpy(synth.activations(rng, (M, K))).to(torch.bfloat16)
+    y = ops.gemm(ty, to_dev(raw, dev), x.to(dev), N, K).cpu().numpy()
+    x64 = x.to(torch.float64).numpy()
+    rb = BLOCK[ty] * (K // 256)
+    for c0 in (0, N - 256):
+        wrows = matrix_ref(ty, raw[c0 * rb:(c0 + 256) * rb], 256, K)
+        assert matmul.rel_maxnorm(y[:, c0:c0 + 256], matmul.gemm_rows_f64(x64, wrows)) < TOL, c0

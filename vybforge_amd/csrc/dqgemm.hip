@@ -37,6 +37,9 @@ int64_t mmq_workspace_size(int64_t M, int64_t N, int64_t K);
 int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
              int64_t ldy, const void *RS, void *ws, int64_t ws_bytes, hipStream_t s);
 int64_t mmq_i8_workspace_size(int64_t M, int64_t N, int64_t K);
+// the super-block (Q4_K, Q5_K, Q6_K, IQ2_S) GEMM (kqgemm.hip)
+int kq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
+            int64_t ldy, const void *RS, hipStream_t s);
 int mmq_i8_gemm(const void *W, const int8_t *Xq, const float *Xs, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
                 int64_t ldy, const void *RS, void *ws, int64_t ws_bytes, hipStream_t s);
 
@@ -417,10 +420,21 @@ using namespace vybdq;
 static int gemm_check(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K, int x_dt,
                       int y_dt, int64_t ldy) {
   VYBDQ_REQUIRE(W && X && Y, VYBDQ_ERR_ARG, "null W, X or Y");
-  VYBDQ_REQUIRE(wtype == 2 || wtype == 8, VYBDQ_ERR_ARG, "wtype must be 2 (q4_0) or 8 (Q8_0)");
+  VYBDQ_REQUIRE(wtype == 2 || wtype == 8 || wtype == 12 || wtype == 13 || wtype == 14 || wtype == 22, VYBDQ_ERR_ARG,
+                "wtype must be 2 (q4_0), 8 (Q8_0), 12 (Q4_K), 13 (Q5_K), 14 (Q6_K) or 22 (IQ2_S)");
   VYBDQ_REQUIRE(dt_valid_in(x_dt), VYBDQ_ERR_ARG, "x_dt must be F32, F16 or BF16");
   VYBDQ_REQUIRE(dt_valid_out(y_dt), VYBDQ_ERR_ARG, "y_dt must be F32, F16, BF16 or F64");
   VYBDQ_REQUIRE(M >= 1 && M < (1 << 24), VYBDQ_ERR_SHAPE, "M out of range");
+  if (wtype >= 12) {  // super-block types: K % 256 == 0, tiles of 64 weight rows
+    VYBDQ_REQUIRE(K >= 256 && K % 256 == 0 && K < (1 << 24), VYBDQ_ERR_SHAPE,
+                  "super-block types need K a positive multiple of 256");
+    VYBDQ_REQUIRE(N >= 64 && N % 64 == 0 && N < (1 << 24), VYBDQ_ERR_SHAPE,
+                  "super-block types need N a positive multiple of 64");
+    VYBDQ_REQUIRE(M * K < (int64_t(1) << 40), VYBDQ_ERR_SHAPE, "M * K too large");
+    VYBDQ_REQUIRE(ldy == 0 || ldy >= N, VYBDQ_ERR_SHAPE, "ldy must be 0 (= N) or >= N");
+    VYBDQ_REQUIRE((W & 3) == 0 && (X & 15) == 0, VYBDQ_ERR_ALIGN, "W must be 4-byte and X 16-byte aligned");
+    return VYBDQ_OK;
+  }
   VYBDQ_REQUIRE(K >= 64 && K % 64 == 0, VYBDQ_ERR_SHAPE, "K must be a positive multiple of 64");
   VYBDQ_REQUIRE(N >= 16 && N % 16 == 0 && N < (1 << 24), VYBDQ_ERR_SHAPE, "N must be a positive multiple of 16");
   VYBDQ_REQUIRE(N % 64 == 0 || (M >= 64 && mmq_supported(M, N, K)), VYBDQ_ERR_SHAPE,
@@ -442,7 +456,7 @@ extern "C" int vybdq_gemm_ws(int wtype, uint64_t W, uint64_t X, uint64_t Y, int6
   if (rc) return rc;
   VYBDQ_REQUIRE(ws == 0 || (ws & 255) == 0, VYBDQ_ERR_ALIGN, "workspace must be 256-byte aligned");
   VYBDQ_REQUIRE(ws_bytes >= 0, VYBDQ_ERR_WORKSPACE, "negative workspace size");
-  if (M >= 64 && mmq_supported(M, N, K))
+  if (wtype <= 8 && M >= 64 && mmq_supported(M, N, K))
     return mmq_gemm(wtype, reinterpret_cast<const void *>(W), reinterpret_cast<const void *>(X), x_dt,
                     reinterpret_cast<void *>(Y), y_dt, M, N, K, ldy ? ldy : N, reinterpret_cast<const void *>(RS),
                     ws ? reinterpret_cast<void *>(ws) : nullptr, ws ? ws_bytes : 0, as_stream(stream));
@@ -467,6 +481,7 @@ extern "C" int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t
   a.RS = reinterpret_cast<const void *>(RS);
   a.G = 1;
   hipStream_t s = as_stream(stream);
+  if (wtype >= 12) return kq_gemm(wtype, a.W, a.X, x_dt, a.Y, y_dt, M, N, K, a.ldy, a.RS, s);
   if (M >= 64 && mmq_supported(M, N, K))
     return mmq_gemm(wtype, a.W, a.X, x_dt, a.Y, y_dt, M, N, K, a.ldy, a.RS, nullptr, 0, s);
   if (N % 128 != 0 || M < 64) {
