@@ -41,7 +41,7 @@ QWEN3_4B = dict(hidden=2560, q=4096, kv=1024, inter=9728, layers=36)
 STACK_TRAFFIC = dict(bytes_per_launch=14402381, source="profiles/q4_0_gemv_decode_stack.md (rocprofv3 --pmc)")
 
 CONFIGS = ["stack", "stack_chain", "gemv1", "kquant", "producers", "router", "exl3", "prefill", "prefill_i8",
-           "prefill_kq", "moe", "copy"]
+           "prefill_kq", "moe", "pblock", "copy"]
 
 
 def parse():
@@ -651,6 +651,62 @@ def run_moe(args, torch, dev, tokens=None, built=None):
                 bytes_per_step=nbytes, launches_per_step=R, check=check)
 
 
+def run_pblock(args, torch, dev):
+    """vybdq_launch_pblock on the reference's parameter blocks beside the direct entry points, at the
+    q4_0 GEMV 9728x2560 (f32 x, 24 rotated weight copies) and the Q8_0 prefill GEMMs M=512 (f32 X,
+    3 rotated copies of each shape, no workspace)."""
+    import numpy as np
+    from vybforge_amd import _lib, ops, synth
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 7)
+    stream = lambda: torch.cuda.current_stream().cuda_stream
+    out = {}
+    N, K = 9728, 2560
+    copies = [synth.q4_0_weights_torch(gen, N, K, dev) for _ in range(24)]
+    x = torch.randn(K, generator=gen, device=dev)
+    y = torch.empty(1, N, device=dev)
+    pbs = []
+    for W in copies:
+        w = np.zeros(32, np.int64)
+        w[0:7] = [W.data_ptr(), x.data_ptr(), y.data_ptr(), 1, N, K, 4]
+        w[10], w[14] = 8, 8
+        pbs.append(torch.from_numpy(w).to(dev))
+    ms_d, _ = timed_graph(torch, [lambda W=W: ops.gemv(ops.GGML_Q4_0, W, x, N, K, out=y) for W in copies],
+                          args.steps, args.warmup)
+    ms_p, _ = timed_graph(torch, [lambda pb=pb: _lib.call("vybdq_launch_pblock", _lib.PB_GEMV + 2, pb.data_ptr(),
+                                                             stream()) for pb in pbs], args.steps, args.warmup)
+    b = N * K // 32 * 18 + 4 * K + 4 * N
+    out["gemv_q4_0_9728x2560"] = dict(direct_us=round(ms_d * 1e3 / 24, 3), pblock_us=round(ms_p * 1e3 / 24, 3),
+                                      direct_GBs=round(b / (ms_d / 24 * 1e-3) / 1e9, 1),
+                                      pblock_GBs=round(b / (ms_p / 24 * 1e-3) / 1e9, 1))
+    del copies, pbs
+    M = 512
+    direct, pblk, flops = [], [], 0
+    keep = []
+    for Nn, Kk in PREFILL_SHAPES:
+        X = torch.randn(M, Kk, generator=gen, device=dev)
+        Y = torch.empty(M, Nn, device=dev)
+        for _ in range(3):
+            W = synth.q8_0_weights_torch(gen, Nn, Kk, dev)
+            direct.append(lambda W=W, X=X, Y=Y, Nn=Nn, Kk=Kk: ops.gemm(ops.GGML_Q8_0, W, X, Nn, Kk, out=Y))
+            w = np.zeros(32, np.int64)
+            w[0:10] = [W.data_ptr(), X.data_ptr(), Y.data_ptr(), M, Nn, Kk, -Nn, 0, 0, (M + 63) // 64]
+            pb = torch.from_numpy(w).to(dev)
+            pblk.append(lambda pb=pb: _lib.call("vybdq_launch_pblock", _lib.PB_GEMM + 8, pb.data_ptr(), stream()))
+            keep += [W, X, Y, pb]
+            flops += 2 * M * Nn * Kk
+    ms_d, _ = timed_graph(torch, direct, args.steps, args.warmup)
+    ms_p, _ = timed_graph(torch, pblk, args.steps, args.warmup)
+    out["gemm_q8_0_prefill_m512_f32x"] = dict(direct_tflops=round(flops / (ms_d * 1e-3) / 1e12, 1),
+                                              pblock_tflops=round(flops / (ms_p * 1e-3) / 1e12, 1))
+    if _lib.lib.vybdq_pblock_status() != 0:
+        raise CheckFailed("a p-block launch reported: " + _lib.last_error())
+    ratio = out["gemv_q4_0_9728x2560"]["direct_us"] / out["gemv_q4_0_9728x2560"]["pblock_us"]
+    return dict(value=ratio, unit="x", ms_step=ms_p, wall=0.0, flops=flops, roofline=out,
+                workload="vybdq_launch_pblock vs the direct entry points (GEMV 9728x2560 q4_0, Q8_0 prefill M=512)",
+                bytes_per_step=0, launches_per_step=len(pblk))
+
+
 def run_copy(args, torch, dev):
     """Calibration leg for the HBM traffic counters: a plain device copy of known size, 256 MiB
     read + 256 MiB written per step. rocprofv3 FETCH_SIZE / WRITE_SIZE of this run, divided by
@@ -720,7 +776,7 @@ def main():
     dev = torch.device("cuda:0")
     runners = dict(gemv1=run_gemv1, kquant=run_kquant, producers=run_producers, router=run_router, exl3=run_exl3,
                    prefill=run_prefill, prefill_i8=run_prefill_i8, prefill_kq=run_prefill_kq, moe=run_moe,
-                   copy=run_copy)
+                   pblock=run_pblock, copy=run_copy)
     configs = None
     try:
         if args.config in ("all", "stack", "stack_chain"):

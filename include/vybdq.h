@@ -330,6 +330,36 @@ int64_t vybdq_gemm_q8_0_i8_workspace_size(int64_t M, int64_t N, int64_t K);
 int vybdq_gemm_q8_0_i8(uint64_t W, uint64_t Xq, uint64_t Xs, uint64_t Y, int64_t M, int64_t N, int64_t K, int y_dt,
                        int64_t ldy, uint64_t RS, uint64_t ws, int64_t ws_bytes, uint64_t stream);
 
+/* ---- the reference's own parameter blocks ------------------------------------------------ */
+
+/* kind of a parameter block: one of these plus the GGML type id of W (2, 8, 12, 13, 14, 22) */
+#define VYBDQ_PB_GEMV 0x100    /* set_gemv layout (the packed GEMV kernels) */
+#define VYBDQ_PB_GEMM 0x200    /* set_gemm layout, X float32 (the gen_rpf prefill tiles) */
+#define VYBDQ_PB_GEMM_XH 0x300 /* set_gemm layout, X fp16 (the gen_rpf --xh tiles) */
+
+/* Launch one GEMV or prefill GEMM described by a reference parameter block at device address P
+   (8-byte aligned): little-endian int64 words, each read by the kernel when the launch runs (the
+   reference rewrites block words with asynchronous copies inside its captured decode graph,
+   native/host/ridge_decode.vyb:168-180), so the host reads nothing and the call can be captured.
+   Replaces lk(h, gx, bx, p) (ridge_decode.vyb:204-227) with h picked by gemv_h / gemm_h (:295-311).
+   VYBDQ_PB_GEMV + ty, set_gemv (ridge_decode.vyb:264-270): W@0 X@8 Y@16 M@24 N@32 K@40 YE@48
+     W2@56 NS2@64 Y2@72 YE2@80 W3@88 NS3@96 Y3@104 YE3@112 RS@120 (GRID@128 unused): up to three
+     row segments sharing x f32 [K]; M must be 1; YE = 4: f32 output, otherwise f64 output plus the
+     f64 residual RS (segment 1); K % 64 == 0 (super-block types K % 256 == 0), K <= 20480;
+     W 4-byte and X 16-byte aligned.
+   VYBDQ_PB_GEMM / VYBDQ_PB_GEMM_XH + ty, set_gemm (ridge_decode.vyb:272-275, native/tools/gen_rpf.py:2-8):
+     W@0 X@8 Y@16 S@24 N@32 K@40 LDY@48 RS@56 (G@64, NMT@72 unused): Y[s, n] = RS[s, n] +
+     sum_k X[s, k] W[n, k] for s < S; LDY >= N: Y float64 of row stride LDY, RS float64 or 0;
+     LDY <= -N: Y float32 of row stride -LDY, RS ignored; K % 256 == 0; N % 16 == 0 (q4_0 / Q8_0) or
+     N % 64 == 0 (super-block types); no K split (the block has no workspace word).
+   A block whose words violate these is not computed (nothing is written) and the next
+   vybdq_pblock_status() on the device reports it; the call itself only checks kind and P. */
+int vybdq_launch_pblock(int kind, uint64_t P, uint64_t stream);
+
+/* Synchronises the current device, then returns 0 or the error of an invalid parameter block
+   launched on it since the previous call (and clears it). */
+int vybdq_pblock_status(void);
+
 /* ---- MoE layer ---------------------------------------------------------------------------- */
 
 /* Router alone: idx_out int32 [T, topk] (descending choice, ties to the lower id),

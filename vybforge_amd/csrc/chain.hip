@@ -1,4 +1,4 @@
-// Persistent chain of dependent q4_0 / Q8_0 GEMV stages in one launch, gfx950.
+// Persistent chain of dependent GEMV stages (any GGUF type of the pair GEMV) in one launch, gfx950.
 //
 // A decode step is a sequence of GEMVs where stage s may consume stage s-1's output. As
 // separate launches each stage pays the dependent-launch floor (~1.7 us per graph node) plus
@@ -25,10 +25,17 @@
 // the counters, leaving the workspace zero-filled for the next call.
 #include "gemv_dev.h"
 
+#include <atomic>
+
 namespace vybdq {
 
 constexpr int kChainThreads = 256;
 constexpr uint32_t kSpinLimit = 1u << 22;  // ~0.5 s of s_sleep polling before giving up
+
+// units (64 weights) per lane per load batch
+template <int FMT> constexpr int chain_batch() {
+  return FMT == FMT_Q4_0 ? 4 : (FMT == FMT_Q4_K || FMT == FMT_IQ2_S) ? 4 : 2;
+}
 
 struct StageDesc {
   const uint8_t *W[3];
@@ -49,7 +56,8 @@ __device__ __forceinline__ int ye_to_dt(int64_t ye) {
   return VYBDQ_F64;
 }
 
-__device__ __forceinline__ StageDesc read_stage(const int64_t *pb) {
+// ref_layout: the reference's 136-byte block (x is f32, q4_0 in GGUF order; no XE / ORDER words)
+__device__ __forceinline__ StageDesc read_stage(const int64_t *pb, bool ref_layout) {
   StageDesc d;
   d.W[0] = reinterpret_cast<const uint8_t *>(pb[0]);
   d.X = reinterpret_cast<const void *>(pb[1]);
@@ -66,8 +74,15 @@ __device__ __forceinline__ StageDesc read_stage(const int64_t *pb) {
   d.Y[2] = reinterpret_cast<void *>(pb[13]);
   d.ydt[2] = ye_to_dt(pb[14]);
   d.RS = reinterpret_cast<const void *>(pb[15]);
-  d.xdt = pb[17] == 2 ? VYBDQ_F16 : pb[17] == 258 ? VYBDQ_BF16 : VYBDQ_F32;
-  d.order = static_cast<int>(pb[18]);
+  if (ref_layout) {
+    d.xdt = VYBDQ_F32;
+    d.order = VYBDQ_Q4_GGML;
+  } else {
+    d.xdt = pb[17] == 2 ? VYBDQ_F16 : pb[17] == 258 ? VYBDQ_BF16 : VYBDQ_F32;
+    d.order = static_cast<int>(pb[18]);
+  }
+  // the reference adds RS only in its f64 output mode (native/kernels/rgemv.vyb:13-15)
+  if (ref_layout && d.ydt[0] != VYBDQ_F64) d.RS = nullptr;
   d.end[0] = n1;
   d.end[1] = n1 + n2;
   d.end[2] = n1 + n2 + n3;
@@ -86,27 +101,36 @@ __device__ __forceinline__ int chain_pick_g(int64_t rows, int P, int nwaves) {
   return best;
 }
 
-template <int FMT>
-__global__ void __launch_bounds__(kChainThreads) k_gemv_chain(const int64_t *__restrict__ pblocks, int nstages,
+template <int FMT, int NT = kChainThreads>
+__global__ void __launch_bounds__(NT) k_gemv_chain(const int64_t *__restrict__ pblocks, int nstages,
                                                               int64_t pstride_words, int64_t maxK,
-                                                              uint32_t *__restrict__ ws) {
+                                                              uint32_t *__restrict__ ws, int ref_layout) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  constexpr int U = Fmt<FMT>::U;
+  constexpr int U = chain_batch<FMT>();
   constexpr int PD = Fmt<FMT>::PAIR_DWORDS;
+  constexpr int KALIGN = is_kquant<FMT>() ? 256 : 64;
   uint32_t *err = ws;
   uint32_t *cnt = ws + 1;
   const int maxP = static_cast<int>(maxK >> 6);
   char *lds = smem;
   float *sx = reinterpret_cast<float *>(smem + static_cast<size_t>(maxP) * XPAIR_STRIDE);
   const int nwg = gridDim.x;
-  const int nwaves = nwg * (kChainThreads / 64);
-  const int gw = blockIdx.x * (kChainThreads / 64) + (threadIdx.x >> 6);
+  const int nwaves = nwg * (NT / 64);
+  const int gw = blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-
   for (int s = 0; s < nstages; ++s) {
-    const StageDesc st = read_stage(pblocks + s * pstride_words);
+    const StageDesc st = read_stage(pblocks + s * pstride_words, ref_layout != 0);
     const int P = static_cast<int>(st.K >> 6);
-    const bool valid = st.K > 0 && st.K % 64 == 0 && st.K <= maxK && st.end[2] > 0 && pblocks[s * pstride_words + 3] == 1;
+    // every word that addresses memory is checked before use: null or misaligned pointers, negative
+    // segment sizes, M != 1 or a K the LDS stage does not hold leave the stage uncomputed (error bit)
+    bool segs_ok = st.end[0] >= 0 && st.end[1] >= st.end[0] && st.end[2] >= st.end[1];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const bool used = st.end[i] > (i == 0 ? 0 : st.end[i - 1]);
+      segs_ok = segs_ok && (!used || (st.W[i] && st.Y[i] && (reinterpret_cast<uintptr_t>(st.W[i]) & 3) == 0));
+    }
+    const bool valid = segs_ok && st.K > 0 && st.K % KALIGN == 0 && st.K <= maxK && st.end[2] > 0 &&
+                       st.X && (reinterpret_cast<uintptr_t>(st.X) & 15) == 0 && pblocks[s * pstride_words + 3] == 1;
     const int64_t rows = valid ? st.end[2] : 0;
     const int G = valid ? chain_pick_g(rows, P, nwaves) : 64;
     const int rpt = 64 / G;  // rows per wave tile
@@ -122,12 +146,11 @@ __global__ void __launch_bounds__(kChainThreads) k_gemv_chain(const int64_t *__r
       if (row >= st.end[0]) sg = (row >= st.end[1]) ? 2 : 1;
       if (!act) sg = 0;
       lrow = act ? row - (sg == 0 ? 0 : (sg == 1 ? st.end[0] : st.end[1])) : 0;
-      wrow = pick3_ptr(st.W, sg) + lrow * (static_cast<int64_t>(P) * Fmt<FMT>::PAIR_BYTES);
+      wrow = pick3_ptr(st.W, sg) + lrow * unit_row_bytes<FMT>(P);
     };
-    auto pair_ptr = [&](const uint8_t *wrow, int i) {
-      int p = ks + G * i;
-      p = p < P ? p : (ks < P ? ks : 0);
-      return wrow + static_cast<int64_t>(p) * Fmt<FMT>::PAIR_BYTES;
+    auto pair_idx = [&](int i) {
+      const int p = ks + G * i;
+      return p < P ? p : (ks < P ? ks : 0);
     };
 
     // 1. prefetch the first batch of this wave's first tile (independent of stage s-1)
@@ -138,7 +161,7 @@ __global__ void __launch_bounds__(kChainThreads) k_gemv_chain(const int64_t *__r
       tile_row(t < tiles ? t : 0, sg, lrow, wrow, act);
       if (valid) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) load_pair<FMT>(pair_ptr(wrow, u), dw[u]);
+        for (int u = 0; u < U; ++u) load_unit<FMT>(wrow, pair_idx(u), dw[u]);
       }
     }
 
@@ -163,10 +186,29 @@ __global__ void __launch_bounds__(kChainThreads) k_gemv_chain(const int64_t *__r
       __syncthreads();
     }
 
-    // 3. stage x_s into LDS (it may be stage s-1's output)
+    // 3. stage x_s into LDS (it may be stage s-1's output); IQ2_S: then its grid tables behind the
+    // block sums, where the unit dot of this stage's P reads them
     if (valid) {
+      if constexpr (FMT == FMT_IQ2_S) {
+        u4 *gridh = iq2s_lds_grid(sx, 1, P);
+        for (int i = threadIdx.x; i < 1024 + 256; i += NT) {
+          uint32_t q[4];
+          if (i < 1024) {
+            const unsigned long long e = kIq2sGrid[i];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+              q[k] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(static_cast<float>((e >> (16 * k)) & 0xff)),
+                                                     static_cast<_Float16>(static_cast<float>((e >> (16 * k + 8)) & 0xff))});
+          } else {
+            const uint32_t sb = static_cast<uint32_t>(i - 1024);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) q[k] = (((sb >> (2 * k)) & 1u) << 15) | (((sb >> (2 * k + 1)) & 1u) << 31);
+          }
+          gridh[i] = u4{q[0], q[1], q[2], q[3]};
+        }
+      }
       const int nchunk = 8 * P;
-      for (int c = threadIdx.x; c < nchunk; c += kChainThreads) {
+      for (int c = threadIdx.x; c < nchunk; c += NT) {
         if (st.xdt == VYBDQ_F32) {
           uint32_t r[8];
           load_x_chunk<8>(st.X, 8 * static_cast<int64_t>(c), r);
@@ -190,16 +232,16 @@ __global__ void __launch_bounds__(kChainThreads) k_gemv_chain(const int64_t *__r
         for (int i0 = 0; i0 < npl; i0 += U) {
           if (!first || i0 > 0) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) load_pair<FMT>(pair_ptr(wrow, i0 + u), dw[u]);
+            for (int u = 0; u < U; ++u) load_unit<FMT>(wrow, pair_idx(i0 + u), dw[u]);
           }
           if (act) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
               if (i0 + u < npl) {
-                if (FMT == FMT_Q8_0 || st.order == VYBDQ_Q4_GGML)
-                  pair_dot<FMT, VYBDQ_Q4_GGML, 1>(dw[u], lds, sx, P, ks + G * (i0 + u), acc);
+                if (FMT != FMT_Q4_0 || st.order == VYBDQ_Q4_GGML)
+                  unit_dot<FMT, VYBDQ_Q4_GGML, 1>(dw[u], lds, sx, P, ks + G * (i0 + u), acc);
                 else
-                  pair_dot<FMT, VYBDQ_Q4_INTERLEAVED, 1>(dw[u], lds, sx, P, ks + G * (i0 + u), acc);
+                  unit_dot<FMT, VYBDQ_Q4_INTERLEAVED, 1>(dw[u], lds, sx, P, ks + G * (i0 + u), acc);
               }
             }
           }
@@ -225,6 +267,8 @@ __global__ void __launch_bounds__(kChainThreads) k_gemv_chain(const int64_t *__r
     // agent-scope release (an L2 writeback, then the increment) makes them visible chip-wide.
     // A fence per thread would write back the whole L2 256 times per workgroup per stage.
     // __syncthreads() does not wait for outstanding global stores, so wait for them first.
+    // A single stage has no waiter: the end of the kernel publishes its stores.
+    if (nstages == 1) break;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -238,32 +282,66 @@ __global__ void __launch_bounds__(kChainThreads) k_gemv_chain(const int64_t *__r
   }
 }
 
-template <int FMT>
-static int chain_launch(uint64_t P, int nstages, int64_t pstride, int64_t maxK, uint64_t ws, hipStream_t s) {
+template <int FMT, int NT>
+static int chain_launch_nt(uint64_t P, int nstages, int64_t pstride, int64_t maxK, uint64_t ws, int ref_layout,
+                        int max_per_cu, hipStream_t s) {
   const int maxP = static_cast<int>(maxK / 64);
-  const size_t lds = static_cast<size_t>(maxP) * (XPAIR_STRIDE + 2 * 4);
+  const size_t lds = static_cast<size_t>(maxP) * (XPAIR_STRIDE + 2 * 4) + (FMT == FMT_IQ2_S ? kIq2sLdsBytes : 0);
   if (lds > 160 * 1024) return set_error(VYBDQ_ERR_SHAPE, "gemv chain: max_K too large for the LDS x stage");
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("gemv chain: hipGetDevice: ") + hipGetErrorString(e));
-  int cus = 0;
-  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("gemv chain: CU count: ") + hipGetErrorString(e));
-  const void *fn = reinterpret_cast<const void *>(&k_gemv_chain<FMT>);
-  if (lds > 64 * 1024) {
-    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("gemv chain: LDS attribute: ") + hipGetErrorString(e));
-  }
+  if (dev < 0 || dev >= 64) return set_error(VYBDQ_ERR_HIP, "gemv chain: device index out of range");
+  const int cus = device_cu_count();
+  const void *fn = reinterpret_cast<const void *>(&k_gemv_chain<FMT, NT>);
+  // resident workgroups per CU for this LDS size: queried once per device and size (the LDS
+  // attribute and the occupancy query stay out of later launches, which may be under capture)
+  static std::atomic<int64_t> occ[64];  // (lds << 8) | workgroups per CU, 0 = not queried
+  const int64_t key = static_cast<int64_t>(lds) << 8;
   int per_cu = 0;
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kChainThreads, lds);
-  if (e != hipSuccess || per_cu < 1)
-    return set_error(VYBDQ_ERR_HIP, "gemv chain: kernel cannot be resident (occupancy query failed)");
-  // two workgroups per CU keep the waits short while every workgroup stays resident
-  const int grid = cus * (per_cu < 2 ? per_cu : 2);
-  hipLaunchKernelGGL((k_gemv_chain<FMT>), dim3(grid), dim3(kChainThreads), lds, s,
+  const int64_t have = occ[dev].load(std::memory_order_relaxed);
+  if ((have & ~int64_t(0xff)) == key && (have & 0xff) > 0) {
+    per_cu = static_cast<int>(have & 0xff);
+  } else {
+    if (lds > 64 * 1024) {
+      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+      if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("gemv chain: LDS attribute: ") + hipGetErrorString(e));
+    }
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NT, lds);
+    if (e != hipSuccess || per_cu < 1 || per_cu > 255)
+      return set_error(VYBDQ_ERR_HIP, "gemv chain: kernel cannot be resident (occupancy query failed)");
+    occ[dev].store(key | per_cu, std::memory_order_relaxed);
+  }
+  // a chain: two workgroups per CU keep the waits short while every workgroup stays resident; one
+  // stage (no waits): as many as fit
+  const int grid = cus * (per_cu < max_per_cu ? per_cu : max_per_cu);
+  hipLaunchKernelGGL((k_gemv_chain<FMT, NT>), dim3(grid), dim3(NT), lds, s,
                      reinterpret_cast<const int64_t *>(P), nstages, pstride / 8, maxK,
-                     reinterpret_cast<uint32_t *>(ws));
+                     reinterpret_cast<uint32_t *>(ws), ref_layout);
   return check_launch("gemv chain");
+}
+
+// 256-thread workgroups: a chain runs two per CU (short waits), a single stage (no waits, the GEMV
+// kind of vybdq_launch_pblock) as many as fit, so that a wave's rows are covered in one round
+// (512-thread workgroups hold fewer waves per CU at these register counts: measured slower).
+template <int FMT>
+static int chain_launch(uint64_t P, int nstages, int64_t pstride, int64_t maxK, uint64_t ws, int ref_layout,
+                        int max_per_cu, hipStream_t s) {
+  return chain_launch_nt<FMT, kChainThreads>(P, nstages, pstride, maxK, ws, ref_layout, max_per_cu, s);
+}
+
+// GGML type id -> the chain launch of that format (also the GEMV kind of vybdq_launch_pblock:
+// one stage in the reference's own block layout, pblock.hip)
+int chain_dispatch(int wtype, uint64_t P, int nstages, int64_t pstride, int64_t maxK, uint64_t ws, int ref_layout,
+                   int max_per_cu, hipStream_t s) {
+  switch (wtype) {
+    case 2: return chain_launch<FMT_Q4_0>(P, nstages, pstride, maxK, ws, ref_layout, max_per_cu, s);
+    case 8: return chain_launch<FMT_Q8_0>(P, nstages, pstride, maxK, ws, ref_layout, max_per_cu, s);
+    case 12: return chain_launch<FMT_Q4_K>(P, nstages, pstride, maxK, ws, ref_layout, max_per_cu, s);
+    case 13: return chain_launch<FMT_Q5_K>(P, nstages, pstride, maxK, ws, ref_layout, max_per_cu, s);
+    case 14: return chain_launch<FMT_Q6_K>(P, nstages, pstride, maxK, ws, ref_layout, max_per_cu, s);
+    default: return chain_launch<FMT_IQ2_S>(P, nstages, pstride, maxK, ws, ref_layout, max_per_cu, s);
+  }
 }
 
 }  // namespace vybdq
@@ -278,14 +356,14 @@ extern "C" int64_t vybdq_chain_workspace_size(int nstages) {
 extern "C" int vybdq_gemv_chain(int wtype, uint64_t P, int nstages, int64_t pstride, int64_t max_K, uint64_t ws,
                                 uint64_t stream) {
   VYBDQ_REQUIRE(P && ws, VYBDQ_ERR_ARG, "null P or workspace");
-  VYBDQ_REQUIRE(wtype == 2 || wtype == 8, VYBDQ_ERR_ARG, "wtype must be 2 (q4_0) or 8 (Q8_0)");
+  VYBDQ_REQUIRE(wtype == 2 || wtype == 8 || wtype == 12 || wtype == 13 || wtype == 14 || wtype == 22, VYBDQ_ERR_ARG,
+                "wtype must be 2 (q4_0), 8 (Q8_0), 12 (Q4_K), 13 (Q5_K), 14 (Q6_K) or 22 (IQ2_S)");
   VYBDQ_REQUIRE(nstages >= 1 && nstages <= (1 << 20), VYBDQ_ERR_SHAPE, "nstages out of range");
   VYBDQ_REQUIRE(pstride >= 152 && pstride % 8 == 0, VYBDQ_ERR_SHAPE, "pstride must be >= 152 and a multiple of 8");
   VYBDQ_REQUIRE(max_K >= 64 && max_K % 64 == 0, VYBDQ_ERR_SHAPE, "max_K must be a positive multiple of 64");
   VYBDQ_REQUIRE((P & 7) == 0 && (ws & 3) == 0, VYBDQ_ERR_ALIGN, "P must be 8-byte and ws 4-byte aligned");
-  hipStream_t s = as_stream(stream);
-  if (wtype == 2) return chain_launch<FMT_Q4_0>(P, nstages, pstride, max_K, ws, s);
-  return chain_launch<FMT_Q8_0>(P, nstages, pstride, max_K, ws, s);
+  VYBDQ_REQUIRE(wtype <= 8 || max_K % 256 == 0, VYBDQ_ERR_SHAPE, "super-block types need max_K % 256 == 0");
+  return chain_dispatch(wtype, P, nstages, pstride, max_K, ws, 0, 2, as_stream(stream));
 }
 
 extern "C" int vybdq_chain_status(uint64_t ws) {

@@ -132,7 +132,6 @@ __device__ __forceinline__ void kq_unit_to_lds(const uint32_t (&dw)[Fmt<FMT>::PA
       uint32_t out[16];
 #pragma unroll
       for (int l2 = 0; l2 < 4; ++l2) {
-        const int l = 4 * hb + l2;
         const uint32_t idx = __builtin_amdgcn_ubfe(ix[hb], 8 * l2, 8) | (__builtin_amdgcn_ubfe(dw[6], 8 * hb + 2 * l2, 2) << 8);
         const unsigned long long e = kIq2sGrid[idx];
         const uint32_t sgn = __builtin_amdgcn_ubfe(sg[hb], 8 * l2, 8);
@@ -143,7 +142,6 @@ __device__ __forceinline__ void kq_unit_to_lds(const uint32_t (&dw)[Fmt<FMT>::PA
           const float v = dl * static_cast<float>(static_cast<uint32_t>(e >> (8 * j)) & 0xffu);
           w[j] = ((sgn >> j) & 1u) ? -v : v;
         }
-        (void)l;
 #pragma unroll
         for (int j = 0; j < 4; ++j) out[4 * l2 + j] = pack_h2(w[2 * j], w[2 * j + 1]);
       }
@@ -189,13 +187,11 @@ __device__ __forceinline__ u4 kq_x_f16(const KqX<XDT> &c) {
   return o;
 }
 
+// One output tile (m-tile mt, n-tile nt); every thread of the workgroup calls it.
 template <int FMT, int XDT>
-__global__ void __launch_bounds__(256, 2) k_kq_gemm(KqArgs a) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[kKqBM * kKqLda];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[kKqBN * kKqLda];
+__device__ __forceinline__ void kq_tile(const KqArgs &a, int mt, int nt, _Float16 *As, _Float16 *Bs) {
   constexpr int PD = Fmt<FMT>::PAIR_DWORDS;
   constexpr int XC = kKqBM * kKqBK / 8 / 256;  // X chunks of 8 per thread per step
-  const int mt = blockIdx.x % a.m_tiles, nt = blockIdx.x / a.m_tiles;
   const int row0 = mt * kKqBM;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
@@ -275,11 +271,71 @@ __global__ void __launch_bounds__(256, 2) k_kq_gemm(KqArgs a) {
     }
 }
 
+template <int FMT, int XDT>
+__global__ void __launch_bounds__(256, 2) k_kq_gemm(KqArgs a) {
+  __shared__ __attribute__((aligned(16))) _Float16 As[kKqBM * kKqLda];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[kKqBN * kKqLda];
+  kq_tile<FMT, XDT>(a, blockIdx.x % a.m_tiles, blockIdx.x / a.m_tiles, As, Bs);
+}
+
+// The reference's set_gemm block (W@0 X@8 Y@16 S@24 N@32 K@40 LDY@48 RS@56; LDY >= 0: Y f64 of
+// row stride LDY with the f64 residual RS, LDY < 0: Y f32 of row stride -LDY), every word read here
+// when the launch runs; a persistent grid walks the tiles. Invalid words: nothing is written and
+// bit 4 of *status is set.
+template <int FMT, int XDT>
+__global__ void __launch_bounds__(256, 2) k_kq_gemm_pb(const int64_t *__restrict__ pb, uint32_t *__restrict__ status) {
+  __shared__ __attribute__((aligned(16))) _Float16 As[kKqBM * kKqLda];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[kKqBN * kKqLda];
+  const int64_t W = pb[0], X = pb[1], Y = pb[2], M = pb[3], N = pb[4], K = pb[5], LDY = pb[6], RS = pb[7];
+  const int64_t ldy = LDY < 0 ? -LDY : LDY;
+  const bool ok = W && X && Y && M >= 1 && M < (1 << 24) && N >= 64 && N % 64 == 0 && N < (1 << 24) && K >= 256 &&
+                  K % 256 == 0 && K < (1 << 24) && ldy >= N && (W & 3) == 0 && (X & 15) == 0;
+  if (!ok) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) __hip_atomic_fetch_or(status, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  KqArgs a{};
+  a.W = reinterpret_cast<const uint8_t *>(W);
+  a.S = static_cast<int>(K / 256);
+  a.rowbytes = static_cast<int64_t>(a.S) * KqSb<FMT>::BYTES;
+  a.X = reinterpret_cast<const void *>(X);
+  a.M = static_cast<int>(M);
+  a.N = static_cast<int>(N);
+  a.m_tiles = static_cast<int>((M + kKqBM - 1) / kKqBM);
+  a.Y = reinterpret_cast<void *>(Y);
+  a.ydt = LDY < 0 ? VYBDQ_F32 : VYBDQ_F64;
+  a.ldy = ldy;
+  a.RS = LDY < 0 ? nullptr : reinterpret_cast<const void *>(RS);
+  const int units = a.m_tiles * (a.N / kKqBN);
+  for (int u = blockIdx.x; u < units; u += gridDim.x) {
+    kq_tile<FMT, XDT>(a, u % a.m_tiles, u / a.m_tiles, As, Bs);
+    __builtin_amdgcn_s_barrier();  // the next tile's first LDS stores wait for this tile's last reads
+  }
+}
+
 template <int FMT>
 static int kq_launch(KqArgs &a, int xdt, hipStream_t s) {
   const unsigned grid = static_cast<unsigned>(a.m_tiles) * static_cast<unsigned>(a.N / kKqBN);
   VYBDQ_DISPATCH_IN(xdt, XDT, hipLaunchKernelGGL((k_kq_gemm<FMT, XDT>), dim3(grid), dim3(256), 0, s, a));
   return check_launch("super-block gemm");
+}
+
+template <int FMT>
+static int kq_pb_launch(int xdt, const int64_t *pb, uint32_t *status, hipStream_t s) {
+  const unsigned grid = static_cast<unsigned>(2 * device_cu_count());
+  if (xdt == VYBDQ_F16) hipLaunchKernelGGL((k_kq_gemm_pb<FMT, VYBDQ_F16>), dim3(grid), dim3(256), 0, s, pb, status);
+  else hipLaunchKernelGGL((k_kq_gemm_pb<FMT, VYBDQ_F32>), dim3(grid), dim3(256), 0, s, pb, status);
+  return check_launch("p-block super-block gemm");
+}
+
+// The GEMM kind of vybdq_launch_pblock for wtype 12, 13, 14, 22 (pblock.hip); xdt F32 or F16.
+int kq_gemm_pblock(int wtype, int xdt, const int64_t *pb, uint32_t *status, hipStream_t s) {
+  switch (wtype) {
+    case 12: return kq_pb_launch<FMT_Q4_K>(xdt, pb, status, s);
+    case 13: return kq_pb_launch<FMT_Q5_K>(xdt, pb, status, s);
+    case 14: return kq_pb_launch<FMT_Q6_K>(xdt, pb, status, s);
+    default: return kq_pb_launch<FMT_IQ2_S>(xdt, pb, status, s);
+  }
 }
 
 // Called by vybdq_gemm for wtype 12, 13, 14, 22 after its argument checks (K % 256 == 0,

@@ -419,18 +419,9 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
   mm_finish<MT, NFX, NF, 4, SWI>(a, sm.last, tile, split, row0, fb, acc);
 }
 
+// One work unit (m-tile, n-tile, K split) of the GEMM; every wave of the workgroup calls it.
 template <int FMT, int XDT, int MT, int NFX>
-__global__ void __launch_bounds__(256, 1) k_mmq(MmArgs a) {
-  constexpr int NA = MmFmt<FMT>::D;
-  __shared__ __attribute__((aligned(16))) uint8_t a0[MT * 4096];
-  __shared__ __attribute__((aligned(16))) uint8_t a1[MT * 4096];
-  __shared__ __attribute__((aligned(16))) uint8_t a2[NA > 2 ? MT * 4096 : 16];
-  __shared__ __attribute__((aligned(16))) uint8_t a3[NA > 3 ? MT * 4096 : 16];
-  __shared__ uint32_t last;
-  const MmLds<MT> sm{{a0, a1, a2, a3}, &last};
-  const int units = a.m_tiles * a.n_tiles * a.splits;
-  int id = blockIdx.x;
-  if (a.xcd) id = (blockIdx.x & 7) * (units >> 3) + (blockIdx.x >> 3);
+__device__ __forceinline__ void mmq_unit(const MmArgs &a, const MmLds<MT> &sm, int id) {
   const int mt = id % a.m_tiles;
   const int rest = id / a.m_tiles;
   const int ntile = rest % a.n_tiles;
@@ -454,6 +445,24 @@ __global__ void __launch_bounds__(256, 1) k_mmq(MmArgs a) {
     case 1: mm_body<FMT, XDT, MT, NFX, 1>(a, sm, tile, split, row0, fb, s0, s1); break;
     default: mm_body<FMT, XDT, MT, NFX, 0>(a, sm, tile, split, row0, fb, s0, s1); break;
   }
+}
+
+#define VYBDQ_MMQ_LDS(FMT, MT)                                                        \
+  constexpr int NA_ = MmFmt<FMT>::D;                                                  \
+  __shared__ __attribute__((aligned(16))) uint8_t a0[MT * 4096];                      \
+  __shared__ __attribute__((aligned(16))) uint8_t a1[MT * 4096];                      \
+  __shared__ __attribute__((aligned(16))) uint8_t a2[NA_ > 2 ? MT * 4096 : 16];       \
+  __shared__ __attribute__((aligned(16))) uint8_t a3[NA_ > 3 ? MT * 4096 : 16];       \
+  __shared__ uint32_t last;                                                           \
+  const MmLds<MT> sm{{a0, a1, a2, a3}, &last}
+
+template <int FMT, int XDT, int MT, int NFX>
+__global__ void __launch_bounds__(256, 1) k_mmq(MmArgs a) {
+  VYBDQ_MMQ_LDS(FMT, MT);
+  const int units = a.m_tiles * a.n_tiles * a.splits;
+  int id = blockIdx.x;
+  if (a.xcd) id = (blockIdx.x & 7) * (units >> 3) + (blockIdx.x >> 3);
+  mmq_unit<FMT, XDT, MT, NFX>(a, sm, id);
 }
 
 // Split-K reduction: Y = RS + sum over splits (in split order) of the partial tiles, one float4
