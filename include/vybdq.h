@@ -98,7 +98,11 @@ int vybdq_gemv(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t
 
 /* Y[m, n] = RS[m, n] + sum_k X[m, k] * W[n, k] for m < M, n < N.
    X: x_dt (F32, F16, BF16) [M, K]; Y: y_dt (F32, F16, BF16, F64) [M, N]; RS: same type as
-   Y or 0. K % 32 == 0; 1 <= M <= 8. Accumulation in float32.
+   Y or 0. K % 32 == 0; 1 <= M <= 8. Accumulation in float32. Every GEMV entry point (and the
+   MoE layer's expert GEMV up to 64 tokens) stages X as fp16 per 32-element block: F32 / BF16 X
+   is first scaled by the power of two that brings the block's largest |x| into [2^14, 2^15)
+   (folded back into the block's weight scale), so activations of any magnitude neither overflow
+   nor flush to zero; F32 values are rounded to fp16 (11 significant bits) at staging.
    Replaces gemv_q8_0's sibling for q4_0 (p-block W@0 X@8 Y@16 M@24 N@32 K@40 YE@48 RS@120,
    native/kernels/rgemv.vyb:13-15, native/kernels/qwen3.vyb:395-440); the reference has no
    fused q4_0 GEMV, only deq_q4_0 followed by the f64 gemm (native/kernels/gemm.vyb:15-39). */

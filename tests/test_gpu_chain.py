@@ -119,3 +119,21 @@ def test_chain_invalid_stage_reports(dev):
     ch()
     assert ch.status() == _lib.ERR_SHAPE
     assert "invalid" in _lib.last_error()
+
+
+@pytest.mark.parametrize("kind", ["outlier", "fp16_limit", "tiny"])
+def test_chain_activation_range(dev, kind):
+    """The chain's x stage scales each block like the one-shot GEMV: f32 x of any magnitude."""
+    from tests.test_gpu_kquant import _x_pattern
+    N, K = 512, 2048
+    rng = np.random.default_rng(len(kind))
+    raw = synth.q4_0_weights(rng, N, K)
+    x = torch.from_numpy(_x_pattern(kind, rng, 1, K)[0]).to(dev)
+    W = torch.from_numpy(raw).to(dev)
+    y = torch.empty(N, dtype=torch.float32, device=dev)
+    chain = ops.GemvChain(ops.GGML_Q4_0, [ops.pblock(x, K, [(W, y, N)])], dev)
+    chain()
+    assert chain.status() == 0
+    ref = matmul.gemv_q4_0_f64(raw, x.cpu().numpy().astype(np.float64), N, K)[0]
+    assert np.all(np.isfinite(y.cpu().numpy()))
+    assert matmul.rel_maxnorm(y.cpu().numpy(), ref) < matmul.TOL

@@ -204,3 +204,36 @@ def test_gemm_superblock_prefill_shape(dev, ty, N, K):
     for c0 in (0, N - 256):
         wrows = matrix_ref(ty, raw[c0 * rb:(c0 + 256) * rb], 256, K)
         assert matmul.rel_maxnorm(y[:, c0:c0 + 256], matmul.gemm_rows_f64(x64, wrows)) < TOL, c0
+
+
+def _x_pattern(kind, rng, M, K):
+    x = rng.standard_normal((M, K))
+    if kind == "outlier":        # one channel a million times the rest
+        x[:, K // 3] = 1e6
+    elif kind == "offset":       # a large common offset
+        x = x + 1000.0
+    elif kind == "fp16_limit":   # around and past the largest fp16 (65504)
+        x = x * 3e4 + np.where(rng.random((M, K)) < 0.05, 7e4, 0.0)
+    elif kind == "tiny":         # below the fp16 normal range
+        x = x * 1e-7
+    elif kind == "huge":
+        x = x * 1e12
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("ty", SEG_TYPES)
+@pytest.mark.parametrize("kind", ["outlier", "offset", "fp16_limit", "tiny", "huge"])
+@pytest.mark.parametrize("xdt,M", [("f32", 1), ("bf16", 1), ("f32", 3)])
+def test_gemv_activation_range(dev, ty, kind, xdt, M):
+    """float32 / bf16 activations of any magnitude: each 32-element block is staged as fp16 after a
+    power-of-two scale, so nothing overflows to inf or flushes to zero (the reference multiplies
+    float32 x directly, native/kernels/rgemv.vyb:299-368)."""
+    N, K = 300, 2560
+    kinds = ["outlier", "offset", "fp16_limit", "tiny", "huge"]
+    rng = np.random.default_rng(1000 * ty + 10 * kinds.index(kind) + M + (5 if xdt == "bf16" else 0))
+    raw = _weights(ty, rng, N, K)
+    xd, x64 = x_as(_x_pattern(kind, rng, M, K), xdt, dev)
+    y = ops.gemv(ty, to_dev(raw, dev), xd.reshape(M, K), N, K).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x64.reshape(M, K), _rows(ty, raw, N, K))
+    assert np.all(np.isfinite(y))
+    assert matmul.rel_maxnorm(y, ref) < TOL

@@ -286,7 +286,7 @@ template <int FMT, int NT>
 static int chain_launch_nt(uint64_t P, int nstages, int64_t pstride, int64_t maxK, uint64_t ws, int ref_layout,
                         int max_per_cu, hipStream_t s) {
   const int maxP = static_cast<int>(maxK / 64);
-  const size_t lds = static_cast<size_t>(maxP) * (XPAIR_STRIDE + 2 * 4) + (FMT == FMT_IQ2_S ? kIq2sLdsBytes : 0);
+  const size_t lds = static_cast<size_t>(maxP) * XSTAGE_PAIR_BYTES + (FMT == FMT_IQ2_S ? kIq2sLdsBytes : 0);
   if (lds > 160 * 1024) return set_error(VYBDQ_ERR_SHAPE, "gemv chain: max_K too large for the LDS x stage");
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);

@@ -63,9 +63,15 @@ __device__ __forceinline__ V *pick3_ptr(V *const (&a)[3], int i) {
 }
 
 // LDS x stage, per X row m: pair p (64 fp16, natural order) at byte m*P*144 + 144*p (a 16-B pad
-// per pair keeps the G lanes that read consecutive pairs on distinct banks); block sums at
-// sx[m*2P + b].
+// per pair keeps the G lanes that read consecutive pairs on distinct banks); per 32-element block
+// b = m*2P + (block of the row), sx[2b] = the sum of its staged fp16 values and sx[2b + 1] = its
+// scale: the block's x values are scale * (staged values). For float32 / bf16 activations the
+// scale is the power of two that brings the block's largest |x| into [2^14, 2^15) (block_scale),
+// so activations of any magnitude stage without overflow or subnormals; fp16 activations stage
+// as they are (scale 1). The dot products multiply the scale into the block's weight scale.
 constexpr int XPAIR_STRIDE = 144;
+constexpr int XSX_PER_PAIR = 4;                                  // floats of sx per pair (2 blocks)
+constexpr int XSTAGE_PAIR_BYTES = XPAIR_STRIDE + 4 * XSX_PER_PAIR;  // LDS bytes per staged pair
 
 // Raw x chunk (8 consecutive elements) -> registers: XW = 4 dwords for fp16/bf16, 8 for f32.
 template <int XW>
@@ -104,23 +110,62 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+  const int t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false);
+  return fmaxf(v, __builtin_bit_cast(float, t));
+}
+
+// Block scale for the largest |x| of a block: with ex its biased float32 exponent
+// (2^(ex - 127) <= amax < 2^(ex - 126)), the block is staged as x * 2^-e, e = ex - 141, which brings
+// its largest value into [2^14, 2^15): no overflow for large activations, no fp16 subnormals for
+// small ones (a power of two: exact). e is clamped to [-100, 113] (beyond that the block is still
+// representable, if less precisely); all-zero blocks stay unscaled. Returns 2^e, writes 2^-e.
+__device__ __forceinline__ float block_scale(float amax, float &inv) {
+  const int ex = static_cast<int>((__float_as_uint(amax) >> 23) & 0xffu);
+  if (ex == 0) {
+    inv = 1.0f;
+    return 1.0f;
+  }
+  int e = ex - 141;
+  e = e < -100 ? -100 : (e > 113 ? 113 : e);
+  inv = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
+  return __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
+}
+
 // Convert a raw chunk to 4 fp16 pairs, store it at its LDS slot and reduce the block sums:
 // chunk c holds x[8c .. 8c+7] (for every X row m, since K = 64 P), lives in pair c>>3 at
 // (c>>3)*144 + (c&7)*16, and its 32-element block is c>>2. The 4 chunks of a block belong to 4
-// consecutive threads, which combine their partial sums with two xor shuffles.
+// consecutive threads, which combine their partial maxima and sums with two xor shuffles.
 template <int XW>
 __device__ __forceinline__ void stage_chunk(const uint32_t (&r)[XW], int xdt, int c, char *lds, float *sx) {
   uint32_t h[4];
+  float scale = 1.0f;
   if constexpr (XW == 8) {
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(__uint_as_float(r[j])));
+    amax = dpp_max<DPP_QUAD_XOR1>(amax);
+    amax = dpp_max<DPP_QUAD_XOR2>(amax);
+    float inv;
+    scale = block_scale(amax, inv);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      h[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(__uint_as_float(r[2 * j])),
-                                             static_cast<_Float16>(__uint_as_float(r[2 * j + 1]))});
+      h[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(__uint_as_float(r[2 * j]) * inv),
+                                             static_cast<_Float16>(__uint_as_float(r[2 * j + 1]) * inv)});
   } else if (xdt == VYBDQ_BF16) {
+    float amax = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      h[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(__uint_as_float(r[j] << 16)),
-                                             static_cast<_Float16>(__uint_as_float(r[j] & 0xffff0000u))});
+      amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(r[j] << 16)), fabsf(__uint_as_float(r[j] & 0xffff0000u))));
+    amax = dpp_max<DPP_QUAD_XOR1>(amax);
+    amax = dpp_max<DPP_QUAD_XOR2>(amax);
+    float inv;
+    scale = block_scale(amax, inv);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      h[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(__uint_as_float(r[j] << 16) * inv),
+                                             static_cast<_Float16>(__uint_as_float(r[j] & 0xffff0000u) * inv)});
   } else {
 #pragma unroll
     for (int j = 0; j < 4; ++j) h[j] = r[j];
@@ -133,7 +178,12 @@ __device__ __forceinline__ void stage_chunk(const uint32_t (&r)[XW], int xdt, in
   for (int j = 0; j < 4; ++j) s = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, h[j]), ones, s, false);
   s = dpp_add<DPP_QUAD_XOR1>(s);
   s = dpp_add<DPP_QUAD_XOR2>(s);
-  if ((c & 3) == 0) sx[c >> 2] = s;
+  if ((c & 3) == 0) *reinterpret_cast<float2 *>(sx + 2 * (c >> 2)) = float2{s, scale};
+}
+
+// {sum, scale} of x block b (b = m*2P + block of the row)
+__device__ __forceinline__ float2 x_block(const float *sx, int b) {
+  return *reinterpret_cast<const float2 *>(sx + 2 * b);
 }
 
 typedef uint32_t u4a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -224,8 +274,9 @@ __device__ __forceinline__ void pair_dot(const uint32_t (&dw)[Fmt<FMT>::PAIR_DWO
           ps = __builtin_amdgcn_fdot2(wv[4 * c + j], __builtin_bit_cast(h2, xw), ps, false);
         }
       }
-      const float part = fmaf(-Fmt<FMT>::CORR, sx[m * 2 * P + 2 * p + h], ps);
-      acc[m] = fmaf(d, part, acc[m]);
+      const float2 xb = x_block(sx, m * 2 * P + 2 * p + h);
+      const float part = fmaf(-Fmt<FMT>::CORR, xb.x, ps);
+      acc[m] = fmaf(d * xb.y, part, acc[m]);
     }
   }
 }

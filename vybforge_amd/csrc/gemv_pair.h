@@ -22,8 +22,10 @@
 // weights per register, and v_dot2_f32_f16 multiplies-and-accumulates two weights per op in
 // float32. Per block, sum_k x_k (q_k - OFF) = dot - (1024 + OFF) * sum_k x_k with the block
 // sum of the same fp16 x from the stage, then y += d * partial. OFF = 8 for q4_0 nibbles;
-// Q8_0 bytes are biased to unsigned (q ^ 0x80 = q + 128), OFF = 128. Float32 x is rounded to
-// fp16 at staging; the resulting error (~1e-4 relative) is well inside the 2e-3 gate.
+// Q8_0 bytes are biased to unsigned (q ^ 0x80 = q + 128), OFF = 128. Float32 and bf16 x are
+// staged as fp16 per 32-element block after a power-of-two block scale (gemv_dev.h block_scale:
+// no overflow, no subnormals), which multiplies into d; the fp16 rounding of float32 x
+// (~1e-4 relative) is well inside the 2e-3 gate.
 #pragma once
 #include <cstdio>
 #include <cstdlib>
@@ -204,7 +206,7 @@ template <int FMT, int G, int ORDER, int M, int XW, int U>
 static int launch_gu(const void *X, int xdt, int64_t K, const Segs &segs, int threads, hipStream_t s) {
   const int64_t rows = segs.end[2];
   const int P = static_cast<int>(K / 64);
-  const size_t lds = static_cast<size_t>(M) * P * (XPAIR_STRIDE + 2 * 4) + (FMT == FMT_IQ2_S ? kIq2sLdsBytes : 0);
+  const size_t lds = static_cast<size_t>(M) * P * XSTAGE_PAIR_BYTES + (FMT == FMT_IQ2_S ? kIq2sLdsBytes : 0);
   if (lds > static_cast<size_t>(kMaxLds)) return set_error(VYBDQ_ERR_SHAPE, "gemv: K too large for the LDS x stage at this M");
   const int rows_per_wg = threads / G;
   const unsigned grid = static_cast<unsigned>((rows + rows_per_wg - 1) / rows_per_wg);

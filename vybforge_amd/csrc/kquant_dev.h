@@ -40,7 +40,7 @@ template <> struct Fmt<FMT_Q5_K> {
 // entries of 8 fp16 magnitudes, then 256 sign patterns as fp16 sign-bit masks, 16 B each
 constexpr size_t kIq2sLdsBytes = (1024 + 256) * 16 + 16;
 __device__ __forceinline__ u4 *iq2s_lds_grid(float *sx, int M, int P) {
-  return reinterpret_cast<u4 *>(sx + ((2 * M * P + 3) & ~3));  // sx is 16-B aligned
+  return reinterpret_cast<u4 *>(sx + ((XSX_PER_PAIR * M * P + 3) & ~3));  // sx is 16-B aligned
 }
 
 template <> struct Fmt<FMT_IQ2_S> {
@@ -185,8 +185,8 @@ __device__ __forceinline__ void unit_dot_kq(const uint32_t (&dw)[Fmt<FMT>::PAIR_
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         const float ps = block_dot(wv, lds + m * P * XPAIR_STRIDE + p * XPAIR_STRIDE + 64 * h);
-        const float s = sx[m * 2 * P + 2 * p + h];
-        acc[m] = fmaf(ds, fmaf(-1024.0f, s, ps), fmaf(-dm, s, acc[m]));
+        const float2 xb = x_block(sx, m * 2 * P + 2 * p + h);
+        acc[m] = fmaf(xb.y, fmaf(ds, fmaf(-1024.0f, xb.x, ps), -dm * xb.x), acc[m]);
       }
     }
   } else if constexpr (FMT == FMT_IQ2_S) {
@@ -218,7 +218,7 @@ __device__ __forceinline__ void unit_dot_kq(const uint32_t (&dw)[Fmt<FMT>::PAIR_
           const uint32_t xw = xv[k];
           ps = __builtin_amdgcn_fdot2(wv[k], __builtin_bit_cast(h2, xw), ps, false);
         }
-        acc[m] = fmaf(dl, ps, acc[m]);
+        acc[m] = fmaf(dl * x_block(sx, m * 2 * P + 2 * p + ib).y, ps, acc[m]);
       }
     }
   } else {
@@ -256,7 +256,7 @@ __device__ __forceinline__ void unit_dot_kq(const uint32_t (&dw)[Fmt<FMT>::PAIR_
       for (int m = 0; m < M; ++m) {
         float p0, p1;
         block_dot16(wv, lds + m * P * XPAIR_STRIDE + xp * XPAIR_STRIDE + 64 * part, p0, p1);
-        acc[m] = fmaf(d, fmaf(s0, p0, s1 * p1), acc[m]);
+        acc[m] = fmaf(d * x_block(sx, m * 2 * P + 2 * xp + part).y, fmaf(s0, p0, s1 * p1), acc[m]);
       }
     }
   }

@@ -239,7 +239,7 @@ __global__ void __launch_bounds__(256) k_moe_gemv(MoeGvArgs a) {
 template <int FMT, int G, int U, bool SWI, int XW, int MCMAX>
 int moe_gemv_launch2(const MoeGvArgs &a, int max_groups, hipStream_t s) {
   const void *fn = reinterpret_cast<const void *>(&k_moe_gemv<FMT, G, U, SWI, XW, MCMAX>);
-  const size_t lds = static_cast<size_t>(a.mc) * a.P * (XPAIR_STRIDE + 2 * 4);
+  const size_t lds = static_cast<size_t>(a.mc) * a.P * XSTAGE_PAIR_BYTES;
   if (lds > 64 * 1024) {
     static bool raised = false;  // one attribute call per instantiation
     if (!raised) {
