@@ -295,7 +295,8 @@ int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t X, ui
    (2 = q4_0 GGUF order, 8 = Q8_0, 12 = Q4_K, 13 = Q5_K, 14 = Q6_K, 22 = IQ2_S): weights are
    dequantized to fp16 (q4_0 / Q8_0: d * (q - OFF), one rounding; super-block types: the exact
    value rounded to float32, then to fp16, as vybdq_dequant's F16 output) and multiplied with fp16
-   MFMA, float32 accumulation; X (f32/f16/bf16) is converted to fp16 (|x| < 65504).
+   MFMA, float32 accumulation; X (f32/f16/bf16) is converted to fp16 as it is (|x| < 65504, as
+   the reference's f16 tiles require; vybdq_gemm_ws lifts this).
    q4_0 / Q8_0: K % 64 == 0; M >= 64 with K % 256 == 0 and N % 16 == 0 runs the kernel that
    dequantizes into the MFMA operand registers; other shapes need N % 64 == 0 and stage the
    dequantized tile in LDS. Super-block types: K % 256 == 0, N % 64 == 0, any M.
@@ -313,7 +314,9 @@ int64_t vybdq_gemm_workspace_size(int wtype, int64_t M, int64_t N, int64_t K);
    workgroups: each stores float32 partials and a second kernel sums them in split order, so
    results stay deterministic for a fixed shape and workspace (they may differ in the last bits
    from the unsplit vybdq_gemm); bf16/f32 X is converted to fp16 once into the workspace instead of
-   once per output tile. Calls that share a workspace must not overlap. The reference's gemm_q80
+   once per output tile, each row scaled by the power of two that brings its largest |x| into
+   [2^14, 2^15) (multiplied back into the row's outputs), so X of any magnitude neither overflows nor
+   flushes to zero. Calls that share a workspace must not overlap. The reference's gemm_q80
    has no workspace (native/tools/gen_rpf.py:58-62); this is the same GEMM for shapes whose
    tiles alone do not fill the GPU. */
 int vybdq_gemm_ws(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K, int x_dt,

@@ -318,3 +318,23 @@ def test_moe_layer_glm_shapes(dev):
     # GLM-5 expert shapes (H 6144, I 2048) with few experts so the float64 oracle stays cheap
     out, ref = moe_case(dev, ops.GGML_Q4_0, 16, H=6144, I=2048, E=4, k=2, seed=7)
     assert matmul.rel_maxnorm(out, ref) < TOL
+
+
+@pytest.mark.parametrize("ty", [ops.GGML_Q4_0, ops.GGML_Q8_0])
+@pytest.mark.parametrize("kind", ["outlier", "offset", "fp16_limit", "tiny", "huge"])
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+@pytest.mark.parametrize("M,N,K", [(200, 256, 4096), (512, 128, 5120)])
+def test_gemm_ws_activation_range(dev, ty, kind, xdt, M, N, K):
+    """vybdq_gemm_ws converts X to fp16 once, each row scaled by the power of two that brings its
+    largest |x| into [2^14, 2^15) (multiplied back in the epilogue and the split-K reduce): bf16 /
+    float32 activations of any magnitude neither overflow nor flush to zero."""
+    from tests.test_gpu_kquant import _x_pattern
+    kinds = ["outlier", "offset", "fp16_limit", "tiny", "huge"]
+    rng = np.random.default_rng(77 + 10 * kinds.index(kind) + ty + M)
+    raw = weights(ty, rng, N, K)
+    x = torch.from_numpy(_x_pattern(kind, rng, M, K)).to(TDT[xdt])
+    ws = ops.GemmWorkspace([(M, N, K)], dev, ty)
+    y = ops.gemm(ty, dev_t(raw, dev), x.to(dev), N, K, workspace=ws).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x.to(torch.float64).numpy(), ref_rows(ty, raw, N, K))
+    assert np.all(np.isfinite(y))
+    assert matmul.rel_maxnorm(y, ref) < TOL

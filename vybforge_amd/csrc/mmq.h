@@ -59,6 +59,7 @@ struct MmArgs {
   float *part;            // split partials [tile][split][waves][NFX][MT][64][4]
   const uint8_t *W2;      // SwiGLU: the up rows (W holds the gate rows, same layout)
   float limit;            // SwiGLU clamp
+  const float *xscale;    // per output row: X row m was staged as X / xscale[m] (null: 1)
 };
 
 __device__ __forceinline__ float mm_silu(float g) { return g / (1.0f + __expf(-g)); }
@@ -202,10 +203,11 @@ __device__ __forceinline__ void mm_finish(const MmArgs &a, uint32_t *last, int t
         const int m = row0 + 16 * i + 4 * g + r;
         if (m >= a.M) continue;
         const int64_t idx = static_cast<int64_t>(m) * a.ldy + n;
-        float v = acc[i][f][r];
+        const float xs = a.xscale ? a.xscale[m] : 1.0f;
+        float v = acc[i][f][r] * xs;
         if constexpr (SWI) {
           const float gt = fminf(v, a.limit);
-          const float up = fminf(fmaxf(acc[i][NF + f][r], -a.limit), a.limit);
+          const float up = fminf(fmaxf(acc[i][NF + f][r] * xs, -a.limit), a.limit);
           v = mm_silu(gt) * up;
         }
         switch (a.ydt) {
@@ -502,11 +504,12 @@ __global__ void __launch_bounds__(256) k_mm_reduce(MmArgs a) {
     const int m = row0 + r;
     if (m >= a.M) continue;
     const int64_t idx = static_cast<int64_t>(m) * a.ldy + n;
+    const float v = a.xscale ? tot[r] * a.xscale[m] : tot[r];
     switch (a.ydt) {
-      case VYBDQ_F32: store_elem<VYBDQ_F32>(a.Y, a.RS, idx, tot[r]); break;
-      case VYBDQ_F16: store_elem<VYBDQ_F16>(a.Y, a.RS, idx, tot[r]); break;
-      case VYBDQ_BF16: store_elem<VYBDQ_BF16>(a.Y, a.RS, idx, tot[r]); break;
-      default: store_elem<VYBDQ_F64>(a.Y, a.RS, idx, tot[r]); break;
+      case VYBDQ_F32: store_elem<VYBDQ_F32>(a.Y, a.RS, idx, v); break;
+      case VYBDQ_F16: store_elem<VYBDQ_F16>(a.Y, a.RS, idx, v); break;
+      case VYBDQ_BF16: store_elem<VYBDQ_BF16>(a.Y, a.RS, idx, v); break;
+      default: store_elem<VYBDQ_F64>(a.Y, a.RS, idx, v); break;
     }
   }
 }

@@ -90,24 +90,67 @@ bool mmq_supported(int64_t M, int64_t N, int64_t K) {
   return M >= 1 && K % 256 == 0 && N % 16 == 0 && N >= 16 && M * K < (int64_t(1) << 31);
 }
 
-// X -> fp16 copy (8 elements per thread): bf16 is exact in the fp16 normal range, f32 rounds to
-// nearest even. The GEMM then streams the fp16 copy straight into LDS.
+// X -> fp16 copy, one workgroup per row: the row's largest |x| is brought into [2^14, 2^15) by a
+// power of two 2^-e (exact; all-zero rows and rows whose e would leave [-100, 113] are clamped),
+// the scaled row is rounded to fp16 (bf16 values exactly, f32 to nearest even) and 2^e goes to
+// xscale[row], which the GEMM epilogue multiplies back: activations of any magnitude neither
+// overflow nor flush to zero. The GEMM then streams the fp16 copy straight into LDS.
 template <int XDT>
-__global__ void __launch_bounds__(256) k_x_to_f16(const void *__restrict__ X, u4 *__restrict__ Xh, int64_t n8) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= n8) return;
-  XChunk<XDT> c;
-  x_load<XDT>(X, static_cast<uint32_t>(i * 8), c);
-  Xh[i] = x_to_f16<XDT>(c);
+__global__ void __launch_bounds__(256) k_x_to_f16(const void *__restrict__ X, u4 *__restrict__ Xh,
+                                                  float *__restrict__ xscale, int64_t K) {
+  __shared__ float wmax[4];
+  const int64_t row = blockIdx.x;
+  const int64_t n8 = K / 8;
+  float amax = 0.f;
+  for (int64_t i = threadIdx.x; i < n8; i += 256) {
+    XChunk<XDT> c;
+    x_load<XDT>(X, static_cast<uint32_t>(row * K + i * 8), c);
+    if constexpr (XDT == VYBDQ_F32) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(__uint_as_float(c.r[j >> 2][j & 3])));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t v = c.r[j];
+        amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(v << 16)), fabsf(__uint_as_float(v & 0xffff0000u))));
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  float inv;
+  const float scale = block_scale(amax, inv);
+  if (threadIdx.x == 0) xscale[row] = scale;
+  for (int64_t i = threadIdx.x; i < n8; i += 256) {
+    XChunk<XDT> c;
+    x_load<XDT>(X, static_cast<uint32_t>(row * K + i * 8), c);
+    u4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float a, b;
+      if constexpr (XDT == VYBDQ_F32) {
+        a = __uint_as_float(c.r[j >> 1][2 * (j & 1)]);
+        b = __uint_as_float(c.r[j >> 1][2 * (j & 1) + 1]);
+      } else {
+        a = __uint_as_float(c.r[j] << 16);
+        b = __uint_as_float(c.r[j] & 0xffff0000u);
+      }
+      o[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(a * inv), static_cast<_Float16>(b * inv)});
+    }
+    Xh[row * n8 + i] = o;
+  }
 }
 
 static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 
-// workspace: [split partials][fp16 copy of X]
+// workspace: [split partials][fp16 copy of X][X row scales]
 int64_t mmq_workspace_size(int64_t M, int64_t N, int64_t K) {
   if (!mmq_supported(M, N, K)) return 0;
   return align256(mm_plan(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K / 128), true).ws_bytes) +
-         align256(M * K * 2);
+         align256(M * K * 2) + align256(M * 4);
 }
 
 int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
@@ -117,16 +160,19 @@ int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   if (p.splits > 1 && ws_bytes < p.ws_bytes) p = mm_plan(static_cast<int>(M), static_cast<int>(N), S, false);
   // with room for it, a non-fp16 X is converted once up front (instead of once per N tile)
   const int64_t xh_off = align256(p.ws_bytes);
-  if (ws && xdt != VYBDQ_F16 && ws_bytes >= xh_off + M * K * 2) {
+  const int64_t sc_off = xh_off + align256(M * K * 2);
+  const float *xscale = nullptr;
+  if (ws && xdt != VYBDQ_F16 && ws_bytes >= sc_off + M * 4) {
     u4 *xh = reinterpret_cast<u4 *>(static_cast<char *>(ws) + xh_off);
-    const int64_t n8 = M * K / 8;
-    const unsigned grid = static_cast<unsigned>((n8 + 255) / 256);
-    if (xdt == VYBDQ_BF16) hipLaunchKernelGGL(k_x_to_f16<VYBDQ_BF16>, dim3(grid), dim3(256), 0, s, X, xh, n8);
-    else hipLaunchKernelGGL(k_x_to_f16<VYBDQ_F32>, dim3(grid), dim3(256), 0, s, X, xh, n8);
+    float *sc = reinterpret_cast<float *>(static_cast<char *>(ws) + sc_off);
+    const unsigned grid = static_cast<unsigned>(M);
+    if (xdt == VYBDQ_BF16) hipLaunchKernelGGL(k_x_to_f16<VYBDQ_BF16>, dim3(grid), dim3(256), 0, s, X, xh, sc, K);
+    else hipLaunchKernelGGL(k_x_to_f16<VYBDQ_F32>, dim3(grid), dim3(256), 0, s, X, xh, sc, K);
     const int rc = check_launch("mmq x->f16");
     if (rc) return rc;
     X = xh;
     xdt = VYBDQ_F16;
+    xscale = sc;
   }
   MmArgs a{};
   a.W = static_cast<const uint8_t *>(W);
@@ -145,6 +191,7 @@ int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   a.ydt = ydt;
   a.ldy = ldy;
   a.RS = RS;
+  a.xscale = xscale;
   if (p.splits > 1) {
     a.part = static_cast<float *>(ws);
   }
