@@ -87,3 +87,25 @@ def test_errors(tmp_path):
             assert h == _lib.ERR_ARG
     assert lib.vybdq_gguf_info(12345, 0) == _lib.ERR_ARG
     assert lib.vybdq_gguf_open(str(tmp_path / "missing.gguf").encode()) == _lib.ERR_ARG
+
+
+def test_corrupt_counts_and_sizes_are_errors(tmp_path):
+    """Counts larger than the file can hold and array sizes whose byte count overflows 64 bits are
+    rejected with an error code (no allocation of the claimed size, no exception across the C ABI)."""
+    import struct
+    from vybforge_amd import _lib
+
+    def write(name, body):
+        p = tmp_path / name
+        p.write_bytes(b"GGUF" + struct.pack("<I", 3) + body)
+        return str(p).encode()
+
+    huge = write("huge_counts.gguf", struct.pack("<QQ", 1 << 62, 1 << 62) + b"\0" * 64)
+    assert _lib.lib.vybdq_gguf_open(huge) == _lib.ERR_ARG
+    assert "counts" in _lib.last_error()
+    key = b"a.b"
+    arr = struct.pack("<QQ", 0, 1) + struct.pack("<Q", len(key)) + key + struct.pack("<I", 9)
+    arr += struct.pack("<IQ", 10, (1 << 63) + 5) + b"\0" * 64  # u64 array whose byte size wraps
+    wrap = write("array_wrap.gguf", arr)
+    assert _lib.lib.vybdq_gguf_open(wrap) == _lib.ERR_ARG
+    assert "array" in _lib.last_error()

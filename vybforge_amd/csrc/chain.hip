@@ -288,30 +288,19 @@ static int chain_launch_nt(uint64_t P, int nstages, int64_t pstride, int64_t max
   const int maxP = static_cast<int>(maxK / 64);
   const size_t lds = static_cast<size_t>(maxP) * XSTAGE_PAIR_BYTES + (FMT == FMT_IQ2_S ? kIq2sLdsBytes : 0);
   if (lds > 160 * 1024) return set_error(VYBDQ_ERR_SHAPE, "gemv chain: max_K too large for the LDS x stage");
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("gemv chain: hipGetDevice: ") + hipGetErrorString(e));
-  if (dev < 0 || dev >= 64) return set_error(VYBDQ_ERR_HIP, "gemv chain: device index out of range");
   const int cus = device_cu_count();
   const void *fn = reinterpret_cast<const void *>(&k_gemv_chain<FMT, NT>);
   // resident workgroups per CU for this LDS size: queried once per device and size (the LDS
   // attribute and the occupancy query stay out of later launches, which may be under capture)
-  static std::atomic<int64_t> occ[64];  // (lds << 8) | workgroups per CU, 0 = not queried
-  const int64_t key = static_cast<int64_t>(lds) << 8;
-  int per_cu = 0;
-  const int64_t have = occ[dev].load(std::memory_order_relaxed);
-  if ((have & ~int64_t(0xff)) == key && (have & 0xff) > 0) {
-    per_cu = static_cast<int>(have & 0xff);
-  } else {
-    if (lds > 64 * 1024) {
-      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-      if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("gemv chain: LDS attribute: ") + hipGetErrorString(e));
-    }
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NT, lds);
-    if (e != hipSuccess || per_cu < 1 || per_cu > 255)
-      return set_error(VYBDQ_ERR_HIP, "gemv chain: kernel cannot be resident (occupancy query failed)");
-    occ[dev].store(key | per_cu, std::memory_order_relaxed);
+  if (lds > 64 * 1024) {
+    static std::atomic<uint64_t> raised{0};
+    const int rc = ensure_lds_limit(fn, 160 * 1024, raised, "gemv chain");
+    if (rc) return rc;
   }
+  static std::atomic<int64_t> occ[64];
+  int per_cu = 0;
+  const int orc = resident_per_cu(fn, NT, lds, occ, per_cu, "gemv chain");
+  if (orc) return orc;
   // a chain: two workgroups per CU keep the waits short while every workgroup stays resident; one
   // stage (no waits): as many as fit
   const int grid = cus * (per_cu < max_per_cu ? per_cu : max_per_cu);

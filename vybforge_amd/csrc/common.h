@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
+#include <atomic>
 #include <string>
 
 #include "vybdq.h"
@@ -21,7 +22,44 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 int set_error(int code, const std::string &msg);
 int check_launch(const char *what);  // hipGetLastError after a launch
+// a launch-plan override from the environment, only when VYBDQ_TUNING is set (else null)
+const char *tuning_env(const char *name);
 inline hipStream_t as_stream(uint64_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Raise a kernel's dynamic-LDS limit to `bytes` once per device: `done` is the caller's static mask
+// of devices already raised (one per kernel instantiation; atomic, so host threads may race here).
+inline int ensure_lds_limit(const void *fn, int bytes, std::atomic<uint64_t> &done, const char *what) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return set_error(VYBDQ_ERR_HIP, std::string(what) + ": no current HIP device");
+  const uint64_t bit = uint64_t(1) << dev;
+  if (done.load(std::memory_order_relaxed) & bit) return VYBDQ_OK;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string(what) + ": LDS attribute: " + hipGetErrorString(e));
+  done.fetch_or(bit, std::memory_order_relaxed);
+  return VYBDQ_OK;
+}
+
+// Resident workgroups per CU of a kernel at `lds` bytes of dynamic LDS: queried once per device and
+// LDS size; `cache` is the caller's static per-device word ((lds << 8) | count, 0 = not queried).
+inline int resident_per_cu(const void *fn, int threads, size_t lds, std::atomic<int64_t> (&cache)[64], int &per_cu,
+                           const char *what) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return set_error(VYBDQ_ERR_HIP, std::string(what) + ": no current HIP device");
+  const int64_t key = static_cast<int64_t>(lds) << 8;
+  const int64_t have = cache[dev].load(std::memory_order_relaxed);
+  if ((have & ~int64_t(0xff)) == key && (have & 0xff) > 0) {
+    per_cu = static_cast<int>(have & 0xff);
+    return VYBDQ_OK;
+  }
+  int nb = 0;
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, threads, lds);
+  if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string(what) + ": occupancy: " + hipGetErrorString(e));
+  per_cu = nb < 1 ? 1 : (nb > 255 ? 255 : nb);
+  cache[dev].store(key | per_cu, std::memory_order_relaxed);
+  return VYBDQ_OK;
+}
 
 // Compute units of the current device (cached per device; 256 if the query fails).
 inline int device_cu_count() {

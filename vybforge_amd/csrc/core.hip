@@ -17,6 +17,17 @@ int check_launch(const char *what) {
   return VYBDQ_OK;
 }
 
+// The launch-plan overrides (VYBDQ_GEMV_PLAN, VYBDQ_MMQ_PLAN, VYBDQ_MOE_*, VYBDQ_EXL3_SPLITS) are
+// read only when VYBDQ_TUNING was set when the library first needed one; otherwise no launch
+// reads the environment.
+const char *tuning_env(const char *name) {
+  static const bool enabled = [] {
+    const char *t = getenv("VYBDQ_TUNING");
+    return t && t[0] && t[0] != '0';
+  }();
+  return enabled ? getenv(name) : nullptr;
+}
+
 // ---- decode-only kernels ----------------------------------------------------------------
 // One thread per 8 consecutive output elements of one block (4 threads per block): the
 // thread loads the block scale and its 4 quant bytes, decodes exactly (fp16 d times a small

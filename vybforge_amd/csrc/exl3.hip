@@ -547,7 +547,7 @@ static Exl3Split exl3_splits(int64_t K, int64_t N, int BP) {
   int S = static_cast<int>((target + groups - 1) / groups);
   if (S > 16) S = 16;
   if (S > KB / 4) S = KB / 4 > 0 ? KB / 4 : 1;
-  if (const char *e = getenv("VYBDQ_EXL3_SPLITS")) S = atoi(e);  // tuning override
+  if (const char *e = tuning_env("VYBDQ_EXL3_SPLITS")) S = atoi(e);  // tuning override
   if (S < 1) S = 1;
   int kbs = (KB + S - 1) / S;
   kbs = (kbs + 7) / 8 * 8;
@@ -617,12 +617,10 @@ extern "C" int vybdq_dequant_exl3(uint64_t trellis, uint64_t suh, uint64_t svh, 
   void *o = reinterpret_cast<void *>(out);
 #define L(CB, ODT)                                                                                         \
   do {                                                                                                     \
-    static bool raised = false;                                                                            \
-    if (!raised) {                                                                                         \
-      (void)hipFuncSetAttribute(reinterpret_cast<const void *>(&k_exl3_dequant<CB, ODT>),                   \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));        \
-      raised = true;                                                                                       \
-    }                                                                                                      \
+    static std::atomic<uint64_t> raised{0};                                                                \
+    const int rc = ensure_lds_limit(reinterpret_cast<const void *>(&k_exl3_dequant<CB, ODT>),              \
+                                    static_cast<int>(lds), raised, "vybdq_dequant_exl3");                  \
+    if (rc) return rc;                                                                                     \
     hipLaunchKernelGGL((k_exl3_dequant<CB, ODT>), grid, dim3(256), lds, s, t, su, sv, o, NB);             \
   } while (0)
   if (codebook == VYBDQ_EXL3_MCG) {
@@ -645,13 +643,9 @@ static void exl3_gemm_launch(const uint16_t *t, const void *X, int xdt, const _F
                              int NB, const Exl3Split &sp, hipStream_t s) {
   const size_t lds = exl3_lds_bytes(BP, sp.kbs);  // <= 160 KB, checked by the caller
   if (lds > 64 * 1024) {
-    static bool raised = false;  // one attribute call per instantiation
-    if (!raised) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void *>(&k_exl3_gemm<CB, BP>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-        return;  // the launch below then fails and check_launch reports it
-      raised = true;
-    }
+    static std::atomic<uint64_t> raised{0};
+    if (ensure_lds_limit(reinterpret_cast<const void *>(&k_exl3_gemm<CB, BP>), 160 * 1024, raised, "exl3 gemm"))
+      return;  // the launch below then fails and check_launch reports it
   }
   hipLaunchKernelGGL((k_exl3_gemm<CB, BP>), dim3(static_cast<unsigned>(NB / 8), static_cast<unsigned>(sp.S)),
                      dim3(256), lds, s, t, X, xdt, su, sv, Y, ydt, B, xp, zp, arr, K, NB, sp.kbs);

@@ -27,6 +27,7 @@
 // no overflow, no subnormals), which multiplies into d; the fp16 rounding of float32 x
 // (~1e-4 relative) is well inside the 2e-3 gate.
 #pragma once
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include "gemv_dev.h"
@@ -172,7 +173,7 @@ static int pair_umax(int fmt) {
 // ceil(P / G) pairs (up to the format's largest), narrowed while the grid would not be resident in
 // one round; 256 threads (one workgroup of 16 waves per CU was measured 16% slower on the decode
 // stack). For batches (M > 1) the smallest G with ~4 waves per CU whose row fits one widest batch.
-// VYBDQ_GEMV_PLAN="G,U,T" overrides the plan.
+// VYBDQ_GEMV_PLAN="G,U,T" overrides the plan (read only with VYBDQ_TUNING set, common.h).
 static PairPlan pair_plan(int fmt, int64_t rows, int P, int64_t M) {
   const int umax = pair_umax(fmt);
   PairPlan pl{64, umax, 256};
@@ -192,7 +193,7 @@ static PairPlan pair_plan(int fmt, int64_t rows, int P, int64_t M) {
     pl.G = G;
     pl.U = U < umax ? U : umax;
   }
-  if (const char *e = getenv("VYBDQ_GEMV_PLAN")) {
+  if (const char *e = tuning_env("VYBDQ_GEMV_PLAN")) {
     int g = 0, u = 0, t = 0;
     if (sscanf(e, "%d,%d,%d", &g, &u, &t) == 3 && (g == 8 || g == 16 || g == 32 || g == 64) && u >= 1 &&
         u <= umax && (t == 64 || t == 128 || t == 256) && t >= g) {
@@ -211,13 +212,10 @@ static int launch_gu(const void *X, int xdt, int64_t K, const Segs &segs, int th
   const int rows_per_wg = threads / G;
   const unsigned grid = static_cast<unsigned>((rows + rows_per_wg - 1) / rows_per_wg);
   if (lds > 64 * 1024) {
-    static bool raised = false;  // one attribute call per instantiation
-    if (!raised) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_pair<FMT, G, ORDER, M, XW, U>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
-      if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("gemv: LDS attribute: ") + hipGetErrorString(e));
-      raised = true;
-    }
+    static std::atomic<uint64_t> raised{0};  // one attribute call per instantiation and device
+    const int rc = ensure_lds_limit(reinterpret_cast<const void *>(&k_gemv_pair<FMT, G, ORDER, M, XW, U>), kMaxLds,
+                                    raised, "gemv");
+    if (rc) return rc;
   }
   hipLaunchKernelGGL((k_gemv_pair<FMT, G, ORDER, M, XW, U>), dim3(grid), dim3(threads), lds, s, X, xdt, K, segs);
   return check_launch("gemv");

@@ -158,7 +158,10 @@ static int parse(const char *path, GgufFile &g) {
   g.version = r.get<uint32_t>();
   if (g.version < 2 || g.version > 3) return set_error(VYBDQ_ERR_ARG, "gguf: unsupported version");
   const uint64_t nt = r.get<uint64_t>(), nkv = r.get<uint64_t>();
-  if (!r.ok() || nt > g.file_size || nkv > g.file_size) return set_error(VYBDQ_ERR_ARG, "gguf: bad counts");
+  // every metadata pair takes at least 13 bytes (key length, type, one value byte) and every tensor
+  // info 24 (name length, n_dims, type, offset): counts beyond what the file can hold are corrupt
+  const uint64_t rest = g.file_size - r.pos();
+  if (!r.ok() || nkv > rest / 13 || nt > rest / 24) return set_error(VYBDQ_ERR_ARG, "gguf: bad counts");
   for (uint64_t k = 0; k < nkv; ++k) {
     std::string key = r.str();
     GgufValue v;
@@ -172,7 +175,8 @@ static int parse(const char *path, GgufFile &g) {
       if (!r.ok() || v.arr_len < 0) return set_error(VYBDQ_ERR_ARG, "gguf: bad array");
       const int sb = scalar_bytes(v.arr_type);
       if (sb) {
-        if (!r.skip(static_cast<uint64_t>(v.arr_len) * sb)) return set_error(VYBDQ_ERR_ARG, "gguf: truncated array");
+        if (static_cast<uint64_t>(v.arr_len) > UINT64_MAX / sb || !r.skip(static_cast<uint64_t>(v.arr_len) * sb))
+          return set_error(VYBDQ_ERR_ARG, "gguf: truncated array");
       } else {
         for (int64_t e = 0; e < v.arr_len; ++e)
           if (!skip_value(r, v.arr_type, 1)) return set_error(VYBDQ_ERR_ARG, "gguf: bad array element");
@@ -205,12 +209,13 @@ static int parse(const char *path, GgufFile &g) {
 }
 
 static std::mutex g_mu;
-static std::vector<std::unique_ptr<GgufFile>> g_files;  // handle h -> g_files[h - 1]
+static std::vector<std::shared_ptr<GgufFile>> g_files;  // handle h -> g_files[h - 1]
 
-static GgufFile *lookup(int64_t h) {
+// The file of handle h, shared: a concurrent vybdq_gguf_close only drops the table's reference.
+static std::shared_ptr<GgufFile> lookup(int64_t h) {
   std::lock_guard<std::mutex> lk(g_mu);
   if (h < 1 || h > static_cast<int64_t>(g_files.size())) return nullptr;
-  return g_files[h - 1].get();
+  return g_files[h - 1];
 }
 
 static int64_t tensor_bytes(const GgufTensor &t) {
@@ -221,7 +226,7 @@ static int64_t tensor_bytes(const GgufTensor &t) {
     if (d < 0 || (d && n > INT64_MAX / d)) return -1;
     n *= d;
   }
-  if (n % ts.blk) return -1;
+  if (n % ts.blk || n / ts.blk > INT64_MAX / ts.bytes) return -1;
   return n / ts.blk * ts.bytes;
 }
 
@@ -239,7 +244,7 @@ static int64_t copy_str(const std::string &s, char *buf, int64_t cap) {
 using namespace vybdq;
 
 #define GGUF_GET(h, g)                                                     \
-  GgufFile *g = lookup(h);                                                 \
+  const std::shared_ptr<GgufFile> g = lookup(h);                           \
   if (!g) return set_error(VYBDQ_ERR_ARG, "gguf: unknown handle")
 #define GGUF_TENSOR(g, i)                                                  \
   if (i < 0 || i >= static_cast<int64_t>(g->tensors.size()))               \
@@ -250,12 +255,16 @@ using namespace vybdq;
 
 extern "C" int64_t vybdq_gguf_open(const char *path) {
   VYBDQ_REQUIRE(path, VYBDQ_ERR_ARG, "null path");
-  auto g = std::make_unique<GgufFile>();
-  const int rc = parse(path, *g);
-  if (rc) return rc;
-  std::lock_guard<std::mutex> lk(g_mu);
-  g_files.push_back(std::move(g));
-  return static_cast<int64_t>(g_files.size());
+  try {  // no exception crosses the C boundary (allocation failures on corrupt counts included)
+    auto g = std::make_shared<GgufFile>();
+    const int rc = parse(path, *g);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_files.push_back(std::move(g));
+    return static_cast<int64_t>(g_files.size());
+  } catch (const std::exception &e) {
+    return set_error(VYBDQ_ERR_ARG, std::string("gguf: ") + e.what());
+  }
 }
 
 extern "C" int vybdq_gguf_close(int64_t h) {
@@ -339,7 +348,7 @@ extern "C" int64_t vybdq_gguf_kv_field(int64_t h, int64_t i, int what) {
 }
 
 extern "C" double vybdq_gguf_kv_float(int64_t h, int64_t i) {
-  GgufFile *g = lookup(h);
+  const std::shared_ptr<GgufFile> g = lookup(h);
   if (!g || i < 0 || i >= static_cast<int64_t>(g->kv.size())) return 0.0;
   const GgufValue &v = g->kv[i].second;
   return (v.type == 6 || v.type == 12) ? v.f : static_cast<double>(v.i);
@@ -422,7 +431,11 @@ extern "C" int vybdq_gguf_load_slab(int64_t h, uint64_t dev, int64_t dev_bytes, 
     if (fseeko(f, static_cast<off_t>(pos), SEEK_SET) != 0) return set_error(VYBDQ_ERR_ARG, "gguf: seek failed");
     for (int64_t done = 0; done < n;) {
       const int64_t m = n - done < kChunk ? n - done : kChunk;
-      buf.resize(static_cast<size_t>(m));
+      try {
+        buf.resize(static_cast<size_t>(m));
+      } catch (const std::exception &ex) {
+        return set_error(VYBDQ_ERR_ARG, std::string("gguf: host buffer: ") + ex.what());
+      }
       if (fread(buf.data(), 1, m, f) != static_cast<size_t>(m)) return set_error(VYBDQ_ERR_ARG, "gguf: read failed");
       hipError_t e = hipMemcpyAsync(reinterpret_cast<char *>(dev) + off + done, buf.data(), m, hipMemcpyHostToDevice, s);
       if (e == hipSuccess) e = hipStreamSynchronize(s);  // the host buffer is reused

@@ -68,7 +68,7 @@ static MmPlan mm_plan(int M, int N, int S, bool allow_split, int nfx = kMmNFX, d
     }
   }
   // tuning / test override: VYBDQ_MMQ_PLAN="F,splits" (ignored when it does not fit the shape)
-  if (const char *ov = getenv("VYBDQ_MMQ_PLAN")) {
+  if (const char *ov = tuning_env("VYBDQ_MMQ_PLAN")) {
     int F = 0, splits = 1;
     if (sscanf(ov, "%d,%d", &F, &splits) >= 1 && F >= 1 && F <= 4 * nfx && F <= Ftot && splits >= 1 &&
         splits <= 8 && splits <= S && (splits == 1 || allow_split)) {

@@ -449,7 +449,7 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
   MoeWs m = moe_layout(reinterpret_cast<char *>(ws), T, H, I, E, topk);
   if (H % 256 == 0 && I % 256 == 0) {
     int MT = T > 16 ? 2 : 1;  // 16-row fragments per m-tile (VYBDQ_MOE_MT overrides: 1 or 2)
-    if (const char *e = getenv("VYBDQ_MOE_MT")) MT = atoi(e) == 1 ? 1 : 2;
+    if (const char *e = tuning_env("VYBDQ_MOE_MT")) MT = atoi(e) == 1 ? 1 : 2;
     const int n = static_cast<int>(T * topk);
     const bool shared = s_gate != 0;
     int *idx = idx_out ? reinterpret_cast<int *>(idx_out) : m.idx;
@@ -464,12 +464,12 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
     }
     // few tokens per expert: grouped GEMV (one tile per expert); else the grouped MFMA GEMM
     int gv_max = 64;  // measured crossover (T = 1..64: the GEMV path is faster)
-    if (const char *e = getenv("VYBDQ_MOE_GEMV_MAX_T")) gv_max = atoi(e);
+    if (const char *e = tuning_env("VYBDQ_MOE_GEMV_MAX_T")) gv_max = atoi(e);
     const bool gv = T <= gv_max && H / 64 <= 256 * 4 && I / 64 <= 256 * 4;
     // GEMV groups hold at most one x stage of tokens: larger experts (and the shared expert)
     // become several groups over the same weights that run side by side
     int mc = kMoeGvMC;  // tokens per GEMV group (experts with more rows: several groups)
-    if (const char *e = getenv("VYBDQ_MOE_GEMV_MC")) mc = atoi(e) < 1 ? 1 : (atoi(e) > kMoeGvMC ? kMoeGvMC : atoi(e));
+    if (const char *e = tuning_env("VYBDQ_MOE_GEMV_MC")) mc = atoi(e) < 1 ? 1 : (atoi(e) > kMoeGvMC ? kMoeGvMC : atoi(e));
     if (mc > T) mc = static_cast<int>(T);  // no group holds more rows than there are tokens
     // tiles: m-tiles of 16 MT rows for the MFMA GEMM; tiles2: groups of at most mc rows for the GEMV
     const int BMr = 16 * MT;
@@ -522,8 +522,8 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       // overrides; -1: equal ranges). Measured on H = 6144, I = 2048, 256 experts, top-8.
       const int grid_def = T <= 2 ? 0 : -2;
       int grid_env[2] = {grid_def, grid_def}, cols_env[2] = {0, 0};
-      if (const char *e = getenv("VYBDQ_MOE_GEMV_GRID")) sscanf(e, "%d,%d", &grid_env[0], &grid_env[1]);
-      if (const char *e = getenv("VYBDQ_MOE_GEMV_COLS")) sscanf(e, "%d,%d", &cols_env[0], &cols_env[1]);
+      if (const char *e = tuning_env("VYBDQ_MOE_GEMV_GRID")) sscanf(e, "%d,%d", &grid_env[0], &grid_env[1]);
+      if (const char *e = tuning_env("VYBDQ_MOE_GEMV_COLS")) sscanf(e, "%d,%d", &cols_env[0], &cols_env[1]);
       const int cus = device_cu_count();
       auto cols_for = [&](int64_t N, int cpp, int forced) {
         if (forced < 0) return 0;

@@ -241,12 +241,9 @@ int moe_gemv_launch2(const MoeGvArgs &a, int max_groups, hipStream_t s) {
   const void *fn = reinterpret_cast<const void *>(&k_moe_gemv<FMT, G, U, SWI, XW, MCMAX>);
   const size_t lds = static_cast<size_t>(a.mc) * a.P * XSTAGE_PAIR_BYTES;
   if (lds > 64 * 1024) {
-    static bool raised = false;  // one attribute call per instantiation
-    if (!raised) {
-      const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("moe gemv: LDS attribute: ") + hipGetErrorString(e));
-      raised = true;
-    }
+    static std::atomic<uint64_t> raised{0};
+    const int rc = ensure_lds_limit(fn, 160 * 1024, raised, "moe gemv");
+    if (rc) return rc;
   }
   constexpr int CPP = moe_gv_cpp(G, SWI);
   const int spg = (a.N + CPP - 1) / CPP;
@@ -260,17 +257,12 @@ int moe_gemv_launch2(const MoeGvArgs &a, int max_groups, hipStream_t s) {
   int per_cu = a.wg_per_cu;
   if (per_cu <= 0) {
     const int mult = per_cu < 0 ? -per_cu : 1;
-    // resident workgroups per CU for this LDS size (the last query per instantiation is kept)
-    static size_t q_lds = ~size_t(0);
-    static int q_nb = 0;
-    if (q_lds != lds) {
-      int nb = 0;
-      const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, 256, lds);
-      if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("moe gemv: occupancy: ") + hipGetErrorString(e));
-      q_nb = nb < 1 ? 1 : nb;
-      q_lds = lds;
-    }
-    per_cu = q_nb * mult;
+    // resident workgroups per CU for this LDS size (per device; the last size queried is kept)
+    static std::atomic<int64_t> occ[64];
+    int nb = 1;
+    const int rc = resident_per_cu(fn, 256, lds, occ, nb, "moe gemv");
+    if (rc) return rc;
+    per_cu = nb * mult;
   }
   const int64_t units = static_cast<int64_t>(max_groups) * spg;
   int64_t grid = static_cast<int64_t>(per_cu) * device_cu_count();

@@ -7,6 +7,8 @@ native/host/ridge_decode.vyb:295-328) and fills a parameter block
 All calls are asynchronous on torch's current stream and allocate only their outputs.
 """
 
+import math
+
 import torch
 
 from . import _lib
@@ -51,10 +53,39 @@ def row_bytes(ty, K):
     return (K // BLOCK_WEIGHTS[ty]) * BLOCK_BYTES[ty]
 
 
+# ---- shape checks: the C-ABI sees only pointers, so every size is checked against the tensors
+# here, before a launch could read or write past them
+
+def _nbytes(t):
+    return t.numel() * t.element_size()
+
+
+def _need(cond, msg):
+    if not cond:
+        raise ValueError(msg)
+
+
+def _check_weights(W, ty, rows, K, what="W"):
+    _need(W is not None and _nbytes(W) >= rows * row_bytes(ty, K),
+          f"{what} holds {_nbytes(W) if W is not None else 0} B, fewer than {rows} rows of {row_bytes(ty, K)} B")
+
+
+def _check_out(out, shape, what="out"):
+    _need(out.numel() == math.prod(shape), f"{what} has {out.numel()} elements, expected {tuple(shape)}")
+
+
+def _check_residual(residual, out):
+    if residual is not None:
+        _need(residual.dtype == out.dtype and residual.numel() == out.numel(),
+              "residual must have the output's dtype and shape")
+
+
 def dequant(ty, W, nblocks, out_dtype=torch.float32, order=Q4_GGML, out=None):
     """Decode nblocks packed blocks to out [nblocks*32] (the bit-exact gate path)."""
+    _need(_nbytes(W) >= nblocks * BLOCK_BYTES.get(ty, 0), "W holds fewer than nblocks blocks")
     if out is None:
         out = torch.empty(nblocks * 32, dtype=out_dtype, device=W.device)
+    _check_out(out, (nblocks * 32,))
     if ty == GGML_Q4_0:
         call("vybdq_dequant_q4_0", _ptr(W), _ptr(out), nblocks, order, _dt(out.dtype), _stream())
     elif ty == GGML_Q8_0:
@@ -66,8 +97,11 @@ def dequant(ty, W, nblocks, out_dtype=torch.float32, order=Q4_GGML, out=None):
 
 def dequant_any(ty, W, n, out_dtype=torch.float32, out=None):
     """Decode the first n weights of a packed tensor of GGML type ty (vybdq_dequant)."""
+    _need(ty in BLOCK_BYTES and n % BLOCK_WEIGHTS[ty] == 0, "n must be whole blocks of a known type")
+    _need(_nbytes(W) >= n // BLOCK_WEIGHTS[ty] * BLOCK_BYTES[ty], "W holds fewer than n weights")
     if out is None:
         out = torch.empty(n, dtype=out_dtype, device=W.device)
+    _check_out(out, (n,))
     call("vybdq_dequant", ty, _ptr(W), _ptr(out), n, _dt(out.dtype), _stream())
     return out
 
@@ -75,12 +109,17 @@ def dequant_any(ty, W, n, out_dtype=torch.float32, out=None):
 def gemv(ty, W, X, N, K, y_dtype=torch.float32, residual=None, order=Q4_GGML, out=None):
     """Y[m, n] = RS[m, n] + sum_k X[m, k] W[n, k]; X [M, K] or [K]; returns Y [M, N] or [N]."""
     squeeze = X.dim() == 1
+    _need(X.shape[-1] == K, f"X has {X.shape[-1]} columns, K = {K}")
     X2 = X.reshape(1, K) if squeeze else X
     M = X2.shape[0]
+    _need(ty in BLOCK_BYTES, f"unsupported GGUF type {ty}")
+    _check_weights(W, ty, N, K)
     if out is None:
         out = torch.empty((M, N), dtype=y_dtype, device=X.device)
+    _check_out(out, (M, N))
     if residual is not None and residual.dtype != out.dtype:
         raise TypeError("residual must have the output dtype")
+    _check_residual(residual, out)
     if ty == GGML_Q4_0:
         call("vybdq_gemv_q4_0", _ptr(W), _ptr(X2), _ptr(out), M, N, K, _dt(X2.dtype), _dt(out.dtype),
              _ptr(residual), order, _stream())
@@ -97,6 +136,10 @@ def gemv(ty, W, X, N, K, y_dtype=torch.float32, residual=None, order=Q4_GGML, ou
 
 def gemv_q4_0_seg3(X, K, segs, order=Q4_GGML):
     """Fused q4_0 GEMVs sharing X. segs: list of up to 3 (W, Y, N) with Y preallocated."""
+    _need(X.numel() == K, f"X holds {X.numel()} elements, K = {K}")
+    for i, (W, Y, N) in enumerate(segs):
+        _check_weights(W, GGML_Q4_0, N, K, f"segment {i} W")
+        _check_out(Y, (N,), f"segment {i} Y")
     args = []
     for i in range(3):
         if i < len(segs):
@@ -110,19 +153,21 @@ def gemv_q4_0_seg3(X, K, segs, order=Q4_GGML):
 def gemv_seg3(ty, X, K, segs):
     """Fused GEMVs of GGUF type ty sharing X [M, K] (or [K]) in one launch (vybdq_gemv_seg3).
     segs: up to 3 (W, Y, N) or (W, Y, N, residual) with Y preallocated [M, N] (or [N])."""
+    _need(X.shape[-1] == K, f"X has {X.shape[-1]} columns, K = {K}")
     X2 = X.reshape(1, K) if X.dim() == 1 else X
     M = X2.shape[0]
+    for i, seg in enumerate(segs):
+        W, Y, N = seg[:3]
+        RS = seg[3] if len(seg) > 3 else None
+        if N > 0:
+            _need(Y.numel() == M * N, f"segment {i}: Y holds {Y.numel()} elements, expected {M} x {N}")
+            _check_weights(W, ty, N, K, f"segment {i}: W")
+            _need(RS is None or (RS.dtype == Y.dtype and RS.numel() == Y.numel()), f"segment {i}: residual must match Y")
     args = []
     for i in range(3):
         if i < len(segs) and segs[i][2] > 0:
             W, Y, N = segs[i][:3]
             RS = segs[i][3] if len(segs[i]) > 3 else None
-            if Y.numel() != M * N:
-                raise ValueError(f"segment {i}: Y holds {Y.numel()} elements, expected {M} x {N}")
-            if W.numel() * W.element_size() < N * row_bytes(ty, K):
-                raise ValueError(f"segment {i}: W holds fewer than N rows of {row_bytes(ty, K)} B")
-            if RS is not None and (RS.dtype != Y.dtype or RS.numel() != Y.numel()):
-                raise ValueError(f"segment {i}: residual must match Y")
             args += [_ptr(W), _ptr(Y), N, _dt(Y.dtype), _ptr(RS)]
         else:
             args += [0, 0, 0, F32, 0]
@@ -138,6 +183,8 @@ def quant_q8_act(X, out=None):
         d = torch.empty((M, K // 32), dtype=torch.float32, device=X.device)
     else:
         q, d = out
+    _need(q.dtype == torch.int8 and q.numel() == M * K, "Xq must be int8 [M, K]")
+    _need(d.dtype == torch.float32 and d.numel() == M * (K // 32), "Xs must be float32 [M, K/32]")
     call("vybdq_quant_q8_act", _ptr(X2), _ptr(q), _ptr(d), M, K, _dt(X2.dtype), _stream())
     return q, d
 
@@ -149,6 +196,7 @@ def rmsnorm_q8(X, W, eps, y_dtype=None, f32_copy=False, q8=True):
     (vybdq_rmsnorm_q8). Returns (Y or None, Y32 or None, Xq or None, Xs or None)."""
     X2 = X.reshape(1, -1) if X.dim() == 1 else X
     M, N = X2.shape
+    _need(W.numel() == N and W.dtype == X2.dtype, "W must be [N] of X's dtype")
     dev = X.device
     Y = torch.empty((M, N), dtype=y_dtype, device=dev) if y_dtype is not None else None
     Y32 = torch.empty((M, N), dtype=torch.float32, device=dev) if f32_copy else None
@@ -163,6 +211,7 @@ def swiglu_q8(G, U, h_dtype=torch.float32, q8=True):
     """h = silu(G) * U elementwise with the q8 copy of float32(h) (vybdq_swiglu_q8).
     Returns (H or None, Xq or None, Xs or None)."""
     n = G.numel()
+    _need(U.numel() == n and U.dtype == G.dtype, "U must match G")
     dev = G.device
     H = torch.empty(n, dtype=h_dtype, device=dev) if h_dtype is not None else None
     Xq = torch.empty(n, dtype=torch.int8, device=dev) if q8 else None
@@ -239,6 +288,7 @@ EXL3_MCG, EXL3_3INST = _lib.EXL3_MCG, _lib.EXL3_3INST
 
 def exl3_decode_tiles(trellis, K, N, out_dtype=torch.float16, codebook=_lib.EXL3_MCG):
     """trellis uint16/int16 [K/16, N/16, 64] -> rotated-basis What [K, N]."""
+    _need(trellis.numel() == K * N // 4 and trellis.element_size() == 2, "trellis must be 16-bit [K/16, N/16, 64]")
     out = torch.empty((K, N), dtype=out_dtype, device=trellis.device)
     call("vybdq_exl3_decode_tiles", _ptr(trellis), _ptr(out), K, N, codebook, _dt(out_dtype), _stream())
     return out
@@ -246,6 +296,8 @@ def exl3_decode_tiles(trellis, K, N, out_dtype=torch.float16, codebook=_lib.EXL3
 
 def exl3_dequant(trellis, suh, svh, K, N, out_dtype=torch.float32, codebook=_lib.EXL3_MCG):
     """Full W [K, N] = diag(suh) Hs What Hs diag(svh)."""
+    _need(trellis.numel() == K * N // 4 and trellis.element_size() == 2, "trellis must be 16-bit [K/16, N/16, 64]")
+    _need(suh.numel() == K and svh.numel() == N, "suh must hold K and svh N values")
     out = torch.empty((K, N), dtype=out_dtype, device=trellis.device)
     call("vybdq_dequant_exl3", _ptr(trellis), _ptr(suh), _ptr(svh), _ptr(out), K, N, codebook,
          _dt(out_dtype), _stream())
@@ -256,6 +308,9 @@ class Exl3Linear:
     """x [B, K] -> y [B, N] through the fused EXL3 GEMM, with its workspace."""
 
     def __init__(self, trellis, suh, svh, K, N, codebook=_lib.EXL3_MCG, max_batch=16):
+        _need(trellis.numel() == K * N // 4 and trellis.element_size() == 2, "trellis must be 16-bit [K/16, N/16, 64]")
+        _need(suh.numel() == K and svh.numel() == N and suh.dtype == svh.dtype == torch.float16,
+              "suh must be fp16 [K] and svh fp16 [N]")
         self.t, self.suh, self.svh, self.K, self.N, self.cb = trellis, suh, svh, K, N, codebook
         nbytes = max(_lib.lib.vybdq_exl3_workspace_size(b, K, N) for b in (1, 2, 4, 8, max_batch))
         if nbytes < 0:
@@ -267,8 +322,10 @@ class Exl3Linear:
 
     def __call__(self, X, y_dtype=torch.float32, out=None):
         B = X.shape[0]
+        _need(X.dim() == 2 and X.shape[1] == self.K, f"X must be [B, {self.K}]")
         if out is None:
             out = torch.empty((B, self.N), dtype=y_dtype, device=X.device)
+        _check_out(out, (B, self.N))
         call("vybdq_exl3_gemm", _ptr(self.t), _ptr(self.suh), _ptr(self.svh), _ptr(X), _ptr(out), B,
              self.K, self.N, self.cb, _dt(X.dtype), _dt(out.dtype), self.ws_ptr, self.ws_bytes, _stream())
         return out
@@ -281,8 +338,13 @@ def gemm(ty, W, X, N, K, y_dtype=torch.float32, residual=None, out=None, workspa
 
     workspace: a GemmWorkspace (split-K partials) or None for the unsplit GEMM."""
     M = X.shape[0]
+    _need(X.dim() == 2 and X.shape[1] == K, f"X must be [M, {K}]")
+    _need(ty in BLOCK_BYTES, f"unsupported GGUF type {ty}")
+    _check_weights(W, ty, N, K)
     if out is None:
         out = torch.empty((M, N), dtype=y_dtype, device=X.device)
+    _check_out(out, (M, N))
+    _check_residual(residual, out)
     if workspace is None:
         call("vybdq_gemm", ty, _ptr(W), _ptr(X), _ptr(out), M, N, K, _dt(X.dtype), _dt(out.dtype), 0,
              _ptr(residual), _stream())
@@ -296,8 +358,13 @@ def gemm_q8_0_i8(W, Xq, Xs, N, K, y_dtype=torch.float32, residual=None, out=None
     """int8 path: Y [M, N] from xq8-quantized activations (Xq int8 [M, K], Xs float32 [M, K/32])
     and packed Q8_0 rows W, through int8 MFMA with per-block float32 scaling."""
     M = Xq.shape[0]
+    _need(Xq.dtype == torch.int8 and Xq.numel() == M * K, f"Xq must be int8 [M, {K}]")
+    _need(Xs.dtype == torch.float32 and Xs.numel() == M * (K // 32), f"Xs must be float32 [M, {K // 32}]")
+    _check_weights(W, GGML_Q8_0, N, K)
     if out is None:
         out = torch.empty((M, N), dtype=y_dtype, device=Xq.device)
+    _check_out(out, (M, N))
+    _check_residual(residual, out)
     ws, nb = (workspace.ptr, workspace.nbytes) if workspace is not None else (0, 0)
     call("vybdq_gemm_q8_0_i8", _ptr(W), _ptr(Xq), _ptr(Xs), _ptr(out), M, N, K, _dt(out.dtype), 0, _ptr(residual),
          ws, nb, _stream())
@@ -322,6 +389,7 @@ def router_logits(X, W, y_dtype=torch.float64):
     """Y [T, E] = X [T, H] W^T (W [E, H]) accumulated in float64 (vybdq_router_logits)."""
     T, H = X.shape
     E = W.shape[0]
+    _need(W.dim() == 2 and W.shape[1] == H, "W must be [E, H]")
     Y = torch.empty((T, E), dtype=y_dtype, device=X.device)
     call("vybdq_router_logits", _ptr(X), _dt(X.dtype), _ptr(W), _dt(W.dtype), _ptr(Y), _dt(Y.dtype), T, E, H,
          _stream())
@@ -330,6 +398,7 @@ def router_logits(X, W, y_dtype=torch.float64):
 
 def moe_route(logits, topk, bias=None, scale=2.5):
     T, E = logits.shape
+    _need(bias is None or (bias.numel() == E and bias.dtype == torch.float32), "bias must be float32 [E]")
     idx = torch.empty((T, topk), dtype=torch.int32, device=logits.device)
     w = torch.empty((T, topk), dtype=torch.float32, device=logits.device)
     call("vybdq_moe_route", _ptr(logits), _dt(logits.dtype), _ptr(bias), _ptr(idx), _ptr(w), T, E, topk,
@@ -342,6 +411,14 @@ class MoeLayer:
 
     def __init__(self, ty, w_gate, w_up, w_down, H, I, E, topk=8, shared=None, scale=2.5, limit=10.0,
                  bias=None):
+        _check_weights(w_gate, ty, E * I, H, "w_gate")
+        _check_weights(w_up, ty, E * I, H, "w_up")
+        _check_weights(w_down, ty, E * H, I, "w_down")
+        if shared:
+            _check_weights(shared[0], ty, I, H, "shared gate")
+            _check_weights(shared[1], ty, I, H, "shared up")
+            _check_weights(shared[2], ty, H, I, "shared down")
+        _need(bias is None or (bias.numel() == E and bias.dtype == torch.float32), "bias must be float32 [E]")
         self.ty, self.H, self.I, self.E, self.topk = ty, H, I, E, topk
         self.w = (w_gate, w_up, w_down)
         self.shared = shared
@@ -363,8 +440,11 @@ class MoeLayer:
         """out [T, H] for x [T, H] and logits [T, E]. noalloc: run through
         vybdq_moe_forward_noalloc (the library's per-GPU scratch instead of this layer's workspace)."""
         T = x.shape[0]
+        _need(x.dim() == 2 and x.shape[1] == self.H, f"x must be [T, {self.H}]")
+        _need(logits.dim() == 2 and tuple(logits.shape) == (T, self.E), f"logits must be [T, {self.E}]")
         if out is None:
             out = torch.empty((T, self.H), dtype=out_dtype, device=x.device)
+        _check_out(out, (T, self.H))
         idx = w = None
         if routing:
             idx = torch.empty((T, self.topk), dtype=torch.int32, device=x.device)
