@@ -59,7 +59,8 @@ struct MmArgs {
   float *part;            // split partials [tile][split][waves][NFX][MT][64][4]
   const uint8_t *W2;      // SwiGLU: the up rows (W holds the gate rows, same layout)
   float limit;            // SwiGLU clamp
-  const float *xscale;    // per output row: X row m was staged as X / xscale[m] (null: 1)
+  const float *xscale;    // per X row: X row r was staged as X / xscale[r] (null: 1); output row m
+                          // reads it at r = row_map[m] where a row map is given
 };
 
 __device__ __forceinline__ float mm_silu(float g) { return g / (1.0f + __expf(-g)); }
@@ -203,7 +204,7 @@ __device__ __forceinline__ void mm_finish(const MmArgs &a, uint32_t *last, int t
         const int m = row0 + 16 * i + 4 * g + r;
         if (m >= a.M) continue;
         const int64_t idx = static_cast<int64_t>(m) * a.ldy + n;
-        const float xs = a.xscale ? a.xscale[m] : 1.0f;
+        const float xs = a.xscale ? a.xscale[a.row_map ? a.row_map[m] : m] : 1.0f;
         float v = acc[i][f][r] * xs;
         if constexpr (SWI) {
           const float gt = fminf(v, a.limit);
@@ -504,7 +505,7 @@ __global__ void __launch_bounds__(256) k_mm_reduce(MmArgs a) {
     const int m = row0 + r;
     if (m >= a.M) continue;
     const int64_t idx = static_cast<int64_t>(m) * a.ldy + n;
-    const float v = a.xscale ? tot[r] * a.xscale[m] : tot[r];
+    const float v = a.xscale ? tot[r] * a.xscale[a.row_map ? a.row_map[m] : m] : tot[r];
     switch (a.ydt) {
       case VYBDQ_F32: store_elem<VYBDQ_F32>(a.Y, a.RS, idx, v); break;
       case VYBDQ_F16: store_elem<VYBDQ_F16>(a.Y, a.RS, idx, v); break;
@@ -521,6 +522,10 @@ int mm_reduce_launch(const MmArgs &a, hipStream_t s) {
   hipLaunchKernelGGL((k_mm_reduce<NW, MT, NFX, MH>), dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0, s, a);
   return check_launch("mmq split-K reduce");
 }
+
+// X [M][K] (f32 or bf16, 16-byte aligned, K % 8 == 0) -> xh [M][K] fp16 and xscale[M], one
+// workgroup per row (mmq_host.hip)
+int x_rows_to_f16(const void *X, int xdt, int64_t M, int64_t K, void *xh, float *xscale, hipStream_t s);
 
 template <int FMT, int XDT>
 int mmq_launch(MmArgs &a, hipStream_t s) {

@@ -144,6 +144,14 @@ __global__ void __launch_bounds__(256) k_x_to_f16(const void *__restrict__ X, u4
   }
 }
 
+int x_rows_to_f16(const void *X, int xdt, int64_t M, int64_t K, void *xh, float *xscale, hipStream_t s) {
+  u4 *o = static_cast<u4 *>(xh);
+  const unsigned grid = static_cast<unsigned>(M);
+  if (xdt == VYBDQ_BF16) hipLaunchKernelGGL(k_x_to_f16<VYBDQ_BF16>, dim3(grid), dim3(256), 0, s, X, o, xscale, K);
+  else hipLaunchKernelGGL(k_x_to_f16<VYBDQ_F32>, dim3(grid), dim3(256), 0, s, X, o, xscale, K);
+  return check_launch("x -> f16 rows");
+}
+
 static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 
 // workspace: [split partials][fp16 copy of X][X row scales]
@@ -165,10 +173,7 @@ int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   if (ws && xdt != VYBDQ_F16 && ws_bytes >= sc_off + M * 4) {
     u4 *xh = reinterpret_cast<u4 *>(static_cast<char *>(ws) + xh_off);
     float *sc = reinterpret_cast<float *>(static_cast<char *>(ws) + sc_off);
-    const unsigned grid = static_cast<unsigned>(M);
-    if (xdt == VYBDQ_BF16) hipLaunchKernelGGL(k_x_to_f16<VYBDQ_BF16>, dim3(grid), dim3(256), 0, s, X, xh, sc, K);
-    else hipLaunchKernelGGL(k_x_to_f16<VYBDQ_F32>, dim3(grid), dim3(256), 0, s, X, xh, sc, K);
-    const int rc = check_launch("mmq x->f16");
+    const int rc = x_rows_to_f16(X, xdt, M, K, xh, sc, s);
     if (rc) return rc;
     X = xh;
     xdt = VYBDQ_F16;

@@ -441,6 +441,8 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
   VYBDQ_REQUIRE(need > 0, VYBDQ_ERR_SHAPE, "unsupported T, H, I, E or topk (E <= 1024, topk <= 64)");
   VYBDQ_REQUIRE(H % 64 == 0 && I % 64 == 0, VYBDQ_ERR_SHAPE, "H and I must be multiples of 64");
   VYBDQ_REQUIRE(T * topk < (1 << 24), VYBDQ_ERR_SHAPE, "too many tokens");
+  VYBDQ_REQUIRE((T * topk + T) * (H > I ? H : I) < (int64_t(1) << 31), VYBDQ_ERR_SHAPE,
+                "too many tokens for H and I (the routed and shared rows times max(H, I) must stay below 2^31)");
   VYBDQ_REQUIRE(ws && (ws & 255) == 0 && ws_bytes >= need, VYBDQ_ERR_WORKSPACE,
                 "workspace must be 256-byte aligned and at least vybdq_moe_workspace_size bytes");
   VYBDQ_REQUIRE((x & 15) == 0 && (w_gate & 3) == 0 && (w_up & 3) == 0 && (w_down & 3) == 0, VYBDQ_ERR_ALIGN,
@@ -590,7 +592,21 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       g.W2s = reinterpret_cast<const uint8_t *>(s_up);
       g.tiles = m.tiles;
       g.ntiles = m.ntiles;
-      rc = run(x_dt, true, g);
+      int gxdt = x_dt;
+      if (x_dt != VYBDQ_F16) {
+        // f32 / bf16 x: an fp16 copy with a power-of-two scale per token, so that the GEMM streams X
+        // straight into LDS (its register path for other types waits on the X loads in issue
+        // order, which drains the weight ring every step). The copy lives in `rows`, which only
+        // the down GEMM writes, after gate|up has read it.
+        _Float16 *xh = reinterpret_cast<_Float16 *>(m.rows);
+        float *xsc = reinterpret_cast<float *>(xh + T * H);
+        rc = x_rows_to_f16(reinterpret_cast<const void *>(x), x_dt, T, H, xh, xsc, s);
+        if (rc) return rc;
+        g.m.X = xh;
+        g.m.xscale = xsc;
+        gxdt = VYBDQ_F16;
+      }
+      rc = run(gxdt, true, g);
       if (rc) return rc;
       // down -> rows [n + T][H] f32
       MoeMmArgs d = g;
@@ -600,6 +616,7 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       d.m.X = m.act;
       d.m.ldx = I;
       d.m.row_map = nullptr;
+      d.m.xscale = nullptr;
       d.m.N = static_cast<int>(H);
       d.m.S = static_cast<int>(I / 128);
       d.m.n_tiles = static_cast<int>(H / (16 * kMoeF));
