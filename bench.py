@@ -651,10 +651,25 @@ def run_moe(args, torch, dev, tokens=None, built=None):
                 bytes_per_step=nbytes, launches_per_step=R, check=check)
 
 
+def exl3_map_file():
+    """The reference's map.bin body (256 x 16-byte slots: 4 u16 nibble indices, 4 u8 positions,
+    u16 row, u16 col; native/exl3/gen_map_bin.py) followed by its u32 inverse, from the tile-slot
+    composition table kept with the test fixtures."""
+    import struct
+    with open(os.path.join(HERE, "tests", "golden", "exl3_tile_slot_composition.json")) as f:
+        slots = sorted(json.load(f)["slots"], key=lambda sl: (sl[0], sl[1]))
+    body, inv = b"", [0] * 256
+    for i, (r, c, comp) in enumerate(slots):
+        body += struct.pack("<4H4BHH", *[m for m, _ in comp], *[p for _, p in comp], r, c)
+        inv[r * 16 + c] = i
+    return body + struct.pack("<256I", *inv)
+
+
 def run_pblock(args, torch, dev):
     """vybdq_launch_pblock on the reference's parameter blocks beside the direct entry points, at the
     q4_0 GEMV 9728x2560 (f32 x, 24 rotated weight copies) and the Q8_0 prefill GEMMs M=512 (f32 X,
-    3 rotated copies of each shape, no workspace)."""
+    3 rotated copies of each shape, no workspace); then the MoE fixture block at S=16 and the fused
+    EXL3 decode + column transform at 2048x4096, which have no direct counterpart."""
     import numpy as np
     from vybforge_amd import _lib, ops, synth
     gen = torch.Generator(device=dev)
@@ -699,12 +714,44 @@ def run_pblock(args, torch, dev):
     ms_p, _ = timed_graph(torch, pblk, args.steps, args.warmup)
     out["gemm_q8_0_prefill_m512_f32x"] = dict(direct_tflops=round(flops / (ms_d * 1e-3) / 1e12, 1),
                                               pblock_tflops=round(flops / (ms_p * 1e-3) / 1e12, 1))
+    n_gemm = len(pblk)
+    del keep, direct, pblk
+    # the MoE fixture block (dense f32 expert weights, H=4096, I=2048, 288 experts, top-8) at S=16
+    S, H, I, E = 16, 4096, 2048, 288
+    mw = [torch.randn(*sh, generator=gen, device=dev) * 0.02 for sh in [(H, I), (H, I), (I, H)] * 2]
+    my = torch.randn(S, H, generator=gen, device=dev)
+    mg = torch.randn(E, H, generator=gen, device=dev) * 0.03
+    mb = torch.zeros(E, device=dev)
+    mo = [torch.empty(n, device=dev) for n in (S * E, S * 8, S * 8, S * 9 * I, S * H)]
+    words = np.array([my.data_ptr(), mg.data_ptr(), mb.data_ptr(), mo[0].data_ptr(), mo[1].data_ptr(),
+                      mo[2].data_ptr(), mo[3].data_ptr(), *[w.data_ptr() for w in mw], mo[4].data_ptr(), S], np.int64)
+    mpb = torch.from_numpy(words).to(dev)
+    ms_m, _ = timed_graph(torch, [lambda: _lib.call("vybdq_launch_pblock", _lib.PB_MOE, mpb.data_ptr(), stream())],
+                          args.steps, args.warmup)
+    mbytes = sum(w.numel() * 4 for w in mw) + mg.numel() * 4
+    out["moe_fixture_s16"] = dict(us=round(ms_m * 1e3, 2), weight_GBs=round(mbytes / (ms_m * 1e-3) / 1e9, 1))
+    del mw, mo
+    # the fused EXL3 decode + column transform (exl3dq1s) of the 2048 x 4096 down_proj the map is for
+    rows, cw = 2048, 4096
+    q = torch.randint(0, 256, ((rows // 16) * (cw // 16) * 128,), generator=gen, device=dev, dtype=torch.uint8)
+    td = torch.from_numpy(np.frombuffer(np.array([cw, rows * cw // 256], "<i8").tobytes() + exl3_map_file(),
+                                        np.uint8).copy()).to(dev)
+    Hm = torch.tensor([[1.0 if bin(r & c).count("1") % 2 == 0 else -1.0 for c in range(128)] for r in range(128)],
+                      device=dev) / 128 ** 0.5  # Sylvester Hadamard-128, orthonormal
+    T = torch.empty(rows * cw, device=dev)
+    xpb = torch.tensor([q.data_ptr(), td.data_ptr(), Hm.data_ptr(), T.data_ptr(), cw, td.data_ptr() + 16 + 4096],
+                       dtype=torch.int64, device=dev)
+    ms_x, _ = timed_graph(torch, [lambda: _lib.call("vybdq_launch_pblock_grid", _lib.PB_EXL3DQ, xpb.data_ptr(),
+                                                    rows * cw // 256, 256, stream())], args.steps, args.warmup)
+    out["exl3dq_2048x4096"] = dict(us=round(ms_x * 1e3, 2),
+                                   tflops=round(2 * rows * cw * 128 / (ms_x * 1e-3) / 1e12, 1),
+                                   out_GBs=round(rows * cw * 4 / (ms_x * 1e-3) / 1e9, 1))
     if _lib.lib.vybdq_pblock_status() != 0:
         raise CheckFailed("a p-block launch reported: " + _lib.last_error())
     ratio = out["gemv_q4_0_9728x2560"]["direct_us"] / out["gemv_q4_0_9728x2560"]["pblock_us"]
     return dict(value=ratio, unit="x", ms_step=ms_p, wall=0.0, flops=flops, roofline=out,
                 workload="vybdq_launch_pblock vs the direct entry points (GEMV 9728x2560 q4_0, Q8_0 prefill M=512)",
-                bytes_per_step=0, launches_per_step=len(pblk))
+                bytes_per_step=0, launches_per_step=n_gemm)
 
 
 def run_copy(args, torch, dev):

@@ -339,10 +339,14 @@ int vybdq_gemm_q8_0_i8(uint64_t W, uint64_t Xq, uint64_t Xs, uint64_t Y, int64_t
 
 /* ---- the reference's own parameter blocks ------------------------------------------------ */
 
-/* kind of a parameter block: one of these plus the GGML type id of W (2, 8, 12, 13, 14, 22) */
-#define VYBDQ_PB_GEMV 0x100    /* set_gemv layout (the packed GEMV kernels) */
-#define VYBDQ_PB_GEMM 0x200    /* set_gemm layout, X float32 (the gen_rpf prefill tiles) */
-#define VYBDQ_PB_GEMM_XH 0x300 /* set_gemm layout, X fp16 (the gen_rpf --xh tiles) */
+/* kind of a parameter block: GEMV / GEMM kinds plus the GGML type id of W (2, 8, 12, 13, 14, 22);
+   the MoE and EXL3 kinds take no type id */
+#define VYBDQ_PB_GEMV 0x100     /* set_gemv layout (the packed GEMV kernels) */
+#define VYBDQ_PB_GEMM 0x200     /* set_gemm layout, X float32 (the gen_rpf prefill tiles) */
+#define VYBDQ_PB_GEMM_XH 0x300  /* set_gemm layout, X fp16 (the gen_rpf --xh tiles) */
+#define VYBDQ_PB_MOE 0x400      /* moe_route + moe_act + moe_down block (native/kernels/moe.vyb) */
+#define VYBDQ_PB_EXL3DQ 0x500   /* exl3dq1 / exl3dq1s block (exl3.vyb, exl3dq.vyb); needs the grid */
+#define VYBDQ_PB_EXL3INV 0x600  /* exl3inv block (exl3.vyb) */
 
 /* Launch one GEMV or prefill GEMM described by a reference parameter block at device address P
    (8-byte aligned): little-endian int64 words, each read by the kernel when the launch runs (the
@@ -359,9 +363,26 @@ int vybdq_gemm_q8_0_i8(uint64_t W, uint64_t Xq, uint64_t Xs, uint64_t Y, int64_t
      sum_k X[s, k] W[n, k] for s < S; LDY >= N: Y float64 of row stride LDY, RS float64 or 0;
      LDY <= -N: Y float32 of row stride -LDY, RS ignored; K % 256 == 0; N % 16 == 0 (q4_0 / Q8_0) or
      N % 64 == 0 (super-block types); no K split (the block has no workspace word).
+   VYBDQ_PB_MOE, moe.vyb:15-19 (replaces the three launches of moe_driver.vyb:150-159):
+     y@0 G@8 bias@16 LG@24 IX@32 WT@40 AC@48 wg_e@56 wu_e@64 wd_e@72 wg_s@80 wu_s@88 wd_s@96
+     out@104 S@112; fixed H = 4096, I = 2048, 288 experts, top-8, dense float32 weights [in][out];
+     1 <= S <= 256; writes LG [S][288], IX [S][8] (expert ids as floats), WT [S][8],
+     AC [S][9][2048] and out [S][4096]; y, G, AC 16-byte and the other buffers 4-byte aligned.
+   VYBDQ_PB_EXL3INV, exl3.vyb:318-333: td@0 nbody@8; writes the inverse tile map
+     (u32 [256] at td + 16 + nbody).
    A block whose words violate these is not computed (nothing is written) and the next
    vybdq_pblock_status() on the device reports it; the call itself only checks kind and P. */
 int vybdq_launch_pblock(int kind, uint64_t P, uint64_t stream);
+
+/* vybdq_launch_pblock with the reference launch's grid (grid_x blocks of block_x threads), for
+   kinds whose extent is the thread count rather than a block word; other kinds ignore the grid.
+   Replaces cuda_launch4i(f, grid_x, 1, 1, block_x, 1, 1, p) (native/host/moe_driver.vyb:20).
+   VYBDQ_PB_EXL3DQ, exl3.vyb:264 / exl3dq.vyb:8-11: q@0 td@8 H@16 T@24 cw@32 invbase@40 with
+     grid_x * block_x = rows * cw threads; rows % 128 == 0, cw % 128 == 0; writes
+     T f32 [rows / 128][cw / 128][128][128] (rows % 128 * 128 + d inside a block) =
+     the map-decoded 4-bpw mcg weights of each 128-column block times H f32 [128][128],
+     summed over c ascending in float32; q, H, T 16-byte and td, inv 4-byte aligned. */
+int vybdq_launch_pblock_grid(int kind, uint64_t P, uint32_t grid_x, uint32_t block_x, uint64_t stream);
 
 /* Synchronises the current device, then returns 0 or the error of an invalid parameter block
    launched on it since the previous call (and clears it). */

@@ -55,6 +55,77 @@ def decode_window(w16, codebook=CB_MCG):
     return (lo.astype(np.float32) + hi.astype(np.float32)).astype(np.float16)
 
 
+def decode_window_f32(w16, codebook=CB_MCG):
+    """uint16 windows -> float32 lo + hi without the fp16 rounding (exl3.vyb:305-309 and
+    exl3dq.vyb:88-92: w32 = (fp16_to_f64(lo) + fp16_to_f64(hi)) as Float32; the halves never have
+    exponent 0 or 31, so the reference's inf/nan and subnormal branches are never taken)."""
+    y = hash_window(w16, codebook)
+    lo = (y & np.uint32(0xFFFF)).astype(np.uint16).view(np.float16).astype(np.float64)
+    hi = (y >> np.uint32(16)).astype(np.uint16).view(np.float16).astype(np.float64)
+    return (lo + hi).astype(np.float32)
+
+
+def tile_map_bytes(slotmap=None):
+    """The 256 x 16-byte tile-map body of map.bin (native/exl3/gen_map_bin.py:1-9, 32-37): per slot
+    in (row, col) order 4 u16 nibble indices, 4 u8 nibble positions, u16 row, u16 col, little-endian."""
+    rows, cols, nib, pos = slotmap or load_slot_composition()
+    rec = np.zeros((256, 16), np.uint8)
+    rec[:, 0:8] = nib.astype("<u2").view(np.uint8).reshape(256, 8)
+    rec[:, 8:12] = pos.astype(np.uint8)
+    rec[:, 12:14] = rows.astype("<u2").view(np.uint8).reshape(256, 2)
+    rec[:, 14:16] = cols.astype("<u2").view(np.uint8).reshape(256, 2)
+    return rec.tobytes()
+
+
+def tile_map_inverse(body):
+    """exl3inv (exl3.vyb:318-333): u32 [256], inv[row * 16 + col] = slot, from a map body."""
+    rec = np.frombuffer(body, np.uint8).reshape(256, 16)
+    r = rec[:, 12].astype(np.int64) | rec[:, 13].astype(np.int64) << 8
+    c = rec[:, 14].astype(np.int64) | rec[:, 15].astype(np.int64) << 8
+    inv = np.zeros(256, np.uint32)
+    inv[r * 16 + c] = np.arange(256, dtype=np.uint32)
+    return inv
+
+
+def map_decode_f32(q, rows, cw, body, inv):
+    """exl3dq1's phase 1 (exl3.vyb:286-309; exl3dq.vyb:60-92): the float32 weights What [rows, cw]
+    decoded through a tile map: element (row, col) takes slot inv[(row % 16) 16 + col % 16] of
+    tile (row / 16) (cw / 16) + col / 16 (128 bytes of q each) and ORs its four nibbles."""
+    q = np.frombuffer(q, np.uint8).reshape(rows // 16, cw // 16, 128)
+    rec = np.frombuffer(body, np.uint8).reshape(256, 16)
+    nidx = rec[:, 0:8].copy().view("<u2").astype(np.int64)          # [256, 4]
+    pp = rec[:, 8:12].astype(np.int64)                                # [256, 4]
+    r16, c16 = np.meshgrid(np.arange(16), np.arange(16), indexing="ij")
+    slot = np.asarray(inv, np.int64)[(r16 * 16 + c16).ravel()].reshape(16, 16)
+    w16 = np.zeros((rows // 16, cw // 16, 16, 16), np.uint32)
+    for i in range(4):
+        n = nidx[slot, i]                                             # [16, 16]
+        byte = q[:, :, n // 2].astype(np.uint32)                      # [kb, nb, 16, 16]
+        nib = (byte >> (np.uint32(4) * (n % 2).astype(np.uint32))) & np.uint32(15)
+        w16 |= nib << (np.uint32(4) * pp[slot, i].astype(np.uint32))
+    what = decode_window_f32(w16).transpose(0, 2, 1, 3).reshape(rows, cw)
+    return what
+
+
+def column_transform_f64(what, H):
+    """exl3dq1's phase 2 in float64 (exl3.vyb:310-315; exl3dq.vyb:96-112): for each 128-column
+    block, T_block = What_block @ H; returned flat in the reference's T order
+    (row / 128 * cw / 128 + col / 128) * 16384 + row % 128 * 128 + d (a half band of 64 rows
+    keeps its place inside the 128-row band)."""
+    what = np.asarray(what, np.float64)
+    rows, cw = what.shape
+    H = np.asarray(H, np.float64)
+    nbc = cw // 128
+    out = np.zeros(((rows + 127) // 128) * nbc * 16384)
+    for kb in range(0, rows, 128):
+        band = what[kb:kb + 128]
+        for nb in range(nbc):
+            blk = band[:, nb * 128:(nb + 1) * 128] @ H
+            base = (kb // 128 * nbc + nb) * 16384
+            out[base:base + blk.size] = blk.ravel()
+    return out
+
+
 def load_slot_composition(path=None):
     """Tile-slot composition: (rows[256], cols[256], nib[256,4], pos[256,4]) in (r, c) order.
 

@@ -107,3 +107,47 @@ def bucket(idx, n_experts):
     offsets = np.concatenate([[0], np.cumsum(counts)])
     order = np.argsort(flat, kind="stable")
     return counts, offsets, order
+
+
+def fixture_route(lg32, bias, topk=8, scale=SCALE):
+    """moe_route's selection and weights (native/kernels/moe.vyb:53-89) from float32 logits:
+    greedy rounds, each taking the first expert (ascending id) whose sigmoid(logit) + bias is
+    strictly above both -1e9 and every other unused choice, expert 0 when none is; weights
+    sigmoid(logit[idx]) / (sum + 1e-20) * scale summed in lane order. float64."""
+    lg = np.asarray(lg32, np.float64)
+    S, E = lg.shape
+    sc = sigmoid(lg) + np.asarray(bias, np.float64)[None, :]
+    idx = np.zeros((S, topk), np.int64)
+    for s in range(S):
+        used = np.zeros(E, bool)
+        for l in range(topk):
+            cand = np.where(used | ~(sc[s] > -1e9), -np.inf, sc[s])
+            best = int(np.argmax(cand)) if np.isfinite(cand).any() else 0
+            idx[s, l] = best
+            used[best] = True
+    raw = sigmoid(np.take_along_axis(lg, idx, axis=1))
+    tot = np.zeros(S)
+    for l in range(topk):
+        tot = tot + raw[:, l]
+    return idx, raw / (tot[:, None] + 1e-20) * scale
+
+
+def fixture_block(y, G, bias, wg_e, wu_e, wd_e, wg_s, wu_s, wd_s, topk=8, scale=SCALE,
+                  limit=SWIGLU_LIMIT):
+    """The reference's MoE fixture kernels (native/kernels/moe.vyb:1-170) in float64: weights dense
+    [in][out] (gate/up [H][I], down [I][H]); every routed lane uses the one expert (wg_e, wu_e,
+    wd_e), lane topk is the shared expert. Returns (LG float64 [S, E], idx [S, topk], w [S, topk],
+    act float64 [S, topk + 1, I], out float64 [S, H]); routing runs on float32-rounded logits
+    as the kernels store them."""
+    y = np.asarray(y, np.float64)
+    lg = y @ np.asarray(G, np.float64).T
+    idx, w = fixture_route(lg.astype(np.float32), bias, topk, scale)
+    a_e = swiglu(y @ np.asarray(wg_e, np.float64), y @ np.asarray(wu_e, np.float64), limit)
+    a_s = swiglu(y @ np.asarray(wg_s, np.float64), y @ np.asarray(wu_s, np.float64), limit)
+    act = np.concatenate([np.repeat(a_e[:, None, :], topk, axis=1), a_s[:, None, :]], axis=1)
+    part = a_e @ np.asarray(wd_e, np.float64)
+    out = np.zeros_like(part)
+    for l in range(topk):
+        out = out + w[:, l:l + 1] * part
+    out = out + a_s @ np.asarray(wd_s, np.float64)
+    return lg, idx, w, act, out

@@ -80,3 +80,18 @@ def test_moe_noalloc_size_limit_on_host():
                                             256, 8, 2.5, 10.0, 0)
     assert rc == _lib.ERR_WORKSPACE
     assert "scratch" in _lib.last_error()
+
+
+def test_pblock_preconditions_on_host():
+    """vybdq_launch_pblock / _grid reject a null or misaligned block, an unknown kind and an EXL3DQ
+    block without its grid before they touch the device."""
+    from vybforge_amd import _lib
+    L = _lib.lib
+    assert L.vybdq_launch_pblock(_lib.PB_MOE, 0, 0) == _lib.ERR_ARG
+    assert L.vybdq_launch_pblock(_lib.PB_MOE, 4100, 0) == _lib.ERR_ALIGN
+    assert L.vybdq_launch_pblock(_lib.PB_GEMV + 3, 4096, 0) == _lib.ERR_ARG
+    assert L.vybdq_launch_pblock(0x700, 4096, 0) == _lib.ERR_ARG
+    assert L.vybdq_launch_pblock(_lib.PB_EXL3DQ, 4096, 0) == _lib.ERR_ARG
+    assert "grid" in _lib.last_error()
+    assert L.vybdq_launch_pblock_grid(_lib.PB_EXL3DQ, 4096, 0, 256, 0) == _lib.ERR_SHAPE
+    assert L.vybdq_launch_pblock_grid(_lib.PB_EXL3DQ, 0, 1, 256, 0) == _lib.ERR_ARG

@@ -335,3 +335,78 @@ def test_gemv_orientation():
     x = rng.standard_normal(64)
     W = q.reshape(3, 64).astype(np.float64) - 8
     np.testing.assert_allclose(matmul.gemv_q4_0_f64(raw, x, 3, 64)[0], W @ x, rtol=1e-12)
+
+
+# ---- exl3dq1 / exl3inv (the fused decode + column transform parameter-block kinds) -------------
+
+def test_exl3_tile_map_bytes_match_reference_map_bin():
+    """The map.bin body rebuilt from the slot composition hashes to the reference's own
+    (native/exl3/map.bin, sha256 recorded beside the composition fixture)."""
+    import hashlib
+    gold = json.load(open(os.path.join(GOLDEN, "exl3_tile_slot_composition.json")))
+    assert hashlib.sha256(exl3.tile_map_bytes()).hexdigest() == gold["map_bin_body_sha256"]
+
+
+def test_exl3_window_f32_is_the_exact_half_sum():
+    """All 65536 windows: the float32 value is the exact sum of the two fp16 halves, and it rounds
+    to the pinned fp16 decode."""
+    w = np.arange(65536, dtype=np.uint32)
+    y = exl3.hash_window(w)
+    lo = (y & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float64)
+    hi = (y >> 16).astype(np.uint16).view(np.float16).astype(np.float64)
+    f = exl3.decode_window_f32(w)
+    assert np.array_equal(f.astype(np.float64), lo + hi)
+    assert np.array_equal(f.astype(np.float16), exl3.decode_window(w))
+
+
+def test_exl3_map_decode_matches_slot_decode():
+    """Decoding through the map bytes and their inverse equals the pinned slot-composition decode
+    (up to the fp16 rounding that exl3dq1 does not apply)."""
+    rng = np.random.default_rng(7)
+    rows, cw = 64, 256
+    q = rng.integers(0, 256, (rows // 16) * (cw // 16) * 128, dtype=np.uint8).tobytes()
+    body = exl3.tile_map_bytes()
+    what = exl3.map_decode_f32(q, rows, cw, body, exl3.tile_map_inverse(body))
+    trellis = np.frombuffer(q, "<u2").reshape(rows // 16, cw // 16, 64)
+    assert np.array_equal(what.astype(np.float16), exl3.decode_rotated(trellis))
+
+
+def test_exl3_column_transform_layout():
+    """Identity H returns What in the reference's T order; Hadamard H inverts by H^T / 128."""
+    rng = np.random.default_rng(8)
+    what = rng.standard_normal((192, 256))
+    t = exl3.column_transform_f64(what, np.eye(128))
+    for row, col in [(0, 0), (5, 130), (127, 255), (128, 7), (191, 200)]:
+        off = (row // 128 * 2 + col // 128) * 16384 + row % 128 * 128 + col % 128
+        assert t[off] == what[row, col]
+    H = exl3.hadamard128()
+    th = exl3.column_transform_f64(what, H)
+    blk = th[16384:2 * 16384].reshape(128, 128)   # rows 0..127, columns 128..255
+    assert np.allclose(blk @ H.T / 128.0, what[:128, 128:256], atol=1e-12)
+
+
+def test_moe_fixture_block_matches_moe_forward():
+    """The fixture semantics (one expert on every routed lane) equal the pinned moe_forward with
+    that expert for every id and the same float32-rounded logits."""
+    rng = np.random.default_rng(9)
+    S, H, I, E = 6, 64, 32, 288
+    y = rng.standard_normal((S, H))
+    G = rng.standard_normal((E, H)) * 0.2
+    b = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    ws = [rng.standard_normal(s) * 0.3 for s in [(H, I), (H, I), (I, H), (H, I), (H, I), (I, H)]]
+    lg, idx, w, act, out = moe.fixture_block(y, G, b, *ws)
+    ref, ridx, rw = moe.moe_forward(y, lg.astype(np.float32).astype(np.float64),
+                                    lambda e: (ws[0].T, ws[1].T, ws[2].T), (ws[3].T, ws[4].T, ws[5].T), bias=b)
+    assert np.array_equal(idx, ridx)
+    assert np.abs(w - rw).max() < 1e-15
+    assert np.abs(out - ref).max() <= 1e-12 * np.abs(ref).max()
+    assert np.array_equal(act[:, 0], act[:, 7])
+
+
+def test_moe_fixture_route_empty_round_takes_expert_zero():
+    """Choices at or below -1e9 never win (moe.vyb:53-74): an all-excluded token picks expert 0."""
+    lg = np.zeros((1, 288), np.float32)
+    bias = np.full(288, -2e9, np.float32)
+    bias[[5, 9]] = 0.0
+    idx, _ = moe.fixture_route(lg, bias)
+    assert idx[0, :2].tolist() == [5, 9] and (idx[0, 2:] == 0).all()

@@ -19,8 +19,9 @@ Q4_GGML, Q4_INTERLEAVED = 0, 1
 EXL3_3INST, EXL3_MCG = 0, 1
 MOE_NOALLOC_MAX_BYTES = 64 * 1024 * 1024  # VYBDQ_MOE_NOALLOC_MAX_BYTES
 PB_GEMV, PB_GEMM, PB_GEMM_XH = 0x100, 0x200, 0x300
+PB_MOE, PB_EXL3DQ, PB_EXL3INV = 0x400, 0x500, 0x600
 
-_u64, _i64, _int = ctypes.c_uint64, ctypes.c_int64, ctypes.c_int
+_u64, _i64, _int, _u32 = ctypes.c_uint64, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32
 
 # name -> argtypes (restype int unless listed in _RESTYPE)
 SIGNATURES = {
@@ -88,6 +89,7 @@ SIGNATURES = {
     "vybdq_gemm_q8_0_i8_workspace_size": [_i64, _i64, _i64],
     "vybdq_gemm_q8_0_i8": [_u64, _u64, _u64, _u64, _i64, _i64, _i64, _int, _i64, _u64, _u64, _i64, _u64],
     "vybdq_launch_pblock": [_int, _u64, _u64],
+    "vybdq_launch_pblock_grid": [_int, _u64, _u32, _u32, _u64],
     "vybdq_pblock_status": [],
     "vybdq_moe_route": [_u64, _int, _u64, _u64, _u64, _i64, _i64, _i64, ctypes.c_double, _u64],
     "vybdq_moe_workspace_size": [_i64, _i64, _i64, _i64, _i64],

@@ -59,21 +59,21 @@ __device__ __forceinline__ int ye_to_dt(int64_t ye) {
 // ref_layout: the reference's 136-byte block (x is f32, q4_0 in GGUF order; no XE / ORDER words)
 __device__ __forceinline__ StageDesc read_stage(const int64_t *pb, bool ref_layout) {
   StageDesc d;
-  d.W[0] = reinterpret_cast<const uint8_t *>(pb[0]);
-  d.X = reinterpret_cast<const void *>(pb[1]);
-  d.Y[0] = reinterpret_cast<void *>(pb[2]);
+  d.W[0] = gptr<const uint8_t>(pb[0]);
+  d.X = gptr<const void>(pb[1]);
+  d.Y[0] = gptr<void>(pb[2]);
   const int64_t n1 = pb[4];
   d.K = pb[5];
   d.ydt[0] = ye_to_dt(pb[6]);
-  d.W[1] = reinterpret_cast<const uint8_t *>(pb[7]);
+  d.W[1] = gptr<const uint8_t>(pb[7]);
   const int64_t n2 = pb[8];
-  d.Y[1] = reinterpret_cast<void *>(pb[9]);
+  d.Y[1] = gptr<void>(pb[9]);
   d.ydt[1] = ye_to_dt(pb[10]);
-  d.W[2] = reinterpret_cast<const uint8_t *>(pb[11]);
+  d.W[2] = gptr<const uint8_t>(pb[11]);
   const int64_t n3 = pb[12];
-  d.Y[2] = reinterpret_cast<void *>(pb[13]);
+  d.Y[2] = gptr<void>(pb[13]);
   d.ydt[2] = ye_to_dt(pb[14]);
-  d.RS = reinterpret_cast<const void *>(pb[15]);
+  d.RS = gptr<const void>(pb[15]);
   if (ref_layout) {
     d.xdt = VYBDQ_F32;
     d.order = VYBDQ_Q4_GGML;

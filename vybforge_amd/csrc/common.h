@@ -96,6 +96,14 @@ constexpr int DPP_ROW_SHR = 0x110;     // + n: lane i <- lane i - n of its row
 
 // ---- device: element load/store -------------------------------------------------------
 
+// A device address read from memory (a parameter-block word) as a pointer into global memory.
+// Through a plain integer-to-pointer cast the compiler cannot tell global from LDS and emits flat
+// loads, which also count against lgkmcnt: every LDS wait would then wait for them as well.
+template <class T>
+__device__ __forceinline__ T *gptr(int64_t a) {
+  return (T *)(T __attribute__((address_space(1))) *)a;
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }

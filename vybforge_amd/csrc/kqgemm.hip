@@ -295,17 +295,17 @@ __global__ void __launch_bounds__(256, 2) k_kq_gemm_pb(const int64_t *__restrict
     return;
   }
   KqArgs a{};
-  a.W = reinterpret_cast<const uint8_t *>(W);
+  a.W = gptr<const uint8_t>(W);
   a.S = static_cast<int>(K / 256);
   a.rowbytes = static_cast<int64_t>(a.S) * KqSb<FMT>::BYTES;
-  a.X = reinterpret_cast<const void *>(X);
+  a.X = gptr<const void>(X);
   a.M = static_cast<int>(M);
   a.N = static_cast<int>(N);
   a.m_tiles = static_cast<int>((M + kKqBM - 1) / kKqBM);
-  a.Y = reinterpret_cast<void *>(Y);
+  a.Y = gptr<void>(Y);
   a.ydt = LDY < 0 ? VYBDQ_F32 : VYBDQ_F64;
   a.ldy = ldy;
-  a.RS = LDY < 0 ? nullptr : reinterpret_cast<const void *>(RS);
+  a.RS = LDY < 0 ? nullptr : gptr<const void>(RS);
   const int units = a.m_tiles * (a.N / kKqBN);
   for (int u = blockIdx.x; u < units; u += gridDim.x) {
     kq_tile<FMT, XDT>(a, u % a.m_tiles, u / a.m_tiles, As, Bs);

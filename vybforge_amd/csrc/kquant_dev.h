@@ -52,9 +52,11 @@ template <> struct Fmt<FMT_Q6_K> {
   static constexpr int PAIR_DWORDS = 23;  // ql window 9 + qh window 9 + scales window 3 + d + shift
 };
 
+// p rounded down to a 4-byte boundary by pointer arithmetic (an integer round trip would lose the
+// pointer's address space, and loads through it would become flat loads)
 template <int FMT>
 __device__ __forceinline__ const uint32_t *dword_floor(const uint8_t *p) {
-  return reinterpret_cast<const uint32_t *>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(3));
+  return reinterpret_cast<const uint32_t *>(p - (reinterpret_cast<uintptr_t>(p) & 3));
 }
 
 template <int N>

@@ -26,9 +26,13 @@ namespace vybdq {
 int chain_dispatch(int wtype, uint64_t P, int nstages, int64_t pstride, int64_t maxK, uint64_t ws, int ref_layout,
                    int max_per_cu, hipStream_t s);
 int kq_gemm_pblock(int wtype, int xdt, const int64_t *pb, uint32_t *status, hipStream_t s);
+// pblock_moe.hip / pblock_exl3.hip
+int pb_moe_launch(const int64_t *pb, uint32_t *status, hipStream_t s);
+int pb_exl3dq_launch(const int64_t *pb, int64_t threads, uint32_t *status, hipStream_t s);
+int pb_exl3inv_launch(const int64_t *pb, uint32_t *status, hipStream_t s);
 
 // status word bits (word 0 of the per-device status array; word 1 is the chain's stage counter)
-constexpr uint32_t kPbWaitTimeout = 1u, kPbBadGemv = 2u, kPbBadGemm = 4u;
+constexpr uint32_t kPbWaitTimeout = 1u, kPbBadGemv = 2u, kPbBadGemm = 4u, kPbBadMoe = 8u, kPbBadExl3 = 16u;
 // largest K of a GEMV block (the chain's LDS x stage is sized for it: 48.6 KB, 3 workgroups per CU)
 constexpr int64_t kPbMaxK = 20480;
 
@@ -37,8 +41,10 @@ static __device__ __align__(256) uint32_t pb_status[64] = {0};
 namespace {
 std::mutex g_pb_mu;
 uint64_t g_pb_status[64];  // device address of pb_status per device
+}  // namespace
 
-int status_address(uint64_t &ptr) {
+// the current device's status array (hipGetSymbolAddress once per device)
+int pb_status_address(uint64_t &ptr) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
     return set_error(VYBDQ_ERR_HIP, "vybdq_launch_pblock: no current HIP device");
@@ -54,7 +60,6 @@ int status_address(uint64_t &ptr) {
   ptr = g_pb_status[dev];
   return VYBDQ_OK;
 }
-}  // namespace
 
 // The host planner's tile choice (mmq_host.hip mm_plan) without K splits, for `grid` workgroups:
 // fragments per tile F minimising rounds x super-steps x (fixed + per-fragment cycles).
@@ -95,9 +100,9 @@ __global__ void __launch_bounds__(256, 1) k_mmq_pb(const int64_t *__restrict__ p
     return;
   }
   MmArgs a{};
-  a.W = reinterpret_cast<const uint8_t *>(W);
+  a.W = gptr<const uint8_t>(W);
   a.rowbytes = (K / 32) * MmFmt<FMT>::BB;
-  a.X = reinterpret_cast<const void *>(X);
+  a.X = gptr<const void>(X);
   a.ldx = K;
   a.M = static_cast<int>(M);
   a.N = static_cast<int>(N);
@@ -106,10 +111,10 @@ __global__ void __launch_bounds__(256, 1) k_mmq_pb(const int64_t *__restrict__ p
   a.splits = 1;
   a.sps = a.S;
   a.xcd = 0;
-  a.Y = reinterpret_cast<void *>(Y);
+  a.Y = gptr<void>(Y);
   a.ydt = LDY < 0 ? VYBDQ_F32 : VYBDQ_F64;
   a.ldy = ldy;
-  a.RS = LDY < 0 ? nullptr : reinterpret_cast<const void *>(RS);
+  a.RS = LDY < 0 ? nullptr : gptr<const void>(RS);
   const int units = a.m_tiles * a.n_tiles;
   for (int u = blockIdx.x; u < units; u += gridDim.x) mmq_unit<FMT, XDT, kMmMT, kMmNFX>(a, sm, u);
 }
@@ -127,13 +132,25 @@ using namespace vybdq;
 extern "C" int vybdq_launch_pblock(int kind, uint64_t P, uint64_t stream) {
   VYBDQ_REQUIRE(P, VYBDQ_ERR_ARG, "null parameter block");
   VYBDQ_REQUIRE((P & 7) == 0, VYBDQ_ERR_ALIGN, "the parameter block must be 8-byte aligned");
+  if (kind == VYBDQ_PB_MOE || kind == VYBDQ_PB_EXL3INV) {
+    uint64_t st = 0;
+    const int rc = pb_status_address(st);
+    if (rc) return rc;
+    const auto *pb = reinterpret_cast<const int64_t *>(P);
+    auto *status = reinterpret_cast<uint32_t *>(st);
+    return kind == VYBDQ_PB_MOE ? pb_moe_launch(pb, status, as_stream(stream))
+                                : pb_exl3inv_launch(pb, status, as_stream(stream));
+  }
+  VYBDQ_REQUIRE(kind != VYBDQ_PB_EXL3DQ, VYBDQ_ERR_ARG,
+                "VYBDQ_PB_EXL3DQ takes its extent from the grid: use vybdq_launch_pblock_grid");
   const int op = kind & ~0xff, ty = kind & 0xff;
   VYBDQ_REQUIRE(op == VYBDQ_PB_GEMV || op == VYBDQ_PB_GEMM || op == VYBDQ_PB_GEMM_XH, VYBDQ_ERR_ARG,
-                "kind must be VYBDQ_PB_GEMV, VYBDQ_PB_GEMM or VYBDQ_PB_GEMM_XH plus a GGML type id");
+                "kind must be VYBDQ_PB_GEMV, VYBDQ_PB_GEMM or VYBDQ_PB_GEMM_XH plus a GGML type id, or "
+                "VYBDQ_PB_MOE, VYBDQ_PB_EXL3DQ or VYBDQ_PB_EXL3INV");
   VYBDQ_REQUIRE(ty == 2 || ty == 8 || ty == 12 || ty == 13 || ty == 14 || ty == 22, VYBDQ_ERR_ARG,
                 "the type id must be 2 (q4_0), 8 (Q8_0), 12 (Q4_K), 13 (Q5_K), 14 (Q6_K) or 22 (IQ2_S)");
   uint64_t st = 0;
-  const int rc = status_address(st);
+  const int rc = pb_status_address(st);
   if (rc) return rc;
   hipStream_t s = as_stream(stream);
   if (op == VYBDQ_PB_GEMV) return chain_dispatch(ty, P, 1, 256, kPbMaxK, st, 1, 8, s);
@@ -147,9 +164,22 @@ extern "C" int vybdq_launch_pblock(int kind, uint64_t P, uint64_t stream) {
                           : mmq_pb_launch<FMT_Q8_0, VYBDQ_F16>(pb, status, s);
 }
 
+extern "C" int vybdq_launch_pblock_grid(int kind, uint64_t P, uint32_t grid_x, uint32_t block_x, uint64_t stream) {
+  if (kind != VYBDQ_PB_EXL3DQ) return vybdq_launch_pblock(kind, P, stream);
+  VYBDQ_REQUIRE(P, VYBDQ_ERR_ARG, "null parameter block");
+  VYBDQ_REQUIRE((P & 7) == 0, VYBDQ_ERR_ALIGN, "the parameter block must be 8-byte aligned");
+  const int64_t threads = static_cast<int64_t>(grid_x) * block_x;
+  VYBDQ_REQUIRE(threads > 0, VYBDQ_ERR_SHAPE, "the grid has no threads");
+  uint64_t st = 0;
+  const int rc = pb_status_address(st);
+  if (rc) return rc;
+  return pb_exl3dq_launch(reinterpret_cast<const int64_t *>(P), threads, reinterpret_cast<uint32_t *>(st),
+                          as_stream(stream));
+}
+
 extern "C" int vybdq_pblock_status(void) {
   uint64_t st = 0;
-  const int rc = status_address(st);
+  const int rc = pb_status_address(st);
   if (rc) return rc;
   uint32_t v = 0;
   hipError_t e = hipDeviceSynchronize();
@@ -161,6 +191,9 @@ extern "C" int vybdq_pblock_status(void) {
   if (e != hipSuccess) return set_error(VYBDQ_ERR_HIP, std::string("vybdq_pblock_status: ") + hipGetErrorString(e));
   if (v & kPbBadGemv) return set_error(VYBDQ_ERR_SHAPE, "a GEMV parameter block was invalid (M != 1, K, N or pointers)");
   if (v & kPbBadGemm) return set_error(VYBDQ_ERR_SHAPE, "a GEMM parameter block was invalid (S, N, K, LDY or pointers)");
+  if (v & kPbBadMoe) return set_error(VYBDQ_ERR_SHAPE, "a MoE parameter block was invalid (S or pointers)");
+  if (v & kPbBadExl3)
+    return set_error(VYBDQ_ERR_SHAPE, "an EXL3 parameter block was invalid (cw, the grid, pointers or the tile map)");
   if (v & kPbWaitTimeout) return set_error(VYBDQ_ERR_HIP, "a GEMV parameter block launch timed out");
   return VYBDQ_OK;
 }
