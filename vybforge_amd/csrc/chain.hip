@@ -89,14 +89,17 @@ __device__ __forceinline__ StageDesc read_stage(const int64_t *pb, bool ref_layo
   return d;
 }
 
-// Lanes per row for a stage: minimise (tiles per wave) x (pairs per lane), ties -> smaller G.
-__device__ __forceinline__ int chain_pick_g(int64_t rows, int P, int nwaves) {
-  int best = 16;
-  int64_t best_cost = -1;
-  for (int G = 16; G <= 64; G *= 2) {
-    const int64_t tiles = (rows + (64 / G) - 1) / (64 / G);
-    const int64_t cost = ((tiles + nwaves - 1) / nwaves) * ((P + G - 1) / G);
-    if (best_cost < 0 || cost < best_cost) { best = G; best_cost = cost; }
+// Lanes per row for a stage (log2: 4, 5 or 6): minimise (tiles per wave) x (pairs per lane), ties ->
+// smaller G. 32-bit unsigned arithmetic (rows < 2^30): this runs at the start of every launch, before
+// the first weight load can be issued.
+__device__ __forceinline__ int chain_pick_lg(uint32_t rows, uint32_t P, uint32_t nwaves) {
+  int best = 4;
+  uint32_t best_cost = 0xffffffffu;
+#pragma unroll
+  for (int lg = 4; lg <= 6; ++lg) {
+    const uint32_t tiles = (rows + (64u >> lg) - 1) >> (6 - lg);
+    const uint32_t cost = ((tiles + nwaves - 1) / nwaves) * ((P + (1u << lg) - 1) >> lg);
+    if (cost < best_cost) { best = lg; best_cost = cost; }
   }
   return best;
 }
@@ -130,17 +133,20 @@ __global__ void __launch_bounds__(NT) k_gemv_chain(const int64_t *__restrict__ p
       segs_ok = segs_ok && (!used || (st.W[i] && st.Y[i] && (reinterpret_cast<uintptr_t>(st.W[i]) & 3) == 0));
     }
     const bool valid = segs_ok && st.K > 0 && st.K % KALIGN == 0 && st.K <= maxK && st.end[2] > 0 &&
-                       st.X && (reinterpret_cast<uintptr_t>(st.X) & 15) == 0 && pblocks[s * pstride_words + 3] == 1;
+                       st.end[2] < (int64_t(1) << 30) && st.X && (reinterpret_cast<uintptr_t>(st.X) & 15) == 0 &&
+                       pblocks[s * pstride_words + 3] == 1;
     const int64_t rows = valid ? st.end[2] : 0;
-    const int G = valid ? chain_pick_g(rows, P, nwaves) : 64;
-    const int rpt = 64 / G;  // rows per wave tile
-    const int64_t tiles = (rows + rpt - 1) / rpt;
-    const int ks = lane % G;
-    const int npl = ks < P ? (P - ks + G - 1) / G : 0;  // pairs per lane per row
+    const int lg = valid ? chain_pick_lg(static_cast<uint32_t>(rows), static_cast<uint32_t>(P),
+                                         static_cast<uint32_t>(nwaves)) : 6;
+    const int G = 1 << lg;
+    const int rpt = 64 >> lg;  // rows per wave tile
+    const int64_t tiles = (rows + rpt - 1) >> (6 - lg);
+    const int ks = lane & (G - 1);
+    const int npl = ks < P ? (P - ks + G - 1) >> lg : 0;  // pairs per lane per row
 
     // tile -> (segment, local row, row pointer); lanes past the end read row 0 of segment 0
     auto tile_row = [&](int64_t t, int &sg, int64_t &lrow, const uint8_t *&wrow, bool &act) {
-      const int64_t row = t * rpt + lane / G;
+      const int64_t row = t * rpt + (lane >> lg);
       act = row < rows;
       sg = 0;
       if (row >= st.end[0]) sg = (row >= st.end[1]) ? 2 : 1;
