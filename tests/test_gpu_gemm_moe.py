@@ -270,13 +270,24 @@ def test_moe_layer_no_shared(dev):
 
 
 @pytest.mark.parametrize("ty", [ops.GGML_Q4_0, ops.GGML_Q8_0])
-@pytest.mark.parametrize("T", [1, 7, 16, 17, 40])
+@pytest.mark.parametrize("T", [1, 7, 16, 17, 40, 48])
 @pytest.mark.parametrize("shared", [True, False])
 def test_moe_layer_grouped_mfma(dev, ty, T, shared):
-    """H and I multiples of 256: the grouped register-operand MFMA path. T <= 16 uses 16-row
-    m-tiles, larger T 32-row ones; with 8 experts and top-4 several experts get more rows than one
-    m-tile, and the shared expert is one more group over all tokens."""
+    """H and I multiples of 256: the grouped MFMA paths. q4_0: the grouped GEMV at one token, the
+    LDS-staged body with 16-row m-tiles while the experts average at most 20 rows (T <= 40 here),
+    the register-operand body with 32-row m-tiles above; Q8_0: the register-operand body, 16-row
+    m-tiles up to 16 tokens. With 8 experts and top-4 several experts get more rows than one m-tile,
+    and the shared expert is one more group over all tokens."""
     out, ref = moe_case(dev, ty, T, H=512, I=256, E=8, k=4, seed=100 + T + ty, shared=shared)
+    assert matmul.rel_maxnorm(out, ref) < TOL
+
+
+@pytest.mark.parametrize("T,mt", [(7, "1"), (17, "1"), (40, "2")])
+def test_moe_layer_q4_register_body(dev, monkeypatch, T, mt):
+    """q4_0 through the register-operand body (VYBDQ_MOE_LDS=0) at both m-tile heights."""
+    monkeypatch.setenv("VYBDQ_MOE_LDS", "0")
+    monkeypatch.setenv("VYBDQ_MOE_MT", mt)
+    out, ref = moe_case(dev, ops.GGML_Q4_0, T, H=512, I=256, E=8, k=4, seed=150 + T, shared=True)
     assert matmul.rel_maxnorm(out, ref) < TOL
 
 

@@ -450,7 +450,11 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
   hipStream_t s = as_stream(stream);
   MoeWs m = moe_layout(reinterpret_cast<char *>(ws), T, H, I, E, topk);
   if (H % 256 == 0 && I % 256 == 0) {
-    int MT = T > 16 ? 2 : 1;  // 16-row fragments per m-tile (VYBDQ_MOE_MT overrides: 1 or 2)
+    // 16-row fragments per m-tile (VYBDQ_MOE_MT overrides: 1 or 2). q4_0: 16-row tiles (the
+    // LDS-staged body) while the experts average at most 20 rows, then 32-row tiles (measured on
+    // H = 6144, I = 2048, 256 experts, top-8: 16-row tiles win up to T ~ 700). Q8_0: 32-row tiles
+    // above 16 tokens.
+    int MT = wtype == 2 ? (T * topk <= 20 * E ? 1 : 2) : (T > 16 ? 2 : 1);
     if (const char *e = tuning_env("VYBDQ_MOE_MT")) MT = atoi(e) == 1 ? 1 : 2;
     const int n = static_cast<int>(T * topk);
     const bool shared = s_gate != 0;
@@ -464,8 +468,10 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
                         topk, scale, idx, wts, s);
       if (rc) return rc;
     }
-    // few tokens per expert: grouped GEMV (one tile per expert); else the grouped MFMA GEMM
-    int gv_max = 64;  // measured crossover (T = 1..64: the GEMV path is faster)
+    // few tokens per expert: grouped GEMV (one tile per expert); else the grouped MFMA GEMM.
+    // Measured crossovers: q4_0 (LDS-staged MFMA body) the GEMV only at one token (T = 2: 2.8
+    // against 2.5 TB/s, T = 16: 4.0 against 3.0); Q8_0 the GEMV up to 64 tokens.
+    int gv_max = wtype == 2 ? 1 : 64;
     if (const char *e = tuning_env("VYBDQ_MOE_GEMV_MAX_T")) gv_max = atoi(e);
     const bool gv = T <= gv_max && H / 64 <= 256 * 4 && I / 64 <= 256 * 4;
     // GEMV groups hold at most one x stage of tokens: larger experts (and the shared expert)

@@ -4,6 +4,12 @@
 namespace vybdq {
 
 int moe_mm_q4(int xdt, int mt, bool swi, const MoeMmArgs &g, int max_tiles, hipStream_t s) {
+  // 16-row m-tiles with fp16 X (the converted tokens, the activations): the weights are staged
+  // through LDS (VYBDQ_MOE_LDS=0 under VYBDQ_TUNING keeps the register-operand body)
+  const char *e = tuning_env("VYBDQ_MOE_LDS");
+  const bool lds_off = e && e[0] == '0';
+  if (!lds_off && mt == 1 && moe_mm_lds_ok(FMT_Q4_0, xdt, swi, g))
+    return swi ? moe_mm_lds_launch<128, 1, true>(g, max_tiles, s) : moe_mm_lds_launch<128, 1, false>(g, max_tiles, s);
   if (swi) {
     switch (xdt) {
       case VYBDQ_F32: return mt == 1 ? moe_mm_launch<FMT_Q4_0, VYBDQ_F32, 1, true>(g, max_tiles, s)
