@@ -235,7 +235,8 @@ def run_stack(args, torch, dev):
     n_launch = len(launches)
     per_launch_us = ms_step * 1e3 / n_launch
     achieved = bytes_tok / n_launch / (per_launch_us * 1e-6) / 1e9
-    traffic = STACK_TRAFFIC["bytes_per_launch"] if args.config == "stack" else None
+    # the graph of launches (not the persistent chain) is what the profile's counters measured
+    traffic = STACK_TRAFFIC["bytes_per_launch"] if args.config in ("stack", "all") else None
     roofline = hbm_roofline(achieved, kernel,
                             basis="algorithmic bytes per launch / (HIP-event time of the timed replays / launches); "
                                   "the per-launch time includes the gap between dependent launches",
