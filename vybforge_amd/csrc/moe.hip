@@ -68,12 +68,11 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // equal logits prefer the lower id), and the wave maximum of the keys is taken on the VALU; the
 // double-precision sigmoid is evaluated only for the k winners, in selection order (the same
 // arithmetic as k_moe_route).
-template <int LDT>
-__device__ __forceinline__ void route_keyed(const void *__restrict__ logits, int t, int E, int topk, double scale,
-                                            int *__restrict__ idx_out, float *__restrict__ w_out,
-                                            int *__restrict__ idx_copy) {
+template <int LDT, int PER>  // PER: experts per lane, E <= 64 PER
+__device__ __forceinline__ void route_keyed_n(const void *__restrict__ logits, int t, int E, int topk, double scale,
+                                              int *__restrict__ idx_out, float *__restrict__ w_out,
+                                              int *__restrict__ idx_copy) {
   const int lane = threadIdx.x & 63;
-  constexpr int PER = 16;  // experts per lane (E <= 1024)
   uint64_t key[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
@@ -113,6 +112,16 @@ __device__ __forceinline__ void route_keyed(const void *__restrict__ logits, int
     tot += __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
   }
   if (lane < topk) w_out[t * topk + lane] = static_cast<float>(my_sc / (tot + 1e-20) * scale);
+}
+
+// the k selection rounds are serial: every key a lane scans is paid k times (E <= 1024)
+template <int LDT>
+__device__ __forceinline__ void route_keyed(const void *__restrict__ logits, int t, int E, int topk, double scale,
+                                            int *__restrict__ idx_out, float *__restrict__ w_out,
+                                            int *__restrict__ idx_copy) {
+  if (E <= 256) route_keyed_n<LDT, 4>(logits, t, E, topk, scale, idx_out, w_out, idx_copy);
+  else if (E <= 512) route_keyed_n<LDT, 8>(logits, t, E, topk, scale, idx_out, w_out, idx_copy);
+  else route_keyed_n<LDT, 16>(logits, t, E, topk, scale, idx_out, w_out, idx_copy);
 }
 
 template <int LDT>
