@@ -1,10 +1,11 @@
 """CPU oracle for the fused dequant-matmul path — TEST INFRASTRUCTURE ONLY.
 
 This package is a numpy restatement of the reference algorithms on the packed-weight
-dequant -> GEMV/GEMM path. Only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker (or the
-timed CPU baseline). The product path (``vybforge_amd`` + ``libvybdq.so``) never
-imports or calls anything here and fails loudly when the HIP library is missing.
+dequant -> GEMV/GEMM path. Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``
+(its ``cpu_baseline`` leg and the output checks after each timed region) may import it,
+and only to check results or as the timed CPU baseline, never as the thing measured.
+The product path (``vybforge_amd`` + ``libvybdq.so``) never imports or calls anything here
+and fails loudly when the HIP library is missing.
 
 Modules and the reference code each one restates (paths relative to the reference
 repository root):
