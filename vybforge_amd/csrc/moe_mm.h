@@ -163,7 +163,7 @@ __global__ void __launch_bounds__(256, (MlShape<R, MT>::PER_CU)) k_moe_mm_lds(Mo
   auto dma = [](const void *src, const void *dst) {
     const uint32_t l = __builtin_amdgcn_readfirstlane(
         static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)dst)));
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "memory", "m0");
   };
   auto issue = [&](auto bi, int st) {
     const int64_t kb = static_cast<int64_t>(st) * kMlRun;
