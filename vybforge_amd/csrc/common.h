@@ -104,6 +104,26 @@ __device__ __forceinline__ T *gptr(int64_t a) {
   return (T *)(T __attribute__((address_space(1))) *)a;
 }
 
+// Direct global -> LDS load of 16 bytes per lane: lane L's 16 bytes at src go to LDS dst + 16 L
+// (dst wave-uniform). Issued from asm, so the compiler does not track it: it inserts no waits of
+// its own for it (its direct-to-LDS bookkeeping merges conservatively at loop heads and would drain
+// every load there), the caller waits for it by vmcnt explicitly, and the compiler's own waits for
+// loads issued before it only grow longer. One wait state between the M0 write and the load.
+__device__ __forceinline__ void lds_dma16(const void *src, const void *dst) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)dst)));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "memory", "m0");
+}
+
+// The same with a wave-uniform base address (scalar registers) and a 32-bit lane byte offset: one
+// offset register per load instead of a 64-bit address pair.
+__device__ __forceinline__ void lds_dma16_s(const void *base, uint32_t off, const void *dst) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)dst)));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(l)
+               : "memory", "m0");
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }

@@ -37,7 +37,9 @@
 namespace vybdq {
 
 constexpr int kMmMT = 8;    // BM = 128
-constexpr int kMmNFX = 5;   // up to 20 fragments (320 columns) per tile
+constexpr int kMmNFX = 5;   // up to 20 fragments (320 columns) per tile, 4 waves
+constexpr int kMmNFX8 = 3;  // 8 waves: up to 24 fragments
+constexpr int kMmPartFrags = 8 * kMmNFX8 > 4 * kMmNFX ? 8 * kMmNFX8 : 4 * kMmNFX;  // split partial slots per tile
 
 typedef _Float16 hf8 __attribute__((ext_vector_type(8)));
 
@@ -66,12 +68,14 @@ struct MmArgs {
 __device__ __forceinline__ float mm_silu(float g) { return g / (1.0f + __expf(-g)); }
 
 template <int FMT> struct MmFmt;
+// D: weight super-steps in flight per lane (the register ring) with 4 waves; D8 with 8 waves
+// (half the registers per wave)
 template <> struct MmFmt<FMT_Q4_0> {
-  static constexpr int BB = 18, WD = 5, D = 4;
+  static constexpr int BB = 18, WD = 5, D = 4, D8 = 2;
   static constexpr float OFF = 1032.0f;
 };
 template <> struct MmFmt<FMT_Q8_0> {
-  static constexpr int BB = 34, WD = 9, D = 3;
+  static constexpr int BB = 34, WD = 9, D = 3, D8 = 2;
   static constexpr float OFF = 1152.0f;
 };
 
@@ -88,6 +92,23 @@ __device__ __forceinline__ void load_window(const uint8_t *p, uint32_t (&w)[WD])
     w[4 * i + 3] = t[3];
   }
   w[WD - 1] = reinterpret_cast<const uint32_t *>(p)[WD - 1];
+}
+
+// The same window as buffer loads: wave-uniform resource (base address in scalar registers) and
+// super-step offset `soff`, 32-bit lane offset `voff`; one offset register per lane and fragment,
+// where 64-bit lane pointers would take two per fragment plus their update arithmetic.
+template <int WD>
+__device__ __forceinline__ void load_window_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                                uint32_t (&w)[WD]) {
+#pragma unroll
+  for (int i = 0; i < WD / 4; ++i) {
+    const u4 t = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff + 16 * i), static_cast<int>(soff), 0);
+    w[4 * i + 0] = t[0];
+    w[4 * i + 1] = t[1];
+    w[4 * i + 2] = t[2];
+    w[4 * i + 3] = t[3];
+  }
+  w[WD - 1] = __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(voff + 4 * (WD - 1)), static_cast<int>(soff), 0);
 }
 
 // The 8 fp16 weights of step t (elements 8t .. 8t+7 of the lane's block) from its window.
@@ -223,40 +244,58 @@ __device__ __forceinline__ void mm_finish(const MmArgs &a, uint32_t *last, int t
 
 // Per-wave body for NF owned fragments (NF wave-uniform; NF = 0 waves only stage X). SWI: each
 // owned fragment is a pair, gate rows from W and the same up rows from W2 (2 NF B fragments).
-template <int FMT, int XDT, int MT, int NFX, int NF, bool SWI = false>
+template <int FMT, int XDT, int MT, int NFX, int NF, bool SWI = false, int NW = 4>
 __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, int tile, int split, int row0, int fb,
                                         int s0, int s1) {
   constexpr int WD = MmFmt<FMT>::WD;
-  constexpr int D = MmFmt<FMT>::D;
+  constexpr int D = NW == 8 ? MmFmt<FMT>::D8 : MmFmt<FMT>::D;
   constexpr int BB = MmFmt<FMT>::BB;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, nl = lane & 15;
 
   constexpr int NB = (SWI ? 2 : 1) * NF;  // B fragments per step
-  // ---- weight windows: lane (nl, g), fragment f -> row (fb + f) * 16 + nl, block 4s + g
+  // ---- weight windows: lane (nl, g), fragment f -> row (fb + f) * 16 + nl, block 4s + g, read by
+  // buffer loads: base = row fb * 16 (wave-uniform resource), super-step offset s * 4 BB (scalar),
+  // lane offset (f * 16 + nl) rows + the block's dword-aligned start (NB * 16 rows of a K < 2^25
+  // matrix stay below 2^32 bytes). Super-steps past the range re-read the last one.
+  // With 4 waves (512 registers per lane) each lane keeps 64-bit row pointers instead.
+  uint32_t loff[NB > 0 ? NB : 1];
   const uint8_t *wrow[NB > 0 ? NB : 1];
 #pragma unroll
   for (int f = 0; f < NB; ++f) {
     const int fr = f < NF ? f : f - NF;
+    loff[f] = static_cast<uint32_t>((fr * 16 + nl) * a.rowbytes) + static_cast<uint32_t>(g * BB - 2 * (g & 1));
     const int64_t n = static_cast<int64_t>(fb + fr) * 16 + nl;
     wrow[f] = (f < NF ? a.W : a.W2) + n * a.rowbytes + (g * BB - 2 * (g & 1));
   }
+  const __amdgpu_buffer_rsrc_t wr0 = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(a.W + static_cast<int64_t>(fb) * 16 * a.rowbytes), 0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t wr1 = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>((SWI ? a.W2 : a.W) + static_cast<int64_t>(fb) * 16 * a.rowbytes), 0, 0x7fffffff, 0x00020000);
   const uint32_t sel = (g & 1) ? 0x07060504u : 0x05040302u;  // quant dword j from (w[j+1], w[j])
   const uint32_t shd = (g & 1) ? 16u : 0u;
-  auto wptr = [&](int f, int s) {
+  auto wload = [&](int f, int s, uint32_t (&dst)[WD]) {
     s = s < s1 ? s : s1 - 1;
-    return wrow[f] + static_cast<int64_t>(s) * (4 * BB);
+    if constexpr (NW == 8) {
+      load_window_buf<WD>(f < NF ? wr0 : wr1, loff[f], static_cast<uint32_t>(s) * (4 * BB), dst);
+    } else {
+      load_window<WD>(wrow[f] + static_cast<int64_t>(s) * (4 * BB), dst);
+    }
   };
 
-  // ---- X chunks: thread (w, lane) stages chunk (i, t = w) for i < MT: row row0 + 16 i + nl,
-  // k = 128 s + 32 g + 8 w
-  uint32_t xoff[MT];
+  // ---- X chunks: the MT x 4 chunks (m-fragment i, step t) of a super-step are split among the
+  // NW waves: thread (w, lane) stages chunks (i = ib + j, t = w % 4) for j < XC: row
+  // row0 + 16 i + nl, k = 128 s + 32 g + 8 t
+  static_assert(NW == 4 || NW == 8, "waves per workgroup");
+  constexpr int XC = MT * 4 / NW;
+  const int xt = w & 3, ib = (w >> 2) * XC;
+  uint32_t xoff[XC];
 #pragma unroll
-  for (int i = 0; i < MT; ++i) {
-    int r = row0 + 16 * i + nl;
+  for (int j = 0; j < XC; ++j) {
+    int r = row0 + 16 * (ib + j) + nl;
     r = r < a.M ? r : a.M - 1;
     const int xr = a.row_map ? a.row_map[r] : r;
-    xoff[i] = static_cast<uint32_t>(static_cast<int64_t>(xr) * a.ldx) + 32 * g + 8 * w;
+    xoff[j] = static_cast<uint32_t>(static_cast<int64_t>(xr) * a.ldx) + 32 * g + 8 * xt;
   }
   auto xk = [&](int s) {
     s = s < s1 ? s : s1 - 1;
@@ -269,23 +308,32 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
   constexpr bool DMA = XDT == VYBDQ_F16;
   constexpr int NA = D;  // X stages in LDS (the register path uses them one stage ahead)
   static_assert(D % NA == 0, "ring slot and LDS stage advance together");
-  XChunk<XDT> xc[DMA ? 1 : MT];
+  XChunk<XDT> xc[DMA ? 1 : XC];
   auto x_dma = [&](int s, uint8_t *dst) {
     const uint32_t k = xk(s);
+    const uint16_t *xb = static_cast<const uint16_t *>(a.X) + k;
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
-      __builtin_amdgcn_global_load_lds(
-          (const void __attribute__((address_space(1))) *)(static_cast<const uint16_t *>(a.X) + xoff[i] + k),
-          (void __attribute__((address_space(3))) *)(dst + (i * 4 + w) * 1024), 16, 0, 0);
+    for (int j = 0; j < XC; ++j) {
+      uint8_t *d = dst + ((ib + j) * 4 + xt) * 1024;
+      if constexpr (NW == 8) {
+        // two ring stages: the compiler's own bookkeeping of direct-to-LDS loads would drain every
+        // load at the loop head, so these are issued untracked (the waits below are explicit)
+        lds_dma16_s(xb, 2 * xoff[j], d);
+      } else {
+        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1))) *)(xb + xoff[j]),
+                                         (void __attribute__((address_space(3))) *)d, 16, 0, 0);
+      }
+    }
   };
   auto x_regs = [&](int s) {
     const uint32_t k = xk(s);
 #pragma unroll
-    for (int i = 0; i < MT; ++i) x_load<XDT>(a.X, xoff[i] + k, xc[i]);
+    for (int j = 0; j < XC; ++j) x_load<XDT>(a.X, xoff[j] + k, xc[j]);
   };
   auto x_stage = [&](uint8_t *dst) {
 #pragma unroll
-    for (int i = 0; i < MT; ++i) *reinterpret_cast<u4 *>(dst + ((i * 4 + w) * 64 + lane) * 16) = x_to_f16<XDT>(xc[i]);
+    for (int j = 0; j < XC; ++j)
+      *reinterpret_cast<u4 *>(dst + (((ib + j) * 4 + xt) * 64 + lane) * 16) = x_to_f16<XDT>(xc[j]);
   };
   // Workgroup barrier without memory fences: each wave has already waited for the memory
   // operations the other waves depend on (its X DMA by vmcnt, its LDS stores by lgkmcnt), and
@@ -308,7 +356,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
   // Loads younger than X(s + 1) when step s ends in the steady state: W(s + 2 - NA + D), then per
   // step X(.) and W(.) for the NA - 2 steps after it. Earlier steps have at least as many, so
   // waiting for this many is safe everywhere (it may wait a little longer in the first steps).
-  constexpr int YOUNGER = (NA - 2) * (MT + NB * LPW) + NB * LPW;
+  constexpr int YOUNGER = (NA - 2) * (XC + NB * LPW) + NB * LPW;
 
   f4 acc[MT][NB > 0 ? NB : 1];
 #pragma unroll
@@ -326,18 +374,18 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
       for (int j = 0; j < D; ++j) {
         if (j < NA - 1) x_dma(s0 + j, sm.a[j]);
 #pragma unroll
-        for (int f = 0; f < NB; ++f) load_window<WD>(wptr(f, s0 + j), ring[j][f]);
+        for (int f = 0; f < NB; ++f) wload(f, s0 + j, ring[j][f]);
         __builtin_amdgcn_sched_barrier(0);
       }
-      wait_vm(std::integral_constant<int, (NA - 2) * (MT + NB * LPW) + 2 * NB * LPW < 64
-                                              ? (NA - 2) * (MT + NB * LPW) + 2 * NB * LPW : 63>{});
-      if constexpr ((NA - 2) * (MT + NB * LPW) + 2 * NB * LPW >= 64) wait_vm(std::integral_constant<int, 0>{});
+      wait_vm(std::integral_constant<int, (NA - 2) * (XC + NB * LPW) + 2 * NB * LPW < 64
+                                              ? (NA - 2) * (XC + NB * LPW) + 2 * NB * LPW : 63>{});
+      if constexpr ((NA - 2) * (XC + NB * LPW) + 2 * NB * LPW >= 64) wait_vm(std::integral_constant<int, 0>{});
     } else {
       x_regs(s0);
 #pragma unroll
       for (int d = 0; d < D; ++d) {
 #pragma unroll
-        for (int f = 0; f < NB; ++f) load_window<WD>(wptr(f, s0 + d), ring[d][f]);
+        for (int f = 0; f < NB; ++f) wload(f, s0 + d, ring[d][f]);
         __builtin_amdgcn_sched_barrier(0);
       }
       x_stage(sm.a[0]);
@@ -349,16 +397,20 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
   // are produced while the current MFMAs run
   auto compute = [&](const uint32_t (&slot)[NB > 0 ? NB : 1][WD], const uint8_t *abase) {
     if constexpr (NB > 0) {
-      hf8 af[2][MT];
+      // ABUF = 2: the A fragments of step t + 1 are read into the other buffer at the start of
+      // step t; ABUF = 1 (8 waves, 256 registers per lane): fragment i of step t + 1 is read into
+      // af[0][i] right after the last MFMA of step t that reads it
+      constexpr int ABUF = NW == 4 ? 2 : 1;
+      hf8 af[ABUF][MT];
 #pragma unroll
       for (int i = 0; i < MT; ++i) af[0][i] = *reinterpret_cast<const hf8 *>(abase + (i * 4 * 64 + lane) * 16);
       hf8 bcur = dequant_step<FMT>(slot[0], 0, sel, shd);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        if (t < 3) {
+        if (ABUF == 2 && t < 3) {
 #pragma unroll
           for (int i = 0; i < MT; ++i)
-            af[(t + 1) & 1][i] = *reinterpret_cast<const hf8 *>(abase + ((i * 4 + t + 1) * 64 + lane) * 16);
+            af[(t + 1) % ABUF][i] = *reinterpret_cast<const hf8 *>(abase + ((i * 4 + t + 1) * 64 + lane) * 16);
         }
 #pragma unroll
         for (int f = 0; f < NB; ++f) {
@@ -368,8 +420,11 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
           hf8 bnext = bcur;
           if (!last) bnext = dequant_step<FMT>(slot[fn], tn, sel, shd);
 #pragma unroll
-          for (int i = 0; i < MT; ++i)
-            acc[i][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t & 1][i], bcur, acc[i][f], 0, 0, 0);
+          for (int i = 0; i < MT; ++i) {
+            acc[i][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t % ABUF][i], bcur, acc[i][f], 0, 0, 0);
+            if (ABUF == 1 && t < 3 && f == NB - 1)
+              af[0][i] = *reinterpret_cast<const hf8 *>(abase + ((i * 4 + t + 1) * 64 + lane) * 16);
+          }
           bcur = bnext;
         }
       }
@@ -387,7 +442,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
     if constexpr (decltype(refill)::value) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int f = 0; f < NB; ++f) load_window<WD>(wptr(f, s + D), ring[d][f]);
+      for (int f = 0; f < NB; ++f) wload(f, s + D, ring[d][f]);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (DMA) wait_vm(std::integral_constant<int, YOUNGER>{});
     } else {
@@ -419,11 +474,12 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
     if (s + 2 < s1) step(I2{}, No{}, s + 2);
   }
 
-  mm_finish<MT, NFX, NF, 4, SWI>(a, sm.last, tile, split, row0, fb, acc);
+  mm_finish<MT, NFX, NF, NW, SWI>(a, sm.last, tile, split, row0, fb, acc);
 }
 
-// One work unit (m-tile, n-tile, K split) of the GEMM; every wave of the workgroup calls it.
-template <int FMT, int XDT, int MT, int NFX>
+// One work unit (m-tile, n-tile, K split) of the GEMM; every wave of the workgroup calls it. The
+// tile's F fragments are split among the NW waves (F / NW each, the first F % NW waves one more).
+template <int FMT, int XDT, int MT, int NFX, int NW = 4>
 __device__ __forceinline__ void mmq_unit(const MmArgs &a, const MmLds<MT> &sm, int id) {
   const int mt = id % a.m_tiles;
   const int rest = id / a.m_tiles;
@@ -433,7 +489,7 @@ __device__ __forceinline__ void mmq_unit(const MmArgs &a, const MmLds<MT> &sm, i
   const int s0 = split * a.sps;
   const int s1 = s0 + a.sps < a.S ? s0 + a.sps : a.S;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int Fq = a.F >> 2, Fr = a.F & 3;
+  const int Fq = a.F / NW, Fr = a.F % NW;
   const int fb = ntile * a.F + w * Fq + (w < Fr ? w : Fr);
   int nf = Fq + (w < Fr ? 1 : 0);
   const int left = (a.N >> 4) - fb;
@@ -441,12 +497,12 @@ __device__ __forceinline__ void mmq_unit(const MmArgs &a, const MmLds<MT> &sm, i
   const int row0 = mt * 16 * MT;
   static_assert(NFX <= 5, "fragment variants");
   switch (nf) {
-    case 5: if constexpr (NFX >= 5) mm_body<FMT, XDT, MT, NFX, 5>(a, sm, tile, split, row0, fb, s0, s1); break;
-    case 4: if constexpr (NFX >= 4) mm_body<FMT, XDT, MT, NFX, 4>(a, sm, tile, split, row0, fb, s0, s1); break;
-    case 3: mm_body<FMT, XDT, MT, NFX, 3>(a, sm, tile, split, row0, fb, s0, s1); break;
-    case 2: mm_body<FMT, XDT, MT, NFX, 2>(a, sm, tile, split, row0, fb, s0, s1); break;
-    case 1: mm_body<FMT, XDT, MT, NFX, 1>(a, sm, tile, split, row0, fb, s0, s1); break;
-    default: mm_body<FMT, XDT, MT, NFX, 0>(a, sm, tile, split, row0, fb, s0, s1); break;
+    case 5: if constexpr (NFX >= 5) mm_body<FMT, XDT, MT, NFX, 5, false, NW>(a, sm, tile, split, row0, fb, s0, s1); break;
+    case 4: if constexpr (NFX >= 4) mm_body<FMT, XDT, MT, NFX, 4, false, NW>(a, sm, tile, split, row0, fb, s0, s1); break;
+    case 3: if constexpr (NFX >= 3) mm_body<FMT, XDT, MT, NFX, 3, false, NW>(a, sm, tile, split, row0, fb, s0, s1); break;
+    case 2: mm_body<FMT, XDT, MT, NFX, 2, false, NW>(a, sm, tile, split, row0, fb, s0, s1); break;
+    case 1: mm_body<FMT, XDT, MT, NFX, 1, false, NW>(a, sm, tile, split, row0, fb, s0, s1); break;
+    default: mm_body<FMT, XDT, MT, NFX, 0, false, NW>(a, sm, tile, split, row0, fb, s0, s1); break;
   }
 }
 
@@ -459,13 +515,13 @@ __device__ __forceinline__ void mmq_unit(const MmArgs &a, const MmLds<MT> &sm, i
   __shared__ uint32_t last;                                                           \
   const MmLds<MT> sm{{a0, a1, a2, a3}, &last}
 
-template <int FMT, int XDT, int MT, int NFX>
-__global__ void __launch_bounds__(256, 1) k_mmq(MmArgs a) {
+template <int FMT, int XDT, int MT, int NFX, int NW = 4>
+__global__ void __launch_bounds__(64 * NW, 1) k_mmq(MmArgs a) {
   VYBDQ_MMQ_LDS(FMT, MT);
   const int units = a.m_tiles * a.n_tiles * a.splits;
   int id = blockIdx.x;
   if (a.xcd) id = (blockIdx.x & 7) * (units >> 3) + (blockIdx.x >> 3);
-  mmq_unit<FMT, XDT, MT, NFX>(a, sm, id);
+  mmq_unit<FMT, XDT, MT, NFX, NW>(a, sm, id);
 }
 
 // Split-K reduction: Y = RS + sum over splits (in split order) of the partial tiles, one float4
@@ -487,9 +543,10 @@ __global__ void __launch_bounds__(256) k_mm_reduce(MmArgs a) {
   const int f = e % NFX;
   const int w = e / NFX;
   const int mt = tile % a.m_tiles, ntile = tile / a.m_tiles;
-  const int q = w % (NW / MH);  // fragment quarter of this wave
-  const int mh = w / (NW / MH);
-  const int Fq = a.F >> 2, Fr = a.F & 3;
+  constexpr int NQ = NW / MH;  // fragment groups
+  const int q = w % NQ;         // fragment group of this wave
+  const int mh = w / NQ;
+  const int Fq = a.F / NQ, Fr = a.F % NQ;
   const int fb = ntile * a.F + q * Fq + (q < Fr ? q : Fr);
   int nf = Fq + (q < Fr ? 1 : 0);
   const int left = (a.N >> 4) - fb;
@@ -527,10 +584,24 @@ int mm_reduce_launch(const MmArgs &a, hipStream_t s) {
 // workgroup per row (mmq_host.hip)
 int x_rows_to_f16(const void *X, int xdt, int64_t M, int64_t K, void *xh, float *xscale, hipStream_t s);
 
+// fp16 X (streamed into LDS by direct loads): 8 waves per workgroup, two per SIMD, so that one
+// wave's dequantization issues while the other's MFMAs run; every wave owns at most kMmNFX8
+// fragments (F <= 4 kMmNFX = 8 kMmNFX8 - 4). Other X types: 4 waves (the register X path needs the
+// registers of one wave per SIMD).
 template <int FMT, int XDT>
 int mmq_launch(MmArgs &a, hipStream_t s) {
   const int64_t units = static_cast<int64_t>(a.m_tiles) * a.n_tiles * a.splits;
   a.xcd = units % 8 == 0 ? 1 : 0;
+  bool eight = XDT == VYBDQ_F16;
+  if (const char *e = tuning_env("VYBDQ_MMQ_WAVES")) eight = eight && e[0] != '4';
+  if constexpr (XDT == VYBDQ_F16) {
+    if (eight) {
+      hipLaunchKernelGGL((k_mmq<FMT, XDT, kMmMT, kMmNFX8, 8>), dim3(static_cast<unsigned>(units)), dim3(512), 0, s, a);
+      const int rc = check_launch("mmq gemm");
+      if (rc) return rc;
+      return mm_reduce_launch<8, kMmMT, kMmNFX8, 1>(a, s);
+    }
+  }
   hipLaunchKernelGGL((k_mmq<FMT, XDT, kMmMT, kMmNFX>), dim3(static_cast<unsigned>(units)), dim3(256), 0, s, a);
   const int rc = check_launch("mmq gemm");
   if (rc) return rc;

@@ -24,7 +24,7 @@ struct MmPlan {
 };
 
 static int64_t mm_part_bytes(int64_t tiles, int splits) {
-  return tiles * splits * 4LL * kMmNFX * kMmMT * 64 * 4 * 4;
+  return tiles * splits * static_cast<int64_t>(kMmPartFrags) * kMmMT * 64 * 4 * 4;
 }
 
 // Tiling: pick fragments per tile F and the K split that minimise an estimate of the run time:
