@@ -86,8 +86,9 @@ static MmPlan mm_plan(int M, int N, int S, bool allow_split, int nfx = kMmNFX, d
   return best;
 }
 
+// K < 2^24: the 8-wave body addresses a wave's weight rows by 32-bit offsets
 bool mmq_supported(int64_t M, int64_t N, int64_t K) {
-  return M >= 1 && K % 256 == 0 && N % 16 == 0 && N >= 16 && M * K < (int64_t(1) << 31);
+  return M >= 1 && K % 256 == 0 && K < (int64_t(1) << 24) && N % 16 == 0 && N >= 16 && M * K < (int64_t(1) << 31);
 }
 
 // X -> fp16 copy, one workgroup per row: the row's largest |x| is brought into [2^14, 2^15) by a
@@ -95,38 +96,28 @@ bool mmq_supported(int64_t M, int64_t N, int64_t K) {
 // the scaled row is rounded to fp16 (bf16 values exactly, f32 to nearest even) and 2^e goes to
 // xscale[row], which the GEMM epilogue multiplies back: activations of any magnitude neither
 // overflow nor flush to zero. The GEMM then streams the fp16 copy straight into LDS.
-template <int XDT>
+// CH > 0: the row (at most 256 CH chunks of 8) is loaded once into registers, all loads issued
+// before the first use; CH = 0: two passes over the row (any K).
+template <int XDT, int CH>
 __global__ void __launch_bounds__(256) k_x_to_f16(const void *__restrict__ X, u4 *__restrict__ Xh,
                                                   float *__restrict__ xscale, int64_t K) {
   __shared__ float wmax[4];
   const int64_t row = blockIdx.x;
   const int64_t n8 = K / 8;
-  float amax = 0.f;
-  for (int64_t i = threadIdx.x; i < n8; i += 256) {
-    XChunk<XDT> c;
-    x_load<XDT>(X, static_cast<uint32_t>(row * K + i * 8), c);
+  auto chunk_max = [](const XChunk<XDT> &c, float m) {
     if constexpr (XDT == VYBDQ_F32) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(__uint_as_float(c.r[j >> 2][j & 3])));
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(__uint_as_float(c.r[j >> 2][j & 3])));
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t v = c.r[j];
-        amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(v << 16)), fabsf(__uint_as_float(v & 0xffff0000u))));
+        m = fmaxf(m, fmaxf(fabsf(__uint_as_float(v << 16)), fabsf(__uint_as_float(v & 0xffff0000u))));
       }
     }
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  float inv;
-  const float scale = block_scale(amax, inv);
-  if (threadIdx.x == 0) xscale[row] = scale;
-  for (int64_t i = threadIdx.x; i < n8; i += 256) {
-    XChunk<XDT> c;
-    x_load<XDT>(X, static_cast<uint32_t>(row * K + i * 8), c);
+    return m;
+  };
+  auto chunk_f16 = [](const XChunk<XDT> &c, float inv) {
     u4 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -140,15 +131,64 @@ __global__ void __launch_bounds__(256) k_x_to_f16(const void *__restrict__ X, u4
       }
       o[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(a * inv), static_cast<_Float16>(b * inv)});
     }
-    Xh[row * n8 + i] = o;
+    return o;
+  };
+  float amax = 0.f;
+  XChunk<XDT> cc[CH > 0 ? CH : 1];
+  if constexpr (CH > 0) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int64_t i = threadIdx.x + 256 * j;
+      if (i < n8) x_load<XDT>(X, static_cast<uint32_t>(row * K + i * 8), cc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < CH; ++j)
+      if (threadIdx.x + 256 * j < n8) amax = chunk_max(cc[j], amax);
+  } else {
+    for (int64_t i = threadIdx.x; i < n8; i += 256) {
+      XChunk<XDT> c;
+      x_load<XDT>(X, static_cast<uint32_t>(row * K + i * 8), c);
+      amax = chunk_max(c, amax);
+    }
   }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  float inv;
+  const float scale = block_scale(amax, inv);
+  if (threadIdx.x == 0) xscale[row] = scale;
+  if constexpr (CH > 0) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int64_t i = threadIdx.x + 256 * j;
+      if (i < n8) Xh[row * n8 + i] = chunk_f16(cc[j], inv);
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < n8; i += 256) {
+      XChunk<XDT> c;
+      x_load<XDT>(X, static_cast<uint32_t>(row * K + i * 8), c);
+      Xh[row * n8 + i] = chunk_f16(c, inv);
+    }
+  }
+}
+
+template <int XDT>
+static void x_to_f16_launch(const void *X, u4 *o, float *xscale, int64_t M, int64_t K, hipStream_t s) {
+  const unsigned grid = static_cast<unsigned>(M);
+  const int64_t per = (K / 8 + 255) / 256;  // chunks per thread
+  if (per <= 2) hipLaunchKernelGGL((k_x_to_f16<XDT, 2>), dim3(grid), dim3(256), 0, s, X, o, xscale, K);
+  else if (per <= 4) hipLaunchKernelGGL((k_x_to_f16<XDT, 4>), dim3(grid), dim3(256), 0, s, X, o, xscale, K);
+  else if (per <= 8) hipLaunchKernelGGL((k_x_to_f16<XDT, 8>), dim3(grid), dim3(256), 0, s, X, o, xscale, K);
+  else if (per <= 12) hipLaunchKernelGGL((k_x_to_f16<XDT, 12>), dim3(grid), dim3(256), 0, s, X, o, xscale, K);
+  else hipLaunchKernelGGL((k_x_to_f16<XDT, 0>), dim3(grid), dim3(256), 0, s, X, o, xscale, K);
 }
 
 int x_rows_to_f16(const void *X, int xdt, int64_t M, int64_t K, void *xh, float *xscale, hipStream_t s) {
   u4 *o = static_cast<u4 *>(xh);
-  const unsigned grid = static_cast<unsigned>(M);
-  if (xdt == VYBDQ_BF16) hipLaunchKernelGGL(k_x_to_f16<VYBDQ_BF16>, dim3(grid), dim3(256), 0, s, X, o, xscale, K);
-  else hipLaunchKernelGGL(k_x_to_f16<VYBDQ_F32>, dim3(grid), dim3(256), 0, s, X, o, xscale, K);
+  if (xdt == VYBDQ_BF16) x_to_f16_launch<VYBDQ_BF16>(X, o, xscale, M, K, s);
+  else x_to_f16_launch<VYBDQ_F32>(X, o, xscale, M, K, s);
   return check_launch("x -> f16 rows");
 }
 
