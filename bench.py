@@ -475,7 +475,8 @@ def run_prefill(args, torch, dev):
         check = dict(ok=True, rel=max(rels), what="last copy of each shape, 512 rows x first 256 columns, float64 oracle")
     roofline = dict(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s",
                     frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), traffic=None,
-                    kernel="k_mmq<Q8_0,bf16> (fp16 MFMA 16x16x32, weights dequantized into operand registers)",
+                    kernel="k_mmq<Q8_0, fp16 X, 8 waves> (bf16 X converted once per GEMM; fp16 MFMA 16x16x32, "
+                           "weights dequantized into operand registers)",
                     basis="flops per step / event time", avg_launch_us=round(per * 1e3, 3),
                     flops_per_launch=flops // len(launches))
     return dict(value=tflops, unit="TFLOP/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
