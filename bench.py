@@ -493,19 +493,25 @@ def run_prefill_kq(args, torch, dev):
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed + 6)
     launches, flops, nbytes = [], 0, 0
+    # Q4_K uses the workspace (bf16 X converted once, the register-operand body); the other types
+    # decode their tiles into LDS and take none
+    ws = ops.GemmWorkspace([(M, N, K) for N, K in PREFILL_SHAPES], dev, ty)
+    wsa = ws if ws.nbytes else None
     for N, K in PREFILL_SHAPES:
         x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
         y = torch.empty(M, N, device=dev)
         for _ in range(3):
             W = kquant_blocks_gpu(torch, gen, ty, N, K, dev)
-            launches.append(lambda W=W, x=x, y=y, N=N, K=K: ops.gemm(ty, W, x, N, K, out=y))
+            launches.append(lambda W=W, x=x, y=y, N=N, K=K: ops.gemm(ty, W, x, N, K, out=y, workspace=wsa))
             flops += 2 * M * N * K
             nbytes += ops.row_bytes(ty, K) * N + 2 * M * K + 4 * M * N
     ms, wall = timed_graph(torch, launches, args.steps, args.warmup)
     tflops = flops / (ms * 1e-3) / 1e12
     roofline = dict(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s",
                     frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), traffic=None,
-                    kernel=f"k_kq_gemm<{name}> (units decoded to fp16 in LDS, fp16 MFMA 16x16x32)",
+                    kernel=(f"k_mmq<{name}, fp16 X, 8 waves> (bf16 X converted once per GEMM; weights dequantized "
+                            "into operand registers, super-block heads staged in LDS)" if ty == 12 else
+                            f"k_kq_gemm<{name}> (units decoded to fp16 in LDS, fp16 MFMA 16x16x32)"),
                     basis="flops per step / event time", avg_launch_us=round(ms * 1e3 / len(launches), 3))
     return dict(value=tflops, unit="TFLOP/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
                 workload=f"{name} prefill GEMMs M=512: 5120->17408 and 17408->5120 (bf16 X, f32 Y)",

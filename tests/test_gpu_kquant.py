@@ -237,3 +237,62 @@ def test_gemv_activation_range(dev, ty, kind, xdt, M):
     ref = matmul.gemm_rows_f64(x64.reshape(M, K), _rows(ty, raw, N, K))
     assert np.all(np.isfinite(y))
     assert matmul.rel_maxnorm(y, ref) < TOL
+
+
+def _gemm_ws(ty, W, xd, N, K, dev):
+    M = xd.shape[0]
+    ws = ops.GemmWorkspace([(M, N, K)], dev, ty)
+    assert ws.nbytes > 0 or xd.dtype == torch.float16
+    return ops.gemm(ty, W, xd, N, K, workspace=ws)
+
+
+@pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 17408)])
+def test_gemm_q4k_register_body_prefill_shape(dev, N, K):
+    """Q4_K at the prefill shapes through vybdq_gemm_ws (bf16 X converted once into the workspace,
+    the 8-wave tile body with the weights dequantized into the MFMA operand registers and the
+    super-block heads staged in LDS; 17408 -> 5120 splits K): 256 columns of the first and the
+    last weight tiles against the float64 oracle."""
+    ty, M = ops.GGML_Q4_K, 512
+    rng = np.random.default_rng(N + 7)
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = torch.from_numpy(synth.activations(rng, (M, K))).to(torch.bfloat16)
+    y = _gemm_ws(ty, to_dev(raw, dev), x.to(dev), N, K, dev).cpu().numpy()
+    x64 = x.to(torch.float64).numpy()
+    rb = BLOCK[ty] * (K // 256)
+    for c0 in (0, N - 256):
+        wrows = matrix_ref(ty, raw[c0 * rb:(c0 + 256) * rb], 256, K)
+        assert matmul.rel_maxnorm(y[:, c0:c0 + 256], matmul.gemm_rows_f64(x64, wrows)) < TOL, c0
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 64, 256), (100, 320, 512), (130, 1088, 768), (200, 256, 16384),
+                                   (513, 2112, 2560)])
+@pytest.mark.parametrize("xdt", ["f16", "bf16_ws", "f32_ws"])
+def test_gemm_q4k_register_body_edges(dev, M, N, K, xdt):
+    """The Q4_K register-operand body: partial m-tiles (100, 130, 513 rows), a partial last n-tile,
+    odd super-step counts per split (K = 768), a long K that splits (16384), fp16 X directly and
+    bf16 / f32 X through the workspace; every output against the float64 oracle."""
+    ty = ops.GGML_Q4_K
+    rng = np.random.default_rng(M + N + K)
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = synth.activations(rng, (M, K))
+    xd, x64 = x_as(x, xdt.split("_")[0], dev)
+    W = to_dev(raw, dev)
+    y = (_gemm_ws(ty, W, xd.reshape(M, K), N, K, dev) if xdt.endswith("_ws")
+         else ops.gemm(ty, W, xd.reshape(M, K), N, K)).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x64.reshape(M, K), matrix_ref(ty, raw, N, K))
+    assert matmul.rel_maxnorm(y, ref) < TOL
+
+
+@pytest.mark.parametrize("kind", ["outlier", "offset", "fp16_limit", "tiny", "huge"])
+def test_gemm_q4k_register_body_activation_range(dev, kind):
+    """f32 X of any magnitude through the workspace: each row is converted to fp16 after a
+    power-of-two scale that is multiplied back into its outputs."""
+    ty, M, N, K = ops.GGML_Q4_K, 128, 512, 2560
+    kinds = ["outlier", "offset", "fp16_limit", "tiny", "huge"]
+    rng = np.random.default_rng(300 + kinds.index(kind))
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = _x_pattern(kind, rng, M, K)
+    y = _gemm_ws(ty, to_dev(raw, dev), to_dev(x, dev), N, K, dev).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x.astype(np.float64), matrix_ref(ty, raw, N, K))
+    assert np.all(np.isfinite(y))
+    assert matmul.rel_maxnorm(y, ref) < TOL

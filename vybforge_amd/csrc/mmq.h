@@ -71,13 +71,60 @@ template <int FMT> struct MmFmt;
 // D: weight super-steps in flight per lane (the register ring) with 4 waves; D8 with 8 waves
 // (half the registers per wave)
 template <> struct MmFmt<FMT_Q4_0> {
-  static constexpr int BB = 18, WD = 5, D = 4, D8 = 2;
+  static constexpr int BB = 18, WD = 5, D = 4, D8 = 2, SB = 0;
   static constexpr float OFF = 1032.0f;
 };
 template <> struct MmFmt<FMT_Q8_0> {
-  static constexpr int BB = 34, WD = 9, D = 3, D8 = 2;
+  static constexpr int BB = 34, WD = 9, D = 3, D8 = 2, SB = 0;
   static constexpr float OFF = 1152.0f;
 };
+// Q4_K: 144-byte super-blocks of 256 (d, dmin, 12 scale bytes, 128 nibble bytes); a 128-k super-step
+// is half a super-block. A lane's window: the 32 nibble bytes of its sub-block's pair (sub-block
+// j = 4 (s & 1) + g: low nibbles of qs[32 (j / 2) ..] for even j, high for odd). The 16-byte
+// heads (d, dmin, scales) of the tile's rows go to LDS with the X stage (one direct load per wave
+// and step), so the register ring holds only the nibbles.
+template <> struct MmFmt<FMT_Q4_K> {
+  static constexpr int BB = 0, WD = 8, D = 3, D8 = 2, SB = 144;
+  static constexpr float OFF = 0.0f;
+};
+
+// Q4_K sub-block j = 4 odd + g of the super-block with head hd: fp16(d * sc) and fp16(dmin * m) (the
+// products in float32, get_scale_min_k4), packed as (ds, -dm). Both 6-bit forms are extracted and
+// one is selected, so the wave-uniform parity costs no branch.
+__device__ __forceinline__ uint32_t q4k_scales(const u4 hd, int g, bool odd) {
+  const uint32_t o = 8u * static_cast<uint32_t>(g);
+  const uint32_t a0 = __builtin_amdgcn_ubfe(hd[1], o, 6), b0 = __builtin_amdgcn_ubfe(hd[2], o, 6);
+  const uint32_t a1 = __builtin_amdgcn_ubfe(hd[3], o, 4) | (__builtin_amdgcn_ubfe(hd[1], o + 6, 2) << 4);
+  const uint32_t b1 = __builtin_amdgcn_ubfe(hd[3], o + 4, 4) | (__builtin_amdgcn_ubfe(hd[2], o + 6, 2) << 4);
+  const float sc = static_cast<float>(odd ? a1 : a0), mn = static_cast<float>(odd ? b1 : b0);
+  return __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(half_bits_to_f32(hd[0] & 0xffffu) * sc),
+                                         static_cast<_Float16>(-(half_bits_to_f32(hd[0] >> 16) * mn))});
+}
+
+// The 8 fp16 weights of step t (elements 8t .. 8t+7 of the lane's sub-block; sh = 4 for the high
+// nibbles): q exact in fp16 (0x64vv - 1024), then one fp16 fma q * ds - dm. (The decode and the
+// super-block GEMM round the float32 value of the same expression once to fp16; this differs from
+// it by the fp16 rounding of ds and dm, within one fp16 ulp of the weight's scale.)
+__device__ __forceinline__ _Float16 __attribute__((ext_vector_type(8))) q4k_step(const uint32_t (&w)[8], int t,
+                                                                                 uint32_t sh, uint32_t sd) {
+  const h2 v2 = __builtin_bit_cast(h2, sd);
+  const h2 ds = {v2[0], v2[0]}, ndm = {v2[1], v2[1]};
+  const h2 k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+  _Float16 __attribute__((ext_vector_type(8))) r;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t v = (w[2 * t + h] >> sh) & 0x0F0F0F0Fu;
+    const h2 q0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, v, SEL_B01)) - k1024;
+    const h2 q1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, v, SEL_B23)) - k1024;
+    const h2 p0 = __builtin_elementwise_fma(q0, ds, ndm);
+    const h2 p1 = __builtin_elementwise_fma(q1, ds, ndm);
+    r[4 * h + 0] = p0[0];
+    r[4 * h + 1] = p0[1];
+    r[4 * h + 2] = p1[0];
+    r[4 * h + 3] = p1[1];
+  }
+  return r;
+}
 
 // a WD-dword window starting at a 4-byte-aligned address
 template <int WD>
@@ -191,6 +238,7 @@ template <int MT>
 struct MmLds {
   uint8_t *a[4];
   uint32_t *last;
+  uint8_t *h[4];  // Q4_K: the super-block heads of the tile's rows, one stage per X stage
 };
 
 // Split-K reduction (when the tile's super-steps were split) and the epilogue store of one wave's
@@ -259,15 +307,20 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
   // lane offset (f * 16 + nl) rows + the block's dword-aligned start (NB * 16 rows of a K < 2^25
   // matrix stay below 2^32 bytes). Super-steps past the range re-read the last one.
   // With 4 waves (512 registers per lane) each lane keeps 64-bit row pointers instead.
+  // Q4_K (KQ): the lane offset is the row start; the head and the nibble run are placed per step.
+  constexpr bool KQ = FMT == FMT_Q4_K;
+  static_assert(!KQ || !SWI, "super-block rows: plain GEMM only");
+  const int lane_blk = KQ ? 0 : g * BB - 2 * (g & 1);
   uint32_t loff[NB > 0 ? NB : 1];
   const uint8_t *wrow[NB > 0 ? NB : 1];
 #pragma unroll
   for (int f = 0; f < NB; ++f) {
     const int fr = f < NF ? f : f - NF;
-    loff[f] = static_cast<uint32_t>((fr * 16 + nl) * a.rowbytes) + static_cast<uint32_t>(g * BB - 2 * (g & 1));
+    loff[f] = static_cast<uint32_t>((fr * 16 + nl) * a.rowbytes) + static_cast<uint32_t>(lane_blk);
     const int64_t n = static_cast<int64_t>(fb + fr) * 16 + nl;
-    wrow[f] = (f < NF ? a.W : a.W2) + n * a.rowbytes + (g * BB - 2 * (g & 1));
+    wrow[f] = (f < NF ? a.W : a.W2) + n * a.rowbytes + lane_blk;
   }
+  const uint32_t qg = 16 + 32 * (g >> 1);  // Q4_K: the lane group's nibble run in a half super-block
   const __amdgpu_buffer_rsrc_t wr0 = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(a.W + static_cast<int64_t>(fb) * 16 * a.rowbytes), 0, 0x7fffffff, 0x00020000);
   const __amdgpu_buffer_rsrc_t wr1 = __builtin_amdgcn_make_buffer_rsrc(
@@ -276,7 +329,17 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
   const uint32_t shd = (g & 1) ? 16u : 0u;
   auto wload = [&](int f, int s, uint32_t (&dst)[WD]) {
     s = s < s1 ? s : s1 - 1;
-    if constexpr (NW == 8) {
+    if constexpr (KQ) {
+      // the 32 nibble bytes of half s & 1 of super-block s / 2, lane group g
+      const uint32_t qo = static_cast<uint32_t>(s >> 1) * MmFmt<FMT>::SB + 64u * static_cast<uint32_t>(s & 1);
+      const u4 q0 = __builtin_amdgcn_raw_buffer_load_b128(wr0, static_cast<int>(loff[f] + qg), static_cast<int>(qo), 0);
+      const u4 q1 = __builtin_amdgcn_raw_buffer_load_b128(wr0, static_cast<int>(loff[f] + qg + 16), static_cast<int>(qo), 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dst[i] = q0[i];
+        dst[4 + i] = q1[i];
+      }
+    } else if constexpr (NW == 8) {
       load_window_buf<WD>(f < NF ? wr0 : wr1, loff[f], static_cast<uint32_t>(s) * (4 * BB), dst);
     } else {
       load_window<WD>(wrow[f] + static_cast<int64_t>(s) * (4 * BB), dst);
@@ -325,6 +388,17 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
       }
     }
   };
+  // Q4_K heads: wave w stages rows 64 w + lane of the tile (clamped to its last row) at row * 16
+  static_assert(!KQ || (NW == 8 && DMA), "super-block rows: 8-wave body with fp16 X only");
+  const int tile_row0 = KQ ? (tile / a.m_tiles) * a.F * 16 : 0;
+  const int tile_rows = KQ ? (a.N - tile_row0 < a.F * 16 ? a.N - tile_row0 : a.F * 16) : 1;
+  const int hrow = KQ ? (64 * w + lane < tile_rows ? 64 * w + lane : tile_rows - 1) : 0;
+  const uint32_t hoff = static_cast<uint32_t>(hrow * a.rowbytes);
+  const uint8_t *hbase0 = a.W + static_cast<int64_t>(tile_row0) * a.rowbytes;
+  auto h_dma = [&](int s, uint8_t *dst) {
+    s = s < s1 ? s : s1 - 1;
+    lds_dma16_s(hbase0 + static_cast<int64_t>(s >> 1) * MmFmt<FMT>::SB, hoff, dst + w * 1024);
+  };
   auto x_regs = [&](int s) {
     const uint32_t k = xk(s);
 #pragma unroll
@@ -352,11 +426,12 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
   };
-  constexpr int LPW = WD / 4 + 1;  // load instructions per weight window
+  constexpr int LPW = KQ ? 2 : WD / 4 + 1;  // load instructions per weight window
+  constexpr int XL = XC + (KQ ? 1 : 0);     // X-side loads per wave and step (Q4_K: + the heads)
   // Loads younger than X(s + 1) when step s ends in the steady state: W(s + 2 - NA + D), then per
   // step X(.) and W(.) for the NA - 2 steps after it. Earlier steps have at least as many, so
   // waiting for this many is safe everywhere (it may wait a little longer in the first steps).
-  constexpr int YOUNGER = (NA - 2) * (XC + NB * LPW) + NB * LPW;
+  constexpr int YOUNGER = (NA - 2) * (XL + NB * LPW) + NB * LPW;
 
   f4 acc[MT][NB > 0 ? NB : 1];
 #pragma unroll
@@ -372,14 +447,17 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
     if constexpr (DMA) {
 #pragma unroll
       for (int j = 0; j < D; ++j) {
-        if (j < NA - 1) x_dma(s0 + j, sm.a[j]);
+        if (j < NA - 1) {
+          x_dma(s0 + j, sm.a[j]);
+          if constexpr (KQ) h_dma(s0 + j, sm.h[j]);
+        }
 #pragma unroll
         for (int f = 0; f < NB; ++f) wload(f, s0 + j, ring[j][f]);
         __builtin_amdgcn_sched_barrier(0);
       }
-      wait_vm(std::integral_constant<int, (NA - 2) * (XC + NB * LPW) + 2 * NB * LPW < 64
-                                              ? (NA - 2) * (XC + NB * LPW) + 2 * NB * LPW : 63>{});
-      if constexpr ((NA - 2) * (XC + NB * LPW) + 2 * NB * LPW >= 64) wait_vm(std::integral_constant<int, 0>{});
+      wait_vm(std::integral_constant<int, (NA - 2) * (XL + NB * LPW) + 2 * NB * LPW < 64
+                                              ? (NA - 2) * (XL + NB * LPW) + 2 * NB * LPW : 63>{});
+      if constexpr ((NA - 2) * (XL + NB * LPW) + 2 * NB * LPW >= 64) wait_vm(std::integral_constant<int, 0>{});
     } else {
       x_regs(s0);
 #pragma unroll
@@ -395,8 +473,22 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
 
   // MFMAs of one super-step: A fragments of step t + 1 and the B fragment after the current one
   // are produced while the current MFMAs run
-  auto compute = [&](const uint32_t (&slot)[NB > 0 ? NB : 1][WD], const uint8_t *abase) {
+  auto compute = [&](const uint32_t (&slot)[NB > 0 ? NB : 1][WD], const uint8_t *abase, const uint8_t *hb, int s) {
     if constexpr (NB > 0) {
+      // Q4_K: the lane's sub-block scale and min per fragment, once per super-step, from the
+      // row heads staged with this step's X
+      uint32_t sd[KQ ? NB : 1];
+      if constexpr (KQ) {
+        const bool odd = (s & 1) != 0;
+#pragma unroll
+        for (int f = 0; f < NB; ++f)
+          sd[f] = q4k_scales(*reinterpret_cast<const u4 *>(hb + ((fb + f) * 16 + nl - tile_row0) * 16), g, odd);
+      }
+      const uint32_t nsh = 4u * static_cast<uint32_t>(g & 1);
+      auto bstep = [&](int f, int t) {
+        if constexpr (KQ) return q4k_step(slot[f], t, nsh, sd[f]);
+        else return dequant_step<FMT>(slot[f], t, sel, shd);
+      };
       // ABUF = 2: the A fragments of step t + 1 are read into the other buffer at the start of
       // step t; ABUF = 1 (8 waves, 256 registers per lane): fragment i of step t + 1 is read into
       // af[0][i] right after the last MFMA of step t that reads it
@@ -404,7 +496,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
       hf8 af[ABUF][MT];
 #pragma unroll
       for (int i = 0; i < MT; ++i) af[0][i] = *reinterpret_cast<const hf8 *>(abase + (i * 4 * 64 + lane) * 16);
-      hf8 bcur = dequant_step<FMT>(slot[0], 0, sel, shd);
+      hf8 bcur = bstep(0, 0);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         if (ABUF == 2 && t < 3) {
@@ -418,7 +510,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
           const int fn = f + 1 < NB ? f + 1 : 0;
           const int tn = f + 1 < NB ? t : t + 1;
           hf8 bnext = bcur;
-          if (!last) bnext = dequant_step<FMT>(slot[fn], tn, sel, shd);
+          if (!last) bnext = bstep(fn, tn);
 #pragma unroll
           for (int i = 0; i < MT; ++i) {
             acc[i][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t % ABUF][i], bcur, acc[i][f], 0, 0, 0);
@@ -436,9 +528,10 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
   auto step = [&](auto dc, auto refill, int s) {
     constexpr int d = decltype(dc)::value;
     if constexpr (DMA) x_dma(s + NA - 1, sm.a[(d + NA - 1) % NA]);
+    if constexpr (KQ) h_dma(s + NA - 1, sm.h[(d + NA - 1) % NA]);
     else x_regs(s + 1);
     __builtin_amdgcn_sched_barrier(0);
-    compute(ring[d], sm.a[d % NA]);
+    compute(ring[d], sm.a[d % NA], sm.h[d % NA], s);
     if constexpr (decltype(refill)::value) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -513,7 +606,12 @@ __device__ __forceinline__ void mmq_unit(const MmArgs &a, const MmLds<MT> &sm, i
   __shared__ __attribute__((aligned(16))) uint8_t a2[NA_ > 2 ? MT * 4096 : 16];       \
   __shared__ __attribute__((aligned(16))) uint8_t a3[NA_ > 3 ? MT * 4096 : 16];       \
   __shared__ uint32_t last;                                                           \
-  const MmLds<MT> sm{{a0, a1, a2, a3}, &last}
+  constexpr int NH_ = FMT == FMT_Q4_K ? 8192 : 16;                                    \
+  __shared__ __attribute__((aligned(16))) uint8_t h0[NH_];                            \
+  __shared__ __attribute__((aligned(16))) uint8_t h1[NH_];                            \
+  __shared__ __attribute__((aligned(16))) uint8_t h2_[NA_ > 2 ? NH_ : 16];            \
+  __shared__ __attribute__((aligned(16))) uint8_t h3[NA_ > 3 ? NH_ : 16];             \
+  const MmLds<MT> sm{{a0, a1, a2, a3}, &last, {h0, h1, h2_, h3}}
 
 template <int FMT, int XDT, int MT, int NFX, int NW = 4>
 __global__ void __launch_bounds__(64 * NW, 1) k_mmq(MmArgs a) {
@@ -594,18 +692,23 @@ int mmq_launch(MmArgs &a, hipStream_t s) {
   a.xcd = units % 8 == 0 ? 1 : 0;
   bool eight = XDT == VYBDQ_F16;
   if (const char *e = tuning_env("VYBDQ_MMQ_WAVES")) eight = eight && e[0] != '4';
+  static_assert(FMT != FMT_Q4_K || XDT == VYBDQ_F16, "Q4_K rows: fp16 X (the 8-wave body) only");
   if constexpr (XDT == VYBDQ_F16) {
-    if (eight) {
-      hipLaunchKernelGGL((k_mmq<FMT, XDT, kMmMT, kMmNFX8, 8>), dim3(static_cast<unsigned>(units)), dim3(512), 0, s, a);
+    if (eight || FMT == FMT_Q4_K) {
+      constexpr int NFX8 = FMT == FMT_Q4_K ? 2 : kMmNFX8;  // Q4_K: F <= 16 (the planner's limit)
+      hipLaunchKernelGGL((k_mmq<FMT, XDT, kMmMT, NFX8, 8>), dim3(static_cast<unsigned>(units)), dim3(512), 0, s, a);
       const int rc = check_launch("mmq gemm");
       if (rc) return rc;
-      return mm_reduce_launch<8, kMmMT, kMmNFX8, 1>(a, s);
+      return mm_reduce_launch<8, kMmMT, NFX8, 1>(a, s);
     }
   }
-  hipLaunchKernelGGL((k_mmq<FMT, XDT, kMmMT, kMmNFX>), dim3(static_cast<unsigned>(units)), dim3(256), 0, s, a);
-  const int rc = check_launch("mmq gemm");
-  if (rc) return rc;
-  return mm_reduce_launch<4, kMmMT, kMmNFX, 1>(a, s);
+  if constexpr (FMT != FMT_Q4_K) {
+    hipLaunchKernelGGL((k_mmq<FMT, XDT, kMmMT, kMmNFX>), dim3(static_cast<unsigned>(units)), dim3(256), 0, s, a);
+    const int rc = check_launch("mmq gemm");
+    if (rc) return rc;
+    return mm_reduce_launch<4, kMmMT, kMmNFX, 1>(a, s);
+  }
+  return VYBDQ_OK;
 }
 
 }  // namespace vybdq

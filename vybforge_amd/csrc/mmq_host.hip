@@ -14,6 +14,7 @@ extern template int mmq_launch<FMT_Q4_0, VYBDQ_F32>(MmArgs &, hipStream_t);
 extern template int mmq_launch<FMT_Q8_0, VYBDQ_F16>(MmArgs &, hipStream_t);
 extern template int mmq_launch<FMT_Q8_0, VYBDQ_BF16>(MmArgs &, hipStream_t);
 extern template int mmq_launch<FMT_Q8_0, VYBDQ_F32>(MmArgs &, hipStream_t);
+extern template int mmq_launch<FMT_Q4_K, VYBDQ_F16>(MmArgs &, hipStream_t);
 
 // ---- host --------------------------------------------------------------------------------
 
@@ -195,17 +196,21 @@ int x_rows_to_f16(const void *X, int xdt, int64_t M, int64_t K, void *xh, float 
 static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 
 // workspace: [split partials][fp16 copy of X][X row scales]
-int64_t mmq_workspace_size(int64_t M, int64_t N, int64_t K) {
+// Q4_K tiles: at most 16 fragments (two per wave: its nibble windows, the scale words and 96
+// accumulators fill the 256 registers of a wave at three)
+static int mm_nfx(int wtype) { return wtype == 12 ? 4 : kMmNFX; }
+
+int64_t mmq_workspace_size(int wtype, int64_t M, int64_t N, int64_t K) {
   if (!mmq_supported(M, N, K)) return 0;
-  return align256(mm_plan(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K / 128), true).ws_bytes) +
+  return align256(mm_plan(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K / 128), true, mm_nfx(wtype)).ws_bytes) +
          align256(M * K * 2) + align256(M * 4);
 }
 
 int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
              int64_t ldy, const void *RS, void *ws, int64_t ws_bytes, hipStream_t s) {
   const int S = static_cast<int>(K / 128);
-  MmPlan p = mm_plan(static_cast<int>(M), static_cast<int>(N), S, ws != nullptr);
-  if (p.splits > 1 && ws_bytes < p.ws_bytes) p = mm_plan(static_cast<int>(M), static_cast<int>(N), S, false);
+  MmPlan p = mm_plan(static_cast<int>(M), static_cast<int>(N), S, ws != nullptr, mm_nfx(wtype));
+  if (p.splits > 1 && ws_bytes < p.ws_bytes) p = mm_plan(static_cast<int>(M), static_cast<int>(N), S, false, mm_nfx(wtype));
   // with room for it, a non-fp16 X is converted once up front (instead of once per N tile)
   const int64_t xh_off = align256(p.ws_bytes);
   const int64_t sc_off = xh_off + align256(M * K * 2);
@@ -221,7 +226,7 @@ int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   }
   MmArgs a{};
   a.W = static_cast<const uint8_t *>(W);
-  a.rowbytes = K / 32 * (wtype == 2 ? 18 : 34);
+  a.rowbytes = wtype == 12 ? K / 256 * MmFmt<FMT_Q4_K>::SB : K / 32 * (wtype == 2 ? 18 : 34);
   a.X = X;
   a.ldx = K;
   a.M = static_cast<int>(M);
@@ -239,6 +244,11 @@ int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   a.xscale = xscale;
   if (p.splits > 1) {
     a.part = static_cast<float *>(ws);
+  }
+  if (wtype == 12) {
+    // the Q4_K body streams fp16 X: bf16 / f32 X needs the workspace for its conversion
+    if (xdt != VYBDQ_F16) return set_error(VYBDQ_ERR_WORKSPACE, "mmq gemm: Q4_K with bf16/f32 X needs the workspace");
+    return mmq_launch<FMT_Q4_K, VYBDQ_F16>(a, s);
   }
   if (wtype == 2) {
     switch (xdt) {
