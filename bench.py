@@ -493,8 +493,8 @@ def run_prefill_kq(args, torch, dev):
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed + 6)
     launches, flops, nbytes = [], 0, 0
-    # Q4_K uses the workspace (bf16 X converted once, the register-operand body); the other types
-    # decode their tiles into LDS and take none
+    # Q4_K / Q5_K use the workspace (bf16 X converted once, the register-operand body); the other
+    # types decode their tiles into LDS and take none
     ws = ops.GemmWorkspace([(M, N, K) for N, K in PREFILL_SHAPES], dev, ty)
     wsa = ws if ws.nbytes else None
     for N, K in PREFILL_SHAPES:
@@ -510,7 +510,7 @@ def run_prefill_kq(args, torch, dev):
     roofline = dict(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s",
                     frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), traffic=None,
                     kernel=(f"k_mmq<{name}, fp16 X, 8 waves> (bf16 X converted once per GEMM; weights dequantized "
-                            "into operand registers, super-block heads staged in LDS)" if ty == 12 else
+                            "into operand registers, super-block heads staged in LDS)" if ty in (12, 13) else
                             f"k_kq_gemm<{name}> (units decoded to fp16 in LDS, fp16 MFMA 16x16x32)"),
                     basis="flops per step / event time", avg_launch_us=round(ms * 1e3 / len(launches), 3))
     return dict(value=tflops, unit="TFLOP/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,

@@ -246,13 +246,17 @@ def _gemm_ws(ty, W, xd, N, K, dev):
     return ops.gemm(ty, W, xd, N, K, workspace=ws)
 
 
+REG_BODY = [ops.GGML_Q4_K, ops.GGML_Q5_K]
+
+
+@pytest.mark.parametrize("ty", REG_BODY)
 @pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 17408)])
-def test_gemm_q4k_register_body_prefill_shape(dev, N, K):
-    """Q4_K at the prefill shapes through vybdq_gemm_ws (bf16 X converted once into the workspace,
-    the 8-wave tile body with the weights dequantized into the MFMA operand registers and the
-    super-block heads staged in LDS; 17408 -> 5120 splits K): 256 columns of the first and the
-    last weight tiles against the float64 oracle."""
-    ty, M = ops.GGML_Q4_K, 512
+def test_gemm_q4k_register_body_prefill_shape(dev, ty, N, K):
+    """Q4_K / Q5_K at the prefill shapes through vybdq_gemm_ws (bf16 X converted once into the
+    workspace, the 8-wave tile body with the weights dequantized into the MFMA operand registers
+    and the super-block heads (Q5_K: with the high bits) staged in LDS; 17408 -> 5120 splits K):
+    256 columns of the first and the last weight tiles against the float64 oracle."""
+    M = 512
     rng = np.random.default_rng(N + 7)
     raw = synth.kquant_weights(rng, ty, N, K)
     x = torch.from_numpy(synth.activations(rng, (M, K))).to(torch.bfloat16)
@@ -264,15 +268,15 @@ def test_gemm_q4k_register_body_prefill_shape(dev, N, K):
         assert matmul.rel_maxnorm(y[:, c0:c0 + 256], matmul.gemm_rows_f64(x64, wrows)) < TOL, c0
 
 
+@pytest.mark.parametrize("ty", REG_BODY)
 @pytest.mark.parametrize("M,N,K", [(64, 64, 256), (100, 320, 512), (130, 1088, 768), (200, 256, 16384),
                                    (513, 2112, 2560)])
 @pytest.mark.parametrize("xdt", ["f16", "bf16_ws", "f32_ws"])
-def test_gemm_q4k_register_body_edges(dev, M, N, K, xdt):
-    """The Q4_K register-operand body: partial m-tiles (100, 130, 513 rows), a partial last n-tile,
-    odd super-step counts per split (K = 768), a long K that splits (16384), fp16 X directly and
-    bf16 / f32 X through the workspace; every output against the float64 oracle."""
-    ty = ops.GGML_Q4_K
-    rng = np.random.default_rng(M + N + K)
+def test_gemm_q4k_register_body_edges(dev, ty, M, N, K, xdt):
+    """The Q4_K / Q5_K register-operand body: partial m-tiles (100, 130, 513 rows), a partial last
+    n-tile, odd super-step counts per split (K = 768), a long K that splits (16384), fp16 X directly
+    and bf16 / f32 X through the workspace; every output against the float64 oracle."""
+    rng = np.random.default_rng(M + N + K + ty)
     raw = synth.kquant_weights(rng, ty, N, K)
     x = synth.activations(rng, (M, K))
     xd, x64 = x_as(x, xdt.split("_")[0], dev)
@@ -283,13 +287,14 @@ def test_gemm_q4k_register_body_edges(dev, M, N, K, xdt):
     assert matmul.rel_maxnorm(y, ref) < TOL
 
 
+@pytest.mark.parametrize("ty", REG_BODY)
 @pytest.mark.parametrize("kind", ["outlier", "offset", "fp16_limit", "tiny", "huge"])
-def test_gemm_q4k_register_body_activation_range(dev, kind):
+def test_gemm_q4k_register_body_activation_range(dev, ty, kind):
     """f32 X of any magnitude through the workspace: each row is converted to fp16 after a
     power-of-two scale that is multiplied back into its outputs."""
-    ty, M, N, K = ops.GGML_Q4_K, 128, 512, 2560
+    M, N, K = 128, 512, 2560
     kinds = ["outlier", "offset", "fp16_limit", "tiny", "huge"]
-    rng = np.random.default_rng(300 + kinds.index(kind))
+    rng = np.random.default_rng(300 + 10 * ty + kinds.index(kind))
     raw = synth.kquant_weights(rng, ty, N, K)
     x = _x_pattern(kind, rng, M, K)
     y = _gemm_ws(ty, to_dev(raw, dev), to_dev(x, dev), N, K, dev).cpu().numpy()

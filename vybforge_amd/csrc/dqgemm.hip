@@ -445,7 +445,7 @@ static int gemm_check(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, 
 }
 
 extern "C" int64_t vybdq_gemm_workspace_size(int wtype, int64_t M, int64_t N, int64_t K) {
-  if ((wtype != 2 && wtype != 8 && wtype != 12) || M < 64 || !mmq_supported(M, N, K)) return 0;
+  if ((wtype != 2 && wtype != 8 && wtype != 12 && wtype != 13) || M < 64 || !mmq_supported(M, N, K)) return 0;
   return mmq_workspace_size(wtype, M, N, K);
 }
 
@@ -456,8 +456,9 @@ extern "C" int vybdq_gemm_ws(int wtype, uint64_t W, uint64_t X, uint64_t Y, int6
   if (rc) return rc;
   VYBDQ_REQUIRE(ws == 0 || (ws & 255) == 0, VYBDQ_ERR_ALIGN, "workspace must be 256-byte aligned");
   VYBDQ_REQUIRE(ws_bytes >= 0, VYBDQ_ERR_WORKSPACE, "negative workspace size");
-  // Q4_K: the register-operand body streams fp16 X, so bf16 / f32 X needs room for its conversion
-  const bool q4k_ok = wtype == 12 && M >= 64 && K < (int64_t(1) << 22) && mmq_supported(M, N, K) &&
+  // Q4_K / Q5_K: the register-operand body streams fp16 X, so bf16 / f32 X needs room for its
+  // conversion
+  const bool q4k_ok = (wtype == 12 || wtype == 13) && M >= 64 && K < (int64_t(1) << 22) && mmq_supported(M, N, K) &&
                       (x_dt == VYBDQ_F16 || (ws && ws_bytes >= mmq_workspace_size(wtype, M, N, K)));
   if ((wtype <= 8 && M >= 64 && mmq_supported(M, N, K)) || q4k_ok)
     return mmq_gemm(wtype, reinterpret_cast<const void *>(W), reinterpret_cast<const void *>(X), x_dt,
@@ -484,9 +485,10 @@ extern "C" int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t
   a.RS = reinterpret_cast<const void *>(RS);
   a.G = 1;
   hipStream_t s = as_stream(stream);
-  // Q4_K from 64 rows with fp16 X: the register-operand tile body (with a workspace any X type,
-  // vybdq_gemm_ws); the other super-block types and the other Q4_K calls decode tiles into LDS
-  if (wtype == 12 && x_dt == VYBDQ_F16 && M >= 64 && K < (int64_t(1) << 22) && mmq_supported(M, N, K))
+  // Q4_K / Q5_K from 64 rows with fp16 X: the register-operand tile body (with a workspace any X
+  // type, vybdq_gemm_ws); the other super-block types and the other calls decode tiles into LDS
+  if ((wtype == 12 || wtype == 13) && x_dt == VYBDQ_F16 && M >= 64 && K < (int64_t(1) << 22) &&
+      mmq_supported(M, N, K))
     return mmq_gemm(wtype, a.W, a.X, x_dt, a.Y, y_dt, M, N, K, a.ldy, a.RS, nullptr, 0, s);
   if (wtype >= 12) return kq_gemm(wtype, a.W, a.X, x_dt, a.Y, y_dt, M, N, K, a.ldy, a.RS, s);
   if (M >= 64 && mmq_supported(M, N, K))

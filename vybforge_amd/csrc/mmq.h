@@ -71,11 +71,11 @@ template <int FMT> struct MmFmt;
 // D: weight super-steps in flight per lane (the register ring) with 4 waves; D8 with 8 waves
 // (half the registers per wave)
 template <> struct MmFmt<FMT_Q4_0> {
-  static constexpr int BB = 18, WD = 5, D = 4, D8 = 2, SB = 0;
+  static constexpr int BB = 18, WD = 5, D = 4, D8 = 2, SB = 0, HB = 0, QS = 0;
   static constexpr float OFF = 1032.0f;
 };
 template <> struct MmFmt<FMT_Q8_0> {
-  static constexpr int BB = 34, WD = 9, D = 3, D8 = 2, SB = 0;
+  static constexpr int BB = 34, WD = 9, D = 3, D8 = 2, SB = 0, HB = 0, QS = 0;
   static constexpr float OFF = 1152.0f;
 };
 // Q4_K: 144-byte super-blocks of 256 (d, dmin, 12 scale bytes, 128 nibble bytes); a 128-k super-step
@@ -85,6 +85,15 @@ template <> struct MmFmt<FMT_Q8_0> {
 // and step), so the register ring holds only the nibbles.
 template <> struct MmFmt<FMT_Q4_K> {
   static constexpr int BB = 0, WD = 8, D = 3, D8 = 2, SB = 144;
+  static constexpr int HB = 16, QS = 16;  // bytes of each row's super-block head staged in LDS; nibble start
+  static constexpr float OFF = 0.0f;
+};
+// Q5_K: 176-byte super-blocks (d, dmin, 12 scale bytes, 32 high-bit bytes, 128 nibble bytes): the
+// same nibble windows, and the head staged in LDS is 48 bytes (with the high bits: bit j of
+// qh[l] is the fifth bit of element l of sub-block j).
+template <> struct MmFmt<FMT_Q5_K> {
+  static constexpr int BB = 0, WD = 8, D = 3, D8 = 2, SB = 176;
+  static constexpr int HB = 48, QS = 48;
   static constexpr float OFF = 0.0f;
 };
 
@@ -105,15 +114,19 @@ __device__ __forceinline__ uint32_t q4k_scales(const u4 hd, int g, bool odd) {
 // nibbles): q exact in fp16 (0x64vv - 1024), then one fp16 fma q * ds - dm. (The decode and the
 // super-block GEMM round the float32 value of the same expression once to fp16; this differs from
 // it by the fp16 rounding of ds and dm, within one fp16 ulp of the weight's scale.)
+// Q5_K: hb2 = the 8 high-bit bytes of the step's elements; bit j of each is the fifth bit.
+template <bool Q5>
 __device__ __forceinline__ _Float16 __attribute__((ext_vector_type(8))) q4k_step(const uint32_t (&w)[8], int t,
-                                                                                 uint32_t sh, uint32_t sd) {
+                                                                                 uint32_t sh, uint32_t sd,
+                                                                                 u2 hb2 = u2{0u, 0u}, uint32_t j = 0) {
   const h2 v2 = __builtin_bit_cast(h2, sd);
   const h2 ds = {v2[0], v2[0]}, ndm = {v2[1], v2[1]};
   const h2 k1024 = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
   _Float16 __attribute__((ext_vector_type(8))) r;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const uint32_t v = (w[2 * t + h] >> sh) & 0x0F0F0F0Fu;
+    uint32_t v = (w[2 * t + h] >> sh) & 0x0F0F0F0Fu;
+    if constexpr (Q5) v |= ((hb2[h] >> j) << 4) & 0x10101010u;
     const h2 q0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, v, SEL_B01)) - k1024;
     const h2 q1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(C64, v, SEL_B23)) - k1024;
     const h2 p0 = __builtin_elementwise_fma(q0, ds, ndm);
@@ -307,8 +320,9 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
   // lane offset (f * 16 + nl) rows + the block's dword-aligned start (NB * 16 rows of a K < 2^25
   // matrix stay below 2^32 bytes). Super-steps past the range re-read the last one.
   // With 4 waves (512 registers per lane) each lane keeps 64-bit row pointers instead.
-  // Q4_K (KQ): the lane offset is the row start; the head and the nibble run are placed per step.
-  constexpr bool KQ = FMT == FMT_Q4_K;
+  // Q4_K / Q5_K (KQ): the lane offset is the row start; the nibble run is placed per step.
+  constexpr bool KQ = FMT == FMT_Q4_K || FMT == FMT_Q5_K;
+  constexpr int HB = MmFmt<FMT>::HB, HC = HB / 16;  // head bytes per row in LDS, 16-byte loads per row
   static_assert(!KQ || !SWI, "super-block rows: plain GEMM only");
   const int lane_blk = KQ ? 0 : g * BB - 2 * (g & 1);
   uint32_t loff[NB > 0 ? NB : 1];
@@ -320,7 +334,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
     const int64_t n = static_cast<int64_t>(fb + fr) * 16 + nl;
     wrow[f] = (f < NF ? a.W : a.W2) + n * a.rowbytes + lane_blk;
   }
-  const uint32_t qg = 16 + 32 * (g >> 1);  // Q4_K: the lane group's nibble run in a half super-block
+  const uint32_t qg = MmFmt<FMT>::QS + 32 * (g >> 1);  // the lane group's nibble run in a half super-block
   const __amdgpu_buffer_rsrc_t wr0 = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(a.W + static_cast<int64_t>(fb) * 16 * a.rowbytes), 0, 0x7fffffff, 0x00020000);
   const __amdgpu_buffer_rsrc_t wr1 = __builtin_amdgcn_make_buffer_rsrc(
@@ -388,16 +402,25 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
       }
     }
   };
-  // Q4_K heads: wave w stages rows 64 w + lane of the tile (clamped to its last row) at row * 16
+  // Super-block heads: the first HB bytes of each tile row's super-block, row r at r * HB in LDS;
+  // 16-byte chunk c = 64 (HC w + i) + lane (load i of wave w) is byte 16 (c % HC) of row c / HC
+  // (rows past the tile clamped to its last row)
   static_assert(!KQ || (NW == 8 && DMA), "super-block rows: 8-wave body with fp16 X only");
   const int tile_row0 = KQ ? (tile / a.m_tiles) * a.F * 16 : 0;
   const int tile_rows = KQ ? (a.N - tile_row0 < a.F * 16 ? a.N - tile_row0 : a.F * 16) : 1;
-  const int hrow = KQ ? (64 * w + lane < tile_rows ? 64 * w + lane : tile_rows - 1) : 0;
-  const uint32_t hoff = static_cast<uint32_t>(hrow * a.rowbytes);
+  uint32_t hoff[HC > 0 ? HC : 1];
+#pragma unroll
+  for (int i = 0; i < HC; ++i) {
+    const int c = 64 * (HC * w + i) + lane;
+    const int r = c / HC < tile_rows ? c / HC : tile_rows - 1;
+    hoff[i] = static_cast<uint32_t>(r * a.rowbytes) + 16u * static_cast<uint32_t>(c % HC);
+  }
   const uint8_t *hbase0 = a.W + static_cast<int64_t>(tile_row0) * a.rowbytes;
   auto h_dma = [&](int s, uint8_t *dst) {
     s = s < s1 ? s : s1 - 1;
-    lds_dma16_s(hbase0 + static_cast<int64_t>(s >> 1) * MmFmt<FMT>::SB, hoff, dst + w * 1024);
+#pragma unroll
+    for (int i = 0; i < HC; ++i)
+      lds_dma16_s(hbase0 + static_cast<int64_t>(s >> 1) * MmFmt<FMT>::SB, hoff[i], dst + (HC * w + i) * 1024);
   };
   auto x_regs = [&](int s) {
     const uint32_t k = xk(s);
@@ -427,7 +450,7 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
   };
   constexpr int LPW = KQ ? 2 : WD / 4 + 1;  // load instructions per weight window
-  constexpr int XL = XC + (KQ ? 1 : 0);     // X-side loads per wave and step (Q4_K: + the heads)
+  constexpr int XL = XC + HC;               // X-side loads per wave and step (+ the super-block heads)
   // Loads younger than X(s + 1) when step s ends in the steady state: W(s + 2 - NA + D), then per
   // step X(.) and W(.) for the NA - 2 steps after it. Earlier steps have at least as many, so
   // waiting for this many is safe everywhere (it may wait a little longer in the first steps).
@@ -478,15 +501,19 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
       // Q4_K: the lane's sub-block scale and min per fragment, once per super-step, from the
       // row heads staged with this step's X
       uint32_t sd[KQ ? NB : 1];
+      const uint32_t jq = 4u * static_cast<uint32_t>(s & 1) + static_cast<uint32_t>(g);  // the lane's sub-block
       if constexpr (KQ) {
         const bool odd = (s & 1) != 0;
 #pragma unroll
         for (int f = 0; f < NB; ++f)
-          sd[f] = q4k_scales(*reinterpret_cast<const u4 *>(hb + ((fb + f) * 16 + nl - tile_row0) * 16), g, odd);
+          sd[f] = q4k_scales(*reinterpret_cast<const u4 *>(hb + ((fb + f) * 16 + nl - tile_row0) * HB), g, odd);
       }
       const uint32_t nsh = 4u * static_cast<uint32_t>(g & 1);
       auto bstep = [&](int f, int t) {
-        if constexpr (KQ) return q4k_step(slot[f], t, nsh, sd[f]);
+        if constexpr (FMT == FMT_Q5_K)
+          return q4k_step<true>(slot[f], t, nsh, sd[f],
+                                *reinterpret_cast<const u2 *>(hb + ((fb + f) * 16 + nl - tile_row0) * HB + 16 + 8 * t), jq);
+        else if constexpr (KQ) return q4k_step<false>(slot[f], t, nsh, sd[f]);
         else return dequant_step<FMT>(slot[f], t, sel, shd);
       };
       // ABUF = 2: the A fragments of step t + 1 are read into the other buffer at the start of
@@ -606,7 +633,7 @@ __device__ __forceinline__ void mmq_unit(const MmArgs &a, const MmLds<MT> &sm, i
   __shared__ __attribute__((aligned(16))) uint8_t a2[NA_ > 2 ? MT * 4096 : 16];       \
   __shared__ __attribute__((aligned(16))) uint8_t a3[NA_ > 3 ? MT * 4096 : 16];       \
   __shared__ uint32_t last;                                                           \
-  constexpr int NH_ = FMT == FMT_Q4_K ? 8192 : 16;                                    \
+  constexpr int NH_ = MmFmt<FMT>::HB > 0 ? 512 * MmFmt<FMT>::HB : 16;                \
   __shared__ __attribute__((aligned(16))) uint8_t h0[NH_];                            \
   __shared__ __attribute__((aligned(16))) uint8_t h1[NH_];                            \
   __shared__ __attribute__((aligned(16))) uint8_t h2_[NA_ > 2 ? NH_ : 16];            \
@@ -692,17 +719,18 @@ int mmq_launch(MmArgs &a, hipStream_t s) {
   a.xcd = units % 8 == 0 ? 1 : 0;
   bool eight = XDT == VYBDQ_F16;
   if (const char *e = tuning_env("VYBDQ_MMQ_WAVES")) eight = eight && e[0] != '4';
-  static_assert(FMT != FMT_Q4_K || XDT == VYBDQ_F16, "Q4_K rows: fp16 X (the 8-wave body) only");
+  constexpr bool KQ = FMT == FMT_Q4_K || FMT == FMT_Q5_K;
+  static_assert(!KQ || XDT == VYBDQ_F16, "super-block rows: fp16 X (the 8-wave body) only");
   if constexpr (XDT == VYBDQ_F16) {
-    if (eight || FMT == FMT_Q4_K) {
-      constexpr int NFX8 = FMT == FMT_Q4_K ? 2 : kMmNFX8;  // Q4_K: F <= 16 (the planner's limit)
+    if (eight || KQ) {
+      constexpr int NFX8 = KQ ? 2 : kMmNFX8;  // super-block rows: F <= 16 (the planner's limit)
       hipLaunchKernelGGL((k_mmq<FMT, XDT, kMmMT, NFX8, 8>), dim3(static_cast<unsigned>(units)), dim3(512), 0, s, a);
       const int rc = check_launch("mmq gemm");
       if (rc) return rc;
       return mm_reduce_launch<8, kMmMT, NFX8, 1>(a, s);
     }
   }
-  if constexpr (FMT != FMT_Q4_K) {
+  if constexpr (!KQ) {
     hipLaunchKernelGGL((k_mmq<FMT, XDT, kMmMT, kMmNFX>), dim3(static_cast<unsigned>(units)), dim3(256), 0, s, a);
     const int rc = check_launch("mmq gemm");
     if (rc) return rc;

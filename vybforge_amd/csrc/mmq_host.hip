@@ -15,6 +15,7 @@ extern template int mmq_launch<FMT_Q8_0, VYBDQ_F16>(MmArgs &, hipStream_t);
 extern template int mmq_launch<FMT_Q8_0, VYBDQ_BF16>(MmArgs &, hipStream_t);
 extern template int mmq_launch<FMT_Q8_0, VYBDQ_F32>(MmArgs &, hipStream_t);
 extern template int mmq_launch<FMT_Q4_K, VYBDQ_F16>(MmArgs &, hipStream_t);
+extern template int mmq_launch<FMT_Q5_K, VYBDQ_F16>(MmArgs &, hipStream_t);
 
 // ---- host --------------------------------------------------------------------------------
 
@@ -196,9 +197,9 @@ int x_rows_to_f16(const void *X, int xdt, int64_t M, int64_t K, void *xh, float 
 static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 
 // workspace: [split partials][fp16 copy of X][X row scales]
-// Q4_K tiles: at most 16 fragments (two per wave: its nibble windows, the scale words and 96
-// accumulators fill the 256 registers of a wave at three)
-static int mm_nfx(int wtype) { return wtype == 12 ? 4 : kMmNFX; }
+// Q4_K / Q5_K tiles: at most 16 fragments (two per wave: its nibble windows, the scale words and
+// 96 accumulators fill the 256 registers of a wave at three)
+static int mm_nfx(int wtype) { return wtype == 12 || wtype == 13 ? 4 : kMmNFX; }
 
 int64_t mmq_workspace_size(int wtype, int64_t M, int64_t N, int64_t K) {
   if (!mmq_supported(M, N, K)) return 0;
@@ -226,7 +227,9 @@ int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   }
   MmArgs a{};
   a.W = static_cast<const uint8_t *>(W);
-  a.rowbytes = wtype == 12 ? K / 256 * MmFmt<FMT_Q4_K>::SB : K / 32 * (wtype == 2 ? 18 : 34);
+  a.rowbytes = wtype == 12   ? K / 256 * MmFmt<FMT_Q4_K>::SB
+               : wtype == 13 ? K / 256 * MmFmt<FMT_Q5_K>::SB
+                             : K / 32 * (wtype == 2 ? 18 : 34);
   a.X = X;
   a.ldx = K;
   a.M = static_cast<int>(M);
@@ -245,10 +248,11 @@ int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   if (p.splits > 1) {
     a.part = static_cast<float *>(ws);
   }
-  if (wtype == 12) {
-    // the Q4_K body streams fp16 X: bf16 / f32 X needs the workspace for its conversion
-    if (xdt != VYBDQ_F16) return set_error(VYBDQ_ERR_WORKSPACE, "mmq gemm: Q4_K with bf16/f32 X needs the workspace");
-    return mmq_launch<FMT_Q4_K, VYBDQ_F16>(a, s);
+  if (wtype == 12 || wtype == 13) {
+    // the super-block body streams fp16 X: bf16 / f32 X needs the workspace for its conversion
+    if (xdt != VYBDQ_F16)
+      return set_error(VYBDQ_ERR_WORKSPACE, "mmq gemm: Q4_K / Q5_K with bf16/f32 X needs the workspace");
+    return wtype == 12 ? mmq_launch<FMT_Q4_K, VYBDQ_F16>(a, s) : mmq_launch<FMT_Q5_K, VYBDQ_F16>(a, s);
   }
   if (wtype == 2) {
     switch (xdt) {
