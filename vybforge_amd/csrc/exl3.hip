@@ -285,7 +285,7 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   extern __shared__ __attribute__((aligned(16))) char smem[];
   __shared__ int is_last;
   const int g = blockIdx.x, s = blockIdx.y, S = gridDim.y;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)), lane = threadIdx.x & 63;
   const int t = lane >> 3, j = lane & 7;
   const int KB = static_cast<int>(K / 16);
   const int kb_begin = s * kb_per_split;
@@ -325,10 +325,22 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   const int xstride = MMA ? rows + 8 : rows;
   const int nch = nkb / 8;
   if constexpr (!FUSED) {
-    for (int i = threadIdx.x; i < BP * rows / 8; i += blockDim.x) {
-      const int b = i / (rows / 8), c = i % (rows / 8);
-      *reinterpret_cast<u4 *>(reinterpret_cast<_Float16 *>(smem) + b * xstride + 8 * c) =
-          *reinterpret_cast<const u4 *>(xp + b * K + 16 * static_cast<int64_t>(kb_begin) + 8 * c);
+    // four 16-byte chunks per thread in flight at a time (one round trip per 1024 chunks)
+    const int nc = BP * rows / 8;
+    for (int i0 = threadIdx.x; i0 < nc; i0 += 4 * blockDim.x) {
+      u4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * blockDim.x;
+        const int b = i / (rows / 8), c = i % (rows / 8);
+        if (i < nc) v[u] = *reinterpret_cast<const u4 *>(xp + b * K + 16 * static_cast<int64_t>(kb_begin) + 8 * c);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * blockDim.x;
+        const int b = i / (rows / 8), c = i % (rows / 8);
+        if (i < nc) *reinterpret_cast<u4 *>(reinterpret_cast<_Float16 *>(smem) + b * xstride + 8 * c) = v[u];
+      }
     }
   }
   for (int cb = wave; FUSED && cb < BP * nch; cb += 4) {  // one 128 chunk per wave at a time
@@ -440,16 +452,22 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
       }
     }
   };
-  for (int k0 = w_begin; k0 < w_end; k0 += kD) {
+  // Whole groups of kD k-blocks without conditions, each ring slot refilled right after the step
+  // that consumed it (into the same registers): the loads stay in flight across groups. (A
+  // per-block bound made every slot a merge of two paths, and a refill issued before the step
+  // needed a second register set that was copied back at the loop end; both made the compiler
+  // wait for every load once per group.) The last (fewer than kD) blocks are already in the ring.
+  int k0 = w_begin;
+  for (; k0 + kD <= w_end; k0 += kD) {
 #pragma unroll
     for (int d = 0; d < kD; ++d) {
-      if (k0 + d < w_end) {
-        const u4 c = ring[d];
-        ring[d] = load_chunk(k0 + d + kD);
-        step(k0 + d, c);
-      }
+      step(k0 + d, ring[d]);
+      ring[d] = load_chunk(k0 + d + kD);
     }
   }
+#pragma unroll
+  for (int d = 0; d < kD - 1; ++d)
+    if (k0 + d < w_end) step(k0 + d, ring[d]);
   // reduce the 4 waves (same columns, different k) in a fixed order
   __syncthreads();
   float *red = reinterpret_cast<float *>(smem);  // [4][BP][kExl3RedStride]
