@@ -554,9 +554,12 @@ __device__ __forceinline__ void mm_body(const MmArgs &a, const MmLds<MT> &sm, in
   // DC % NA); REFILL issues the weights of s + D into the slot
   auto step = [&](auto dc, auto refill, int s) {
     constexpr int d = decltype(dc)::value;
-    if constexpr (DMA) x_dma(s + NA - 1, sm.a[(d + NA - 1) % NA]);
-    if constexpr (KQ) h_dma(s + NA - 1, sm.h[(d + NA - 1) % NA]);
-    else x_regs(s + 1);
+    if constexpr (DMA) {
+      x_dma(s + NA - 1, sm.a[(d + NA - 1) % NA]);
+      if constexpr (KQ) h_dma(s + NA - 1, sm.h[(d + NA - 1) % NA]);
+    } else {
+      x_regs(s + 1);
+    }
     __builtin_amdgcn_sched_barrier(0);
     compute(ring[d], sm.a[d % NA], sm.h[d % NA], s);
     if constexpr (decltype(refill)::value) {
