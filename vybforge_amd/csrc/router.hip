@@ -39,47 +39,71 @@ __device__ __forceinline__ void load8(const void *p, int64_t i, double (&v)[8]) 
   }
 }
 
-template <int XDT, int WDT>
+// TT tokens per pass over the row: the row's weights are loaded once per pass and every token keeps
+// its own accumulator, so each (t, e) sum runs in exactly the order above; one barrier per pass.
+// The grid is (expert rows, token tiles of TT): workgroup (e, y) runs tokens y TT .. y TT + TT - 1.
+template <int XDT, int WDT, int TT>
 __global__ void __launch_bounds__(256) k_router_logits(const void *__restrict__ X, const void *__restrict__ W,
                                                        void *__restrict__ Y, int ydt, int64_t T, int64_t E,
                                                        int64_t H) {
 #pragma clang fp contract(off)
-  __shared__ double wsum[4];
+  __shared__ double wsum[2][4][TT];
   const int q = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t e = blockIdx.x;
   const int64_t Hq = H / 4;
   const int64_t h0 = q * Hq;
-  for (int64_t t = 0; t < T; ++t) {
-    double acc = 0.0;
+  int par = 0;
+  for (int64_t t0 = static_cast<int64_t>(blockIdx.y) * TT; t0 < T; t0 += static_cast<int64_t>(TT) * gridDim.y, par ^= 1) {
+    double acc[TT];
+#pragma unroll
+    for (int u = 0; u < TT; ++u) acc[u] = 0.0;
     for (int64_t k = 8 * lane; k < Hq; k += 512) {
-      double xv[8], wv[8];
-      load8<XDT>(X, t * H + h0 + k, xv);
+      double wv[8];
       load8<WDT>(W, e * H + h0 + k, wv);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc = acc + xv[j] * wv[j];  // a product, then a sum (no contraction)
+      for (int u = 0; u < TT; ++u) {
+        const int64_t t = t0 + u < T ? t0 + u : T - 1;  // past T: a valid row, never stored
+        double xv[8];
+        load8<XDT>(X, t * H + h0 + k, xv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[u] = acc[u] + xv[j] * wv[j];  // a product, then a sum (no contraction)
+      }
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
-    if (lane == 0) wsum[q] = acc;
+    for (int u = 0; u < TT; ++u) {
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) acc[u] = acc[u] + __shfl_xor(acc[u], off, 64);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int u = 0; u < TT; ++u) wsum[par][q][u] = acc[u];
+    }
+    // the two halves of wsum alternate between passes, so one barrier per pass suffices
     __syncthreads();
-    if (threadIdx.x == 0) {
-      const double y = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+    if (threadIdx.x < TT && t0 + threadIdx.x < T) {
+      const int u = threadIdx.x;
+      const double y = ((wsum[par][0][u] + wsum[par][1][u]) + wsum[par][2][u]) + wsum[par][3][u];
+      const int64_t t = t0 + u;
       if (ydt == VYBDQ_F64) static_cast<double *>(Y)[t * E + e] = y;
       else static_cast<float *>(Y)[t * E + e] = static_cast<float>(y);
     }
-    __syncthreads();
   }
 }
 
 template <int WDT>
 static void launch_router(int x_dt, dim3 grid, hipStream_t s, const void *x, const void *w, void *y, int y_dt,
                           int64_t T, int64_t E, int64_t H) {
+#define RL(XDT, TT) hipLaunchKernelGGL((k_router_logits<XDT, WDT, TT>), grid, dim3(256), 0, s, x, w, y, y_dt, T, E, H)
+#define RX(XDT) \
+  do { if (T <= 4) RL(XDT, 1); else if (T <= 64) RL(XDT, 4); else RL(XDT, 16); } while (0)
   switch (x_dt) {
-    case VYBDQ_F64: hipLaunchKernelGGL((k_router_logits<VYBDQ_F64, WDT>), grid, dim3(256), 0, s, x, w, y, y_dt, T, E, H); break;
-    case VYBDQ_F32: hipLaunchKernelGGL((k_router_logits<VYBDQ_F32, WDT>), grid, dim3(256), 0, s, x, w, y, y_dt, T, E, H); break;
-    case VYBDQ_F16: hipLaunchKernelGGL((k_router_logits<VYBDQ_F16, WDT>), grid, dim3(256), 0, s, x, w, y, y_dt, T, E, H); break;
-    default: hipLaunchKernelGGL((k_router_logits<VYBDQ_BF16, WDT>), grid, dim3(256), 0, s, x, w, y, y_dt, T, E, H); break;
+    case VYBDQ_F64: RX(VYBDQ_F64); break;
+    case VYBDQ_F32: RX(VYBDQ_F32); break;
+    case VYBDQ_F16: RX(VYBDQ_F16); break;
+    default: RX(VYBDQ_BF16); break;
   }
+#undef RX
+#undef RL
 }
 
 }  // namespace vybdq
@@ -97,7 +121,11 @@ extern "C" int vybdq_router_logits(uint64_t X, int x_dt, uint64_t W, int w_dt, u
   VYBDQ_REQUIRE((X & 15) == 0 && (W & 15) == 0, VYBDQ_ERR_ALIGN, "X and W must be 16-byte aligned");
   if (T == 0) return VYBDQ_OK;
   hipStream_t s = as_stream(stream);
-  const dim3 grid(static_cast<unsigned>(E));
+  // token tiles (measured at 256 x 6144): one token each up to 4 tokens, 4 up to 64 (1024
+  // workgroups at 16 tokens), 16 above; one pass per workgroup up to 65535 tiles
+  const int64_t tt = T <= 4 ? 1 : T <= 64 ? 4 : 16;
+  const int64_t tiles = (T + tt - 1) / tt;
+  const dim3 grid(static_cast<unsigned>(E), static_cast<unsigned>(tiles < 65535 ? tiles : 65535));
   const void *x = reinterpret_cast<const void *>(X), *w = reinterpret_cast<const void *>(W);
   void *y = reinterpret_cast<void *>(Y);
   VYBDQ_DISPATCH_IN(w_dt, WDT, launch_router<WDT>(x_dt, grid, s, x, w, y, y_dt, T, E, H));
