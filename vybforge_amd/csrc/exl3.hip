@@ -55,53 +55,81 @@ __device__ __forceinline__ uint32_t win_extract(const uint32_t (&w)[6], int o) {
   return __builtin_amdgcn_alignbit(w[i + 1], w[i], s);
 }
 
-// The codebook hash of a window up to the two fp16 halves (before they are added).
+// mcg hash of the 16-bit window in half HI of d (the other half is ignored): x = w * 0xCBAC1FED
+// mod 2^32 from two full-rate 16 x 16-bit products, c = (w * 0xCBAC) << 16 (the multiply writes
+// its low 16 bits to the high half through its SDWA destination select) and x = w * 0x1FED + c
+// (v_mad_u32_u16, whose op_sel takes the window from either half). Written out because the
+// compiler would merge the products into one quarter-rate 32-bit multiply, or shift and add
+// separately.
+template <bool HI>
+__device__ __forceinline__ uint32_t mcg_hash(uint32_t d) {
+  uint32_t c, x;
+  if constexpr (HI) {
+    asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:DWORD"
+        : "=v"(c) : "v"(d), "s"(0xCBACu));
+    asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(x) : "v"(d), "s"(0x1FEDu), "v"(c));
+  } else {
+    asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:WORD_1 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD"
+        : "=v"(c) : "v"(d), "s"(0xCBACu));
+    asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(x) : "v"(d), "s"(0x1FEDu), "v"(c));
+  }
+  return x;
+}
+
+// The codebook hash of a window (its low 16 bits; higher bits are ignored) up to the two fp16
+// halves (before they are added).
 template <int CB>
 __device__ __forceinline__ uint32_t decode_window_halves(uint32_t w) {
-  const uint32_t wl = w & 0xffffu;
-  uint32_t hi, lo;
+  uint32_t x;
   if constexpr (CB == VYBDQ_EXL3_MCG) {
-    hi = wl * 0xCBACu;
-    lo = wl * 0x1FEDu;
+    x = mcg_hash<false>(w);
   } else {
-    hi = wl * 0x0551u;
-    lo = wl * 0x7C72u + 0x03D45AA4u;
+    const uint32_t wl = w & 0xffffu;
+    uint32_t hi = wl * 0x0551u;
+    const uint32_t lo = wl * 0x7C72u + 0x03D45AA4u;
+    // keeps the two 16 x 16-bit products apart (full-rate 24-bit multiplies): combined, the
+    // compiler would emit one quarter-rate 32-bit multiply
+    asm volatile("" : "+v"(hi));
+    x = (hi << 16) + lo;
   }
-  // keeps the two 16 x 16-bit products apart (full-rate 24-bit multiplies): combined, the compiler
-  // would emit one quarter-rate 32-bit multiply
-  asm volatile("" : "+v"(hi));
-  const uint32_t x = (hi << 16) + lo;
   return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
 }
 
+// Lane slot q's window hashed up to the two fp16 halves. A one-piece window at a 16-bit boundary
+// is hashed straight from its stream dword; other one-piece windows are funnel-extracted without
+// a mask (the hash reads only the low 16 bits); two-piece windows are assembled from their masks.
 template <int CB>
-__device__ __forceinline__ _Float16 decode_window(uint32_t w) {
-  // x = w16 * M (+ A) mod 2^32 from two 16x16-bit products; only the low 16 bits of w are used
-  const uint32_t wl = w & 0xffffu;
-  uint32_t hi, lo;
+__device__ __forceinline__ uint32_t slot_halves(const uint32_t (&w)[6], int q) {
+  const int o = kExl3SlotOff0[q];
+  const bool one = kExl3SlotOff1[q] < 0 && kExl3SlotMask0[q] == 0xffffu;
   if constexpr (CB == VYBDQ_EXL3_MCG) {
-    hi = wl * 0xCBACu;
-    lo = wl * 0x1FEDu;
-  } else {
-    hi = wl * 0x0551u;
-    lo = wl * 0x7C72u + 0x03D45AA4u;
+    if (one && (o & 15) == 0) {
+      const uint32_t x = (o & 16) ? mcg_hash<true>(w[o >> 5]) : mcg_hash<false>(w[o >> 5]);
+      return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+    }
   }
-  // keep the two full-rate 16x16 products from being merged into one quarter-rate v_mul_lo_u32
-  asm volatile("" : "+v"(hi));
-  const uint32_t x = (hi << 16) + lo;
-  const uint32_t y = (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
-  const h2 v = __builtin_bit_cast(h2, y);
-  return v[0] + v[1];
+  if (one) return decode_window_halves<CB>(win_extract(w, o));
+  // A two-piece window whose first piece runs to the end of its stream dword and whose second
+  // piece starts a dword is one funnel shift of those two dwords (the second above the first).
+  const unsigned m0 = kExl3SlotMask0[q];
+  const int n = __builtin_popcount(m0), o1 = kExl3SlotOff1[q];
+  if (o1 >= 0 && m0 == (1u << n) - 1 && (o & 31) + n == 32 && ((o1 + n) & 31) == 0 &&
+      kExl3SlotMask1[q] == (0xffffu & ~m0))
+    return decode_window_halves<CB>(__builtin_amdgcn_alignbit(w[(o1 + n) >> 5], w[o >> 5], o & 31));
+  uint32_t x = win_extract(w, o) & kExl3SlotMask0[q];
+  if (kExl3SlotOff1[q] >= 0) x |= win_extract(w, kExl3SlotOff1[q]) & kExl3SlotMask1[q];
+  return decode_window_halves<CB>(x);
 }
 
-// The 32 values of lane j: val[q] = row q of column j (q < 16), row q-16 of column j+8.
+// The 32 values of lane j: val[q] = row q of column j (q < 16), row q-16 of column j+8. Both
+// halves of a hash lie in [0.125, 2), so their float32 sum is exact and one fp16 add rounds it as
+// the reference's float32-sum-then-round does.
 template <int CB>
 __device__ __forceinline__ void lane_decode(const uint32_t (&w)[6], _Float16 (&val)[32]) {
 #pragma unroll
   for (int q = 0; q < 32; ++q) {
-    uint32_t x = win_extract(w, kExl3SlotOff0[q]) & kExl3SlotMask0[q];
-    if (kExl3SlotOff1[q] >= 0) x |= win_extract(w, kExl3SlotOff1[q]) & kExl3SlotMask1[q];
-    val[q] = decode_window<CB>(x);
+    const h2 v = __builtin_bit_cast(h2, slot_halves<CB>(w, q));
+    val[q] = v[0] + v[1];
   }
 }
 
@@ -314,9 +342,6 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
     const int64_t tile = static_cast<int64_t>(kb_begin + kc) * NB + nb;
     return *reinterpret_cast<const u4 *>(trellis + tile * 64 + 8 * j);
   };
-  u4 ring[kD];
-#pragma unroll
-  for (int d = 0; d < kD; ++d) ring[d] = load_chunk(w_begin + d);
   // 1. x' rows of this split: [BP][16 * nkb] fp16 (HALVES: u32 pairs (x, x))
   const int rows = 16 * nkb;
   // x' row stride of the stage (elements): the matrix-core A reads take 16 batch rows at once,
@@ -324,37 +349,71 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   // reads on the same banks)
   const int xstride = MMA ? rows + 8 : rows;
   const int nch = nkb / 8;
+  // Batch <= 2: each wave rotates the 128-chunks cb = wave, wave + 4, ... of x (batch row cb / nch).
+  // The raw x and suh elements of its first kXP chunks are read before the trellis ring: loads
+  // return in order, so the rotation then waits for these alone, not for the ring behind them.
+  constexpr int kXP = 2;
+  // (x elements k, k + 1 of the chunk's batch row: two f32 words, or one word of two 16-bit
+  // halves; suh k, k + 1 as one word of halves. Kept raw: converting them here would wait.)
+  auto x_raw = [&](int cb, uint32_t (&xv)[2], uint32_t &sv) {
+    const int b = cb / nch, c = cb - b * nch;
+    const int64_t k = 16 * static_cast<int64_t>(kb_begin) + 128 * c + 2 * lane;
+    const int64_t i = static_cast<int64_t>(b < B ? b : 0) * K + k;
+    if (xdt == VYBDQ_F32) __builtin_memcpy(xv, static_cast<const float *>(X) + i, 8);
+    else __builtin_memcpy(xv, static_cast<const uint16_t *>(X) + i, 4);
+    __builtin_memcpy(&sv, suh + k, 4);
+  };
+  uint32_t xw[kXP][2], sw[kXP];
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int it = 0; it < kXP; ++it)
+      if (wave + 4 * it < BP * nch) x_raw(wave + 4 * it, xw[it], sw[it]);
+  }
+  // Batch > 2: the rotated x' rows are copied from the workspace in 16-byte chunks, four per
+  // thread at a time; the first four are read before the trellis ring for the same reason.
+  const int nc = BP * rows / 8;
+  auto xp_chunk = [&](int i) {
+    const int b = i / (rows / 8), c = i % (rows / 8);
+    return *reinterpret_cast<const u4 *>(xp + b * K + 16 * static_cast<int64_t>(kb_begin) + 8 * c);
+  };
+  auto xs_store = [&](int i, const u4 v) {
+    const int b = i / (rows / 8), c = i % (rows / 8);
+    *reinterpret_cast<u4 *>(reinterpret_cast<_Float16 *>(smem) + b * xstride + 8 * c) = v;
+  };
+  u4 xv4[4];
   if constexpr (!FUSED) {
-    // four 16-byte chunks per thread in flight at a time (one round trip per 1024 chunks)
-    const int nc = BP * rows / 8;
-    for (int i0 = threadIdx.x; i0 < nc; i0 += 4 * blockDim.x) {
-      u4 v[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i0 + u * blockDim.x;
-        const int b = i / (rows / 8), c = i % (rows / 8);
-        if (i < nc) v[u] = *reinterpret_cast<const u4 *>(xp + b * K + 16 * static_cast<int64_t>(kb_begin) + 8 * c);
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i0 + u * blockDim.x;
-        const int b = i / (rows / 8), c = i % (rows / 8);
-        if (i < nc) *reinterpret_cast<u4 *>(reinterpret_cast<_Float16 *>(smem) + b * xstride + 8 * c) = v[u];
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int i = threadIdx.x + u * blockDim.x;
+      if (i < nc) xv4[u] = xp_chunk(i);
     }
   }
-  for (int cb = wave; FUSED && cb < BP * nch; cb += 4) {  // one 128 chunk per wave at a time
+  __builtin_amdgcn_sched_barrier(0);
+  u4 ring[kD];
+#pragma unroll
+  for (int d = 0; d < kD; ++d) ring[d] = load_chunk(w_begin + d);
+  if constexpr (!FUSED) {
+    for (int i0 = threadIdx.x;;) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (i0 + u * blockDim.x < nc) xs_store(i0 + u * blockDim.x, xv4[u]);
+      i0 += 4 * blockDim.x;
+      if (i0 >= nc) break;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (i0 + u * blockDim.x < nc) xv4[u] = xp_chunk(i0 + u * blockDim.x);
+    }
+  }
+  auto rotate = [&](int cb, const uint32_t (&xv)[2], uint32_t sv) {  // one 128-chunk, whole wave
     const int b = cb / nch, c = cb - b * nch;
     const int r = 128 * c + 2 * lane;
-    const int64_t k = 16 * static_cast<int64_t>(kb_begin) + r;
     float a0 = 0.f, a1 = 0.f;
     if (b < B) {
-      const int64_t i = b * K + k;
-      if (xdt == VYBDQ_F32) { a0 = load_elem<VYBDQ_F32>(X, i); a1 = load_elem<VYBDQ_F32>(X, i + 1); }
-      else if (xdt == VYBDQ_F16) { a0 = load_elem<VYBDQ_F16>(X, i); a1 = load_elem<VYBDQ_F16>(X, i + 1); }
-      else { a0 = load_elem<VYBDQ_BF16>(X, i); a1 = load_elem<VYBDQ_BF16>(X, i + 1); }
-      a0 *= static_cast<float>(suh[k]);
-      a1 *= static_cast<float>(suh[k + 1]);
+      if (xdt == VYBDQ_F32) { a0 = __uint_as_float(xv[0]); a1 = __uint_as_float(xv[1]); }
+      else if (xdt == VYBDQ_F16) { a0 = half_bits_to_f32(xv[0] & 0xffffu); a1 = half_bits_to_f32(xv[0] >> 16); }
+      else { a0 = __uint_as_float(xv[0] << 16); a1 = __uint_as_float(xv[0] & 0xffff0000u); }
+      a0 *= half_bits_to_f32(sv & 0xffffu);
+      a1 *= half_bits_to_f32(sv >> 16);
     }
     fwht128_wave(a0, a1);
     const uint32_t h0 = __builtin_bit_cast(uint16_t, static_cast<_Float16>(a0 * kRScale));
@@ -363,6 +422,16 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
       *reinterpret_cast<u2 *>(reinterpret_cast<uint32_t *>(smem) + b * rows + r) = u2{h0 | (h0 << 16), h1 | (h1 << 16)};
     } else {
       *reinterpret_cast<uint32_t *>(reinterpret_cast<_Float16 *>(smem) + b * rows + r) = h0 | (h1 << 16);
+    }
+  };
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int it = 0; it < kXP; ++it)
+      if (wave + 4 * it < BP * nch) rotate(wave + 4 * it, xw[it], sw[it]);
+    for (int cb = wave + 4 * kXP; cb < BP * nch; cb += 4) {
+      uint32_t xv[2], sv;
+      x_raw(cb, xv, sv);
+      rotate(cb, xv, sv);
     }
   }
   __syncthreads();
@@ -396,9 +465,7 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
       }
 #pragma unroll
       for (int q = 0; q < 32; ++q) {
-        uint32_t x = win_extract(w, kExl3SlotOff0[q]) & kExl3SlotMask0[q];
-        if (kExl3SlotOff1[q] >= 0) x |= win_extract(w, kExl3SlotOff1[q]) & kExl3SlotMask1[q];
-        const h2 y = __builtin_bit_cast(h2, decode_window_halves<CB>(x));
+        const h2 y = __builtin_bit_cast(h2, slot_halves<CB>(w, q));
 #pragma unroll
         for (int b = 0; b < BP; ++b)
           acc[b][q >> 4] = __builtin_amdgcn_fdot2(y, __builtin_bit_cast(h2, xq[b][q & 15]), acc[b][q >> 4], false);
@@ -463,6 +530,9 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
     for (int d = 0; d < kD; ++d) {
       step(k0 + d, ring[d]);
       ring[d] = load_chunk(k0 + d + kD);
+      // keeps the refill here: sunk to the end of the group it would leave no load in flight
+      // while the group's last step waits for its own
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 #pragma unroll
