@@ -84,8 +84,9 @@ def exl3_config4(dev):
 @pytest.mark.parametrize("B,xdt", [(1, torch.float32), (2, torch.float16), (4, torch.float16),
                                    (16, torch.float16), (16, torch.bfloat16)])
 def test_exl3_gemm_config4_shape(dev, exl3_config4, B, xdt):
-    """K = 5120, N = 17408 at every batch regime: one fused launch with 7 k-splits (B <= 2), and
-    the three-launch matrix-core path with 16 k-splits over 2176 workgroups (B = 4, 16)."""
+    """K = 5120, N = 17408 at every batch regime: one fused launch with 14 k-splits over 1904
+    workgroups (B <= 2), and the three-launch matrix-core path with 16 k-splits over 2176
+    workgroups (B = 4, 16)."""
     lin, slices, K, N = exl3_config4
     x = torch.from_numpy(np.random.default_rng(B).standard_normal((B, K)).astype(np.float32)).to(xdt)
     y = lin(x.to(dev)).cpu().numpy()
@@ -98,8 +99,10 @@ def test_exl3_gemm_config4_shape(dev, exl3_config4, B, xdt):
 @pytest.mark.parametrize("K,N", [(128, 256), (1152, 256), (2048, 384)])
 def test_exl3_gemm_splits_and_reuse(dev, K, N):
     """One workspace across calls of several batch sizes and dtypes (the per-block arrival
-    counters must come back to zero after every call): a single k-split (K = 128), a ragged last
-    split (K = 1152: 72 k-blocks in splits of 16), repeated calls bit-identical."""
+    counters must come back to zero after every call): a single k-split (K = 128), even splits
+    (K = 1152: 72 k-blocks, 3 splits of 24 at batch <= 2, 9 of 8 above), a ragged last split
+    (K = 2048 at batch <= 2: 128 k-blocks, 5 splits of 24 and one of 8), repeated calls
+    bit-identical."""
     rng = np.random.default_rng(K + N)
     t, suh, svh = synth.exl3_tensors(rng, K, N)
     lin = ops.Exl3Linear(dev_t(t, dev), dev_t(suh, dev), dev_t(svh, dev), K, N)

@@ -583,10 +583,22 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
   __syncthreads();
   if (!is_last) return;
   for (int b = wave; b < B; b += 4) {
+    // the splits' partials (this lane's two columns as one 8-byte word) in groups of 8 independent
+    // loads, one round trip per group, added in split order
     float a0 = 0.f, a1 = 0.f;
-    for (int sp = 0; sp < S; ++sp) {
-      a0 += __uint_as_float(__hip_atomic_load(zp(sp, b, 2 * lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      a1 += __uint_as_float(__hip_atomic_load(zp(sp, b, 2 * lane + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    for (int s0 = 0; s0 < S; s0 += 8) {
+      uint64_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s0 + u < S)
+          v[u] = __hip_atomic_load(reinterpret_cast<uint64_t *>(zp(s0 + u, b, 2 * lane)), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s0 + u < S) {
+          a0 += __uint_as_float(static_cast<uint32_t>(v[u]));
+          a1 += __uint_as_float(static_cast<uint32_t>(v[u] >> 32));
+        }
     }
     fwht128_wave(a0, a1);
     const int64_t n0 = 128 * static_cast<int64_t>(g) + 2 * lane;
@@ -605,10 +617,19 @@ __global__ void __launch_bounds__(64) k_exl3_out(const float *__restrict__ zpart
                                                  void *__restrict__ Y, int BP, int S, int64_t N) {
   const int blk = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   const int64_t n0 = 128 * static_cast<int64_t>(blk) + 2 * lane;
+  // the splits' partials in groups of 8 independent 8-byte loads, added in split order
   float a0 = 0.f, a1 = 0.f;
-  for (int s = 0; s < S; ++s) {
-    a0 += zpart[(static_cast<int64_t>(s) * BP + b) * N + n0];
-    a1 += zpart[(static_cast<int64_t>(s) * BP + b) * N + n0 + 1];
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    f2 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < S) v[u] = *reinterpret_cast<const f2 *>(zpart + (static_cast<int64_t>(s0 + u) * BP + b) * N + n0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < S) {
+        a0 += v[u][0];
+        a1 += v[u][1];
+      }
   }
   fwht128_wave(a0, a1);
   store_elem<YDT>(Y, nullptr, b * N + n0, a0 * kRScale * static_cast<float>(svh[n0]));
@@ -628,11 +649,21 @@ struct Exl3Split {
 static Exl3Split exl3_splits(int64_t K, int64_t N, int BP) {
   const int KB = static_cast<int>(K / 16);
   const int64_t groups = N / 128;
-  // measured at K = 5120, N = 17408: batch 1 best at 7 splits (952 workgroups: 1680 GB/s against
-  // 1625 at 8 and 1466 at 4); the matrix-core batches (4..16) at 16 (batch 4: 1294 against 1194 GB/s
-  // at 8; batch 16: 8, 12, 20 and 24 splits 9-11% slower)
-  const int64_t target = BP >= 4 ? 2048 : 896;
-  int S = static_cast<int>((target + groups - 1) / groups);
+  int S;
+  if (BP <= 2) {
+    // about 24 k-blocks per split (6 per wave), at most ~8 workgroups per CU. Measured, batch 1:
+    // K = 5120, N = 17408: 14 splits 20.2-20.9 us against 21.3-22.4 at 7-12; K = 10240: 14
+    // splits 37.4 us against 41.0 at 7; K = 2560: 7 splits 13.0 us against 13.7 at 10; K = 17408,
+    // N = 5120: 16 splits 24.8 us (12: 23.6, 7: 29.2). Fewer splits leave some CUs a workgroup
+    // more than others for longer; more add x rotations and partials.
+    S = (KB + 23) / 24;
+    const int64_t fill = groups < 2048 ? 2048 / groups : 1;
+    if (S > fill) S = static_cast<int>(fill);
+  } else {
+    // the matrix-core batches (4..16): ~2048 workgroups (K = 5120, N = 17408: batch 4 at 16 splits
+    // 1294 against 1194 GB/s at 8; batch 16: 8, 12, 20 and 24 splits 9-11% slower)
+    S = static_cast<int>((2048 + groups - 1) / groups);
+  }
   if (S > 16) S = 16;
   if (S > KB / 4) S = KB / 4 > 0 ? KB / 4 : 1;
   if (const char *e = tuning_env("VYBDQ_EXL3_SPLITS")) S = atoi(e);  // tuning override
