@@ -339,6 +339,74 @@ __global__ void __launch_bounds__(256) k_moe_route_bucket(const void *__restrict
   bucket_tiles(idx_lds, T, topk, E, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2, sh);
 }
 
+// At most 64 rows (T * topk <= 64): the same outputs as bucket_tiles from one wave with row i
+// (token i / topk, slot i % topk) in lane i, and no LDS counts, scans or barriers: a row's place
+// is the number of rows of lower expert ids plus the rows of its own expert before it (so rows
+// keep token order inside an expert), and the first row of each expert writes the expert's
+// m-tiles after those of the shared expert and of every lower expert id.
+__device__ __forceinline__ void bucket_rows_wave(const int *idx_lds, int T, int topk, int BMr, int BMr2, int shared,
+                                                 int *__restrict__ pos, int *__restrict__ row_map,
+                                                 int4 *__restrict__ tiles, int *__restrict__ ntiles,
+                                                 int4 *__restrict__ tiles2, int *__restrict__ ntiles2) {
+  const int lane = threadIdx.x & 63;
+  const int n = T * topk;
+  const int id = lane < n ? idx_lds[lane] : 0x7fffffff;
+  int below = 0, before = 0, cnt = 0;
+  for (int j = 0; j < n; ++j) {
+    const int o = __builtin_amdgcn_readlane(id, j);
+    below += o < id;
+    cnt += o == id;
+    before += o == id && j < lane;
+  }
+  const bool first = lane < n && before == 0;  // this lane's row starts its expert's range
+  const int mt = first ? (cnt + BMr - 1) / BMr : 0, mt2 = first ? (cnt + BMr2 - 1) / BMr2 : 0;
+  const int tsh = shared ? (T + BMr - 1) / BMr : 0, tsh2 = shared ? (T + BMr2 - 1) / BMr2 : 0;
+  int t = tsh, t2 = tsh2, tot = tsh, tot2 = tsh2;
+  for (int j = 0; j < n; ++j) {
+    const int o = __builtin_amdgcn_readlane(id, j);
+    const int m = __builtin_amdgcn_readlane(mt, j), m2 = __builtin_amdgcn_readlane(mt2, j);
+    if (o < id) { t += m; t2 += m2; }
+    tot += m;
+    tot2 += m2;
+  }
+  if (lane < n) {
+    pos[lane] = below + before;
+    row_map[below + before] = lane / topk;
+  }
+  for (int m = 0; m < mt; ++m) tiles[t + m] = make_int4(id, below, below + cnt, m);
+  if (tiles2)
+    for (int m = 0; m < mt2; ++m)
+      tiles2[t2 + m] = make_int4(id, below + m * BMr2, below + (cnt < (m + 1) * BMr2 ? cnt : (m + 1) * BMr2), 0);
+  if (lane == 0) {
+    *ntiles = tot;
+    if (ntiles2) *ntiles2 = tot2;
+  }
+  for (int j = lane; j < tsh; j += 64) tiles[j] = make_int4(-1, n, n + T, j);
+  if (tiles2)
+    for (int j = lane; j < tsh2; j += 64)
+      tiles2[j] = make_int4(-1, n + j * BMr2, n + (T < (j + 1) * BMr2 ? T : (j + 1) * BMr2), 0);
+  if (shared)
+    for (int i = lane; i < T; i += 64) row_map[n + i] = i;
+}
+
+// Few tokens and at most 64 rows: routing (wave w takes tokens w, w + 4, ...), then the one-wave
+// bucketing above.
+template <int LDT, bool KEYED>
+__global__ void __launch_bounds__(256) k_moe_route_bucket_w(const void *__restrict__ logits, const float *__restrict__ bias,
+                                                            int E, int topk, double scale, int *__restrict__ idx_out,
+                                                            float *__restrict__ w_out, int T, int BMr, int BMr2,
+                                                            int shared, int *__restrict__ pos, int *__restrict__ row_map,
+                                                            int4 *__restrict__ tiles, int *__restrict__ ntiles,
+                                                            int4 *__restrict__ tiles2, int *__restrict__ ntiles2) {
+  __shared__ int idx_lds[64];
+  for (int t = threadIdx.x >> 6; t < T; t += 4) {
+    if constexpr (KEYED) route_keyed<LDT>(logits, t, E, topk, scale, idx_out, w_out, idx_lds);
+    else route_double<LDT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds);
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) bucket_rows_wave(idx_lds, T, topk, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2);
+}
+
 // out[t][h] = sum_s w[t,s] * rows[pos[t,s]][h] (+ shared[t][h]); fixed slot order.
 template <int ODT>
 __global__ void __launch_bounds__(256) k_moe_combine(const float *__restrict__ rows, const float *__restrict__ shared,
@@ -497,9 +565,17 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       const int e = static_cast<int>(E), k = static_cast<int>(topk), tt = static_cast<int>(T);
       int4 *t2 = gv ? m.tiles2 : nullptr;
       int *n2 = gv ? m.ntiles2 : nullptr;
+      // at most 64 rows: the one-wave bucketing (no LDS counts, scans or barriers)
+      const bool wave_rows = T * topk <= 64;
 #define RB(LDT, KEYED)                                                                                          \
-  hipLaunchKernelGGL((k_moe_route_bucket<LDT, KEYED>), dim3(1), dim3(256), shb, s, lg, bs, e, k, scale, idx, wts, tt, \
-                     BMr, mc, shared ? 1 : 0, m.pos, m.row_map, m.tiles, m.ntiles, t2, n2)
+  do {                                                                                                        \
+    if (wave_rows)                                                                                            \
+      hipLaunchKernelGGL((k_moe_route_bucket_w<LDT, KEYED>), dim3(1), dim3(256), 0, s, lg, bs, e, k, scale, idx, \
+                         wts, tt, BMr, mc, shared ? 1 : 0, m.pos, m.row_map, m.tiles, m.ntiles, t2, n2);       \
+    else                                                                                                      \
+      hipLaunchKernelGGL((k_moe_route_bucket<LDT, KEYED>), dim3(1), dim3(256), shb, s, lg, bs, e, k, scale, idx, \
+                         wts, tt, BMr, mc, shared ? 1 : 0, m.pos, m.row_map, m.tiles, m.ntiles, t2, n2);       \
+  } while (0)
       if (logits_dt == VYBDQ_F64) RB(VYBDQ_F64, false);
       else if (bs) { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT, false)); }
       else { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT, true)); }
