@@ -197,20 +197,14 @@ __global__ void __launch_bounds__(NT) k_gemv_chain(const int64_t *__restrict__ p
     if (valid) {
       if constexpr (FMT == FMT_IQ2_S) {
         u4 *gridh = iq2s_lds_grid(sx, 1, P);
-        for (int i = threadIdx.x; i < 1024 + 256; i += NT) {
-          uint32_t q[4];
-          if (i < 1024) {
-            const unsigned long long e = kIq2sGrid[i];
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-              q[k] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(static_cast<float>((e >> (16 * k)) & 0xff)),
-                                                     static_cast<_Float16>(static_cast<float>((e >> (16 * k + 8)) & 0xff))});
-          } else {
-            const uint32_t sb = static_cast<uint32_t>(i - 1024);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) q[k] = (((sb >> (2 * k)) & 1u) << 15) | (((sb >> (2 * k + 1)) & 1u) << 31);
-          }
-          gridh[i] = u4{q[0], q[1], q[2], q[3]};
+        for (int i0 = threadIdx.x; i0 < 1024 + 256; i0 += 5 * NT) {  // five 16-B loads in flight per thread
+          u4 v[5];
+        #pragma unroll
+          for (int u = 0; u < 5; ++u)
+            if (i0 + u * NT < 1024 + 256) v[u] = reinterpret_cast<const u4 *>(kIq2sLdsTab)[i0 + u * NT];
+        #pragma unroll
+          for (int u = 0; u < 5; ++u)
+            if (i0 + u * NT < 1024 + 256) gridh[i0 + u * NT] = v[u];
         }
       }
       const int nchunk = 8 * P;

@@ -89,22 +89,18 @@ __global__ void __launch_bounds__(256) k_gemv_pair(const void *__restrict__ X, i
   }
   if constexpr (FMT == FMT_IQ2_S) {
     // after the x stage: the IQ2_S grid as fp16 (16 KB: entry i = its 8 magnitudes, exact) and
-    // the 256 sign patterns as fp16 sign-bit masks (4 KB: bit j of s -> bit 15 of half j)
+    // the 256 sign patterns as fp16 sign-bit masks (4 KB: bit j of s -> bit 15 of half j),
+    // copied from the table the generator precomputed (converting them here cost ~150 VALU
+    // instructions per wave, a fifth of a 9728 x 2560 GEMV's)
     u4 *gridh = iq2s_lds_grid(sx, M, P);
-    for (int i = threadIdx.x; i < 1024 + 256; i += T) {
-      uint32_t q[4];
-      if (i < 1024) {
-        const unsigned long long e = kIq2sGrid[i];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          q[k] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(static_cast<float>((e >> (16 * k)) & 0xff)),
-                                                 static_cast<_Float16>(static_cast<float>((e >> (16 * k + 8)) & 0xff))});
-      } else {
-        const uint32_t sb = static_cast<uint32_t>(i - 1024);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) q[k] = (((sb >> (2 * k)) & 1u) << 15) | (((sb >> (2 * k + 1)) & 1u) << 31);
-      }
-      gridh[i] = u4{q[0], q[1], q[2], q[3]};
+    for (int i0 = threadIdx.x; i0 < 1024 + 256; i0 += 5 * T) {  // five 16-B loads in flight per thread
+      u4 v[5];
+    #pragma unroll
+      for (int u = 0; u < 5; ++u)
+        if (i0 + u * T < 1024 + 256) v[u] = reinterpret_cast<const u4 *>(kIq2sLdsTab)[i0 + u * T];
+    #pragma unroll
+      for (int u = 0; u < 5; ++u)
+        if (i0 + u * T < 1024 + 256) gridh[i0 + u * T] = v[u];
     }
   }
   __syncthreads();
