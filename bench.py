@@ -493,8 +493,8 @@ def run_prefill_kq(args, torch, dev):
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed + 6)
     launches, flops, nbytes = [], 0, 0
-    # Q4_K / Q5_K use the workspace (bf16 X converted once, the register-operand body); the other
-    # types decode their tiles into LDS and take none
+    # every type uses the workspace: bf16 X converted once; Q4_K / Q5_K then run the register-operand
+    # body, Q6_K / IQ2_S the 128-row tiles (with the K split's partials)
     ws = ops.GemmWorkspace([(M, N, K) for N, K in PREFILL_SHAPES], dev, ty)
     wsa = ws if ws.nbytes else None
     for N, K in PREFILL_SHAPES:
@@ -511,7 +511,8 @@ def run_prefill_kq(args, torch, dev):
                     frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), traffic=None,
                     kernel=(f"k_mmq<{name}, fp16 X, 8 waves> (bf16 X converted once per GEMM; weights dequantized "
                             "into operand registers, super-block heads staged in LDS)" if ty in (12, 13) else
-                            f"k_kq_gemm<{name}> (units decoded to fp16 in LDS, fp16 MFMA 16x16x32)"),
+                            f"k_kq_mm<{name}> (bf16 X converted once per GEMM; 128-row tiles, runs decoded "
+                            "to fp16 in LDS, fp16 MFMA 16x16x32, K split reduced in the workspace)"),
                     basis="flops per step / event time", avg_launch_us=round(ms * 1e3 / len(launches), 3))
     return dict(value=tflops, unit="TFLOP/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
                 workload=f"{name} prefill GEMMs M=512: 5120->17408 and 17408->5120 (bf16 X, f32 Y)",

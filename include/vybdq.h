@@ -302,14 +302,18 @@ int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t X, ui
    dequantized tile in LDS. Super-block types: K % 256 == 0, N % 64 == 0, any M. Q4_K with
    M >= 64, K < 2^22 and fp16 X (any X type through vybdq_gemm_ws) dequantizes into the operand
    registers too, each weight as one fp16 fma q * fp16(d sc) - fp16(dmin m) (within one fp16 ulp
-   of the weight's scale of the F16 dequant value).
+   of the weight's scale of the F16 dequant value). Q6_K and IQ2_S with M >= 96, M K < 2^30 and
+   fp16 X (any X type through vybdq_gemm_ws) run 128-row tiles whose weights are formed in fp16
+   arithmetic: fp16(d sc) * (q - 32), fp16(d (0.5 + s) / 4) * grid magnitude (one product
+   rounding after the rounding of the scale).
    Replaces gemm_q80 and its siblings picked by gemm_h(ty) (native/host/ridge_decode.vyb:295-302,
    native/tools/gen_rpf.py:1-10,142-149, p-block W@0 X@8 Y@16 S@24 N@32 K@40 LDY@48 RS@56). */
 int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K, int x_dt,
                int y_dt, int64_t ldy, uint64_t RS, uint64_t stream);
 
-/* Workspace bytes vybdq_gemm_ws can use at (M, N, K) (q4_0, Q8_0, Q4_K from 64 rows): split-K
-   partials and the fp16 copy of a bf16/f32 X; 0 when the shape does not use the workspace. */
+/* Workspace bytes vybdq_gemm_ws can use at (M, N, K) (q4_0, Q8_0, Q4_K, Q5_K from 64 rows; Q6_K,
+   IQ2_S from 96 rows): split-K partials and the fp16 copy of a bf16/f32 X; 0 when the shape does
+   not use the workspace. */
 int64_t vybdq_gemm_workspace_size(int wtype, int64_t M, int64_t N, int64_t K);
 
 /* vybdq_gemm with a caller workspace ws (256-byte aligned, ws_bytes, any contents; 0 = none). With

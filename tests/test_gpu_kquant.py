@@ -301,3 +301,85 @@ def test_gemm_q4k_register_body_activation_range(dev, ty, kind):
     ref = matmul.gemm_rows_f64(x.astype(np.float64), matrix_ref(ty, raw, N, K))
     assert np.all(np.isfinite(y))
     assert matmul.rel_maxnorm(y, ref) < TOL
+
+
+TILE128 = [ops.GGML_Q6_K, ops.GGML_IQ2_S]
+
+
+@pytest.mark.parametrize("ty", TILE128)
+@pytest.mark.parametrize("N,K", [(17408, 5120), (5120, 17408)])
+def test_gemm_128row_tiles_prefill_shape(dev, ty, N, K):
+    """Q6_K / IQ2_S at the prefill shapes through vybdq_gemm_ws: bf16 X converted once into the
+    workspace, 128-row tiles with the planner's tile width and K split; 256 columns of the first
+    and the last weight tiles against the float64 oracle."""
+    M = 512
+    rng = np.random.default_rng(N + 17 + ty)
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = torch.from_numpy(synth.activations(rng, (M, K))).to(torch.bfloat16)
+    y = _gemm_ws(ty, to_dev(raw, dev), x.to(dev), N, K, dev).cpu().numpy()
+    x64 = x.to(torch.float64).numpy()
+    rb = BLOCK[ty] * (K // 256)
+    for c0 in (0, N - 256):
+        wrows = matrix_ref(ty, raw[c0 * rb:(c0 + 256) * rb], 256, K)
+        assert matmul.rel_maxnorm(y[:, c0:c0 + 256], matmul.gemm_rows_f64(x64, wrows)) < TOL, c0
+
+
+@pytest.mark.parametrize("ty", TILE128)
+@pytest.mark.parametrize("M,N,K", [(96, 64, 256), (130, 320, 768), (200, 256, 4096), (513, 1152, 2560)])
+@pytest.mark.parametrize("xdt,splits", [("f16", None), ("bf16_ws", "1"), ("bf16_ws", "3"), ("f32_ws", "2"),
+                                        ("f32_ws", None)])
+def test_gemm_128row_tiles_edges(dev, monkeypatch, ty, M, N, K, xdt, splits):
+    """The 128-row tile path: partial m-tiles (96, 130, 200, 513 rows), odd super-block counts per
+    row (K = 768: rows 2 bytes past a dword boundary), K splits reduced in the workspace, fp16 X
+    directly and bf16 / f32 X through the workspace; every output against the float64 oracle."""
+    if splits is not None:
+        monkeypatch.setenv("VYBDQ_KQ2_SPLITS", splits)
+    rng = np.random.default_rng(M + N + K + ty + 5)
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = synth.activations(rng, (M, K))
+    xd, x64 = x_as(x, xdt.split("_")[0], dev)
+    W = to_dev(raw, dev)
+    y = (_gemm_ws(ty, W, xd.reshape(M, K), N, K, dev) if xdt.endswith("_ws")
+         else ops.gemm(ty, W, xd.reshape(M, K), N, K)).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x64.reshape(M, K), matrix_ref(ty, raw, N, K))
+    assert matmul.rel_maxnorm(y, ref) < TOL
+
+
+@pytest.mark.parametrize("ty", TILE128)
+@pytest.mark.parametrize("ydt", [torch.float16, torch.bfloat16, torch.float64])
+@pytest.mark.parametrize("splits", ["1", "3"])
+def test_gemm_128row_tiles_residual_ldy(dev, monkeypatch, ty, ydt, splits):
+    """Residual of the output type and a row stride wider than N, in the tile epilogue (one split)
+    and in the split reduce."""
+    monkeypatch.setenv("VYBDQ_KQ2_SPLITS", splits)
+    M, N, K, ldy = 150, 256, 1024, 300
+    rng = np.random.default_rng(ty + 21 + int(splits))
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = synth.activations(rng, (M, K))
+    rs = torch.from_numpy(synth.activations(rng, (M, ldy)).astype(np.float64)).to(ydt)
+    y = rs.clone().to(dev)
+    Wd, Xd = to_dev(raw, dev), to_dev(x, dev)  # held until the launch has run
+    ws = ops.GemmWorkspace([(M, N, K)], dev, ty)
+    from vybforge_amd._lib import call
+    call("vybdq_gemm_ws", ty, Wd.data_ptr(), Xd.data_ptr(), y.data_ptr(), M, N, K, ops.F32, ops._dt(ydt), ldy,
+         y.data_ptr(), ws.ptr, ws.nbytes, torch.cuda.current_stream().cuda_stream)
+    got = y.to(torch.float64).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x, matrix_ref(ty, raw, N, K), rs.to(torch.float64).numpy()[:, :N])
+    assert gate(got[:, :N], ref, ydt) < TOL
+    np.testing.assert_array_equal(got[:, N:], rs.to(torch.float64).numpy()[:, N:])  # columns past N untouched
+
+
+@pytest.mark.parametrize("ty", TILE128)
+@pytest.mark.parametrize("kind", ["outlier", "offset", "fp16_limit", "tiny", "huge"])
+def test_gemm_128row_tiles_activation_range(dev, ty, kind):
+    """f32 X of any magnitude through the workspace: each row is converted to fp16 after a
+    power-of-two scale that is multiplied back into its outputs."""
+    M, N, K = 128, 512, 2560
+    kinds = ["outlier", "offset", "fp16_limit", "tiny", "huge"]
+    rng = np.random.default_rng(400 + 10 * ty + kinds.index(kind))
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = _x_pattern(kind, rng, M, K)
+    y = _gemm_ws(ty, to_dev(raw, dev), to_dev(x, dev), N, K, dev).cpu().numpy()
+    ref = matmul.gemm_rows_f64(x.astype(np.float64), matrix_ref(ty, raw, N, K))
+    assert np.all(np.isfinite(y))
+    assert matmul.rel_maxnorm(y, ref) < TOL

@@ -38,6 +38,9 @@ int mmq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
              int64_t ldy, const void *RS, void *ws, int64_t ws_bytes, hipStream_t s);
 int64_t mmq_i8_workspace_size(int64_t M, int64_t N, int64_t K);
 // the super-block (Q4_K, Q5_K, Q6_K, IQ2_S) GEMM (kqgemm.hip)
+int64_t kq2_workspace_size(int wtype, int64_t M, int64_t N, int64_t K);
+int kq2_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
+             int64_t ldy, const void *RS, void *ws, int64_t ws_bytes, hipStream_t s);
 int kq_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
             int64_t ldy, const void *RS, hipStream_t s);
 int mmq_i8_gemm(const void *W, const int8_t *Xq, const float *Xs, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
@@ -445,6 +448,7 @@ static int gemm_check(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, 
 }
 
 extern "C" int64_t vybdq_gemm_workspace_size(int wtype, int64_t M, int64_t N, int64_t K) {
+  if (wtype == 14 || wtype == 22) return M >= 1 && N >= 64 && K >= 256 ? kq2_workspace_size(wtype, M, N, K) : 0;
   if ((wtype != 2 && wtype != 8 && wtype != 12 && wtype != 13) || M < 64 || !mmq_supported(M, N, K)) return 0;
   return mmq_workspace_size(wtype, M, N, K);
 }
@@ -460,6 +464,13 @@ extern "C" int vybdq_gemm_ws(int wtype, uint64_t W, uint64_t X, uint64_t Y, int6
   // conversion
   const bool q4k_ok = (wtype == 12 || wtype == 13) && M >= 64 && K < (int64_t(1) << 22) && mmq_supported(M, N, K) &&
                       (x_dt == VYBDQ_F16 || (ws && ws_bytes >= mmq_workspace_size(wtype, M, N, K)));
+  if (wtype == 14 || wtype == 22) {  // 128-row tiles over the workspace's fp16 copy of X
+    const int r = kq2_gemm(wtype, reinterpret_cast<const void *>(W), reinterpret_cast<const void *>(X), x_dt,
+                           reinterpret_cast<void *>(Y), y_dt, M, N, K, ldy ? ldy : N,
+                           reinterpret_cast<const void *>(RS), ws ? reinterpret_cast<void *>(ws) : nullptr,
+                           ws ? ws_bytes : 0, as_stream(stream));
+    if (r != 1) return r;
+  }
   if ((wtype <= 8 && M >= 64 && mmq_supported(M, N, K)) || q4k_ok)
     return mmq_gemm(wtype, reinterpret_cast<const void *>(W), reinterpret_cast<const void *>(X), x_dt,
                     reinterpret_cast<void *>(Y), y_dt, M, N, K, ldy ? ldy : N, reinterpret_cast<const void *>(RS),
@@ -490,6 +501,10 @@ extern "C" int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t
   if ((wtype == 12 || wtype == 13) && x_dt == VYBDQ_F16 && M >= 64 && K < (int64_t(1) << 22) &&
       mmq_supported(M, N, K))
     return mmq_gemm(wtype, a.W, a.X, x_dt, a.Y, y_dt, M, N, K, a.ldy, a.RS, nullptr, 0, s);
+  if ((wtype == 14 || wtype == 22) && x_dt == VYBDQ_F16) {  // fp16 X from 96 rows: 128-row tiles
+    const int r = kq2_gemm(wtype, a.W, a.X, x_dt, a.Y, y_dt, M, N, K, a.ldy, a.RS, nullptr, 0, s);
+    if (r != 1) return r;
+  }
   if (wtype >= 12) return kq_gemm(wtype, a.W, a.X, x_dt, a.Y, y_dt, M, N, K, a.ldy, a.RS, s);
   if (M >= 64 && mmq_supported(M, N, K))
     return mmq_gemm(wtype, a.W, a.X, x_dt, a.Y, y_dt, M, N, K, a.ldy, a.RS, nullptr, 0, s);

@@ -20,6 +20,7 @@
 // X is converted to fp16: activations must stay below 65504 in magnitude.
 #include "gemv_dev.h"
 
+#include <cstdlib>
 #include <type_traits>
 
 namespace vybdq {
@@ -58,96 +59,94 @@ __device__ __forceinline__ void store_run32(_Float16 *dst, const uint32_t (&v)[1
   for (int i = 0; i < 4; ++i) p[i] = u4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
 }
 
-// Decode unit g (64 weights) of the super-block whose windows dw holds into the weight row `row`
-// of the LDS tile (element e of the super-block at row[e]).
+// Decode run h (0 or 1: 32 weights) of unit g (64 weights) of the super-block whose windows dw
+// holds into 32 fp16 at dst (16-byte aligned); run_elem<FMT>(g, h) is the super-block element of
+// dst[0]. Every weight is computed exactly as the decode gate does (float32, one rounding, then
+// one rounding to fp16).
 template <int FMT>
-__device__ __forceinline__ void kq_unit_to_lds(const uint32_t (&dw)[Fmt<FMT>::PAIR_DWORDS], int g, _Float16 *row) {
+__device__ __forceinline__ int run_elem(int g, int h) {
+  if constexpr (FMT == FMT_Q6_K) return 128 * (g >> 1) + 64 * h + 32 * (g & 1);
+  else return 64 * g + 32 * h;
+}
+
+template <int FMT>
+__device__ __forceinline__ void kq_run_to_lds(const uint32_t (&dw)[Fmt<FMT>::PAIR_DWORDS], int g, int h, _Float16 *dst) {
+  uint32_t out[16];
   if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q5_K) {
-    // sub-blocks 2g (low nibbles of qs[32g..]) and 2g+1 (high nibbles): elements 64g .. 64g+63;
+    // sub-block 2g + h (h = 0: low nibbles of qs[32g..], h = 1: high nibbles);
     // w = d*sc*q - dmin*m as the decode gate computes it (one fma)
     constexpr int QS = FMT == FMT_Q4_K ? 4 : 12;
     const float d = half_bits_to_f32(dw[0] & 0xffffu);
     const float dmin = half_bits_to_f32(dw[0] >> 16);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float sc, mn;
-      scale_min_k4(dw[1], dw[2], dw[3], 2 * g + h, sc, mn);
-      const float ds = d * sc, dm = dmin * mn;
-      uint32_t out[16];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        uint32_t v = h == 0 ? (dw[QS + t] & 0x0F0F0F0Fu) : ((dw[QS + t] >> 4) & 0x0F0F0F0Fu);
-        if constexpr (FMT == FMT_Q5_K) v |= ((dw[4 + t] >> (2 * g + h)) & 0x01010101u) << 4;
-        float w[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) w[b] = fmaf(ds, static_cast<float>((v >> (8 * b)) & 0xffu), -dm);
-        out[2 * t] = pack_h2(w[0], w[1]);
-        out[2 * t + 1] = pack_h2(w[2], w[3]);
-      }
-      store_run32(row + 64 * g + 32 * h, out);
-    }
-  } else if constexpr (FMT == FMT_Q6_K) {
-    // unit g = (half hf, part): low nibbles of ql[64hf + 32part ..] are elements
-    // 128hf + 32part + l, high nibbles 128hf + 64 + 32part + l; w = d*sc*(q - 32), exact in f32
-    const int hf = g >> 1, part = g & 1;
-    const uint32_t sh = dw[22];
-    uint32_t ql[8], qh[8];
+    float sc, mn;
+    scale_min_k4(dw[1], dw[2], dw[3], 2 * g + h, sc, mn);
+    const float ds = d * sc, dm = dmin * mn;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      ql[t] = __builtin_amdgcn_alignbit(dw[t + 1], dw[t], sh);
-      qh[t] = __builtin_amdgcn_alignbit(dw[9 + t + 1], dw[9 + t], sh);
+      uint32_t v = h == 0 ? (dw[QS + t] & 0x0F0F0F0Fu) : ((dw[QS + t] >> 4) & 0x0F0F0F0Fu);
+      if constexpr (FMT == FMT_Q5_K) v |= ((dw[4 + t] >> (2 * g + h)) & 0x01010101u) << 4;
+      float w[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) w[b] = fmaf(ds, static_cast<float>((v >> (8 * b)) & 0xffu), -dm);
+      out[2 * t] = pack_h2(w[0], w[1]);
+      out[2 * t + 1] = pack_h2(w[2], w[3]);
     }
-    const uint32_t sc0 = __builtin_amdgcn_alignbit(dw[19], dw[18], sh);  // scales[8hf + 0..3]
-    const uint32_t sc1 = __builtin_amdgcn_alignbit(dw[20], dw[19], sh);  // scales[8hf + 4..7]
+  } else if constexpr (FMT == FMT_Q6_K) {
+    // unit g = (half hf, part): low nibbles of ql[64hf + 32part ..] (h = 0) are elements
+    // 128hf + 32part + l, high nibbles (h = 1) 128hf + 64 + 32part + l; w = d*sc*(q - 32), exact
+    // in f32
+    const int part = g & 1;
+    const uint32_t sh = dw[22];
+    const int hs = h == 0 ? 2 * part : 4 + 2 * part;
+    const uint32_t scw = __builtin_amdgcn_alignbit(dw[19 + h], dw[18 + h], sh);  // scales[8hf + 4h ..]
     const float d = half_bits_to_f32(dw[21]);
+    const float ds0 = d * static_cast<float>(static_cast<int8_t>(__builtin_amdgcn_ubfe(scw, 16 * part, 8)));
+    const float ds1 = d * static_cast<float>(static_cast<int8_t>(__builtin_amdgcn_ubfe(scw, 16 * part + 8, 8)));
 #pragma unroll
-    for (int nh = 0; nh < 2; ++nh) {
-      const int hs = nh == 0 ? 2 * part : 4 + 2 * part;
-      const uint32_t scw = nh == 0 ? sc0 : sc1;
-      const float ds0 = d * static_cast<float>(static_cast<int8_t>(__builtin_amdgcn_ubfe(scw, 16 * part, 8)));
-      const float ds1 = d * static_cast<float>(static_cast<int8_t>(__builtin_amdgcn_ubfe(scw, 16 * part + 8, 8)));
-      uint32_t out[16];
+    for (int t = 0; t < 8; ++t) {
+      const uint32_t ql = __builtin_amdgcn_alignbit(dw[t + 1], dw[t], sh);
+      const uint32_t qh = __builtin_amdgcn_alignbit(dw[9 + t + 1], dw[9 + t], sh);
+      const uint32_t v = (h == 0 ? (ql & 0x0F0F0F0Fu) : ((ql >> 4) & 0x0F0F0F0Fu)) | (((qh >> hs) & 0x03030303u) << 4);
+      const float ds = t < 4 ? ds0 : ds1;  // elements 4t .. 4t+3: scale of the 16-element half
+      float w[4];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const uint32_t v = (nh == 0 ? (ql[t] & 0x0F0F0F0Fu) : ((ql[t] >> 4) & 0x0F0F0F0Fu)) |
-                           (((qh[t] >> hs) & 0x03030303u) << 4);
-        const float ds = t < 4 ? ds0 : ds1;  // elements 4t .. 4t+3: scale of the 16-element half
-        float w[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) w[b] = ds * static_cast<float>(static_cast<int>((v >> (8 * b)) & 0xffu) - 32);
-        out[2 * t] = pack_h2(w[0], w[1]);
-        out[2 * t + 1] = pack_h2(w[2], w[3]);
-      }
-      store_run32(row + 128 * hf + 64 * nh + 32 * part, out);
+      for (int b = 0; b < 4; ++b) w[b] = ds * static_cast<float>(static_cast<int>((v >> (8 * b)) & 0xffu) - 32);
+      out[2 * t] = pack_h2(w[0], w[1]);
+      out[2 * t + 1] = pack_h2(w[2], w[3]);
     }
   } else {
-    // IQ2_S unit g = groups 8g .. 8g+7 of 8 weights = elements 64g .. 64g+63; group l: grid entry
-    // qs | 2 qh bits << 8, sign byte, scale d * (0.5 + 4-bit) / 4 per 16 weights (exact in f32)
+    // IQ2_S unit g = groups 8g .. 8g+7 of 8 weights = elements 64g .. 64g+63, run h = groups
+    // 8g + 4h ..; group l: grid entry qs | 2 qh bits << 8, sign byte, scale d * (0.5 + 4-bit) / 4
+    // per 16 weights (exact in f32)
     const uint32_t sh = dw[9];
-    const uint32_t ix[2] = {__builtin_amdgcn_alignbit(dw[1], dw[0], sh), __builtin_amdgcn_alignbit(dw[2], dw[1], sh)};
-    const uint32_t sg[2] = {__builtin_amdgcn_alignbit(dw[4], dw[3], sh), __builtin_amdgcn_alignbit(dw[5], dw[4], sh)};
+    const uint32_t ix = __builtin_amdgcn_alignbit(dw[1 + h], dw[h], sh);
+    const uint32_t sg = __builtin_amdgcn_alignbit(dw[4 + h], dw[3 + h], sh);
     const float d = half_bits_to_f32(dw[8]) * 0.25f;
 #pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-      uint32_t out[16];
+    for (int l2 = 0; l2 < 4; ++l2) {
+      const uint32_t idx = __builtin_amdgcn_ubfe(ix, 8 * l2, 8) | (__builtin_amdgcn_ubfe(dw[6], 8 * h + 2 * l2, 2) << 8);
+      const unsigned long long e = kIq2sGrid[idx];
+      const uint32_t sgn = __builtin_amdgcn_ubfe(sg, 8 * l2, 8);
+      const float dl = d * (0.5f + static_cast<float>(__builtin_amdgcn_ubfe(dw[7], 8 * h + 4 * (l2 >> 1), 4)));
+      float w[8];
 #pragma unroll
-      for (int l2 = 0; l2 < 4; ++l2) {
-        const uint32_t idx = __builtin_amdgcn_ubfe(ix[hb], 8 * l2, 8) | (__builtin_amdgcn_ubfe(dw[6], 8 * hb + 2 * l2, 2) << 8);
-        const unsigned long long e = kIq2sGrid[idx];
-        const uint32_t sgn = __builtin_amdgcn_ubfe(sg[hb], 8 * l2, 8);
-        const float dl = d * (0.5f + static_cast<float>(__builtin_amdgcn_ubfe(dw[7], 8 * hb + 4 * (l2 >> 1), 4)));
-        float w[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float v = dl * static_cast<float>(static_cast<uint32_t>(e >> (8 * j)) & 0xffu);
-          w[j] = ((sgn >> j) & 1u) ? -v : v;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) out[4 * l2 + j] = pack_h2(w[2 * j], w[2 * j + 1]);
+      for (int j = 0; j < 8; ++j) {
+        const float v = dl * static_cast<float>(static_cast<uint32_t>(e >> (8 * j)) & 0xffu);
+        w[j] = ((sgn >> j) & 1u) ? -v : v;
       }
-      store_run32(row + 64 * g + 32 * hb, out);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) out[4 * l2 + j] = pack_h2(w[2 * j], w[2 * j + 1]);
     }
   }
+  store_run32(dst, out);
+}
+
+// Decode unit g (64 weights) of the super-block whose windows dw holds into the weight row `row`
+// of the LDS tile (element e of the super-block at row[e]).
+template <int FMT>
+__device__ __forceinline__ void kq_unit_to_lds(const uint32_t (&dw)[Fmt<FMT>::PAIR_DWORDS], int g, _Float16 *row) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) kq_run_to_lds<FMT>(dw, g, h, row + run_elem<FMT>(g, h));
 }
 
 // 8 consecutive X elements (row offset off) -> 8 fp16 in a u4
@@ -326,6 +325,414 @@ static int kq_pb_launch(int xdt, const int64_t *pb, uint32_t *status, hipStream_
   if (xdt == VYBDQ_F16) hipLaunchKernelGGL((k_kq_gemm_pb<FMT, VYBDQ_F16>), dim3(grid), dim3(256), 0, s, pb, status);
   else hipLaunchKernelGGL((k_kq_gemm_pb<FMT, VYBDQ_F32>), dim3(grid), dim3(256), 0, s, pb, status);
   return check_launch("p-block super-block gemm");
+}
+
+// ---- 128-row tiles over fp16 X (Q6_K, IQ2_S from 96 rows) ----------------------------------
+//
+// Tile = 128 X rows x 64 weight rows, K step = 128 (half a super-block = four 32-weight runs).
+// Four waves in a 2 x 2 grid each own 64 rows x 32 columns (4 x 2 accumulator fragments), so per
+// 32-k slice a wave reads 6 operand fragments from LDS for 8 MFMAs (the 64-row tile above reads 5
+// for 4); each weight is decoded once per 128 X rows. Wave w decodes run w of the step for all 64
+// weight rows (lane = row), so every run-dependent choice is wave-uniform and every address is a
+// wave-uniform base plus a per-lane offset that does not change from step to step. The run's
+// weights are formed in fp16 arithmetic: Q6_K as fp16(d·sc) × (q − 32) (q − 32 exact from the
+// 0x64vv bit pattern), IQ2_S as the grid's magnitude bytes (one 8-byte grid row per 8 weights)
+// × fp16(d·(0.5 + s)/4) with the sign bits applied:
+// each weight differs from the decode's fp16 value by at most the rounding of the scale and one
+// product rounding. X is fp16: the caller's, or the workspace copy that x_rows_to_f16 made with
+// a power-of-two scale per row (xscale), multiplied back into the outputs. Split K: each split
+// writes f32 partials [split][M][N] to the workspace and k_kq_reduce sums them in split order and
+// applies the epilogue. Three workgroups share a CU (52 KB of LDS each).
+constexpr int kK2BM = 128, kK2BN = 64, kK2BK = 128;
+constexpr int kK2Lda = kK2BK + 8;  // fp16 row stride in LDS (16-B pad)
+
+struct Kq2Args {
+  const uint8_t *W;      // weight rows, rowbytes apart
+  uint32_t rowbytes;
+  const _Float16 *X;     // [M][K] fp16
+  const float *xscale;   // per X row (null: 1)
+  int M, N, K;
+  int S2;                // 128-k steps per row (K / 128)
+  int m_tiles, n_tiles, splits, sps;
+  int xcd;               // 1: workgroups of one XCD take consecutive units
+  void *Y;
+  int ydt;
+  int64_t ldy;
+  const void *RS;
+  float *part;           // splits > 1: [splits][M][N] f32 partials
+};
+
+template <int FMT> struct K2Run;
+// Q6_K run (half hf, part, nibble nh): ql[64hf + 32part ..] and qh[32hf ..] as 9-dword windows,
+// the run's two scale bytes, d
+template <> struct K2Run<FMT_Q6_K> { static constexpr int DW = 20; };
+// IQ2_S run (sub-block j): its 4 grid-index bytes and 4 sign bytes as 2-dword windows, qh[j],
+// scales[j], d
+template <> struct K2Run<FMT_IQ2_S> { static constexpr int DW = 7; };
+
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t *base, uint32_t off) {
+  return *reinterpret_cast<const uint32_t *>(base + off);
+}
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *base, uint32_t off) {
+  return *reinterpret_cast<const uint16_t *>(base + off);
+}
+
+// Loads of run r for the super-block at sbase + o (o: this lane's byte offset, 2-byte aligned)
+template <int FMT>
+__device__ __forceinline__ void k2_load_run(const uint8_t *sbase, uint32_t o, int hf, int r,
+                                            uint32_t (&d)[K2Run<FMT>::DW]) {
+  if constexpr (FMT == FMT_Q6_K) {
+    const int part = r >> 1, nh = r & 1;
+    const uint32_t of = o & ~3u;
+    const uint8_t *ql = sbase + 64 * hf + 32 * part, *qh = sbase + 128 + 32 * hf;
+    const u4a4 a0 = *reinterpret_cast<const u4a4 *>(ql + of), a1 = *reinterpret_cast<const u4a4 *>(ql + of + 16);
+    const u4a4 b0 = *reinterpret_cast<const u4a4 *>(qh + of), b1 = *reinterpret_cast<const u4a4 *>(qh + of + 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      d[i] = a0[i];
+      d[4 + i] = a1[i];
+      d[9 + i] = b0[i];
+      d[13 + i] = b1[i];
+    }
+    d[8] = ld_u32(ql, of + 32);
+    d[17] = ld_u32(qh, of + 32);
+    d[18] = ld_u16(sbase + 192 + 8 * hf + 4 * nh + 2 * part, o);  // scales of the run's two 16-halves
+    d[19] = ld_u16(sbase + 208, o);                                 // d
+  } else {
+    const int j = 4 * hf + r;
+    const uint32_t of = (o + 2) & ~3u;  // the index and sign windows start 2 bytes past o
+    const uint8_t *ix = sbase + 2 + 4 * j - 2, *sg = sbase + 34 + 4 * j - 2;
+    d[0] = ld_u32(ix, of);
+    d[1] = ld_u32(ix, of + 4);
+    d[2] = ld_u32(sg, of);
+    d[3] = ld_u32(sg, of + 4);
+    d[4] = *(sbase + 66 + j + o);  // qh of sub-block j
+    d[5] = *(sbase + 74 + j + o);  // its two 4-bit scales
+    d[6] = ld_u16(sbase, o);       // d
+  }
+}
+
+// 32 fp16 weights of the run (as 16 packed pairs) from its loads; sh = 16 when the lane's windows
+// start 2 bytes past the dword they were loaded from
+template <int FMT>
+__device__ __forceinline__ void k2_decode_run(const uint32_t (&d)[K2Run<FMT>::DW], uint32_t sh, int r,
+                                              uint32_t (&out)[16]) {
+  if constexpr (FMT == FMT_Q6_K) {
+    const int part = r >> 1, nh = r & 1;
+    const uint32_t qls = 4 * nh, qhs = 2 * part + 4 * nh;  // nibble of ql, bit pair of qh
+    const float dd = half_bits_to_f32(d[19]);
+    const h2 ds0 = {static_cast<_Float16>(dd * static_cast<float>(static_cast<int8_t>(d[18] & 0xffu))),
+                    static_cast<_Float16>(dd * static_cast<float>(static_cast<int8_t>(d[18] & 0xffu)))};
+    const h2 ds1 = {static_cast<_Float16>(dd * static_cast<float>(static_cast<int8_t>(d[18] >> 8))),
+                    static_cast<_Float16>(dd * static_cast<float>(static_cast<int8_t>(d[18] >> 8)))};
+    const h2 bias = {static_cast<_Float16>(-1056.0f), static_cast<_Float16>(-1056.0f)};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const uint32_t ql = __builtin_amdgcn_alignbit(d[t + 1], d[t], sh) >> qls;
+      const uint32_t qh = (__builtin_amdgcn_alignbit(d[9 + t + 1], d[9 + t], sh) >> qhs) & 0x03030303u;
+      const uint32_t v = (ql & 0x0F0F0F0Fu) | (qh << 4);  // 4 six-bit q in bytes
+      // bytes b -> fp16 halves 0x64bb = 1024 + b; minus 1056 = q - 32 exactly; times the scale
+      const h2 p0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u));
+      const h2 p1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u));
+      const h2 ds = t < 4 ? ds0 : ds1;  // elements 4t .. 4t+3: scale of the 16-element half
+      out[2 * t] = __builtin_bit_cast(uint32_t, (p0 + bias) * ds);
+      out[2 * t + 1] = __builtin_bit_cast(uint32_t, (p1 + bias) * ds);
+    }
+  } else {
+    const uint32_t ix = __builtin_amdgcn_alignbit(d[1], d[0], sh);
+    const uint32_t sg = __builtin_amdgcn_alignbit(d[3], d[2], sh);
+    const float dd = half_bits_to_f32(d[6]) * 0.25f;
+    const h2 bias = {static_cast<_Float16>(-1024.0f), static_cast<_Float16>(-1024.0f)};
+#pragma unroll
+    for (int l2 = 0; l2 < 4; ++l2) {
+      const uint32_t idx = __builtin_amdgcn_ubfe(ix, 8 * l2, 8) | (__builtin_amdgcn_ubfe(d[4], 2 * l2, 2) << 8);
+      const unsigned long long e = kIq2sGrid[idx];  // 8 magnitude bytes
+      const uint32_t e0 = static_cast<uint32_t>(e), e1 = static_cast<uint32_t>(e >> 32);
+      const uint32_t sgn = __builtin_amdgcn_ubfe(sg, 8 * l2, 8);
+      const float dl = dd * (0.5f + static_cast<float>(__builtin_amdgcn_ubfe(d[5], 4 * (l2 >> 1), 4)));
+      const h2 dh = {static_cast<_Float16>(dl), static_cast<_Float16>(dl)};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        // bytes -> fp16 1024 + b, minus 1024 (exact), times the scale; sign bits 2k, 2k+1 of the
+        // sign byte -> bits 15, 31
+        const uint32_t src = k < 2 ? e0 : e1;
+        const h2 p = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, src, k & 1 ? 0x04030402u : 0x04010400u));
+        const uint32_t m = ((sgn >> (2 * k)) & 1u) << 15 | ((sgn >> (2 * k + 1)) & 1u) << 31;
+        out[4 * l2 + k] = __builtin_bit_cast(uint32_t, (p + bias) * dh) ^ m;
+      }
+    }
+  }
+}
+
+template <int FMT>
+__global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
+  constexpr int DW = K2Run<FMT>::DW;
+  __shared__ __attribute__((aligned(16))) _Float16 As[kK2BM * kK2Lda];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[kK2BN * kK2Lda];
+
+  const int units = a.m_tiles * a.n_tiles * a.splits;
+  int u = static_cast<int>(blockIdx.x);
+  if (a.xcd) u = (u & 7) * (units >> 3) + (u >> 3);  // workgroups are dealt to the 8 XCDs in turn
+  const int mn_tiles = a.m_tiles * a.n_tiles;
+  const int split = u / mn_tiles;
+  const int mn = u - split * mn_tiles;
+  // weight tiles fastest: the workgroups of one XCD share one 128-row X tile (K/splits x 256 B,
+  // held in the XCD's L2) and stream the weight tiles; X is read 4 x as many bytes per step as
+  // the weights
+  const int nt = mn % a.n_tiles, mt = mn / a.n_tiles;
+  const int s0 = split * a.sps;
+  const int s1 = s0 + a.sps < a.S2 ? s0 + a.sps : a.S2;
+  const int row0 = mt * kK2BM;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave >> 1, wc = wave & 1;
+
+  // decode task: run `wave` of the step for weight row `lane`
+  const uint8_t *wtile = a.W + static_cast<int64_t>(nt) * kK2BN * a.rowbytes;
+  const uint32_t wlane = static_cast<uint32_t>(lane) * a.rowbytes;
+  constexpr int SB = KqSb<FMT>::BYTES;
+  _Float16 *bdst = Bs + lane * kK2Lda + (FMT == FMT_Q6_K ? 64 * (wave & 1) + 32 * (wave >> 1) : 32 * wave);
+  // X task: chunk c = tid + 256 i: tile row c >> 4, k offset 8 (c & 15) (a wave loads 4 rows x
+  // 256 contiguous bytes per instruction; fragment-ordered loads of 16 rows x 64 B measured 28%
+  // slower); rows past M read row M - 1 (they feed only outputs that are never stored); byte
+  // offsets (M K < 2^30)
+  uint32_t xoff[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = tid + 256 * i;
+    int m = row0 + (c >> 4);
+    m = m < a.M ? m : a.M - 1;
+    xoff[i] = 2u * (static_cast<uint32_t>(m) * static_cast<uint32_t>(a.K) + 8u * static_cast<uint32_t>(c & 15));
+  }
+  const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.X);
+
+  f4 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  uint32_t dw[DW];
+  u4 xr[8];
+  uint32_t sh = 0;
+  auto load_step = [&](int s) {
+    const int sbi = s >> 1;
+    const uint32_t o = wlane + static_cast<uint32_t>(sbi) * SB;  // this lane's super-block
+    k2_load_run<FMT>(wtile, o, s & 1, wave, dw);
+    sh = FMT == FMT_Q6_K ? ((o & 2) ? 16u : 0u) : ((o & 2) ? 0u : 16u);
+    const uint8_t *xs = xb + static_cast<int64_t>(s) * (2 * kK2BK);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xr[i] = *reinterpret_cast<const u4 *>(xs + xoff[i]);
+  };
+  auto bar = [] {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS accesses are done
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+  };
+
+  if (s0 < s1) load_step(s0);
+  for (int s = s0; s < s1; ++s) {
+    {
+      uint32_t w[16];
+      k2_decode_run<FMT>(dw, sh, wave, w);
+      store_run32(bdst, w);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<u4 *>(As + (c >> 4) * kK2Lda + 8 * (c & 15)) = xr[i];
+    }
+    if (s + 1 < s1) load_step(s + 1);  // the next step's loads run under this step's MFMAs
+    bar();
+#pragma unroll
+    for (int kk = 0; kk < kK2BK / 32; ++kk) {
+      kh8 bf[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bf[j] = *reinterpret_cast<const kh8 *>(Bs + (32 * wc + 16 * j + (lane & 15)) * kK2Lda + 32 * kk + 8 * (lane >> 4));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const kh8 af =
+            *reinterpret_cast<const kh8 *>(As + (64 * wr + 16 * i + (lane & 15)) * kK2Lda + 32 * kk + 8 * (lane >> 4));
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+      }
+    }
+    bar();
+  }
+
+  // acc[i][j][q] = C[row0 + 64 wr + 16 i + 4 (lane >> 4) + q][64 nt + 32 wc + 16 j + (lane & 15)]
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int m = row0 + 64 * wr + 16 * i + 4 * (lane >> 4) + q;
+      if (m >= a.M) continue;
+      const float xs = a.xscale ? a.xscale[m] : 1.0f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t n = static_cast<int64_t>(nt) * kK2BN + 32 * wc + 16 * j + (lane & 15);
+        if (a.splits > 1) {
+          a.part[(static_cast<int64_t>(split) * a.M + m) * a.N + n] = acc[i][j][q];
+          continue;
+        }
+        const int64_t idx = static_cast<int64_t>(m) * a.ldy + n;
+        const float v = acc[i][j][q] * xs;
+        switch (a.ydt) {
+          case VYBDQ_F32: store_elem<VYBDQ_F32>(a.Y, a.RS, idx, v); break;
+          case VYBDQ_F16: store_elem<VYBDQ_F16>(a.Y, a.RS, idx, v); break;
+          case VYBDQ_BF16: store_elem<VYBDQ_BF16>(a.Y, a.RS, idx, v); break;
+          default: store_elem<VYBDQ_F64>(a.Y, a.RS, idx, v); break;
+        }
+      }
+    }
+}
+
+// Sum of the split partials in split order, times the X row scale, then the epilogue; four
+// consecutive columns per thread (N % 64 == 0).
+template <int YDT>
+__global__ void __launch_bounds__(256) k_kq_reduce(const float *__restrict__ part, int splits, int M, int N,
+                                                  const float *__restrict__ xscale, void *Y, int64_t ldy,
+                                                  const void *RS) {
+  const int64_t mn = static_cast<int64_t>(M) * N;
+  const int64_t n4 = mn / 4;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; e < n4;
+       e += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t i0 = 4 * e;
+    f4 v = *reinterpret_cast<const f4 *>(part + i0);
+    for (int sp = 1; sp < splits; ++sp) {
+      const f4 w = *reinterpret_cast<const f4 *>(part + sp * mn + i0);
+      v = v + w;
+    }
+    const int64_t m = i0 / N, n = i0 - m * N;
+    const float xs = xscale ? xscale[m] : 1.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) store_elem<YDT>(Y, RS, m * ldy + n + q, v[q] * xs);
+  }
+}
+
+struct Kq2Plan {
+  int m_tiles, n_tiles, splits, sps;
+  int64_t part_bytes;
+};
+
+// K split minimising the busiest CU's time plus the partial traffic (written once, read back
+// once). Three workgroups fit a CU; a CU with c workgroups runs them three at a time, and a step
+// costs (MI355X, Q6_K at the prefill shapes, in µs per step of the group) 3.4 with three resident,
+// 2.72 with two, 2.2 with one.
+static Kq2Plan kq2_plan(int M, int N, int S2, bool allow_split) {
+  const int cus = device_cu_count();
+  const int m_tiles = (M + kK2BM - 1) / kK2BM, n_tiles = N / kK2BN;
+  Kq2Plan best{m_tiles, n_tiles, 1, S2, 0};
+  double best_t = -1;
+  for (int splits = 1; splits <= (allow_split ? 8 : 1) && splits <= S2; ++splits) {
+    const int sps = (S2 + splits - 1) / splits;
+    if ((splits - 1) * sps >= S2) continue;
+    const int64_t units = static_cast<int64_t>(m_tiles) * n_tiles * splits;
+    const int64_t c = (units + cus - 1) / cus;
+    const double rem = c % 3 == 0 ? 0.0 : (c % 3 == 2 ? 2.72 : 2.2);
+    double t = sps * (static_cast<double>(c / 3) * 3.4 + rem);
+    if (splits > 1) t += static_cast<double>(M) * N * 4 * (splits + 1) / 5.0e6 + 3.0;
+    if (best_t < 0 || t < best_t - 1e-9) {
+      best_t = t;
+      best.splits = splits;
+      best.sps = sps;
+    }
+  }
+  // tuning / test override: VYBDQ_KQ2_SPLITS=n (ignored when it does not fit the shape)
+  if (const char *ov = tuning_env("VYBDQ_KQ2_SPLITS")) {
+    const int splits = atoi(ov);
+    if (splits >= 1 && splits <= 8 && splits <= S2 && (splits == 1 || allow_split)) {
+      const int sps = (S2 + splits - 1) / splits;
+      if ((splits - 1) * sps < S2) {
+        best.splits = splits;
+        best.sps = sps;
+      }
+    }
+  }
+  best.part_bytes = best.splits > 1 ? static_cast<int64_t>(best.splits) * M * N * 4 : 0;
+  return best;
+}
+
+static int64_t kq_align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+// 32-bit byte offsets: X (M K fp16), a weight tile (64 rows)
+bool kq2_supported(int wtype, int64_t M, int64_t N, int64_t K) {
+  return (wtype == 14 || wtype == 22) && M >= 96 && M * K < (int64_t(1) << 30) && M * N < (int64_t(1) << 31) &&
+         N % 64 == 0 && K % 256 == 0 && K < (int64_t(1) << 24);
+}
+
+// workspace: [split partials][fp16 copy of X][X row scales]
+int64_t kq2_workspace_size(int wtype, int64_t M, int64_t N, int64_t K) {
+  if (!kq2_supported(wtype, M, N, K)) return 0;
+  const Kq2Plan p = kq2_plan(static_cast<int>(M), static_cast<int>(N), static_cast<int>(K / 128), true);
+  return kq_align256(p.part_bytes) + kq_align256(M * K * 2) + kq_align256(M * 4);
+}
+
+int x_rows_to_f16(const void *X, int xdt, int64_t M, int64_t K, void *xh, float *xscale, hipStream_t s);
+
+template <int FMT>
+static int kq2_launch(const Kq2Args &a, hipStream_t s) {
+  const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles * a.splits;
+  hipLaunchKernelGGL((k_kq_mm<FMT>), dim3(grid), dim3(256), 0, s, a);
+  return check_launch("super-block gemm (128-row tiles)");
+}
+
+// Q6_K / IQ2_S with fp16 X, or any X with a workspace of kq2_workspace_size bytes. Returns 1 when
+// the call does not fit this path (the caller takes the 64-row tiles).
+int kq2_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
+             int64_t ldy, const void *RS, void *ws, int64_t ws_bytes, hipStream_t s) {
+  if (!kq2_supported(wtype, M, N, K)) return 1;
+  const int S2 = static_cast<int>(K / 128);
+  const int64_t need_x = xdt == VYBDQ_F16 ? 0 : kq_align256(M * K * 2) + kq_align256(M * 4);
+  if (need_x && (!ws || ws_bytes < need_x)) return 1;
+  Kq2Plan p = kq2_plan(static_cast<int>(M), static_cast<int>(N), S2, ws != nullptr);
+  if (p.splits > 1 && ws_bytes < kq_align256(p.part_bytes) + need_x)
+    p = kq2_plan(static_cast<int>(M), static_cast<int>(N), S2, false);
+  const int64_t xh_off = p.splits > 1 ? kq_align256(p.part_bytes) : 0;
+  const float *xscale = nullptr;
+  if (need_x) {
+    char *base = static_cast<char *>(ws) + xh_off;
+    float *sc = reinterpret_cast<float *>(base + kq_align256(M * K * 2));
+    const int rc = x_rows_to_f16(X, xdt, M, K, base, sc, s);
+    if (rc) return rc;
+    X = base;
+    xscale = sc;
+  }
+  Kq2Args a{};
+  a.W = static_cast<const uint8_t *>(W);
+  a.rowbytes = static_cast<uint32_t>(K / 256 * (wtype == 14 ? KqSb<FMT_Q6_K>::BYTES : KqSb<FMT_IQ2_S>::BYTES));
+  a.X = static_cast<const _Float16 *>(X);
+  a.xscale = xscale;
+  a.M = static_cast<int>(M);
+  a.N = static_cast<int>(N);
+  a.K = static_cast<int>(K);
+  a.S2 = S2;
+  a.m_tiles = p.m_tiles;
+  a.n_tiles = p.n_tiles;
+  a.splits = p.splits;
+  a.sps = p.sps;
+  a.xcd = (static_cast<int64_t>(p.m_tiles) * p.n_tiles * p.splits) % 8 == 0 ? 1 : 0;
+  a.Y = Y;
+  a.ydt = ydt;
+  a.ldy = ldy;
+  a.RS = RS;
+  a.part = p.splits > 1 ? static_cast<float *>(ws) : nullptr;
+  int rc;
+  rc = wtype == 14 ? kq2_launch<FMT_Q6_K>(a, s) : kq2_launch<FMT_IQ2_S>(a, s);
+  if (rc || p.splits == 1) return rc;
+  const int64_t n4 = M * N / 4;
+  const unsigned grid = static_cast<unsigned>(n4 / 256 < 4096 ? (n4 + 255) / 256 : 4096);
+  switch (ydt) {
+    case VYBDQ_F32: hipLaunchKernelGGL(k_kq_reduce<VYBDQ_F32>, dim3(grid), dim3(256), 0, s, a.part, p.splits, a.M, a.N, xscale, Y, ldy, RS); break;
+    case VYBDQ_F16: hipLaunchKernelGGL(k_kq_reduce<VYBDQ_F16>, dim3(grid), dim3(256), 0, s, a.part, p.splits, a.M, a.N, xscale, Y, ldy, RS); break;
+    case VYBDQ_BF16: hipLaunchKernelGGL(k_kq_reduce<VYBDQ_BF16>, dim3(grid), dim3(256), 0, s, a.part, p.splits, a.M, a.N, xscale, Y, ldy, RS); break;
+    default: hipLaunchKernelGGL(k_kq_reduce<VYBDQ_F64>, dim3(grid), dim3(256), 0, s, a.part, p.splits, a.M, a.N, xscale, Y, ldy, RS); break;
+  }
+  return check_launch("super-block gemm split reduce");
 }
 
 // The GEMM kind of vybdq_launch_pblock for wtype 12, 13, 14, 22 (pblock.hip); xdt F32 or F16.
