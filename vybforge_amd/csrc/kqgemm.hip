@@ -332,9 +332,10 @@ static int kq_pb_launch(int xdt, const int64_t *pb, uint32_t *status, hipStream_
 // Tile = 128 X rows x 64 weight rows, K step = 128 (half a super-block = four 32-weight runs).
 // Four waves in a 2 x 2 grid each own 64 rows x 32 columns (4 x 2 accumulator fragments), so per
 // 32-k slice a wave reads 6 operand fragments from LDS for 8 MFMAs (the 64-row tile above reads 5
-// for 4); each weight is decoded once per 128 X rows. Wave w decodes run w of the step for all 64
-// weight rows (lane = row), so every run-dependent choice is wave-uniform and every address is a
-// wave-uniform base plus a per-lane offset that does not change from step to step. The run's
+// for 4); each weight is decoded once per 128 X rows. Thread t decodes run t % 4 of weight row
+// t / 4; run-dependent choices are shift amounts and address offsets (no per-lane indexing of
+// register arrays), and every address is a wave-uniform base plus a per-lane 32-bit offset that
+// does not change from step to step. The run's
 // weights are formed in fp16 arithmetic: Q6_K as fp16(d·sc) × (q − 32) (q − 32 exact from the
 // 0x64vv bit pattern), IQ2_S as the grid's magnitude bytes (one 8-byte grid row per 8 weights)
 // × fp16(d·(0.5 + s)/4) with the sign bits applied:
@@ -377,15 +378,18 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t *base, uint32_t off) {
   return *reinterpret_cast<const uint16_t *>(base + off);
 }
 
-// Loads of run r for the super-block at sbase + o (o: this lane's byte offset, 2-byte aligned)
+// Loads of run r of half hf for the super-block at sbase + o (sbase + 64 hf wave-uniform; o and
+// the run's offsets within the super-block per lane, 32-bit, so every load is a scalar base plus
+// a vector offset)
 template <int FMT>
 __device__ __forceinline__ void k2_load_run(const uint8_t *sbase, uint32_t o, int hf, int r,
                                             uint32_t (&d)[K2Run<FMT>::DW]) {
   if constexpr (FMT == FMT_Q6_K) {
-    const int part = r >> 1, nh = r & 1;
+    const uint32_t part = static_cast<uint32_t>(r) >> 1, nh = static_cast<uint32_t>(r) & 1u;
     const uint32_t of = o & ~3u;
-    const uint8_t *ql = sbase + 64 * hf + 32 * part, *qh = sbase + 128 + 32 * hf;
-    const u4a4 a0 = *reinterpret_cast<const u4a4 *>(ql + of), a1 = *reinterpret_cast<const u4a4 *>(ql + of + 16);
+    const uint8_t *ql = sbase + 64 * hf, *qh = sbase + 128 + 32 * hf;
+    const uint32_t qo = of + 32 * part;
+    const u4a4 a0 = *reinterpret_cast<const u4a4 *>(ql + qo), a1 = *reinterpret_cast<const u4a4 *>(ql + qo + 16);
     const u4a4 b0 = *reinterpret_cast<const u4a4 *>(qh + of), b1 = *reinterpret_cast<const u4a4 *>(qh + of + 16);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -394,21 +398,21 @@ __device__ __forceinline__ void k2_load_run(const uint8_t *sbase, uint32_t o, in
       d[9 + i] = b0[i];
       d[13 + i] = b1[i];
     }
-    d[8] = ld_u32(ql, of + 32);
+    d[8] = ld_u32(ql, qo + 32);
     d[17] = ld_u32(qh, of + 32);
-    d[18] = ld_u16(sbase + 192 + 8 * hf + 4 * nh + 2 * part, o);  // scales of the run's two 16-halves
-    d[19] = ld_u16(sbase + 208, o);                                 // d
+    d[18] = ld_u16(sbase + 192 + 8 * hf, o + 4 * nh + 2 * part);  // scales of the run's two 16-halves
+    d[19] = ld_u16(sbase + 208, o);                               // d
   } else {
-    const int j = 4 * hf + r;
-    const uint32_t of = (o + 2) & ~3u;  // the index and sign windows start 2 bytes past o
-    const uint8_t *ix = sbase + 2 + 4 * j - 2, *sg = sbase + 34 + 4 * j - 2;
+    // sub-block j = 4 hf + r; the index and sign windows start 2 bytes past o
+    const uint32_t of = ((o + 2) & ~3u) + 4 * static_cast<uint32_t>(r);
+    const uint8_t *ix = sbase + 16 * hf, *sg = sbase + 32 + 16 * hf;
     d[0] = ld_u32(ix, of);
     d[1] = ld_u32(ix, of + 4);
     d[2] = ld_u32(sg, of);
     d[3] = ld_u32(sg, of + 4);
-    d[4] = *(sbase + 66 + j + o);  // qh of sub-block j
-    d[5] = *(sbase + 74 + j + o);  // its two 4-bit scales
-    d[6] = ld_u16(sbase, o);       // d
+    d[4] = *(sbase + 66 + 4 * hf + o + r);  // qh of sub-block j
+    d[5] = *(sbase + 74 + 4 * hf + o + r);  // its two 4-bit scales
+    d[6] = ld_u16(sbase, o);                 // d
   }
 }
 
@@ -487,11 +491,15 @@ __global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wr = wave >> 1, wc = wave & 1;
 
-  // decode task: run `wave` of the step for weight row `lane`
+  // decode task: run `run` of the step for weight row `brow`: the four runs of a row sit in four
+  // adjacent lanes, so a weight load instruction touches 16 rows (one wave per run, 64 rows per
+  // instruction, measured 13-25% slower: the address unit is busy for the whole kernel and
+  // serves a load by the cache lines it touches)
+  const int brow = tid >> 2, run = tid & 3;
   const uint8_t *wtile = a.W + static_cast<int64_t>(nt) * kK2BN * a.rowbytes;
-  const uint32_t wlane = static_cast<uint32_t>(lane) * a.rowbytes;
+  const uint32_t wlane = static_cast<uint32_t>(brow) * a.rowbytes;
   constexpr int SB = KqSb<FMT>::BYTES;
-  _Float16 *bdst = Bs + lane * kK2Lda + (FMT == FMT_Q6_K ? 64 * (wave & 1) + 32 * (wave >> 1) : 32 * wave);
+  _Float16 *bdst = Bs + brow * kK2Lda + (FMT == FMT_Q6_K ? 64 * (run & 1) + 32 * (run >> 1) : 32 * run);
   // X task: chunk c = tid + 256 i: tile row c >> 4, k offset 8 (c & 15) (a wave loads 4 rows x
   // 256 contiguous bytes per instruction; fragment-ordered loads of 16 rows x 64 B measured 28%
   // slower); rows past M read row M - 1 (they feed only outputs that are never stored); byte
@@ -512,17 +520,20 @@ __global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  uint32_t dw[DW];
-  u4 xr[8];
-  uint32_t sh = 0;
-  auto load_step = [&](int s) {
+  // one register stage of loads, refilled right after its step's LDS stores (a second stage, two
+  // workgroups per CU, measured 5-15% slower)
+  constexpr int PIPE = 1;
+  uint32_t dw[PIPE][DW];
+  u4 xr[PIPE][8];
+  uint32_t sh[PIPE];
+  auto load_step = [&](int s, int p) {
     const int sbi = s >> 1;
     const uint32_t o = wlane + static_cast<uint32_t>(sbi) * SB;  // this lane's super-block
-    k2_load_run<FMT>(wtile, o, s & 1, wave, dw);
-    sh = FMT == FMT_Q6_K ? ((o & 2) ? 16u : 0u) : ((o & 2) ? 0u : 16u);
+    k2_load_run<FMT>(wtile, o, s & 1, run, dw[p]);
+    sh[p] = FMT == FMT_Q6_K ? ((o & 2) ? 16u : 0u) : ((o & 2) ? 0u : 16u);
     const uint8_t *xs = xb + static_cast<int64_t>(s) * (2 * kK2BK);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xr[i] = *reinterpret_cast<const u4 *>(xs + xoff[i]);
+    for (int i = 0; i < 8; ++i) xr[p][i] = *reinterpret_cast<const u4 *>(xs + xoff[i]);
   };
   auto bar = [] {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS accesses are done
@@ -532,20 +543,18 @@ __global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
   };
-
-  if (s0 < s1) load_step(s0);
-  for (int s = s0; s < s1; ++s) {
+  auto step = [&](int s, int p) {
     {
       uint32_t w[16];
-      k2_decode_run<FMT>(dw, sh, wave, w);
+      k2_decode_run<FMT>(dw[p], sh[p], run, w);
       store_run32(bdst, w);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int c = tid + 256 * i;
-      *reinterpret_cast<u4 *>(As + (c >> 4) * kK2Lda + 8 * (c & 15)) = xr[i];
+      *reinterpret_cast<u4 *>(As + (c >> 4) * kK2Lda + 8 * (c & 15)) = xr[p][i];
     }
-    if (s + 1 < s1) load_step(s + 1);  // the next step's loads run under this step's MFMAs
+    if (s + PIPE < s1) load_step(s + PIPE, p);  // these loads run under the next PIPE steps
     bar();
 #pragma unroll
     for (int kk = 0; kk < kK2BK / 32; ++kk) {
@@ -562,6 +571,15 @@ __global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
       }
     }
     bar();
+  };
+
+#pragma unroll
+  for (int p = 0; p < PIPE; ++p)
+    if (s0 + p < s1) load_step(s0 + p, p);
+  for (int s = s0; s < s1; s += PIPE) {
+#pragma unroll
+    for (int p = 0; p < PIPE; ++p)
+      if (s + p < s1) step(s + p, p);
   }
 
   // acc[i][j][q] = C[row0 + 64 wr + 16 i + 4 (lane >> 4) + q][64 nt + 32 wc + 16 j + (lane & 15)]
@@ -621,8 +639,8 @@ struct Kq2Plan {
 
 // K split minimising the busiest CU's time plus the partial traffic (written once, read back
 // once). Three workgroups fit a CU; a CU with c workgroups runs them three at a time, and a step
-// costs (MI355X, Q6_K at the prefill shapes, in µs per step of the group) 3.4 with three resident,
-// 2.72 with two, 2.2 with one.
+// costs (MI355X, Q6_K at the prefill shapes, in µs per step of the group) 2.98 with three
+// resident, 2.19 with two, ~1.7 with one.
 static Kq2Plan kq2_plan(int M, int N, int S2, bool allow_split) {
   const int cus = device_cu_count();
   const int m_tiles = (M + kK2BM - 1) / kK2BM, n_tiles = N / kK2BN;
@@ -633,8 +651,8 @@ static Kq2Plan kq2_plan(int M, int N, int S2, bool allow_split) {
     if ((splits - 1) * sps >= S2) continue;
     const int64_t units = static_cast<int64_t>(m_tiles) * n_tiles * splits;
     const int64_t c = (units + cus - 1) / cus;
-    const double rem = c % 3 == 0 ? 0.0 : (c % 3 == 2 ? 2.72 : 2.2);
-    double t = sps * (static_cast<double>(c / 3) * 3.4 + rem);
+    const double rem = c % 3 == 0 ? 0.0 : (c % 3 == 2 ? 2.19 : 1.7);
+    double t = sps * (static_cast<double>(c / 3) * 2.98 + rem);
     if (splits > 1) t += static_cast<double>(M) * N * 4 * (splits + 1) / 5.0e6 + 3.0;
     if (best_t < 0 || t < best_t - 1e-9) {
       best_t = t;
