@@ -522,18 +522,11 @@ __global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
 
   // one register stage of loads, refilled right after its step's LDS stores (a second stage, two
   // workgroups per CU, measured 5-15% slower)
-  constexpr int PIPE = 1;
-  uint32_t dw[PIPE][DW];
-  u4 xr[PIPE][8];
-  uint32_t sh[PIPE];
-  auto load_step = [&](int s, int p) {
-    const int sbi = s >> 1;
-    const uint32_t o = wlane + static_cast<uint32_t>(sbi) * SB;  // this lane's super-block
-    k2_load_run<FMT>(wtile, o, s & 1, run, dw[p]);
-    sh[p] = FMT == FMT_Q6_K ? ((o & 2) ? 16u : 0u) : ((o & 2) ? 0u : 16u);
+  u4 xr[8];
+  auto load_x = [&](int s) {
     const uint8_t *xs = xb + static_cast<int64_t>(s) * (2 * kK2BK);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xr[p][i] = *reinterpret_cast<const u4 *>(xs + xoff[i]);
+    for (int i = 0; i < 8; ++i) xr[i] = *reinterpret_cast<const u4 *>(xs + xoff[i]);
   };
   auto bar = [] {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS accesses are done
@@ -543,18 +536,20 @@ __global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
   };
-  auto step = [&](int s, int p) {
+  // the step's decoded run and X chunks -> LDS
+  auto stage = [&](const uint32_t (&d)[DW], uint32_t sh) {
     {
       uint32_t w[16];
-      k2_decode_run<FMT>(dw[p], sh[p], run, w);
+      k2_decode_run<FMT>(d, sh, run, w);
       store_run32(bdst, w);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int c = tid + 256 * i;
-      *reinterpret_cast<u4 *>(As + (c >> 4) * kK2Lda + 8 * (c & 15)) = xr[p][i];
+      *reinterpret_cast<u4 *>(As + (c >> 4) * kK2Lda + 8 * (c & 15)) = xr[i];
     }
-    if (s + PIPE < s1) load_step(s + PIPE, p);  // these loads run under the next PIPE steps
+  };
+  auto mfma_step = [&] {
     bar();
 #pragma unroll
     for (int kk = 0; kk < kK2BK / 32; ++kk) {
@@ -573,13 +568,103 @@ __global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
     bar();
   };
 
+  if constexpr (FMT == FMT_Q6_K) {
+    // The four lanes of a weight row load the row's super-block once per two steps: lane r takes
+    // ql[32 r ..] (8 dwords and the next), qh[16 r ..] (4 dwords and the next), and its run's
+    // scale pairs of both halves; each step gathers the run's ql / qh windows from the quad by
+    // DPP lane moves. Half the load instructions of one run-window set per step.
+    uint32_t rq[9], rh[5], rd = 0, rsc[2], sh = 0;
+    const uint32_t part = static_cast<uint32_t>(run) >> 1, nh = static_cast<uint32_t>(run) & 1u;
+    auto load_sb = [&](int sbi) {
+      const uint32_t o = wlane + static_cast<uint32_t>(sbi) * SB;  // this lane's super-block
+      const uint32_t of = o & ~3u;
+      const uint32_t qo = of + 32 * static_cast<uint32_t>(run), ho = of + 128 + 16 * static_cast<uint32_t>(run);
+      const u4a4 a0 = *reinterpret_cast<const u4a4 *>(wtile + qo), a1 = *reinterpret_cast<const u4a4 *>(wtile + qo + 16);
+      const u4a4 b0 = *reinterpret_cast<const u4a4 *>(wtile + ho);
 #pragma unroll
-  for (int p = 0; p < PIPE; ++p)
-    if (s0 + p < s1) load_step(s0 + p, p);
-  for (int s = s0; s < s1; s += PIPE) {
+      for (int i = 0; i < 4; ++i) {
+        rq[i] = a0[i];
+        rq[4 + i] = a1[i];
+        rh[i] = b0[i];
+      }
+      rq[8] = ld_u32(wtile, qo + 32);
+      rh[4] = ld_u32(wtile, ho + 16);
+      rsc[0] = ld_u16(wtile + 192, o + 4 * nh + 2 * part);
+      rsc[1] = ld_u16(wtile + 200, o + 4 * nh + 2 * part);
+      rd = ld_u16(wtile + 208, o);
+      sh = (o & 2) ? 16u : 0u;
+    };
+    // half HF: the run's ql window is lane 2 HF + part's, its qh window lanes 2 HF and 2 HF + 1's;
+    // the window dwords are fetched from the quad as the decode reaches them
+    auto stage_q6 = [&](auto hf_c) {
+      constexpr int HF = decltype(hf_c)::value;
+      constexpr int QL = (2 * HF) | (2 * HF) << 2 | (2 * HF + 1) << 4 | (2 * HF + 1) << 6;
+      constexpr int H0 = 0x55 * (2 * HF), H1 = 0x55 * (2 * HF + 1);
+      auto qlw = [&](int t) { return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(rq[t]), QL, 0xf, 0xf, false)); };
+      auto qhw = [&](int t) {
+        return t < 4 ? static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(rh[t]), H0, 0xf, 0xf, false))
+                     : static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(rh[t - 4]), H1, 0xf, 0xf, false));
+      };
+      const uint32_t qls = 4 * nh, qhs = 2 * part + 4 * nh;  // nibble of ql, bit pair of qh
+      const float dd = half_bits_to_f32(rd);
+      const uint32_t sc = rsc[HF];
+      const h2 ds0 = {static_cast<_Float16>(dd * static_cast<float>(static_cast<int8_t>(sc & 0xffu))),
+                      static_cast<_Float16>(dd * static_cast<float>(static_cast<int8_t>(sc & 0xffu)))};
+      const h2 ds1 = {static_cast<_Float16>(dd * static_cast<float>(static_cast<int8_t>(sc >> 8))),
+                      static_cast<_Float16>(dd * static_cast<float>(static_cast<int8_t>(sc >> 8)))};
+      const h2 bias = {static_cast<_Float16>(-1056.0f), static_cast<_Float16>(-1056.0f)};
+      uint32_t w[16];
+      uint32_t l0 = qlw(0), h0 = qhw(0);
 #pragma unroll
-    for (int p = 0; p < PIPE; ++p)
-      if (s + p < s1) step(s + p, p);
+      for (int t = 0; t < 8; ++t) {
+        const uint32_t l1 = qlw(t + 1);
+        const uint32_t h1 = t + 1 < 8 ? qhw(t + 1)
+                                      : static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(rh[4]), H1, 0xf, 0xf, false));
+        const uint32_t ql = __builtin_amdgcn_alignbit(l1, l0, sh) >> qls;
+        const uint32_t qh = (__builtin_amdgcn_alignbit(h1, h0, sh) >> qhs) & 0x03030303u;
+        const uint32_t v = (ql & 0x0F0F0F0Fu) | (qh << 4);
+        const h2 p0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u));
+        const h2 p1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u));
+        const h2 ds = t < 4 ? ds0 : ds1;
+        w[2 * t] = __builtin_bit_cast(uint32_t, (p0 + bias) * ds);
+        w[2 * t + 1] = __builtin_bit_cast(uint32_t, (p1 + bias) * ds);
+        l0 = l1;
+        h0 = h1;
+      }
+      store_run32(bdst, w);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int c = tid + 256 * i;
+        *reinterpret_cast<u4 *>(As + (c >> 4) * kK2Lda + 8 * (c & 15)) = xr[i];
+      }
+    };
+    if (s0 < s1) {
+      load_sb(s0 >> 1);
+      load_x(s0);
+    }
+    for (int s = s0; s < s1; ++s) {
+      if (s & 1) stage_q6(std::integral_constant<int, 1>{});
+      else stage_q6(std::integral_constant<int, 0>{});
+      if (s + 1 < s1) {  // these loads run under this step's MFMAs
+        if (s & 1) load_sb((s + 1) >> 1);
+        load_x(s + 1);
+      }
+      mfma_step();
+    }
+  } else {
+    uint32_t dw[DW], sh = 0;
+    auto load_step = [&](int s) {
+      const uint32_t o = wlane + static_cast<uint32_t>(s >> 1) * SB;  // this lane's super-block
+      k2_load_run<FMT>(wtile, o, s & 1, run, dw);
+      sh = (o & 2) ? 0u : 16u;
+      load_x(s);
+    };
+    if (s0 < s1) load_step(s0);
+    for (int s = s0; s < s1; ++s) {
+      stage(dw, sh);
+      if (s + 1 < s1) load_step(s + 1);  // these loads run under this step's MFMAs
+      mfma_step();
+    }
   }
 
   // acc[i][j][q] = C[row0 + 64 wr + 16 i + 4 (lane >> 4) + q][64 nt + 32 wc + 16 j + (lane & 15)]
