@@ -468,15 +468,11 @@ __device__ __forceinline__ void k2_decode_run(const uint32_t (&d)[K2Run<FMT>::DW
   }
 }
 
+// One unit u (split, m-tile, weight tile) of the 128-row tiling; every thread of the workgroup
+// calls it.
 template <int FMT>
-__global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
+__device__ __forceinline__ void kq2_tile(const Kq2Args &a, int u, _Float16 *As, _Float16 *Bs) {
   constexpr int DW = K2Run<FMT>::DW;
-  __shared__ __attribute__((aligned(16))) _Float16 As[kK2BM * kK2Lda];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[kK2BN * kK2Lda];
-
-  const int units = a.m_tiles * a.n_tiles * a.splits;
-  int u = static_cast<int>(blockIdx.x);
-  if (a.xcd) u = (u & 7) * (units >> 3) + (u >> 3);  // workgroups are dealt to the 8 XCDs in turn
   const int mn_tiles = a.m_tiles * a.n_tiles;
   const int split = u / mn_tiles;
   const int mn = u - split * mn_tiles;
@@ -503,16 +499,16 @@ __global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
   // X task: chunk c = tid + 256 i: tile row c >> 4, k offset 8 (c & 15) (a wave loads 4 rows x
   // 256 contiguous bytes per instruction; fragment-ordered loads of 16 rows x 64 B measured 28%
   // slower); rows past M read row M - 1 (they feed only outputs that are never stored); byte
-  // offsets (M K < 2^30)
+  // offsets from the tile's first row (128 K fp16 < 2^32 bytes for K < 2^24)
   uint32_t xoff[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int c = tid + 256 * i;
     int m = row0 + (c >> 4);
     m = m < a.M ? m : a.M - 1;
-    xoff[i] = 2u * (static_cast<uint32_t>(m) * static_cast<uint32_t>(a.K) + 8u * static_cast<uint32_t>(c & 15));
+    xoff[i] = 2u * (static_cast<uint32_t>(m - row0) * static_cast<uint32_t>(a.K) + 8u * static_cast<uint32_t>(c & 15));
   }
-  const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.X);
+  const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.X + static_cast<int64_t>(row0) * a.K);
 
   f4 acc[4][2];
 #pragma unroll
@@ -694,6 +690,53 @@ __global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
     }
 }
 
+template <int FMT>
+__global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
+  __shared__ __attribute__((aligned(16))) _Float16 As[kK2BM * kK2Lda];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[kK2BN * kK2Lda];
+  const int units = a.m_tiles * a.n_tiles * a.splits;
+  int u = static_cast<int>(blockIdx.x);
+  if (a.xcd) u = (u & 7) * (units >> 3) + (u >> 3);  // workgroups are dealt to the 8 XCDs in turn
+  kq2_tile<FMT>(a, u, As, Bs);
+}
+
+// The reference's set_gemm block with fp16 X (the GEMM_XH kind; see k_kq_gemm_pb for the words)
+// on the 128-row tiles: a persistent grid of three workgroups per CU walks the tiles, one split.
+template <int FMT>
+__global__ void __launch_bounds__(256, 3) k_kq_mm_pb(const int64_t *__restrict__ pb, uint32_t *__restrict__ status) {
+  __shared__ __attribute__((aligned(16))) _Float16 As[kK2BM * kK2Lda];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[kK2BN * kK2Lda];
+  const int64_t W = pb[0], X = pb[1], Y = pb[2], M = pb[3], N = pb[4], K = pb[5], LDY = pb[6], RS = pb[7];
+  const int64_t ldy = LDY < 0 ? -LDY : LDY;
+  const bool ok = W && X && Y && M >= 1 && M < (1 << 24) && N >= 64 && N % 64 == 0 && N < (1 << 24) && K >= 256 &&
+                  K % 256 == 0 && K < (1 << 24) && ldy >= N && (W & 3) == 0 && (X & 15) == 0;
+  if (!ok) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) __hip_atomic_fetch_or(status, 4u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  Kq2Args a{};
+  a.W = gptr<const uint8_t>(W);
+  a.rowbytes = static_cast<uint32_t>(K / 256 * KqSb<FMT>::BYTES);
+  a.X = gptr<const _Float16>(X);
+  a.M = static_cast<int>(M);
+  a.N = static_cast<int>(N);
+  a.K = static_cast<int>(K);
+  a.S2 = static_cast<int>(K / 128);
+  a.m_tiles = static_cast<int>((M + kK2BM - 1) / kK2BM);
+  a.n_tiles = static_cast<int>(N / kK2BN);
+  a.splits = 1;
+  a.sps = a.S2;
+  a.Y = gptr<void>(Y);
+  a.ydt = LDY < 0 ? VYBDQ_F32 : VYBDQ_F64;
+  a.ldy = ldy;
+  a.RS = LDY < 0 ? nullptr : gptr<const void>(RS);
+  const int units = a.m_tiles * a.n_tiles;
+  for (int u = blockIdx.x; u < units; u += gridDim.x) {
+    kq2_tile<FMT>(a, u, As, Bs);
+    __builtin_amdgcn_s_barrier();  // the next tile's first LDS stores wait for this tile's last reads
+  }
+}
+
 // Sum of the split partials in split order, times the X row scale, then the epilogue; four
 // consecutive columns per thread (N % 64 == 0).
 template <int YDT>
@@ -764,7 +807,7 @@ static int64_t kq_align256(int64_t b) { return (b + 255) / 256 * 256; }
 
 // 32-bit byte offsets: X (M K fp16), a weight tile (64 rows)
 bool kq2_supported(int wtype, int64_t M, int64_t N, int64_t K) {
-  return (wtype == 14 || wtype == 22) && M >= 96 && M * K < (int64_t(1) << 30) && M * N < (int64_t(1) << 31) &&
+  return (wtype == 14 || wtype == 22) && M >= 96 && M * N < (int64_t(1) << 31) &&
          N % 64 == 0 && K % 256 == 0 && K < (int64_t(1) << 24);
 }
 
@@ -839,7 +882,14 @@ int kq2_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
 }
 
 // The GEMM kind of vybdq_launch_pblock for wtype 12, 13, 14, 22 (pblock.hip); xdt F32 or F16.
+// Q6_K / IQ2_S with fp16 X run the 128-row tiles.
 int kq_gemm_pblock(int wtype, int xdt, const int64_t *pb, uint32_t *status, hipStream_t s) {
+  if ((wtype == 14 || wtype == 22) && xdt == VYBDQ_F16) {
+    const unsigned grid = static_cast<unsigned>(3 * device_cu_count());
+    if (wtype == 14) hipLaunchKernelGGL((k_kq_mm_pb<FMT_Q6_K>), dim3(grid), dim3(256), 0, s, pb, status);
+    else hipLaunchKernelGGL((k_kq_mm_pb<FMT_IQ2_S>), dim3(grid), dim3(256), 0, s, pb, status);
+    return check_launch("p-block super-block gemm (128-row tiles)");
+  }
   switch (wtype) {
     case 12: return kq_pb_launch<FMT_Q4_K>(xdt, pb, status, s);
     case 13: return kq_pb_launch<FMT_Q5_K>(xdt, pb, status, s);
