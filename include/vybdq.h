@@ -302,8 +302,8 @@ int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t X, ui
    dequantized tile in LDS. Super-block types: K % 256 == 0, N % 64 == 0, any M. Q4_K with
    M >= 64, K < 2^22 and fp16 X (any X type through vybdq_gemm_ws) dequantizes into the operand
    registers too, each weight as one fp16 fma q * fp16(d sc) - fp16(dmin m) (within one fp16 ulp
-   of the weight's scale of the F16 dequant value). Q6_K and IQ2_S with M >= 96 and
-   fp16 X (any X type through vybdq_gemm_ws) run 128-row tiles whose weights are formed in fp16
+   of the weight's scale of the F16 dequant value). Q6_K and IQ2_S with M >= 96 and fp16 or
+   bf16 X (f32 X through vybdq_gemm_ws) run 128-row tiles whose weights are formed in fp16
    arithmetic: fp16(d sc) * (q - 32), fp16(d (0.5 + s) / 4) * grid magnitude (one product
    rounding after the rounding of the scale).
    Replaces gemm_q80 and its siblings picked by gemm_h(ty) (native/host/ridge_decode.vyb:295-302,

@@ -468,9 +468,18 @@ __device__ __forceinline__ void k2_decode_run(const uint32_t (&d)[K2Run<FMT>::DW
   }
 }
 
+// 8 bf16 -> 8 fp16 (as they are: |x| < 65504)
+__device__ __forceinline__ u4 bf16x8_to_f16(const u4 &v) {
+  u4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = pack_h2(__uint_as_float(v[j] << 16), __uint_as_float(v[j] & 0xffff0000u));
+  return o;
+}
+
 // One unit u (split, m-tile, weight tile) of the 128-row tiling; every thread of the workgroup
-// calls it.
-template <int FMT>
+// calls it. XB: X is bf16, converted to fp16 as it is staged into LDS (vybdq_gemm without a
+// workspace; |x| < 65504).
+template <int FMT, bool XB = false>
 __device__ __forceinline__ void kq2_tile(const Kq2Args &a, int u, _Float16 *As, _Float16 *Bs) {
   constexpr int DW = K2Run<FMT>::DW;
   const int mn_tiles = a.m_tiles * a.n_tiles;
@@ -542,7 +551,7 @@ __device__ __forceinline__ void kq2_tile(const Kq2Args &a, int u, _Float16 *As, 
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int c = tid + 256 * i;
-      *reinterpret_cast<u4 *>(As + (c >> 4) * kK2Lda + 8 * (c & 15)) = xr[i];
+      *reinterpret_cast<u4 *>(As + (c >> 4) * kK2Lda + 8 * (c & 15)) = XB ? bf16x8_to_f16(xr[i]) : xr[i];
     }
   };
   auto mfma_step = [&] {
@@ -631,7 +640,7 @@ __device__ __forceinline__ void kq2_tile(const Kq2Args &a, int u, _Float16 *As, 
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int c = tid + 256 * i;
-        *reinterpret_cast<u4 *>(As + (c >> 4) * kK2Lda + 8 * (c & 15)) = xr[i];
+        *reinterpret_cast<u4 *>(As + (c >> 4) * kK2Lda + 8 * (c & 15)) = XB ? bf16x8_to_f16(xr[i]) : xr[i];
       }
     };
     if (s0 < s1) {
@@ -690,14 +699,14 @@ __device__ __forceinline__ void kq2_tile(const Kq2Args &a, int u, _Float16 *As, 
     }
 }
 
-template <int FMT>
+template <int FMT, bool XB>
 __global__ void __launch_bounds__(256, 3) k_kq_mm(Kq2Args a) {
   __shared__ __attribute__((aligned(16))) _Float16 As[kK2BM * kK2Lda];
   __shared__ __attribute__((aligned(16))) _Float16 Bs[kK2BN * kK2Lda];
   const int units = a.m_tiles * a.n_tiles * a.splits;
   int u = static_cast<int>(blockIdx.x);
   if (a.xcd) u = (u & 7) * (units >> 3) + (u >> 3);  // workgroups are dealt to the 8 XCDs in turn
-  kq2_tile<FMT>(a, u, As, Bs);
+  kq2_tile<FMT, XB>(a, u, As, Bs);
 }
 
 // The reference's set_gemm block with fp16 X (the GEMM_XH kind; see k_kq_gemm_pb for the words)
@@ -821,19 +830,23 @@ int64_t kq2_workspace_size(int wtype, int64_t M, int64_t N, int64_t K) {
 int x_rows_to_f16(const void *X, int xdt, int64_t M, int64_t K, void *xh, float *xscale, hipStream_t s);
 
 template <int FMT>
-static int kq2_launch(const Kq2Args &a, hipStream_t s) {
+static int kq2_launch(const Kq2Args &a, bool xb, hipStream_t s) {
   const unsigned grid = static_cast<unsigned>(a.m_tiles) * a.n_tiles * a.splits;
-  hipLaunchKernelGGL((k_kq_mm<FMT>), dim3(grid), dim3(256), 0, s, a);
+  if (xb) hipLaunchKernelGGL((k_kq_mm<FMT, true>), dim3(grid), dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((k_kq_mm<FMT, false>), dim3(grid), dim3(256), 0, s, a);
   return check_launch("super-block gemm (128-row tiles)");
 }
 
-// Q6_K / IQ2_S with fp16 X, or any X with a workspace of kq2_workspace_size bytes. Returns 1 when
-// the call does not fit this path (the caller takes the 64-row tiles).
+// Q6_K / IQ2_S with fp16 or bf16 X, or f32 X with a workspace of kq2_workspace_size bytes. Returns
+// 1 when the call does not fit this path (the caller takes the 64-row tiles).
 int kq2_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt, int64_t M, int64_t N, int64_t K,
              int64_t ldy, const void *RS, void *ws, int64_t ws_bytes, hipStream_t s) {
   if (!kq2_supported(wtype, M, N, K)) return 1;
   const int S2 = static_cast<int>(K / 128);
-  const int64_t need_x = xdt == VYBDQ_F16 ? 0 : kq_align256(M * K * 2) + kq_align256(M * 4);
+  int64_t need_x = xdt == VYBDQ_F16 ? 0 : kq_align256(M * K * 2) + kq_align256(M * 4);
+  // bf16 X without room for its scaled fp16 copy: converted in the tile as it is (|x| < 65504)
+  const bool xb = xdt == VYBDQ_BF16 && (!ws || ws_bytes < need_x);
+  if (xb) need_x = 0;
   if (need_x && (!ws || ws_bytes < need_x)) return 1;
   Kq2Plan p = kq2_plan(static_cast<int>(M), static_cast<int>(N), S2, ws != nullptr);
   if (p.splits > 1 && ws_bytes < kq_align256(p.part_bytes) + need_x)
@@ -851,7 +864,7 @@ int kq2_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   Kq2Args a{};
   a.W = static_cast<const uint8_t *>(W);
   a.rowbytes = static_cast<uint32_t>(K / 256 * (wtype == 14 ? KqSb<FMT_Q6_K>::BYTES : KqSb<FMT_IQ2_S>::BYTES));
-  a.X = static_cast<const _Float16 *>(X);
+  a.X = static_cast<const _Float16 *>(X);  // fp16, or bf16 bits when xb
   a.xscale = xscale;
   a.M = static_cast<int>(M);
   a.N = static_cast<int>(N);
@@ -868,7 +881,7 @@ int kq2_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   a.RS = RS;
   a.part = p.splits > 1 ? static_cast<float *>(ws) : nullptr;
   int rc;
-  rc = wtype == 14 ? kq2_launch<FMT_Q6_K>(a, s) : kq2_launch<FMT_IQ2_S>(a, s);
+  rc = wtype == 14 ? kq2_launch<FMT_Q6_K>(a, xb, s) : kq2_launch<FMT_IQ2_S>(a, xb, s);
   if (rc || p.splits == 1) return rc;
   const int64_t n4 = M * N / 4;
   const unsigned grid = static_cast<unsigned>(n4 / 256 < 4096 ? (n4 + 255) / 256 : 4096);
