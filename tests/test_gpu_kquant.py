@@ -383,3 +383,29 @@ def test_gemm_128row_tiles_activation_range(dev, ty, kind):
     ref = matmul.gemm_rows_f64(x.astype(np.float64), matrix_ref(ty, raw, N, K))
     assert np.all(np.isfinite(y))
     assert matmul.rel_maxnorm(y, ref) < TOL
+
+
+@pytest.mark.parametrize("ty", TILE128)
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+@pytest.mark.parametrize("room", ["x_only", "none"])
+def test_gemm_128row_tiles_small_workspace(dev, monkeypatch, ty, xdt, room):
+    """vybdq_gemm_ws with less workspace than the planned K split needs: room for the fp16 copy of
+    X only (one split), or for nothing (bf16 X converted in the tile, f32 X on the 64-row tiles);
+    every output against the float64 oracle."""
+    monkeypatch.setenv("VYBDQ_KQ2_SPLITS", "3")
+    M, N, K = 200, 320, 3072
+    rng = np.random.default_rng(ty + len(xdt) + len(room))
+    raw = synth.kquant_weights(rng, ty, N, K)
+    x = synth.activations(rng, (M, K))
+    xd, x64 = x_as(x, xdt, dev)
+    Wd = to_dev(raw, dev)
+    full = _lib.lib.vybdq_gemm_workspace_size(ty, M, N, K)
+    nb = 0 if room == "none" else (M * K * 2 + 255) // 256 * 256 + (M * 4 + 255) // 256 * 256
+    assert nb < full
+    ws = torch.zeros(nb + 256, dtype=torch.uint8, device=dev)
+    wp = (ws.data_ptr() + 255) // 256 * 256 if nb else 0
+    y = torch.empty(M, N, dtype=torch.float32, device=dev)
+    _lib.call("vybdq_gemm_ws", ty, Wd.data_ptr(), xd.data_ptr(), y.data_ptr(), M, N, K, ops._dt(xd.dtype), ops.F32,
+              0, 0, wp, nb, torch.cuda.current_stream().cuda_stream)
+    ref = matmul.gemm_rows_f64(x64.reshape(M, K), matrix_ref(ty, raw, N, K))
+    assert matmul.rel_maxnorm(y.cpu().numpy(), ref) < TOL
