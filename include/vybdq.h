@@ -305,7 +305,8 @@ int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uint64_t X, ui
    of the weight's scale of the F16 dequant value). Q6_K and IQ2_S with M >= 96 and fp16 or
    bf16 X (f32 X through vybdq_gemm_ws) run 128-row tiles whose weights are formed in fp16
    arithmetic: fp16(d sc) * (q - 32), fp16(d (0.5 + s) / 4) * grid magnitude (one product
-   rounding after the rounding of the scale).
+   rounding after the rounding of the scale); so do Q4_K and Q5_K with bf16 X from 96 rows
+   (fp16(d sc) * q - fp16(dmin m), as the register body).
    Replaces gemm_q80 and its siblings picked by gemm_h(ty) (native/host/ridge_decode.vyb:295-302,
    native/tools/gen_rpf.py:1-10,142-149, p-block W@0 X@8 Y@16 S@24 N@32 K@40 LDY@48 RS@56). */
 int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t M, int64_t N, int64_t K, int x_dt,

@@ -501,7 +501,8 @@ extern "C" int vybdq_gemm(int wtype, uint64_t W, uint64_t X, uint64_t Y, int64_t
   if ((wtype == 12 || wtype == 13) && x_dt == VYBDQ_F16 && M >= 64 && K < (int64_t(1) << 22) &&
       mmq_supported(M, N, K))
     return mmq_gemm(wtype, a.W, a.X, x_dt, a.Y, y_dt, M, N, K, a.ldy, a.RS, nullptr, 0, s);
-  if ((wtype == 14 || wtype == 22) && x_dt != VYBDQ_F32) {  // fp16 / bf16 X from 96 rows: 128-row tiles
+  // fp16 / bf16 X from 96 rows (Q4_K / Q5_K: bf16, fp16 took the register body above): 128-row tiles
+  if ((wtype == 14 || wtype == 22) ? x_dt != VYBDQ_F32 : (wtype >= 12 && x_dt == VYBDQ_BF16)) {
     const int r = kq2_gemm(wtype, a.W, a.X, x_dt, a.Y, y_dt, M, N, K, a.ldy, a.RS, nullptr, 0, s);
     if (r != 1) return r;
   }

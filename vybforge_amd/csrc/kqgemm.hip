@@ -364,6 +364,10 @@ struct Kq2Args {
 };
 
 template <int FMT> struct K2Run;
+// Q4_K / Q5_K run (sub-block j): the 16-byte head (d, dmin, 12 scale bytes), Q5_K the 32 high-bit
+// bytes, and the 32 nibble bytes of qs[32 (j / 2) ..]
+template <> struct K2Run<FMT_Q4_K> { static constexpr int DW = 12; };
+template <> struct K2Run<FMT_Q5_K> { static constexpr int DW = 20; };
 // Q6_K run (half hf, part, nibble nh): ql[64hf + 32part ..] and qh[32hf ..] as 9-dword windows,
 // the run's two scale bytes, d
 template <> struct K2Run<FMT_Q6_K> { static constexpr int DW = 20; };
@@ -384,7 +388,28 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t *base, uint32_t off) {
 template <int FMT>
 __device__ __forceinline__ void k2_load_run(const uint8_t *sbase, uint32_t o, int hf, int r,
                                             uint32_t (&d)[K2Run<FMT>::DW]) {
-  if constexpr (FMT == FMT_Q6_K) {
+  if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q5_K) {
+    // 144 / 176-byte super-blocks keep every window dword aligned
+    constexpr int QS = FMT == FMT_Q4_K ? 16 : 48;
+    const uint32_t j = 4 * static_cast<uint32_t>(hf) + static_cast<uint32_t>(r);
+    const u4a4 h = *reinterpret_cast<const u4a4 *>(sbase + o);
+    const uint32_t qo = o + QS + 32 * (j >> 1);
+    const u4a4 q0 = *reinterpret_cast<const u4a4 *>(sbase + qo), q1 = *reinterpret_cast<const u4a4 *>(sbase + qo + 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      d[i] = h[i];
+      d[K2Run<FMT>::DW - 8 + i] = q0[i];
+      d[K2Run<FMT>::DW - 4 + i] = q1[i];
+    }
+    if constexpr (FMT == FMT_Q5_K) {
+      const u4a4 b0 = *reinterpret_cast<const u4a4 *>(sbase + o + 16), b1 = *reinterpret_cast<const u4a4 *>(sbase + o + 32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        d[4 + i] = b0[i];
+        d[8 + i] = b1[i];
+      }
+    }
+  } else if constexpr (FMT == FMT_Q6_K) {
     const uint32_t part = static_cast<uint32_t>(r) >> 1, nh = static_cast<uint32_t>(r) & 1u;
     const uint32_t of = o & ~3u;
     const uint8_t *ql = sbase + 64 * hf, *qh = sbase + 128 + 32 * hf;
@@ -421,7 +446,26 @@ __device__ __forceinline__ void k2_load_run(const uint8_t *sbase, uint32_t o, in
 template <int FMT>
 __device__ __forceinline__ void k2_decode_run(const uint32_t (&d)[K2Run<FMT>::DW], uint32_t sh, int r,
                                               uint32_t (&out)[16]) {
-  if constexpr (FMT == FMT_Q6_K) {
+  if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q5_K) {
+    // run r of half hf is sub-block j = 4 hf + r; the caller passes r + 4 hf. w = fp16(d sc) q -
+    // fp16(dmin m) by one packed fma per pair (q exact from the 0x64qq bit pattern)
+    const uint32_t j = static_cast<uint32_t>(r);
+    float sc, mn;
+    scale_min_k4(d[1], d[2], d[3], static_cast<int>(j), sc, mn);
+    const _Float16 dsh = static_cast<_Float16>(half_bits_to_f32(d[0] & 0xffffu) * sc);
+    const _Float16 dmh = static_cast<_Float16>(-(half_bits_to_f32(d[0] >> 16) * mn));
+    const h2 ds = {dsh, dsh}, dm = {dmh, dmh};
+    const h2 bias = {static_cast<_Float16>(-1024.0f), static_cast<_Float16>(-1024.0f)};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      uint32_t v = (d[K2Run<FMT>::DW - 8 + t] >> (4 * (j & 1u))) & 0x0F0F0F0Fu;
+      if constexpr (FMT == FMT_Q5_K) v |= ((d[4 + t] >> j) & 0x01010101u) << 4;
+      const h2 p0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u)) + bias;
+      const h2 p1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u)) + bias;
+      out[2 * t] = __builtin_bit_cast(uint32_t, p0 * ds + dm);
+      out[2 * t + 1] = __builtin_bit_cast(uint32_t, p1 * ds + dm);
+    }
+  } else if constexpr (FMT == FMT_Q6_K) {
     const int part = r >> 1, nh = r & 1;
     const uint32_t qls = 4 * nh, qhs = 2 * part + 4 * nh;  // nibble of ql, bit pair of qh
     const float dd = half_bits_to_f32(d[19]);
@@ -542,10 +586,10 @@ __device__ __forceinline__ void kq2_tile(const Kq2Args &a, int u, _Float16 *As, 
     asm volatile("" ::: "memory");
   };
   // the step's decoded run and X chunks -> LDS
-  auto stage = [&](const uint32_t (&d)[DW], uint32_t sh) {
+  auto stage = [&](const uint32_t (&d)[DW], uint32_t sh, int rr) {
     {
       uint32_t w[16];
-      k2_decode_run<FMT>(d, sh, run, w);
+      k2_decode_run<FMT>(d, sh, rr, w);
       store_run32(bdst, w);
     }
 #pragma unroll
@@ -666,7 +710,8 @@ __device__ __forceinline__ void kq2_tile(const Kq2Args &a, int u, _Float16 *As, 
     };
     if (s0 < s1) load_step(s0);
     for (int s = s0; s < s1; ++s) {
-      stage(dw, sh);
+      // Q4_K / Q5_K decode by sub-block index 4 hf + run
+      stage(dw, sh, FMT == FMT_IQ2_S ? run : run + 4 * (s & 1));
       if (s + 1 < s1) load_step(s + 1);  // these loads run under this step's MFMAs
       mfma_step();
     }
@@ -816,7 +861,7 @@ static int64_t kq_align256(int64_t b) { return (b + 255) / 256 * 256; }
 
 // 32-bit byte offsets: X (M K fp16), a weight tile (64 rows)
 bool kq2_supported(int wtype, int64_t M, int64_t N, int64_t K) {
-  return (wtype == 14 || wtype == 22) && M >= 96 && M * N < (int64_t(1) << 31) &&
+  return (wtype == 12 || wtype == 13 || wtype == 14 || wtype == 22) && M >= 96 && M * N < (int64_t(1) << 31) &&
          N % 64 == 0 && K % 256 == 0 && K < (int64_t(1) << 24);
 }
 
@@ -863,7 +908,10 @@ int kq2_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   }
   Kq2Args a{};
   a.W = static_cast<const uint8_t *>(W);
-  a.rowbytes = static_cast<uint32_t>(K / 256 * (wtype == 14 ? KqSb<FMT_Q6_K>::BYTES : KqSb<FMT_IQ2_S>::BYTES));
+  a.rowbytes = static_cast<uint32_t>(K / 256 * (wtype == 12   ? KqSb<FMT_Q4_K>::BYTES
+                                                  : wtype == 13 ? KqSb<FMT_Q5_K>::BYTES
+                                                  : wtype == 14 ? KqSb<FMT_Q6_K>::BYTES
+                                                                : KqSb<FMT_IQ2_S>::BYTES));
   a.X = static_cast<const _Float16 *>(X);  // fp16, or bf16 bits when xb
   a.xscale = xscale;
   a.M = static_cast<int>(M);
@@ -881,7 +929,12 @@ int kq2_gemm(int wtype, const void *W, const void *X, int xdt, void *Y, int ydt,
   a.RS = RS;
   a.part = p.splits > 1 ? static_cast<float *>(ws) : nullptr;
   int rc;
-  rc = wtype == 14 ? kq2_launch<FMT_Q6_K>(a, xb, s) : kq2_launch<FMT_IQ2_S>(a, xb, s);
+  switch (wtype) {
+    case 12: rc = kq2_launch<FMT_Q4_K>(a, xb, s); break;
+    case 13: rc = kq2_launch<FMT_Q5_K>(a, xb, s); break;
+    case 14: rc = kq2_launch<FMT_Q6_K>(a, xb, s); break;
+    default: rc = kq2_launch<FMT_IQ2_S>(a, xb, s); break;
+  }
   if (rc || p.splits == 1) return rc;
   const int64_t n4 = M * N / 4;
   const unsigned grid = static_cast<unsigned>(n4 / 256 < 4096 ? (n4 + 255) / 256 : 4096);
