@@ -436,13 +436,21 @@ def run_exl3(args, torch, dev, batch=None):
 PREFILL_SHAPES = [(17408, 5120), (5120, 17408)]  # (N, K): up, down
 
 
-def _prefill_check(args, name, W, y, N, K, xref):
-    from oracle import matmul
+def _prefill_check(args, name, W, y, N, K, xref, ty=8):
+    """The first 256 output columns of a prefill GEMM against the float64 oracle (GGUF type ty)."""
+    from oracle import iquants, kquants, matmul
+    from vybforge_amd import ops
     if args.no_check:
         return None
     cols = 256
-    rb = K // 32 * 34
-    wrows = matmul.q8_0_matrix(W[:cols * rb].cpu().numpy(), cols, K)
+    rb = ops.row_bytes(ty, K)
+    raw = W[:cols * rb].cpu().numpy()
+    if ty == ops.GGML_Q8_0:
+        wrows = matmul.q8_0_matrix(raw, cols, K)
+    elif ty == ops.GGML_IQ2_S:
+        wrows = iquants.dequant_iq2_s(raw).reshape(cols, K)
+    else:
+        wrows = kquants.DEQUANT[ty](raw).reshape(cols, K)
     ref = matmul.gemm_rows_f64(xref, wrows)
     return expect(f"{name} N={N} K={K}", rel_gate(y[:, :cols].cpu().numpy(), ref))
 
@@ -492,7 +500,7 @@ def run_prefill_kq(args, torch, dev):
     name = {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 22: "IQ2_S"}[ty]
     gen = torch.Generator(device=dev)
     gen.manual_seed(args.seed + 6)
-    launches, flops, nbytes = [], 0, 0
+    launches, flops, nbytes, last = [], 0, 0, []
     # every type uses the workspace: bf16 X converted once; Q4_K / Q5_K then run the register-operand
     # body, Q6_K / IQ2_S the 128-row tiles (with the K split's partials)
     ws = ops.GemmWorkspace([(M, N, K) for N, K in PREFILL_SHAPES], dev, ty)
@@ -505,8 +513,14 @@ def run_prefill_kq(args, torch, dev):
             launches.append(lambda W=W, x=x, y=y, N=N, K=K: ops.gemm(ty, W, x, N, K, out=y, workspace=wsa))
             flops += 2 * M * N * K
             nbytes += ops.row_bytes(ty, K) * N + 2 * M * K + 4 * M * N
+        last.append((W, x, y, N, K))
     ms, wall = timed_graph(torch, launches, args.steps, args.warmup)
     tflops = flops / (ms * 1e-3) / 1e12
+    check = None
+    if not args.no_check:
+        rels = [_prefill_check(args, f"prefill_kq {name}", W, y, N, K, x.to(torch.float64).cpu().numpy(), ty)
+                for W, x, y, N, K in last]
+        check = dict(ok=True, rel=max(rels), what="last copy of each shape, 512 rows x first 256 columns, float64 oracle")
     roofline = dict(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s",
                     frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), traffic=None,
                     kernel=(f"k_mmq<{name}, fp16 X, 8 waves> (bf16 X converted once per GEMM; weights dequantized "
@@ -516,7 +530,7 @@ def run_prefill_kq(args, torch, dev):
                     basis="flops per step / event time", avg_launch_us=round(ms * 1e3 / len(launches), 3))
     return dict(value=tflops, unit="TFLOP/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
                 workload=f"{name} prefill GEMMs M=512: 5120->17408 and 17408->5120 (bf16 X, f32 Y)",
-                bytes_per_step=nbytes, launches_per_step=len(launches))
+                bytes_per_step=nbytes, launches_per_step=len(launches), check=check)
 
 
 def run_prefill_i8(args, torch, dev):

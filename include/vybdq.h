@@ -52,9 +52,11 @@ extern "C" {
                                   the reference's deq_q4_0 intrinsic, pinned by its fixture
                                   (native/gguf/mk_fixture.vyb:86-99, dequant_gguf.vyb:118-127) */
 
-/* EXL3 codebooks (exllamav3 numbering) */
-#define VYBDQ_EXL3_3INST 0 /* x = w*89226354 + 64248484 (QTIP 3INST) */
-#define VYBDQ_EXL3_MCG 1   /* x = w*0xCBAC1FED: the codebook of the reference's checkpoint */
+/* EXL3 codebook (exllamav3 numbering). mcg, x = w*0xCBAC1FED, is exllamav3's decode_3inst at
+   cb=1 and the only codebook the reference implements (native/exl3/exl3_ref.py:19-22,
+   native/kernels/exl3.vyb:15-19); every EXL3 entry point returns VYBDQ_ERR_ARG for any other
+   value (codebook 0, QTIP's multiply-add 3INST, and codebook 2, mul1, are not supported). */
+#define VYBDQ_EXL3_MCG 1
 
 /* ---- library ------------------------------------------------------------------------- */
 

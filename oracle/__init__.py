@@ -33,7 +33,8 @@ Pinning (what checks each function, all under tests/):
   xq8              round-trip bound, RNE ties, zero block, saturation.   -> pinned (properties)
   exl3 decode      all-zero-trellis KAT (1.84375), exhaustive 65536-window check against
                    an integer-only fp16 decode, slot-map invariants.     -> pinned
-  exl3 3inst (cb0) QTIP paper constants only; no fixture anywhere.       -> parity unpinned
+  exl3 codebook    only mcg (cb 1) exists, as in the reference (exl3_ref.py:19-22);
+                   any other codebook id raises ValueError.              -> pinned (KAT above)
   exl3 dequant     closed form of the all-zero trellis after the Hadamard sandwich,
                    H orthogonality, per-block linearity.                 -> pinned
   moe              the reference's committed MoE goldens (routing ids/weights, and the

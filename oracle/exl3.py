@@ -8,8 +8,9 @@ Storage per weight matrix W [K, N] (K = in features, N = out features):
   suh fp16 [K], svh fp16 [N]
 Rotated-basis value of tile slot (r, c): a 16-bit window w16 composed from 4 nibbles of
 the tile stream by the tile-slot composition table, then
-  mcg   (codebook 1):  x = w16 * 0xCBAC1FED mod 2^32
-  3inst (codebook 0):  x = (w16 * 89226354 + 64248484) mod 2^32   [QTIP paper; parity unpinned]
+  mcg (codebook 1, exllamav3's decode_3inst at cb=1, exl3_ref.py:19-22):
+      x = w16 * 0xCBAC1FED mod 2^32
+  (the only codebook the reference implements; any other codebook id raises ValueError)
   y = (x & 0x8FFF8FFF) ^ 0x3B603B60 ; value = fp16(fp16(y & 0xFFFF) + fp16(y >> 16))
   (the two halves are summed in float32 and rounded once to fp16, exl3_ref.py:46-47)
 Reconstruction per 128x128 block: W = diag(suh) (H/sqrt(128)) What (H/sqrt(128)) diag(svh),
@@ -22,13 +23,10 @@ import os
 import numpy as np
 
 MCG_MAGIC = 0xCBAC1FED
-INST3_MUL = 89226354
-INST3_ADD = 64248484
 AND_MASK = 0x8FFF8FFF
 XOR_MASK = 0x3B603B60
 R_SCALE = 0.08838834764831845  # 1/sqrt(128)
 
-CB_3INST = 0
 CB_MCG = 1
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -38,12 +36,9 @@ SLOTMAP_GOLDEN = os.path.join(_HERE, "..", "tests", "golden", "exl3_tile_slot_co
 def hash_window(w16, codebook=CB_MCG):
     """uint16-valued windows -> uint32 y (before the fp16 split)."""
     w = np.asarray(w16).astype(np.uint64)
-    if codebook == CB_MCG:
-        x = (w * np.uint64(MCG_MAGIC)) & np.uint64(0xFFFFFFFF)
-    elif codebook == CB_3INST:
-        x = (w * np.uint64(INST3_MUL) + np.uint64(INST3_ADD)) & np.uint64(0xFFFFFFFF)
-    else:
-        raise ValueError(f"unknown codebook {codebook}")
+    if codebook != CB_MCG:
+        raise ValueError(f"unsupported codebook {codebook}: the reference implements only mcg (1)")
+    x = (w * np.uint64(MCG_MAGIC)) & np.uint64(0xFFFFFFFF)
     return ((x & np.uint64(AND_MASK)) ^ np.uint64(XOR_MASK)).astype(np.uint32)
 
 

@@ -95,3 +95,16 @@ def test_pblock_preconditions_on_host():
     assert "grid" in _lib.last_error()
     assert L.vybdq_launch_pblock_grid(_lib.PB_EXL3DQ, 4096, 0, 256, 0) == _lib.ERR_SHAPE
     assert L.vybdq_launch_pblock_grid(_lib.PB_EXL3DQ, 0, 1, 256, 0) == _lib.ERR_ARG
+
+
+@pytest.mark.parametrize("cb", [0, 2, -1])
+def test_exl3_rejects_codebooks_other_than_mcg(cb):
+    """Only the mcg codebook (1) exists in the reference; every EXL3 entry point refuses any other
+    id on the host, before it touches the device."""
+    from vybforge_amd import _lib
+    L = _lib.lib
+    assert L.vybdq_exl3_decode_tiles(4096, 4096, 128, 128, cb, 0, 0) == _lib.ERR_ARG
+    assert "codebook" in _lib.last_error()
+    assert L.vybdq_dequant_exl3(4096, 4096, 4096, 4096, 128, 128, cb, 0, 0) == _lib.ERR_ARG
+    assert L.vybdq_exl3_gemm(4096, 4096, 4096, 4096, 4096, 1, 128, 128, cb, 1, 0, 4096, 1 << 20, 0) == _lib.ERR_ARG
+    assert "codebook" in _lib.last_error()

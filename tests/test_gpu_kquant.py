@@ -409,3 +409,26 @@ def test_gemm_128row_tiles_small_workspace(dev, monkeypatch, ty, xdt, room):
               0, 0, wp, nb, torch.cuda.current_stream().cuda_stream)
     ref = matmul.gemm_rows_f64(x64.reshape(M, K), matrix_ref(ty, raw, N, K))
     assert matmul.rel_maxnorm(y.cpu().numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("ty", TILE128)
+def test_gemm_ws_x_past_2_32_elements(dev, ty):
+    """bf16 X of more than 2^32 elements through vybdq_gemm_ws (M = 2^20 + 128 rows, K = 4096, so
+    the rows from 2^20 on start past element 2^32): the conversion into the fp16 workspace copy
+    addresses every row from a 64-bit base, so the last rows are their own (a 32-bit element offset
+    would wrap them onto the first rows). The first and the last 128 rows against the float64
+    oracle."""
+    M, N, K = (1 << 20) + 128, 64, 4096
+    rng = np.random.default_rng(90 + ty)
+    raw = synth.kquant_weights(rng, ty, N, K)
+    g = torch.Generator(device=dev)
+    g.manual_seed(91)
+    x = torch.empty((M, K), dtype=torch.bfloat16, device=dev).normal_(generator=g)
+    y = _gemm_ws(ty, to_dev(raw, dev), x, N, K, dev)
+    wref = matrix_ref(ty, raw, N, K)
+    for r0 in (0, M - 128):
+        x64 = x[r0:r0 + 128].to(torch.float64).cpu().numpy()
+        got = y[r0:r0 + 128].cpu().numpy()
+        assert matmul.rel_maxnorm(got, matmul.gemm_rows_f64(x64, wref)) < TOL, r0
+    del x, y
+    torch.cuda.empty_cache()

@@ -31,16 +31,14 @@ def test_upload_matches_file(dev, tmp_path):
     assert f.to_device("z", dev).numel() == 0
 
 
-@pytest.mark.parametrize("cb", [ops.EXL3_MCG, ops.EXL3_3INST])
-def test_exl3_layer_from_sharded_checkpoint(dev, tmp_path, cb):
-    rng = np.random.default_rng(61 + cb)
+def test_exl3_layer_from_sharded_checkpoint(dev, tmp_path):
+    rng = np.random.default_rng(62)
+    cb = ops.EXL3_MCG
     K, N = 512, 384
     t, suh, svh = synth.exl3_tensors(rng, K, N)
     pre = "model.language_model.layers.3.mlp.experts.0.down_proj"
     shard1 = [(pre + ".trellis", t.view(np.int16))]
-    shard2 = [(pre + ".suh", suh), (pre + ".svh", svh)]
-    if cb == ops.EXL3_MCG:
-        shard2.append((pre + ".mcg", np.array([0], np.int32)))
+    shard2 = [(pre + ".suh", suh), (pre + ".svh", svh), (pre + ".mcg", np.array([1], np.int32))]
     st_writer.write(tmp_path / "model-00001-of-00002.safetensors", shard1)
     st_writer.write(tmp_path / "model-00002-of-00002.safetensors", shard2)
     st_writer.write_index(tmp_path / "model.safetensors.index.json",
@@ -59,15 +57,19 @@ def test_exl3_layer_from_sharded_checkpoint(dev, tmp_path, cb):
     np.testing.assert_array_equal(direct(xd).cpu().numpy(), y)
 
 
-def test_exl3_layer_rejects_mul1_and_bad_shapes(dev, tmp_path):
+def test_exl3_layer_rejects_other_codebooks_and_bad_shapes(dev, tmp_path):
     rng = np.random.default_rng(63)
     t, suh, svh = synth.exl3_tensors(rng, 128, 128)
+    mcg = np.array([1], np.int32)
     st_writer.write(tmp_path / "m.safetensors", [("p.trellis", t.view(np.int16)), ("p.suh", suh), ("p.svh", svh),
-                                                  ("p.mul1", np.array([1], np.int32)),
+                                                  ("p.mcg", mcg), ("p.mul1", np.array([1], np.int32)),
                                                   ("q.trellis", t.view(np.int16)), ("q.suh", suh[:64]),
-                                                  ("q.svh", svh)])
+                                                  ("q.svh", svh), ("q.mcg", mcg),
+                                                  ("r.trellis", t.view(np.int16)), ("r.suh", suh), ("r.svh", svh)])
     ck = Checkpoint(tmp_path)
     with pytest.raises(NotImplementedError):
-        exl3_linear(ck, "p", dev)
+        exl3_linear(ck, "p", dev)   # mul1 codebook
     with pytest.raises(ValueError):
-        exl3_linear(ck, "q", dev)
+        exl3_linear(ck, "q", dev)   # suh of the wrong length
+    with pytest.raises(NotImplementedError):
+        exl3_linear(ck, "r", dev)   # no .mcg: the multiply-add codebook

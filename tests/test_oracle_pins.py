@@ -171,14 +171,15 @@ def test_exl3_window_decode_exhaustive():
     assert e_lo.min() >= 12 and e_lo.max() <= 15 and e_hi.min() >= 12 and e_hi.max() <= 15
 
 
-def test_exl3_3inst_hash_definition():
-    # codebook 0 (QTIP 3INST): x = w*89226354 + 64248484 mod 2^32 (parity unpinned:
-    # no fixture exists; this pins only the restated formula)
+def test_exl3_only_mcg_codebook():
+    # the reference implements one codebook, mcg (exl3_ref.py:19-22): any other id is rejected
+    # rather than decoded with constants nothing in the reference fixes
     w = np.array([0, 1, 65535], np.uint32)
-    y = exl3.hash_window(w, exl3.CB_3INST)
-    for wi, yi in zip(w.tolist(), y.tolist()):
-        x = (wi * 89226354 + 64248484) % (1 << 32)
-        assert yi == (x & 0x8FFF8FFF) ^ 0x3B603B60
+    for cb in (0, 2, -1):
+        with pytest.raises(ValueError):
+            exl3.hash_window(w, cb)
+        with pytest.raises(ValueError):
+            exl3.decode_window(w, cb)
 
 
 def test_exl3_slot_map_invariants():

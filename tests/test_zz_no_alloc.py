@@ -1,8 +1,8 @@
 """The allocation-free MoE entry point (vybdq_moe_forward_noalloc) against vybdq_moe_forward with a
 caller workspace: the same routing and bit-identical outputs, on two calls in a row of which the
 second is smaller (the scratch keeps the first call's contents), on both grouped expert kernels
-(multi-token GEMV up to 64 tokens, matrix-core GEMM above), and the size limit rejected before
-any launch."""
+(the grouped GEMV: q4_0 at one token, Q8_0 up to 64 tokens; the matrix-core GEMM above), and the
+size limit rejected before any launch."""
 
 import numpy as np
 import pytest
@@ -39,7 +39,7 @@ def _ref(ty, host, x, logits):
 
 
 @pytest.mark.parametrize("ty", [ops.GGML_Q4_0, ops.GGML_Q8_0])
-@pytest.mark.parametrize("Ts", [(16, 5), (96, 70), (80, 3)])
+@pytest.mark.parametrize("Ts", [(16, 5), (96, 70), (80, 3), (16, 1), (4, 1)])
 def test_moe_noalloc_matches_workspace_entry(dev, ty, Ts):
     layer, host = _layer(dev, ty, seed=sum(Ts) + ty)
     gen = torch.Generator(device=dev)

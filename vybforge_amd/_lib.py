@@ -16,7 +16,7 @@ OK = 0
 ERR_ARG, ERR_SHAPE, ERR_ALIGN, ERR_HIP, ERR_WORKSPACE = -1, -2, -3, -4, -5
 F32, F16, BF16, F64 = 0, 1, 2, 3
 Q4_GGML, Q4_INTERLEAVED = 0, 1
-EXL3_3INST, EXL3_MCG = 0, 1
+EXL3_MCG = 1
 MOE_NOALLOC_MAX_BYTES = 64 * 1024 * 1024  # VYBDQ_MOE_NOALLOC_MAX_BYTES
 PB_GEMV, PB_GEMM, PB_GEMM_XH = 0x100, 0x200, 0x300
 PB_MOE, PB_EXL3DQ, PB_EXL3INV = 0x400, 0x500, 0x600

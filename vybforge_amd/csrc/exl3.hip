@@ -3,9 +3,11 @@
 // Format (native/exl3/README.md:24-49, native/exl3/exl3_ref.py:1-120): W [K, N] stored as
 // 16x16 tiles, trellis uint16 [K/16][N/16][64] (256 nibbles per tile, LSB-first), suh fp16 [K],
 // svh fp16 [N]. Tile slot (r, c) takes a 16-bit window of the tile's nibble stream through the
-// tile-slot composition table and decodes it with the codebook hash:
-//   mcg   (1): x = w * 0xCBAC1FED            3inst (0): x = w * 89226354 + 64248484   (mod 2^32)
-//   y = (x & 0x8FFF8FFF) ^ 0x3B603B60;  value = fp16(fp16(y.lo) + fp16(y.hi))
+// tile-slot composition table and decodes it with the mcg codebook hash (exllamav3's
+// decode_3inst at cb=1, the only codebook the reference implements: native/exl3/exl3_ref.py:19-22,
+// native/kernels/exl3.vyb:15-19):
+//   x = w * 0xCBAC1FED (mod 2^32);  y = (x & 0x8FFF8FFF) ^ 0x3B603B60;
+//   value = fp16(fp16(y.lo) + fp16(y.hi))
 // Both halves of y always lie in [0.125, 2), so their float32 sum is exact and one fp16 add
 // (round to nearest even) equals the reference's float32-sum-then-round.
 // W = diag(suh) (H/sqrt(128)) What (H/sqrt(128)) diag(svh) per 128x128 block, H = Sylvester
@@ -76,59 +78,42 @@ __device__ __forceinline__ uint32_t mcg_hash(uint32_t d) {
   return x;
 }
 
-// The codebook hash of a window (its low 16 bits; higher bits are ignored) up to the two fp16
-// halves (before they are added).
-template <int CB>
+// The mcg hash of a window (its low 16 bits; higher bits are ignored) up to the two fp16 halves
+// (before they are added).
 __device__ __forceinline__ uint32_t decode_window_halves(uint32_t w) {
-  uint32_t x;
-  if constexpr (CB == VYBDQ_EXL3_MCG) {
-    x = mcg_hash<false>(w);
-  } else {
-    const uint32_t wl = w & 0xffffu;
-    uint32_t hi = wl * 0x0551u;
-    const uint32_t lo = wl * 0x7C72u + 0x03D45AA4u;
-    // keeps the two 16 x 16-bit products apart (full-rate 24-bit multiplies): combined, the
-    // compiler would emit one quarter-rate 32-bit multiply
-    asm volatile("" : "+v"(hi));
-    x = (hi << 16) + lo;
-  }
-  return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
+  return (mcg_hash<false>(w) & 0x8FFF8FFFu) ^ 0x3B603B60u;
 }
 
 // Lane slot q's window hashed up to the two fp16 halves. A one-piece window at a 16-bit boundary
 // is hashed straight from its stream dword; other one-piece windows are funnel-extracted without
 // a mask (the hash reads only the low 16 bits); two-piece windows are assembled from their masks.
-template <int CB>
 __device__ __forceinline__ uint32_t slot_halves(const uint32_t (&w)[6], int q) {
   const int o = kExl3SlotOff0[q];
   const bool one = kExl3SlotOff1[q] < 0 && kExl3SlotMask0[q] == 0xffffu;
-  if constexpr (CB == VYBDQ_EXL3_MCG) {
-    if (one && (o & 15) == 0) {
-      const uint32_t x = (o & 16) ? mcg_hash<true>(w[o >> 5]) : mcg_hash<false>(w[o >> 5]);
-      return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
-    }
+  if (one && (o & 15) == 0) {
+    const uint32_t x = (o & 16) ? mcg_hash<true>(w[o >> 5]) : mcg_hash<false>(w[o >> 5]);
+    return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
   }
-  if (one) return decode_window_halves<CB>(win_extract(w, o));
+  if (one) return decode_window_halves(win_extract(w, o));
   // A two-piece window whose first piece runs to the end of its stream dword and whose second
   // piece starts a dword is one funnel shift of those two dwords (the second above the first).
   const unsigned m0 = kExl3SlotMask0[q];
   const int n = __builtin_popcount(m0), o1 = kExl3SlotOff1[q];
   if (o1 >= 0 && m0 == (1u << n) - 1 && (o & 31) + n == 32 && ((o1 + n) & 31) == 0 &&
       kExl3SlotMask1[q] == (0xffffu & ~m0))
-    return decode_window_halves<CB>(__builtin_amdgcn_alignbit(w[(o1 + n) >> 5], w[o >> 5], o & 31));
+    return decode_window_halves(__builtin_amdgcn_alignbit(w[(o1 + n) >> 5], w[o >> 5], o & 31));
   uint32_t x = win_extract(w, o) & kExl3SlotMask0[q];
   if (kExl3SlotOff1[q] >= 0) x |= win_extract(w, kExl3SlotOff1[q]) & kExl3SlotMask1[q];
-  return decode_window_halves<CB>(x);
+  return decode_window_halves(x);
 }
 
 // The 32 values of lane j: val[q] = row q of column j (q < 16), row q-16 of column j+8. Both
 // halves of a hash lie in [0.125, 2), so their float32 sum is exact and one fp16 add rounds it as
 // the reference's float32-sum-then-round does.
-template <int CB>
 __device__ __forceinline__ void lane_decode(const uint32_t (&w)[6], _Float16 (&val)[32]) {
 #pragma unroll
   for (int q = 0; q < 32; ++q) {
-    const h2 v = __builtin_bit_cast(h2, slot_halves<CB>(w, q));
+    const h2 v = __builtin_bit_cast(h2, slot_halves(w, q));
     val[q] = v[0] + v[1];
   }
 }
@@ -164,7 +149,7 @@ __device__ __forceinline__ void chunk_window(const u4 c, uint32_t (&w)[6]) {
 
 // ---- decode-only: rotated basis What [K, N] ------------------------------------------------
 
-template <int CB, int ODT>
+template <int ODT>
 __global__ void __launch_bounds__(256) k_exl3_decode(const uint16_t *__restrict__ trellis, void *__restrict__ out,
                                                      int64_t ntiles, int NB) {
   const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -174,7 +159,7 @@ __global__ void __launch_bounds__(256) k_exl3_decode(const uint16_t *__restrict_
   uint32_t w[6];
   lane_window(trellis, safe, j, w);
   _Float16 v[32];
-  lane_decode<CB>(w, v);
+  lane_decode(w, v);
   if (tile >= ntiles) return;
   const int64_t kb = tile / NB, nb = tile % NB;
   const int64_t N = static_cast<int64_t>(NB) * 16;
@@ -231,7 +216,7 @@ __device__ __forceinline__ void fwht128_wave(float &a0, float &a1) {
 // One workgroup per 128x128 block: decode the 64 tiles into LDS (float, rows padded to 129),
 // FWHT every row, then every column, scale, store.
 
-template <int CB, int ODT>
+template <int ODT>
 __global__ void __launch_bounds__(256) k_exl3_dequant(const uint16_t *__restrict__ trellis,
                                                       const _Float16 *__restrict__ suh,
                                                       const _Float16 *__restrict__ svh, void *__restrict__ out,
@@ -246,7 +231,7 @@ __global__ void __launch_bounds__(256) k_exl3_dequant(const uint16_t *__restrict
     uint32_t w[6];
     lane_window(trellis, tile, j, w);
     _Float16 v[32];
-    lane_decode<CB>(w, v);
+    lane_decode(w, v);
 #pragma unroll
     for (int q = 0; q < 32; ++q)
       blk[(16 * tk + (q & 15)) * 129 + 16 * tn + j + (q >> 4) * 8] = static_cast<float>(v[q]);
@@ -303,7 +288,7 @@ __global__ void __launch_bounds__(64) k_exl3_xprep(const void *__restrict__ X, c
   xp[b * K + k0 + 1] = static_cast<_Float16>(a1 * kRScale);
 }
 
-template <int CB, int BP>
+template <int BP>
 __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ trellis, const void *__restrict__ X,
                                                    int xdt, const _Float16 *__restrict__ suh,
                                                    const _Float16 *__restrict__ svh, void *__restrict__ Y, int ydt,
@@ -465,7 +450,7 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
       }
 #pragma unroll
       for (int q = 0; q < 32; ++q) {
-        const h2 y = __builtin_bit_cast(h2, slot_halves<CB>(w, q));
+        const h2 y = __builtin_bit_cast(h2, slot_halves(w, q));
 #pragma unroll
         for (int b = 0; b < BP; ++b)
           acc[b][q >> 4] = __builtin_amdgcn_fdot2(y, __builtin_bit_cast(h2, xq[b][q & 15]), acc[b][q >> 4], false);
@@ -473,7 +458,7 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
       return;
     }
     _Float16 v[32];
-    lane_decode<CB>(w, v);
+    lane_decode(w, v);
     if constexpr (MMA) {
       // v[i] = W[16 kk + i][c0], v[16 + i] = W[16 kk + i][c0 + 8]: into k half (kk & 1) of the tile
       const int c0 = 16 * t + j;
@@ -688,7 +673,8 @@ using namespace vybdq;
 
 static int exl3_check(uint64_t trellis, int64_t K, int64_t N, int codebook) {
   VYBDQ_REQUIRE(trellis, VYBDQ_ERR_ARG, "null trellis");
-  VYBDQ_REQUIRE(codebook == VYBDQ_EXL3_MCG || codebook == VYBDQ_EXL3_3INST, VYBDQ_ERR_ARG, "unknown codebook");
+  VYBDQ_REQUIRE(codebook == VYBDQ_EXL3_MCG, VYBDQ_ERR_ARG,
+                "unsupported codebook: only mcg (1) is implemented, as in the reference");
   VYBDQ_REQUIRE(K > 0 && N > 0 && K % 16 == 0 && N % 16 == 0, VYBDQ_ERR_SHAPE, "K and N must be positive multiples of 16");
   VYBDQ_REQUIRE((trellis & 15) == 0, VYBDQ_ERR_ALIGN, "trellis must be 16-byte aligned");
   VYBDQ_REQUIRE(N / 16 < (1 << 30) && K / 16 < (1 << 30), VYBDQ_ERR_SHAPE, "too many tiles");
@@ -708,12 +694,8 @@ extern "C" int vybdq_exl3_decode_tiles(uint64_t trellis, uint64_t out, int64_t K
   hipStream_t s = as_stream(stream);
   const auto *t = reinterpret_cast<const uint16_t *>(trellis);
   void *o = reinterpret_cast<void *>(out);
-#define L(CB, ODT) hipLaunchKernelGGL((k_exl3_decode<CB, ODT>), dim3(grid), dim3(256), 0, s, t, o, ntiles, NB)
-  if (codebook == VYBDQ_EXL3_MCG) {
-    if (out_dt == VYBDQ_F32) L(VYBDQ_EXL3_MCG, VYBDQ_F32); else if (out_dt == VYBDQ_F16) L(VYBDQ_EXL3_MCG, VYBDQ_F16); else L(VYBDQ_EXL3_MCG, VYBDQ_F64);
-  } else {
-    if (out_dt == VYBDQ_F32) L(VYBDQ_EXL3_3INST, VYBDQ_F32); else if (out_dt == VYBDQ_F16) L(VYBDQ_EXL3_3INST, VYBDQ_F16); else L(VYBDQ_EXL3_3INST, VYBDQ_F64);
-  }
+#define L(ODT) hipLaunchKernelGGL((k_exl3_decode<ODT>), dim3(grid), dim3(256), 0, s, t, o, ntiles, NB)
+  if (out_dt == VYBDQ_F32) L(VYBDQ_F32); else if (out_dt == VYBDQ_F16) L(VYBDQ_F16); else L(VYBDQ_F64);
 #undef L
   return check_launch("vybdq_exl3_decode_tiles");
 }
@@ -734,19 +716,15 @@ extern "C" int vybdq_dequant_exl3(uint64_t trellis, uint64_t suh, uint64_t svh, 
   const auto *su = reinterpret_cast<const _Float16 *>(suh);
   const auto *sv = reinterpret_cast<const _Float16 *>(svh);
   void *o = reinterpret_cast<void *>(out);
-#define L(CB, ODT)                                                                                         \
+#define L(ODT)                                                                                             \
   do {                                                                                                     \
     static std::atomic<uint64_t> raised{0};                                                                \
-    const int rc = ensure_lds_limit(reinterpret_cast<const void *>(&k_exl3_dequant<CB, ODT>),              \
+    const int rc = ensure_lds_limit(reinterpret_cast<const void *>(&k_exl3_dequant<ODT>),                  \
                                     static_cast<int>(lds), raised, "vybdq_dequant_exl3");                  \
     if (rc) return rc;                                                                                     \
-    hipLaunchKernelGGL((k_exl3_dequant<CB, ODT>), grid, dim3(256), lds, s, t, su, sv, o, NB);             \
+    hipLaunchKernelGGL((k_exl3_dequant<ODT>), grid, dim3(256), lds, s, t, su, sv, o, NB);                 \
   } while (0)
-  if (codebook == VYBDQ_EXL3_MCG) {
-    if (out_dt == VYBDQ_F32) L(VYBDQ_EXL3_MCG, VYBDQ_F32); else if (out_dt == VYBDQ_F16) L(VYBDQ_EXL3_MCG, VYBDQ_F16); else L(VYBDQ_EXL3_MCG, VYBDQ_F64);
-  } else {
-    if (out_dt == VYBDQ_F32) L(VYBDQ_EXL3_3INST, VYBDQ_F32); else if (out_dt == VYBDQ_F16) L(VYBDQ_EXL3_3INST, VYBDQ_F16); else L(VYBDQ_EXL3_3INST, VYBDQ_F64);
-  }
+  if (out_dt == VYBDQ_F32) L(VYBDQ_F32); else if (out_dt == VYBDQ_F16) L(VYBDQ_F16); else L(VYBDQ_F64);
 #undef L
   return check_launch("vybdq_dequant_exl3");
 }
@@ -756,17 +734,17 @@ extern "C" int64_t vybdq_exl3_workspace_size(int64_t B, int64_t K, int64_t N) {
   return exl3_ws_bytes(B, K, N);
 }
 
-template <int CB, int BP>
+template <int BP>
 static void exl3_gemm_launch(const uint16_t *t, const void *X, int xdt, const _Float16 *su, const _Float16 *sv,
                              void *Y, int ydt, int B, const _Float16 *xp, float *zp, uint32_t *arr, int64_t K,
                              int NB, const Exl3Split &sp, hipStream_t s) {
   const size_t lds = exl3_lds_bytes(BP, sp.kbs);  // <= 160 KB, checked by the caller
   if (lds > 64 * 1024) {
     static std::atomic<uint64_t> raised{0};
-    if (ensure_lds_limit(reinterpret_cast<const void *>(&k_exl3_gemm<CB, BP>), 160 * 1024, raised, "exl3 gemm"))
+    if (ensure_lds_limit(reinterpret_cast<const void *>(&k_exl3_gemm<BP>), 160 * 1024, raised, "exl3 gemm"))
       return;  // the launch below then fails and check_launch reports it
   }
-  hipLaunchKernelGGL((k_exl3_gemm<CB, BP>), dim3(static_cast<unsigned>(NB / 8), static_cast<unsigned>(sp.S)),
+  hipLaunchKernelGGL((k_exl3_gemm<BP>), dim3(static_cast<unsigned>(NB / 8), static_cast<unsigned>(sp.S)),
                      dim3(256), lds, s, t, X, xdt, su, sv, Y, ydt, B, xp, zp, arr, K, NB, sp.kbs);
 }
 
@@ -802,16 +780,13 @@ extern "C" int vybdq_exl3_gemm(uint64_t trellis, uint64_t suh, uint64_t svh, uin
     const dim3 gx(static_cast<unsigned>(K / 128), static_cast<unsigned>(BP));
     VYBDQ_DISPATCH_IN(x_dt, XDT, hipLaunchKernelGGL((k_exl3_xprep<XDT>), gx, dim3(64), 0, s, x, su, xp, b, K));
   }
-#define G(CB)                                                                                         \
-  switch (BP) {                                                                                       \
-    case 1: exl3_gemm_launch<CB, 1>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;   \
-    case 2: exl3_gemm_launch<CB, 2>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;   \
-    case 4: exl3_gemm_launch<CB, 4>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;   \
-    case 8: exl3_gemm_launch<CB, 8>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;   \
-    default: exl3_gemm_launch<CB, 16>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break; \
+  switch (BP) {
+    case 1: exl3_gemm_launch<1>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;
+    case 2: exl3_gemm_launch<2>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;
+    case 4: exl3_gemm_launch<4>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;
+    case 8: exl3_gemm_launch<8>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;
+    default: exl3_gemm_launch<16>(t, x, x_dt, su, sv, y, y_dt, b, xp, zp, arr, K, NB, sp, s); break;
   }
-  if (codebook == VYBDQ_EXL3_MCG) { G(VYBDQ_EXL3_MCG) } else { G(VYBDQ_EXL3_3INST) }
-#undef G
   if (!exl3_fused(BP)) {
     const dim3 go(static_cast<unsigned>(N / 128), static_cast<unsigned>(B));
     VYBDQ_DISPATCH_IN(y_dt, YDT, hipLaunchKernelGGL((k_exl3_out<YDT>), go, dim3(64), 0, s, zp, sv, y, BP, sp.S, N));

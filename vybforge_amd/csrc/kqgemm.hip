@@ -327,7 +327,8 @@ static int kq_pb_launch(int xdt, const int64_t *pb, uint32_t *status, hipStream_
   return check_launch("p-block super-block gemm");
 }
 
-// ---- 128-row tiles over fp16 X (Q6_K, IQ2_S from 96 rows) ----------------------------------
+// ---- 128-row tiles over fp16 X (Q6_K and IQ2_S from 96 rows; Q4_K and Q5_K from 96 rows with
+// bf16 X and no workspace) -------------------------------------------------------------------
 //
 // Tile = 128 X rows x 64 weight rows, K step = 128 (half a super-block = four 32-weight runs).
 // Four waves in a 2 x 2 grid each own 64 rows x 32 columns (4 x 2 accumulator fragments), so per
@@ -368,9 +369,6 @@ template <int FMT> struct K2Run;
 // bytes, and the 32 nibble bytes of qs[32 (j / 2) ..]
 template <> struct K2Run<FMT_Q4_K> { static constexpr int DW = 12; };
 template <> struct K2Run<FMT_Q5_K> { static constexpr int DW = 20; };
-// Q6_K run (half hf, part, nibble nh): ql[64hf + 32part ..] and qh[32hf ..] as 9-dword windows,
-// the run's two scale bytes, d
-template <> struct K2Run<FMT_Q6_K> { static constexpr int DW = 20; };
 // IQ2_S run (sub-block j): its 4 grid-index bytes and 4 sign bytes as 2-dword windows, qh[j],
 // scales[j], d
 template <> struct K2Run<FMT_IQ2_S> { static constexpr int DW = 7; };
@@ -384,10 +382,12 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t *base, uint32_t off) {
 
 // Loads of run r of half hf for the super-block at sbase + o (sbase + 64 hf wave-uniform; o and
 // the run's offsets within the super-block per lane, 32-bit, so every load is a scalar base plus
-// a vector offset)
+// a vector offset). Q6_K does not come here: its four row lanes share the super-block's loads
+// (kq2_tile).
 template <int FMT>
 __device__ __forceinline__ void k2_load_run(const uint8_t *sbase, uint32_t o, int hf, int r,
                                             uint32_t (&d)[K2Run<FMT>::DW]) {
+  static_assert(FMT != FMT_Q6_K, "Q6_K runs are loaded by the quad path of kq2_tile");
   if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q5_K) {
     // 144 / 176-byte super-blocks keep every window dword aligned
     constexpr int QS = FMT == FMT_Q4_K ? 16 : 48;
@@ -409,24 +409,6 @@ __device__ __forceinline__ void k2_load_run(const uint8_t *sbase, uint32_t o, in
         d[8 + i] = b1[i];
       }
     }
-  } else if constexpr (FMT == FMT_Q6_K) {
-    const uint32_t part = static_cast<uint32_t>(r) >> 1, nh = static_cast<uint32_t>(r) & 1u;
-    const uint32_t of = o & ~3u;
-    const uint8_t *ql = sbase + 64 * hf, *qh = sbase + 128 + 32 * hf;
-    const uint32_t qo = of + 32 * part;
-    const u4a4 a0 = *reinterpret_cast<const u4a4 *>(ql + qo), a1 = *reinterpret_cast<const u4a4 *>(ql + qo + 16);
-    const u4a4 b0 = *reinterpret_cast<const u4a4 *>(qh + of), b1 = *reinterpret_cast<const u4a4 *>(qh + of + 16);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      d[i] = a0[i];
-      d[4 + i] = a1[i];
-      d[9 + i] = b0[i];
-      d[13 + i] = b1[i];
-    }
-    d[8] = ld_u32(ql, qo + 32);
-    d[17] = ld_u32(qh, of + 32);
-    d[18] = ld_u16(sbase + 192 + 8 * hf, o + 4 * nh + 2 * part);  // scales of the run's two 16-halves
-    d[19] = ld_u16(sbase + 208, o);                               // d
   } else {
     // sub-block j = 4 hf + r; the index and sign windows start 2 bytes past o
     const uint32_t of = ((o + 2) & ~3u) + 4 * static_cast<uint32_t>(r);
@@ -446,6 +428,7 @@ __device__ __forceinline__ void k2_load_run(const uint8_t *sbase, uint32_t o, in
 template <int FMT>
 __device__ __forceinline__ void k2_decode_run(const uint32_t (&d)[K2Run<FMT>::DW], uint32_t sh, int r,
                                               uint32_t (&out)[16]) {
+  static_assert(FMT != FMT_Q6_K, "Q6_K runs are decoded by the quad path of kq2_tile");
   if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q5_K) {
     // run r of half hf is sub-block j = 4 hf + r; the caller passes r + 4 hf. w = fp16(d sc) q -
     // fp16(dmin m) by one packed fma per pair (q exact from the 0x64qq bit pattern)
@@ -464,27 +447,6 @@ __device__ __forceinline__ void k2_decode_run(const uint32_t (&d)[K2Run<FMT>::DW
       const h2 p1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u)) + bias;
       out[2 * t] = __builtin_bit_cast(uint32_t, p0 * ds + dm);
       out[2 * t + 1] = __builtin_bit_cast(uint32_t, p1 * ds + dm);
-    }
-  } else if constexpr (FMT == FMT_Q6_K) {
-    const int part = r >> 1, nh = r & 1;
-    const uint32_t qls = 4 * nh, qhs = 2 * part + 4 * nh;  // nibble of ql, bit pair of qh
-    const float dd = half_bits_to_f32(d[19]);
-    const h2 ds0 = {static_cast<_Float16>(dd * static_cast<float>(static_cast<int8_t>(d[18] & 0xffu))),
-                    static_cast<_Float16>(dd * static_cast<float>(static_cast<int8_t>(d[18] & 0xffu)))};
-    const h2 ds1 = {static_cast<_Float16>(dd * static_cast<float>(static_cast<int8_t>(d[18] >> 8))),
-                    static_cast<_Float16>(dd * static_cast<float>(static_cast<int8_t>(d[18] >> 8)))};
-    const h2 bias = {static_cast<_Float16>(-1056.0f), static_cast<_Float16>(-1056.0f)};
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const uint32_t ql = __builtin_amdgcn_alignbit(d[t + 1], d[t], sh) >> qls;
-      const uint32_t qh = (__builtin_amdgcn_alignbit(d[9 + t + 1], d[9 + t], sh) >> qhs) & 0x03030303u;
-      const uint32_t v = (ql & 0x0F0F0F0Fu) | (qh << 4);  // 4 six-bit q in bytes
-      // bytes b -> fp16 halves 0x64bb = 1024 + b; minus 1056 = q - 32 exactly; times the scale
-      const h2 p0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u));
-      const h2 p1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u));
-      const h2 ds = t < 4 ? ds0 : ds1;  // elements 4t .. 4t+3: scale of the 16-element half
-      out[2 * t] = __builtin_bit_cast(uint32_t, (p0 + bias) * ds);
-      out[2 * t + 1] = __builtin_bit_cast(uint32_t, (p1 + bias) * ds);
     }
   } else {
     const uint32_t ix = __builtin_amdgcn_alignbit(d[1], d[0], sh);
@@ -525,7 +487,6 @@ __device__ __forceinline__ u4 bf16x8_to_f16(const u4 &v) {
 // workspace; |x| < 65504).
 template <int FMT, bool XB = false>
 __device__ __forceinline__ void kq2_tile(const Kq2Args &a, int u, _Float16 *As, _Float16 *Bs) {
-  constexpr int DW = K2Run<FMT>::DW;
   const int mn_tiles = a.m_tiles * a.n_tiles;
   const int split = u / mn_tiles;
   const int mn = u - split * mn_tiles;
@@ -584,19 +545,6 @@ __device__ __forceinline__ void kq2_tile(const Kq2Args &a, int u, _Float16 *As, 
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
-  };
-  // the step's decoded run and X chunks -> LDS
-  auto stage = [&](const uint32_t (&d)[DW], uint32_t sh, int rr) {
-    {
-      uint32_t w[16];
-      k2_decode_run<FMT>(d, sh, rr, w);
-      store_run32(bdst, w);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = tid + 256 * i;
-      *reinterpret_cast<u4 *>(As + (c >> 4) * kK2Lda + 8 * (c & 15)) = XB ? bf16x8_to_f16(xr[i]) : xr[i];
-    }
   };
   auto mfma_step = [&] {
     bar();
@@ -701,6 +649,20 @@ __device__ __forceinline__ void kq2_tile(const Kq2Args &a, int u, _Float16 *As, 
       mfma_step();
     }
   } else {
+    constexpr int DW = K2Run<FMT>::DW;
+    // the step's decoded run and X chunks -> LDS
+    auto stage = [&](const uint32_t (&d)[DW], uint32_t sh, int rr) {
+      {
+        uint32_t w[16];
+        k2_decode_run<FMT>(d, sh, rr, w);
+        store_run32(bdst, w);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int c = tid + 256 * i;
+        *reinterpret_cast<u4 *>(As + (c >> 4) * kK2Lda + 8 * (c & 15)) = XB ? bf16x8_to_f16(xr[i]) : xr[i];
+      }
+    };
     uint32_t dw[DW], sh = 0;
     auto load_step = [&](int s) {
       const uint32_t o = wlane + static_cast<uint32_t>(s >> 1) * SB;  // this lane's super-block

@@ -106,6 +106,9 @@ __global__ void __launch_bounds__(256) k_x_to_f16(const void *__restrict__ X, u4
   __shared__ float wmax[4];
   const int64_t row = blockIdx.x;
   const int64_t n8 = K / 8;
+  // the row's base in 64-bit arithmetic (M * K may exceed 2^32 elements); offsets inside the row
+  // are 32-bit (every caller bounds K below 2^24)
+  const void *Xr = static_cast<const char *>(X) + row * K * (XDT == VYBDQ_F32 ? 4 : 2);
   auto chunk_max = [](const XChunk<XDT> &c, float m) {
     if constexpr (XDT == VYBDQ_F32) {
 #pragma unroll
@@ -141,7 +144,7 @@ __global__ void __launch_bounds__(256) k_x_to_f16(const void *__restrict__ X, u4
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int64_t i = threadIdx.x + 256 * j;
-      if (i < n8) x_load<XDT>(X, static_cast<uint32_t>(row * K + i * 8), cc[j]);
+      if (i < n8) x_load<XDT>(Xr, static_cast<uint32_t>(i * 8), cc[j]);
     }
 #pragma unroll
     for (int j = 0; j < CH; ++j)
@@ -149,7 +152,7 @@ __global__ void __launch_bounds__(256) k_x_to_f16(const void *__restrict__ X, u4
   } else {
     for (int64_t i = threadIdx.x; i < n8; i += 256) {
       XChunk<XDT> c;
-      x_load<XDT>(X, static_cast<uint32_t>(row * K + i * 8), c);
+      x_load<XDT>(Xr, static_cast<uint32_t>(i * 8), c);
       amax = chunk_max(c, amax);
     }
   }
@@ -170,7 +173,7 @@ __global__ void __launch_bounds__(256) k_x_to_f16(const void *__restrict__ X, u4
   } else {
     for (int64_t i = threadIdx.x; i < n8; i += 256) {
       XChunk<XDT> c;
-      x_load<XDT>(X, static_cast<uint32_t>(row * K + i * 8), c);
+      x_load<XDT>(Xr, static_cast<uint32_t>(i * 8), c);
       Xh[row * n8 + i] = chunk_f16(c, inv);
     }
   }

@@ -283,7 +283,7 @@ class GemvChain:
 
 # ---- EXL3 --------------------------------------------------------------------------------
 
-EXL3_MCG, EXL3_3INST = _lib.EXL3_MCG, _lib.EXL3_3INST
+EXL3_MCG = _lib.EXL3_MCG
 
 
 def exl3_decode_tiles(trellis, K, N, out_dtype=torch.float16, codebook=_lib.EXL3_MCG):

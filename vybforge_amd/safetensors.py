@@ -184,8 +184,11 @@ class Checkpoint:
 def exl3_linear(ckpt, prefix, device, max_batch=16):
     """ops.Exl3Linear from <prefix>.trellis / .suh / .svh (+ .mcg) of a Checkpoint.
 
-    K = 16 * trellis.shape[0], N = 16 * trellis.shape[1]; the codebook is mcg when <prefix>.mcg is
-    present and 3INST otherwise; a <prefix>.mul1 tensor (a third codebook) is rejected."""
+    K = 16 * trellis.shape[0], N = 16 * trellis.shape[1]. The codebook must be mcg, the only one
+    the reference implements: <prefix>.mcg must be present (its value is not read: the reference
+    documents it both as the id 1, native/exl3/exl3_ref.py:11, and as the multiplier 0xCBAC1FED,
+    native/exl3/README.md:32). A layer without it (exllamav3's multiply-add codebook) or with
+    <prefix>.mul1 is rejected."""
     _, tr = ckpt.locate(prefix + ".trellis")
     if len(tr["shape"]) != 3 or tr["shape"][2] != 64 or tr["dtype"] not in ("I16", "U16"):
         raise ValueError(f"{prefix}.trellis: expected int16 [K/16, N/16, 64], got {tr['dtype']} {tr['shape']}")
@@ -196,8 +199,9 @@ def exl3_linear(ckpt, prefix, device, max_batch=16):
             raise ValueError(f"{prefix}.{sfx}: expected F16 [{n}], got {ti['dtype']} {ti['shape']}")
     if f"{prefix}.mul1" in ckpt:
         raise NotImplementedError(f"{prefix}: the mul1 codebook is not supported")
-    cb = ops.EXL3_MCG if f"{prefix}.mcg" in ckpt else ops.EXL3_3INST
+    if f"{prefix}.mcg" not in ckpt:
+        raise NotImplementedError(f"{prefix}: no .mcg tensor; only the mcg codebook is supported")
     t = ckpt.to_device(prefix + ".trellis", device, torch.int16)
     suh = ckpt.to_device(prefix + ".suh", device)
     svh = ckpt.to_device(prefix + ".svh", device)
-    return ops.Exl3Linear(t, suh, svh, K, N, cb, max_batch=max_batch)
+    return ops.Exl3Linear(t, suh, svh, K, N, ops.EXL3_MCG, max_batch=max_batch)
