@@ -443,6 +443,31 @@ int vybdq_moe_forward_noalloc(int wtype, uint64_t x, int x_dt, uint64_t logits, 
                               int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk, double scale,
                               double limit, uint64_t stream);
 
+/* ---- MoE layer with EXL3 routed experts -------------------------------------------------- */
+
+/* Workspace bytes for vybdq_moe_forward_exl3, or -1 for an unsupported shape. */
+int64_t vybdq_moe_exl3_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk);
+
+/* The reference's production GLM-5.3 MoE layer (native/glm53/glm_engine.vyb:2728-2990) in one call:
+   out [T, H] = sum_s w[t,s] * FFN_{idx[t,s]}(x[t]) + FFN_shared(x[t]), FFN(x) =
+   (silu(min(x Wg, limit)) * clamp(x Wu, -limit, limit)) Wd, routing as vybdq_moe_forward (bias: the
+   e_score_correction_bias, selection only). Routed experts are EXL3 4-bpw matrices (mcg codebook):
+   `experts` is a device table uint64 [E][9] of the addresses of gate.trellis, gate.suh, gate.svh,
+   up.trellis, up.suh, up.svh, down.trellis, down.suh, down.svh of each expert (trellis int16
+   [in/16][out/16][64], 16-byte aligned; suh fp16 [in]; svh fp16 [out]; gate/up in = H, out = I;
+   down in = I, out = H). The shared expert (s_gate, s_up [I][H], s_down [H][I], bf16 [out][in] as
+   mlp.shared_experts.*.weight, 16-byte aligned; or all 0) runs on every token with weight 1.
+   x [T, H] f32/f16/bf16 (16-byte aligned), logits [T, E], out F32/F16/BF16; H, I multiples of 128.
+   Routing, bucketing, the per-expert EXL3 products (trellis decoded in registers, the Hadamard
+   rotations applied to the activations) and the combine all run on the stream: no host loop, no
+   host synchronisation, no dequantized weights. Replaces the per-expert loop with exl3_deq32 + f64
+   GEMMs (glm_engine.vyb:2804-2953) and the shared expert's deq_bf16 + GEMMs (:2955-2990). */
+int vybdq_moe_forward_exl3(uint64_t x, int x_dt, uint64_t logits, int logits_dt, uint64_t bias, uint64_t experts,
+                           uint64_t s_gate, uint64_t s_up, uint64_t s_down, uint64_t out, int out_dt,
+                           uint64_t idx_out, uint64_t w_out, int64_t T, int64_t H, int64_t I, int64_t E,
+                           int64_t topk, double scale, double limit, uint64_t ws, int64_t ws_bytes,
+                           uint64_t stream);
+
 /* ---- activation quantizer ------------------------------------------------------------ */
 
 /* xq8 semantics per row and per 32-value block: a = max|x|, d = a/127, q = sat_s8(rne(x*127/a))

@@ -99,9 +99,13 @@ SIGNATURES = {
     "vybdq_moe_forward_noalloc": [_int, _u64, _int, _u64, _int, _u64, _u64, _u64, _u64, _u64, _u64, _u64, _u64,
                                   _int, _u64, _u64, _i64, _i64, _i64, _i64, _i64, ctypes.c_double,
                                   ctypes.c_double, _u64],
+    "vybdq_moe_exl3_workspace_size": [_i64, _i64, _i64, _i64, _i64],
+    "vybdq_moe_forward_exl3": [_u64, _int, _u64, _int, _u64, _u64, _u64, _u64, _u64, _u64, _int, _u64, _u64,
+                               _i64, _i64, _i64, _i64, _i64, ctypes.c_double, ctypes.c_double, _u64, _i64, _u64],
 }
 _RESTYPE = {"vybdq_last_error": ctypes.c_char_p, "vybdq_chain_workspace_size": ctypes.c_int64,
             "vybdq_exl3_workspace_size": ctypes.c_int64, "vybdq_moe_workspace_size": ctypes.c_int64,
+            "vybdq_moe_exl3_workspace_size": ctypes.c_int64,
             "vybdq_gemm_workspace_size": ctypes.c_int64, "vybdq_gemm_q8_0_i8_workspace_size": ctypes.c_int64,
             "vybdq_gguf_kv_float": ctypes.c_double}
 for _n in ("vybdq_gguf_open", "vybdq_gguf_info", "vybdq_gguf_find_tensor", "vybdq_gguf_find_kv",

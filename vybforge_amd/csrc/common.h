@@ -168,6 +168,23 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t bits16) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
 }
 
+// Block scale for the largest |x| of a block: with ex its biased float32 exponent
+// (2^(ex - 127) <= amax < 2^(ex - 126)), the block is staged as x * 2^-e, e = ex - 141, which brings
+// its largest value into [2^14, 2^15): no overflow for large activations, no fp16 subnormals for
+// small ones (a power of two: exact). e is clamped to [-100, 113] (beyond that the block is still
+// representable, if less precisely); all-zero blocks stay unscaled. Returns 2^e, writes 2^-e.
+__device__ __forceinline__ float block_scale(float amax, float &inv) {
+  const int ex = static_cast<int>((__float_as_uint(amax) >> 23) & 0xffu);
+  if (ex == 0) {
+    inv = 1.0f;
+    return 1.0f;
+  }
+  int e = ex - 141;
+  e = e < -100 ? -100 : (e > 113 ? 113 : e);
+  inv = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
+  return __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
+}
+
 }  // namespace vybdq
 
 // Dispatch a runtime dtype to a template parameter.

@@ -490,6 +490,47 @@ static int launch_route(const void *lg, int logits_dt, const float *bias, int64_
   return check_launch("moe route");
 }
 
+namespace vybdq {
+
+// Routing and bucketing for a grouped expert call without shared-expert rows (moe_exl3.hip):
+// idx / w [T topk], pos ((token, slot) -> row), row_map (row -> token) and the row groups of at
+// most BMr rows, both as m-tiles (tiles) and as explicit row ranges {expert, r0, r1, 0} (tiles2),
+// in the caller's memory. Up to 8 tokens one launch (routing and bucketing in one workgroup),
+// else the router and one bucketing workgroup.
+int moe_route_bucket(const void *logits, int logits_dt, const float *bias, int64_t T, int64_t E, int64_t topk,
+                     double scale, int BMr, int *idx, float *w, int *pos, int *row_map, int4 *tiles, int *ntiles,
+                     int4 *tiles2, int *ntiles2, hipStream_t s) {
+  const int e = static_cast<int>(E), k = static_cast<int>(topk), tt = static_cast<int>(T);
+  if (T <= 8) {
+    const bool wave_rows = T * topk <= 64;
+    const size_t shb = static_cast<size_t>(2 * E + T * topk) * 4;
+#define RB(LDT, KEYED)                                                                                          \
+  do {                                                                                                        \
+    if (wave_rows)                                                                                            \
+      hipLaunchKernelGGL((k_moe_route_bucket_w<LDT, KEYED>), dim3(1), dim3(256), 0, s, logits, bias, e, k, scale, \
+                         idx, w, tt, BMr, BMr, 0, pos, row_map, tiles, ntiles, tiles2, ntiles2);               \
+    else                                                                                                      \
+      hipLaunchKernelGGL((k_moe_route_bucket<LDT, KEYED>), dim3(1), dim3(256), shb, s, logits, bias, e, k, scale, \
+                         idx, w, tt, BMr, BMr, 0, pos, row_map, tiles, ntiles, tiles2, ntiles2);               \
+  } while (0)
+    if (logits_dt == VYBDQ_F64) RB(VYBDQ_F64, false);
+    else if (bias) { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT, false)); }
+    else { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT, true)); }
+#undef RB
+    return check_launch("moe route + bucket");
+  }
+  const int rc = launch_route(logits, logits_dt, bias, T, E, topk, scale, idx, w, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_moe_bucket_tiles, dim3(1), dim3(256), static_cast<size_t>(2 * E) * 4, s, idx, tt, k, e, BMr,
+                     BMr, 0, pos, row_map, tiles, ntiles, tiles2, ntiles2);
+  return check_launch("moe bucket");
+}
+
+// Upper bound of the row-group list of moe_route_bucket for groups of at most `rows` rows.
+int64_t moe_tiles_bound(int64_t T, int64_t E, int64_t k, int64_t rows) { return moe_max_tiles(T, E, k, rows); }
+
+}  // namespace vybdq
+
 extern "C" int vybdq_moe_route(uint64_t logits, int logits_dt, uint64_t bias, uint64_t idx_out, uint64_t w_out,
                                int64_t T, int64_t E, int64_t topk, double scale, uint64_t stream) {
   VYBDQ_REQUIRE(logits && idx_out && w_out, VYBDQ_ERR_ARG, "null logits, idx_out or w_out");

@@ -460,3 +460,69 @@ class MoeLayer:
             ws, nb = self._workspace(T, x.device)
             call("vybdq_moe_forward", *args, ws, nb, _stream())
         return (out, idx, w) if routing else out
+
+
+EXL3_EXPERT_FIELDS = ("gate_proj.trellis", "gate_proj.suh", "gate_proj.svh", "up_proj.trellis", "up_proj.suh",
+                      "up_proj.svh", "down_proj.trellis", "down_proj.suh", "down_proj.svh")
+
+
+class MoeExl3Layer:
+    """The GLM-5.3 MoE layer with EXL3 4-bpw routed experts and a bf16 shared expert
+    (vybdq_moe_forward_exl3; the reference's native/glm53/glm_engine.vyb:2728-2990).
+
+    experts: E sequences of the 9 device tensors of EXL3_EXPERT_FIELDS (trellis int16
+    [in/16, out/16, 64], suh fp16 [in], svh fp16 [out]; gate/up in = H, out = I; down in = I, out = H),
+    wherever they live in device memory. shared: (gate [I, H], up [I, H], down [H, I]) bf16 or None.
+    bias: the e_score_correction_bias (float32 [E], selection only) or None."""
+
+    def __init__(self, experts, H, I, topk=8, shared=None, scale=2.5, limit=10.0, bias=None):
+        E = len(experts)
+        _need(E >= 1 and H % 128 == 0 and I % 128 == 0, "need experts and H, I multiples of 128")
+        shapes = ((H // 16, I // 16, 64), (H,), (I,)) * 2 + ((I // 16, H // 16, 64), (I,), (H,))
+        addrs = []
+        for e, ts in enumerate(experts):
+            _need(len(ts) == 9, f"expert {e}: need the 9 tensors {EXL3_EXPERT_FIELDS}")
+            for f, (t, shp) in enumerate(zip(ts, shapes)):
+                ok = (t.element_size() == 2 and t.numel() == math.prod(shp) and t.is_cuda and t.is_contiguous() and
+                      (f % 3 != 0 or t.data_ptr() % 16 == 0) and (f % 3 == 0 or t.dtype == torch.float16))
+                _need(ok, f"expert {e} {EXL3_EXPERT_FIELDS[f]}: expected 16-bit {shp}")
+                addrs.append(t.data_ptr())
+        dev = experts[0][0].device
+        self.table = torch.tensor(addrs, dtype=torch.int64).to(dev)
+        self.experts = [tuple(ts) for ts in experts]  # the table holds their addresses
+        if shared is not None:
+            for t, shp, what in zip(shared, ((I, H), (I, H), (H, I)), ("gate", "up", "down")):
+                _need(t.dtype == torch.bfloat16 and tuple(t.shape) == shp and t.data_ptr() % 16 == 0,
+                      f"shared {what} must be bf16 {shp}")
+        _need(bias is None or (bias.numel() == E and bias.dtype == torch.float32), "bias must be float32 [E]")
+        self.H, self.I, self.E, self.topk = H, I, E, topk
+        self.shared, self.scale, self.limit, self.bias = shared, scale, limit, bias
+        self._ws, self._ws_bytes = None, 0
+
+    def _workspace(self, T, device):
+        n = _lib.lib.vybdq_moe_exl3_workspace_size(T, self.H, self.I, self.E, self.topk)
+        if n < 0:
+            raise ValueError("unsupported MoE shape")
+        if self._ws is None or self._ws_bytes < n:
+            self._ws = torch.empty(n + 256, dtype=torch.uint8, device=device)
+            self._ws_bytes = n
+        return (self._ws.data_ptr() + 255) // 256 * 256, self._ws_bytes
+
+    def __call__(self, x, logits, out_dtype=torch.float32, out=None, routing=False):
+        """out [T, H] for x [T, H] and logits [T, E] (and the routing when routing=True)."""
+        T = x.shape[0]
+        _need(x.dim() == 2 and x.shape[1] == self.H, f"x must be [T, {self.H}]")
+        _need(logits.dim() == 2 and tuple(logits.shape) == (T, self.E), f"logits must be [T, {self.E}]")
+        if out is None:
+            out = torch.empty((T, self.H), dtype=out_dtype, device=x.device)
+        _check_out(out, (T, self.H))
+        idx = w = None
+        if routing:
+            idx = torch.empty((T, self.topk), dtype=torch.int32, device=x.device)
+            w = torch.empty((T, self.topk), dtype=torch.float32, device=x.device)
+        sg, su, sd = self.shared if self.shared else (None, None, None)
+        ws, nb = self._workspace(T, x.device)
+        call("vybdq_moe_forward_exl3", _ptr(x), _dt(x.dtype), _ptr(logits), _dt(logits.dtype), _ptr(self.bias),
+             _ptr(self.table), _ptr(sg), _ptr(su), _ptr(sd), _ptr(out), _dt(out.dtype), _ptr(idx), _ptr(w), T, self.H,
+             self.I, self.E, self.topk, float(self.scale), float(self.limit), ws, nb, _stream())
+        return (out, idx, w) if routing else out

@@ -205,3 +205,54 @@ def exl3_linear(ckpt, prefix, device, max_batch=16):
     suh = ckpt.to_device(prefix + ".suh", device)
     svh = ckpt.to_device(prefix + ".svh", device)
     return ops.Exl3Linear(t, suh, svh, K, N, ops.EXL3_MCG, max_batch=max_batch)
+
+
+def moe_exl3_layer(ckpt, prefix, device, n_experts, topk=8, scale=2.5, limit=10.0):
+    """ops.MoeExl3Layer of one GLM-5.3 MoE layer from a checkpoint, by the reference's tensor names
+    (native/glm53/glm_engine.vyb:2733-2736,2845-2862,2955-2960; naming in native/glm53/loader.py:20-35):
+    <prefix>mlp.experts.<e>.{gate,up,down}_proj.{trellis,suh,svh,mcg} for e < n_experts (EXL3 4-bpw,
+    mcg codebook), <prefix>mlp.shared_experts.{gate,up,down}_proj.weight (bf16 [out, in]) and
+    <prefix>mlp.gate.e_score_correction_bias (f32 [E], the selection bias). H and I come from the
+    first expert's trellis shapes; every expert must match them."""
+    experts = []
+    H = I = None
+    for e in range(n_experts):
+        ep = f"{prefix}mlp.experts.{e}."
+        ts = []
+        for proj in ("gate_proj", "up_proj", "down_proj"):
+            base = ep + proj
+            if f"{base}.mcg" not in ckpt:
+                raise NotImplementedError(f"{base}: no .mcg tensor; only the mcg codebook is supported")
+            _, tr = ckpt.locate(base + ".trellis")
+            if len(tr["shape"]) != 3 or tr["shape"][2] != 64 or tr["dtype"] not in ("I16", "U16"):
+                raise ValueError(f"{base}.trellis: expected int16 [in/16, out/16, 64], got {tr['dtype']} {tr['shape']}")
+            kin, nout = 16 * tr["shape"][0], 16 * tr["shape"][1]
+            if proj == "gate_proj" and H is None:
+                H, I = kin, nout
+            want = (H, I) if proj != "down_proj" else (I, H)
+            if (kin, nout) != want:
+                raise ValueError(f"{base}.trellis: [in {kin}, out {nout}], expected {want}")
+            ts.append(ckpt.to_device(base + ".trellis", device, torch.int16))
+            for sfx, n in (("suh", kin), ("svh", nout)):
+                _, ti = ckpt.locate(f"{base}.{sfx}")
+                if ti["dtype"] != "F16" or ti["shape"] != [n]:
+                    raise ValueError(f"{base}.{sfx}: expected F16 [{n}], got {ti['dtype']} {ti['shape']}")
+                ts.append(ckpt.to_device(f"{base}.{sfx}", device))
+        experts.append(ts)
+    shared = None
+    sp = f"{prefix}mlp.shared_experts."
+    if sp + "gate_proj.weight" in ckpt:
+        shared = []
+        for proj, shp in (("gate_proj", [I, H]), ("up_proj", [I, H]), ("down_proj", [H, I])):
+            _, ti = ckpt.locate(f"{sp}{proj}.weight")
+            if ti["dtype"] != "BF16" or ti["shape"] != shp:
+                raise ValueError(f"{sp}{proj}.weight: expected BF16 {shp}, got {ti['dtype']} {ti['shape']}")
+            shared.append(ckpt.to_device(f"{sp}{proj}.weight", device))
+    bias = None
+    bname = f"{prefix}mlp.gate.e_score_correction_bias"
+    if bname in ckpt:
+        bias = ckpt.to_device(bname, device, torch.float32) if ckpt.locate(bname)[1]["dtype"] == "F32" else None
+        if bias is None or bias.numel() != n_experts:
+            raise ValueError(f"{bname}: expected F32 [{n_experts}]")
+    return ops.MoeExl3Layer(experts, H, I, topk=topk, shared=tuple(shared) if shared else None, scale=scale,
+                            limit=limit, bias=bias)
