@@ -41,7 +41,7 @@ QWEN3_4B = dict(hidden=2560, q=4096, kv=1024, inter=9728, layers=36)
 STACK_TRAFFIC = dict(bytes_per_launch=14402381, source="profiles/q4_0_gemv_decode_stack.md (rocprofv3 --pmc)")
 
 CONFIGS = ["stack", "stack_chain", "gemv1", "kquant", "producers", "router", "exl3", "prefill", "prefill_i8",
-           "prefill_kq", "moe", "pblock", "copy"]
+           "prefill_kq", "moe", "moe_exl3", "pblock", "copy"]
 
 
 def parse():
@@ -635,19 +635,24 @@ def check_moe(torch, layer, x, logits, out, idx, w, ntok=2):
 def run_moe(args, torch, dev, tokens=None, built=None):
     """GLM-5-style MoE layer, H=6144, 256 routed + 1 shared expert, top-8, I=2048, q4_0 expert tensors
     (5.46 GB), T tokens bf16, router logits N(0,1). T <= 16: the step is R layer calls on R distinct
-    (x, logits) pairs, so the experts hit per step exceed the 256 MB MALL."""
+    (x, logits) pairs, each call with its own shared expert (as each layer of a model has), so the
+    experts hit per step exceed the 256 MB MALL."""
+    from vybforge_amd import ops, synth
     H, E, k = MOE["H"], MOE["E"], MOE["k"]
     I = MOE["I"]
     T = tokens or args.tokens
-    layer, gen = built or build_moe(torch, dev, args.seed + 5)
+    base, gen = built or build_moe(torch, dev, args.seed + 5)
     R = 8 if T == 1 else (2 if T <= 16 else 1)
+    q4 = lambda n, kk: synth.q4_0_weights_torch(gen, n, kk, dev)
+    layers = [base] + [ops.MoeLayer(ops.GGML_Q4_0, *base.w, H, I, E, k, shared=(q4(I, H), q4(I, H), q4(H, I)))
+                       for _ in range(R - 1)]
     xs = [torch.randn(T, H, generator=gen, device=dev).to(torch.bfloat16) for _ in range(R)]
     lgs = [torch.randn(T, E, generator=gen, device=dev) for _ in range(R)]
     outs = [torch.empty(T, H, device=dev) for _ in range(R)]
-    routed = [layer(xs[r], lgs[r], routing=True) for r in range(R)]
+    routed = [layers[r](xs[r], lgs[r], routing=True) for r in range(R)]
     distinct = [int(torch.unique(rt[1]).numel()) for rt in routed]
     union = int(torch.unique(torch.cat([rt[1].reshape(-1) for rt in routed])).numel())
-    ms, wall = timed_graph(torch, [lambda r=r: layer(xs[r], lgs[r], out=outs[r]) for r in range(R)], args.steps,
+    ms, wall = timed_graph(torch, [lambda r=r: layers[r](xs[r], lgs[r], out=outs[r]) for r in range(R)], args.steps,
                            args.warmup)
     per_expert = 3 * I * H // 32 * 18
     nbytes = sum((d + 1) * per_expert + T * H * 2 + T * E * 4 + T * H * 4 for d in distinct)
@@ -659,7 +664,7 @@ def run_moe(args, torch, dev, tokens=None, built=None):
         for r in sorted({0, R - 1}):
             if not torch.equal(outs[r], routed[r][0]):
                 raise CheckFailed(f"moe T={T}: graph replay output differs from the eager call")
-            rels.append(check_moe(torch, layer, xs[r], lgs[r], outs[r], routed[r][1], routed[r][2]))
+            rels.append(check_moe(torch, layers[r], xs[r], lgs[r], outs[r], routed[r][1], routed[r][2]))
         check = dict(ok=True, rel=max(rels), what="routing of every token; 2 tokens x 256 columns vs float64 oracle; "
                                                   "graph replay == eager")
     path = "k_moe_gemv" if T <= 64 else "k_moe_mm"
@@ -669,8 +674,114 @@ def run_moe(args, torch, dev, tokens=None, built=None):
     return dict(value=gbs, unit="GB/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
                 tflops=round(flops / (ms * 1e-3) / 1e12, 3),
                 workload=f"GLM-5-style MoE layer T={T}: H=6144, 256+1 experts, top-8, I=2048, q4_0; {R} layer "
-                         f"call(s) per step on distinct inputs ({sum(distinct) / R:.1f} routed experts hit per call, "
-                         f"{union} distinct per step)",
+                         f"call(s) per step on distinct inputs, each with its own shared expert "
+                         f"({sum(distinct) / R:.1f} routed experts hit per call, {union} distinct per step)",
+                bytes_per_step=nbytes, launches_per_step=R, check=check)
+
+
+# ---- the reference's GLM-5.3 MoE layer: EXL3 routed experts + bf16 shared expert ----------------
+
+MOE53 = dict(H=4096, I=2048, E=288, k=8)
+
+
+def build_moe_exl3(torch, dev, seed, n_shared=1):
+    """288 EXL3 4-bpw experts (distinct seeded trellis, suh/svh = +-|N(0, 0.12)|, so that the expert
+    matrices have entries of about N(0, 0.02) like a real checkpoint's; 3.6 GB) and n_shared bf16 shared
+    experts (N(0, 0.02)), e_score_correction_bias N(0, 0.05); layer j uses shared expert j."""
+    from vybforge_amd import ops
+    H, I, E, k = MOE53["H"], MOE53["I"], MOE53["E"], MOE53["k"]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    sgn = lambda n: torch.randint(0, 2, (n,), generator=gen, device=dev) * 2 - 1
+    sc = lambda n: ((torch.randn(n, generator=gen, device=dev) * 0.12).abs() * sgn(n)).to(torch.float16)
+    experts = []
+    for _ in range(E):
+        ts = []
+        for K, N in ((H, I), (H, I), (I, H)):
+            t = torch.randint(0, 65536, (K // 16, N // 16, 64), generator=gen, device=dev,
+                              dtype=torch.int32).to(torch.uint16).view(torch.int16)
+            ts += [t, sc(K), sc(N)]
+        experts.append(ts)
+    bf = lambda n, kk: (torch.randn(n, kk, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(E, generator=gen, device=dev) * 0.05
+    layers = [ops.MoeExl3Layer(experts, H, I, topk=k, shared=(bf(I, H), bf(I, H), bf(H, I)), bias=bias)
+              for _ in range(n_shared)]
+    return layers, gen
+
+
+def check_moe_exl3(torch, layer, x, logits, out, idx, w):
+    """Routing of every token against the oracle router (bias included; identical ids, |dw| < 1e-4);
+    the last token's output on 256 columns of H against float64 (each hit expert decoded on the host,
+    its products in the FWHT form x W = svh * fwht(fwht(x * suh) What))."""
+    import numpy as np
+    from oracle import exl3, moe
+    H, k = MOE53["H"], MOE53["k"]
+    T = x.shape[0]
+    bias = layer.bias.cpu().numpy()
+    ridx, rw = moe.route_logits(logits.to(torch.float64).cpu().numpy(), k, bias)
+    if not np.array_equal(idx.cpu().numpy(), ridx) or np.abs(w.cpu().numpy() - rw).max() >= 1e-4:
+        raise CheckFailed(f"moe_exl3 T={T}: routing differs from the oracle")
+    c0 = (T * 997) % (H - 256) // 128 * 128
+    t = T - 1
+    xt = x[t:t + 1].to(torch.float64).cpu().numpy()
+    h = lambda a: a.cpu().numpy().astype(np.float64)
+    tr = lambda a: a.view(torch.int16).cpu().numpy().view(np.uint16)
+    apply = lambda v, what, suh, svh: exl3.fwht128_rows(exl3.fwht128_rows(v * suh) @ what) * svh
+    sg, su, sd = (a.to(torch.float64).cpu().numpy() for a in layer.shared)
+    sh_ref = moe.ffn_rows(xt, sg, su, sd[c0:c0 + 256])[0]
+    ref = np.zeros(256)
+    for s in range(k):
+        e = layer.experts[int(ridx[t, s])]
+        g = apply(xt, exl3.decode_rotated(tr(e[0])).astype(np.float64), h(e[1]), h(e[2]))
+        u = apply(xt, exl3.decode_rotated(tr(e[3])).astype(np.float64), h(e[4]), h(e[5]))
+        # the down projection's 256 columns: two 128-column Hadamard blocks
+        nb = slice(c0 // 16, (c0 + 256) // 16)
+        wd = exl3.decode_rotated(tr(e[6])[:, nb]).astype(np.float64)
+        ref += rw[t, s] * apply(moe.swiglu(g, u), wd, h(e[7]), h(e[8])[c0:c0 + 256])[0]
+    got = out.cpu().numpy()[t:t + 1, c0:c0 + 256]
+    # the whole output, and the routed experts' part alone (the shared expert cannot mask it)
+    return max(expect(f"moe_exl3 T={T}", rel_gate(got, (sh_ref + ref)[None])),
+               expect(f"moe_exl3 T={T} routed part", rel_gate(got - sh_ref[None], ref[None])))
+
+
+def run_moe_exl3(args, torch, dev, tokens=None, built=None):
+    """The reference's GLM-5.3 MoE layer (native/glm53/glm_engine.vyb:2728-2990) in one call: H=4096,
+    288 EXL3 4-bpw routed experts + 1 bf16 shared expert, top-8 with the selection bias, I=2048, T tokens
+    bf16. T <= 16: R layer calls per step on distinct inputs, each with its own shared expert."""
+    H, I, E, k = MOE53["H"], MOE53["I"], MOE53["E"], MOE53["k"]
+    T = tokens or args.tokens
+    R = 8 if T == 1 else (2 if T <= 16 else 1)
+    layers, gen = built or build_moe_exl3(torch, dev, args.seed + 9, n_shared=R)
+    xs = [torch.randn(T, H, generator=gen, device=dev).to(torch.bfloat16) for _ in range(R)]
+    lgs = [torch.randn(T, E, generator=gen, device=dev) for _ in range(R)]
+    outs = [torch.empty(T, H, device=dev) for _ in range(R)]
+    routed = [layers[r](xs[r], lgs[r], routing=True) for r in range(R)]
+    distinct = [int(torch.unique(rt[1]).numel()) for rt in routed]
+    ms, wall = timed_graph(torch, [lambda r=r: layers[r](xs[r], lgs[r], out=outs[r]) for r in range(R)], args.steps,
+                           args.warmup)
+    per_expert = 3 * H * I // 2 + 3 * 2 * (H + I)   # trellis (4 bits per weight) + suh / svh
+    shared = 3 * H * I * 2
+    nbytes = sum(d * per_expert + shared + T * H * 2 + T * E * 4 + T * H * 4 for d in distinct)
+    flops = R * T * (k + 1) * 3 * 2 * I * H
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    check = None
+    if not args.no_check:
+        r = R - 1
+        if not torch.equal(outs[r], routed[r][0]):
+            raise CheckFailed(f"moe_exl3 T={T}: graph replay output differs from the eager call")
+        rel = check_moe_exl3(torch, layers[r], xs[r], lgs[r], outs[r], routed[r][1], routed[r][2])
+        check = dict(ok=True, rel=rel, what="routing of every token; the last token x 256 columns vs float64 "
+                                            "oracle; graph replay == eager")
+    gemm = "k_mx_gemm<1>" if T == 1 else ("k_mx_gemm<2>" if T * k <= 2 * min(E, T * k) else "k_mx_gemm<16>")
+    roofline = hbm_roofline(gbs, f"EXL3 MoE layer: route+bucket, x rotation, {gemm} gate|up and down (trellis "
+                                 "decoded in registers), SwiGLU between rotations, bf16 shared expert, combine",
+                            "algorithmic bytes (hit experts' trellis + scales, shared expert, activations) / "
+                            "event time", avg_layer_us=round(ms * 1e3 / R, 3), bytes_per_layer=nbytes // R)
+    return dict(value=gbs, unit="GB/s", ms_step=ms, wall=wall, roofline=roofline, flops=flops,
+                tflops=round(flops / (ms * 1e-3) / 1e12, 3),
+                workload=f"GLM-5.3 MoE layer T={T}: H=4096, 288 EXL3 4-bpw experts + 1 bf16 shared expert, top-8 "
+                         f"with selection bias, I=2048; {R} layer call(s) per step on distinct inputs, each with its "
+                         f"own shared expert ({sum(distinct) / R:.1f} routed experts hit per call)",
                 bytes_per_step=nbytes, launches_per_step=R, check=check)
 
 
@@ -830,6 +941,11 @@ def run_all(args, torch, dev):
         leg(f"cfg5_moe_T{T}", run_moe, tokens=T, built=built)
     del built
     torch.cuda.empty_cache()
+    built = build_moe_exl3(torch, dev, args.seed + 9, n_shared=8)
+    for T in (1, 16, 256):
+        leg(f"glm53_moe_exl3_T{T}", run_moe_exl3, tokens=T, built=built)
+    del built
+    torch.cuda.empty_cache()
     return recs
 
 
@@ -846,6 +962,7 @@ def main():
     dev = torch.device("cuda:0")
     runners = dict(gemv1=run_gemv1, kquant=run_kquant, producers=run_producers, router=run_router, exl3=run_exl3,
                    prefill=run_prefill, prefill_i8=run_prefill_i8, prefill_kq=run_prefill_kq, moe=run_moe,
+                   moe_exl3=run_moe_exl3,
                    pblock=run_pblock, copy=run_copy)
     configs = None
     try:

@@ -416,8 +416,10 @@ int64_t vybdq_moe_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int
    shared expert (s_gate/s_up/s_down, or all 0) is one such matrix each. x [T, H] (f32/f16/bf16,
    16-byte aligned), logits [T, E]. Tokens are bucketed per expert on the device and each
    expert's rows run through grouped dequant GEMMs; no host synchronisation. idx_out/w_out
-   (optional) receive the routing. Replaces the reference's per-expert host loop
-   (native/glm53/glm_engine.vyb:2720-2953) and moe_route/moe_act/moe_down (moe.vyb:1-170). */
+   (optional) receive the routing. Replaces the reference's moe_route/moe_act/moe_down
+   (moe.vyb:1-170) for GGUF-quantized experts, with the bucketing and per-expert FFN structure of
+   its host loop (native/glm53/glm_engine.vyb:2804-2953); that loop's own weights (EXL3 routed
+   experts, a bf16 shared expert) go through vybdq_moe_forward_exl3. */
 int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logits, int logits_dt, uint64_t bias,
                       uint64_t w_gate, uint64_t w_up, uint64_t w_down, uint64_t s_gate, uint64_t s_up,
                       uint64_t s_down, uint64_t out, int out_dt, uint64_t idx_out, uint64_t w_out, int64_t T,

@@ -31,12 +31,25 @@ def _bf16(rng, shape, scale=0.02):
     return t, t.to(torch.float64).numpy()
 
 
+# suh / svh of the routed experts ~ +-|N(0, SCALE)|: W = diag(suh) Hs What Hs diag(svh) then has
+# entries of about N(0, 0.02) like a real checkpoint's (and like the bf16 shared expert here), so
+# the routed experts weigh in the outputs as much as the shared expert does
+SCALE = 0.12
+
+
+def _scales(rng, K, N):
+    sgn = lambda n: rng.integers(0, 2, n) * 2 - 1
+    suh = (np.abs(rng.standard_normal(K) * SCALE) * sgn(K)).astype(np.float16)
+    svh = (np.abs(rng.standard_normal(N) * SCALE) * sgn(N)).astype(np.float16)
+    return suh, svh
+
+
 def _expert_tensors(rng, H, I):
     """The 9 host arrays of one EXL3 expert in the table order of ops.EXL3_EXPERT_FIELDS."""
     out = []
     for K, N in ((H, I), (H, I), (I, H)):
-        t, suh, svh = synth.exl3_tensors(rng, K, N)
-        out += [t, suh, svh]
+        t, _, _ = synth.exl3_tensors(rng, K, N)
+        out += [t, *_scales(rng, K, N)]
     return out
 
 
@@ -83,7 +96,11 @@ def test_moe_exl3_small(dev, T, xdt, with_shared, with_bias):
                                     bias=bias)
     np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
     assert np.abs(w.cpu().numpy() - rw).max() < 1e-6
-    assert matmul.rel_maxnorm(y.cpu().numpy(), ref) < TOL
+    y = y.cpu().numpy()
+    assert matmul.rel_maxnorm(y, ref) < TOL
+    if with_shared:  # the routed experts' part alone, so that the shared expert cannot mask it
+        sh_ref = moe.ffn_rows(x.to(torch.float64).numpy(), *sh64)
+        assert matmul.rel_maxnorm(y - sh_ref, ref - sh_ref) < TOL
 
 
 def test_moe_exl3_out_dtypes_and_f16_x(dev):
@@ -175,13 +192,6 @@ def glm_layer(dev):
     return layer, whats, scales, tuple(v for _, v in sh), bias
 
 
-def _scales(rng, K, N):
-    sgn = lambda n: rng.integers(0, 2, n) * 2 - 1
-    suh = (np.abs(rng.standard_normal(K) * 0.01) * sgn(K)).astype(np.float16)
-    svh = (np.abs(rng.standard_normal(N) * 0.01) * sgn(N)).astype(np.float16)
-    return suh, svh
-
-
 def _apply(x, what, suh, svh):
     return exl3.fwht128_rows(exl3.fwht128_rows(x * suh) @ what) * svh
 
@@ -201,11 +211,13 @@ def test_moe_exl3_glm53_shapes(dev, glm_layer, T):
     x64 = x.to(torch.float64).numpy()
     y = y.cpu().numpy()
     for t in sorted({0, T - 1}):
-        ref = moe.ffn_rows(x64[t:t + 1], *sh64)[0]
+        sh_ref = moe.ffn_rows(x64[t:t + 1], *sh64)[0]
+        routed = np.zeros(H)
         for s in range(k):
             e = int(ridx[t, s])
             (sg, vg), (su, vu), (sd, vd) = scales[e]
             g = _apply(x64[t:t + 1], whats[0][e % POOL], sg, vg)
             u = _apply(x64[t:t + 1], whats[1][e % POOL], su, vu)
-            ref = ref + rw[t, s] * _apply(moe.swiglu(g, u), whats[2][e % POOL], sd, vd)[0]
-        assert matmul.rel_maxnorm(y[t], ref) < TOL, (T, t)
+            routed += rw[t, s] * _apply(moe.swiglu(g, u), whats[2][e % POOL], sd, vd)[0]
+        assert matmul.rel_maxnorm(y[t], sh_ref + routed) < TOL, (T, t)
+        assert matmul.rel_maxnorm(y[t] - sh_ref, routed) < TOL, (T, t, "routed part")
