@@ -137,3 +137,78 @@ def test_chain_activation_range(dev, kind):
     ref = matmul.gemv_q4_0_f64(raw, x.cpu().numpy().astype(np.float64), N, K)[0]
     assert np.all(np.isfinite(y.cpu().numpy()))
     assert matmul.rel_maxnorm(y.cpu().numpy(), ref) < matmul.TOL
+
+
+@pytest.mark.parametrize("ty", [ops.GGML_Q4_K, ops.GGML_Q5_K, ops.GGML_Q6_K, ops.GGML_IQ2_S])
+def test_chain_superblock_types(dev, ty):
+    """Two dependent stages of a super-block type (the second reads the first's fp16 output)."""
+    from tests.test_gpu_kquant import matrix_ref
+    rng = np.random.default_rng(15 + ty)
+    K0, N0, N1 = 2560, 1024, 768
+    raw0, raw1 = synth.kquant_weights(rng, ty, N0, K0), synth.kquant_weights(rng, ty, N1, N0)
+    x = torch.from_numpy(synth.activations(rng, (K0,))).to(torch.float16).to(dev)
+    Y0 = torch.empty(N0, dtype=torch.float16, device=dev)
+    Y1 = torch.empty(N1, dtype=torch.float32, device=dev)
+    ch = ops.GemvChain(ty, [ops.pblock(x, K0, [(dev_bytes(raw0, dev), Y0, N0)]),
+                            ops.pblock(Y0, N0, [(dev_bytes(raw1, dev), Y1, N1)])], dev)
+    ch()
+    assert ch.status() == 0, _lib.last_error()
+    ref0 = matrix_ref(ty, raw0, N0, K0) @ x.to(torch.float64).cpu().numpy()
+    assert gate16(Y0.to(torch.float64).cpu().numpy(), ref0) < TOL
+    ref1 = matrix_ref(ty, raw1, N1, N0) @ Y0.to(torch.float64).cpu().numpy()
+    assert matmul.rel_maxnorm(Y1.cpu().numpy(), ref1) < TOL
+
+
+def test_chain_decode_stack_shapes(dev):
+    """Two layers of the decode stack's stages (q|k|v, o, gate|up, down; fp16 x and y) as the
+    benchmark runs them, each stage on its own N(0, 1) input (chained raw q4_0 GEMVs grow past the
+    fp16 range: the weights' -8 d sum(x) term compounds; stage-to-stage data flow is tested above):
+    lane groups of 16 (q|k|v), 32 (o, down) and 4 (gate|up, 19456 rows: 16 rows per tile)."""
+    H, Q, KV, I = 2560, 4096, 1024, 9728
+    rng = np.random.default_rng(16)
+    f16 = torch.float16
+    xin = lambda k: torch.from_numpy(synth.activations(rng, (k,))).to(f16).to(dev)
+    shapes = dict(q=(Q, H), k=(KV, H), v=(KV, H), o=(H, Q), gate=(I, H), up=(I, H), down=(H, I))  # (rows, K)
+    pbs, checks = [], []
+    for _ in range(2):
+        W = {n: synth.q4_0_weights(rng, r, k) for n, (r, k) in shapes.items()}
+        Wd = {n: dev_bytes(a, dev) for n, a in W.items()}
+        y = {n: torch.empty(r, dtype=f16, device=dev) for n, (r, _) in shapes.items()}
+        xs = dict(attn=xin(H), o=xin(Q), mlp=xin(H), down=xin(I))
+        pbs.append(ops.pblock(xs["attn"], H, [(Wd["q"], y["q"], Q), (Wd["k"], y["k"], KV), (Wd["v"], y["v"], KV)]))
+        pbs.append(ops.pblock(xs["o"], Q, [(Wd["o"], y["o"], H)]))
+        pbs.append(ops.pblock(xs["mlp"], H, [(Wd["gate"], y["gate"], I), (Wd["up"], y["up"], I)]))
+        pbs.append(ops.pblock(xs["down"], I, [(Wd["down"], y["down"], H)]))
+        checks.append((W, y, xs))
+    ch = ops.GemvChain(ops.GGML_Q4_0, pbs, dev)
+    ch()
+    assert ch.status() == 0, _lib.last_error()
+    for W, y, xs in checks:
+        x64 = lambda t: t.to(torch.float64).cpu().numpy()
+        for n, src in (("q", xs["attn"]), ("k", xs["attn"]), ("v", xs["attn"]), ("o", xs["o"]), ("gate", xs["mlp"]),
+                       ("up", xs["mlp"]), ("down", xs["down"])):
+            r, k = shapes[n]
+            ref = matmul.gemv_q4_0_f64(W[n], x64(src), r, k)[0]
+            assert gate16(x64(y[n]), ref) < TOL, n
+    assert int(ch.ws.abs().sum()) == 0
+
+
+def test_chain_stage_larger_than_the_held_registers(dev):
+    """30000 rows of K = 4096: more tiles than row-owning waves (a second round of tiles) and more
+    units per lane than the registers hold (the rest streamed after the wait); then a dependent
+    stage reading the first 16384 of its outputs."""
+    rng = np.random.default_rng(17)
+    N0, K0, N1, K1 = 30000, 4096, 256, 16384
+    raw0 = synth.q4_0_weights(rng, N0, K0)
+    raw1 = synth.q4_0_weights(rng, N1, K1)
+    x = torch.from_numpy(synth.activations(rng, (K0,))).to(dev)
+    Y0 = torch.empty(N0, dtype=torch.float32, device=dev)
+    Y1 = torch.empty(N1, dtype=torch.float32, device=dev)
+    ch = ops.GemvChain(ops.GGML_Q4_0, [ops.pblock(x, K0, [(dev_bytes(raw0, dev), Y0, N0)]),
+                                       ops.pblock(Y0, K1, [(dev_bytes(raw1, dev), Y1, N1)])], dev)
+    ch()
+    assert ch.status() == 0, _lib.last_error()
+    ref0 = matmul.gemv_q4_0_f64(raw0, x.to(torch.float64).cpu().numpy(), N0, K0)[0]
+    assert matmul.rel_maxnorm(Y0.cpu().numpy(), ref0) < TOL
+    ref1 = matmul.gemv_q4_0_f64(raw1, Y0.to(torch.float64).cpu().numpy()[:K1], N1, K1)[0]
+    assert matmul.rel_maxnorm(Y1.cpu().numpy(), ref1) < TOL

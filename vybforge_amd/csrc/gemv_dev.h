@@ -100,10 +100,10 @@ __device__ __forceinline__ float dpp_add(float v) {
 // broadcasts then fold rows together. The group total is in the group's last lane (G - 1).
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
-  static_assert(G == 8 || G == 16 || G == 32 || G == 64, "group size");
+  static_assert(G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group size");
   v = dpp_add<DPP_QUAD_XOR1>(v);
   v = dpp_add<DPP_QUAD_XOR2>(v);
-  v = dpp_add<DPP_HALF_MIRROR>(v);
+  if constexpr (G >= 8) v = dpp_add<DPP_HALF_MIRROR>(v);
   if constexpr (G >= 16) v = dpp_add<DPP_ROW_MIRROR>(v);
   if constexpr (G >= 32) v = dpp_add<DPP_BCAST15, 0xA>(v);  // rows 1, 3 += rows 0, 2
   if constexpr (G >= 64) v = dpp_add<DPP_BCAST31, 0x8>(v);  // row 3 += rows 0 + 1

@@ -23,8 +23,7 @@
 namespace vybdq {
 
 // defined in chain.hip / kqgemm.hip
-int chain_dispatch(int wtype, uint64_t P, int nstages, int64_t pstride, int64_t maxK, uint64_t ws, int ref_layout,
-                   int max_per_cu, hipStream_t s);
+int pb_gemv_dispatch(int wtype, uint64_t P, int64_t maxK, uint32_t *status, hipStream_t s);
 int kq_gemm_pblock(int wtype, int xdt, const int64_t *pb, uint32_t *status, hipStream_t s);
 // pblock_moe.hip / pblock_exl3.hip
 int pb_moe_launch(const int64_t *pb, uint32_t *status, hipStream_t s);
@@ -153,7 +152,7 @@ extern "C" int vybdq_launch_pblock(int kind, uint64_t P, uint64_t stream) {
   const int rc = pb_status_address(st);
   if (rc) return rc;
   hipStream_t s = as_stream(stream);
-  if (op == VYBDQ_PB_GEMV) return chain_dispatch(ty, P, 1, 256, kPbMaxK, st, 1, 8, s);
+  if (op == VYBDQ_PB_GEMV) return pb_gemv_dispatch(ty, P, kPbMaxK, reinterpret_cast<uint32_t *>(st), s);
   const int xdt = op == VYBDQ_PB_GEMM ? VYBDQ_F32 : VYBDQ_F16;
   const auto *pb = reinterpret_cast<const int64_t *>(P);
   auto *status = reinterpret_cast<uint32_t *>(st);
