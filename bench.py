@@ -248,44 +248,168 @@ def run_stack(args, torch, dev):
                 bytes_per_step=bytes_tok, launches_per_step=n_launch, check=check)
 
 
-def cpu_baseline_stack(target_s=10.0, target_all_s=6.0):
-    """numpy oracle path on a bounded sample: q4_0 -> f32 decode, then BLAS matvec. The reported
-    value is one thread; the same sample is also timed with BLAS on every host core."""
-    import numpy as np
-    from threadpoolctl import threadpool_info, threadpool_limits
+# ---- CPU baselines: the repo's numpy path (oracle decode + BLAS) on the host's cores ----------------
+
+CPU_RUNS = 5  # timed runs per leg after one warm-up; the median is reported
+
+
+def _cpu_share():
+    """Host threads for the all-cores leg: the affinity mask, capped at the 16-thread share of one
+    GPU on a shared host."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return max(1, min(n, 16))
+
+
+def _cpu_leg(fn, threads):
+    """Median wall time of CPU_RUNS calls of fn(threads) after one warm-up; BLAS limited to 1 thread
+    per caller thread (the all-cores legs split the work over `threads` host threads themselves)."""
+    import statistics
+    from threadpoolctl import threadpool_limits
+    with threadpool_limits(limits=1):
+        fn(threads)
+        ts = []
+        for _ in range(CPU_RUNS):
+            t0 = time.perf_counter()
+            fn(threads)
+            ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def _split(n, parts):
+    step = (n + parts - 1) // parts
+    return [(a, min(a + step, n)) for a in range(0, n, step)]
+
+
+def _par(fn, ranges, threads):
+    """fn over row ranges on `threads` host threads (numpy releases the GIL in its vector loops)."""
+    import concurrent.futures as cf
+    if threads == 1:
+        return [fn(r) for r in ranges]
+    with cf.ThreadPoolExecutor(threads) as ex:
+        return list(ex.map(fn, ranges))
+
+
+def _q4_gemv_rows(raw, N, K, x):
+    """The float32 numpy path of one q4_0 GEMV, as a function of a row range."""
     from oracle import formats
+    rb = K // 32 * 18
+    rows = raw.reshape(N, rb)
+
+    def part(r):
+        w = formats.dequant_q4_0(rows[r[0]:r[1]].reshape(-1)).reshape(r[1] - r[0], K)
+        return w @ x
+    return part
+
+
+def cpu_baselines():
+    """Each configuration's workload (or a bounded sample of it) through this repo's numpy path: the
+    oracle's vectorised decode to float32, then numpy matmul (BLAS), 1 thread and the host's thread
+    share; the median of CPU_RUNS runs each. Returns {config: record}, records in the units of the GPU
+    figures with the same algorithmic bytes / flops."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+    from oracle import exl3, formats, kquants, matmul, moe
     from vybforge_amd import synth
-    shapes, _, _, _ = stack_bytes()
+    ncpu = _cpu_share()
     rng = np.random.default_rng(1)
+    out = {}
+
+    def record(value_fn, unit, sample, run, gate=None):
+        t1 = _cpu_leg(run, 1)
+        tn = _cpu_leg(run, ncpu)
+        rec = dict(value=round(value_fn(t1), 4), unit=unit, cores=1, kind="port", sample=sample,
+                   median_of=CPU_RUNS, value_all_cores=round(value_fn(tn), 4), cores_all=ncpu)
+        if gate is not None:
+            tg = _cpu_leg(gate, 1)
+            rec["value_fp64_gate"] = round(value_fn(tg), 4)
+        return rec
+
+    # the decode stack: one layer's 7 GEMVs (fp16 activations computed in float32)
+    shapes, _, _, _ = stack_bytes()
     mats = [(synth.q4_0_weights(rng, n, k), n, k) for n, k in shapes]
-    xs = {k: rng.standard_normal(k).astype(np.float16) for _, k in shapes}
+    xs = {k: rng.standard_normal(k).astype(np.float16).astype(np.float32) for _, k in shapes}
     layer_bytes = sum(raw.size + 2 * k + 2 * n for raw, n, k in mats)
+    parts = [(_q4_gemv_rows(raw, n, k, xs[k]), n) for raw, n, k in mats]
 
-    def run(limit, seconds):
-        done = 0
-        t0 = time.perf_counter()
-        with threadpool_limits(limits=limit):
-            while True:
-                for raw, n, k in mats:
-                    w = formats.dequant_q4_0(raw).reshape(n, k)
-                    y = w @ xs[k].astype(np.float32)
-                    y.astype(np.float16)
-                done += 1
-                el = time.perf_counter() - t0
-                if el >= seconds:
-                    return done, el
+    def stack_run(threads):
+        for f, n in parts:
+            np.concatenate(_par(f, _split(n, threads), threads))
 
-    done, el = run(1, target_s)
-    ncpu = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    done_all, el_all = run(ncpu, target_all_s)
+    def stack_gate(_):
+        for raw, n, k in mats:
+            matmul.gemv_q4_0_f64(raw, xs[k], n, k)
+    out["stack"] = record(lambda t: layer_bytes / t / 1e9, "GB/s",
+                          "one layer of the 36-layer q4_0 stack (7 GEMVs, 56.8 MB packed) per run",
+                          stack_run, stack_gate)
+
+    # config 1: q4_0 GEMV 9728 x 2560, f32 x
+    N, K = 9728, 2560
+    raw1 = synth.q4_0_weights(rng, N, K)
+    x1 = rng.standard_normal(K).astype(np.float32)
+    f1 = _q4_gemv_rows(raw1, N, K, x1)
+    b1 = raw1.size + 4 * K + 4 * N
+    out["cfg1_q4_0_gemv_9728x2560"] = record(
+        lambda t: b1 / t / 1e9, "GB/s", "the whole GEMV per run",
+        lambda th: np.concatenate(_par(f1, _split(N, th), th)),
+        lambda _: matmul.gemv_q4_0_f64(raw1, x1, N, K))
+
+    # config 3: Q8_0 prefill M = 512, both projections on a 512-column slice of the output
+    M, cols = 512, 512
+    pre = []
+    for N, K in PREFILL_SHAPES:
+        raw = synth.q8_0_weights(rng, cols, K)
+        pre.append((raw, K, rng.standard_normal((M, K)).astype(np.float32)))
+    pflops = sum(2 * M * cols * K for _, K, _ in pre)
+
+    def prefill_run(threads):
+        for raw, K, x in pre:
+            rows = raw.reshape(cols, K // 32 * 34)
+            ws = _par(lambda r: formats.dequant_q8_0(rows[r[0]:r[1]].reshape(-1)).reshape(r[1] - r[0], K),
+                      _split(cols, threads), threads)
+            w = np.concatenate(ws)
+            _par(lambda r: x[r[0]:r[1]] @ w.T, _split(M, threads), threads)
+    out["cfg3_q8_0_prefill_m512"] = record(
+        lambda t: pflops / t / 1e12, "TFLOP/s",
+        "M=512, 5120->17408 and 17408->5120 on 512 output columns each (1.93 GFLOP per run)", prefill_run,
+        lambda _: [matmul.gemm_rows_f64(x, matmul.q8_0_matrix(raw, cols, K)) for raw, K, x in pre])
+
+    # config 4: EXL3 K=5120, batch 1 and 16, on a 1024-column slice (the oracle's float64 dequant)
+    K, ncol = 5120, 1024
+    t4, suh, svh = synth.exl3_tensors(rng, K, ncol)
+    for B in (1, 16):
+        x4 = rng.standard_normal((B, K)).astype(np.float32)
+        b4 = t4.size * 2 + 2 * K + 2 * ncol + B * (2 * K + 4 * ncol)
+
+        def exl3_run(threads, x4=x4):
+            w = np.concatenate(_par(lambda r: exl3.dequant_exl3_f64(t4[:, r[0] // 16:r[1] // 16], suh,
+                                                                     svh[r[0]:r[1]]).astype(np.float32),
+                                    [(128 * a, 128 * b) for a, b in _split(ncol // 128, threads)], threads), axis=1)
+            return x4 @ w
+        out[f"cfg4_exl3_b{B}"] = record(lambda t: b4 / t / 1e9, "GB/s",
+                                        f"K=5120 x 1024 columns of the 17408, batch {B}", exl3_run)
+
+    # config 5: GLM-5 MoE, one routed expert's FFN (3 q4_0 matrices 6144 x 2048) on 2 tokens per run
+    H, I = MOE["H"], MOE["I"]
+    ex = [synth.q4_0_weights(rng, I, H), synth.q4_0_weights(rng, I, H), synth.q4_0_weights(rng, H, I)]
+    x5 = rng.standard_normal((2, H)).astype(np.float32)
+    b5 = sum(a.size for a in ex) + 2 * 2 * H + 4 * 2 * H
+
+    def moe_run(threads):
+        dq = lambda raw, n, k: np.concatenate(_par(
+            lambda r: formats.dequant_q4_0(raw.reshape(n, k // 32 * 18)[r[0]:r[1]].reshape(-1)).reshape(r[1] - r[0], k),
+            _split(n, threads), threads))
+        wg, wu, wd = dq(ex[0], I, H), dq(ex[1], I, H), dq(ex[2], H, I)
+        return moe.swiglu(x5 @ wg.T, x5 @ wu.T) @ wd.T
+    out["cfg5_moe"] = record(lambda t: b5 / t / 1e9, "GB/s",
+                             "one routed expert's FFN (21.2 MB of q4_0) on 2 tokens per run", moe_run)
+
     blas = ", ".join(f"{i.get('internal_api')} {i.get('version')}" for i in threadpool_info()
                      if i.get("user_api") == "blas") or "unknown"
-    return dict(value=round(layer_bytes * done / el / 1e9, 3), unit="GB/s", cores=1, kind="port",
-                sample=f"{done} layers of the 36-layer stack (7 GEMVs each, 56.8 MB packed), "
-                       "numpy f32 decode + BLAS matvec, 1 thread",
-                value_all_cores=round(layer_bytes * done_all / el_all / 1e9, 3), cores_all=ncpu,
-                host=dict(cpu_count=os.cpu_count(), affinity=ncpu, blas=blas,
-                          omp_num_threads=os.environ.get("OMP_NUM_THREADS")))
+    host = dict(cpu_count=os.cpu_count(), affinity=len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity")
+                else None, threads_all_cores=ncpu, blas=blas, omp_num_threads=os.environ.get("OMP_NUM_THREADS"))
+    for r in out.values():
+        r["host"] = host
+    return out
 
 
 # ---- config 1: one q4_0 GEMV ----------------------------------------------------------------
@@ -979,8 +1103,15 @@ def main():
         sys.exit(3)
     cpu = None
     if not args.no_cpu and args.config in ("all", "stack", "stack_chain"):
-        log("cpu baseline ...")
-        cpu = cpu_baseline_stack()
+        log("cpu baselines ...")
+        t0 = time.perf_counter()
+        cpus = cpu_baselines()
+        log(f"cpu baselines: {time.perf_counter() - t0:.1f} s")
+        cpu = cpus["stack"]
+        for name, rec in (configs or {}).items():
+            key = max((k for k in cpus if name == k or name.startswith(k + "_")), key=len, default=None)
+            if key is not None:
+                rec["cpu_baseline"] = cpus[key]
     line = dict(
         metric=METRIC, value=round(r["value"], 2), unit=r.get("unit", "GB/s"), n_gpus=1, steps=args.steps,
         warmup=args.warmup, ms_per_step=round(r["ms_step"], 4), higher_is_better=True,

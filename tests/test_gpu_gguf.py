@@ -151,6 +151,31 @@ def test_gemv_seg3_qkv(dev):
         assert gate(y.to(torch.float64).cpu().numpy(), ref, torch.float16) < TOL
 
 
+@pytest.mark.parametrize("N,K", [(2560, 4096), (2560, 9728)])
+def test_gemv_decode_stack_fp16_launches(dev, N, K):
+    """The decode stack's fp16-x / fp16-y launches of o (4096 -> 2560) and down (9728 -> 2560), the
+    instantiations the benchmark replays, against the float64 oracle on every row."""
+    rng = np.random.default_rng(N + K)
+    raw = synth.q4_0_weights(rng, N, K)
+    xd, x64 = x_as(synth.activations(rng, (K,)), "f16", dev)
+    y = ops.gemv(ops.GGML_Q4_0, to_dev(raw, dev), xd, N, K, y_dtype=torch.float16)
+    ref = matmul.gemv_q4_0_f64(raw, x64, N, K)[0]
+    assert gate(y.to(torch.float64).cpu().numpy(), ref, torch.float16) < TOL
+
+
+def test_gemv_decode_stack_gate_up_launch(dev):
+    """The decode stack's gate|up launch: two 9728-row segments sharing one fp16 x of 2560."""
+    K, I = 2560, 9728
+    rng = np.random.default_rng(77)
+    raws = [synth.q4_0_weights(rng, I, K) for _ in range(2)]
+    xd, x64 = x_as(synth.activations(rng, (K,)), "f16", dev)
+    ys = [torch.empty(I, dtype=torch.float16, device=dev) for _ in range(2)]
+    ops.gemv_q4_0_seg3(xd, K, [(to_dev(r, dev), y, I) for r, y in zip(raws, ys)])
+    for r, y in zip(raws, ys):
+        ref = matmul.gemv_q4_0_f64(r, x64, I, K)[0]
+        assert gate(y.to(torch.float64).cpu().numpy(), ref, torch.float16) < TOL
+
+
 @pytest.mark.parametrize("plan", ["8,5,256", "8,1,64", "16,3,128", "16,2,256", "32,2,128", "32,5,64",
                                   "64,3,256", "64,1,128"])
 @pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
