@@ -136,6 +136,29 @@ int vybdq_gemv_seg3(int wtype, uint64_t X, int64_t M, int64_t K, int x_dt,
                     uint64_t W2, uint64_t Y2, int64_t N2, int y_dt2, uint64_t RS2,
                     uint64_t W3, uint64_t Y3, int64_t N3, int y_dt3, uint64_t RS3, uint64_t stream);
 
+/* Decode GEMV on an xq8 activation row: Y[n] = RS[n] + sum_k W[n, k] * x'[k] with
+   x'[k] = Xs[k / 32] * Xq[k] (Xq int8 [K], Xs float32 [K/32]: the layout vybdq_quant_q8_act,
+   vybdq_rmsnorm_q8 and vybdq_swiglu_q8 write; the reference keeps both in one buffer, Xs = Xq + K).
+   wtype 12 (Q4_K), 13 (Q5_K) or 22 (IQ2_S). Every 32-weight sub-block product is an exact integer
+   dot product, scaled and accumulated in float32: the result matches the float64 GEMV of x' to
+   float32 rounding, and differs from the exact entry points (vybdq_gemv on x) by the activation
+   quantization, which the reference accepts on its default decode path (doc/RIDGE-27B.md:75-84).
+   K % 256 == 0, K <= 65536; Xq 16-byte and Xs 4-byte aligned; W 4-byte aligned; y_dt F32, F16,
+   BF16 or F64, RS of the same type or 0. Replaces gemv_iq2s_q (p-block W@0 X@8 Y@16 N@32 K@40
+   YE@48 RS@120 G@128, native/kernels/rgemv7.vyb:3-96), gemv_q4k_q / gemv_q4k_qu
+   (native/kernels/rq4kq.vyb:7-89,93-274) and gemv_q5k_q / gemv_q5k_qu
+   (native/kernels/rq5kq.vyb:8-80,82-268); the IQ2_S grid is built in. */
+int vybdq_gemv_xq8(int wtype, uint64_t W, uint64_t Xq, uint64_t Xs, uint64_t Y, int64_t N, int64_t K,
+                   int y_dt, uint64_t RS, uint64_t stream);
+
+/* vybdq_gemv_xq8 over up to three matrices sharing the xq8 row (segments as vybdq_gemv_seg3),
+   one launch: the multi-segment block of gemv_q4k_q / gemv_q5k_q (W2/NS2/Y2/YE2 @56-80,
+   W3/NS3/Y3/YE3 @88-112, native/kernels/rq4kq.vyb:18-33). */
+int vybdq_gemv_xq8_seg3(int wtype, uint64_t Xq, uint64_t Xs, int64_t K,
+                        uint64_t W, uint64_t Y, int64_t N, int y_dt, uint64_t RS,
+                        uint64_t W2, uint64_t Y2, int64_t N2, int y_dt2, uint64_t RS2,
+                        uint64_t W3, uint64_t Y3, int64_t N3, int y_dt3, uint64_t RS3, uint64_t stream);
+
 /* Router logits Y [T, E] = X [T, H] W^T with W [E, H] (w_dt F32, F16 or BF16; the checkpoint's
    router weight is bf16), X of x_dt (F32, F16, BF16 or F64), accumulated in float64 (every
    product exact; fixed lane-strided order); y_dt F64 or F32. vybdq_moe_route / vybdq_moe_forward

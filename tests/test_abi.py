@@ -55,6 +55,25 @@ def test_gemv_preconditions(args, code, text):
     assert text in _lib.last_error()
 
 
+@pytest.mark.parametrize("args,code,text", [
+    # (wtype, W, Xq, Xs, Y, N, K, y_dt, RS, stream)
+    ((14, 4, 16, 4, 4, 16, 256, 0, 0, 0), -1, "wtype must be"),     # Q6_K has no xq8 GEMV
+    ((12, 4, 16, 4, 4, 16, 320, 0, 0, 0), -2, "K must be"),         # K % 256 != 0
+    ((12, 4, 16, 4, 4, 16, 65792, 0, 0, 0), -2, "at most 65536"),
+    ((22, 4, 8, 4, 4, 16, 256, 0, 0, 0), -3, "Xq must be"),         # Xq not 16-byte aligned
+    ((22, 4, 16, 2, 4, 16, 256, 0, 0, 0), -3, "Xs must be"),        # Xs not 4-byte aligned
+    ((13, 2, 16, 4, 4, 16, 256, 0, 0, 0), -3, "W must be"),         # W not 4-byte aligned
+    ((13, 0, 16, 4, 4, 16, 256, 0, 0, 0), -1, "null W"),
+    ((13, 4, 16, 4, 4, 0, 256, 0, 0, 0), -2, "N must be"),
+    ((13, 4, 16, 4, 4, 16, 256, 9, 0, 0), -1, "y_dt"),
+])
+def test_gemv_xq8_preconditions(args, code, text):
+    from vybforge_amd import _lib
+    rc = _lib.lib.vybdq_gemv_xq8(*args)
+    assert rc == code
+    assert text in _lib.last_error()
+
+
 def test_dequant_preconditions():
     from vybforge_amd import _lib
     assert _lib.lib.vybdq_dequant_q4_0(0, 1, 1, 0, 0, 0) == _lib.ERR_ARG

@@ -411,3 +411,40 @@ def test_moe_fixture_route_empty_round_takes_expert_zero():
     bias[[5, 9]] = 0.0
     idx, _ = moe.fixture_route(lg, bias)
     assert idx[0, :2].tolist() == [5, 9] and (idx[0, 2:] == 0).all()
+
+
+# ---- the xq8-activation decode GEMV gate ------------------------------------------------
+
+@pytest.mark.parametrize("ty", [12, 13, 22])
+def test_xq8_gemv_gate_equals_factored_integer_form(ty):
+    # the gate (decoded rows @ x' in float64) against the reference kernels' factored arithmetic
+    # (integer sub-block dots from the packed bytes, scale / min fields in their dword form): a
+    # dropped min term, a wrong nibble half or scale field, or a sign applied to the wrong group
+    # fails here
+    from vybforge_amd import synth
+    rng = np.random.default_rng(ty)
+    N, K = 24, 768
+    raw = synth.kquant_weights(rng, ty, N, K)
+    xq, xd = formats.quant_q8_act(rng.standard_normal(K).astype(np.float32) * 3)
+    a = matmul.gemv_xq8_f64(ty, raw, xq, xd, N, K)
+    b = matmul.gemv_xq8_factored_f64(ty, raw, xq, xd, N, K)
+    assert matmul.rel_maxnorm(a, b) < 1e-13
+
+
+@pytest.mark.parametrize("ty", [12, 13, 22])
+def test_xq8_gemv_gate_reduces_to_the_exact_gemv(ty):
+    # x = q / 8 with every block's largest |q| = 127 quantizes without loss (d = 1/8, xq = q), so the
+    # gate equals the exact-activation GEMV of the decoded rows
+    from oracle import iquants, kquants
+    from vybforge_amd import synth
+    rng = np.random.default_rng(40 + ty)
+    N, K = 16, 512
+    raw = synth.kquant_weights(rng, ty, N, K)
+    q = rng.integers(-127, 128, K)
+    q.reshape(-1, 32)[:, 5] = 127
+    x = (q / 8.0).astype(np.float32)
+    xq, xd = formats.quant_q8_act(x)
+    assert np.array_equal(xq, q) and np.all(xd == np.float32(0.125))
+    w = iquants.matrix_iq2_s(raw, N, K) if ty == 22 else kquants.matrix(ty, raw, N, K)
+    exact = w @ x.astype(np.float64)
+    assert matmul.rel_maxnorm(matmul.gemv_xq8_f64(ty, raw, xq, xd, N, K), exact) < 1e-14

@@ -42,6 +42,11 @@ SIGNATURES = {
                         _u64, _u64, _i64, _int, _u64,
                         _u64, _u64, _i64, _int, _u64, _u64],
     "vybdq_quant_q8_act": [_u64, _u64, _u64, _i64, _i64, _int, _u64],
+    "vybdq_gemv_xq8": [_int, _u64, _u64, _u64, _u64, _i64, _i64, _int, _u64, _u64],
+    "vybdq_gemv_xq8_seg3": [_int, _u64, _u64, _i64,
+                            _u64, _u64, _i64, _int, _u64,
+                            _u64, _u64, _i64, _int, _u64,
+                            _u64, _u64, _i64, _int, _u64, _u64],
     "vybdq_gguf_open": [ctypes.c_char_p],
     "vybdq_gguf_close": [_i64],
     "vybdq_gguf_info": [_i64, _int],

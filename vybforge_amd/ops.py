@@ -189,6 +189,48 @@ def quant_q8_act(X, out=None):
     return q, d
 
 
+XQ8_TYPES = (GGML_Q4_K, GGML_Q5_K, GGML_IQ2_S)
+
+
+def _check_xq8(Xq, Xs, K):
+    _need(Xq.dtype == torch.int8 and Xq.numel() == K, f"Xq must be int8 [{K}]")
+    _need(Xs.dtype == torch.float32 and Xs.numel() == K // 32, f"Xs must be float32 [{K // 32}]")
+
+
+def gemv_xq8(ty, W, Xq, Xs, N, K, y_dtype=torch.float32, residual=None, out=None):
+    """Decode GEMV on one xq8 row (vybdq_gemv_xq8): Y[n] = RS[n] + sum_k W[n, k] Xs[k/32] Xq[k];
+    ty Q4_K, Q5_K or IQ2_S. Returns Y [N]."""
+    _need(ty in XQ8_TYPES, f"xq8 GEMV: unsupported GGUF type {ty}")
+    _check_xq8(Xq, Xs, K)
+    _check_weights(W, ty, N, K)
+    if out is None:
+        out = torch.empty(N, dtype=y_dtype, device=Xq.device)
+    _need(out.numel() == N, f"out must hold {N} elements")
+    _need(residual is None or (residual.dtype == out.dtype and residual.numel() == N), "residual must match out")
+    call("vybdq_gemv_xq8", ty, _ptr(W), _ptr(Xq), _ptr(Xs), _ptr(out), N, K, _dt(out.dtype), _ptr(residual),
+         _stream())
+    return out
+
+
+def gemv_xq8_seg3(ty, Xq, Xs, K, segs):
+    """Fused xq8 GEMVs sharing one xq8 row (vybdq_gemv_xq8_seg3). segs: up to 3 (W, Y, N) or
+    (W, Y, N, residual) with Y preallocated [N]."""
+    _need(ty in XQ8_TYPES, f"xq8 GEMV: unsupported GGUF type {ty}")
+    _check_xq8(Xq, Xs, K)
+    args = []
+    for i in range(3):
+        if i < len(segs) and segs[i][2] > 0:
+            W, Y, N = segs[i][:3]
+            RS = segs[i][3] if len(segs[i]) > 3 else None
+            _check_weights(W, ty, N, K, f"segment {i}: W")
+            _need(Y.numel() == N, f"segment {i}: Y must hold {N} elements")
+            _need(RS is None or (RS.dtype == Y.dtype and RS.numel() == N), f"segment {i}: residual must match Y")
+            args += [_ptr(W), _ptr(Y), N, _dt(Y.dtype), _ptr(RS)]
+        else:
+            args += [0, 0, 0, F32, 0]
+    call("vybdq_gemv_xq8_seg3", ty, _ptr(Xq), _ptr(Xs), K, *args, _stream())
+
+
 # ---- persistent GEMV chain ---------------------------------------------------------------
 
 def rmsnorm_q8(X, W, eps, y_dtype=None, f32_copy=False, q8=True):
