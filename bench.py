@@ -40,7 +40,7 @@ QWEN3_4B = dict(hidden=2560, q=4096, kv=1024, inter=9728, layers=36)
 # not by this run
 STACK_TRAFFIC = dict(bytes_per_launch=14402381, source="profiles/q4_0_gemv_decode_stack.md (rocprofv3 --pmc)")
 
-CONFIGS = ["stack", "stack_chain", "gemv1", "kquant", "producers", "router", "exl3", "prefill", "prefill_i8",
+CONFIGS = ["stack", "stack_chain", "gemv1", "kquant", "xq8", "producers", "router", "exl3", "prefill", "prefill_i8",
            "prefill_kq", "moe", "moe_exl3", "pblock", "copy"]
 
 
@@ -460,6 +460,38 @@ def run_kquant(args, torch, dev):
                                       avg_launch_us=round(per * 1e3, 3), bytes_per_launch=bytes_call),
                 workload=f"{name} GEMV 9728x2560 fp16 x (24 rotated copies)",
                 bytes_per_step=bytes_call * len(copies), launches_per_step=len(copies))
+
+
+def run_xq8(args, torch, dev):
+    """Decode GEMV on an xq8 activation row (int8 + f32 scale per 32) at 9728x2560, 24 rotated weight
+    copies; --wtype 12 / 13 / 22. The last output is checked against the float64 gate of x'."""
+    from vybforge_amd import ops
+    N, K, ty = 9728, 2560, args.wtype
+    if ty not in ops.XQ8_TYPES:
+        raise SystemExit("--config xq8 takes --wtype 12, 13 or 22")
+    name = {12: "Q4_K", 13: "Q5_K", 22: "IQ2_S"}[ty]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    copies = [kquant_blocks_gpu(torch, gen, ty, N, K, dev) for _ in range(24)]
+    xq, xd = ops.quant_q8_act(torch.randn(K, generator=gen, device=dev))
+    xq, xd = xq.reshape(K), xd.reshape(K // 32)
+    y = torch.empty(N, device=dev)
+    ms, wall = timed_graph(torch, [lambda W=W: ops.gemv_xq8(ty, W, xq, xd, N, K, out=y) for W in copies], args.steps,
+                           args.warmup)
+    per = ms / len(copies)
+    bytes_call = ops.row_bytes(ty, K) * N + K + K // 8 + 4 * N
+    value = bytes_call / (per * 1e-3) / 1e9
+    check = None
+    if not args.no_check:
+        from oracle import matmul
+        ref = matmul.gemv_xq8_f64(ty, copies[-1].cpu().numpy(), xq.cpu().numpy(), xd.cpu().numpy(), N, K)
+        check = dict(ok=True, rel=expect(f"xq8 {name}", rel_gate(y.cpu().numpy(), ref), 1e-5),
+                     what="last copy, all rows, float64 gate of the xq8-dequantized x")
+    return dict(value=value, ms_step=ms, wall=wall, flops=2 * N * K * len(copies),
+                roofline=hbm_roofline(value, f"k_gemv_xq8<{name}>", "bytes per GEMV / (event time / 24 launches)",
+                                      avg_launch_us=round(per * 1e3, 3), bytes_per_launch=bytes_call),
+                workload=f"{name} GEMV 9728x2560 on xq8 x (24 rotated copies)",
+                bytes_per_step=bytes_call * len(copies), launches_per_step=len(copies), check=check)
 
 
 def run_producers(args, torch, dev):
@@ -1084,7 +1116,7 @@ def main():
     if not torch.cuda.is_available():
         sys.exit("no GPU visible")
     dev = torch.device("cuda:0")
-    runners = dict(gemv1=run_gemv1, kquant=run_kquant, producers=run_producers, router=run_router, exl3=run_exl3,
+    runners = dict(gemv1=run_gemv1, kquant=run_kquant, xq8=run_xq8, producers=run_producers, router=run_router, exl3=run_exl3,
                    prefill=run_prefill, prefill_i8=run_prefill_i8, prefill_kq=run_prefill_kq, moe=run_moe,
                    moe_exl3=run_moe_exl3,
                    pblock=run_pblock, copy=run_copy)
