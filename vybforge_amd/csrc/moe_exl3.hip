@@ -55,6 +55,26 @@ __device__ __forceinline__ const T *mx_ptr(const uint64_t *tab, int e, int p, in
 
 __device__ __forceinline__ float mx_silu(float g) { return g / (1.0f + __expf(-g)); }
 
+// sum over s < S of the float pair at base + s * stride, added in split order: loads in groups of 8
+// independent 8-byte loads (one round trip per group; a loop that adds each load as it arrives
+// waits S round trips)
+__device__ __forceinline__ f2 mx_sum_splits(const float *base, int64_t stride, int S) {
+  f2 acc = f2{0.f, 0.f};
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    f2 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      v[u] = s0 + u < S ? *reinterpret_cast<const f2 *>(base + static_cast<int64_t>(s0 + u) * stride) : f2{0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < S) {
+        acc[0] += v[u][0];
+        acc[1] += v[u][1];
+      }
+  }
+  return acc;
+}
+
 // ---- 2. x' rows -------------------------------------------------------------------------------
 // One workgroup of kMxRowWaves waves per ((token, slot), projection); wave w rotates the 128-chunks
 // w, w + kMxRowWaves, ... (at most CPW each), then the row's largest |x'| sets its scale.
@@ -366,15 +386,10 @@ __global__ void __launch_bounds__(64 * kMxRowWaves) k_mx_mid(const uint64_t *__r
     a[q][0] = a[q][1] = 0.f;
     if (c < nch) {
       const int64_t n0 = 128 * static_cast<int64_t>(c) + 2 * lane;
-      float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
-      for (int s = 0; s < S; ++s) {
-        const float *zr = zpart + (static_cast<int64_t>(s) * rows + r) * (2 * I);
-        const f2 gv = *reinterpret_cast<const f2 *>(zr + n0), uv = *reinterpret_cast<const f2 *>(zr + I + n0);
-        g0 += gv[0];
-        g1 += gv[1];
-        u0 += uv[0];
-        u1 += uv[1];
-      }
+      const float *zr = zpart + static_cast<int64_t>(r) * (2 * I) + n0;
+      const f2 gs = mx_sum_splits(zr, static_cast<int64_t>(rows) * (2 * I), S);
+      const f2 us = mx_sum_splits(zr + I, static_cast<int64_t>(rows) * (2 * I), S);
+      float g0 = gs[0], g1 = gs[1], u0 = us[0], u1 = us[1];
       g0 *= sg;
       g1 *= sg;
       u0 *= su;
@@ -510,11 +525,22 @@ __global__ void __launch_bounds__(256) k_bf16_swiglu(const float *__restrict__ p
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= static_cast<int64_t>(T) * N) return;
   const int64_t m = i / N, n = i % N;
+  const float *o = part + m * (2 * N) + n;
+  const int64_t stride = static_cast<int64_t>(T) * (2 * N);
   float g = 0.f, u = 0.f;
-  for (int s = 0; s < S; ++s) {
-    const float *o = part + (static_cast<int64_t>(s) * T + m) * (2 * N);
-    g += o[n];
-    u += o[N + n];
+  for (int s0 = 0; s0 < S; s0 += 8) {  // groups of 8 independent loads, added in split order
+    float gv[8], uv[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      gv[q] = s0 + q < S ? o[static_cast<int64_t>(s0 + q) * stride] : 0.f;
+      uv[q] = s0 + q < S ? o[static_cast<int64_t>(s0 + q) * stride + N] : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (s0 + q < S) {
+        g += gv[q];
+        u += uv[q];
+      }
   }
   g = fminf(g, limit);
   u = fminf(fmaxf(u, -limit), limit);
@@ -534,40 +560,44 @@ __global__ void __launch_bounds__(256) k_bf16_terms(const void *__restrict__ X, 
 }
 
 // ---- 7. combine -----------------------------------------------------------------------------------
-// grid (T, H / 128 chunks), one wave each
+// grid (T, H / 128 chunks), kMxRowWaves waves: wave j finishes the slots j, j + kMxRowWaves, ... of
+// the token (splits summed, output rotation, svh) into LDS; wave 0 then adds them with their routing
+// weights in slot order, and the shared expert's partials in split order
+constexpr int kMxMaxTopk = 64;
 template <int ODT>
-__global__ void __launch_bounds__(64) k_mx_combine(const uint64_t *__restrict__ tab, const int *__restrict__ idx,
-                                                  const int *__restrict__ pos, const float *__restrict__ w, int topk,
-                                                  const float *__restrict__ zd, const float *__restrict__ ascale,
-                                                  int S, int rows, int64_t H,
-                                                  const float *__restrict__ sh, int Ssh, int T,
-                                                  void *__restrict__ out) {
-  const int t = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
+__global__ void __launch_bounds__(64 * kMxRowWaves) k_mx_combine(const uint64_t *__restrict__ tab,
+                                                                const int *__restrict__ idx,
+                                                                const int *__restrict__ pos,
+                                                                const float *__restrict__ w, int topk,
+                                                                const float *__restrict__ zd,
+                                                                const float *__restrict__ ascale, int S, int rows,
+                                                                int64_t H, const float *__restrict__ sh, int Ssh,
+                                                                int T, void *__restrict__ out) {
+  __shared__ f2 zs[kMxMaxTopk][64];
+  const int t = blockIdx.x, c = blockIdx.y, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int64_t n0 = 128 * static_cast<int64_t>(c) + 2 * lane;
-  float y0 = 0.f, y1 = 0.f;
-  for (int sl = 0; sl < topk; ++sl) {
+  for (int sl = wave; sl < topk; sl += kMxRowWaves) {
     const int i = t * topk + sl;
     const int e = idx[i], r = pos[i];
-    float z0 = 0.f, z1 = 0.f;
-    for (int s = 0; s < S; ++s) {
-      const f2 v = *reinterpret_cast<const f2 *>(zd + (static_cast<int64_t>(s) * rows + r) * H + n0);
-      z0 += v[0];
-      z1 += v[1];
-    }
-    z0 *= ascale[r];
-    z1 *= ascale[r];
+    const f2 z = mx_sum_splits(zd + static_cast<int64_t>(r) * H + n0, static_cast<int64_t>(rows) * H, S);
+    float z0 = z[0] * ascale[r], z1 = z[1] * ascale[r];
     fwht128_wave(z0, z1);
     const _Float16 *svd = mx_ptr<_Float16>(tab, e, 2, 2);
-    const float wt = w[i];
-    y0 = fmaf(wt, z0 * kRScale * static_cast<float>(svd[n0]), y0);
-    y1 = fmaf(wt, z1 * kRScale * static_cast<float>(svd[n0 + 1]), y1);
+    zs[sl][lane] = f2{z0 * kRScale * static_cast<float>(svd[n0]), z1 * kRScale * static_cast<float>(svd[n0 + 1])};
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float y0 = 0.f, y1 = 0.f;
+  for (int sl = 0; sl < topk; ++sl) {
+    const float wt = w[t * topk + sl];
+    y0 = fmaf(wt, zs[sl][lane][0], y0);
+    y1 = fmaf(wt, zs[sl][lane][1], y1);
   }
   if (sh) {
-    for (int s = 0; s < Ssh; ++s) {
-      const f2 v = *reinterpret_cast<const f2 *>(sh + (static_cast<int64_t>(s) * T + t) * H + n0);
-      y0 += v[0];
-      y1 += v[1];
-    }
+    const f2 v = mx_sum_splits(sh + static_cast<int64_t>(t) * H + n0, static_cast<int64_t>(T) * H, Ssh);
+    y0 += v[0];
+    y1 += v[1];
   }
   store_elem<ODT>(out, nullptr, static_cast<int64_t>(t) * H + n0, y0);
   store_elem<ODT>(out, nullptr, static_cast<int64_t>(t) * H + n0 + 1, y1);
@@ -850,8 +880,8 @@ extern "C" int vybdq_moe_forward_exl3(uint64_t x, int x_dt, uint64_t logits, int
   }
   // 7. combine
   VYBDQ_DISPATCH_IN(out_dt, ODT,
-      hipLaunchKernelGGL((k_mx_combine<ODT>), dim3(static_cast<unsigned>(T), static_cast<unsigned>(H / 128)), dim3(64),
-                         0, s, tab, idx, m.pos, wts, k, m.zd, m.as, p.dn.S, n, H, shared ? m.sd : nullptr, p.Ssd,
+      hipLaunchKernelGGL((k_mx_combine<ODT>), dim3(static_cast<unsigned>(T), static_cast<unsigned>(H / 128)),
+                         dim3(64 * kMxRowWaves), 0, s, tab, idx, m.pos, wts, k, m.zd, m.as, p.dn.S, n, H, shared ? m.sd : nullptr, p.Ssd,
                          static_cast<int>(T), reinterpret_cast<void *>(out)));
   return check_launch("moe exl3 combine");
 }
