@@ -130,63 +130,191 @@ __global__ void __launch_bounds__(64) k_moe_route_logit(const void *__restrict__
   route_keyed<LDT>(logits, blockIdx.x, E, topk, scale, idx_out, w_out, nullptr);
 }
 
+// Smallest / largest 32-bit value over the wave (DPP steps as wave_max_u64), in every lane.
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_ext_u32(uint32_t v) {
+  auto step = [&](auto ctrl, auto rows) {
+    constexpr int C = decltype(ctrl)::value, R = decltype(rows)::value;
+    const uint32_t o = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+        static_cast<int>(MAX ? 0u : 0xffffffffu), static_cast<int>(v), C, R, 0xf, false));
+    v = MAX ? (o > v ? o : v) : (o < v ? o : v);
+  };
+  step(std::integral_constant<int, DPP_QUAD_XOR1>{}, std::integral_constant<int, 0xf>{});
+  step(std::integral_constant<int, DPP_QUAD_XOR2>{}, std::integral_constant<int, 0xf>{});
+  step(std::integral_constant<int, DPP_HALF_MIRROR>{}, std::integral_constant<int, 0xf>{});
+  step(std::integral_constant<int, DPP_ROW_MIRROR>{}, std::integral_constant<int, 0xf>{});
+  step(std::integral_constant<int, DPP_BCAST15>{}, std::integral_constant<int, 0xa>{});
+  step(std::integral_constant<int, DPP_BCAST31>{}, std::integral_constant<int, 0x8>{});
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+// A double's order as an unsigned 64-bit key: larger double, larger key; -0 keys as +0 (they
+// compare equal), and NaN keys below every number (a NaN never compares greater).
+__device__ __forceinline__ uint64_t double_order_key(double d) {
+  if (d != d) return 0;
+  uint64_t b = __double_as_longlong(d);
+  if (b == 0x8000000000000000ull) b = 0;
+  return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+
+// Routing of one token by the whole 256-thread workgroup: thread i holds experts i, i + 256, i + 512
+// and i + 768 (E <= 1024) with their double-precision sigmoid scores and keys (score + bias, or the
+// logit without a bias); each wave selects the top-k of its threads' experts, and wave 0 selects the
+// top-k of the 4 k candidates. A selection round is a wave maximum (DPP, on the VALU) of the top 32
+// bits of the lanes' best order keys; only when several lanes share it, of the low 32 bits among
+// those and then the lowest expert id (ties to the lower id); the owner lane retires its winner. Keys, the tie rule, the scores and the weight arithmetic (scores
+// over their sum in selection order, times scale) are one total order and one formula, so the
+// result is that of a single pass over all E experts.
+struct RouteLds {  // candidate c = wave * k + its selection round
+  uint64_t key[256];
+  double sc[256];
+  int e[256];
+  double slot_sc[64];
+};
+
 template <int LDT>
-__device__ __forceinline__ void route_double(const void *__restrict__ logits, const float *__restrict__ bias, int t,
-                                             int E, int topk, double scale, int *__restrict__ idx_out,
-                                             float *__restrict__ w_out, int *__restrict__ idx_copy) {
-  const int lane = threadIdx.x & 63;
-  constexpr int PER = 16;  // experts per lane (E <= 1024)
-  double key[PER];
-  double score[PER];
-  for (int i = 0; i < PER; ++i) {
-    const int e = lane + 64 * i;
+__device__ __forceinline__ void route_double_wg(const void *__restrict__ logits, const float *__restrict__ bias, int t,
+                                                int E, int topk, double scale, int *__restrict__ idx_out,
+                                                float *__restrict__ w_out, int *__restrict__ idx_copy, RouteLds &L) {
+  constexpr uint32_t kNone = 0x7fffffffu;  // no candidate (and above every expert id)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint64_t key[4];
+  uint32_t eid[4];
+  double score[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tid + 256 * i;
+    key[i] = 0;
+    eid[i] = kNone;
+    score[i] = 0.0;
     if (e < E) {
       const double l = load_logit<LDT>(logits, static_cast<int64_t>(t) * E + e);
       score[i] = 1.0 / (1.0 + exp(-l));
-      key[i] = bias ? score[i] + static_cast<double>(bias[e]) : l;
-    } else {
-      score[i] = 0.0;
-      key[i] = -INFINITY;
+      key[i] = double_order_key(bias ? score[i] + static_cast<double>(bias[e]) : l);
+      eid[i] = static_cast<uint32_t>(e);
     }
   }
-  double tot = 0.0;
-  double my_sc = 0.0;  // lane s keeps slot s's raw score
-  for (int s = 0; s < topk; ++s) {
-    // lane-local best (lowest index among equal keys), then wave argmax with the same rule
-    double bk = -INFINITY;
-    int be = 1 << 30;
-    for (int i = 0; i < PER; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && (key[i] > bk || (key[i] == bk && e < be))) { bk = key[i]; be = e; }
+  // one selection round over (key, eid, score) of up to 4 entries per lane; the winner's entry is
+  // retired; returns the winner's key, id and score in every lane
+  auto select = [&](uint64_t (&k)[4], uint32_t (&id)[4], const double (&sc)[4], uint64_t &wk, uint32_t &we,
+                    double &ws) {
+    uint64_t bk = 0;
+    uint32_t be = kNone;
+    double bs = 0.0;
+    // (an empty entry, key 0 and id kNone, never beats the start value: no test of it, no branch)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool take = (k[i] > bk) | ((k[i] == bk) & (id[i] < be));
+      bk = take ? k[i] : bk;
+      be = take ? id[i] : be;
+      bs = take ? sc[i] : bs;
     }
-    for (int off = 32; off > 0; off >>= 1) {
-      const double ok = __shfl_xor(bk, off, 64);
-      const int oe = __shfl_xor(be, off, 64);
-      if (ok > bk || (ok == bk && oe < be)) { bk = ok; be = oe; }
+    // the top 32 key bits decide unless several lanes share the largest; then the low 32 bits,
+    // then the lowest id
+    const uint32_t khi = static_cast<uint32_t>(bk >> 32);
+    const uint32_t mhi = wave_ext_u32<true>(khi);
+    uint64_t own = __ballot(khi == mhi && be != kNone);
+    if (__popcll(own) > 1) {
+      const uint32_t klo = khi == mhi ? static_cast<uint32_t>(bk) : 0u;
+      const uint32_t mlo = wave_ext_u32<true>(klo);
+      const uint32_t e1 = wave_ext_u32<false>(khi == mhi && klo == mlo ? be : kNone);
+      own = __ballot(be == e1 && e1 != kNone);
     }
-    // the owner retires the winner
-    double sc = 0.0;
-    if ((be & 63) == lane) {
-      const int i = be >> 6;
-      for (int ii = 0; ii < PER; ++ii)
-        if (ii == i) { sc = score[ii]; key[ii] = -INFINITY; }
-    }
-    sc = __shfl(sc, be & 63, 64);
+    const int src = own ? static_cast<int>(__builtin_ctzll(own)) : 0;
+    we = own ? static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(be), src)) : kNone;
+    wk = (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(khi), src))) << 32) |
+         static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(bk)), src));
+    const uint64_t sb = __double_as_longlong(bs);
+    const uint32_t slo = __builtin_amdgcn_readlane(static_cast<uint32_t>(sb), src);
+    const uint32_t shi = __builtin_amdgcn_readlane(static_cast<uint32_t>(sb >> 32), src);
+    ws = __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(shi) << 32) | slo));
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (id[i] == we) {  // retired (ids are unique): an empty entry again
+        id[i] = kNone;
+        k[i] = 0;
+      }
+  };
+  for (int s = 0; s < topk; ++s) {  // this wave's top-k
+    uint64_t wk;
+    uint32_t we;
+    double ws;
+    select(key, eid, score, wk, we, ws);
     if (lane == 0) {
-      idx_out[t * topk + s] = be;
-      if (idx_copy) idx_copy[t * topk + s] = be;
+      L.key[wave * topk + s] = wk;
+      L.sc[wave * topk + s] = ws;
+      L.e[wave * topk + s] = static_cast<int>(we);
     }
-    if (lane == s) my_sc = sc;
-    tot += sc;
   }
-  if (lane < topk) w_out[t * topk + lane] = static_cast<float>(my_sc / (tot + 1e-20) * scale);
+  __syncthreads();
+  if (wave == 0 && 4 * topk <= 64) {
+    // the top-k of the 4 k candidates by rank: lane c holds candidate c and counts the candidates
+    // that beat it (larger key, or the same key and a lower id), reading them from LDS (the same
+    // word for every lane); a rank below k is the candidate's slot
+    const int nc = 4 * topk;
+    const bool have = lane < nc;
+    const uint64_t myk = have ? L.key[lane] : 0;
+    const uint32_t mye = have ? static_cast<uint32_t>(L.e[lane]) : kNone;
+    // (an empty candidate, key 0 and id kNone, beats no real one: no test of it, no branch)
+    int rank = 0;
+    for (int c0 = 0; c0 < nc; c0 += 8) {  // 8 candidates read before any is compared
+      uint64_t k2[8];
+      uint32_t e2[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        k2[j] = L.key[c0 + j];
+        e2[j] = static_cast<uint32_t>(L.e[c0 + j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        rank += static_cast<int>((c0 + j < nc) & ((k2[j] > myk) | ((k2[j] == myk) & (e2[j] < mye))));
+    }
+    if (have && mye != kNone && rank < topk) {
+      idx_out[t * topk + rank] = static_cast<int>(mye);
+      if (idx_copy) idx_copy[t * topk + rank] = static_cast<int>(mye);
+      L.slot_sc[rank] = L.sc[lane];
+    }
+    __builtin_amdgcn_wave_barrier();
+    double tot = 0.0;  // the scores summed in slot order
+    for (int q = 0; q < topk; ++q) tot += L.slot_sc[q];
+    if (lane < topk) w_out[t * topk + lane] = static_cast<float>(L.slot_sc[lane] / (tot + 1e-20) * scale);
+  } else if (wave == 0) {  // more than 64 candidates: k selection rounds over lanes holding 4 each
+    uint64_t ck[4];
+    uint32_t ce[4];
+    double cs[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = lane + 64 * j;
+      const bool ok = c < 4 * topk;
+      ck[j] = ok ? L.key[c] : 0;
+      cs[j] = ok ? L.sc[c] : 0.0;
+      ce[j] = ok ? static_cast<uint32_t>(L.e[c]) : kNone;
+    }
+    double my_sc = 0.0, tot = 0.0;
+    for (int s = 0; s < topk; ++s) {
+      uint64_t wk;
+      uint32_t we;
+      double ws;
+      select(ck, ce, cs, wk, we, ws);
+      if (lane == 0) {
+        idx_out[t * topk + s] = static_cast<int>(we);
+        if (idx_copy) idx_copy[t * topk + s] = static_cast<int>(we);
+      }
+      if (lane == s) my_sc = ws;
+      tot += ws;
+    }
+    if (lane < topk) w_out[t * topk + lane] = static_cast<float>(my_sc / (tot + 1e-20) * scale);
+  }
+  __syncthreads();  // L is reused by the next token
 }
 
+// one token per workgroup of 256 threads
 template <int LDT>
-__global__ void __launch_bounds__(64) k_moe_route(const void *__restrict__ logits, const float *__restrict__ bias,
-                                                  int E, int topk, double scale, int *__restrict__ idx_out,
-                                                  float *__restrict__ w_out) {
-  route_double<LDT>(logits, bias, blockIdx.x, E, topk, scale, idx_out, w_out, nullptr);
+__global__ void __launch_bounds__(256) k_moe_route(const void *__restrict__ logits, const float *__restrict__ bias,
+                                                   int E, int topk, double scale, int *__restrict__ idx_out,
+                                                   float *__restrict__ w_out) {
+  __shared__ RouteLds L;
+  route_double_wg<LDT>(logits, bias, blockIdx.x, E, topk, scale, idx_out, w_out, nullptr, L);
 }
 
 // One workgroup: per-expert counts, exclusive scans, and each (token, slot)'s bucket position
@@ -331,9 +459,11 @@ __global__ void __launch_bounds__(256) k_moe_route_bucket(const void *__restrict
                                                           int4 *__restrict__ tiles2, int *__restrict__ ntiles2) {
   extern __shared__ int sh[];
   int *idx_lds = sh + 2 * E;  // [T * topk]
-  for (int t = threadIdx.x >> 6; t < T; t += 4) {
-    if constexpr (KEYED) route_keyed<LDT>(logits, t, E, topk, scale, idx_out, w_out, idx_lds);
-    else route_double<LDT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds);
+  if constexpr (KEYED) {
+    for (int t = threadIdx.x >> 6; t < T; t += 4) route_keyed<LDT>(logits, t, E, topk, scale, idx_out, w_out, idx_lds);
+  } else {
+    __shared__ RouteLds L;
+    for (int t = 0; t < T; ++t) route_double_wg<LDT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds, L);
   }
   __syncthreads();
   bucket_tiles(idx_lds, T, topk, E, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2, sh);
@@ -399,9 +529,11 @@ __global__ void __launch_bounds__(256) k_moe_route_bucket_w(const void *__restri
                                                             int4 *__restrict__ tiles, int *__restrict__ ntiles,
                                                             int4 *__restrict__ tiles2, int *__restrict__ ntiles2) {
   __shared__ int idx_lds[64];
-  for (int t = threadIdx.x >> 6; t < T; t += 4) {
-    if constexpr (KEYED) route_keyed<LDT>(logits, t, E, topk, scale, idx_out, w_out, idx_lds);
-    else route_double<LDT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds);
+  if constexpr (KEYED) {
+    for (int t = threadIdx.x >> 6; t < T; t += 4) route_keyed<LDT>(logits, t, E, topk, scale, idx_out, w_out, idx_lds);
+  } else {
+    __shared__ RouteLds L;
+    for (int t = 0; t < T; ++t) route_double_wg<LDT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds, L);
   }
   __syncthreads();
   if (threadIdx.x < 64) bucket_rows_wave(idx_lds, T, topk, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2);
@@ -477,15 +609,16 @@ extern "C" int64_t vybdq_moe_workspace_size(int64_t T, int64_t H, int64_t I, int
 // their own value, with the same ties-to-the-lower-id rule).
 static int launch_route(const void *lg, int logits_dt, const float *bias, int64_t T, int64_t E, int64_t topk,
                         double scale, int *idx, float *w, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(T)), block(64);
+  const dim3 grid(static_cast<unsigned>(T)), block(64), block_wg(256);
   const int e = static_cast<int>(E), k = static_cast<int>(topk);
   if (logits_dt == VYBDQ_F64) {
-    hipLaunchKernelGGL((k_moe_route<VYBDQ_F64>), grid, block, 0, s, lg, bias, e, k, scale, idx, w);
+    hipLaunchKernelGGL((k_moe_route<VYBDQ_F64>), grid, block_wg, 0, s, lg, bias, e, k, scale, idx, w);
   } else if (!bias) {
     VYBDQ_DISPATCH_IN(logits_dt, LDT,
         hipLaunchKernelGGL((k_moe_route_logit<LDT>), grid, block, 0, s, lg, e, k, scale, idx, w));
   } else {
-    VYBDQ_DISPATCH_IN(logits_dt, LDT, hipLaunchKernelGGL((k_moe_route<LDT>), grid, block, 0, s, lg, bias, e, k, scale, idx, w));
+    VYBDQ_DISPATCH_IN(logits_dt, LDT,
+        hipLaunchKernelGGL((k_moe_route<LDT>), grid, block_wg, 0, s, lg, bias, e, k, scale, idx, w));
   }
   return check_launch("moe route");
 }
