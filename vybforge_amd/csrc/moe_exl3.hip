@@ -23,9 +23,11 @@
 //     a' = FWHT(a * suh_down)/sqrt(128) per row, stored as fp16 with its own power-of-two row scale
 //     (a' is small: activations times suh, and subnormal in fp16 without it).
 //  5. k_mx_gemm (down): zd[split][row][n] from a' and the down trellis.
-//  6. shared expert: k_bf16_mm over every token (bf16 matrix cores; activations that are not bf16
-//     enter as two bf16 terms hi + lo, 16 significant bits), the SwiGLU in its epilogue or in
-//     k_bf16_swiglu after a K split, then the down projection into per-split partials.
+//  6. shared expert, carried by the launches of 3 / 4 / 5 as extra workgroups (its bf16 weights
+//     stream from HBM while the routed workgroups decode trellis): gate | up over every token on
+//     the bf16 matrix cores into per-split partials (activations that are not bf16 enter as two
+//     bf16 terms hi + lo, 16 significant bits), the SwiGLU with the mid launch, the down projection
+//     into per-split partials.
 //  7. k_mx_combine: out[t] = sum_s w[t,s] svh_down * FWHT(scale_row sum_split zd[row(t,s)])/sqrt(128)
 //     + sum_split shared[t], slots in order (deterministic).
 //
@@ -132,6 +134,141 @@ __global__ void __launch_bounds__(64 * kMxRowWaves) k_mx_xprep(const void *__res
   if (threadIdx.x == 0) xscale[p * rows + r] = sc;
 }
 
+// ---- 6. shared expert: bf16 weights on the matrix cores, carried by the routed launches ----------
+
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+struct Bf16MmArgs {
+  const uint16_t *W, *W2;     // bf16 [N][K] row-major (W2: the up matrix of gate | up, else null)
+  const uint16_t *X, *Xlo;    // bf16 [T][K]; Xlo: the low terms (X + Xlo = the activations) or null
+  int T, N;
+  int64_t K;
+  int kps;                    // 32-wide k-steps per split
+  float *part;                // [S][T][nout] (nout = N, or 2 N for gate | up: gate then up)
+};
+
+// f32 -> two bf16 terms: hi = bf16(v) (nearest even), lo = bf16(v - hi) (v - hi is exact)
+__device__ __forceinline__ void bf16_split(float v, uint16_t &hi, uint16_t &lo) {
+  hi = f32_to_bf16(v);
+  lo = f32_to_bf16(v - bf16_to_f32(hi));
+}
+
+// tile (column group bx of N / 64, split s, token tile bz of ceil(T / 16)), 4 waves: wave w owns
+// columns 64 bx + 16 w .. + 16 (PAIR: of both gate and up) for 16 tokens over the split's k-range.
+// Lane l reads row (l & 15) of the A and B operands at k offset 8 (l >> 4): 16 contiguous bytes
+// of one weight row per lane, so each load instruction covers 64 bytes of 16 rows and two
+// consecutive k-steps a whole 128-byte line of each row. kD k-steps of loads in flight.
+template <bool PAIR, bool LO>
+__device__ __forceinline__ void bf16_mm_tile(const Bf16MmArgs &a, int bx, int s, int bz) {
+  constexpr int kD = 4;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+  const int n0 = 64 * bx + 16 * wave;
+  const int m0 = 16 * bz;
+  const int64_t K = a.K;
+  const int nks = static_cast<int>(K / 32);
+  const int ks0 = s * a.kps;
+  const int ks1 = min(ks0 + a.kps, nks);
+  const int am = m0 + (lane & 15);
+  const bool arow_ok = am < a.T;
+  const int64_t koff = 8 * (lane >> 4);
+  const uint16_t *ap = a.X + static_cast<int64_t>(arow_ok ? am : 0) * K + koff;
+  const uint16_t *alp = LO ? a.Xlo + static_cast<int64_t>(arow_ok ? am : 0) * K + koff : nullptr;
+  const uint16_t *bp = a.W + static_cast<int64_t>(n0 + (lane & 15)) * K + koff;
+  const uint16_t *bp2 = PAIR ? a.W2 + static_cast<int64_t>(n0 + (lane & 15)) * K + koff : nullptr;
+  struct Step { bf8 x, xl, w, w2; };
+  auto load = [&](int ks) {
+    Step st;
+    const int kc = ks < ks1 ? ks : ks0;  // in range
+    const int64_t o = 32 * static_cast<int64_t>(kc);
+    st.w = *reinterpret_cast<const bf8 *>(bp + o);
+    if constexpr (PAIR) st.w2 = *reinterpret_cast<const bf8 *>(bp2 + o);
+    st.x = arow_ok ? *reinterpret_cast<const bf8 *>(ap + o) : bf8{};
+    if constexpr (LO) st.xl = arow_ok ? *reinterpret_cast<const bf8 *>(alp + o) : bf8{};
+    return st;
+  };
+  f4 acc = f4{0.f, 0.f, 0.f, 0.f}, acc2 = f4{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](const Step &st) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.x, st.w, acc, 0, 0, 0);
+    if constexpr (LO) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.xl, st.w, acc, 0, 0, 0);
+    if constexpr (PAIR) {
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.x, st.w2, acc2, 0, 0, 0);
+      if constexpr (LO) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.xl, st.w2, acc2, 0, 0, 0);
+    }
+  };
+  Step ring[kD];
+#pragma unroll
+  for (int d = 0; d < kD; ++d) ring[d] = load(ks0 + d);
+  int k = ks0;
+  for (; k + kD <= ks1; k += kD) {
+#pragma unroll
+    for (int d = 0; d < kD; ++d) {
+      mma(ring[d]);
+      ring[d] = load(k + d + kD);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < kD - 1; ++d)
+    if (k + d < ks1) mma(ring[d]);
+  // acc[r] = C[token m0 + 4 (lane >> 4) + r][column n0 + (lane & 15)]
+  const int n = n0 + (lane & 15);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = m0 + 4 * (lane >> 4) + r;
+    if (m >= a.T) continue;
+    const int nout = PAIR ? 2 * a.N : a.N;
+    float *o = a.part + (static_cast<int64_t>(s) * a.T + m) * nout;
+    o[n] = acc[r];
+    if constexpr (PAIR) o[a.N + n] = acc2[r];
+  }
+}
+
+// The shared expert's tiles carried by a routed launch: tile i = (column group i mod ngx, split,
+// token tile), ngx = N / 64; `tiles` of them in all.
+struct MxShared {
+  Bf16MmArgs mm;
+  int ngx, S, tiles;
+};
+
+// gate | up partials [S][T][2 N] -> act hi + lo bf16 [T][N], splits summed in order; element i
+__device__ __forceinline__ void bf16_swiglu_elem(const float *__restrict__ part, int S, int T, int N, float limit,
+                                                 uint16_t *__restrict__ act, uint16_t *__restrict__ act_lo, int64_t i) {
+  if (i >= static_cast<int64_t>(T) * N) return;
+  const int64_t m = i / N, n = i % N;
+  const float *o = part + m * (2 * N) + n;
+  const int64_t stride = static_cast<int64_t>(T) * (2 * N);
+  float g = 0.f, u = 0.f;
+  for (int s0 = 0; s0 < S; s0 += 8) {  // groups of 8 independent loads, added in split order
+    float gv[8], uv[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      gv[q] = s0 + q < S ? o[static_cast<int64_t>(s0 + q) * stride] : 0.f;
+      uv[q] = s0 + q < S ? o[static_cast<int64_t>(s0 + q) * stride + N] : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (s0 + q < S) {
+        g += gv[q];
+        u += uv[q];
+      }
+  }
+  g = fminf(g, limit);
+  u = fminf(fmaxf(u, -limit), limit);
+  uint16_t hi, lo;
+  bf16_split(mx_silu(g) * u, hi, lo);
+  act[i] = hi;
+  act_lo[i] = lo;
+}
+
+// activations that are not bf16 -> hi + lo bf16 terms
+template <int XDT>
+__global__ void __launch_bounds__(256) k_bf16_terms(const void *__restrict__ X, int64_t n, uint16_t *__restrict__ hi,
+                                                    uint16_t *__restrict__ lo) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  bf16_split(load_elem<XDT>(X, i), hi[i], lo[i]);
+}
+
 // ---- 3. / 5. grouped EXL3 products -------------------------------------------------------------
 
 struct MxGemmArgs {
@@ -146,6 +283,7 @@ struct MxGemmArgs {
   int Np;              // output features per projection (multiple of 128)
   int ncat;            // nproj Np
   int kbs;             // 16-row k-blocks per split (a multiple of 8)
+  int gy;              // grid y of the routed column blocks; shared-expert workgroups follow
 };
 
 constexpr int kMxRedStride = 132;  // floats per row of the per-wave partials (16-column groups on distinct banks)
@@ -163,10 +301,24 @@ __host__ __device__ constexpr size_t mx_lds_bytes(int BP, int kbs) {
 // quarter of the split's k-blocks on the block's 128 columns, the waves' partials summed in LDS in
 // a fixed order. The group index is the fastest grid dimension and the bound is a multiple of 8,
 // so every column block of one group runs on the same XCD (its L2 holds the group's x' rows).
-template <int BP>
-__global__ void __launch_bounds__(256) k_mx_gemm(const MxGemmArgs a) {
+// SH: the launch also carries the shared expert's tiles (0 none; 1 gate | up, bf16 activations;
+// 2 gate | up, activations as bf16 hi + lo terms; 3 down, hi + lo), as workgroups with blockIdx.x
+// past the routed groups' bound: its bf16 weights stream from HBM while the routed workgroups
+// decode trellis on the VALU.
+template <int BP, int SH>
+__global__ void __launch_bounds__(256) k_mx_gemm(const MxGemmArgs a, const MxShared sh) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int jt = blockIdx.x;
+  if constexpr (SH != 0) {
+    if (static_cast<int>(blockIdx.y) >= a.gy) {  // rows of y past the routed column blocks
+      const int i = ((static_cast<int>(blockIdx.y) - a.gy) * static_cast<int>(gridDim.z) + static_cast<int>(blockIdx.z)) *
+                        static_cast<int>(gridDim.x) + jt;
+      if (i >= sh.tiles) return;
+      const int bx = i % sh.ngx, rest = i / sh.ngx;
+      bf16_mm_tile<SH != 3, SH != 1>(sh.mm, bx, rest % sh.S, rest / sh.S);
+      return;
+    }
+  }
   if (jt >= *a.ngroups) return;
   const int4 grp = a.groups[jt];
   const int e = grp.x, r0 = grp.y, B = grp.z - grp.y;  // 1 <= B <= BP
@@ -360,18 +512,31 @@ __global__ void __launch_bounds__(256) k_mx_gemm(const MxGemmArgs a) {
   }
 }
 
+// the shared expert's SwiGLU carried by the mid launch (workgroups past the routed rows)
+struct MxSwiglu {
+  const float *part;  // [S][T][2 N] gate | up partials
+  int S, T, N;
+  uint16_t *act, *act_lo;
+};
+
 // ---- 4. output rotation of gate | up, SwiGLU, input rotation of down ----------------------------
 // One workgroup per (token, slot) row, wave w on the 128-chunks w, w + kMxRowWaves, ...; the
-// splits' partials are summed in split order and multiplied by the row's x' scale
+// splits' partials are summed in split order and multiplied by the row's x' scale. Workgroups past
+// the rows apply the shared expert's SwiGLU.
 template <int CPW>
 __global__ void __launch_bounds__(64 * kMxRowWaves) k_mx_mid(const uint64_t *__restrict__ tab,
                                                             const int *__restrict__ idx, const int *__restrict__ pos,
                                                             const float *__restrict__ zpart,
                                                             const float *__restrict__ xscale, int S, int rows,
                                                             int64_t I, float limit, _Float16 *__restrict__ act,
-                                                            float *__restrict__ ascale) {
+                                                            float *__restrict__ ascale, const MxSwiglu sh) {
   __shared__ float wm[kMxRowWaves];
   const int i = blockIdx.x, lane = threadIdx.x & 63;
+  if (i >= rows) {  // the shared expert's SwiGLU, 64 kMxRowWaves elements per workgroup
+    bf16_swiglu_elem(sh.part, sh.S, sh.T, sh.N, limit, sh.act, sh.act_lo,
+                     static_cast<int64_t>(i - rows) * (64 * kMxRowWaves) + threadIdx.x);
+    return;
+  }
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int e = idx[i], r = pos[i];
   const int nch = static_cast<int>(I / 128);
@@ -417,146 +582,6 @@ __global__ void __launch_bounds__(64 * kMxRowWaves) k_mx_mid(const uint64_t *__r
           h2{static_cast<_Float16>(a[q][0] * f), static_cast<_Float16>(a[q][1] * f)};
   }
   if (threadIdx.x == 0) ascale[r] = sc;
-}
-
-// ---- 6. shared expert: bf16 weights on the matrix cores ------------------------------------------
-
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-
-struct Bf16MmArgs {
-  const uint16_t *W, *W2;     // bf16 [N][K] row-major (W2: the up matrix of gate | up, else null)
-  const uint16_t *X, *Xlo;    // bf16 [T][K]; Xlo: the low terms (X + Xlo = the activations) or null
-  int T, N;
-  int64_t K;
-  int kps;                    // 32-wide k-steps per split
-  float *part;                // [S][T][nout] (nout = N, or 2 N for gate | up: gate then up)
-  uint16_t *act, *act_lo;     // gate | up with one split: silu(min(g, L)) * clamp(u, -L, L) as hi + lo bf16
-  float limit;
-};
-
-// f32 -> two bf16 terms: hi = bf16(v) (nearest even), lo = bf16(v - hi) (v - hi is exact)
-__device__ __forceinline__ void bf16_split(float v, uint16_t &hi, uint16_t &lo) {
-  hi = f32_to_bf16(v);
-  lo = f32_to_bf16(v - bf16_to_f32(hi));
-}
-
-// grid (N / 64 column groups, S splits, ceil(T / 16) token tiles), 4 waves: wave w owns columns
-// 64 blockIdx.x + 16 w .. + 16 (PAIR: of both gate and up) for 16 tokens over the split's k-range.
-// Lane l reads row (l & 15) of the A and B operands at k offset 8 (l >> 4): 16 contiguous bytes
-// of one weight row per lane, so each load instruction covers 64 bytes of 16 rows and two
-// consecutive k-steps a whole 128-byte line of each row. kD k-steps of loads in flight.
-template <bool PAIR, bool LO, bool SWI>
-__global__ void __launch_bounds__(256) k_bf16_mm(const Bf16MmArgs a) {
-  constexpr int kD = 4;
-  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)), lane = threadIdx.x & 63;
-  const int n0 = 64 * static_cast<int>(blockIdx.x) + 16 * wave;
-  const int s = blockIdx.y;
-  const int m0 = 16 * static_cast<int>(blockIdx.z);
-  const int64_t K = a.K;
-  const int nks = static_cast<int>(K / 32);
-  const int ks0 = s * a.kps;
-  const int ks1 = min(ks0 + a.kps, nks);
-  const int am = m0 + (lane & 15);
-  const bool arow_ok = am < a.T;
-  const int64_t koff = 8 * (lane >> 4);
-  const uint16_t *ap = a.X + static_cast<int64_t>(arow_ok ? am : 0) * K + koff;
-  const uint16_t *alp = LO ? a.Xlo + static_cast<int64_t>(arow_ok ? am : 0) * K + koff : nullptr;
-  const uint16_t *bp = a.W + static_cast<int64_t>(n0 + (lane & 15)) * K + koff;
-  const uint16_t *bp2 = PAIR ? a.W2 + static_cast<int64_t>(n0 + (lane & 15)) * K + koff : nullptr;
-  struct Step { bf8 x, xl, w, w2; };
-  auto load = [&](int ks) {
-    Step st;
-    const int kc = ks < ks1 ? ks : ks0;  // in range
-    const int64_t o = 32 * static_cast<int64_t>(kc);
-    st.w = *reinterpret_cast<const bf8 *>(bp + o);
-    if constexpr (PAIR) st.w2 = *reinterpret_cast<const bf8 *>(bp2 + o);
-    st.x = arow_ok ? *reinterpret_cast<const bf8 *>(ap + o) : bf8{};
-    if constexpr (LO) st.xl = arow_ok ? *reinterpret_cast<const bf8 *>(alp + o) : bf8{};
-    return st;
-  };
-  f4 acc = f4{0.f, 0.f, 0.f, 0.f}, acc2 = f4{0.f, 0.f, 0.f, 0.f};
-  auto mma = [&](const Step &st) {
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.x, st.w, acc, 0, 0, 0);
-    if constexpr (LO) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.xl, st.w, acc, 0, 0, 0);
-    if constexpr (PAIR) {
-      acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.x, st.w2, acc2, 0, 0, 0);
-      if constexpr (LO) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.xl, st.w2, acc2, 0, 0, 0);
-    }
-  };
-  Step ring[kD];
-#pragma unroll
-  for (int d = 0; d < kD; ++d) ring[d] = load(ks0 + d);
-  int k = ks0;
-  for (; k + kD <= ks1; k += kD) {
-#pragma unroll
-    for (int d = 0; d < kD; ++d) {
-      mma(ring[d]);
-      ring[d] = load(k + d + kD);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-#pragma unroll
-  for (int d = 0; d < kD - 1; ++d)
-    if (k + d < ks1) mma(ring[d]);
-  // acc[r] = C[token m0 + 4 (lane >> 4) + r][column n0 + (lane & 15)]
-  const int n = n0 + (lane & 15);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = m0 + 4 * (lane >> 4) + r;
-    if (m >= a.T) continue;
-    if constexpr (SWI) {
-      const float gv = fminf(acc[r], a.limit), uv = fminf(fmaxf(acc2[r], -a.limit), a.limit);
-      uint16_t hi, lo;
-      bf16_split(mx_silu(gv) * uv, hi, lo);
-      a.act[static_cast<int64_t>(m) * a.N + n] = hi;
-      a.act_lo[static_cast<int64_t>(m) * a.N + n] = lo;
-    } else {
-      const int nout = PAIR ? 2 * a.N : a.N;
-      float *o = a.part + (static_cast<int64_t>(s) * a.T + m) * nout;
-      o[n] = acc[r];
-      if constexpr (PAIR) o[a.N + n] = acc2[r];
-    }
-  }
-}
-
-// gate | up partials [S][T][2 N] -> act hi + lo bf16 [T][N], splits summed in order
-__global__ void __launch_bounds__(256) k_bf16_swiglu(const float *__restrict__ part, int S, int T, int N, float limit,
-                                                     uint16_t *__restrict__ act, uint16_t *__restrict__ act_lo) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= static_cast<int64_t>(T) * N) return;
-  const int64_t m = i / N, n = i % N;
-  const float *o = part + m * (2 * N) + n;
-  const int64_t stride = static_cast<int64_t>(T) * (2 * N);
-  float g = 0.f, u = 0.f;
-  for (int s0 = 0; s0 < S; s0 += 8) {  // groups of 8 independent loads, added in split order
-    float gv[8], uv[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      gv[q] = s0 + q < S ? o[static_cast<int64_t>(s0 + q) * stride] : 0.f;
-      uv[q] = s0 + q < S ? o[static_cast<int64_t>(s0 + q) * stride + N] : 0.f;
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-      if (s0 + q < S) {
-        g += gv[q];
-        u += uv[q];
-      }
-  }
-  g = fminf(g, limit);
-  u = fminf(fmaxf(u, -limit), limit);
-  uint16_t hi, lo;
-  bf16_split(mx_silu(g) * u, hi, lo);
-  act[i] = hi;
-  act_lo[i] = lo;
-}
-
-// activations that are not bf16 -> hi + lo bf16 terms
-template <int XDT>
-__global__ void __launch_bounds__(256) k_bf16_terms(const void *__restrict__ X, int64_t n, uint16_t *__restrict__ hi,
-                                                    uint16_t *__restrict__ lo) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= n) return;
-  bf16_split(load_elem<XDT>(X, i), hi[i], lo[i]);
 }
 
 // ---- 7. combine -----------------------------------------------------------------------------------
@@ -701,37 +726,40 @@ static MxWs mx_layout(char *base, const MxPlan &p, int64_t T, int64_t H, int64_t
   m.xl = reinterpret_cast<uint16_t *>(take(2 * T * H));
   m.ah = reinterpret_cast<uint16_t *>(take(2 * T * I));
   m.al = reinterpret_cast<uint16_t *>(take(2 * T * I));
-  m.sgu = reinterpret_cast<float *>(take(p.Ssg > 1 ? 4 * static_cast<int64_t>(p.Ssg) * T * 2 * I : 0));
+  m.sgu = reinterpret_cast<float *>(take(4 * static_cast<int64_t>(p.Ssg) * T * 2 * I));
   m.sd = reinterpret_cast<float *>(take(4 * static_cast<int64_t>(p.Ssd) * T * H));
   m.bytes = off;
   return m;
 }
 
-template <int BP>
-static int mx_gemm_launch(const MxGemmArgs &a, int nproj, int S, int max_groups, hipStream_t s) {
+template <int BP, int SH>
+static int mx_gemm_launch(const MxGemmArgs &a, const MxShared &sh, int nproj, int S, int max_groups, hipStream_t s) {
   const size_t lds = mx_lds_bytes(BP, a.kbs);
-  hipLaunchKernelGGL((k_mx_gemm<BP>), dim3(static_cast<unsigned>(max_groups), static_cast<unsigned>(nproj * a.Np / 128),
-                                          static_cast<unsigned>(S)),
-                     dim3(256), lds, s, a);
+  const unsigned gx = static_cast<unsigned>(max_groups), gz = static_cast<unsigned>(S);
+  const unsigned extra = SH ? static_cast<unsigned>((sh.tiles + gx * gz - 1) / (gx * gz)) : 0u;
+  MxGemmArgs b = a;
+  b.gy = nproj * a.Np / 128;
+  hipLaunchKernelGGL((k_mx_gemm<BP, SH>), dim3(gx, static_cast<unsigned>(b.gy) + extra, gz), dim3(256), lds, s, b, sh);
   return check_launch("moe exl3 grouped product");
 }
 
-static int mx_gemm(int BP, const MxGemmArgs &a, int nproj, int S, int max_groups, hipStream_t s) {
-  if (BP == 1) return mx_gemm_launch<1>(a, nproj, S, max_groups, s);
-  if (BP == 2) return mx_gemm_launch<2>(a, nproj, S, max_groups, s);
-  return mx_gemm_launch<16>(a, nproj, S, max_groups, s);
+// the grouped product of the routed experts, carrying the shared expert's tiles of kind SH
+template <int BP>
+static int mx_gemm_bp(int SH, const MxGemmArgs &a, const MxShared &sh, int nproj, int S, int max_groups,
+                      hipStream_t s) {
+  switch (SH) {
+    case 1: return mx_gemm_launch<BP, 1>(a, sh, nproj, S, max_groups, s);
+    case 2: return mx_gemm_launch<BP, 2>(a, sh, nproj, S, max_groups, s);
+    case 3: return mx_gemm_launch<BP, 3>(a, sh, nproj, S, max_groups, s);
+    default: return mx_gemm_launch<BP, 0>(a, sh, nproj, S, max_groups, s);
+  }
 }
 
-// gate | up with one split: the SwiGLU epilogue; otherwise per-split partials
-template <bool PAIR, bool LO>
-static void bf16_mm_launch(const Bf16MmArgs &a, int S, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(a.N / 64), static_cast<unsigned>(S), static_cast<unsigned>((a.T + 15) / 16));
-  if constexpr (PAIR) {
-    if (S == 1) hipLaunchKernelGGL((k_bf16_mm<true, LO, true>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((k_bf16_mm<true, LO, false>), grid, dim3(256), 0, s, a);
-  } else {
-    hipLaunchKernelGGL((k_bf16_mm<false, LO, false>), grid, dim3(256), 0, s, a);
-  }
+static int mx_gemm(int BP, int SH, const MxGemmArgs &a, const MxShared &sh, int nproj, int S, int max_groups,
+                   hipStream_t s) {
+  if (BP == 1) return mx_gemm_bp<1>(SH, a, sh, nproj, S, max_groups, s);
+  if (BP == 2) return mx_gemm_bp<2>(SH, a, sh, nproj, S, max_groups, s);
+  return mx_gemm_bp<16>(SH, a, sh, nproj, S, max_groups, s);
 }
 
 }  // namespace vybdq
@@ -806,12 +834,57 @@ extern "C" int vybdq_moe_forward_exl3(uint64_t x, int x_dt, uint64_t logits, int
   ga.Np = static_cast<int>(I);
   ga.ncat = static_cast<int>(2 * I);
   ga.kbs = p.gu.kbs;
-  rc = mx_gemm(p.BP, ga, 2, p.gu.S, p.max_groups, s);
+  // the shared expert's gate | up ride on this launch, its SwiGLU on the mid launch, its down
+  // projection on the down launch (bf16 weights on the matrix cores: activations that are not
+  // bf16 enter as two bf16 terms hi + lo, 16 significant bits)
+  const bool shared = s_gate != 0;
+  const bool lo = x_dt != VYBDQ_BF16;
+  MxShared shg{}, shd{};
+  if (shared) {
+    const uint16_t *xh = reinterpret_cast<const uint16_t *>(x);
+    if (lo) {
+      const int64_t ne = T * H;
+      VYBDQ_DISPATCH_IN(x_dt, XDT,
+          hipLaunchKernelGGL((k_bf16_terms<XDT>), dim3(static_cast<unsigned>((ne + 255) / 256)), dim3(256), 0, s,
+                             reinterpret_cast<const void *>(x), ne, m.xh, m.xl));
+      rc = check_launch("moe shared expert activation terms");
+      if (rc) return rc;
+      xh = m.xh;
+    }
+    Bf16MmArgs &b = shg.mm;
+    b.W = reinterpret_cast<const uint16_t *>(s_gate);
+    b.W2 = reinterpret_cast<const uint16_t *>(s_up);
+    b.X = xh;
+    b.Xlo = lo ? m.xl : nullptr;
+    b.T = static_cast<int>(T);
+    b.N = static_cast<int>(I);
+    b.K = H;
+    b.kps = p.kps_g;
+    b.part = m.sgu;
+    shg.ngx = static_cast<int>(I / 64);
+    shg.S = p.Ssg;
+    shg.tiles = shg.ngx * p.Ssg * static_cast<int>((T + 15) / 16);
+    Bf16MmArgs &d = shd.mm;
+    d.W = reinterpret_cast<const uint16_t *>(s_down);
+    d.X = m.ah;
+    d.Xlo = m.al;
+    d.T = static_cast<int>(T);
+    d.N = static_cast<int>(H);
+    d.K = I;
+    d.kps = p.kps_d;
+    d.part = m.sd;
+    shd.ngx = static_cast<int>(H / 64);
+    shd.S = p.Ssd;
+    shd.tiles = shd.ngx * p.Ssd * static_cast<int>((T + 15) / 16);
+  }
+  rc = mx_gemm(p.BP, shared ? (lo ? 2 : 1) : 0, ga, shg, 2, p.gu.S, p.max_groups, s);
   if (rc) return rc;
   // 4. SwiGLU between the rotations
+  MxSwiglu sw{m.sgu, p.Ssg, static_cast<int>(T), static_cast<int>(I), m.ah, m.al};
+  const unsigned mid_sh = shared ? static_cast<unsigned>((T * I + 64 * kMxRowWaves - 1) / (64 * kMxRowWaves)) : 0u;
 #define MID(CPW)                                                                                                \
-  hipLaunchKernelGGL((k_mx_mid<CPW>), dim3(static_cast<unsigned>(n)), dim3(64 * kMxRowWaves), 0, s, tab, idx, m.pos,  \
-                     m.zgu, m.xs, p.gu.S, n, I, static_cast<float>(limit), m.act, m.as)
+  hipLaunchKernelGGL((k_mx_mid<CPW>), dim3(static_cast<unsigned>(n) + mid_sh), dim3(64 * kMxRowWaves), 0, s, tab, idx, \
+                     m.pos, m.zgu, m.xs, p.gu.S, n, I, static_cast<float>(limit), m.act, m.as, sw)
   if (cpw_i <= 1) MID(1); else if (cpw_i <= 2) MID(2); else if (cpw_i <= 4) MID(4); else MID(8);
 #undef MID
   rc = check_launch("moe exl3 swiglu");
@@ -825,59 +898,8 @@ extern "C" int vybdq_moe_forward_exl3(uint64_t x, int x_dt, uint64_t logits, int
   da.Np = static_cast<int>(H);
   da.ncat = static_cast<int>(H);
   da.kbs = p.dn.kbs;
-  rc = mx_gemm(p.BP, da, 1, p.dn.S, p.max_groups, s);
+  rc = mx_gemm(p.BP, shared ? 3 : 0, da, shd, 1, p.dn.S, p.max_groups, s);
   if (rc) return rc;
-  // 6. shared expert
-  const bool shared = s_gate != 0;
-  if (shared) {
-    const bool lo = x_dt != VYBDQ_BF16;
-    const uint16_t *xh = reinterpret_cast<const uint16_t *>(x);
-    if (lo) {
-      const int64_t ne = T * H;
-      VYBDQ_DISPATCH_IN(x_dt, XDT,
-          hipLaunchKernelGGL((k_bf16_terms<XDT>), dim3(static_cast<unsigned>((ne + 255) / 256)), dim3(256), 0, s,
-                             reinterpret_cast<const void *>(x), ne, m.xh, m.xl));
-      rc = check_launch("moe shared expert activation terms");
-      if (rc) return rc;
-      xh = m.xh;
-    }
-    Bf16MmArgs b{};
-    b.W = reinterpret_cast<const uint16_t *>(s_gate);
-    b.W2 = reinterpret_cast<const uint16_t *>(s_up);
-    b.X = xh;
-    b.Xlo = lo ? m.xl : nullptr;
-    b.T = static_cast<int>(T);
-    b.N = static_cast<int>(I);
-    b.K = H;
-    b.kps = p.kps_g;
-    b.part = m.sgu;
-    b.act = m.ah;
-    b.act_lo = m.al;
-    b.limit = static_cast<float>(limit);
-    if (lo) bf16_mm_launch<true, true>(b, p.Ssg, s);
-    else bf16_mm_launch<true, false>(b, p.Ssg, s);
-    rc = check_launch("moe shared expert gate | up");
-    if (rc) return rc;
-    if (p.Ssg > 1) {
-      const int64_t ne = T * I;
-      hipLaunchKernelGGL(k_bf16_swiglu, dim3(static_cast<unsigned>((ne + 255) / 256)), dim3(256), 0, s, m.sgu, p.Ssg,
-                         static_cast<int>(T), static_cast<int>(I), static_cast<float>(limit), m.ah, m.al);
-      rc = check_launch("moe shared expert swiglu");
-      if (rc) return rc;
-    }
-    Bf16MmArgs d{};
-    d.W = reinterpret_cast<const uint16_t *>(s_down);
-    d.X = m.ah;
-    d.Xlo = m.al;
-    d.T = static_cast<int>(T);
-    d.N = static_cast<int>(H);
-    d.K = I;
-    d.kps = p.kps_d;
-    d.part = m.sd;
-    bf16_mm_launch<false, true>(d, p.Ssd, s);
-    rc = check_launch("moe shared expert down");
-    if (rc) return rc;
-  }
   // 7. combine
   VYBDQ_DISPATCH_IN(out_dt, ODT,
       hipLaunchKernelGGL((k_mx_combine<ODT>), dim3(static_cast<unsigned>(T), static_cast<unsigned>(H / 128)),
