@@ -7,7 +7,8 @@
 //   expert e: a = silu(min(x Wg_e, L)) * clamp(x Wu_e, -L, L); e_out = a Wd_e
 //   out[t] = sum_s w[t, s] e_out[idx[t, s]](t) + shared(x[t])
 // Without a bias the selection is by logit (sigmoid is monotone: exact order, no float32
-// saturation ties); with a bias the choice is computed in double, as the reference does.
+// saturation ties); with a bias the choice is computed in double, as the reference does. One
+// 256-thread workgroup routes a token (route_double_wg).
 //
 // Pipeline (all on the stream, no host syncs), when H and I are multiples of 256: route ->
 // bucket (one workgroup: per-expert counts, a parallel scan, the lists of row groups of the
@@ -41,96 +42,9 @@ __device__ __forceinline__ double load_logit(const void *p, int64_t i) {
   else return static_cast<double>(load_elem<LDT>(p, i));
 }
 
-// Largest 64-bit value over the wave, on the VALU (DPP steps as in group_sum), in every lane.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  auto step = [&](auto ctrl, auto rows) {
-    constexpr int C = decltype(ctrl)::value, R = decltype(rows)::value;
-    const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
-    const uint32_t olo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(lo), C, R, 0xf, false));
-    const uint32_t ohi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(hi), C, R, 0xf, false));
-    const uint64_t o = (static_cast<uint64_t>(ohi) << 32) | olo;
-    v = o > v ? o : v;
-  };
-  step(std::integral_constant<int, DPP_QUAD_XOR1>{}, std::integral_constant<int, 0xf>{});
-  step(std::integral_constant<int, DPP_QUAD_XOR2>{}, std::integral_constant<int, 0xf>{});
-  step(std::integral_constant<int, DPP_HALF_MIRROR>{}, std::integral_constant<int, 0xf>{});
-  step(std::integral_constant<int, DPP_ROW_MIRROR>{}, std::integral_constant<int, 0xf>{});
-  step(std::integral_constant<int, DPP_BCAST15>{}, std::integral_constant<int, 0xa>{});
-  step(std::integral_constant<int, DPP_BCAST31>{}, std::integral_constant<int, 0x8>{});
-  // lane 63 holds the maximum
-  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), 63);
-  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(v >> 32), 63);
-  return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-
-// Router without a selection bias (the selection is then by logit): each candidate is one 64-bit
-// key, the order-preserving bits of its float32 logit above the complement of its expert id (so
-// equal logits prefer the lower id), and the wave maximum of the keys is taken on the VALU; the
-// double-precision sigmoid is evaluated only for the k winners, in selection order (the same
-// arithmetic as k_moe_route).
-template <int LDT, int PER>  // PER: experts per lane, E <= 64 PER
-__device__ __forceinline__ void route_keyed_n(const void *__restrict__ logits, int t, int E, int topk, double scale,
-                                              int *__restrict__ idx_out, float *__restrict__ w_out,
-                                              int *__restrict__ idx_copy) {
-  const int lane = threadIdx.x & 63;
-  uint64_t key[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int e = lane + 64 * i;
-    key[i] = 0;  // below every real key
-    if (e < E) {
-      uint32_t u = __float_as_uint(load_elem<LDT>(logits, static_cast<int64_t>(t) * E + e));
-      if (u == 0x80000000u) u = 0;  // -0 ties with +0
-      u ^= (u >> 31) ? 0xffffffffu : 0x80000000u;
-      key[i] = (static_cast<uint64_t>(u) << 32) | (0xffffffffu - static_cast<uint32_t>(e));
-    }
-  }
-  float my_l = 0.f;  // lane s keeps the logit of the s-th winner
-  for (int s = 0; s < topk; ++s) {
-    uint64_t bk = 0;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) bk = key[i] > bk ? key[i] : bk;
-    bk = wave_max_u64(bk);
-    const int be = static_cast<int>(0xffffffffu - static_cast<uint32_t>(bk));
-#pragma unroll
-    for (int i = 0; i < PER; ++i)
-      if (key[i] == bk) key[i] = 0;  // the owner retires the winner
-    const uint32_t hk = static_cast<uint32_t>(bk >> 32);  // the logit's bits, mapped back
-    if (lane == 0) {
-      idx_out[t * topk + s] = be;
-      if (idx_copy) idx_copy[t * topk + s] = be;
-    }
-    if (lane == s) my_l = __uint_as_float(hk ^ ((hk >> 31) ? 0x80000000u : 0xffffffffu));
-  }
-  // the k sigmoids in parallel (lane s: winner s), summed in selection order
-  const double my_sc = lane < topk ? 1.0 / (1.0 + exp(-static_cast<double>(my_l))) : 0.0;
-  double tot = 0.0;
-  for (int s = 0; s < topk; ++s) {
-    const uint64_t b = __double_as_longlong(my_sc);
-    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(b), s);
-    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(b >> 32), s);
-    tot += __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
-  }
-  if (lane < topk) w_out[t * topk + lane] = static_cast<float>(my_sc / (tot + 1e-20) * scale);
-}
-
-// the k selection rounds are serial: every key a lane scans is paid k times (E <= 1024)
-template <int LDT>
-__device__ __forceinline__ void route_keyed(const void *__restrict__ logits, int t, int E, int topk, double scale,
-                                            int *__restrict__ idx_out, float *__restrict__ w_out,
-                                            int *__restrict__ idx_copy) {
-  if (E <= 256) route_keyed_n<LDT, 4>(logits, t, E, topk, scale, idx_out, w_out, idx_copy);
-  else if (E <= 512) route_keyed_n<LDT, 8>(logits, t, E, topk, scale, idx_out, w_out, idx_copy);
-  else route_keyed_n<LDT, 16>(logits, t, E, topk, scale, idx_out, w_out, idx_copy);
-}
-
-template <int LDT>
-__global__ void __launch_bounds__(64) k_moe_route_logit(const void *__restrict__ logits, int E, int topk, double scale,
-                                                        int *__restrict__ idx_out, float *__restrict__ w_out) {
-  route_keyed<LDT>(logits, blockIdx.x, E, topk, scale, idx_out, w_out, nullptr);
-}
-
-// Smallest / largest 32-bit value over the wave (DPP steps as wave_max_u64), in every lane.
+// Smallest / largest 32-bit value over the wave, in every lane, on the VALU: DPP steps combine the
+// lanes of each quad, half-row and row, then rows 1 and 3 take rows 0 and 2 (row_bcast 15) and row
+// 3 takes rows 0-1 (row_bcast 31); lane 63 then holds the extreme, read back as a scalar.
 template <bool MAX>
 __device__ __forceinline__ uint32_t wave_ext_u32(uint32_t v) {
   auto step = [&](auto ctrl, auto rows) {
@@ -450,7 +364,7 @@ __global__ void __launch_bounds__(256) k_moe_bucket_tiles(const int *__restrict_
 
 // Few tokens: routing (wave w takes tokens w, w + 4, ...) and bucketing in one workgroup; the
 // routed ids also go to LDS, where the bucketing reads them.
-template <int LDT, bool KEYED>
+template <int LDT>
 __global__ void __launch_bounds__(256) k_moe_route_bucket(const void *__restrict__ logits, const float *__restrict__ bias,
                                                           int E, int topk, double scale, int *__restrict__ idx_out,
                                                           float *__restrict__ w_out, int T, int BMr, int BMr2,
@@ -459,12 +373,8 @@ __global__ void __launch_bounds__(256) k_moe_route_bucket(const void *__restrict
                                                           int4 *__restrict__ tiles2, int *__restrict__ ntiles2) {
   extern __shared__ int sh[];
   int *idx_lds = sh + 2 * E;  // [T * topk]
-  if constexpr (KEYED) {
-    for (int t = threadIdx.x >> 6; t < T; t += 4) route_keyed<LDT>(logits, t, E, topk, scale, idx_out, w_out, idx_lds);
-  } else {
-    __shared__ RouteLds L;
-    for (int t = 0; t < T; ++t) route_double_wg<LDT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds, L);
-  }
+  __shared__ RouteLds L;
+  for (int t = 0; t < T; ++t) route_double_wg<LDT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds, L);
   __syncthreads();
   bucket_tiles(idx_lds, T, topk, E, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2, sh);
 }
@@ -521,7 +431,7 @@ __device__ __forceinline__ void bucket_rows_wave(const int *idx_lds, int T, int 
 
 // Few tokens and at most 64 rows: routing (wave w takes tokens w, w + 4, ...), then the one-wave
 // bucketing above.
-template <int LDT, bool KEYED>
+template <int LDT>
 __global__ void __launch_bounds__(256) k_moe_route_bucket_w(const void *__restrict__ logits, const float *__restrict__ bias,
                                                             int E, int topk, double scale, int *__restrict__ idx_out,
                                                             float *__restrict__ w_out, int T, int BMr, int BMr2,
@@ -529,12 +439,8 @@ __global__ void __launch_bounds__(256) k_moe_route_bucket_w(const void *__restri
                                                             int4 *__restrict__ tiles, int *__restrict__ ntiles,
                                                             int4 *__restrict__ tiles2, int *__restrict__ ntiles2) {
   __shared__ int idx_lds[64];
-  if constexpr (KEYED) {
-    for (int t = threadIdx.x >> 6; t < T; t += 4) route_keyed<LDT>(logits, t, E, topk, scale, idx_out, w_out, idx_lds);
-  } else {
-    __shared__ RouteLds L;
-    for (int t = 0; t < T; ++t) route_double_wg<LDT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds, L);
-  }
+  __shared__ RouteLds L;
+  for (int t = 0; t < T; ++t) route_double_wg<LDT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds, L);
   __syncthreads();
   if (threadIdx.x < 64) bucket_rows_wave(idx_lds, T, topk, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2);
 }
@@ -609,17 +515,10 @@ extern "C" int64_t vybdq_moe_workspace_size(int64_t T, int64_t H, int64_t I, int
 // their own value, with the same ties-to-the-lower-id rule).
 static int launch_route(const void *lg, int logits_dt, const float *bias, int64_t T, int64_t E, int64_t topk,
                         double scale, int *idx, float *w, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(T)), block(64), block_wg(256);
+  const dim3 grid(static_cast<unsigned>(T)), block(256);
   const int e = static_cast<int>(E), k = static_cast<int>(topk);
-  if (logits_dt == VYBDQ_F64) {
-    hipLaunchKernelGGL((k_moe_route<VYBDQ_F64>), grid, block_wg, 0, s, lg, bias, e, k, scale, idx, w);
-  } else if (!bias) {
-    VYBDQ_DISPATCH_IN(logits_dt, LDT,
-        hipLaunchKernelGGL((k_moe_route_logit<LDT>), grid, block, 0, s, lg, e, k, scale, idx, w));
-  } else {
-    VYBDQ_DISPATCH_IN(logits_dt, LDT,
-        hipLaunchKernelGGL((k_moe_route<LDT>), grid, block_wg, 0, s, lg, bias, e, k, scale, idx, w));
-  }
+  if (logits_dt == VYBDQ_F64) hipLaunchKernelGGL((k_moe_route<VYBDQ_F64>), grid, block, 0, s, lg, bias, e, k, scale, idx, w);
+  else VYBDQ_DISPATCH_IN(logits_dt, LDT, hipLaunchKernelGGL((k_moe_route<LDT>), grid, block, 0, s, lg, bias, e, k, scale, idx, w));
   return check_launch("moe route");
 }
 
@@ -637,18 +536,17 @@ int moe_route_bucket(const void *logits, int logits_dt, const float *bias, int64
   if (T <= 8) {
     const bool wave_rows = T * topk <= 64;
     const size_t shb = static_cast<size_t>(2 * E + T * topk) * 4;
-#define RB(LDT, KEYED)                                                                                          \
+#define RB(LDT)                                                                                          \
   do {                                                                                                        \
     if (wave_rows)                                                                                            \
-      hipLaunchKernelGGL((k_moe_route_bucket_w<LDT, KEYED>), dim3(1), dim3(256), 0, s, logits, bias, e, k, scale, \
+      hipLaunchKernelGGL((k_moe_route_bucket_w<LDT>), dim3(1), dim3(256), 0, s, logits, bias, e, k, scale, \
                          idx, w, tt, BMr, BMr, 0, pos, row_map, tiles, ntiles, tiles2, ntiles2);               \
     else                                                                                                      \
-      hipLaunchKernelGGL((k_moe_route_bucket<LDT, KEYED>), dim3(1), dim3(256), shb, s, logits, bias, e, k, scale, \
+      hipLaunchKernelGGL((k_moe_route_bucket<LDT>), dim3(1), dim3(256), shb, s, logits, bias, e, k, scale, \
                          idx, w, tt, BMr, BMr, 0, pos, row_map, tiles, ntiles, tiles2, ntiles2);               \
   } while (0)
-    if (logits_dt == VYBDQ_F64) RB(VYBDQ_F64, false);
-    else if (bias) { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT, false)); }
-    else { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT, true)); }
+    if (logits_dt == VYBDQ_F64) RB(VYBDQ_F64);
+    else { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT)); }
 #undef RB
     return check_launch("moe route + bucket");
   }
@@ -741,18 +639,17 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       int *n2 = gv ? m.ntiles2 : nullptr;
       // at most 64 rows: the one-wave bucketing (no LDS counts, scans or barriers)
       const bool wave_rows = T * topk <= 64;
-#define RB(LDT, KEYED)                                                                                          \
+#define RB(LDT)                                                                                          \
   do {                                                                                                        \
     if (wave_rows)                                                                                            \
-      hipLaunchKernelGGL((k_moe_route_bucket_w<LDT, KEYED>), dim3(1), dim3(256), 0, s, lg, bs, e, k, scale, idx, \
+      hipLaunchKernelGGL((k_moe_route_bucket_w<LDT>), dim3(1), dim3(256), 0, s, lg, bs, e, k, scale, idx, \
                          wts, tt, BMr, mc, shared ? 1 : 0, m.pos, m.row_map, m.tiles, m.ntiles, t2, n2);       \
     else                                                                                                      \
-      hipLaunchKernelGGL((k_moe_route_bucket<LDT, KEYED>), dim3(1), dim3(256), shb, s, lg, bs, e, k, scale, idx, \
+      hipLaunchKernelGGL((k_moe_route_bucket<LDT>), dim3(1), dim3(256), shb, s, lg, bs, e, k, scale, idx, \
                          wts, tt, BMr, mc, shared ? 1 : 0, m.pos, m.row_map, m.tiles, m.ntiles, t2, n2);       \
   } while (0)
-      if (logits_dt == VYBDQ_F64) RB(VYBDQ_F64, false);
-      else if (bs) { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT, false)); }
-      else { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT, true)); }
+      if (logits_dt == VYBDQ_F64) RB(VYBDQ_F64);
+      else { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT)); }
 #undef RB
       rc = check_launch("moe route + bucket");
     } else {
