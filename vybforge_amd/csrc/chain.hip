@@ -153,7 +153,21 @@ __global__ void __launch_bounds__(NT) k_pb_gemv(const int64_t *__restrict__ pb, 
       return p < P ? p : (ks < P ? ks : 0);
     };
 
-    // 1. the first batch of this wave's first tile
+    // a workgroup without a tile (the grid is sized for the largest stage) is done: it stages no x
+    if (valid && static_cast<int64_t>(blockIdx.x) * (NT / 64) >= tiles) return;
+
+    // 1. the first x chunks (the block's x is f32: 8 dwords per 8 elements), five per thread,
+    // before any weight load: loads return in order, so the x stage below waits for x alone
+    constexpr int XC = 5;
+    const int nchunk = valid ? 8 * P : 0;
+    uint32_t xr[XC][8];
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+      const int c = threadIdx.x + NT * j;
+      if (c < nchunk) load_x_chunk<8>(st.X, 8 * static_cast<int64_t>(c), xr[j]);
+    }
+
+    // 2. the first batch of this wave's first tile
     int64_t t = gw;
     uint32_t dw[U][PD];
     {
@@ -165,9 +179,14 @@ __global__ void __launch_bounds__(NT) k_pb_gemv(const int64_t *__restrict__ pb, 
       }
     }
 
-    // 2. stage x into LDS; IQ2_S: then its grid tables behind the block sums, where the unit dot of
-    // this stage's P reads them
+    // 3. stage x into LDS (the rest of its chunks loaded as they are staged); IQ2_S: then its grid
+    // tables behind the block sums, where the unit dot of this stage's P reads them
     if (valid) {
+#pragma unroll
+      for (int j = 0; j < XC; ++j) {
+        const int c = threadIdx.x + NT * j;
+        if (c < nchunk) stage_chunk<8>(xr[j], VYBDQ_F32, c, lds, sx);
+      }
       if constexpr (FMT == FMT_IQ2_S) {
         u4 *gridh = iq2s_lds_grid(sx, 1, P);
         for (int i0 = threadIdx.x; i0 < 1024 + 256; i0 += 5 * NT) {  // five 16-B loads in flight per thread
@@ -180,22 +199,15 @@ __global__ void __launch_bounds__(NT) k_pb_gemv(const int64_t *__restrict__ pb, 
             if (i0 + u * NT < 1024 + 256) gridh[i0 + u * NT] = v[u];
         }
       }
-      const int nchunk = 8 * P;
-      for (int c = threadIdx.x; c < nchunk; c += NT) {
-        if (st.xdt == VYBDQ_F32) {
-          uint32_t r[8];
-          load_x_chunk<8>(st.X, 8 * static_cast<int64_t>(c), r);
-          stage_chunk<8>(r, st.xdt, c, lds, sx);
-        } else {
-          uint32_t r[4];
-          load_x_chunk<4>(st.X, 8 * static_cast<int64_t>(c), r);
-          stage_chunk<4>(r, st.xdt, c, lds, sx);
-        }
+      for (int c = threadIdx.x + NT * XC; c < nchunk; c += NT) {
+        uint32_t r[8];
+        load_x_chunk<8>(st.X, 8 * static_cast<int64_t>(c), r);
+        stage_chunk<8>(r, VYBDQ_F32, c, lds, sx);
       }
     }
     __syncthreads();
 
-    // 3. tiles of this wave
+    // 4. tiles of this wave
     if (valid) {
       bool first = true;
       for (; t < tiles; t += nwaves) {
