@@ -311,34 +311,39 @@ __global__ void __launch_bounds__(256) k_exl3_gemm(const uint16_t *__restrict__ 
       }
       return;
     }
-    _Float16 v[32];
-    lane_decode(w, v);
     if constexpr (MMA) {
-      // v[i] = W[16 kk + i][c0], v[16 + i] = W[16 kk + i][c0 + 8]: into k half (kk & 1) of the tile
+      // The 32 slot words of this k-block as they are: word q holds the two fp16 halves of value q
+      // (their sum is the value), q < 16 column c0 at k = 16 kk + q, q >= 16 column c0 + 8. Column
+      // c's 16 words in k order make the tile row [c][k' = 2 k + h], and the MFMA with each x'
+      // value twice in A adds x lo + x hi in float32: no fp16 add or packing of decoded values.
       const int c0 = 16 * t + j;
-      const int half = kk & 1;
-      uint32_t pk[16];
+      uint32_t hw[32];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) pk[i] = __builtin_bit_cast(uint32_t, h2{v[2 * i], v[2 * i + 1]});
-      u4 *d0 = reinterpret_cast<u4 *>(wt + c0 * kExl3WtStride + 32 * half);
-      u4 *d1 = reinterpret_cast<u4 *>(wt + (c0 + 8) * kExl3WtStride + 32 * half);
-      d0[0] = u4{pk[0], pk[1], pk[2], pk[3]};
-      d0[1] = u4{pk[4], pk[5], pk[6], pk[7]};
-      d1[0] = u4{pk[8], pk[9], pk[10], pk[11]};
-      d1[1] = u4{pk[12], pk[13], pk[14], pk[15]};
-      if (half == 1) {
-        // k-blocks kk - 1 and kk complete: A = x'[m][16 (kk - 1) + 8 g .. + 8], B = the tile
-        const int m = lane & 15, gk = lane >> 4;
-        h8 a = h8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (m < BP) a = *reinterpret_cast<const h8 *>(xs + m * xstride + 16 * (kk - 1) + 8 * gk);
+      for (int q = 0; q < 32; ++q) hw[q] = slot_halves(w, q);
+      u4 *d0 = reinterpret_cast<u4 *>(wt + c0 * kExl3WtStride);
+      u4 *d1 = reinterpret_cast<u4 *>(wt + (c0 + 8) * kExl3WtStride);
 #pragma unroll
-        for (int f = 0; f < 8; ++f) {
-          const h8 b = *reinterpret_cast<const h8 *>(wt + (16 * f + m) * kExl3WtStride + 16 * gk);
-          accm[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, accm[f], 0, 0, 0);
-        }
+      for (int i = 0; i < 4; ++i) {
+        d0[i] = u4{hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]};
+        d1[i] = u4{hw[16 + 4 * i], hw[16 + 4 * i + 1], hw[16 + 4 * i + 2], hw[16 + 4 * i + 3]};
+      }
+      // A = x'[m][16 kk + 4 g .. + 4], each value twice (k' = 8 g .. + 8); B = the tile
+      const int m = lane & 15, gk = lane >> 4;
+      u2 xv = u2{0u, 0u};
+      if (m < BP) xv = *reinterpret_cast<const u2 *>(xs + m * xstride + 16 * kk + 4 * gk);
+      const h8 a = __builtin_bit_cast(h8, u4{__builtin_amdgcn_perm(xv[0], xv[0], 0x01000100u),
+                                             __builtin_amdgcn_perm(xv[0], xv[0], 0x03020302u),
+                                             __builtin_amdgcn_perm(xv[1], xv[1], 0x01000100u),
+                                             __builtin_amdgcn_perm(xv[1], xv[1], 0x03020302u)});
+#pragma unroll
+      for (int f = 0; f < 8; ++f) {
+        const h8 b = *reinterpret_cast<const h8 *>(wt + (16 * f + m) * kExl3WtStride + 16 * gk);
+        accm[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, accm[f], 0, 0, 0);
       }
       return;
     }
+    _Float16 v[32];
+    lane_decode(w, v);
     h2 pj[8], pj8[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {

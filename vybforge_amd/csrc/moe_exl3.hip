@@ -374,26 +374,25 @@ __global__ void __launch_bounds__(256) k_mx_gemm(const MxGemmArgs a, const MxSha
       if (i < nc) xv4[u] = x_chunk(i);
     }
   }
-  // larger groups: the matrix-core A fragment of k-blocks (kk, kk + 1), kk even: x' row lane & 15
-  // (zero past the group), k offset 8 (lane >> 4), read from the workspace (L2) one group of kD
-  // k-blocks ahead, beside the trellis ring
+  // larger groups: the matrix-core A values of k-block kk: x' row lane & 15 (zero past the group),
+  // k offset 4 (lane >> 4), four fp16 read from the workspace (L2) one group of kD k-blocks ahead,
+  // beside the trellis ring (each is used twice in the A fragment, see step)
   const int am = lane & 15;
-  const _Float16 *arow = xsrc + static_cast<int64_t>(am < B ? am : 0) * K + 8 * (lane >> 4);
+  const _Float16 *arow = xsrc + static_cast<int64_t>(am < B ? am : 0) * K + 4 * (lane >> 4);
   auto load_a = [&](int kk) {
-    h8 v = h8{0, 0, 0, 0, 0, 0, 0, 0};
+    u2 v = u2{0u, 0u};
     const int kc = kk < w_end ? kk : w_begin;
-    if (am < B) v = *reinterpret_cast<const h8 *>(arow + 16 * kc);
+    if (am < B) v = *reinterpret_cast<const u2 *>(arow + 16 * kc);
     return v;
   };
   __builtin_amdgcn_sched_barrier(0);
   u4 ring[kD];
-  h8 aring[HALVES ? 1 : kD / 2];
-  if constexpr (HALVES) aring[0] = h8{0, 0, 0, 0, 0, 0, 0, 0};
+  u2 aring[HALVES ? 1 : kD];
+  if constexpr (HALVES) aring[0] = u2{0u, 0u};
 #pragma unroll
   for (int d = 0; d < kD; ++d) {
     ring[d] = load_chunk(w_begin + d);
-    if constexpr (!HALVES)
-      if ((d & 1) == 0) aring[d >> 1] = load_a(w_begin + d);
+    if constexpr (!HALVES) aring[d] = load_a(w_begin + d);
   }
   if constexpr (HALVES) {
     for (int i0 = threadIdx.x;;) {
@@ -416,7 +415,7 @@ __global__ void __launch_bounds__(256) k_mx_gemm(const MxGemmArgs a, const MxSha
 #pragma unroll
   for (int f = 0; f < (HALVES ? 1 : 8); ++f) accm[f] = f4{0.f, 0.f, 0.f, 0.f};
   char *wt = smem + static_cast<size_t>(wave) * kExl3WtBytes;
-  auto step = [&](int kk, const u4 c, const h8 av) {
+  auto step = [&](int kk, const u4 c, const u2 av) {
     uint32_t w[6];
     chunk_window(c, w);
     if constexpr (HALVES) {
@@ -441,46 +440,47 @@ __global__ void __launch_bounds__(256) k_mx_gemm(const MxGemmArgs a, const MxSha
           acc[b][q >> 4] = __builtin_amdgcn_fdot2(y, __builtin_bit_cast(h2, xq[b][q & 15]), acc[b][q >> 4], false);
       }
     } else {
-      _Float16 v[32];
-      lane_decode(w, v);
-      // v[i] = What[16 kk + i][c0], v[16 + i] = What[16 kk + i][c0 + 8]: into k half (kk & 1) of the tile
+      // the 32 slot words as they are (two fp16 halves per value, whose sum is the value): column
+      // c's 16 words in k order are the tile row [c][k' = 2 k + h], and the MFMA with each x'
+      // value twice in A adds x lo + x hi in float32 (as the k_exl3_gemm matrix-core path)
       const int c0 = 16 * t + j;
-      const int half = kk & 1;
-      uint32_t pk[16];
+      uint32_t hw[32];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) pk[i] = __builtin_bit_cast(uint32_t, h2{v[2 * i], v[2 * i + 1]});
-      u4 *d0 = reinterpret_cast<u4 *>(wt + c0 * kExl3WtStride + 32 * half);
-      u4 *d1 = reinterpret_cast<u4 *>(wt + (c0 + 8) * kExl3WtStride + 32 * half);
-      d0[0] = u4{pk[0], pk[1], pk[2], pk[3]};
-      d0[1] = u4{pk[4], pk[5], pk[6], pk[7]};
-      d1[0] = u4{pk[8], pk[9], pk[10], pk[11]};
-      d1[1] = u4{pk[12], pk[13], pk[14], pk[15]};
-      if (half == 1) {
-        const int gk = lane >> 4;
+      for (int q = 0; q < 32; ++q) hw[q] = slot_halves(w, q);
+      u4 *d0 = reinterpret_cast<u4 *>(wt + c0 * kExl3WtStride);
+      u4 *d1 = reinterpret_cast<u4 *>(wt + (c0 + 8) * kExl3WtStride);
 #pragma unroll
-        for (int f = 0; f < 8; ++f) {
-          const h8 bw = *reinterpret_cast<const h8 *>(wt + (16 * f + am) * kExl3WtStride + 16 * gk);
-          accm[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bw, accm[f], 0, 0, 0);
-        }
+      for (int i = 0; i < 4; ++i) {
+        d0[i] = u4{hw[4 * i], hw[4 * i + 1], hw[4 * i + 2], hw[4 * i + 3]};
+        d1[i] = u4{hw[16 + 4 * i], hw[16 + 4 * i + 1], hw[16 + 4 * i + 2], hw[16 + 4 * i + 3]};
+      }
+      const h8 a = __builtin_bit_cast(h8, u4{__builtin_amdgcn_perm(av[0], av[0], 0x01000100u),
+                                             __builtin_amdgcn_perm(av[0], av[0], 0x03020302u),
+                                             __builtin_amdgcn_perm(av[1], av[1], 0x01000100u),
+                                             __builtin_amdgcn_perm(av[1], av[1], 0x03020302u)});
+      const int gk = lane >> 4;
+#pragma unroll
+      for (int f = 0; f < 8; ++f) {
+        const h8 bw = *reinterpret_cast<const h8 *>(wt + (16 * f + am) * kExl3WtStride + 16 * gk);
+        accm[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bw, accm[f], 0, 0, 0);
       }
     }
   };
-  // Whole groups of kD k-blocks, each ring slot refilled right after the step that consumed it
-  // (the A fragment of a pair after the pair's second step); the last blocks are in the ring.
+  // Whole groups of kD k-blocks, each ring slot (trellis chunk and A values) refilled right after the
+  // step that consumed it; the last blocks are in the ring.
   int k0 = w_begin;
   for (; k0 + kD <= w_end; k0 += kD) {
 #pragma unroll
     for (int d = 0; d < kD; ++d) {
-      step(k0 + d, ring[d], aring[HALVES ? 0 : d >> 1]);
+      step(k0 + d, ring[d], aring[HALVES ? 0 : d]);
       ring[d] = load_chunk(k0 + d + kD);
-      if constexpr (!HALVES)
-        if (d & 1) aring[d >> 1] = load_a(k0 + d - 1 + kD);
+      if constexpr (!HALVES) aring[d] = load_a(k0 + d + kD);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 #pragma unroll
   for (int d = 0; d < kD - 1; ++d)
-    if (k0 + d < w_end) step(k0 + d, ring[d], aring[HALVES ? 0 : d >> 1]);
+    if (k0 + d < w_end) step(k0 + d, ring[d], aring[HALVES ? 0 : d]);
 
   // reduce the 4 waves (same columns, different k) in a fixed order, then this split's partial
   __syncthreads();
