@@ -957,7 +957,8 @@ def exl3_map_file():
 
 def run_pblock(args, torch, dev):
     """vybdq_launch_pblock on the reference's parameter blocks beside the direct entry points, at the
-    q4_0 GEMV 9728x2560 (f32 x, 24 rotated weight copies) and the Q8_0 prefill GEMMs M=512 (f32 X,
+    q4_0 GEMV 9728x2560 (f32 x, 24 rotated weight copies), the four launches of the Qwen3-4B decode
+    stack (f32 x, rotated copies over 256 MB each) and the Q8_0 prefill GEMMs M=512 (f32 X,
     3 rotated copies of each shape, no workspace); then the MoE fixture block at S=16 and the fused
     EXL3 decode + column transform at 2048x4096, which have no direct counterpart."""
     import numpy as np
@@ -985,6 +986,32 @@ def run_pblock(args, torch, dev):
                                       direct_GBs=round(b / (ms_d / 24 * 1e-3) / 1e9, 1),
                                       pblock_GBs=round(b / (ms_p / 24 * 1e-3) / 1e9, 1))
     del copies, pbs
+    # the four launches of the Qwen3-4B decode stack (q|k|v, o, gate|up, down), f32 x, rotated copies
+    # of each (> 256 MB per shape)
+    H, Q, KV, I = QWEN3_4B["hidden"], QWEN3_4B["q"], QWEN3_4B["kv"], QWEN3_4B["inter"]
+    for name, Kk, Ns in (("qkv", H, (Q, KV, KV)), ("o", Q, (H,)), ("gate_up", H, (I, I)), ("down", I, (H,))):
+        nb = sum(Ns) * Kk // 32 * 18
+        nc = (300 << 20) // nb + 1
+        xs = torch.randn(Kk, generator=gen, device=dev)
+        ys = [torch.empty(n, device=dev) for n in Ns]
+        sets = [[synth.q4_0_weights_torch(gen, n, Kk, dev) for n in Ns] for _ in range(nc)]
+        blocks = []
+        for Ws in sets:
+            w = np.zeros(32, np.int64)
+            w[1], w[3], w[5] = xs.data_ptr(), 1, Kk
+            for i, (slot_w, slot_y, slot_n, slot_e) in enumerate(((0, 2, 4, 6), (7, 9, 8, 10), (11, 13, 12, 14))):
+                if i < len(Ns):
+                    w[slot_w], w[slot_y], w[slot_n], w[slot_e] = Ws[i].data_ptr(), ys[i].data_ptr(), Ns[i], 4
+                else:
+                    w[slot_e] = 8
+            blocks.append(torch.from_numpy(w).to(dev))
+        ms_d, _ = timed_graph(torch, [lambda Ws=Ws: ops.gemv_seg3(ops.GGML_Q4_0, xs, Kk, list(zip(Ws, ys, Ns)))
+                                      for Ws in sets], args.steps, args.warmup)
+        ms_p, _ = timed_graph(torch, [lambda pb=pb: _lib.call("vybdq_launch_pblock", _lib.PB_GEMV + 2, pb.data_ptr(),
+                                                                 stream()) for pb in blocks], args.steps, args.warmup)
+        out[f"gemv_stack_{name}"] = dict(direct_us=round(ms_d * 1e3 / nc, 3), pblock_us=round(ms_p * 1e3 / nc, 3),
+                                         ratio=round(ms_p / ms_d, 3))
+        del sets, blocks
     M = 512
     direct, pblk, flops = [], [], 0
     keep = []
