@@ -57,6 +57,28 @@ __device__ __forceinline__ const T *mx_ptr(const uint64_t *tab, int e, int p, in
 
 __device__ __forceinline__ float mx_silu(float g) { return g / (1.0f + __expf(-g)); }
 
+// mx_sum_splits of two pairs (a and b, the same splits), their loads in the same groups
+__device__ __forceinline__ void mx_sum_splits2(const float *a, const float *b, int64_t stride, int S, f2 &sa, f2 &sb) {
+  sa = sb = f2{0.f, 0.f};
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    f2 va[8], vb[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t o = static_cast<int64_t>(s0 + u) * stride;
+      va[u] = s0 + u < S ? *reinterpret_cast<const f2 *>(a + o) : f2{0.f, 0.f};
+      vb[u] = s0 + u < S ? *reinterpret_cast<const f2 *>(b + o) : f2{0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < S) {
+        sa[0] += va[u][0];
+        sa[1] += va[u][1];
+        sb[0] += vb[u][0];
+        sb[1] += vb[u][1];
+      }
+  }
+}
+
 // sum over s < S of the float pair at base + s * stride, added in split order: loads in groups of 8
 // independent 8-byte loads (one round trip per group; a loop that adds each load as it arrives
 // waits S round trips)
@@ -552,8 +574,8 @@ __global__ void __launch_bounds__(64 * kMxRowWaves) k_mx_mid(const uint64_t *__r
     if (c < nch) {
       const int64_t n0 = 128 * static_cast<int64_t>(c) + 2 * lane;
       const float *zr = zpart + static_cast<int64_t>(r) * (2 * I) + n0;
-      const f2 gs = mx_sum_splits(zr, static_cast<int64_t>(rows) * (2 * I), S);
-      const f2 us = mx_sum_splits(zr + I, static_cast<int64_t>(rows) * (2 * I), S);
+      f2 gs, us;
+      mx_sum_splits2(zr, zr + I, static_cast<int64_t>(rows) * (2 * I), S, gs, us);
       float g0 = gs[0], g1 = gs[1], u0 = us[0], u1 = us[1];
       g0 *= sg;
       g1 *= sg;
