@@ -823,7 +823,8 @@ def run_moe(args, torch, dev, tokens=None, built=None):
             rels.append(check_moe(torch, layers[r], xs[r], lgs[r], outs[r], routed[r][1], routed[r][2]))
         check = dict(ok=True, rel=max(rels), what="routing of every token; 2 tokens x 256 columns vs float64 oracle; "
                                                   "graph replay == eager")
-    path = "k_moe_gemv" if T <= 64 else "k_moe_mm"
+    # q4_0 experts: the grouped GEMV at one token, the LDS-staged grouped MFMA GEMM above
+    path = "k_moe_gemv" if T <= 1 else "k_moe_mm_lds"
     roofline = hbm_roofline(gbs, f"MoE layer: route+bucket, {path} gate|up+SwiGLU and down, combine",
                             "algorithmic bytes (hit experts + shared + activations) / event time",
                             avg_layer_us=round(ms * 1e3 / R, 3), bytes_per_layer=nbytes // R)
