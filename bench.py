@@ -1064,6 +1064,31 @@ def run_pblock(args, torch, dev):
     out["exl3dq_2048x4096"] = dict(us=round(ms_x * 1e3, 2),
                                    tflops=round(2 * rows * cw * 128 / (ms_x * 1e-3) / 1e12, 1),
                                    out_GBs=round(rows * cw * 4 / (ms_x * 1e-3) / 1e9, 1))
+    # the other stages of the reference's f32 reconstruction at the same shape: exl3deq32 (map
+    # decode), exl3had132, exl3had232 (with suh / svh), exl3cvt32, and the exl3_deq32 chain
+    # dq1s -> had232 -> cvt32 as one graph
+    nbc, nblocks = cw // 128, rows // 128 * (cw // 128)
+    su = torch.ones(rows, dtype=torch.float16, device=dev)
+    sv = torch.ones(cw, dtype=torch.float16, device=dev)
+    od = torch.empty(rows * cw, device=dev)
+    fd = torch.empty(rows * cw, device=dev)
+    f64 = torch.empty(rows * cw, dtype=torch.float64, device=dev)
+    i64 = lambda ws: torch.tensor([int(w) for w in ws], dtype=torch.int64, device=dev)
+    p1 = i64([od.data_ptr(), T.data_ptr(), Hm.data_ptr(), cw, nbc, nblocks])
+    p2 = i64([T.data_ptr(), fd.data_ptr(), Hm.data_ptr(), su.data_ptr(), sv.data_ptr(), cw, nbc, nblocks])
+    p3 = i64([fd.data_ptr(), f64.data_ptr(), rows * cw])
+    deq = lambda: _lib.call("vybdq_exl3_deq_map", q.data_ptr(), td.data_ptr(), od.data_ptr(), _lib.F32, stream())
+    had1 = lambda: _lib.call("vybdq_launch_pblock", _lib.PB_EXL3HAD132, p1.data_ptr(), stream())
+    had2 = lambda: _lib.call("vybdq_launch_pblock", _lib.PB_EXL3HAD232, p2.data_ptr(), stream())
+    cvt = lambda: _lib.call("vybdq_launch_pblock", _lib.PB_EXL3CVT32, p3.data_ptr(), stream())
+    dq1s = lambda: _lib.call("vybdq_launch_pblock_grid", _lib.PB_EXL3DQ, xpb.data_ptr(), rows * cw // 256, 256, stream())
+    stages = {}
+    for name, fns in [("deq32", [deq]), ("had132", [had1]), ("had232", [had2]), ("cvt32", [cvt]),
+                      ("chain_dq1s_had232_cvt32", [dq1s, had2, cvt])]:
+        ms_s, _ = timed_graph(torch, fns, args.steps, args.warmup)
+        stages[name + "_us"] = round(ms_s * 1e3, 2)
+    out["exl3_stages_2048x4096"] = stages
+    del od, fd, f64
     if _lib.lib.vybdq_pblock_status() != 0:
         raise CheckFailed("a p-block launch reported: " + _lib.last_error())
     ratio = out["gemv_q4_0_9728x2560"]["direct_us"] / out["gemv_q4_0_9728x2560"]["pblock_us"]

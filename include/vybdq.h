@@ -380,6 +380,13 @@ int vybdq_gemm_q8_0_i8(uint64_t W, uint64_t Xq, uint64_t Xs, uint64_t Y, int64_t
 #define VYBDQ_PB_MOE 0x400      /* moe_route + moe_act + moe_down block (native/kernels/moe.vyb) */
 #define VYBDQ_PB_EXL3DQ 0x500   /* exl3dq1 / exl3dq1s block (exl3.vyb, exl3dq.vyb); needs the grid */
 #define VYBDQ_PB_EXL3INV 0x600  /* exl3inv block (exl3.vyb) */
+#define VYBDQ_PB_EXL3HGEN 0x700    /* exl3hgen block (exl3.vyb:36-56): H float64 */
+#define VYBDQ_PB_EXL3HGEN32 0x701  /* exl3hgen32 block (exl3.vyb:124-145): H float32 */
+#define VYBDQ_PB_EXL3HAD1 0x800    /* exl3had1 block (exl3.vyb:58-86): column transform, float64 */
+#define VYBDQ_PB_EXL3HAD132 0x801  /* exl3had132 block (exl3.vyb:147-172): column transform, float32 */
+#define VYBDQ_PB_EXL3HAD2 0x900    /* exl3had2 block (exl3.vyb:88-118): row transform + scales, float64 */
+#define VYBDQ_PB_EXL3HAD232 0x901  /* exl3had232 block (exl3.vyb:174-202): row transform + scales, float32 */
+#define VYBDQ_PB_EXL3CVT32 0xA00   /* exl3cvt32 block (exl3.vyb:247-256): float32 -> float64 */
 
 /* Launch one GEMV or prefill GEMM described by a reference parameter block at device address P
    (8-byte aligned): little-endian int64 words, each read by the kernel when the launch runs (the
@@ -403,6 +410,19 @@ int vybdq_gemm_q8_0_i8(uint64_t W, uint64_t Xq, uint64_t Xs, uint64_t Y, int64_t
      AC [S][9][2048] and out [S][4096]; y, G, AC 16-byte and the other buffers 4-byte aligned.
    VYBDQ_PB_EXL3INV, exl3.vyb:318-333: td@0 nbody@8; writes the inverse tile map
      (u32 [256] at td + 16 + nbody).
+   The stages of the reference's separate EXL3 reconstruction (glm_engine.vyb:1103-1200,
+   native/host/glm_exl3_check32.vyb:150-240), T = float64 for HGEN / HAD1 / HAD2 and float32 for
+   the *32 kinds; every buffer 16-byte aligned except suh / svh (2-byte):
+   VYBDQ_PB_EXL3HGEN / HGEN32: H@0; writes H T [128][128] = (-1)^popcount(i & j) *
+     T(0.08838834764831845).
+   VYBDQ_PB_EXL3HAD1 / HAD132: W@0 Tmp@8 H@16 cw@24 nbc@32 nblocks@40; for each block
+     = kb nbc + nb < nblocks: Tmp[block][b][d] = sum over c ascending of
+     W[(128 kb + b) cw + 128 nb + c] H[c][d] (fma chain); nbc >= 1, cw >= 128 nbc, cw a multiple
+     of 4 (float32) or 2 (float64).
+   VYBDQ_PB_EXL3HAD2 / HAD232: Tmp@0 O@8 H@16 suh@24 svh@32 cw@40 nbc@48 nblocks@56;
+     O[(128 kb + a) cw + 128 nb + d] = (sum over b ascending of H[a][b] Tmp[block][b][d])
+     * T(suh[128 kb + a]) * T(svh[128 nb + d]) (suh, svh fp16).
+   VYBDQ_PB_EXL3CVT32: S@0 D@8 n@16; D float64 [n] = S float32 [n] (S 4-, D 8-byte aligned).
    A block whose words violate these is not computed (nothing is written) and the next
    vybdq_pblock_status() on the device reports it; the call itself only checks kind and P. */
 int vybdq_launch_pblock(int kind, uint64_t P, uint64_t stream);
@@ -420,6 +440,17 @@ int vybdq_launch_pblock_grid(int kind, uint64_t P, uint32_t grid_x, uint32_t blo
 /* Synchronises the current device, then returns 0 or the error of an invalid parameter block
    launched on it since the previous call (and clears it). */
 int vybdq_pblock_status(void);
+
+/* Map-driven EXL3 tile decode, launched as the reference launches exl3deq(q, tab, o) (out_dt
+   VYBDQ_F64, exl3.vyb:375-422) and exl3deq32(q, tab, o) (VYBDQ_F32, exl3.vyb:207-242) with grid
+   ntiles x 256 (native/host/glm_exl3_check32.vyb:165). tab (8-byte aligned): cw@0, ntiles@8, then
+   the 256 x 16-byte map body (4 u16 nibble indices, 4 u8 bit positions, u16 row, u16 col per
+   slot). Slot s of tile t: w16 = OR_i nibble(t, nidx_i) << 4 pos_i, y = (w16 * 0xCBAC1FED mod 2^32
+   & 0x8FFF8FFF) ^ 0x3B603B60, o[(16 (t / (cw / 16)) + row_s) cw + 16 (t % (cw / 16)) + col_s] =
+   fp16(y.lo) + fp16(y.hi) (exact in float32). cw and ntiles are read on the device (the call
+   can be captured); a header or map entry out of range (cw % 16, nibble index >= 256, position
+   >= 4, row or col >= 16) writes nothing and is reported by the next vybdq_pblock_status(). */
+int vybdq_exl3_deq_map(uint64_t q, uint64_t tab, uint64_t out, int out_dt, uint64_t stream);
 
 /* ---- MoE layer ---------------------------------------------------------------------------- */
 

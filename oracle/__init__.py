@@ -17,7 +17,8 @@ repository root):
            xq8 quantizer    native/kernels/rgemv7.vyb:195-214
   exl3     mcg decode, slot map, Hadamard-128, full dequant
                             native/exl3/exl3_ref.py:31-120, native/exl3/README.md:24-49,
-                            native/kernels/exl3.vyb:375-422
+                            native/kernels/exl3.vyb:375-422; the f64 / f32 pipeline stages
+                            exl3hgen, exl3had1, exl3had2, exl3deq32 (exl3.vyb:36-242)
   moe      route / clamped SwiGLU / combine
                             native/glm53/moe_ref.py:25-112, native/kernels/moe.vyb:1-170
   matmul   fp64 GEMV/GEMM gates and the tolerance metric
@@ -37,6 +38,9 @@ Pinning (what checks each function, all under tests/):
                    any other codebook id raises ValueError.              -> pinned (KAT above)
   exl3 dequant     closed form of the all-zero trellis after the Hadamard sandwich,
                    H orthogonality, per-block linearity.                 -> pinned
+  exl3 stages      map_deq equals the pinned map decode; hgen equals the scaled Sylvester
+                   matrix; had1 equals the pinned column transform; had2 after had1 equals
+                   the pinned block rotation.                            -> pinned
   moe              the reference's committed MoE goldens (routing ids/weights, and the
                    block output on a column slice).                      -> pinned
   matmul           fp64 numpy matmul (invariant).                        -> pinned

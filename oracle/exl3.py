@@ -121,6 +121,73 @@ def column_transform_f64(what, H):
     return out
 
 
+def map_deq(q, body, cw, ntiles):
+    """exl3deq / exl3deq32 (exl3.vyb:375-422, 207-242): slot s of tile t composes its window from
+    the four (nibble index, bit position) pairs of map record s and lands at the record's (row, col)
+    inside tile t = (t / (cw / 16), t % (cw / 16)); float32 [ntiles / (cw / 16) 16, cw] (the value
+    is the exact half sum, the same in float32 and float64). ntiles must fill whole 16-row bands."""
+    nbc = cw // 16
+    if ntiles % nbc:
+        raise ValueError("ntiles must be a multiple of cw / 16")
+    q = np.frombuffer(q, np.uint8).reshape(ntiles, 128)
+    rec = np.frombuffer(body, np.uint8)[:4096].reshape(256, 16)
+    nidx = rec[:, 0:8].copy().view("<u2").astype(np.int64)          # [256, 4]
+    pos = rec[:, 8:12].astype(np.int64)                               # [256, 4]
+    rr = rec[:, 12:14].copy().view("<u2").astype(np.int64)[:, 0]
+    cc = rec[:, 14:16].copy().view("<u2").astype(np.int64)[:, 0]
+    w16 = np.zeros((ntiles, 256), np.uint32)
+    for i in range(4):
+        byte = q[:, nidx[:, i] // 2].astype(np.uint32)                # [ntiles, 256]
+        nib = (byte >> (np.uint32(4) * (nidx[:, i] % 2).astype(np.uint32))) & np.uint32(15)
+        w16 |= nib << (np.uint32(4) * pos[:, i].astype(np.uint32))
+    val = decode_window_f32(w16)
+    t = np.arange(ntiles)
+    out = np.zeros((ntiles // nbc * 16, cw), np.float32)
+    out[16 * (t // nbc)[:, None] + rr[None, :], 16 * (t % nbc)[:, None] + cc[None, :]] = val
+    return out
+
+
+def hgen(dtype=np.float64):
+    """exl3hgen / exl3hgen32 (exl3.vyb:36-56, 124-145): H[i][j] = (-1)^popcount(i & j) times the
+    constant 0.08838834764831845 rounded to the stage's precision."""
+    i, j = np.meshgrid(np.arange(128), np.arange(128), indexing="ij")
+    t = i & j
+    par = np.zeros_like(t)
+    for k in range(7):
+        par += (t >> k) & 1
+    c = np.asarray(R_SCALE, np.float64).astype(dtype)
+    return np.where(par % 2 == 1, -c, c).astype(dtype)
+
+
+def had1_f64(W, H, cw, nbc, nblocks):
+    """exl3had1 / exl3had132 (exl3.vyb:58-86, 147-172) in float64: for block = kb nbc + nb,
+    Tmp[block 16384 + b 128 + d] = sum_c W[(128 kb + b) cw + 128 nb + c] H[c][d]."""
+    W = np.asarray(W, np.float64).reshape(-1, cw)
+    H = np.asarray(H, np.float64).reshape(128, 128)
+    out = np.empty(nblocks * 16384)
+    for blk in range(nblocks):
+        kb, nb = divmod(blk, nbc)
+        out[blk * 16384:(blk + 1) * 16384] = (W[128 * kb:128 * kb + 128, 128 * nb:128 * nb + 128] @ H).ravel()
+    return out
+
+
+def had2_f64(tmp, H, suh, svh, cw, nbc, nblocks):
+    """exl3had2 / exl3had232 (exl3.vyb:88-118, 174-202) in float64: O[(128 kb + a) cw + 128 nb + d]
+    = (sum_b H[a][b] Tmp[block 16384 + b 128 + d]) suh[128 kb + a] svh[128 nb + d]; returns
+    O [nblocks / nbc 128, cw] (columns no block writes stay 0)."""
+    tmp = np.asarray(tmp, np.float64)
+    H = np.asarray(H, np.float64).reshape(128, 128)
+    su = np.asarray(suh, np.float64)
+    sv = np.asarray(svh, np.float64)
+    out = np.zeros((nblocks // nbc * 128, cw))
+    for blk in range(nblocks):
+        kb, nb = divmod(blk, nbc)
+        o = H @ tmp[blk * 16384:(blk + 1) * 16384].reshape(128, 128)
+        out[128 * kb:128 * kb + 128, 128 * nb:128 * nb + 128] = (
+            o * su[128 * kb:128 * kb + 128, None] * sv[None, 128 * nb:128 * nb + 128])
+    return out
+
+
 def load_slot_composition(path=None):
     """Tile-slot composition: (rows[256], cols[256], nib[256,4], pos[256,4]) in (r, c) order.
 

@@ -109,11 +109,28 @@ def test_pblock_preconditions_on_host():
     assert L.vybdq_launch_pblock(_lib.PB_MOE, 0, 0) == _lib.ERR_ARG
     assert L.vybdq_launch_pblock(_lib.PB_MOE, 4100, 0) == _lib.ERR_ALIGN
     assert L.vybdq_launch_pblock(_lib.PB_GEMV + 3, 4096, 0) == _lib.ERR_ARG
-    assert L.vybdq_launch_pblock(0x700, 4096, 0) == _lib.ERR_ARG
+    assert L.vybdq_launch_pblock(0xB00, 4096, 0) == _lib.ERR_ARG
+    assert L.vybdq_launch_pblock(0x702, 4096, 0) == _lib.ERR_ARG
     assert L.vybdq_launch_pblock(_lib.PB_EXL3DQ, 4096, 0) == _lib.ERR_ARG
     assert "grid" in _lib.last_error()
     assert L.vybdq_launch_pblock_grid(_lib.PB_EXL3DQ, 4096, 0, 256, 0) == _lib.ERR_SHAPE
     assert L.vybdq_launch_pblock_grid(_lib.PB_EXL3DQ, 0, 1, 256, 0) == _lib.ERR_ARG
+    for kind in (_lib.PB_EXL3HGEN, _lib.PB_EXL3HAD132, _lib.PB_EXL3HAD232, _lib.PB_EXL3CVT32):
+        assert L.vybdq_launch_pblock(kind, 0, 0) == _lib.ERR_ARG
+        assert L.vybdq_launch_pblock(kind, 4100, 0) == _lib.ERR_ALIGN
+
+
+def test_exl3_deq_map_preconditions_on_host():
+    """The map-driven decode (exl3deq / exl3deq32) rejects null pointers, an output type other than
+    float32 / float64 and a misaligned map or output before it touches the device."""
+    from vybforge_amd import _lib
+    L = _lib.lib
+    assert L.vybdq_exl3_deq_map(0, 4096, 4096, _lib.F32, 0) == _lib.ERR_ARG
+    assert L.vybdq_exl3_deq_map(4096, 4096, 0, _lib.F64, 0) == _lib.ERR_ARG
+    assert L.vybdq_exl3_deq_map(4096, 4096, 4096, _lib.F16, 0) == _lib.ERR_ARG
+    assert L.vybdq_exl3_deq_map(4096, 4100, 4096, _lib.F32, 0) == _lib.ERR_ALIGN
+    assert L.vybdq_exl3_deq_map(4096, 4096, 4100, _lib.F64, 0) == _lib.ERR_ALIGN
+    assert L.vybdq_exl3_deq_map(4096, 4096, 4098, _lib.F32, 0) == _lib.ERR_ALIGN
 
 
 @pytest.mark.parametrize("cb", [0, 2, -1])

@@ -273,3 +273,207 @@ def test_pblock_exl3dq_invalid_blocks_are_reported(dev):
     assert (blk.T == -7.0).all()
     with pytest.raises(_lib.VybdqError):
         _lib.call("vybdq_launch_pblock", _lib.PB_EXL3DQ, blk.pb.data_ptr(), stream())
+
+
+# ---- the stages of the separate EXL3 reconstruction: exl3deq(32), exl3hgen(32), exl3had1(32),
+# exl3had2(32), exl3cvt32 (exl3.vyb:36-256), as glm_engine.vyb:1103-1200 and
+# native/host/glm_exl3_check32.vyb:150-240 chain them -------------------------------------------
+
+PREC = {"f64": (np.float64, torch.float64, _lib.F64), "f32": (np.float32, torch.float32, _lib.F32)}
+HGEN = {"f64": _lib.PB_EXL3HGEN, "f32": _lib.PB_EXL3HGEN32}
+HAD1 = {"f64": _lib.PB_EXL3HAD1, "f32": _lib.PB_EXL3HAD132}
+HAD2 = {"f64": _lib.PB_EXL3HAD2, "f32": _lib.PB_EXL3HAD232}
+
+
+def pblock(words, dev):
+    return torch.tensor([int(w) for w in words], dtype=torch.int64, device=dev)
+
+
+def launch(kind, pb):
+    _lib.call("vybdq_launch_pblock", kind, pb.data_ptr(), stream())
+
+
+def map_tab(dev, cw, ntiles, body=None):
+    body = exl3.tile_map_bytes() if body is None else body
+    hdr = np.array([cw, ntiles], "<i8").tobytes()
+    return torch.from_numpy(np.frombuffer(hdr + body, np.uint8).copy()).to(dev)
+
+
+def half_scales(rng, n):
+    return (np.abs(rng.standard_normal(n)) * 0.12 + 0.02).astype(np.float16)
+
+
+@pytest.mark.parametrize("prec", ["f64", "f32"])
+def test_pblock_exl3hgen_bit_exact(dev, prec):
+    npd, td, _ = PREC[prec]
+    H = torch.full((128, 128), -7.0, dtype=td, device=dev)
+    launch(HGEN[prec], pblock([H.data_ptr()], dev))
+    torch.cuda.synchronize()
+    assert status() == 0, _lib.last_error()
+    assert np.array_equal(H.cpu().numpy(), exl3.hgen(npd))
+
+
+@pytest.mark.parametrize("prec", ["f64", "f32"])
+@pytest.mark.parametrize("rows,cw", [(16, 16), (64, 256), (2048, 4096)])
+def test_exl3_deq_map_bit_exact(dev, prec, rows, cw):
+    """exl3deq / exl3deq32 through vybdq_exl3_deq_map: every value bit-exact (the half sum is exact
+    in float32), every position written once; 2048 x 4096 is the down_proj the map was made for."""
+    npd, td, dt = PREC[prec]
+    rng = np.random.default_rng(rows + cw)
+    ntiles = (rows // 16) * (cw // 16)
+    q = rng.integers(0, 256, ntiles * 128, dtype=np.uint8).tobytes()
+    q_d = torch.from_numpy(np.frombuffer(q, np.uint8).copy()).to(dev)
+    tab = map_tab(dev, cw, ntiles)
+    o = torch.full((rows, cw), -7.0, dtype=td, device=dev)
+    _lib.call("vybdq_exl3_deq_map", q_d.data_ptr(), tab.data_ptr(), o.data_ptr(), dt, stream())
+    torch.cuda.synchronize()
+    assert status() == 0, _lib.last_error()
+    ref = exl3.map_deq(q, exl3.tile_map_bytes(), cw, ntiles).astype(npd)
+    assert np.array_equal(o.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("prec", ["f64", "f32"])
+@pytest.mark.parametrize("nbc_full", [True, False])
+def test_pblock_exl3had1(dev, prec, nbc_full):
+    npd, td, _ = PREC[prec]
+    rng = np.random.default_rng(31)
+    rows, cw = 256, 512
+    nbc = cw // 128 if nbc_full else 2
+    nblocks = rows // 128 * nbc
+    W = rng.standard_normal((rows, cw)).astype(npd)
+    H = exl3.hgen(npd)
+    W_d, H_d = torch.from_numpy(W).to(dev), torch.from_numpy(H).to(dev)
+    T = torch.full((rows * cw,), -7.0, dtype=td, device=dev)
+    launch(HAD1[prec], pblock([W_d.data_ptr(), T.data_ptr(), H_d.data_ptr(), cw, nbc, nblocks], dev))
+    torch.cuda.synchronize()
+    assert status() == 0, _lib.last_error()
+    ref = exl3.had1_f64(W, H, cw, nbc, nblocks)
+    got = T.cpu().numpy()
+    # 128-term fma chains against float64 sums in another order
+    assert matmul.rel_maxnorm(got[:nblocks * 16384], ref) < (1e-13 if prec == "f64" else 1e-5)
+    assert (got[nblocks * 16384:] == -7.0).all()
+
+
+@pytest.mark.parametrize("prec", ["f64", "f32"])
+def test_pblock_exl3had2(dev, prec):
+    npd, td, _ = PREC[prec]
+    rng = np.random.default_rng(32)
+    rows, cw = 256, 384
+    nbc, nblocks = cw // 128, rows // 128 * (cw // 128)
+    tmp = rng.standard_normal(nblocks * 16384).astype(npd)
+    H = exl3.hgen(npd)
+    su, sv = half_scales(rng, rows), half_scales(rng, cw)
+    d = [torch.from_numpy(a).to(dev) for a in (tmp, H, su, sv)]
+    O = torch.full((rows, cw), -7.0, dtype=td, device=dev)
+    launch(HAD2[prec], pblock([d[0].data_ptr(), O.data_ptr(), d[1].data_ptr(), d[2].data_ptr(), d[3].data_ptr(),
+                               cw, nbc, nblocks], dev))
+    torch.cuda.synchronize()
+    assert status() == 0, _lib.last_error()
+    ref = exl3.had2_f64(tmp, H, su, sv, cw, nbc, nblocks)
+    assert matmul.rel_maxnorm(O.cpu().numpy(), ref) < (1e-13 if prec == "f64" else 1e-5)
+
+
+@pytest.mark.parametrize("n", [1, 1000003])
+def test_pblock_exl3cvt32_bit_exact(dev, n):
+    rng = np.random.default_rng(n)
+    S = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(dev)
+    D = torch.full((n + 5,), -7.0, dtype=torch.float64, device=dev)
+    launch(_lib.PB_EXL3CVT32, pblock([S.data_ptr(), D.data_ptr(), n], dev))
+    torch.cuda.synchronize()
+    assert status() == 0, _lib.last_error()
+    assert torch.equal(D[:n], S.double()) and (D[n:] == -7.0).all()
+
+
+def exl3_matrix(rng, rows, cw):
+    ntiles = (rows // 16) * (cw // 16)
+    q = rng.integers(0, 256, ntiles * 128, dtype=np.uint8).tobytes()
+    su, sv = half_scales(rng, rows), half_scales(rng, cw)
+    ref = exl3.rotate_blocks(exl3.map_deq(q, exl3.tile_map_bytes(), cw, ntiles), su, sv)
+    return q, su, sv, ref
+
+
+@pytest.mark.parametrize("prec", ["f64", "f32"])
+def test_exl3_separate_pipeline_matches_the_rotation(dev, prec):
+    """deq -> hgen -> had1 -> had2 (-> cvt32 for the f32 chain), glm_exl3_check32.vyb:150-240 with
+    the f64 or the f32 kernels: the float64 result equals the oracle's rotated dequant."""
+    npd, td, dt = PREC[prec]
+    rng = np.random.default_rng(33)
+    rows, cw = 256, 512
+    q, su, sv, ref = exl3_matrix(rng, rows, cw)
+    ntiles, nbc = (rows // 16) * (cw // 16), cw // 128
+    nblocks = rows // 128 * nbc
+    q_d = torch.from_numpy(np.frombuffer(q, np.uint8).copy()).to(dev)
+    tab = map_tab(dev, cw, ntiles)
+    od = torch.empty((rows, cw), dtype=td, device=dev)
+    H = torch.empty((128, 128), dtype=td, device=dev)
+    tmp = torch.empty((rows * cw,), dtype=td, device=dev)
+    fd = torch.empty((rows, cw), dtype=td, device=dev)
+    su_d, sv_d = torch.from_numpy(su).to(dev), torch.from_numpy(sv).to(dev)
+    _lib.call("vybdq_exl3_deq_map", q_d.data_ptr(), tab.data_ptr(), od.data_ptr(), dt, stream())
+    launch(HGEN[prec], pblock([H.data_ptr()], dev))
+    launch(HAD1[prec], pblock([od.data_ptr(), tmp.data_ptr(), H.data_ptr(), cw, nbc, nblocks], dev))
+    launch(HAD2[prec], pblock([tmp.data_ptr(), fd.data_ptr(), H.data_ptr(), su_d.data_ptr(), sv_d.data_ptr(),
+                               cw, nbc, nblocks], dev))
+    if prec == "f32":
+        out = torch.empty((rows, cw), dtype=torch.float64, device=dev)
+        launch(_lib.PB_EXL3CVT32, pblock([fd.data_ptr(), out.data_ptr(), rows * cw], dev))
+    else:
+        out = fd
+    torch.cuda.synchronize()
+    assert status() == 0, _lib.last_error()
+    assert matmul.rel_maxnorm(out.cpu().numpy(), ref) < (1e-12 if prec == "f64" else 1e-5)
+
+
+def test_exl3_fused_pipeline_matches_the_rotation(dev):
+    """exl3dq1s (decode + column transform) -> exl3had232 -> exl3cvt32, the exl3_deq32 chain of
+    glm_engine.vyb:1103-1200, at the down_proj shape 2048 x 4096: float64 out vs the oracle."""
+    rng = np.random.default_rng(34)
+    rows, cw = 2048, 4096
+    nbc, nblocks = cw // 128, rows // 128 * (cw // 128)
+    blk = Exl3Block(dev, rng, rows, cw, np.zeros((128, 128)))
+    launch(_lib.PB_EXL3HGEN32, pblock([blk.H_d.data_ptr()], dev))  # H / sqrt(128) into the block's H
+    su, sv = half_scales(rng, rows), half_scales(rng, cw)
+    ref = exl3.rotate_blocks(exl3.map_deq(blk.q, blk.body, cw, (rows // 16) * (cw // 16)), su, sv)
+    blk.build_inverse()
+    blk.launch(block=256)
+    fd = torch.empty((rows, cw), dtype=torch.float32, device=dev)
+    su_d, sv_d = torch.from_numpy(su).to(dev), torch.from_numpy(sv).to(dev)
+    launch(_lib.PB_EXL3HAD232, pblock([blk.T.data_ptr(), fd.data_ptr(), blk.H_d.data_ptr(), su_d.data_ptr(),
+                                       sv_d.data_ptr(), cw, nbc, nblocks], dev))
+    out = torch.empty((rows, cw), dtype=torch.float64, device=dev)
+    launch(_lib.PB_EXL3CVT32, pblock([fd.data_ptr(), out.data_ptr(), rows * cw], dev))
+    torch.cuda.synchronize()
+    assert status() == 0, _lib.last_error()
+    assert matmul.rel_maxnorm(out.cpu().numpy(), ref) < 1e-5
+
+
+def test_exl3_stage_invalid_blocks_are_reported(dev):
+    """Stage blocks or maps that violate the preconditions write nothing and are reported."""
+    rng = np.random.default_rng(35)
+    W = torch.from_numpy(rng.standard_normal((128, 256)).astype(np.float32)).to(dev)
+    H = torch.from_numpy(exl3.hgen(np.float32)).to(dev)
+    T = torch.full((128 * 256,), -7.0, device=dev)
+    su = torch.ones(256, dtype=torch.float16, device=dev)
+    cases = [
+        (_lib.PB_EXL3HAD132, [W.data_ptr(), T.data_ptr(), H.data_ptr(), 256, 0, 2]),        # nbc = 0
+        (_lib.PB_EXL3HAD132, [W.data_ptr(), T.data_ptr(), H.data_ptr(), 256, 3, 3]),        # 128 nbc > cw
+        (_lib.PB_EXL3HAD132, [W.data_ptr() + 4, T.data_ptr(), H.data_ptr(), 256, 2, 2]),    # misaligned W
+        (_lib.PB_EXL3HAD232, [W.data_ptr(), T.data_ptr(), H.data_ptr(), su.data_ptr() + 1, su.data_ptr(), 256, 2, 2]),
+        (_lib.PB_EXL3HAD232, [W.data_ptr(), T.data_ptr(), H.data_ptr(), su.data_ptr(), su.data_ptr(), 256, 2, 0]),
+        (_lib.PB_EXL3CVT32, [W.data_ptr(), T.data_ptr(), -1]),                              # n < 0
+        (_lib.PB_EXL3CVT32, [W.data_ptr(), T.data_ptr() + 4, 16]),                          # D not 8-aligned
+        (_lib.PB_EXL3HGEN, [T.data_ptr() + 4]),                                               # H f64 misaligned
+    ]
+    for kind, words in cases:
+        launch(kind, pblock(words, dev))
+        assert status() == _lib.ERR_SHAPE, (hex(kind), words)
+        assert (T == -7.0).all()
+    # a map entry whose nibble index leaves the tile, and a cw that is not a multiple of 16
+    q = torch.zeros(2 * 128, dtype=torch.uint8, device=dev)
+    o = torch.full((16, 32), -7.0, device=dev)
+    body = bytearray(exl3.tile_map_bytes())
+    body[16 * 5 + 1] = 1
+    for tab in (map_tab(dev, 32, 2, bytes(body)), map_tab(dev, 24, 2)):
+        _lib.call("vybdq_exl3_deq_map", q.data_ptr(), tab.data_ptr(), o.data_ptr(), _lib.F32, stream())
+        assert status() == _lib.ERR_SHAPE
+        assert (o == -7.0).all()

@@ -386,6 +386,50 @@ def test_exl3_column_transform_layout():
     assert np.allclose(blk @ H.T / 128.0, what[:128, 128:256], atol=1e-12)
 
 
+def test_exl3_map_deq_equals_the_map_decode():
+    """exl3deq's slot-driven placement (each record's own row / col) equals the pinned
+    inverse-map decode for the reference's map, and the all-zero trellis gives the 1.84375 KAT."""
+    rng = np.random.default_rng(11)
+    rows, cw = 64, 256
+    ntiles = (rows // 16) * (cw // 16)
+    q = rng.integers(0, 256, ntiles * 128, dtype=np.uint8).tobytes()
+    body = exl3.tile_map_bytes()
+    got = exl3.map_deq(q, body, cw, ntiles)
+    assert np.array_equal(got, exl3.map_decode_f32(q, rows, cw, body, exl3.tile_map_inverse(body)))
+    assert (exl3.map_deq(bytes(ntiles * 128), body, cw, ntiles) == np.float32(1.84375)).all()
+
+
+def test_exl3_hgen_is_the_scaled_sylvester_matrix():
+    """The Sylvester sign pattern times the reference's literal 0.08838834764831845 (one float64
+    ulp above 1 / sqrt(128); the float32 roundings agree), orthogonal to rounding."""
+    H = exl3.hadamard128()
+    c = 0.08838834764831845
+    assert np.array_equal(exl3.hgen(np.float64), np.where(H > 0, c, -c))
+    assert np.allclose(exl3.hgen(np.float64), H / np.sqrt(128.0), rtol=3e-16, atol=0)
+    assert np.array_equal(exl3.hgen(np.float32), (H / np.sqrt(128.0)).astype(np.float32))
+    assert np.allclose(exl3.hgen() @ exl3.hgen().T, np.eye(128), atol=1e-14)
+
+
+def test_exl3_had1_is_the_column_transform_and_had2_completes_the_rotation():
+    """exl3had1 with nbc = cw / 128 is the pinned column transform; exl3had2 after it is the pinned
+    per-block rotation diag(suh) Hs What Hs diag(svh); a smaller nbc touches only its columns."""
+    rng = np.random.default_rng(12)
+    rows, cw = 256, 384
+    what = rng.standard_normal((rows, cw))
+    su = rng.standard_normal(rows)
+    sv = rng.standard_normal(cw)
+    H = exl3.hgen()
+    nbc, nblocks = cw // 128, rows // 128 * (cw // 128)
+    t = exl3.had1_f64(what, H, cw, nbc, nblocks)
+    assert np.array_equal(t, exl3.column_transform_f64(what, H))
+    w = exl3.had2_f64(t, H, su, sv, cw, nbc, nblocks)
+    assert np.allclose(w, exl3.rotate_blocks(what, su, sv), rtol=0, atol=1e-12)
+    t2 = exl3.had1_f64(what, H, cw, 2, rows // 128 * 2)
+    w2 = exl3.had2_f64(t2, H, su, sv, cw, 2, rows // 128 * 2)
+    assert np.allclose(w2[:, :256], exl3.rotate_blocks(what[:, :256], su, sv[:256]), rtol=0, atol=1e-12)
+    assert (w2[:, 256:] == 0).all()
+
+
 def test_moe_fixture_block_matches_moe_forward():
     """The fixture semantics (one expert on every routed lane) equal the pinned moe_forward with
     that expert for every id and the same float32-rounded logits."""

@@ -20,6 +20,10 @@ EXL3_MCG = 1
 MOE_NOALLOC_MAX_BYTES = 64 * 1024 * 1024  # VYBDQ_MOE_NOALLOC_MAX_BYTES
 PB_GEMV, PB_GEMM, PB_GEMM_XH = 0x100, 0x200, 0x300
 PB_MOE, PB_EXL3DQ, PB_EXL3INV = 0x400, 0x500, 0x600
+PB_EXL3HGEN, PB_EXL3HGEN32 = 0x700, 0x701
+PB_EXL3HAD1, PB_EXL3HAD132 = 0x800, 0x801
+PB_EXL3HAD2, PB_EXL3HAD232 = 0x900, 0x901
+PB_EXL3CVT32 = 0xA00
 
 _u64, _i64, _int, _u32 = ctypes.c_uint64, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32
 
@@ -95,6 +99,7 @@ SIGNATURES = {
     "vybdq_gemm_q8_0_i8": [_u64, _u64, _u64, _u64, _i64, _i64, _i64, _int, _i64, _u64, _u64, _i64, _u64],
     "vybdq_launch_pblock": [_int, _u64, _u64],
     "vybdq_launch_pblock_grid": [_int, _u64, _u32, _u32, _u64],
+    "vybdq_exl3_deq_map": [_u64, _u64, _u64, _int, _u64],
     "vybdq_pblock_status": [],
     "vybdq_moe_route": [_u64, _int, _u64, _u64, _u64, _i64, _i64, _i64, ctypes.c_double, _u64],
     "vybdq_moe_workspace_size": [_i64, _i64, _i64, _i64, _i64],

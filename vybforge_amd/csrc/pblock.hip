@@ -29,6 +29,8 @@ int kq_gemm_pblock(int wtype, int xdt, const int64_t *pb, uint32_t *status, hipS
 int pb_moe_launch(const int64_t *pb, uint32_t *status, hipStream_t s);
 int pb_exl3dq_launch(const int64_t *pb, int64_t threads, uint32_t *status, hipStream_t s);
 int pb_exl3inv_launch(const int64_t *pb, uint32_t *status, hipStream_t s);
+int pb_exl3stage_launch(int kind, const int64_t *pb, uint32_t *status, hipStream_t s);
+int exl3_deq_map_launch(const uint8_t *q, const int64_t *tab, void *o, int out_dt, uint32_t *status, hipStream_t s);
 
 // status word bits (word 0 of the per-device status array; word 1 is the chain's stage counter)
 constexpr uint32_t kPbWaitTimeout = 1u, kPbBadGemv = 2u, kPbBadGemm = 4u, kPbBadMoe = 8u, kPbBadExl3 = 16u;
@@ -140,12 +142,21 @@ extern "C" int vybdq_launch_pblock(int kind, uint64_t P, uint64_t stream) {
     return kind == VYBDQ_PB_MOE ? pb_moe_launch(pb, status, as_stream(stream))
                                 : pb_exl3inv_launch(pb, status, as_stream(stream));
   }
+  if (kind == VYBDQ_PB_EXL3HGEN || kind == VYBDQ_PB_EXL3HGEN32 || kind == VYBDQ_PB_EXL3HAD1 ||
+      kind == VYBDQ_PB_EXL3HAD132 || kind == VYBDQ_PB_EXL3HAD2 || kind == VYBDQ_PB_EXL3HAD232 ||
+      kind == VYBDQ_PB_EXL3CVT32) {
+    uint64_t st = 0;
+    const int rc = pb_status_address(st);
+    if (rc) return rc;
+    return pb_exl3stage_launch(kind, reinterpret_cast<const int64_t *>(P), reinterpret_cast<uint32_t *>(st),
+                               as_stream(stream));
+  }
   VYBDQ_REQUIRE(kind != VYBDQ_PB_EXL3DQ, VYBDQ_ERR_ARG,
                 "VYBDQ_PB_EXL3DQ takes its extent from the grid: use vybdq_launch_pblock_grid");
   const int op = kind & ~0xff, ty = kind & 0xff;
   VYBDQ_REQUIRE(op == VYBDQ_PB_GEMV || op == VYBDQ_PB_GEMM || op == VYBDQ_PB_GEMM_XH, VYBDQ_ERR_ARG,
                 "kind must be VYBDQ_PB_GEMV, VYBDQ_PB_GEMM or VYBDQ_PB_GEMM_XH plus a GGML type id, or "
-                "VYBDQ_PB_MOE, VYBDQ_PB_EXL3DQ or VYBDQ_PB_EXL3INV");
+                "VYBDQ_PB_MOE or one of the VYBDQ_PB_EXL3* kinds");
   VYBDQ_REQUIRE(ty == 2 || ty == 8 || ty == 12 || ty == 13 || ty == 14 || ty == 22, VYBDQ_ERR_ARG,
                 "the type id must be 2 (q4_0), 8 (Q8_0), 12 (Q4_K), 13 (Q5_K), 14 (Q6_K) or 22 (IQ2_S)");
   uint64_t st = 0;
@@ -176,6 +187,18 @@ extern "C" int vybdq_launch_pblock_grid(int kind, uint64_t P, uint32_t grid_x, u
                           as_stream(stream));
 }
 
+extern "C" int vybdq_exl3_deq_map(uint64_t q, uint64_t tab, uint64_t out, int out_dt, uint64_t stream) {
+  VYBDQ_REQUIRE(q && tab && out, VYBDQ_ERR_ARG, "null pointer");
+  VYBDQ_REQUIRE(out_dt == VYBDQ_F32 || out_dt == VYBDQ_F64, VYBDQ_ERR_ARG, "out_dt must be VYBDQ_F32 or VYBDQ_F64");
+  VYBDQ_REQUIRE((tab & 7) == 0 && (out & (out_dt == VYBDQ_F64 ? 7 : 3)) == 0, VYBDQ_ERR_ALIGN,
+                "tab must be 8-byte and out element aligned");
+  uint64_t st = 0;
+  const int rc = pb_status_address(st);
+  if (rc) return rc;
+  return exl3_deq_map_launch(reinterpret_cast<const uint8_t *>(q), reinterpret_cast<const int64_t *>(tab),
+                             reinterpret_cast<void *>(out), out_dt, reinterpret_cast<uint32_t *>(st), as_stream(stream));
+}
+
 extern "C" int vybdq_pblock_status(void) {
   uint64_t st = 0;
   const int rc = pb_status_address(st);
@@ -192,7 +215,8 @@ extern "C" int vybdq_pblock_status(void) {
   if (v & kPbBadGemm) return set_error(VYBDQ_ERR_SHAPE, "a GEMM parameter block was invalid (S, N, K, LDY or pointers)");
   if (v & kPbBadMoe) return set_error(VYBDQ_ERR_SHAPE, "a MoE parameter block was invalid (S or pointers)");
   if (v & kPbBadExl3)
-    return set_error(VYBDQ_ERR_SHAPE, "an EXL3 parameter block was invalid (cw, the grid, pointers or the tile map)");
+    return set_error(VYBDQ_ERR_SHAPE,
+                     "an EXL3 parameter block or map was invalid (cw, nbc, nblocks, the grid, pointers or the tile map)");
   if (v & kPbWaitTimeout) return set_error(VYBDQ_ERR_HIP, "a GEMV parameter block launch timed out");
   return VYBDQ_OK;
 }
