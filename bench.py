@@ -403,6 +403,25 @@ def cpu_baselines():
     out["cfg5_moe"] = record(lambda t: b5 / t / 1e9, "GB/s",
                              "one routed expert's FFN (21.2 MB of q4_0) on 2 tokens per run", moe_run)
 
+    # GLM-5.3 MoE with EXL3 experts: one routed expert's FFN (EXL3 gate / up 4096 -> 2048, down
+    # 2048 -> 4096, the oracle's float64 dequant) on 2 tokens per run
+    Hx, Ix = MOE53["H"], MOE53["I"]
+    mats = [synth.exl3_tensors(rng, Hx, Ix), synth.exl3_tensors(rng, Hx, Ix), synth.exl3_tensors(rng, Ix, Hx)]
+    x6 = rng.standard_normal((2, Hx)).astype(np.float32)
+    b6 = sum(t.size * 2 + s1.size * 2 + s2.size * 2 for t, s1, s2 in mats) + 2 * 2 * Hx + 4 * 2 * Hx
+
+    def exl3_moe_run(threads):
+        def dq(t, su, sv):
+            n = sv.size
+            return np.concatenate(_par(lambda r: exl3.dequant_exl3_f64(t[:, r[0] // 16:r[1] // 16], su,
+                                                                         sv[r[0]:r[1]]).astype(np.float32),
+                                       [(128 * a, 128 * b) for a, b in _split(n // 128, threads)], threads), axis=1)
+        wg, wu, wd = (dq(*m) for m in mats)
+        return moe.swiglu(x6 @ wg, x6 @ wu) @ wd
+    out["glm53_moe_exl3"] = record(lambda t: b6 / t / 1e9, "GB/s",
+                                   "one routed EXL3 expert's FFN (12.6 MB of trellis) on 2 tokens per run",
+                                   exl3_moe_run)
+
     blas = ", ".join(f"{i.get('internal_api')} {i.get('version')}" for i in threadpool_info()
                      if i.get("user_api") == "blas") or "unknown"
     host = dict(cpu_count=os.cpu_count(), affinity=len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity")
