@@ -8,7 +8,7 @@
 //   out[t] = sum_s w[t, s] e_out[idx[t, s]](t) + shared(x[t])
 // Without a bias the selection is by logit (sigmoid is monotone: exact order, no float32
 // saturation ties); with a bias the choice is computed in double, as the reference does. One
-// 256-thread workgroup routes a token (route_double_wg).
+// wave routes a token (route_wave).
 //
 // Pipeline (all on the stream, no host syncs), when H and I are multiples of 256: route ->
 // bucket (one workgroup: per-expert counts, a parallel scan, the lists of row groups of the
@@ -71,60 +71,47 @@ __device__ __forceinline__ uint64_t double_order_key(double d) {
   return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
 }
 
-// Routing of one token by the whole 256-thread workgroup: thread i holds experts i, i + 256, i + 512
-// and i + 768 (E <= 1024) with their double-precision sigmoid scores and keys (score + bias, or the
-// logit without a bias); each wave selects the top-k of its threads' experts, and wave 0 selects the
-// top-k of the 4 k candidates. A selection round is a wave maximum (DPP, on the VALU) of the top 32
-// bits of the lanes' best order keys; only when several lanes share it, of the low 32 bits among
-// those and then the lowest expert id (ties to the lower id); the owner lane retires its winner. Keys, the tie rule, the scores and the weight arithmetic (scores
-// over their sum in selection order, times scale) are one total order and one formula, so the
-// result is that of a single pass over all E experts.
-struct RouteLds {  // candidate c = wave * k + its selection round
-  uint64_t key[256];
-  double sc[256];
-  int e[256];
-  double slot_sc[64];
-};
-
-template <int LDT>
-__device__ __forceinline__ void route_double_wg(const void *__restrict__ logits, const float *__restrict__ bias, int t,
-                                                int E, int topk, double scale, int *__restrict__ idx_out,
-                                                float *__restrict__ w_out, int *__restrict__ idx_copy, RouteLds &L) {
+// Routing of one token by one wave: lane l holds experts l, l + 64, ..., l + 64 (ENT - 1) (E <= 64 ENT)
+// with their order keys (of the double-precision sigmoid score + bias, or of the logit without a
+// bias). A selection round takes each lane's best entry (branch-free), then the wave maximum (DPP, on
+// the VALU) of the top 32 bits of those keys; only when several lanes share it, of the low 32 bits
+// among those and then the lowest expert id (ties to the lower id); the winner is retired where it
+// lives. After topk rounds lane s holds the expert of slot s and computes its score again (the same
+// expression), and the weights are the scores over their sum in slot order, times scale. Keys, the
+// tie rule and the weight arithmetic are one total order and one formula, so the result is that of
+// a single pass over all E experts. (Four waves each selecting among a quarter of the experts, then
+// merging their candidates through LDS, took 4.8 us per token against 3.3 (warm, E = 256, top-8);
+// carrying each entry's score through the rounds instead of recomputing the winners' took 3.5.)
+template <int LDT, int ENT>
+__device__ __forceinline__ void route_wave(const void *__restrict__ logits, const float *__restrict__ bias, int t, int E,
+                                           int topk, double scale, int *__restrict__ idx_out, float *__restrict__ w_out,
+                                           int *__restrict__ idx_copy) {
   constexpr uint32_t kNone = 0x7fffffffu;  // no candidate (and above every expert id)
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint64_t key[4];
-  uint32_t eid[4];
-  double score[4];
+  const int lane = threadIdx.x & 63;
+  uint64_t key[ENT];
+  uint32_t eid[ENT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tid + 256 * i;
+  for (int i = 0; i < ENT; ++i) {
+    const int e = lane + 64 * i;
     key[i] = 0;
     eid[i] = kNone;
-    score[i] = 0.0;
     if (e < E) {
       const double l = load_logit<LDT>(logits, static_cast<int64_t>(t) * E + e);
-      score[i] = 1.0 / (1.0 + exp(-l));
-      key[i] = double_order_key(bias ? score[i] + static_cast<double>(bias[e]) : l);
+      key[i] = double_order_key(bias ? 1.0 / (1.0 + exp(-l)) + static_cast<double>(bias[e]) : l);
       eid[i] = static_cast<uint32_t>(e);
     }
   }
-  // one selection round over (key, eid, score) of up to 4 entries per lane; the winner's entry is
-  // retired; returns the winner's key, id and score in every lane
-  auto select = [&](uint64_t (&k)[4], uint32_t (&id)[4], const double (&sc)[4], uint64_t &wk, uint32_t &we,
-                    double &ws) {
+  uint32_t mine = kNone;  // lane s < topk: the expert of slot s
+  for (int s = 0; s < topk; ++s) {
     uint64_t bk = 0;
     uint32_t be = kNone;
-    double bs = 0.0;
     // (an empty entry, key 0 and id kNone, never beats the start value: no test of it, no branch)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool take = (k[i] > bk) | ((k[i] == bk) & (id[i] < be));
-      bk = take ? k[i] : bk;
-      be = take ? id[i] : be;
-      bs = take ? sc[i] : bs;
+    for (int i = 0; i < ENT; ++i) {
+      const bool take = (key[i] > bk) | ((key[i] == bk) & (eid[i] < be));
+      bk = take ? key[i] : bk;
+      be = take ? eid[i] : be;
     }
-    // the top 32 key bits decide unless several lanes share the largest; then the low 32 bits,
-    // then the lowest id
     const uint32_t khi = static_cast<uint32_t>(bk >> 32);
     const uint32_t mhi = wave_ext_u32<true>(khi);
     uint64_t own = __ballot(khi == mhi && be != kNone);
@@ -135,100 +122,51 @@ __device__ __forceinline__ void route_double_wg(const void *__restrict__ logits,
       own = __ballot(be == e1 && e1 != kNone);
     }
     const int src = own ? static_cast<int>(__builtin_ctzll(own)) : 0;
-    we = own ? static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(be), src)) : kNone;
-    wk = (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(khi), src))) << 32) |
-         static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(bk)), src));
-    const uint64_t sb = __double_as_longlong(bs);
-    const uint32_t slo = __builtin_amdgcn_readlane(static_cast<uint32_t>(sb), src);
-    const uint32_t shi = __builtin_amdgcn_readlane(static_cast<uint32_t>(sb >> 32), src);
-    ws = __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(shi) << 32) | slo));
+    const uint32_t we = own ? static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(be), src)) : kNone;
+    mine = lane == s ? we : mine;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (id[i] == we) {  // retired (ids are unique): an empty entry again
-        id[i] = kNone;
-        k[i] = 0;
-      }
-  };
-  for (int s = 0; s < topk; ++s) {  // this wave's top-k
-    uint64_t wk;
-    uint32_t we;
-    double ws;
-    select(key, eid, score, wk, we, ws);
-    if (lane == 0) {
-      L.key[wave * topk + s] = wk;
-      L.sc[wave * topk + s] = ws;
-      L.e[wave * topk + s] = static_cast<int>(we);
+    for (int i = 0; i < ENT; ++i) {
+      const bool won = eid[i] == we;  // ids are unique: the winner's entry becomes empty
+      eid[i] = won ? kNone : eid[i];
+      key[i] = won ? 0 : key[i];
     }
   }
-  __syncthreads();
-  if (wave == 0 && 4 * topk <= 64) {
-    // the top-k of the 4 k candidates by rank: lane c holds candidate c and counts the candidates
-    // that beat it (larger key, or the same key and a lower id), reading them from LDS (the same
-    // word for every lane); a rank below k is the candidate's slot
-    const int nc = 4 * topk;
-    const bool have = lane < nc;
-    const uint64_t myk = have ? L.key[lane] : 0;
-    const uint32_t mye = have ? static_cast<uint32_t>(L.e[lane]) : kNone;
-    // (an empty candidate, key 0 and id kNone, beats no real one: no test of it, no branch)
-    int rank = 0;
-    for (int c0 = 0; c0 < nc; c0 += 8) {  // 8 candidates read before any is compared
-      uint64_t k2[8];
-      uint32_t e2[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        k2[j] = L.key[c0 + j];
-        e2[j] = static_cast<uint32_t>(L.e[c0 + j]);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        rank += static_cast<int>((c0 + j < nc) & ((k2[j] > myk) | ((k2[j] == myk) & (e2[j] < mye))));
-    }
-    if (have && mye != kNone && rank < topk) {
-      idx_out[t * topk + rank] = static_cast<int>(mye);
-      if (idx_copy) idx_copy[t * topk + rank] = static_cast<int>(mye);
-      L.slot_sc[rank] = L.sc[lane];
-    }
-    __builtin_amdgcn_wave_barrier();
-    double tot = 0.0;  // the scores summed in slot order
-    for (int q = 0; q < topk; ++q) tot += L.slot_sc[q];
-    if (lane < topk) w_out[t * topk + lane] = static_cast<float>(L.slot_sc[lane] / (tot + 1e-20) * scale);
-  } else if (wave == 0) {  // more than 64 candidates: k selection rounds over lanes holding 4 each
-    uint64_t ck[4];
-    uint32_t ce[4];
-    double cs[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = lane + 64 * j;
-      const bool ok = c < 4 * topk;
-      ck[j] = ok ? L.key[c] : 0;
-      cs[j] = ok ? L.sc[c] : 0.0;
-      ce[j] = ok ? static_cast<uint32_t>(L.e[c]) : kNone;
-    }
-    double my_sc = 0.0, tot = 0.0;
-    for (int s = 0; s < topk; ++s) {
-      uint64_t wk;
-      uint32_t we;
-      double ws;
-      select(ck, ce, cs, wk, we, ws);
-      if (lane == 0) {
-        idx_out[t * topk + s] = static_cast<int>(we);
-        if (idx_copy) idx_copy[t * topk + s] = static_cast<int>(we);
-      }
-      if (lane == s) my_sc = ws;
-      tot += ws;
-    }
-    if (lane < topk) w_out[t * topk + lane] = static_cast<float>(my_sc / (tot + 1e-20) * scale);
+  const bool slot = lane < topk && mine != kNone;
+  double sc = 0.0;
+  if (slot) sc = 1.0 / (1.0 + exp(-load_logit<LDT>(logits, static_cast<int64_t>(t) * E + mine)));
+  const uint64_t sb = __double_as_longlong(sc);
+  double tot = 0.0;  // the scores summed in slot order
+  for (int q = 0; q < topk; ++q) {
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(sb), q);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(sb >> 32), q);
+    tot += __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
   }
-  __syncthreads();  // L is reused by the next token
+  if (slot) {
+    idx_out[t * topk + lane] = static_cast<int>(mine);
+    if (idx_copy) idx_copy[t * topk + lane] = static_cast<int>(mine);
+  }
+  if (lane < topk) w_out[t * topk + lane] = static_cast<float>(sc / (tot + 1e-20) * scale);
 }
 
-// one token per workgroup of 256 threads
-template <int LDT>
+// experts per lane of the router for E experts: 4, 5, 8 or 16
+inline int route_ent(int64_t E) { return E <= 256 ? 4 : E <= 320 ? 5 : E <= 512 ? 8 : 16; }
+
+// Dispatch the router's experts per lane to a template parameter.
+#define VYBDQ_DISPATCH_ENT(E, NAME, ...)                                       \
+  switch (route_ent(E)) {                                                     \
+    case 4: { constexpr int NAME = 4; __VA_ARGS__; } break;                   \
+    case 5: { constexpr int NAME = 5; __VA_ARGS__; } break;                   \
+    case 8: { constexpr int NAME = 8; __VA_ARGS__; } break;                   \
+    default: { constexpr int NAME = 16; __VA_ARGS__; } break;                 \
+  }
+
+// one token per wave, four per workgroup
+template <int LDT, int ENT>
 __global__ void __launch_bounds__(256) k_moe_route(const void *__restrict__ logits, const float *__restrict__ bias,
                                                    int E, int topk, double scale, int *__restrict__ idx_out,
-                                                   float *__restrict__ w_out) {
-  __shared__ RouteLds L;
-  route_double_wg<LDT>(logits, bias, blockIdx.x, E, topk, scale, idx_out, w_out, nullptr, L);
+                                                   float *__restrict__ w_out, int T) {
+  const int t = 4 * blockIdx.x + (threadIdx.x >> 6);
+  if (t < T) route_wave<LDT, ENT>(logits, bias, t, E, topk, scale, idx_out, w_out, nullptr);
 }
 
 // One workgroup: per-expert counts, exclusive scans, and each (token, slot)'s bucket position
@@ -364,7 +302,7 @@ __global__ void __launch_bounds__(256) k_moe_bucket_tiles(const int *__restrict_
 
 // Few tokens: routing (wave w takes tokens w, w + 4, ...) and bucketing in one workgroup; the
 // routed ids also go to LDS, where the bucketing reads them.
-template <int LDT>
+template <int LDT, int ENT>
 __global__ void __launch_bounds__(256) k_moe_route_bucket(const void *__restrict__ logits, const float *__restrict__ bias,
                                                           int E, int topk, double scale, int *__restrict__ idx_out,
                                                           float *__restrict__ w_out, int T, int BMr, int BMr2,
@@ -373,8 +311,8 @@ __global__ void __launch_bounds__(256) k_moe_route_bucket(const void *__restrict
                                                           int4 *__restrict__ tiles2, int *__restrict__ ntiles2) {
   extern __shared__ int sh[];
   int *idx_lds = sh + 2 * E;  // [T * topk]
-  __shared__ RouteLds L;
-  for (int t = 0; t < T; ++t) route_double_wg<LDT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds, L);
+  for (int t = threadIdx.x >> 6; t < T; t += 4)
+    route_wave<LDT, ENT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds);
   __syncthreads();
   bucket_tiles(idx_lds, T, topk, E, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2, sh);
 }
@@ -431,7 +369,7 @@ __device__ __forceinline__ void bucket_rows_wave(const int *idx_lds, int T, int 
 
 // Few tokens and at most 64 rows: routing (wave w takes tokens w, w + 4, ...), then the one-wave
 // bucketing above.
-template <int LDT>
+template <int LDT, int ENT>
 __global__ void __launch_bounds__(256) k_moe_route_bucket_w(const void *__restrict__ logits, const float *__restrict__ bias,
                                                             int E, int topk, double scale, int *__restrict__ idx_out,
                                                             float *__restrict__ w_out, int T, int BMr, int BMr2,
@@ -439,8 +377,8 @@ __global__ void __launch_bounds__(256) k_moe_route_bucket_w(const void *__restri
                                                             int4 *__restrict__ tiles, int *__restrict__ ntiles,
                                                             int4 *__restrict__ tiles2, int *__restrict__ ntiles2) {
   __shared__ int idx_lds[64];
-  __shared__ RouteLds L;
-  for (int t = 0; t < T; ++t) route_double_wg<LDT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds, L);
+  for (int t = threadIdx.x >> 6; t < T; t += 4)
+    route_wave<LDT, ENT>(logits, bias, t, E, topk, scale, idx_out, w_out, idx_lds);
   __syncthreads();
   if (threadIdx.x < 64) bucket_rows_wave(idx_lds, T, topk, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2);
 }
@@ -515,10 +453,15 @@ extern "C" int64_t vybdq_moe_workspace_size(int64_t T, int64_t H, int64_t I, int
 // their own value, with the same ties-to-the-lower-id rule).
 static int launch_route(const void *lg, int logits_dt, const float *bias, int64_t T, int64_t E, int64_t topk,
                         double scale, int *idx, float *w, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(T)), block(256);
-  const int e = static_cast<int>(E), k = static_cast<int>(topk);
-  if (logits_dt == VYBDQ_F64) hipLaunchKernelGGL((k_moe_route<VYBDQ_F64>), grid, block, 0, s, lg, bias, e, k, scale, idx, w);
-  else VYBDQ_DISPATCH_IN(logits_dt, LDT, hipLaunchKernelGGL((k_moe_route<LDT>), grid, block, 0, s, lg, bias, e, k, scale, idx, w));
+  const dim3 grid(static_cast<unsigned>((T + 3) / 4)), block(256);
+  const int e = static_cast<int>(E), k = static_cast<int>(topk), tt = static_cast<int>(T);
+  if (logits_dt == VYBDQ_F64) {
+    VYBDQ_DISPATCH_ENT(E, ENT, hipLaunchKernelGGL((k_moe_route<VYBDQ_F64, ENT>), grid, block, 0, s, lg, bias, e, k,
+                                                  scale, idx, w, tt));
+  } else {
+    VYBDQ_DISPATCH_IN(logits_dt, LDT, VYBDQ_DISPATCH_ENT(E, ENT, hipLaunchKernelGGL((k_moe_route<LDT, ENT>), grid, block,
+                                                                                    0, s, lg, bias, e, k, scale, idx, w, tt)));
+  }
   return check_launch("moe route");
 }
 
@@ -536,14 +479,15 @@ int moe_route_bucket(const void *logits, int logits_dt, const float *bias, int64
   if (T <= 8) {
     const bool wave_rows = T * topk <= 64;
     const size_t shb = static_cast<size_t>(2 * E + T * topk) * 4;
-#define RB(LDT)                                                                                          \
-  do {                                                                                                        \
-    if (wave_rows)                                                                                            \
-      hipLaunchKernelGGL((k_moe_route_bucket_w<LDT>), dim3(1), dim3(256), 0, s, logits, bias, e, k, scale, \
-                         idx, w, tt, BMr, BMr, 0, pos, row_map, tiles, ntiles, tiles2, ntiles2);               \
-    else                                                                                                      \
-      hipLaunchKernelGGL((k_moe_route_bucket<LDT>), dim3(1), dim3(256), shb, s, logits, bias, e, k, scale, \
-                         idx, w, tt, BMr, BMr, 0, pos, row_map, tiles, ntiles, tiles2, ntiles2);               \
+#define RB(LDT)                                                                                               \
+  do {                                                                                                             \
+    VYBDQ_DISPATCH_ENT(E, ENT,                                                                                     \
+      if (wave_rows)                                                                                               \
+        hipLaunchKernelGGL((k_moe_route_bucket_w<LDT, ENT>), dim3(1), dim3(256), 0, s, logits, bias, e, k, scale, \
+                           idx, w, tt, BMr, BMr, 0, pos, row_map, tiles, ntiles, tiles2, ntiles2);                 \
+      else                                                                                                         \
+        hipLaunchKernelGGL((k_moe_route_bucket<LDT, ENT>), dim3(1), dim3(256), shb, s, logits, bias, e, k, scale, \
+                           idx, w, tt, BMr, BMr, 0, pos, row_map, tiles, ntiles, tiles2, ntiles2));                \
   } while (0)
     if (logits_dt == VYBDQ_F64) RB(VYBDQ_F64);
     else { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT)); }
@@ -639,14 +583,15 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       int *n2 = gv ? m.ntiles2 : nullptr;
       // at most 64 rows: the one-wave bucketing (no LDS counts, scans or barriers)
       const bool wave_rows = T * topk <= 64;
-#define RB(LDT)                                                                                          \
-  do {                                                                                                        \
-    if (wave_rows)                                                                                            \
-      hipLaunchKernelGGL((k_moe_route_bucket_w<LDT>), dim3(1), dim3(256), 0, s, lg, bs, e, k, scale, idx, \
-                         wts, tt, BMr, mc, shared ? 1 : 0, m.pos, m.row_map, m.tiles, m.ntiles, t2, n2);       \
-    else                                                                                                      \
-      hipLaunchKernelGGL((k_moe_route_bucket<LDT>), dim3(1), dim3(256), shb, s, lg, bs, e, k, scale, idx, \
-                         wts, tt, BMr, mc, shared ? 1 : 0, m.pos, m.row_map, m.tiles, m.ntiles, t2, n2);       \
+#define RB(LDT)                                                                                               \
+  do {                                                                                                             \
+    VYBDQ_DISPATCH_ENT(E, ENT,                                                                                     \
+      if (wave_rows)                                                                                               \
+        hipLaunchKernelGGL((k_moe_route_bucket_w<LDT, ENT>), dim3(1), dim3(256), 0, s, lg, bs, e, k, scale, idx,  \
+                           wts, tt, BMr, mc, shared ? 1 : 0, m.pos, m.row_map, m.tiles, m.ntiles, t2, n2);         \
+      else                                                                                                         \
+        hipLaunchKernelGGL((k_moe_route_bucket<LDT, ENT>), dim3(1), dim3(256), shb, s, lg, bs, e, k, scale, idx,  \
+                           wts, tt, BMr, mc, shared ? 1 : 0, m.pos, m.row_map, m.tiles, m.ntiles, t2, n2));        \
   } while (0)
       if (logits_dt == VYBDQ_F64) RB(VYBDQ_F64);
       else { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT)); }
