@@ -59,8 +59,12 @@ constexpr int moe_gv_cpp(int G, bool swi) { return 4 * (swi ? 32 / G : 64 / G); 
 
 __device__ __forceinline__ float moe_silu(float g) { return g / (1.0f + __expf(-g)); }
 
-// One chunk of MC tokens (rows r0c .. r0c + MC - 1) over the workgroup's columns.
-template <int FMT, int G, int U, int MC, bool SWI, int XW>
+// One chunk of MC tokens (rows r0c .. r0c + MC - 1) over the workgroup's columns. LONG: rows of more
+// than U G pairs, whose lanes take further batches beyond the prefetched U pairs; without it every
+// lane's pairs are the prefetched ones and the pass has no loop (a loop whose batches reload the
+// ring slot made the compiler wait for every load in flight, the next passes' included, before
+// each pass).
+template <int FMT, int G, int U, int MC, bool SWI, int XW, bool LONG>
 __device__ __forceinline__ void moe_gv_chunk(const MoeGvArgs &a, const uint8_t *Wg, const uint8_t *Wu, int r0c,
                                              int n0, int ncols, char *lds, float *sx) {
   constexpr int PD = Fmt<FMT>::PAIR_DWORDS;
@@ -142,19 +146,35 @@ __device__ __forceinline__ void moe_gv_chunk(const MoeGvArgs &a, const uint8_t *
   // pass ps from buffer cur; first pass ps + kMoeGvD - 1 is issued into nxt (the buffer of pass
   // ps - 1, already consumed), so kMoeGvD - 1 passes stay in flight while a pass computes
   auto pass = [&](int ps, uint32_t (&cur)[U][PD], uint32_t (&nxt)[U][PD]) {
-    if (ps + kMoeGvD - 1 < npass) load_pass(ps + kMoeGvD - 1, nxt);
+    // issued on every pass (the last ones re-read the chunk's last pass): the same loads on every
+    // path, so the waits below leave the next passes in flight
+    load_pass(ps + kMoeGvD - 1 < npass ? ps + kMoeGvD - 1 : npass - 1, nxt);
     float acc[MC];
 #pragma unroll
     for (int m = 0; m < MC; ++m) acc[m] = 0.f;
-    for (int i0 = 0; i0 < npairs; i0 += U) {
-      if (i0 > 0) {  // rows with more than U pairs per lane (long K): the next batch, unprefetched
-        const int col = pass_col(ps);
+    if constexpr (LONG) {
+      for (int i0 = 0; i0 < npairs; i0 += U) {
+        if (i0 > 0) {  // rows with more than U pairs per lane (long K): the next batch, unprefetched
+          const int col = pass_col(ps);
 #pragma unroll
-        for (int u = 0; u < U; ++u) load_pair<FMT>(pair_ptr(col, i0 + u), cur[u]);
+          for (int u = 0; u < U; ++u) load_pair<FMT>(pair_ptr(col, i0 + u), cur[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (i0 + u < npairs) pair_dot<FMT, VYBDQ_Q4_GGML, MC>(cur[u], lds, sx, P, ks + G * (i0 + u), acc);
       }
+    } else {
+      // branch-free: a lane with fewer than U pairs (K not a multiple of 64 G) drops the products
+      // of its clamped re-reads
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (i0 + u < npairs) pair_dot<FMT, VYBDQ_Q4_GGML, MC>(cur[u], lds, sx, P, ks + G * (i0 + u), acc);
+      for (int u = 0; u < U; ++u) {
+        float t[MC];
+#pragma unroll
+        for (int m = 0; m < MC; ++m) t[m] = 0.f;
+        pair_dot<FMT, VYBDQ_Q4_GGML, MC>(cur[u], lds, sx, P, u < npairs ? ks + G * u : (ks < P ? ks : 0), t);
+#pragma unroll
+        for (int m = 0; m < MC; ++m) acc[m] += u < npairs ? t[m] : 0.f;
+      }
     }
 #pragma unroll
     for (int m = 0; m < MC; ++m) acc[m] = group_sum<G>(acc[m]);
@@ -177,15 +197,18 @@ __device__ __forceinline__ void moe_gv_chunk(const MoeGvArgs &a, const uint8_t *
       }
     }
   };
+  // LONG: passes past the chunk are skipped. Otherwise every round runs its kMoeGvD passes (those
+  // past the chunk re-read its last pass and store nothing), so every path issues the same loads
+  // and the compiler's waits keep the next passes in flight.
   for (int ps = 0; ps < npass; ps += kMoeGvD) {
 #pragma unroll
     for (int k = 0; k < kMoeGvD; ++k)
-      if (ps + k < npass) pass(ps + k, ring[k], ring[(k + kMoeGvD - 1) % kMoeGvD]);
+      if (!LONG || ps + k < npass) pass(ps + k, ring[k], ring[(k + kMoeGvD - 1) % kMoeGvD]);
   }
 }
 
 // MCMAX: the largest group (1 when every group holds one row: a single token).
-template <int FMT, int G, int U, bool SWI, int XW, int MCMAX>
+template <int FMT, int G, int U, bool SWI, int XW, int MCMAX, bool LONG>
 __global__ void __launch_bounds__(256) k_moe_gemv(MoeGvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int CPP = moe_gv_cpp(G, SWI);
@@ -222,13 +245,13 @@ __global__ void __launch_bounds__(256) k_moe_gemv(MoeGvArgs a) {
     }
     for (int r = d.y; r < d.z; r += a.mc) {
       if constexpr (MCMAX == 1) {
-        moe_gv_chunk<FMT, G, U, 1, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx);
+        moe_gv_chunk<FMT, G, U, 1, SWI, XW, LONG>(a, Wg, Wu, r, n0, ncols, lds, sx);
       } else {
         switch (d.z - r < a.mc ? d.z - r : a.mc) {
-          case 1: moe_gv_chunk<FMT, G, U, 1, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
-          case 2: moe_gv_chunk<FMT, G, U, 2, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
-          case 3: moe_gv_chunk<FMT, G, U, 3, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
-          default: moe_gv_chunk<FMT, G, U, 4, SWI, XW>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
+          case 1: moe_gv_chunk<FMT, G, U, 1, SWI, XW, LONG>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
+          case 2: moe_gv_chunk<FMT, G, U, 2, SWI, XW, LONG>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
+          case 3: moe_gv_chunk<FMT, G, U, 3, SWI, XW, LONG>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
+          default: moe_gv_chunk<FMT, G, U, 4, SWI, XW, LONG>(a, Wg, Wu, r, n0, ncols, lds, sx); break;
         }
       }
     }
@@ -236,9 +259,9 @@ __global__ void __launch_bounds__(256) k_moe_gemv(MoeGvArgs a) {
   }
 }
 
-template <int FMT, int G, int U, bool SWI, int XW, int MCMAX>
+template <int FMT, int G, int U, bool SWI, int XW, int MCMAX, bool LONG>
 int moe_gemv_launch2(const MoeGvArgs &a, int max_groups, hipStream_t s) {
-  const void *fn = reinterpret_cast<const void *>(&k_moe_gemv<FMT, G, U, SWI, XW, MCMAX>);
+  const void *fn = reinterpret_cast<const void *>(&k_moe_gemv<FMT, G, U, SWI, XW, MCMAX, LONG>);
   const size_t lds = static_cast<size_t>(a.mc) * a.P * XSTAGE_PAIR_BYTES;
   if (lds > 64 * 1024) {
     static std::atomic<uint64_t> raised{0};
@@ -251,7 +274,7 @@ int moe_gemv_launch2(const MoeGvArgs &a, int max_groups, hipStream_t s) {
     if (a.cols_per_wg % CPP) return set_error(VYBDQ_ERR_SHAPE, "moe gemv: columns per workgroup not a multiple of the pass");
     const int bs = a.cols_per_wg / CPP;
     const int64_t grid = static_cast<int64_t>(max_groups) * ((spg + bs - 1) / bs);
-    hipLaunchKernelGGL((k_moe_gemv<FMT, G, U, SWI, XW, MCMAX>), dim3(static_cast<unsigned>(grid)), dim3(256), lds, s, a);
+    hipLaunchKernelGGL((k_moe_gemv<FMT, G, U, SWI, XW, MCMAX, LONG>), dim3(static_cast<unsigned>(grid)), dim3(256), lds, s, a);
     return check_launch("moe grouped gemv");
   }
   int per_cu = a.wg_per_cu;
@@ -267,44 +290,47 @@ int moe_gemv_launch2(const MoeGvArgs &a, int max_groups, hipStream_t s) {
   const int64_t units = static_cast<int64_t>(max_groups) * spg;
   int64_t grid = static_cast<int64_t>(per_cu) * device_cu_count();
   grid = grid < units ? grid : units;
-  hipLaunchKernelGGL((k_moe_gemv<FMT, G, U, SWI, XW, MCMAX>), dim3(static_cast<unsigned>(grid)), dim3(256), lds, s, a);
+  hipLaunchKernelGGL((k_moe_gemv<FMT, G, U, SWI, XW, MCMAX, LONG>), dim3(static_cast<unsigned>(grid)), dim3(256), lds, s, a);
   return check_launch("moe grouped gemv");
 }
 
-template <int FMT, int G, int U, bool SWI, int XW>
+template <int FMT, int G, int U, bool SWI, int XW, bool LONG = false>
 int moe_gemv_launch1(const MoeGvArgs &a, int max_groups, hipStream_t s) {
-  return a.mc == 1 ? moe_gemv_launch2<FMT, G, U, SWI, XW, 1>(a, max_groups, s)
-                   : moe_gemv_launch2<FMT, G, U, SWI, XW, kMoeGvMC>(a, max_groups, s);
+  return a.mc == 1 ? moe_gemv_launch2<FMT, G, U, SWI, XW, 1, LONG>(a, max_groups, s)
+                   : moe_gemv_launch2<FMT, G, U, SWI, XW, kMoeGvMC, LONG>(a, max_groups, s);
 }
 
 // gate|up (swi): 32 lanes per row; down: 16. The pair batch covers a row's pairs per lane (at
-// most 4 pairs in flight per lane; longer rows take extra unprefetched batches).
+// most 4 pairs in flight per lane; longer rows take extra unprefetched batches: U = 5 below).
 template <int FMT>
 int moe_gemv_launch(bool swi, const MoeGvArgs &a, int max_groups, hipStream_t s) {
   const int G = swi ? 32 : 16;
   int U = (a.P + G - 1) / G;
-  U = U < 1 ? 1 : (U > 4 ? 4 : U);
+  U = U < 1 ? 1 : (U > 4 ? 5 : U);
   if (swi) {
     if (a.xdt == VYBDQ_F32) {
       switch (U) {
         case 1: return moe_gemv_launch1<FMT, 32, 1, true, 8>(a, max_groups, s);
         case 2: return moe_gemv_launch1<FMT, 32, 2, true, 8>(a, max_groups, s);
         case 3: return moe_gemv_launch1<FMT, 32, 3, true, 8>(a, max_groups, s);
-        default: return moe_gemv_launch1<FMT, 32, 4, true, 8>(a, max_groups, s);
+        case 4: return moe_gemv_launch1<FMT, 32, 4, true, 8>(a, max_groups, s);
+        default: return moe_gemv_launch1<FMT, 32, 4, true, 8, true>(a, max_groups, s);
       }
     }
     switch (U) {
       case 1: return moe_gemv_launch1<FMT, 32, 1, true, 4>(a, max_groups, s);
       case 2: return moe_gemv_launch1<FMT, 32, 2, true, 4>(a, max_groups, s);
       case 3: return moe_gemv_launch1<FMT, 32, 3, true, 4>(a, max_groups, s);
-      default: return moe_gemv_launch1<FMT, 32, 4, true, 4>(a, max_groups, s);
+      case 4: return moe_gemv_launch1<FMT, 32, 4, true, 4>(a, max_groups, s);
+      default: return moe_gemv_launch1<FMT, 32, 4, true, 4, true>(a, max_groups, s);
     }
   }
   switch (U) {  // down: X is the fp16 activations
     case 1: return moe_gemv_launch1<FMT, 16, 1, false, 4>(a, max_groups, s);
     case 2: return moe_gemv_launch1<FMT, 16, 2, false, 4>(a, max_groups, s);
     case 3: return moe_gemv_launch1<FMT, 16, 3, false, 4>(a, max_groups, s);
-    default: return moe_gemv_launch1<FMT, 16, 4, false, 4>(a, max_groups, s);
+    case 4: return moe_gemv_launch1<FMT, 16, 4, false, 4>(a, max_groups, s);
+    default: return moe_gemv_launch1<FMT, 16, 4, false, 4, true>(a, max_groups, s);
   }
 }
 
