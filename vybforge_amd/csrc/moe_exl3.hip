@@ -371,8 +371,11 @@ __global__ void __launch_bounds__(256) k_mx_gemm(const MxGemmArgs a, const MxSha
   const _Float16 *xsrc = a.xp + (static_cast<int64_t>(p) * a.rows + r0) * K + 16 * static_cast<int64_t>(kb_begin);
   const int krows = 16 * nkb;
 
-  // BP <= 2: the rows' (x', x') pairs of the split in LDS; rows past the group read as zero. The
-  // first four 16-byte reads per thread go out before the trellis ring (loads return in order).
+  // BP <= 2: the rows' (x', x') pairs of the split in LDS; rows past the group read as zero. All
+  // of a thread's 16-byte reads (at most 8: the stage holds at most 64 KB, nc <= 2048) go out
+  // before the trellis ring (loads return in order), and none after it: x loads issued after the
+  // ring (a staging loop) made the compiler wait for the whole ring at the top of every k-loop
+  // iteration.
   const int per_row = krows / 8;
   const int nc = HALVES ? BP * per_row : 0;
   auto x_chunk = [&](int i) {
@@ -388,12 +391,13 @@ __global__ void __launch_bounds__(256) k_mx_gemm(const MxGemmArgs a, const MxSha
     d[0] = u4{dup(v[0]), dup(v[0] >> 16), dup(v[1]), dup(v[1] >> 16)};
     d[1] = u4{dup(v[2]), dup(v[2] >> 16), dup(v[3]), dup(v[3] >> 16)};
   };
-  u4 xv4[4];
+  constexpr int XV = HALVES ? 8 : 1;
+  u4 xv[XV];
   if constexpr (HALVES) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < XV; ++u) {
       const int i = threadIdx.x + 256 * u;
-      if (i < nc) xv4[u] = x_chunk(i);
+      if (i < nc) xv[u] = x_chunk(i);
     }
   }
   // larger groups: the matrix-core A values of k-block kk: x' row lane & 15 (zero past the group),
@@ -417,16 +421,9 @@ __global__ void __launch_bounds__(256) k_mx_gemm(const MxGemmArgs a, const MxSha
     if constexpr (!HALVES) aring[d] = load_a(w_begin + d);
   }
   if constexpr (HALVES) {
-    for (int i0 = threadIdx.x;;) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (i0 + 256 * u < nc) x_store(i0 + 256 * u, xv4[u]);
-      i0 += 4 * 256;
-      if (i0 >= nc) break;
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (i0 + 256 * u < nc) xv4[u] = x_chunk(i0 + 256 * u);
-    }
+    for (int u = 0; u < XV; ++u)
+      if (threadIdx.x + 256 * u < nc) x_store(threadIdx.x + 256 * u, xv[u]);
     __syncthreads();
   }
 
