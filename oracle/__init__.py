@@ -23,7 +23,16 @@ repository root):
                             native/glm53/moe_ref.py:25-112, native/kernels/moe.vyb:1-170
   matmul   fp64 GEMV/GEMM gates and the tolerance metric
                             native/kernels/rgemv.vyb:13-15,359-366, native/tools/gen_rpf.py:2-8,
-                            native/glm53/verify_layer0.py:134-139
+                            native/glm53/verify_layer0.py:134-139; the xq8-activation GEMV
+                            gate (gemv_xq8_f64) of gemv_iq2s_q / gemv_q4k_q / gemv_q5k_q
+                            (native/kernels/rgemv7.vyb:3-96, rq4kq.vyb:7-274, rq5kq.vyb:8-268)
+  kquants  Q4_K / Q5_K / Q6_K decode
+                            native/kernels/q4k.vyb:1-70, native/tools/q4k_ref.py:37-60,
+                            native/tools/q5k_ref.py, native/gguf/q6k_verify.py:20-40
+  iquants  IQ2_S decode     native/kernels/rgemv.vyb:24-80, native/tools/iq2_s_ref.py,
+                            grid as native/gguf/iq2s_tables.py holds it
+  producers RMSNorm / SwiGLU with the q8 copy (rms_blkg VYB_RMSQ8, silu32q VYB_SWQ8)
+                            native/kernels/layer.vyb:989-1066,1551-1590, vmath.vyb:7-40
 
 Pinning (what checks each function, all under tests/):
   q4_0 decode      the reference's frozen GGUF fixture block (interleaved order) and
@@ -44,4 +53,20 @@ Pinning (what checks each function, all under tests/):
   moe              the reference's committed MoE goldens (routing ids/weights, and the
                    block output on a column slice).                      -> pinned
   matmul           fp64 numpy matmul (invariant).                        -> pinned
+  gemv_xq8_f64     against the reference kernels' factored integer form
+                   (sum_b dw*dx*sum q_w q_x) and against the exact GEMV when x
+                   quantizes losslessly.                                 -> pinned
+  kquants          blocks assembled byte by byte from the layout description
+                   against closed-form per-element values; scale/min packing round
+                   trip; Q5_K without high bits = Q4_K; Q6_K exact in float32
+                   (tests/test_kquant_oracle.py).                        -> pinned
+  iquants          grid structure (magnitudes in {8, 25, 43}) and byte-assembled
+                   IQ2_S blocks against closed-form values
+                   (tests/test_iquant_oracle.py).                        -> pinned
+  producers        seeded Newton sqrt against the reference's 24-step loop and the
+                   correctly rounded sqrt; ordered sums against exact integer and
+                   rational sums; the reference's exp within its stated 1e-9 of libm;
+                   RMSNorm closed form; the q8 copy is xq8
+                   (tests/test_producers_oracle.py).                     -> pinned
+Every function above is pinned; none is "parity unpinned".
 """

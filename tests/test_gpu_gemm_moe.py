@@ -282,6 +282,19 @@ def test_moe_layer_grouped_mfma(dev, ty, T, shared):
     assert matmul.rel_maxnorm(out, ref) < TOL
 
 
+@pytest.mark.parametrize("T,rows4", [(2, None), (3, None), (4, None), (7, "64"), (16, "64"), (17, "64"),
+                                     (40, "64")])
+@pytest.mark.parametrize("shared", [True, False])
+def test_moe_layer_q4_four_row_tiles(dev, monkeypatch, T, rows4, shared):
+    """q4_0 on 4-row tiles (the LDS-staged body with four stages): by default while the experts hit
+    average at most two rows (T <= 4 here), forced above (VYBDQ_MOE_ROWS4), where experts hold
+    several 4-row tiles, tiles end mid-tile, and the shared expert spans ceil(T / 4) tiles."""
+    if rows4:
+        monkeypatch.setenv("VYBDQ_MOE_ROWS4", rows4)
+    out, ref = moe_case(dev, ops.GGML_Q4_0, T, H=512, I=256, E=8, k=4, seed=400 + T, shared=shared)
+    assert matmul.rel_maxnorm(out, ref) < TOL
+
+
 @pytest.mark.parametrize("T,mt", [(7, "1"), (17, "1"), (40, "2")])
 def test_moe_layer_q4_register_body(dev, monkeypatch, T, mt):
     """q4_0 through the register-operand body (VYBDQ_MOE_LDS=0) at both m-tile heights."""

@@ -550,6 +550,15 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
     int MT = wtype == 2 ? (T * topk <= 20 * E ? 1 : 2) : (T > 16 ? 2 : 1);
     if (const char *e = tuning_env("VYBDQ_MOE_MT")) MT = atoi(e) == 1 ? 1 : 2;
     const int n = static_cast<int>(T * topk);
+    // q4_0 with few rows per expert: 4-row tiles on the LDS-staged body (a smaller X stage, one more
+    // weight stage in flight) while the experts hit average at most ROWS4 rows; the shared expert's
+    // T rows then take ceil(T / 4) tiles over its weights. VYBDQ_MOE_ROWS4 overrides the bound
+    // (0: never).
+    const char *lds_env = tuning_env("VYBDQ_MOE_LDS");
+    int rows4_max = 2;
+    if (const char *e = tuning_env("VYBDQ_MOE_ROWS4")) rows4_max = atoi(e);
+    const int64_t hit = E < T * topk ? E : T * topk;
+    const bool rows4 = wtype == 2 && MT == 1 && !(lds_env && lds_env[0] == '0') && T * topk <= rows4_max * hit;
     const bool shared = s_gate != 0;
     int *idx = idx_out ? reinterpret_cast<int *>(idx_out) : m.idx;
     float *wts = w_out ? reinterpret_cast<float *>(w_out) : m.w;
@@ -572,8 +581,9 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
     int mc = kMoeGvMC;  // tokens per GEMV group (experts with more rows: several groups)
     if (const char *e = tuning_env("VYBDQ_MOE_GEMV_MC")) mc = atoi(e) < 1 ? 1 : (atoi(e) > kMoeGvMC ? kMoeGvMC : atoi(e));
     if (mc > T) mc = static_cast<int>(T);  // no group holds more rows than there are tokens
-    // tiles: m-tiles of 16 MT rows for the MFMA GEMM; tiles2: groups of at most mc rows for the GEMV
-    const int BMr = 16 * MT;
+    // tiles: m-tiles of 16 MT (or 4) rows for the MFMA GEMM; tiles2: groups of at most mc rows for
+    // the GEMV
+    const int BMr = rows4 ? 4 : 16 * MT;
     if (fused_route) {
       const void *lg = reinterpret_cast<const void *>(logits);
       const float *bs = reinterpret_cast<const float *>(bias);
@@ -699,6 +709,7 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       g.W2s = reinterpret_cast<const uint8_t *>(s_up);
       g.tiles = m.tiles;
       g.ntiles = m.ntiles;
+      g.tile_rows = rows4 ? 4 : 0;
       int gxdt = x_dt;
       if (x_dt != VYBDQ_F16) {
         // f32 / bf16 x: an fp16 copy with a power-of-two scale per token, so that the GEMM streams X

@@ -20,6 +20,7 @@ struct MoeMmArgs {
   const uint8_t *Ws, *W2s;  // the shared expert's matrices
   const int4 *tiles;        // m-tile list {expert, r0, r1, m-tile}
   const int *ntiles;        // number of listed m-tiles
+  int tile_rows;            // 4: the list holds 4-row tiles (LDS-staged body only); 0: 16 MT rows
 };
 
 constexpr int kMoeNF = 2;          // fragments (pairs for SWI) per wave
@@ -83,23 +84,30 @@ namespace vybdq {
 // exactly as the body above does (same k-slot assignment, same X fragments).
 constexpr int kMlRun = 8 * 18;  // bytes per row per stage (q4_0, two super-steps)
 
-// R weight rows per workgroup (256: 1 workgroup per CU; 128: 2), MT 16-row m-fragments
-template <int R, int MT> struct MlShape {
+// R weight rows per workgroup (256: 1 workgroup per CU; 128: 2), MT 16-row m-fragments, XR token
+// rows staged per tile: 16 (MT m-fragments of 16 rows, three stages in flight) or 4 (one m-fragment
+// whose A operand repeats the tile's 4 rows: the X part of a stage shrinks from 8 KB to 2 KB, so four
+// stages fit the same LDS and three stay in flight while one computes)
+template <int R, int MT, int XR = 16> struct MlShape {
+  static_assert(XR == 16 || (XR == 4 && MT == 1), "4-row tiles: one m-fragment");
   static constexpr int STAGE_W = R * kMlRun;
-  static constexpr int STAGE = STAGE_W + 2 * MT * 4096;  // + the X chunks of the two super-steps
+  static constexpr int XB = XR == 16 ? MT * 4096 : 1024;  // X bytes per super-step
+  static constexpr int STAGE = STAGE_W + 2 * XB;         // + the X chunks of the two super-steps
   static constexpr int J = STAGE_W / 1024;             // direct-to-LDS weight loads per stage
   static constexpr int NB = R / 64;                    // B fragments per wave per super-step
-  static constexpr int PER_CU = 3 * STAGE <= 80 * 1024 ? 2 : 1;
+  static constexpr int NS = XR == 4 ? 4 : 3;           // stage buffers
+  static constexpr int PER_CU = NS * STAGE <= 80 * 1024 ? 2 : 1;
 };
 
-template <int R, int MT, bool SWI>
-__global__ void __launch_bounds__(256, (MlShape<R, MT>::PER_CU)) k_moe_mm_lds(MoeMmArgs g) {
-  using Sh = MlShape<R, MT>;
-  constexpr int STAGE = Sh::STAGE, STAGE_W = Sh::STAGE_W, J = Sh::J, NB = Sh::NB;
+template <int R, int MT, bool SWI, int XR = 16>
+__global__ void __launch_bounds__(256, (MlShape<R, MT, XR>::PER_CU)) k_moe_mm_lds(MoeMmArgs g) {
+  using Sh = MlShape<R, MT, XR>;
+  constexpr int STAGE = Sh::STAGE, STAGE_W = Sh::STAGE_W, J = Sh::J, NB = Sh::NB, XB = Sh::XB, NS = Sh::NS;
   // one array per stage: the weight rows, then the X chunks of its two super-steps
   __shared__ __attribute__((aligned(16))) uint8_t s0[STAGE];
   __shared__ __attribute__((aligned(16))) uint8_t s1[STAGE];
   __shared__ __attribute__((aligned(16))) uint8_t s2[STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t s3[NS > 3 ? STAGE : 16];
   constexpr int COLS = SWI ? R / 2 : R;  // output columns per workgroup
   constexpr int NF = SWI ? NB / 2 : NB;  // fragments per wave per matrix
   const int n_tiles = g.m.N / COLS;
@@ -116,8 +124,10 @@ __global__ void __launch_bounds__(256, (MlShape<R, MT>::PER_CU)) k_moe_mm_lds(Mo
     Wa = g.m.W + static_cast<int64_t>(d.x) * g.w_stride;
     Wb = SWI ? g.m.W2 + static_cast<int64_t>(d.x) * g.w_stride : Wa;
   }
-  a.M = d.z;  // rows at or past r1 are clamped on load and skipped on store
-  const int row0 = d.y + d.w * 16 * MT;
+  const int row0 = d.y + d.w * (XR == 4 ? 4 : 16 * MT);
+  // rows at or past r1 (and, with 4-row tiles, past the tile's 4 rows) are clamped on load and
+  // skipped on store
+  a.M = XR == 4 && row0 + 4 < d.z ? row0 + 4 : d.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int gq = lane >> 4, nl = lane & 15;
@@ -140,21 +150,34 @@ __global__ void __launch_bounds__(256, (MlShape<R, MT>::PER_CU)) k_moe_mm_lds(Mo
     wsrc[jj] = up ? Wb : Wa;
     woff[jj] = static_cast<uint32_t>(static_cast<int64_t>(col) * a.rowbytes) + 16u * c;
   }
-  // X chunks: thread (w, lane) stages chunk (i, t = w): row row0 + 16 i + nl, k = 128 s + 32 gq + 8 w
-  uint32_t xoff[MT];
-#pragma unroll
-  for (int i = 0; i < MT; ++i) {
-    int r = row0 + 16 * i + nl;
+  // X chunks. XR = 16: thread (w, lane) stages chunk (i, t = w): row row0 + 16 i + nl, k = 128 s +
+  // 32 gq + 8 w. XR = 4: waves 2 and 3 stage super-steps 0 and 1 of a stage (at R = 128 waves 0 and 1
+  // issue one weight load more, so every wave issues five per stage); lane L takes row L / 16 and
+  // 16-byte chunk (L % 16) ^ (L / 16) of the super-step, so chunk c of row r sits at 16-byte slot
+  // 16 r + (c ^ r): the A reads of one step (rows r < 4, chunks 4 gq + t) fall on 16 distinct slots.
+  uint32_t xoff[XR == 4 ? 1 : MT];
+  if constexpr (XR == 4) {
+    const int rr = lane >> 4;
+    int r = row0 + rr;
     r = r < a.M ? r : a.M - 1;
     const int xr = a.row_map ? a.row_map[r] : r;
-    xoff[i] = static_cast<uint32_t>(static_cast<int64_t>(xr) * a.ldx) + 32 * gq + 8 * w;
+    xoff[0] = static_cast<uint32_t>(static_cast<int64_t>(xr) * a.ldx) + 8 * ((lane & 15) ^ rr);
+  } else {
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      int r = row0 + 16 * i + nl;
+      r = r < a.M ? r : a.M - 1;
+      const int xr = a.row_map ? a.row_map[r] : r;
+      xoff[i] = static_cast<uint32_t>(static_cast<int64_t>(xr) * a.ldx) + 32 * gq + 8 * w;
+    }
   }
   // stage buffer B, chosen at compile time
   auto sb = [&](auto bi) -> uint8_t * {
     constexpr int B = decltype(bi)::value;
     if constexpr (B == 0) return s0;
     else if constexpr (B == 1) return s1;
-    else return s2;
+    else if constexpr (B == 2) return s2;
+    else return s3;
   };
   // Direct-to-LDS loads issued from asm (M0 = the wave-uniform LDS base): the compiler does not
   // track them, so it adds no waits of its own before the LDS reads (it merges its direct-to-LDS
@@ -170,15 +193,22 @@ __global__ void __launch_bounds__(256, (MlShape<R, MT>::PER_CU)) k_moe_mm_lds(Mo
 #pragma unroll
     for (int jj = 0; jj < JW; ++jj)
       if (jj < nj) dma(wsrc[jj] + kb + woff[jj], sb(bi) + (w + 4 * jj) * 1024);
+    if constexpr (XR == 4) {
+      if (w >= 2)
+        dma(static_cast<const uint16_t *>(a.X) + xoff[0] + static_cast<uint32_t>(2 * st + w - 2) * 128u,
+            sb(bi) + STAGE_W + (w - 2) * XB);
+    } else {
 #pragma unroll
-    for (int ss = 0; ss < 2; ++ss) {
-      const uint32_t k = static_cast<uint32_t>(2 * st + ss) * 128u;
+      for (int ss = 0; ss < 2; ++ss) {
+        const uint32_t k = static_cast<uint32_t>(2 * st + ss) * 128u;
 #pragma unroll
-      for (int i = 0; i < MT; ++i)
-        dma(static_cast<const uint16_t *>(a.X) + xoff[i] + k, sb(bi) + STAGE_W + ss * MT * 4096 + (i * 4 + w) * 1024);
+        for (int i = 0; i < MT; ++i)
+          dma(static_cast<const uint16_t *>(a.X) + xoff[i] + k, sb(bi) + STAGE_W + ss * XB + (i * 4 + w) * 1024);
+      }
     }
   };
-  // vmcnt wait leaving the loads of `later` stages in flight (a wave issues nj + 2 MT per stage)
+  // vmcnt wait leaving the loads of `later` stages in flight (a wave issues nj + 2 MT loads per
+  // stage; with 4-row tiles nj, plus one on waves 2 and 3)
   auto wait_stages = [&](auto later) {
     constexpr int K = decltype(later)::value;
     auto wait_vm = [](auto n) {
@@ -186,8 +216,15 @@ __global__ void __launch_bounds__(256, (MlShape<R, MT>::PER_CU)) k_moe_mm_lds(Mo
       static_assert(N >= 0 && N < 64, "vmcnt range");
       __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
     };
-    if (nj == JW) wait_vm(std::integral_constant<int, K * (JW + 2 * MT)>{});
-    else wait_vm(std::integral_constant<int, K * (JW - 1 + 2 * MT)>{});
+    if constexpr (XR == 4) {
+      const int per = nj + (w >= 2 ? 1 : 0);  // JW - 1, JW or JW + 1
+      if (per == JW + 1) wait_vm(std::integral_constant<int, K * (JW + 1)>{});
+      else if (per == JW) wait_vm(std::integral_constant<int, K * JW>{});
+      else wait_vm(std::integral_constant<int, K * (JW - 1)>{});
+    } else {
+      if (nj == JW) wait_vm(std::integral_constant<int, K * (JW + 2 * MT)>{});
+      else wait_vm(std::integral_constant<int, K * (JW - 1 + 2 * MT)>{});
+    }
   };
   auto bar = [] {
     asm volatile("" ::: "memory");
@@ -225,17 +262,23 @@ __global__ void __launch_bounds__(256, (MlShape<R, MT>::PER_CU)) k_moe_mm_lds(Mo
 #pragma unroll
         for (int k = 0; k < 5; ++k) win[f][k] = p[k];
       }
-      const uint8_t *abase = sb(bi) + STAGE_W + ss * MT * 4096;
+      const uint8_t *abase = sb(bi) + STAGE_W + ss * XB;
+      // A fragment (m-fragment i, step t): XR = 16 in fragment order; XR = 4 the tile's row nl % 4
+      const int xr4 = nl & 3;
+      auto aoff = [&](int i, int t) {
+        if constexpr (XR == 4) return 256 * xr4 + 16 * ((4 * gq + t) ^ xr4);
+        else return ((i * 4 + t) * 64 + lane) * 16;
+      };
       hf8 af[2][MT];
 #pragma unroll
-      for (int i = 0; i < MT; ++i) af[0][i] = *reinterpret_cast<const hf8 *>(abase + (i * 4 * 64 + lane) * 16);
+      for (int i = 0; i < MT; ++i) af[0][i] = *reinterpret_cast<const hf8 *>(abase + aoff(i, 0));
       hf8 bcur = dequant_step<FMT_Q4_0>(win[0], 0, sel, shd);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         if (t < 3) {
 #pragma unroll
           for (int i = 0; i < MT; ++i)
-            af[(t + 1) & 1][i] = *reinterpret_cast<const hf8 *>(abase + ((i * 4 + t + 1) * 64 + lane) * 16);
+            af[(t + 1) & 1][i] = *reinterpret_cast<const hf8 *>(abase + aoff(i, t + 1));
         }
 #pragma unroll
         for (int f = 0; f < NB; ++f) {
@@ -256,14 +299,18 @@ __global__ void __launch_bounds__(256, (MlShape<R, MT>::PER_CU)) k_moe_mm_lds(Mo
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  // stage i is in buffer i % NS; the issue of stage i + NS - 1 reuses the buffer of stage i - 1,
+  // whose readers finished at the previous iteration's closing barrier
   issue(I0{}, 0);
   if (S2 > 1) issue(I1{}, 1);
-  // stage i is in buffer i % 3; the issue of stage i + 2 reuses the buffer of stage i - 1, whose
-  // readers finished at the previous iteration's closing barrier
+  if (NS > 3 && S2 > 2) issue(I2{}, 2);
   auto iter = [&](auto bi, int i) {
     constexpr int B = decltype(bi)::value;
-    if (i + 2 < S2) {
-      issue(std::integral_constant<int, (B + 2) % 3>{}, i + 2);
+    if (i + NS - 1 < S2) {
+      issue(std::integral_constant<int, (B + NS - 1) % NS>{}, i + NS - 1);
+      wait_stages(std::integral_constant<int, NS - 1>{});
+    } else if (NS > 3 && i + 2 < S2) {
       wait_stages(I2{});
     } else if (i + 1 < S2) {
       wait_stages(I1{});
@@ -275,23 +322,35 @@ __global__ void __launch_bounds__(256, (MlShape<R, MT>::PER_CU)) k_moe_mm_lds(Mo
     bar();
   };
   int i = 0;
-  for (; i + 3 <= S2; i += 3) {
-    iter(I0{}, i);
-    iter(I1{}, i + 1);
-    iter(I2{}, i + 2);
+  if constexpr (NS == 4) {
+    for (; i + 4 <= S2; i += 4) {
+      iter(I0{}, i);
+      iter(I1{}, i + 1);
+      iter(I2{}, i + 2);
+      iter(I3{}, i + 3);
+    }
+    if (i < S2) iter(I0{}, i);
+    if (i + 1 < S2) iter(I1{}, i + 1);
+    if (i + 2 < S2) iter(I2{}, i + 2);
+  } else {
+    for (; i + 3 <= S2; i += 3) {
+      iter(I0{}, i);
+      iter(I1{}, i + 1);
+      iter(I2{}, i + 2);
+    }
+    if (i < S2) iter(I0{}, i);
+    if (i + 1 < S2) iter(I1{}, i + 1);
   }
-  if (i < S2) iter(I0{}, i);
-  if (i + 1 < S2) iter(I1{}, i + 1);
 
   const int fb = (n0 >> 4) + w * NF;
   mm_finish<MT, NF, NF, 4, SWI>(a, nullptr, 0, 0, row0, fb, acc);
 }
 
-template <int R, int MT, bool SWI>
+template <int R, int MT, bool SWI, int XR = 16>
 int moe_mm_lds_launch(const MoeMmArgs &g, int max_tiles, hipStream_t s) {
   constexpr int COLS = SWI ? R / 2 : R;
   const int64_t units = static_cast<int64_t>(max_tiles) * (g.m.N / COLS);
-  hipLaunchKernelGGL((k_moe_mm_lds<R, MT, SWI>), dim3(static_cast<unsigned>(units)), dim3(256), 0, s, g);
+  hipLaunchKernelGGL((k_moe_mm_lds<R, MT, SWI, XR>), dim3(static_cast<unsigned>(units)), dim3(256), 0, s, g);
   return check_launch("moe grouped gemm (LDS weights)");
 }
 

@@ -8,6 +8,11 @@ int moe_mm_q4(int xdt, int mt, bool swi, const MoeMmArgs &g, int max_tiles, hipS
   // through LDS (VYBDQ_MOE_LDS=0 under VYBDQ_TUNING keeps the register-operand body)
   const char *e = tuning_env("VYBDQ_MOE_LDS");
   const bool lds_off = e && e[0] == '0';
+  if (g.tile_rows == 4) {  // 4-row tiles: the LDS-staged body with four stages
+    if (mt != 1 || !moe_mm_lds_ok(FMT_Q4_0, xdt, swi, g))
+      return set_error(VYBDQ_ERR_SHAPE, "moe grouped gemm: 4-row tiles need the LDS-staged body");
+    return swi ? moe_mm_lds_launch<128, 1, true, 4>(g, max_tiles, s) : moe_mm_lds_launch<128, 1, false, 4>(g, max_tiles, s);
+  }
   if (!lds_off && mt == 1 && moe_mm_lds_ok(FMT_Q4_0, xdt, swi, g))
     return swi ? moe_mm_lds_launch<128, 1, true>(g, max_tiles, s) : moe_mm_lds_launch<128, 1, false>(g, max_tiles, s);
   if (swi) {

@@ -4,6 +4,7 @@
 namespace vybdq {
 
 int moe_mm_q8(int xdt, int mt, bool swi, const MoeMmArgs &g, int max_tiles, hipStream_t s) {
+  if (g.tile_rows == 4) return set_error(VYBDQ_ERR_SHAPE, "moe grouped gemm: 4-row tiles are q4_0 only");
   if (swi) {
     switch (xdt) {
       case VYBDQ_F32: return mt == 1 ? moe_mm_launch<FMT_Q8_0, VYBDQ_F32, 1, true>(g, max_tiles, s)
