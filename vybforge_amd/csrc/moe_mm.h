@@ -300,26 +300,20 @@ __global__ void __launch_bounds__(256, (MlShape<R, MT, XR>::PER_CU)) k_moe_mm_ld
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
-  // stage i is in buffer i % NS; the issue of stage i + NS - 1 reuses the buffer of stage i - 1,
-  // whose readers finished at the previous iteration's closing barrier
+  // stage i is in buffer i % NS. One barrier per stage: it follows every wave's wait for stage i
+  // and every wave's reads of stage i - 1, so right after it stage i + NS - 1 is issued into the
+  // buffer of stage i - 1
   issue(I0{}, 0);
   if (S2 > 1) issue(I1{}, 1);
   if (NS > 3 && S2 > 2) issue(I2{}, 2);
   auto iter = [&](auto bi, int i) {
     constexpr int B = decltype(bi)::value;
-    if (i + NS - 1 < S2) {
-      issue(std::integral_constant<int, (B + NS - 1) % NS>{}, i + NS - 1);
-      wait_stages(std::integral_constant<int, NS - 1>{});
-    } else if (NS > 3 && i + 2 < S2) {
-      wait_stages(I2{});
-    } else if (i + 1 < S2) {
-      wait_stages(I1{});
-    } else {
-      wait_stages(I0{});
-    }
+    if (NS > 3 && i + 2 < S2) wait_stages(I2{});
+    else if (i + 1 < S2) wait_stages(I1{});
+    else wait_stages(I0{});
     bar();
+    if (i + NS - 1 < S2) issue(std::integral_constant<int, (B + NS - 1) % NS>{}, i + NS - 1);
     compute(bi);
-    bar();
   };
   int i = 0;
   if constexpr (NS == 4) {
