@@ -8,7 +8,7 @@ import torch
 
 from oracle import moe
 from tests.conftest import GOLDEN
-from vybforge_amd import ops
+from vybforge_amd import ops, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -43,3 +43,49 @@ def test_router_end_to_end_reference_routing(dev):
     idx, wts = ops.moe_route(logits, 8, torch.from_numpy(g["bias"]).to(dev), float(g["scale"]))
     np.testing.assert_array_equal(idx.cpu().numpy(), g["ref_idx"])
     assert np.abs(wts.cpu().numpy() - g["ref_w"]).max() < 1e-6
+
+
+def test_layer_one_token_router_reference_routing(dev):
+    """The router inside the q4_0 MoE layer at one token with a selection bias (its workgroup form:
+    the sigmoids of all 288 experts over four waves, the selection on wave 0) reproduces the
+    reference's routing of each golden token."""
+    g = np.load(f"{GOLDEN}/moe_golden.npz")
+    E, k, H, I = g["logits"].shape[1], 8, 256, 256
+    rng = np.random.default_rng(3)
+    w = lambda n, kk: torch.from_numpy(synth.q4_0_weights(rng, n, kk)).to(dev)
+    gate = torch.cat([w(I, H) for _ in range(E)])
+    up = torch.cat([w(I, H) for _ in range(E)])
+    down = torch.cat([w(H, I) for _ in range(E)])
+    layer = ops.MoeLayer(ops.GGML_Q4_0, gate, up, down, H, I, E, k, scale=float(g["scale"]),
+                         bias=torch.from_numpy(g["bias"]).to(dev))
+    x = torch.randn(1, H, device=dev).to(torch.bfloat16)
+    for t in range(g["logits"].shape[0]):
+        logits = torch.from_numpy(g["logits"][t:t + 1]).to(dev)
+        _, idx, wts = layer(x, logits, routing=True)
+        np.testing.assert_array_equal(idx.cpu().numpy()[0], g["ref_idx"][t])
+        assert np.abs(wts.cpu().numpy()[0] - g["ref_w"][t]).max() < 1e-6
+
+
+@pytest.mark.parametrize("E", [256, 288, 300, 512, 1024])
+@pytest.mark.parametrize("ldt", [torch.float64, torch.float32, torch.float16, torch.bfloat16])
+def test_layer_one_token_router_equals_wave_router(dev, E, ldt):
+    """The workgroup router of the one-token route + bucket launch (sigmoids over the workgroup,
+    selection on one wave) and the one-wave router of vybdq_moe_route give identical ids and
+    weights for every logit type and expert count (4, 5, 8 and 16 experts per router lane)."""
+    k, H, I = 8, 64, 64
+    rng = np.random.default_rng(E)
+    w = lambda n, kk: torch.from_numpy(synth.q4_0_weights(rng, n, kk)).to(dev)
+    gate = torch.cat([w(I, H) for _ in range(E)])
+    up = torch.cat([w(I, H) for _ in range(E)])
+    down = torch.cat([w(H, I) for _ in range(E)])
+    bias = torch.from_numpy(rng.standard_normal(E).astype(np.float32) * 0.05).to(dev)
+    layer = ops.MoeLayer(ops.GGML_Q4_0, gate, up, down, H, I, E, k, bias=bias)
+    x = torch.randn(1, H, device=dev).to(torch.bfloat16)
+    for rep in range(4):
+        logits = torch.from_numpy(rng.standard_normal((1, E))).to(ldt).to(dev)
+        if rep == 3:  # ties: every logit equal, so the bias alone orders the experts
+            logits = torch.zeros((1, E), dtype=ldt, device=dev)
+        _, idx, wts = layer(x, logits, routing=True)
+        i0, w0 = ops.moe_route(logits, k, bias)
+        torch.cuda.synchronize()
+        assert torch.equal(idx, i0) and torch.equal(wts, w0), rep
