@@ -185,6 +185,10 @@ static PairPlan pair_plan(int fmt, int64_t rows, int P, int64_t M) {
     // narrow G (more pairs per lane) until the grid is resident in one round
     const int64_t resident = 32LL * device_cu_count();
     while (G > 16 && rows * G / 64 > resident) G /= 2;
+    // q4_0 rows of exactly 64 pairs (K = 4096): one pair per lane over a whole wave (no idle lane,
+    // one DPP step more) beats two pairs over half a wave (the decode stack's 2560 x 4096 launch,
+    // full-stack graph: 843.0 -> 832.7 us per token)
+    if (fmt == FMT_Q4_0 && P == 64 && rows <= resident) G = 64;
     const int U = (P + G - 1) / G;
     pl.G = G;
     pl.U = U < umax ? U : umax;
