@@ -38,7 +38,7 @@ QWEN3_4B = dict(hidden=2560, q=4096, kv=1024, inter=9728, layers=36)
 # HBM bytes per decode-stack launch from rocprofv3 FETCH_SIZE / WRITE_SIZE (scaled by a plain
 # copy's counters), averaged over the four launches of a layer: measured by the profile below,
 # not by this run
-STACK_TRAFFIC = dict(bytes_per_launch=14402381, source="profiles/q4_0_gemv_decode_stack.md (rocprofv3 --pmc)")
+STACK_TRAFFIC = dict(bytes_per_launch=14413517, source="profiles/q4_0_gemv_decode_stack.md (rocprofv3 --pmc)")
 
 CONFIGS = ["stack", "stack_chain", "gemv1", "kquant", "xq8", "producers", "router", "exl3", "prefill", "prefill_i8",
            "prefill_kq", "moe", "moe_exl3", "pblock", "copy"]
