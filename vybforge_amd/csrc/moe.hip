@@ -472,7 +472,9 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       // while the grid would hold under two workgroups per CU (VYBDQ_MOE_GEMV_COLS="gate_up,down"
       // overrides; -1: equal ranges). Measured on H = 6144, I = 2048, 256 experts, top-8.
       const int grid_def = T <= 2 ? 0 : -2;
-      int grid_env[2] = {grid_def, grid_def}, cols_env[2] = {0, 0};
+      // q4_0 at one token: the down GEMV at one workgroup per CU (two fit; one, with ranges twice as
+      // long, measured 58.0-58.3 against 59.2-59.6 us per GLM-5 layer)
+      int grid_env[2] = {grid_def, T == 1 && wtype == 2 ? 1 : grid_def}, cols_env[2] = {0, 0};
       if (const char *e = tuning_env("VYBDQ_MOE_GEMV_GRID")) sscanf(e, "%d,%d", &grid_env[0], &grid_env[1]);
       if (const char *e = tuning_env("VYBDQ_MOE_GEMV_COLS")) sscanf(e, "%d,%d", &cols_env[0], &cols_env[1]);
       const int cus = device_cu_count();
