@@ -664,7 +664,9 @@ struct MxSplit {
 static MxSplit mx_splits(int64_t K, int64_t groups, int64_t col_blocks, int BP) {
   const int KB = static_cast<int>(K / 16);
   const int64_t units = groups * col_blocks;
-  int S = static_cast<int>((2048 + units - 1) / units);
+  int64_t target = 2048;  // workgroups (VYBDQ_MX_WGS overrides)
+  if (const char *e = tuning_env("VYBDQ_MX_WGS")) target = atoi(e) > 0 ? atoi(e) : target;
+  int S = static_cast<int>((target + units - 1) / units);
   if (S > 16) S = 16;
   if (S > KB / 8) S = KB / 8;
   if (S < 1) S = 1;
