@@ -215,19 +215,42 @@ __global__ void __launch_bounds__(256) k_moe_route_bucket_w(const void *__restri
   if (threadIdx.x < 64) bucket_rows_wave(idx_lds, T, topk, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2);
 }
 
-// out[t][h] = sum_s w[t,s] * rows[pos[t,s]][h] (+ shared[t][h]); fixed slot order.
+// out[t][h] = sum_s w[t,s] * rows[pos[t,s]][h] (+ shared[t][h]); fixed slot order. Four columns per
+// thread (16-byte row loads, H % 4 == 0), all the slots' loads issued before the sums.
 template <int ODT>
 __global__ void __launch_bounds__(256) k_moe_combine(const float *__restrict__ rows, const float *__restrict__ shared,
                                                      const int *__restrict__ pos, const float *__restrict__ w, int T,
                                                      int topk, int64_t H, void *__restrict__ out) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= T * H) return;
+  const int64_t i4 = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i4 >= T * H / 4) return;
+  const int64_t i = 4 * i4;
   const int t = static_cast<int>(i / H);
   const int64_t h = i % H;
-  float acc = 0.f;
-  for (int s = 0; s < topk; ++s) acc = fmaf(w[t * topk + s], rows[static_cast<int64_t>(pos[t * topk + s]) * H + h], acc);
-  if (shared) acc += shared[i];
-  store_elem<ODT>(out, nullptr, i, acc);
+  f4 acc = {0.f, 0.f, 0.f, 0.f};
+  constexpr int SB = 8;  // slots loaded per round trip
+  for (int s0 = 0; s0 < topk; s0 += SB) {
+    f4 v[SB];
+    float ws[SB];
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      if (s0 + u < topk) {
+        v[u] = *reinterpret_cast<const f4 *>(rows + static_cast<int64_t>(pos[t * topk + s0 + u]) * H + h);
+        ws[u] = w[t * topk + s0 + u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+      if (s0 + u < topk)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = fmaf(ws[u], v[u][j], acc[j]);
+  }
+  if (shared) {
+    const f4 sh = *reinterpret_cast<const f4 *>(shared + i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] += sh[j];
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) store_elem<ODT>(out, nullptr, i + j, acc[j]);
 }
 
 struct MoeWs {
@@ -583,7 +606,7 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       if (rc) return rc;
     }
     const float *shr = shared ? m.rows + static_cast<int64_t>(n) * H : nullptr;
-    const int64_t tot = T * H;
+    const int64_t tot = T * H / 4;  // four columns per thread
     const unsigned gc = static_cast<unsigned>((tot + 255) / 256);
     void *o = reinterpret_cast<void *>(out);
     switch (out_dt) {
@@ -633,7 +656,7 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
     if (rc) return rc;
     shared = m.shared;
   }
-  const int64_t tot = T * H;
+  const int64_t tot = T * H / 4;  // four columns per thread
   const unsigned gc = static_cast<unsigned>((tot + 255) / 256);
   void *o = reinterpret_cast<void *>(out);
   switch (out_dt) {
