@@ -103,6 +103,34 @@ def test_moe_exl3_small(dev, T, xdt, with_shared, with_bias):
         assert matmul.rel_maxnorm(y - sh_ref, ref - sh_ref) < TOL
 
 
+@pytest.mark.parametrize("T", [3, 17])
+def test_moe_exl3_combine_chunks(dev, monkeypatch, T):
+    """Top-10 (two slot groups in the combine) at H = 640 (five 128-column chunks: a partial second
+    group of four); the combine at one chunk and at four chunks per workgroup against the oracle,
+    and the two bit-identical (the same additions in the same order)."""
+    H, I, E, k = 640, 256, 12, 10
+    rng = np.random.default_rng(31 + T)
+    host = [_expert_tensors(rng, H, I) for _ in range(E)]
+    sh = [_bf16(rng, s) for s in ((I, H), (I, H), (H, I))]
+    bias = rng.standard_normal(E).astype(np.float32) * 0.1
+    layer = ops.MoeExl3Layer([_to_dev(h, dev) for h in host], H, I, topk=k,
+                             shared=tuple(t.to(dev) for t, _ in sh), bias=torch.from_numpy(bias).to(dev))
+    x = _x(rng, T, H, "bf16")
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32))
+    mats = lambda e: tuple(exl3.dequant_exl3_f64(host[e][3 * p], host[e][3 * p + 1], host[e][3 * p + 2]).T
+                           for p in range(3))
+    ref, ridx, _ = moe.moe_forward(x.to(torch.float64).numpy(), logits.numpy(), mats, tuple(v for _, v in sh),
+                                   topk=k, bias=bias)
+    ys = []
+    for ch in ("1", "4"):
+        monkeypatch.setenv("VYBDQ_MX_COMB", ch)
+        y, idx, _ = layer(x.to(dev), logits.to(dev), routing=True)
+        np.testing.assert_array_equal(idx.cpu().numpy(), ridx)
+        ys.append(y.cpu().numpy())
+        assert matmul.rel_maxnorm(ys[-1], ref) < TOL, ch
+    np.testing.assert_array_equal(ys[0], ys[1])
+
+
 def test_moe_exl3_out_dtypes_and_f16_x(dev):
     """fp16 activations (two bf16 terms into the shared expert) and bf16 / fp16 outputs."""
     H, I, E, k, T = 256, 128, 6, 2, 9

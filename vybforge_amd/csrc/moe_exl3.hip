@@ -604,11 +604,12 @@ __global__ void __launch_bounds__(64 * kMxRowWaves) k_mx_mid(const uint64_t *__r
 }
 
 // ---- 7. combine -----------------------------------------------------------------------------------
-// grid (T, H / 128 chunks), kMxRowWaves waves: wave j finishes the slots j, j + kMxRowWaves, ... of
-// the token (splits summed, output rotation, svh) into LDS; wave 0 then adds them with their routing
-// weights in slot order, and the shared expert's partials in split order
-constexpr int kMxMaxTopk = 64;
-template <int ODT>
+// grid (T, H / (128 CH)), kMxRowWaves waves, CH 128-column chunks per workgroup. The slots go in
+// groups of kMxRowWaves: wave j finishes slot g + j of the group on every chunk (splits summed, their
+// loads for all chunks issued together; output rotation, svh) into LDS, then wave q < CH adds that
+// group's slots of chunk q with their routing weights in slot order; the shared expert's partials
+// follow in split order. CH = 4 where the grid has workgroups to spare, 1 where it is small
+template <int ODT, int CH>
 __global__ void __launch_bounds__(64 * kMxRowWaves) k_mx_combine(const uint64_t *__restrict__ tab,
                                                                 const int *__restrict__ idx,
                                                                 const int *__restrict__ pos,
@@ -617,27 +618,66 @@ __global__ void __launch_bounds__(64 * kMxRowWaves) k_mx_combine(const uint64_t 
                                                                 const float *__restrict__ ascale, int S, int rows,
                                                                 int64_t H, const float *__restrict__ sh, int Ssh,
                                                                 int T, void *__restrict__ out) {
-  __shared__ f2 zs[kMxMaxTopk][64];
-  const int t = blockIdx.x, c = blockIdx.y, lane = threadIdx.x & 63;
+  __shared__ f2 zs[kMxRowWaves][CH][64];
+  const int t = blockIdx.x, lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int64_t n0 = 128 * static_cast<int64_t>(c) + 2 * lane;
-  for (int sl = wave; sl < topk; sl += kMxRowWaves) {
-    const int i = t * topk + sl;
-    const int e = idx[i], r = pos[i];
-    const f2 z = mx_sum_splits(zd + static_cast<int64_t>(r) * H + n0, static_cast<int64_t>(rows) * H, S);
-    float z0 = z[0] * ascale[r], z1 = z[1] * ascale[r];
-    fwht128_wave(z0, z1);
-    const _Float16 *svd = mx_ptr<_Float16>(tab, e, 2, 2);
-    zs[sl][lane] = f2{z0 * kRScale * static_cast<float>(svd[n0]), z1 * kRScale * static_cast<float>(svd[n0 + 1])};
-  }
-  __syncthreads();
-  if (wave != 0) return;
+  const int nch = static_cast<int>(H / 128);
+  const int c0 = blockIdx.y * CH;
+  const bool adder = wave < CH && c0 + wave < nch;
+  const int64_t n0 = 128 * static_cast<int64_t>(adder ? c0 + wave : 0) + 2 * lane;
   float y0 = 0.f, y1 = 0.f;
-  for (int sl = 0; sl < topk; ++sl) {
-    const float wt = w[t * topk + sl];
-    y0 = fmaf(wt, zs[sl][lane][0], y0);
-    y1 = fmaf(wt, zs[sl][lane][1], y1);
+  for (int g = 0; g < topk; g += kMxRowWaves) {
+    const int sl = g + wave;
+    if (sl < topk) {
+      const int i = t * topk + sl;
+      const int e = idx[i], r = pos[i];
+      const _Float16 *svd = mx_ptr<_Float16>(tab, e, 2, 2);
+      const float as = ascale[r];
+      const float *zr = zd + static_cast<int64_t>(r) * H + 2 * lane;
+      f2 z[CH];
+#pragma unroll
+      for (int q = 0; q < CH; ++q) z[q] = f2{0.f, 0.f};
+      constexpr int U = 8 / CH;  // eight loads per round trip: U splits x every chunk
+      for (int s0 = 0; s0 < S; s0 += U) {
+        f2 v[U][CH];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int q = 0; q < CH; ++q) {
+            const int c = c0 + q < nch ? c0 + q : nch - 1;
+            v[u][q] = s0 + u < S ? *reinterpret_cast<const f2 *>(zr + static_cast<int64_t>(s0 + u) * rows * H + 128 * c)
+                                 : f2{0.f, 0.f};
+          }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (s0 + u < S)
+#pragma unroll
+            for (int q = 0; q < CH; ++q) {
+              z[q][0] += v[u][q][0];
+              z[q][1] += v[u][q][1];
+            }
+      }
+#pragma unroll
+      for (int q = 0; q < CH; ++q) {
+        const int c = c0 + q < nch ? c0 + q : nch - 1;
+        const int64_t m = 128 * static_cast<int64_t>(c) + 2 * lane;
+        float z0 = z[q][0] * as, z1 = z[q][1] * as;
+        fwht128_wave(z0, z1);
+        zs[wave][q][lane] = f2{z0 * kRScale * static_cast<float>(svd[m]), z1 * kRScale * static_cast<float>(svd[m + 1])};
+      }
+    }
+    __syncthreads();
+    if (adder) {
+      const int ng = topk - g < kMxRowWaves ? topk - g : kMxRowWaves;
+      for (int j = 0; j < ng; ++j) {
+        const float wt = w[t * topk + g + j];
+        y0 = fmaf(wt, zs[j][wave][lane][0], y0);
+        y1 = fmaf(wt, zs[j][wave][lane][1], y1);
+      }
+    }
+    __syncthreads();
   }
+  if (!adder) return;
   if (sh) {
     const f2 v = mx_sum_splits(sh + static_cast<int64_t>(t) * H + n0, static_cast<int64_t>(T) * H, Ssh);
     y0 += v[0];
@@ -922,8 +962,13 @@ extern "C" int vybdq_moe_forward_exl3(uint64_t x, int x_dt, uint64_t logits, int
   rc = mx_gemm(p.BP, shared ? 3 : 0, da, shd, 1, p.dn.S, p.max_groups, s);
   if (rc) return rc;
   // 7. combine
+  // four chunks per workgroup once the grid holds 2048 workgroups with them, else one
+  bool wide = T * (H / 512) >= 2048;
+  if (const char *e = tuning_env("VYBDQ_MX_COMB")) wide = e[0] == '4';
+  const int CHn = wide ? 4 : 1;
   VYBDQ_DISPATCH_IN(out_dt, ODT,
-      hipLaunchKernelGGL((k_mx_combine<ODT>), dim3(static_cast<unsigned>(T), static_cast<unsigned>(H / 128)),
+      hipLaunchKernelGGL((wide ? k_mx_combine<ODT, 4> : k_mx_combine<ODT, 1>),
+                         dim3(static_cast<unsigned>(T), static_cast<unsigned>((H / 128 + CHn - 1) / CHn)),
                          dim3(64 * kMxRowWaves), 0, s, tab, idx, m.pos, wts, k, m.zd, m.as, p.dn.S, n, H, shared ? m.sd : nullptr, p.Ssd,
                          static_cast<int>(T), reinterpret_cast<void *>(out)));
   return check_launch("moe exl3 combine");
