@@ -89,3 +89,36 @@ def test_layer_one_token_router_equals_wave_router(dev, E, ldt):
         i0, w0 = ops.moe_route(logits, k, bias)
         torch.cuda.synchronize()
         assert torch.equal(idx, i0) and torch.equal(wts, w0), rep
+
+
+@pytest.mark.parametrize("ty", [ops.GGML_Q4_0, ops.GGML_Q8_0])
+@pytest.mark.parametrize("E,k", [(8, 8), (64, 6), (256, 8), (256, 64)])
+@pytest.mark.parametrize("shared,with_bias", [(True, True), (False, False), (True, False)])
+def test_layer_one_token_routing_in_gemv_equals_routing_launch(dev, monkeypatch, ty, E, k, shared, with_bias):
+    """One token on the grouped GEMV routes inside the gate|up launch (rows in slot order); with
+    VYBDQ_MOE_ROUTE_GV=0 a routing + bucketing launch precedes it (rows in expert order). Ids,
+    weights and outputs are bit-identical for every logit type, with and without the selection
+    bias and the shared expert, topk = E included (H and I multiples of 256: the grouped kernels)."""
+    H, I = 256, 512
+    rng = np.random.default_rng(E * 131 + k + 2 * shared + with_bias)
+    q = synth.q4_0_weights if ty == ops.GGML_Q4_0 else synth.q8_0_weights
+    w = lambda n, kk: torch.from_numpy(q(rng, n, kk)).to(dev)
+    gate = torch.cat([w(I, H) for _ in range(E)])
+    up = torch.cat([w(I, H) for _ in range(E)])
+    down = torch.cat([w(H, I) for _ in range(E)])
+    sh = (w(I, H), w(I, H), w(H, I)) if shared else None
+    bias = torch.from_numpy(rng.standard_normal(E).astype(np.float32) * 0.05).to(dev) if with_bias else None
+    layer = ops.MoeLayer(ty, gate, up, down, H, I, E, k, shared=sh, bias=bias)
+    x = torch.from_numpy(synth.activations(rng, (1, H))).to(torch.bfloat16).to(dev)
+    for ldt in (torch.float64, torch.float32, torch.float16, torch.bfloat16):
+        logits = torch.from_numpy(rng.standard_normal((1, E))).to(ldt).to(dev)
+        got = []
+        for env in ("1", "0"):
+            monkeypatch.setenv("VYBDQ_MOE_ROUTE_GV", env)
+            y, idx, wts = layer(x, logits, routing=True)
+            torch.cuda.synchronize()
+            got.append((y.cpu(), idx.cpu(), wts.cpu()))
+        assert torch.equal(got[0][1], got[1][1]) and torch.equal(got[0][2], got[1][2]), ldt
+        assert torch.equal(got[0][0], got[1][0]), ldt
+        i0, w0 = ops.moe_route(logits, k, bias)
+        assert torch.equal(got[0][1], i0.cpu()) and torch.equal(got[0][2], w0.cpu()), ldt

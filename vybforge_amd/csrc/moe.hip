@@ -439,7 +439,14 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
     // tiles: m-tiles of 16 MT (or 4) rows for the MFMA GEMM; tiles2: groups of at most mc rows for
     // the GEMV
     const int BMr = rows4 ? 4 : 16 * MT;
-    if (fused_route) {
+    // one token on the grouped GEMV (up to 256 experts): the gate|up launch routes the token itself
+    // and writes the ids, weights, rows and groups for the down launch and the combine, so no
+    // routing launch precedes it (VYBDQ_MOE_ROUTE_GV=0 keeps the routing launch)
+    bool route_in_gv = gv && T == 1 && E <= 256 && !tuning_env("VYBDQ_MOE_GEMV_COLS");
+    if (const char *e = tuning_env("VYBDQ_MOE_ROUTE_GV")) route_in_gv = route_in_gv && e[0] != '0';
+    if (route_in_gv) {
+      // routed in the gate|up launch below
+    } else if (fused_route) {
       const void *lg = reinterpret_cast<const void *>(logits);
       const float *bs = reinterpret_cast<const float *>(bias);
       const size_t shb = static_cast<size_t>(2 * E + T * topk) * 4;
@@ -517,6 +524,13 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       ga.ldy = I;
       ga.limit = static_cast<float>(limit);
       ga.mc = mc;
+      if (route_in_gv) {
+        ga.rt = MoeGvRoute{reinterpret_cast<const void *>(logits), logits_dt, reinterpret_cast<const float *>(bias),
+                           static_cast<int>(E), static_cast<int>(topk), shared ? 1 : 0, scale, idx, wts, m.pos,
+                           m.tiles2, m.ntiles2};
+        ga.row_map = nullptr;
+        ga.ldx = 0;  // every row is token 0's
+      }
       rc = wtype == 2 ? moe_gemv_q4(true, ga, max_groups, s) : moe_gemv_q8(true, ga, max_groups, s);
       if (rc) return rc;
       MoeGvArgs gd = ga;
@@ -531,6 +545,7 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       gd.xdt = VYBDQ_F16;
       gd.ldx = I;
       gd.row_map = nullptr;
+      gd.rt = MoeGvRoute{};
       gd.N = static_cast<int>(H);
       gd.cols_per_wg = cols_for(H, moe_gv_cpp(16, false), cols_env[1]);
       gd.wg_per_cu = grid_env[1];

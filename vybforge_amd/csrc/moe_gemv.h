@@ -25,8 +25,23 @@
 // (native/glm53/moe_ref.py:81-84). Otherwise the row sums are stored as f32.
 #pragma once
 #include "gemv_dev.h"
+#include "moe_route.h"
 
 namespace vybdq {
+
+// One token routed inside the gate|up launch (E > 0; see moe_gv_route).
+struct MoeGvRoute {
+  const void *logits;
+  int ldt;                 // F64, F32, F16 or BF16
+  const float *bias;       // selection bias or null
+  int E, topk, shared;     // shared: 1 with a shared expert
+  double scale;
+  int *idx_out;            // [topk] expert ids (workgroup 0 writes them)
+  float *w_out;            // [topk] routing weights
+  int *pos;                // [topk] row of each slot: the slot itself
+  int4 *groups_out;        // the groups below, for the down launch
+  int *ngroups_out;
+};
 
 struct MoeGvArgs {
   const uint8_t *W, *W2;   // expert 0's matrix (SWI: gate, up); expert e at + e * w_stride
@@ -49,6 +64,7 @@ struct MoeGvArgs {
   int64_t ldy;
   float limit;
   int mc;                  // tokens per group (x stage), 1..kMoeGvMC
+  MoeGvRoute rt;           // rt.E > 0: route the token here (one token, gate|up, mc = 1)
 };
 
 constexpr int kMoeGvMC = 4;  // largest x stage
@@ -207,22 +223,77 @@ __device__ __forceinline__ void moe_gv_chunk(const MoeGvArgs &a, const uint8_t *
   }
 }
 
-// MCMAX: the largest group (1 when every group holds one row: a single token).
-template <int FMT, int G, int U, bool SWI, int XW, int MCMAX, bool LONG>
+// LDS bytes of the x stage, and of the routing area after it (RENT experts per router lane):
+// groups (80 x 16 B), slot ids and weights (64 + 64 words), keys and scores (64 RENT x 8 B each)
+__host__ __device__ inline size_t moe_gv_xstage_bytes(int mc, int P) { return (static_cast<size_t>(mc) * P * XSTAGE_PAIR_BYTES + 15) & ~size_t(15); }
+constexpr size_t moe_gv_route_bytes(int RENT) { return RENT ? 1280 + 512 + 2 * 64 * 8 * static_cast<size_t>(RENT) : 0; }
+
+// One token's routing by the workgroup (the router of k_moe_route_bucket_w: route_wg), into the
+// groups of the grouped GEMV in LDS: slot s -> group {idx[s], s, s + 1} (row s), the shared expert
+// -> {-1, topk, topk + 1}. Every workgroup routes the token (the same keys, the same selection);
+// workgroup 0 also writes the ids, weights, rows and groups that the down launch and the combine
+// read. Returns the number of groups.
+template <int RENT>
+__device__ __forceinline__ int moe_gv_route(const MoeGvRoute &r, char *buf) {
+  int4 *grp = reinterpret_cast<int4 *>(buf);
+  int *idl = reinterpret_cast<int *>(buf + 1280);
+  float *wl = reinterpret_cast<float *>(buf + 1536);
+  uint64_t *key = reinterpret_cast<uint64_t *>(buf + 1792);
+  double *score = reinterpret_cast<double *>(key + 64 * RENT);
+  if (threadIdx.x < 64) idl[threadIdx.x] = 0;  // every slot names an expert (topk <= E selects only real ones)
+  switch (r.ldt) {
+    case VYBDQ_F64: route_wg_keys<VYBDQ_F64>(r.logits, r.bias, 0, r.E, key, score); break;
+    case VYBDQ_F16: route_wg_keys<VYBDQ_F16>(r.logits, r.bias, 0, r.E, key, score); break;
+    case VYBDQ_BF16: route_wg_keys<VYBDQ_BF16>(r.logits, r.bias, 0, r.E, key, score); break;
+    default: route_wg_keys<VYBDQ_F32>(r.logits, r.bias, 0, r.E, key, score); break;
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) route_wg_select<RENT>(0, r.E, r.topk, r.scale, idl, wl, nullptr, key, score);
+  __syncthreads();
+  const int tid = threadIdx.x, k = r.topk;
+  if (tid <= k) {
+    const int4 d = tid < k ? make_int4(idl[tid], tid, tid + 1, 0) : make_int4(-1, k, k + 1, 0);
+    if (tid < k || r.shared) {
+      grp[tid] = d;
+      if (blockIdx.x == 0) r.groups_out[tid] = d;
+    }
+    if (blockIdx.x == 0 && tid < k) {
+      r.idx_out[tid] = idl[tid];
+      r.w_out[tid] = wl[tid];
+      r.pos[tid] = tid;
+    }
+    if (blockIdx.x == 0 && tid == 0) *r.ngroups_out = k + r.shared;
+  }
+  __syncthreads();
+  return k + r.shared;
+}
+
+// MCMAX: the largest group (1 when every group holds one row: a single token). RENT > 0: the
+// token is routed here first (moe_gv_route; one token, mc = 1, no column blocks).
+template <int FMT, int G, int U, bool SWI, int XW, int MCMAX, bool LONG, int RENT = 0>
 __global__ void __launch_bounds__(256) k_moe_gemv(MoeGvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int CPP = moe_gv_cpp(G, SWI);
   const int spg = (a.N + CPP - 1) / CPP;  // column slices per group
+  const int4 *groups = a.groups;
+  int ngroups;
+  if constexpr (RENT > 0) {
+    char *rbuf = smem + moe_gv_xstage_bytes(a.mc, a.P);
+    ngroups = moe_gv_route<RENT>(a.rt, rbuf);
+    groups = reinterpret_cast<const int4 *>(rbuf);
+  } else {
+    ngroups = *a.ngroups;
+  }
   int64_t beg, end;
   if (a.cols_per_wg > 0) {
     const int bs = a.cols_per_wg / CPP;  // slices per block
     const int nblk = (spg + bs - 1) / bs;
     const int g = blockIdx.x / nblk;
-    if (g >= *a.ngroups) return;
+    if (g >= ngroups) return;
     beg = static_cast<int64_t>(g) * spg + static_cast<int64_t>(blockIdx.x - g * nblk) * bs;
     end = beg + bs < static_cast<int64_t>(g + 1) * spg ? beg + bs : static_cast<int64_t>(g + 1) * spg;
   } else {
-    const int64_t tot = static_cast<int64_t>(*a.ngroups) * spg;
+    const int64_t tot = static_cast<int64_t>(ngroups) * spg;
     beg = tot * blockIdx.x / gridDim.x;
     end = tot * (blockIdx.x + 1) / gridDim.x;
   }
@@ -234,7 +305,7 @@ __global__ void __launch_bounds__(256) k_moe_gemv(MoeGvArgs a) {
     const int n0 = static_cast<int>(u - gb) * CPP;
     const int s1 = static_cast<int>(end - gb < spg ? end - gb : spg);
     const int ncols = (s1 * CPP < a.N ? s1 * CPP : a.N) - n0;
-    const int4 d = a.groups[g];
+    const int4 d = groups[g];
     const uint8_t *Wg, *Wu = nullptr;
     if (d.x < 0) {
       Wg = a.Ws;
@@ -259,10 +330,11 @@ __global__ void __launch_bounds__(256) k_moe_gemv(MoeGvArgs a) {
   }
 }
 
-template <int FMT, int G, int U, bool SWI, int XW, int MCMAX, bool LONG>
+template <int FMT, int G, int U, bool SWI, int XW, int MCMAX, bool LONG, int RENT = 0>
 int moe_gemv_launch2(const MoeGvArgs &a, int max_groups, hipStream_t s) {
-  const void *fn = reinterpret_cast<const void *>(&k_moe_gemv<FMT, G, U, SWI, XW, MCMAX, LONG>);
-  const size_t lds = static_cast<size_t>(a.mc) * a.P * XSTAGE_PAIR_BYTES;
+  const void *fn = reinterpret_cast<const void *>(&k_moe_gemv<FMT, G, U, SWI, XW, MCMAX, LONG, RENT>);
+  const size_t lds = RENT ? moe_gv_xstage_bytes(a.mc, a.P) + moe_gv_route_bytes(RENT)
+                          : static_cast<size_t>(a.mc) * a.P * XSTAGE_PAIR_BYTES;
   if (lds > 64 * 1024) {
     static std::atomic<uint64_t> raised{0};
     const int rc = ensure_lds_limit(fn, 160 * 1024, raised, "moe gemv");
@@ -274,7 +346,7 @@ int moe_gemv_launch2(const MoeGvArgs &a, int max_groups, hipStream_t s) {
     if (a.cols_per_wg % CPP) return set_error(VYBDQ_ERR_SHAPE, "moe gemv: columns per workgroup not a multiple of the pass");
     const int bs = a.cols_per_wg / CPP;
     const int64_t grid = static_cast<int64_t>(max_groups) * ((spg + bs - 1) / bs);
-    hipLaunchKernelGGL((k_moe_gemv<FMT, G, U, SWI, XW, MCMAX, LONG>), dim3(static_cast<unsigned>(grid)), dim3(256), lds, s, a);
+    hipLaunchKernelGGL((k_moe_gemv<FMT, G, U, SWI, XW, MCMAX, LONG, RENT>), dim3(static_cast<unsigned>(grid)), dim3(256), lds, s, a);
     return check_launch("moe grouped gemv");
   }
   int per_cu = a.wg_per_cu;
@@ -290,12 +362,19 @@ int moe_gemv_launch2(const MoeGvArgs &a, int max_groups, hipStream_t s) {
   const int64_t units = static_cast<int64_t>(max_groups) * spg;
   int64_t grid = static_cast<int64_t>(per_cu) * device_cu_count();
   grid = grid < units ? grid : units;
-  hipLaunchKernelGGL((k_moe_gemv<FMT, G, U, SWI, XW, MCMAX, LONG>), dim3(static_cast<unsigned>(grid)), dim3(256), lds, s, a);
+  hipLaunchKernelGGL((k_moe_gemv<FMT, G, U, SWI, XW, MCMAX, LONG, RENT>), dim3(static_cast<unsigned>(grid)), dim3(256), lds, s, a);
   return check_launch("moe grouped gemv");
 }
 
 template <int FMT, int G, int U, bool SWI, int XW, bool LONG = false>
 int moe_gemv_launch1(const MoeGvArgs &a, int max_groups, hipStream_t s) {
+  if constexpr (SWI) {
+    if (a.rt.E > 0) {
+      if (a.mc != 1 || a.cols_per_wg > 0 || a.rt.E > 256 || a.rt.topk < 1 || a.rt.topk > a.rt.E)
+        return set_error(VYBDQ_ERR_ARG, "moe gemv: routing in the gate|up launch needs one token, E <= 256, no column blocks");
+      return moe_gemv_launch2<FMT, G, U, SWI, XW, 1, LONG, 4>(a, max_groups, s);
+    }
+  }
   return a.mc == 1 ? moe_gemv_launch2<FMT, G, U, SWI, XW, 1, LONG>(a, max_groups, s)
                    : moe_gemv_launch2<FMT, G, U, SWI, XW, kMoeGvMC, LONG>(a, max_groups, s);
 }

@@ -154,32 +154,44 @@ __device__ __forceinline__ void route_wave(const void *__restrict__ logits, cons
 // every thread into LDS (keys: E words, scores: E doubles), so each thread evaluates the sigmoid
 // about E / blockDim.x times instead of E / 64; wave 0 then runs the selection rounds on them and
 // reads the winners' scores back. The keys, the selection and the score expression are those of
-// route_wave, so the outputs are identical.
-template <int LDT, int ENT>
-__device__ __forceinline__ void route_wg(const void *__restrict__ logits, const float *__restrict__ bias, int t, int E,
-                                         int topk, double scale, int *__restrict__ idx_out, float *__restrict__ w_out,
-                                         int *__restrict__ idx_copy, uint64_t *key_lds, double *score_lds) {
+// route_wave, so the outputs are identical. route_wg_keys: the key and score part (no barrier).
+template <int LDT>
+__device__ __forceinline__ void route_wg_keys(const void *__restrict__ logits, const float *__restrict__ bias, int t,
+                                              int E, uint64_t *key_lds, double *score_lds) {
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     const double l = load_logit<LDT>(logits, static_cast<int64_t>(t) * E + e);
     const double sc = 1.0 / (1.0 + exp(-l));
     score_lds[e] = sc;
     key_lds[e] = double_order_key(bias ? sc + static_cast<double>(bias[e]) : l);  // = route_key(l, bias, e)
   }
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    uint64_t key[ENT];
-    uint32_t eid[ENT];
+}
+
+// The selection of route_wg on wave 0 (threads 0-63 call it, after a barrier behind route_wg_keys).
+template <int ENT>
+__device__ __forceinline__ void route_wg_select(int t, int E, int topk, double scale, int *__restrict__ idx_out,
+                                                float *__restrict__ w_out, int *__restrict__ idx_copy,
+                                                const uint64_t *key_lds, const double *score_lds) {
+  const int lane = threadIdx.x & 63;
+  uint64_t key[ENT];
+  uint32_t eid[ENT];
 #pragma unroll
-    for (int i = 0; i < ENT; ++i) {
-      const int e = lane + 64 * i;
-      key[i] = e < E ? key_lds[e] : 0;
-      eid[i] = e < E ? static_cast<uint32_t>(e) : kRouteNone;
-    }
-    const uint32_t mine = route_select<ENT>(key, eid, topk);
-    const double sc = lane < topk && mine != kRouteNone ? score_lds[mine] : 0.0;
-    route_store(mine, sc, t, topk, scale, idx_out, w_out, idx_copy);
+  for (int i = 0; i < ENT; ++i) {
+    const int e = lane + 64 * i;
+    key[i] = e < E ? key_lds[e] : 0;
+    eid[i] = e < E ? static_cast<uint32_t>(e) : kRouteNone;
   }
+  const uint32_t mine = route_select<ENT>(key, eid, topk);
+  const double sc = lane < topk && mine != kRouteNone ? score_lds[mine] : 0.0;
+  route_store(mine, sc, t, topk, scale, idx_out, w_out, idx_copy);
+}
+
+template <int LDT, int ENT>
+__device__ __forceinline__ void route_wg(const void *__restrict__ logits, const float *__restrict__ bias, int t, int E,
+                                         int topk, double scale, int *__restrict__ idx_out, float *__restrict__ w_out,
+                                         int *__restrict__ idx_copy, uint64_t *key_lds, double *score_lds) {
+  route_wg_keys<LDT>(logits, bias, t, E, key_lds, score_lds);
+  __syncthreads();
+  if (threadIdx.x < 64) route_wg_select<ENT>(t, E, topk, scale, idx_out, w_out, idx_copy, key_lds, score_lds);
 }
 
 // experts per lane of the router for E experts: 4, 5, 8 or 16
