@@ -1143,11 +1143,11 @@ def sub_record(r):
 
 
 def run_all(args, torch, dev):
-    """Every workload of the metric, each as a sub-record (fewer steps than the headline: each
-    replay is 0.3-15 ms of GPU work)."""
+    """Every workload of the metric, each as a sub-record (at most 100 timed replays after at most
+    10 warm-up replays; each replay is 0.3-15 ms of GPU work)."""
     import copy
     sub = copy.copy(args)
-    sub.steps, sub.warmup = max(5, min(args.steps, 20)), max(2, min(args.warmup, 3))
+    sub.steps, sub.warmup = max(5, min(args.steps, 100)), max(2, min(args.warmup, 10))
     recs = {}
 
     def leg(name, fn, *a, **kw):
@@ -1155,6 +1155,7 @@ def run_all(args, torch, dev):
         t0 = time.perf_counter()
         r = fn(sub, torch, dev, *a, **kw)
         recs[name] = sub_record(r)
+        recs[name].update(steps=sub.steps, warmup=sub.warmup)
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
         log(f"config {name}: {recs[name]['value']} {recs[name]['unit']} ({time.perf_counter() - t0:.1f} s)")

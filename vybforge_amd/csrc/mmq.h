@@ -710,6 +710,90 @@ int mm_reduce_launch(const MmArgs &a, hipStream_t s) {
 
 // X [M][K] (f32 or bf16, 16-byte aligned, K % 8 == 0) -> xh [M][K] fp16 and xscale[M], one
 // workgroup per row (mmq_host.hip)
+// One row of X (K elements, bf16 or f32) -> fp16 with a power-of-two scale that brings the row's
+// largest |x| into [2^14, 2^15), and that scale (the body of x_rows_to_f16; 256 threads, wmax: 4
+// floats of LDS). CH > 0: the row (at most 256 CH chunks of 8) is loaded once into registers, all
+// loads issued before the first use; CH = 0: two passes over the row (any K).
+template <int XDT, int CH>
+__device__ __forceinline__ void x_row_to_f16(const void *__restrict__ X, u4 *__restrict__ Xh,
+                                             float *__restrict__ xscale, int64_t K, int64_t row, float *wmax) {
+  const int64_t n8 = K / 8;
+  // the row's base in 64-bit arithmetic (M * K may exceed 2^32 elements); offsets inside the row
+  // are 32-bit (every caller bounds K below 2^24)
+  const void *Xr = static_cast<const char *>(X) + row * K * (XDT == VYBDQ_F32 ? 4 : 2);
+  auto chunk_max = [](const XChunk<XDT> &c, float m) {
+    if constexpr (XDT == VYBDQ_F32) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(__uint_as_float(c.r[j >> 2][j & 3])));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t v = c.r[j];
+        m = fmaxf(m, fmaxf(fabsf(__uint_as_float(v << 16)), fabsf(__uint_as_float(v & 0xffff0000u))));
+      }
+    }
+    return m;
+  };
+  auto chunk_f16 = [](const XChunk<XDT> &c, float inv) {
+    u4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float a, b;
+      if constexpr (XDT == VYBDQ_F32) {
+        a = __uint_as_float(c.r[j >> 1][2 * (j & 1)]);
+        b = __uint_as_float(c.r[j >> 1][2 * (j & 1) + 1]);
+      } else {
+        a = __uint_as_float(c.r[j] << 16);
+        b = __uint_as_float(c.r[j] & 0xffff0000u);
+      }
+      o[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(a * inv), static_cast<_Float16>(b * inv)});
+    }
+    return o;
+  };
+  float amax = 0.f;
+  XChunk<XDT> cc[CH > 0 ? CH : 1];
+  if constexpr (CH > 0) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int64_t i = threadIdx.x + 256 * j;
+      if (i < n8) x_load<XDT>(Xr, static_cast<uint32_t>(i * 8), cc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < CH; ++j)
+      if (threadIdx.x + 256 * j < n8) amax = chunk_max(cc[j], amax);
+  } else {
+    for (int64_t i = threadIdx.x; i < n8; i += 256) {
+      XChunk<XDT> c;
+      x_load<XDT>(Xr, static_cast<uint32_t>(i * 8), c);
+      amax = chunk_max(c, amax);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  float inv;
+  const float scale = block_scale(amax, inv);
+  if (threadIdx.x == 0) xscale[row] = scale;
+  if constexpr (CH > 0) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int64_t i = threadIdx.x + 256 * j;
+      if (i < n8) Xh[row * n8 + i] = chunk_f16(cc[j], inv);
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < n8; i += 256) {
+      XChunk<XDT> c;
+      x_load<XDT>(Xr, static_cast<uint32_t>(i * 8), c);
+      Xh[row * n8 + i] = chunk_f16(c, inv);
+    }
+  }
+}
+
+// chunks of 8 per thread of a 256-thread row conversion; CH = 2, 4, 8, 12 when it is at most that, else 0
+inline int x_row_chunks(int64_t K) { return static_cast<int>((K / 8 + 255) / 256); }
+
 int x_rows_to_f16(const void *X, int xdt, int64_t M, int64_t K, void *xh, float *xscale, hipStream_t s);
 
 // fp16 X (streamed into LDS by direct loads): 8 waves per workgroup, two per SIMD, so that one

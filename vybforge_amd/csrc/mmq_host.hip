@@ -98,91 +98,17 @@ bool mmq_supported(int64_t M, int64_t N, int64_t K) {
 // the scaled row is rounded to fp16 (bf16 values exactly, f32 to nearest even) and 2^e goes to
 // xscale[row], which the GEMM epilogue multiplies back: activations of any magnitude neither
 // overflow nor flush to zero. The GEMM then streams the fp16 copy straight into LDS.
-// CH > 0: the row (at most 256 CH chunks of 8) is loaded once into registers, all loads issued
-// before the first use; CH = 0: two passes over the row (any K).
 template <int XDT, int CH>
 __global__ void __launch_bounds__(256) k_x_to_f16(const void *__restrict__ X, u4 *__restrict__ Xh,
                                                   float *__restrict__ xscale, int64_t K) {
   __shared__ float wmax[4];
-  const int64_t row = blockIdx.x;
-  const int64_t n8 = K / 8;
-  // the row's base in 64-bit arithmetic (M * K may exceed 2^32 elements); offsets inside the row
-  // are 32-bit (every caller bounds K below 2^24)
-  const void *Xr = static_cast<const char *>(X) + row * K * (XDT == VYBDQ_F32 ? 4 : 2);
-  auto chunk_max = [](const XChunk<XDT> &c, float m) {
-    if constexpr (XDT == VYBDQ_F32) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(__uint_as_float(c.r[j >> 2][j & 3])));
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t v = c.r[j];
-        m = fmaxf(m, fmaxf(fabsf(__uint_as_float(v << 16)), fabsf(__uint_as_float(v & 0xffff0000u))));
-      }
-    }
-    return m;
-  };
-  auto chunk_f16 = [](const XChunk<XDT> &c, float inv) {
-    u4 o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float a, b;
-      if constexpr (XDT == VYBDQ_F32) {
-        a = __uint_as_float(c.r[j >> 1][2 * (j & 1)]);
-        b = __uint_as_float(c.r[j >> 1][2 * (j & 1) + 1]);
-      } else {
-        a = __uint_as_float(c.r[j] << 16);
-        b = __uint_as_float(c.r[j] & 0xffff0000u);
-      }
-      o[j] = __builtin_bit_cast(uint32_t, h2{static_cast<_Float16>(a * inv), static_cast<_Float16>(b * inv)});
-    }
-    return o;
-  };
-  float amax = 0.f;
-  XChunk<XDT> cc[CH > 0 ? CH : 1];
-  if constexpr (CH > 0) {
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      const int64_t i = threadIdx.x + 256 * j;
-      if (i < n8) x_load<XDT>(Xr, static_cast<uint32_t>(i * 8), cc[j]);
-    }
-#pragma unroll
-    for (int j = 0; j < CH; ++j)
-      if (threadIdx.x + 256 * j < n8) amax = chunk_max(cc[j], amax);
-  } else {
-    for (int64_t i = threadIdx.x; i < n8; i += 256) {
-      XChunk<XDT> c;
-      x_load<XDT>(Xr, static_cast<uint32_t>(i * 8), c);
-      amax = chunk_max(c, amax);
-    }
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  float inv;
-  const float scale = block_scale(amax, inv);
-  if (threadIdx.x == 0) xscale[row] = scale;
-  if constexpr (CH > 0) {
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      const int64_t i = threadIdx.x + 256 * j;
-      if (i < n8) Xh[row * n8 + i] = chunk_f16(cc[j], inv);
-    }
-  } else {
-    for (int64_t i = threadIdx.x; i < n8; i += 256) {
-      XChunk<XDT> c;
-      x_load<XDT>(Xr, static_cast<uint32_t>(i * 8), c);
-      Xh[row * n8 + i] = chunk_f16(c, inv);
-    }
-  }
+  x_row_to_f16<XDT, CH>(X, Xh, xscale, K, blockIdx.x, wmax);
 }
 
 template <int XDT>
 static void x_to_f16_launch(const void *X, u4 *o, float *xscale, int64_t M, int64_t K, hipStream_t s) {
   const unsigned grid = static_cast<unsigned>(M);
-  const int64_t per = (K / 8 + 255) / 256;  // chunks per thread
+  const int per = x_row_chunks(K);
   if (per <= 2) hipLaunchKernelGGL((k_x_to_f16<XDT, 2>), dim3(grid), dim3(256), 0, s, X, o, xscale, K);
   else if (per <= 4) hipLaunchKernelGGL((k_x_to_f16<XDT, 4>), dim3(grid), dim3(256), 0, s, X, o, xscale, K);
   else if (per <= 8) hipLaunchKernelGGL((k_x_to_f16<XDT, 8>), dim3(grid), dim3(256), 0, s, X, o, xscale, K);

@@ -176,6 +176,23 @@ __global__ void __launch_bounds__(256) k_moe_bucket_tiles(const int *__restrict_
   bucket_tiles(idx, T, topk, E, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2, sh);
 }
 
+// The bucketing of k_moe_bucket_tiles in workgroup 0 and, in workgroups 1..T, the fp16 copy of
+// the token rows for the grouped MFMA GEMM (x_row_to_f16): two independent jobs in one launch.
+template <int XDT, int CH>
+__global__ void __launch_bounds__(256) k_moe_bucket_xh(const int *__restrict__ idx, int T, int topk, int E, int BMr,
+                                                       int BMr2, int shared, int *__restrict__ pos,
+                                                       int *__restrict__ row_map, int4 *__restrict__ tiles,
+                                                       int *__restrict__ ntiles, int4 *__restrict__ tiles2,
+                                                       int *__restrict__ ntiles2, const void *__restrict__ X,
+                                                       int64_t K, u4 *__restrict__ Xh, float *__restrict__ xscale) {
+  extern __shared__ int sh[];
+  if (blockIdx.x == 0) {
+    bucket_tiles(idx, T, topk, E, BMr, BMr2, shared, pos, row_map, tiles, ntiles, tiles2, ntiles2, sh);
+  } else {
+    x_row_to_f16<XDT, CH>(X, Xh, xscale, K, blockIdx.x - 1, reinterpret_cast<float *>(sh));
+  }
+}
+
 // Few tokens: routing (wave w takes tokens w, w + 4, ...) and bucketing in one workgroup; the
 // routed ids also go to LDS, where the bucketing reads them.
 template <int LDT, int ENT>
@@ -442,6 +459,12 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
     // one token on the grouped GEMV (up to 256 experts): the gate|up launch routes the token itself
     // and writes the ids, weights, rows and groups for the down launch and the combine, so no
     // routing launch precedes it (VYBDQ_MOE_ROUTE_GV=0 keeps the routing launch)
+    // many tokens on the grouped MFMA GEMM with bf16 / f32 x: the fp16 copy of x (into `rows`, which
+    // only the down GEMM writes, after gate|up has read it) rides on the bucketing launch
+    // (VYBDQ_MOE_XH_SEP=1: its own launch)
+    const bool xh_with_bucket = !gv && !fused_route && x_dt != VYBDQ_F16 && !tuning_env("VYBDQ_MOE_XH_SEP");
+    _Float16 *xh_copy = reinterpret_cast<_Float16 *>(m.rows);
+    float *xh_scale = reinterpret_cast<float *>(xh_copy + T * H);
     bool route_in_gv = gv && T == 1 && E <= 256 && !tuning_env("VYBDQ_MOE_GEMV_COLS");
     if (const char *e = tuning_env("VYBDQ_MOE_ROUTE_GV")) route_in_gv = route_in_gv && e[0] != '0';
     if (route_in_gv) {
@@ -469,6 +492,28 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
       else { VYBDQ_DISPATCH_IN(logits_dt, LDT, RB(LDT)); }
 #undef RB
       rc = check_launch("moe route + bucket");
+    } else if (xh_with_bucket) {
+      const int e = static_cast<int>(E), k = static_cast<int>(topk), tt = static_cast<int>(T);
+      const size_t shb = static_cast<size_t>(2 * E) * 4 > 16 ? static_cast<size_t>(2 * E) * 4 : 16;
+      u4 *xo = reinterpret_cast<u4 *>(xh_copy);
+#define BX(XDT, CH)                                                                                                 \
+  hipLaunchKernelGGL((k_moe_bucket_xh<XDT, CH>), dim3(static_cast<unsigned>(T + 1)), dim3(256), shb, s, idx, tt, k, e, \
+                     BMr, mc, shared ? 1 : 0, m.pos, m.row_map, m.tiles, m.ntiles, nullptr, nullptr,                 \
+                     reinterpret_cast<const void *>(x), H, xo, xh_scale)
+#define BXC(XDT)                                                            \
+  do {                                                                      \
+    const int per = x_row_chunks(H);                                        \
+    if (per <= 2) BX(XDT, 2);                                               \
+    else if (per <= 4) BX(XDT, 4);                                          \
+    else if (per <= 8) BX(XDT, 8);                                          \
+    else if (per <= 12) BX(XDT, 12);                                        \
+    else BX(XDT, 0);                                                        \
+  } while (0)
+      if (x_dt == VYBDQ_BF16) BXC(VYBDQ_BF16);
+      else BXC(VYBDQ_F32);
+#undef BXC
+#undef BX
+      rc = check_launch("moe bucket + x rows");
     } else {
       hipLaunchKernelGGL(k_moe_bucket_tiles, dim3(1), dim3(256), static_cast<size_t>(2 * E) * 4, s, idx,
                          static_cast<int>(T), static_cast<int>(topk), static_cast<int>(E), BMr, mc, shared ? 1 : 0,
@@ -588,12 +633,12 @@ extern "C" int vybdq_moe_forward(int wtype, uint64_t x, int x_dt, uint64_t logit
         // straight into LDS (its register path for other types waits on the X loads in issue
         // order, which drains the weight ring every step). The copy lives in `rows`, which only
         // the down GEMM writes, after gate|up has read it.
-        _Float16 *xh = reinterpret_cast<_Float16 *>(m.rows);
-        float *xsc = reinterpret_cast<float *>(xh + T * H);
-        rc = x_rows_to_f16(reinterpret_cast<const void *>(x), x_dt, T, H, xh, xsc, s);
-        if (rc) return rc;
-        g.m.X = xh;
-        g.m.xscale = xsc;
+        if (!xh_with_bucket) {
+          rc = x_rows_to_f16(reinterpret_cast<const void *>(x), x_dt, T, H, xh_copy, xh_scale, s);
+          if (rc) return rc;
+        }
+        g.m.X = xh_copy;
+        g.m.xscale = xh_scale;
         gxdt = VYBDQ_F16;
       }
       rc = run(gxdt, true, g);
