@@ -295,6 +295,24 @@ def test_moe_layer_q4_four_row_tiles(dev, monkeypatch, T, rows4, shared):
     assert matmul.rel_maxnorm(out, ref) < TOL
 
 
+@pytest.mark.parametrize("ty,T", [(ops.GGML_Q4_0, 9), (ops.GGML_Q4_0, 40), (ops.GGML_Q8_0, 80)])
+@pytest.mark.parametrize("H", [512, 6144])
+@pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float32])
+def test_moe_layer_x_copy_in_bucket_launch(dev, monkeypatch, ty, T, H, xdtype):
+    """More than 8 tokens with bf16 / f32 x on the MFMA GEMM: the fp16 copy of x made by workgroups
+    1..T of the bucketing launch and made in its own launch (VYBDQ_MOE_XH_SEP=1) give bit-identical
+    outputs, both within the oracle's gate (H = 512 and 6144: two and three 8-element chunks per
+    thread of the row conversion)."""
+    outs = []
+    for sep in (None, "1"):
+        if sep:
+            monkeypatch.setenv("VYBDQ_MOE_XH_SEP", sep)
+        out, ref = moe_case(dev, ty, T, H=H, I=256, E=8, k=4, seed=900 + T + H, xdtype=xdtype)
+        assert matmul.rel_maxnorm(out, ref) < TOL
+        outs.append(out)
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("T,mt", [(7, "1"), (17, "1"), (40, "2")])
 def test_moe_layer_q4_register_body(dev, monkeypatch, T, mt):
     """q4_0 through the register-operand body (VYBDQ_MOE_LDS=0) at both m-tile heights."""
